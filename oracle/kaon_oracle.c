@@ -1,0 +1,677 @@
+/*
+ * kaon_oracle.c -- CPU restatement of the kaon fused optimizer step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * kernels in k-optimizers_amd/csrc.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it, and only as the checker (or the
+ * timed CPU baseline), never as the product path.
+ *
+ * What it restates (reference = K-Optimizers "kaon" 0.7.4, paths relative to
+ * the reference root):
+ *   - codecs        src/kaon/_momentum_codec.py:72-200, 253-406
+ *   - SR write      src/kaon/_stochastic_rounding.py:70-103
+ *   - weight write  src/kaon/_backend.py:82-122 (SR / none / fp32 / kahan)
+ *   - cautious      src/kaon/_backend.py:127-142
+ *   - GC            src/kaon/_backend.py:147-177 (bf16-rounded, in grad dtype)
+ *   - factored      src/kaon/_factored.py:26-83
+ *   - Adakaon       src/kaon/adakaon.py:968-1014 (== batched :840-966)
+ *   - Lion          src/kaon/lion.py:454-485 (== batched :416-451)
+ *   - AdaMuon       src/kaon/adamuon.py:97-149, 557-615 (== batched :434-555)
+ *   - MSAM/Nekaon   src/kaon/msam.py:169-235, 375-406 ; src/kaon/nekaon.py:162-171
+ *
+ * Rounding model (measured against torch 2.10 CPU in this image, see
+ * tests/test_oracle_torch_semantics.py):
+ *   - lerp(a,b,w): |w|<0.5 -> fma(w, b-a, a), else fma(w-1, b-a, b)
+ *   - add_(x, alpha=s): fma(s, x, self)
+ *   - rsqrt(x): 1/sqrt(x) (two correctly rounded ops)
+ *   - x / python_scalar: true fp32 division by (float)scalar
+ *   - bf16 mean: bf16(fp32_sum / C) (one rounding); bf16 a-b: bf16(fp32(a-b))
+ *   - everything else: one IEEE fp32 op per torch op.  Built with
+ *     -ffp-contract=off so only the explicit fmaf() calls fuse.
+ *
+ * Reduction order.  torch does not specify its fp32 reduction order (it
+ * depends on the CPU ISA and thread count).  This restatement fixes one
+ * canonical, accurate order, which the HIP kernels implement bit-for-bit:
+ *   CSUM(x[0..n)):  256 lanes; lane l accumulates (from +0.0f, in order) the
+ *     elements of 8-element chunks l, l+256, l+512, ...; each 64-lane group is
+ *     reduced by an xor butterfly (offsets 32,16,8,4,2,1); the group results
+ *     of the groups that hold any chunk are folded left to right.
+ *   COLSUM_j over R rows: rows are cut into groups of KAON_COLGROUP (32)
+ *     consecutive rows; each group is summed in row order, the group partials
+ *     are summed in group order.
+ *   Sum of squares for the RMS clip: CSUM over each row (C elements), then
+ *     CSUM over the R row results.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define KAON_COLGROUP 32
+#define KAON_LANES 256
+#define KAON_CHUNK 8
+
+/* dtype codes shared with the HIP library and oracle.py */
+enum { KO_F32 = 0, KO_BF16 = 1 };
+enum { KO_MOM_NONE = 0, KO_MOM_F32 = 1, KO_MOM_BF16 = 2, KO_MOM_INT8 = 3, KO_MOM_4BIT = 4 };
+enum { KO_SR = 0, KO_RN = 1, KO_KAHAN = 2 };
+
+/* ------------------------------------------------------------------ bits */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+static inline float bf16_to_f(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* fp32 -> bf16 round-to-nearest-even; NaN -> 0x7FC0. */
+static inline uint16_t f_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+static inline float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
+
+/* torch.lerp on CPU (fused multiply-add form, branch at |w| = 0.5). */
+static inline float ko_lerp(float a, float b, float w) {
+    float d = b - a;
+    if (fabsf(w) < 0.5f) return fmaf(w, d, a);
+    return fmaf(w - 1.0f, d, b);
+}
+
+static inline float ko_rsqrt(float x) { return 1.0f / sqrtf(x); }
+
+static inline float ko_sign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
+
+/* --------------------------------------------------------------- Philox */
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+ * easy as 1, 2, 3", SC'11).  Multipliers and Weyl key increments are the
+ * published ones. */
+#define PHILOX_M0 0xD2511F53u
+#define PHILOX_M1 0xCD9E8D57u
+#define PHILOX_W0 0x9E3779B9u
+#define PHILOX_W1 0xBB67AE85u
+
+void ko_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        uint64_t p0 = (uint64_t)PHILOX_M0 * c0;
+        uint64_t p1 = (uint64_t)PHILOX_M1 * c2;
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += PHILOX_W0;
+        k1 += PHILOX_W1;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* SR noise word for element e of tensor `tid`, stream `s`:
+ * key = (seed_lo32, step), counter = (e/8 lo, e/8 hi, tid, s);
+ * the 8 elements of a chunk take the 8 16-bit halves, low half first. */
+static inline uint32_t sr_noise(uint64_t seed, uint32_t step, uint32_t tid, uint32_t s,
+                                int64_t e, const uint16_t* inj) {
+    if (inj) return inj[e];
+    uint64_t ch = (uint64_t)e >> 3;
+    uint32_t ctr[4] = {(uint32_t)ch, (uint32_t)(ch >> 32), tid, s};
+    uint32_t key[2] = {(uint32_t)seed, step};
+    uint32_t o[4];
+    ko_philox4x32_10(ctr, key, o);
+    int w = (int)(e & 7);
+    return (o[w >> 1] >> ((w & 1) * 16)) & 0xFFFFu;
+}
+
+void ko_sr_noise_fill(uint16_t* out, int64_t n, uint64_t seed, uint32_t step,
+                      uint32_t tid, uint32_t stream) {
+    for (int64_t e = 0; e < n; ++e) out[e] = (uint16_t)sr_noise(seed, step, tid, stream, e, NULL);
+}
+
+/* _add_stochastic_bf16_ (src/kaon/_stochastic_rounding.py:70-103): the fp32
+ * result x gets 16 bits of noise added to its int32 pattern, then the low 16
+ * bits are cleared; the cast back to bf16 is exact (NaN -> 0x7FC0). */
+static inline uint16_t sr_bf16(float x, uint32_t noise) {
+    uint32_t b = f2u(x) + noise;       /* int32 add, wraps */
+    b &= 0xFFFF0000u;
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+    return (uint16_t)(b >> 16);
+}
+
+/* ------------------------------------------------------- canonical sums */
+float ko_csum(const float* x, int64_t n) {
+    if (n <= 0) return 0.0f;
+    int64_t nch = (n + KAON_CHUNK - 1) / KAON_CHUNK;
+    float acc[KAON_LANES];
+    for (int l = 0; l < KAON_LANES; ++l) {
+        float a = 0.0f;
+        for (int64_t k = l; k < nch; k += KAON_LANES)
+            for (int e = 0; e < KAON_CHUNK; ++e) {
+                int64_t j = KAON_CHUNK * k + e;
+                if (j < n) a = a + x[j];
+            }
+        acc[l] = a;
+    }
+    float s[4];
+    for (int w = 0; w < 4; ++w) {
+        float* a = acc + 64 * w;
+        for (int o = 32; o >= 1; o >>= 1)
+            for (int l = 0; l < o; ++l) a[l] = a[l] + a[l + o];
+        s[w] = a[0];
+    }
+    int nw = (int)((nch + 63) / 64);
+    if (nw > 4) nw = 4;
+    float r = s[0];
+    for (int w = 1; w < nw; ++w) r = r + s[w];
+    return r;
+}
+
+/* ------------------------------------------------------------- tensors */
+typedef struct {
+    void* g;             /* grad, g_dtype; GC is NOT written back */
+    void* p;             /* param, p_dtype, updated in place */
+    void* m;             /* momentum storage (codec), updated in place */
+    float* m_scale;      /* int8: [R] (factored) or [1]; 4bit: [nblocks] */
+    float* row;          /* [R] factored second moment */
+    float* col;          /* [C] */
+    float* v;            /* [n] 1-D second moment */
+    uint16_t* shift;     /* kahan compensation (bf16 param) */
+    int64_t R, C;        /* matrixized shape; 1-D: R = 1, C = n */
+    int32_t g_dtype, p_dtype, codec, block4;
+    int32_t factored;    /* ndim >= 2 */
+    uint32_t tensor_id;  /* SR noise counter field */
+    const uint16_t* noise[3]; /* injected SR noise per stream (nullable) */
+    float* out_m;        /* optional: AdaMuon NS output O [R*C] (fp32), diagnostics */
+    const float* fac_override; /* optional: clip divisor to use instead of the computed
+                                  one (lets a test inject torch's own norm value) */
+} KoTensor;
+
+typedef struct {
+    double lr, beta1, beta2, eps1, wd, clip;
+    int32_t cautious, gc, bf16_method;
+    int32_t ns_steps;
+    uint64_t seed;
+    uint32_t step;
+    /* Nekaon lookahead fused into the Adakaon step */
+    int32_t nk_remove, nk_climb;
+    double nk_k, nk_bound_old, nk_bound_new;
+} KoHyper;
+
+static inline float load_g(const KoTensor* t, int64_t i) {
+    return t->g_dtype == KO_BF16 ? bf16_to_f(((const uint16_t*)t->g)[i]) : ((const float*)t->g)[i];
+}
+static inline float load_p(const KoTensor* t, int64_t i) {
+    return t->p_dtype == KO_BF16 ? bf16_to_f(((const uint16_t*)t->p)[i]) : ((const float*)t->p)[i];
+}
+static inline float round_g(const KoTensor* t, float x) {
+    return t->g_dtype == KO_BF16 ? round_bf16(x) : x;
+}
+
+/* Gradient as the step sees it: GC'd in the grad dtype when enabled and
+ * ndim >= 2 (src/kaon/_backend.py:147-177; the mean is torch's bf16 mean,
+ * i.e. one rounding of fp32_sum / C). */
+static float* centralized_grad(const KoTensor* t, int gc) {
+    int64_t n = t->R * t->C;
+    float* g = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    for (int64_t i = 0; i < n; ++i) g[i] = load_g(t, i);
+    if (gc && t->factored) {
+        for (int64_t r = 0; r < t->R; ++r) {
+            float* gr = g + r * t->C;
+            float mu = round_g(t, ko_csum(gr, t->C) / (float)t->C);
+            for (int64_t j = 0; j < t->C; ++j) gr[j] = round_g(t, gr[j] - mu);
+        }
+    }
+    return g;
+}
+
+/* ----------------------------------------------------------- codecs */
+/* dequant of the stored momentum into fp32 (effective [R, C] layout).
+ * int8: codes * per-row scale (_momentum_codec.py:304, 325); 1-D has one
+ * scale.  4bit: (nibble - 8) * block scale (_momentum_codec.py:144-153). */
+static void mom_dequant(const KoTensor* t, float* out) {
+    int64_t n = t->R * t->C;
+    switch (t->codec) {
+    case KO_MOM_F32: memcpy(out, t->m, sizeof(float) * (size_t)n); break;
+    case KO_MOM_BF16:
+        for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f(((const uint16_t*)t->m)[i]);
+        break;
+    case KO_MOM_INT8: {
+        const int8_t* q = (const int8_t*)t->m;
+        for (int64_t r = 0; r < t->R; ++r) {
+            float sc = t->m_scale[t->factored ? r : 0];
+            for (int64_t j = 0; j < t->C; ++j) out[r * t->C + j] = (float)q[r * t->C + j] * sc;
+        }
+        break;
+    }
+    case KO_MOM_4BIT: {
+        const uint8_t* pk = (const uint8_t*)t->m;
+        for (int64_t i = 0; i < n; ++i) {
+            uint8_t b = pk[i >> 1];
+            int nib = (i & 1) ? ((b >> 4) & 0xF) : (b & 0xF);
+            out[i] = ((float)nib - 8.0f) * t->m_scale[i / t->block4];
+        }
+        break;
+    }
+    default: memset(out, 0, sizeof(float) * (size_t)n);
+    }
+}
+
+/* requant (_quant_int8 :72-83 per row, scalar for 1-D; _quant_4bit :122-141). */
+static void mom_store_quant(const KoTensor* t, const float* mf) {
+    int64_t n = t->R * t->C;
+    if (t->codec == KO_MOM_INT8) {
+        int8_t* q = (int8_t*)t->m;
+        int64_t rows = t->factored ? t->R : 1, cols = t->factored ? t->C : n;
+        for (int64_t r = 0; r < rows; ++r) {
+            float amax = 0.0f;
+            for (int64_t j = 0; j < cols; ++j) amax = fmaxf(amax, fabsf(mf[r * cols + j]));
+            amax = fmaxf(amax, 1e-12f);
+            float sc = amax / 127.0f;
+            t->m_scale[r] = sc;
+            for (int64_t j = 0; j < cols; ++j) {
+                float x = rintf(mf[r * cols + j] / sc);
+                x = fminf(fmaxf(x, -127.0f), 127.0f);
+                q[r * cols + j] = (int8_t)x;
+            }
+        }
+    } else if (t->codec == KO_MOM_4BIT) {
+        uint8_t* pk = (uint8_t*)t->m;
+        int64_t B = t->block4;
+        int64_t nb = (n + B - 1) / B;
+        for (int64_t b = 0; b < nb; ++b) {
+            float amax = 0.0f;
+            for (int64_t i = b * B; i < (b + 1) * B && i < n; ++i) amax = fmaxf(amax, fabsf(mf[i]));
+            amax = fmaxf(amax, 1e-12f);
+            t->m_scale[b] = amax / 7.0f;
+        }
+        memset(pk, 0, (size_t)((n + 1) / 2));
+        for (int64_t i = 0; i < n; ++i) {
+            float x = rintf(mf[i] / t->m_scale[i / B]);
+            x = fminf(fmaxf(x, -7.0f), 7.0f);
+            uint8_t nib = (uint8_t)((int)x + 8);
+            pk[i >> 1] |= (uint8_t)((i & 1) ? (nib << 4) : nib);
+        }
+    } else if (t->codec == KO_MOM_F32) {
+        memcpy(t->m, mf, sizeof(float) * (size_t)n);
+    } else if (t->codec == KO_MOM_BF16) {
+        for (int64_t i = 0; i < n; ++i) ((uint16_t*)t->m)[i] = f_to_bf16(mf[i]);
+    }
+}
+
+/* Codec EMA for Adakaon / AdaMuon (momentum of `upd`, returns delta).
+ * Float codecs lerp in the storage dtype (_momentum_codec.py:266-269);
+ * quantized codecs lerp the fp32 dequant and return the PRE-requant value
+ * (:303-308, :363-371). */
+static void codec_ema(const KoTensor* t, const float* upd, float w1, float* delta) {
+    int64_t n = t->R * t->C;
+    if (t->codec == KO_MOM_BF16) {
+        uint16_t* m = (uint16_t*)t->m;
+        for (int64_t i = 0; i < n; ++i) {
+            float nm = ko_lerp(bf16_to_f(m[i]), round_bf16(upd[i]), w1);
+            m[i] = f_to_bf16(nm);
+            delta[i] = bf16_to_f(m[i]);
+        }
+        return;
+    }
+    if (t->codec == KO_MOM_F32) {
+        float* m = (float*)t->m;
+        for (int64_t i = 0; i < n; ++i) { m[i] = ko_lerp(m[i], upd[i], w1); delta[i] = m[i]; }
+        return;
+    }
+    mom_dequant(t, delta);
+    for (int64_t i = 0; i < n; ++i) delta[i] = ko_lerp(delta[i], upd[i], w1);
+    mom_store_quant(t, delta);
+}
+
+/* ------------------------------------------------------- weight write */
+/* cautious_one_ (src/kaon/_backend.py:139-142): mask = delta*g > 0,
+ * delta = delta*mask / max(mean(mask), 1e-8).  The count is exact. */
+static void cautious(float* delta, const float* g, int64_t n) {
+    int64_t cnt = 0;
+    for (int64_t i = 0; i < n; ++i) cnt += (delta[i] * g[i] > 0.0f);
+    float mean = (float)cnt / (float)n;
+    float den = fmaxf(mean, 1e-8f);
+    for (int64_t i = 0; i < n; ++i) {
+        float mk = (delta[i] * g[i] > 0.0f) ? 1.0f : 0.0f;
+        delta[i] = (delta[i] * mk) / den;
+    }
+}
+
+/* subtract_one_ (src/kaon/_backend.py:82-98): p -= delta. */
+static void write_sub(const KoTensor* t, const float* delta, const KoHyper* h, uint32_t stream) {
+    int64_t n = t->R * t->C;
+    if (t->p_dtype == KO_F32) {
+        float* p = (float*)t->p;
+        for (int64_t i = 0; i < n; ++i) p[i] = p[i] - delta[i];
+        return;
+    }
+    uint16_t* p = (uint16_t*)t->p;
+    if (h->bf16_method == KO_SR) {
+        for (int64_t i = 0; i < n; ++i) {
+            float x = bf16_to_f(p[i]) - delta[i];
+            p[i] = sr_bf16(x, sr_noise(h->seed, h->step, t->tensor_id, stream, i, t->noise[stream]));
+        }
+    } else if (h->bf16_method == KO_RN) {
+        for (int64_t i = 0; i < n; ++i)
+            p[i] = f_to_bf16(bf16_to_f(p[i]) - bf16_to_f(f_to_bf16(delta[i])));
+    } else { /* kahan: shift -= bf16(delta); p0 = p; p += shift; shift += p0 - p */
+        uint16_t* sh = t->shift;
+        for (int64_t i = 0; i < n; ++i) {
+            float s = round_bf16(bf16_to_f(sh[i]) - round_bf16(delta[i]));
+            float p0 = bf16_to_f(p[i]);
+            float p1 = round_bf16(p0 + s);
+            p[i] = f_to_bf16(p1);
+            sh[i] = f_to_bf16(s + round_bf16(p0 - p1));
+        }
+    }
+}
+
+/* add_stochastic_(p, e, alpha=1) / fp32 p += e (msam.py:231-235). */
+static void write_add(const KoTensor* t, const float* e, const KoHyper* h, uint32_t stream) {
+    int64_t n = t->R * t->C;
+    if (t->p_dtype == KO_F32) {
+        float* p = (float*)t->p;
+        for (int64_t i = 0; i < n; ++i) p[i] = p[i] + e[i];
+        return;
+    }
+    uint16_t* p = (uint16_t*)t->p;
+    for (int64_t i = 0; i < n; ++i) {
+        float x = bf16_to_f(p[i]) + e[i];
+        p[i] = sr_bf16(x, sr_noise(h->seed, h->step, t->tensor_id, stream, i, t->noise[stream]));
+    }
+}
+
+/* MSAM norm="none" perturbation (msam.py:223-235):
+ * e = clamp(nan_to_num(m * factor, 0, +b, -b), -b, b); p += e. */
+static void msam_apply(const KoTensor* t, const KoHyper* h, float factor, float bound, uint32_t stream) {
+    int64_t n = t->R * t->C;
+    float* e = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    mom_dequant(t, e);
+    for (int64_t i = 0; i < n; ++i) {
+        float x = e[i] * factor;
+        if (isnan(x)) x = 0.0f;
+        else if (isinf(x)) x = x > 0 ? bound : -bound;
+        x = fminf(fmaxf(x, -bound), bound);
+        e[i] = x;
+    }
+    write_add(t, e, h, stream);
+    free(e);
+}
+
+int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bound, uint32_t stream) {
+    msam_apply(t, h, (float)factor, (float)bound, stream);
+    return 0;
+}
+
+/* ------------------------------------------------ factored second moment */
+/* update_factored_state + factored_inv_sqrt_factors (src/kaon/_factored.py)
+ * on x [R, C]; returns U = (x * r) * c in `u`. */
+static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u) {
+    int64_t R = t->R, C = t->C;
+    float* q = (float*)malloc(sizeof(float) * (size_t)C);
+    float* colacc = (float*)calloc((size_t)C, sizeof(float));
+    float* colsum = (float*)calloc((size_t)C, sizeof(float));
+    for (int64_t r = 0; r < R; ++r) {
+        for (int64_t j = 0; j < C; ++j) {
+            float v = x[r * C + j] * x[r * C + j];
+            if (add_eps) v = v + eps1f;
+            q[j] = v;
+            colacc[j] = colacc[j] + v;
+        }
+        float rmean = ko_csum(q, C) / (float)C;
+        t->row[r] = ko_lerp(t->row[r], rmean, w2);
+        if ((r + 1) % KAON_COLGROUP == 0 || r + 1 == R) {
+            for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + colacc[j]; colacc[j] = 0.0f; }
+        }
+    }
+    float* cf = (float*)malloc(sizeof(float) * (size_t)C);
+    for (int64_t j = 0; j < C; ++j) {
+        t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
+        cf[j] = ko_rsqrt(t->col[j]);
+    }
+    float rm = ko_csum(t->row, R) / (float)R;
+    for (int64_t r = 0; r < R; ++r) {
+        float rf = ko_rsqrt(t->row[r] / rm);
+        for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf) * cf[j];
+    }
+    free(q); free(colacc); free(colsum); free(cf);
+}
+
+/* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):
+ * u /= max((||u|| / sqrt(n)) / clip, 1); u *= scale. */
+static void clip_scale(const KoTensor* t, float* u, double clip, float scale) {
+    int64_t R = t->R, C = t->C, n = R * C;
+    float* rs = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
+    float* sq = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+    for (int64_t r = 0; r < R; ++r) {
+        for (int64_t j = 0; j < C; ++j) sq[j] = u[r * C + j] * u[r * C + j];
+        rs[r] = ko_csum(sq, C);
+    }
+    float ss = ko_csum(rs, R);
+    float rmsv = sqrtf(ss) / (float)sqrt((double)(n > 1 ? n : 1));
+    float fac = fmaxf(rmsv / (float)clip, 1.0f);
+    if (t->fac_override) fac = *t->fac_override;
+    for (int64_t i = 0; i < n; ++i) u[i] = (u[i] / fac) * scale;
+    free(rs); free(sq);
+}
+
+/* ------------------------------------------------------------- Adakaon */
+int ko_adakaon_tensor(const KoTensor* t, const KoHyper* h) {
+    int64_t n = t->R * t->C;
+    if (n <= 0) return 0;
+    float w1 = (float)(1.0 - h->beta1), w2 = (float)(1.0 - h->beta2);
+    float eps1f = (float)h->eps1;
+    float* g = centralized_grad(t, h->gc);
+    float* u = (float*)malloc(sizeof(float) * (size_t)n);
+    float* d = (float*)malloc(sizeof(float) * (size_t)n);
+
+    /* Nekaon removal of the previous climb, at the old momentum, before
+     * the inner step reads p (msam.py:386-388, 202-235; rho = -k so the
+     * removal factor is (-1) * (-k) = k). */
+    if (h->nk_remove) msam_apply(t, h, (float)(h->nk_k), (float)h->nk_bound_old, 0);
+
+    if (t->factored) {
+        factored_update(t, g, w2, eps1f, h->eps1 > 0, u);
+    } else {
+        for (int64_t i = 0; i < n; ++i) {
+            float q = g[i] * g[i];
+            if (h->eps1 > 0) q = q + eps1f;
+            t->v[i] = ko_lerp(t->v[i], q, w2);
+            u[i] = g[i] * ko_rsqrt(t->v[i]);
+        }
+    }
+    clip_scale(t, u, h->clip, (float)h->lr);
+    if (h->beta1 > 0 && t->codec != KO_MOM_NONE) codec_ema(t, u, w1, d);
+    else memcpy(d, u, sizeof(float) * (size_t)n);
+    if (h->wd != 0) {
+        float a = (float)(h->lr * h->wd);
+        for (int64_t i = 0; i < n; ++i) d[i] = fmaf(a, load_p(t, i), d[i]);
+    }
+    if (h->cautious) cautious(d, g, n);
+    write_sub(t, d, h, 1);
+
+    /* Nekaon climb along the requantized new momentum (factor -k). */
+    if (h->nk_climb) msam_apply(t, h, (float)(-h->nk_k), (float)h->nk_bound_new, 2);
+    free(g); free(u); free(d);
+    return 0;
+}
+
+/* ---------------------------------------------------------------- Lion */
+int ko_lion_tensor(const KoTensor* t, const KoHyper* h) {
+    int64_t n = t->R * t->C;
+    if (n <= 0) return 0;
+    float* g = centralized_grad(t, h->gc);
+    float* m = (float*)malloc(sizeof(float) * (size_t)n);
+    float* d = (float*)malloc(sizeof(float) * (size_t)n);
+    float b1 = (float)h->beta1, b2 = (float)h->beta2;
+    float a1 = (float)(1.0 - h->beta1), a2 = (float)(1.0 - h->beta2);
+    mom_dequant(t, m);
+    for (int64_t i = 0; i < n; ++i) {
+        float c = fmaf(a1, g[i], m[i] * b1);
+        d[i] = ko_sign(c);
+        m[i] = fmaf(a2, g[i], m[i] * b2);
+    }
+    /* _store_one: float codecs copy_ the fp32 value, quantized requant */
+    if (t->codec == KO_MOM_F32) memcpy(t->m, m, sizeof(float) * (size_t)n);
+    else if (t->codec == KO_MOM_BF16)
+        for (int64_t i = 0; i < n; ++i) ((uint16_t*)t->m)[i] = f_to_bf16(m[i]);
+    else mom_store_quant(t, m);
+    if (h->wd != 0) {
+        float a = (float)h->wd;
+        for (int64_t i = 0; i < n; ++i) d[i] = fmaf(a, load_p(t, i), d[i]);
+    }
+    if (h->cautious) cautious(d, g, n);
+    float lr = (float)h->lr;
+    for (int64_t i = 0; i < n; ++i) d[i] = d[i] * lr;
+    write_sub(t, d, h, 1);
+    free(g); free(m); free(d);
+    return 0;
+}
+
+/* ------------------------------------------------------------- AdaMuon */
+/* bf16 GEMM with fp32 accumulation in k order, result rounded to bf16.
+ * C[M,N] = A[M,K] * B[K,N] (row-major float arrays holding bf16 values). */
+static void gemm_bf16(const float* A, const float* B, float* Cm, int64_t M, int64_t K, int64_t N) {
+    float* acc = (float*)malloc(sizeof(float) * (size_t)N);
+    for (int64_t i = 0; i < M; ++i) {
+        for (int64_t j = 0; j < N; ++j) acc[j] = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float a = A[i * K + k];
+            const float* br = B + k * N;
+            for (int64_t j = 0; j < N; ++j) acc[j] = fmaf(a, br[j], acc[j]);
+        }
+        for (int64_t j = 0; j < N; ++j) Cm[i * N + j] = round_bf16(acc[j]);
+    }
+    free(acc);
+}
+
+/* zeropower_via_newtonschulz5 (adamuon.py:97-118) on x [R, C]; every torch
+ * op on bf16 tensors rounds to bf16.  out[R*C] gets the fp32 view of the
+ * bf16 result in the original orientation. */
+void ko_newton_schulz(const float* xin, int64_t R, int64_t C, int32_t steps, float* out) {
+    const float a = 3.4445f, b = -4.7750f, c = 2.0315f;
+    int tr = R > C;
+    int64_t m = tr ? C : R, k = tr ? R : C;
+    float* x = (float*)malloc(sizeof(float) * (size_t)(m * k));
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < k; ++j)
+            x[i * k + j] = round_bf16(tr ? xin[j * C + i] : xin[i * C + j]);
+    /* x / (x.norm() + 1e-7): norm of a bf16 tensor -> bf16, + scalar -> bf16 */
+    double ss = 0.0;
+    for (int64_t i = 0; i < m * k; ++i) ss += (double)x[i] * (double)x[i];
+    float nrm = round_bf16((float)sqrt(ss));
+    float den = round_bf16(nrm + 1e-7f);
+    for (int64_t i = 0; i < m * k; ++i) x[i] = round_bf16(x[i] / den);
+    float* xt = (float*)malloc(sizeof(float) * (size_t)(m * k));
+    float* A = (float*)malloc(sizeof(float) * (size_t)(m * m));
+    float* A2 = (float*)malloc(sizeof(float) * (size_t)(m * m));
+    float* Bm = (float*)malloc(sizeof(float) * (size_t)(m * m));
+    float* BX = (float*)malloc(sizeof(float) * (size_t)(m * k));
+    for (int s = 0; s < steps; ++s) {
+        for (int64_t i = 0; i < m; ++i)
+            for (int64_t j = 0; j < k; ++j) xt[j * m + i] = x[i * k + j];
+        gemm_bf16(x, xt, A, m, k, m);                  /* A = x @ x.mT */
+        gemm_bf16(A, A, A2, m, m, m);                  /* A @ A */
+        for (int64_t i = 0; i < m * m; ++i)            /* B = b*A + c*(A@A) */
+            Bm[i] = round_bf16(round_bf16(b * A[i]) + round_bf16(c * A2[i]));
+        gemm_bf16(Bm, x, BX, m, m, k);                 /* B @ x */
+        for (int64_t i = 0; i < m * k; ++i)            /* x = a*x + B@x */
+            x[i] = round_bf16(round_bf16(a * x[i]) + BX[i]);
+    }
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < k; ++j) {
+            if (tr) out[j * C + i] = x[i * k + j];
+            else out[i * C + j] = x[i * k + j];
+        }
+    free(x); free(xt); free(A); free(A2); free(Bm); free(BX);
+}
+
+int ko_adamuon_tensor(const KoTensor* t, const KoHyper* h) {
+    int64_t n = t->R * t->C;
+    if (n <= 0) return 0;
+    float w1 = (float)(1.0 - h->beta1), w2 = (float)(1.0 - h->beta2);
+    float eps1f = (float)h->eps1;
+    float scale = (float)(0.2 * h->lr);
+    float* g = centralized_grad(t, h->gc);
+    float* u = (float*)malloc(sizeof(float) * (size_t)n);
+    float* d = (float*)malloc(sizeof(float) * (size_t)n);
+    if (t->factored) {
+        float* mm = (float*)malloc(sizeof(float) * (size_t)n);
+        if (h->beta1 > 0 && t->codec != KO_MOM_NONE) codec_ema(t, g, w1, mm);
+        else memcpy(mm, g, sizeof(float) * (size_t)n);
+        float* o = (float*)malloc(sizeof(float) * (size_t)n);
+        ko_newton_schulz(mm, t->R, t->C, h->ns_steps, o);
+        if (t->out_m) memcpy(t->out_m, o, sizeof(float) * (size_t)n);
+        factored_update(t, o, w2, eps1f, h->eps1 > 0, u);
+        clip_scale(t, u, h->clip, scale);
+        memcpy(d, u, sizeof(float) * (size_t)n);
+        free(mm); free(o);
+    } else {
+        for (int64_t i = 0; i < n; ++i) {
+            float q = g[i] * g[i];
+            if (h->eps1 > 0) q = q + eps1f;
+            t->v[i] = ko_lerp(t->v[i], q, w2);
+            u[i] = g[i] * ko_rsqrt(t->v[i]);
+        }
+        clip_scale(t, u, h->clip, scale);
+        if (h->beta1 > 0 && t->codec != KO_MOM_NONE) codec_ema(t, u, w1, d);
+        else memcpy(d, u, sizeof(float) * (size_t)n);
+    }
+    if (h->wd != 0) {
+        float a = (float)(h->lr * h->wd);
+        for (int64_t i = 0; i < n; ++i) d[i] = fmaf(a, load_p(t, i), d[i]);
+    }
+    if (h->cautious) cautious(d, g, n);
+    write_sub(t, d, h, 1);
+    free(g); free(u); free(d);
+    return 0;
+}
+
+/* ----------------------------------------------- standalone codec entry */
+/* _quant_int8 on a [rows, cols] fp32 array (rows = 1 for a 1-D param). */
+void ko_quant_int8(const float* mf, int64_t rows, int64_t cols, int8_t* q, float* scale) {
+    KoTensor t;
+    memset(&t, 0, sizeof t);
+    t.R = rows; t.C = cols; t.factored = 1; t.codec = KO_MOM_INT8; t.m = q; t.m_scale = scale;
+    mom_store_quant(&t, mf);
+}
+
+void ko_quant_4bit(const float* mf, int64_t n, int32_t block, uint8_t* packed, float* scale) {
+    KoTensor t;
+    memset(&t, 0, sizeof t);
+    t.R = 1; t.C = n; t.factored = 0; t.codec = KO_MOM_4BIT; t.block4 = block; t.m = packed; t.m_scale = scale;
+    mom_store_quant(&t, mf);
+}
+
+void ko_dequant(int32_t codec, const void* m, const float* scale, int64_t rows, int64_t cols,
+                int32_t block, float* out) {
+    KoTensor t;
+    memset(&t, 0, sizeof t);
+    t.R = rows; t.C = cols; t.factored = 1; t.codec = codec; t.block4 = block;
+    t.m = (void*)m; t.m_scale = (float*)scale;
+    mom_dequant(&t, out);
+}
+
+/* SR of a fp32 array into bf16 with explicit noise (unit tests, bias study). */
+void ko_sr_round(const float* x, const uint16_t* noise, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = sr_bf16(x[i], noise[i]);
+}
+
+int32_t ko_abi_version(void) { return 1; }
+
+/* ------------------------------------------------ primitive test entries */
+/* Elementwise entry points so tests can pin the rounding model against torch. */
+void ko_vec_lerp(const float* a, const float* b, float w, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ko_lerp(a[i], b[i], w);
+}
+
+/* bf16 gradient centralization of a [R, C] bf16 array (bits in, bits out). */
+void ko_vec_gc_bf16(const uint16_t* g, int64_t R, int64_t C, uint16_t* out) {
+    KoTensor t;
+    memset(&t, 0, sizeof t);
+    t.g = (void*)g; t.R = R; t.C = C; t.g_dtype = KO_BF16; t.factored = 1;
+    float* c = centralized_grad(&t, 1);
+    for (int64_t i = 0; i < R * C; ++i) out[i] = f_to_bf16(c[i]);
+    free(c);
+}

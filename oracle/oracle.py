@@ -1,0 +1,399 @@
+"""CPU parity oracle for the kaon fused optimizer step.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker (or as the timed CPU baseline); the product path
+(``k-optimizers_amd/kaon_amd``) never imports it and fails loudly without its
+HIP library.
+
+This wraps ``kaon_oracle.c`` (the per-tensor restatement of the reference
+step, see the header of that file for the reference citations and the
+rounding / reduction-order model) with numpy state that mirrors the
+reference's per-parameter state layout:
+
+* Adakaon ``_init_state``  -- src/kaon/adakaon.py:318-335
+* Lion ``_init_state``     -- src/kaon/lion.py:210-241
+* AdaMuon ``_init_state``  -- src/kaon/adamuon.py:297-316
+* codec ``init_state``     -- src/kaon/_momentum_codec.py:263-264, 296-301, 351-361
+* MSAM / Nekaon lookahead  -- src/kaon/msam.py:169-188, 375-406; src/kaon/nekaon.py:162-171
+
+Arrays: bf16 tensors are ``np.uint16`` bit patterns, fp32 are ``np.float32``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
+
+F32, BF16 = 0, 1
+MOM_CODE = {"none": 0, "float32": 1, "bfloat16": 2, "int8": 3, "4bit": 4}
+BF16_METHOD = {"stochastic_rounding": 0, "none": 1, "kahan": 2}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+class KoTensor(ctypes.Structure):
+    _fields_ = [
+        ("g", ctypes.c_void_p), ("p", ctypes.c_void_p), ("m", ctypes.c_void_p),
+        ("m_scale", ctypes.c_void_p), ("row", ctypes.c_void_p), ("col", ctypes.c_void_p),
+        ("v", ctypes.c_void_p), ("shift", ctypes.c_void_p),
+        ("R", ctypes.c_int64), ("C", ctypes.c_int64),
+        ("g_dtype", ctypes.c_int32), ("p_dtype", ctypes.c_int32),
+        ("codec", ctypes.c_int32), ("block4", ctypes.c_int32),
+        ("factored", ctypes.c_int32), ("tensor_id", ctypes.c_uint32),
+        ("noise", ctypes.c_void_p * 3),
+        ("out_m", ctypes.c_void_p),
+        ("fac_override", ctypes.c_void_p),
+    ]
+
+
+class KoHyper(ctypes.Structure):
+    _fields_ = [
+        ("lr", ctypes.c_double), ("beta1", ctypes.c_double), ("beta2", ctypes.c_double),
+        ("eps1", ctypes.c_double), ("wd", ctypes.c_double), ("clip", ctypes.c_double),
+        ("cautious", ctypes.c_int32), ("gc", ctypes.c_int32), ("bf16_method", ctypes.c_int32),
+        ("ns_steps", ctypes.c_int32),
+        ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
+        ("nk_remove", ctypes.c_int32), ("nk_climb", ctypes.c_int32),
+        ("nk_k", ctypes.c_double), ("nk_bound_old", ctypes.c_double), ("nk_bound_new", ctypes.c_double),
+    ]
+
+
+_lib_handle = None
+
+
+def lib() -> ctypes.CDLL:
+    """The compiled oracle (``make -C oracle``; ``__graft_entry__.build()`` runs it)."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run `make -C oracle`)")
+        L = ctypes.CDLL(_LIB_PATH)
+        for name in ("ko_adakaon_tensor", "ko_lion_tensor", "ko_adamuon_tensor"):
+            getattr(L, name).argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper)]
+            getattr(L, name).restype = ctypes.c_int
+        L.ko_msam_apply.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
+                                    ctypes.c_double, ctypes.c_double, ctypes.c_uint32]
+        L.ko_csum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        L.ko_csum.restype = ctypes.c_float
+        L.ko_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.ko_sr_noise_fill.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64,
+                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        L.ko_quant_int8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+        L.ko_quant_4bit.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+        L.ko_dequant.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                 ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+        L.ko_sr_round.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        L.ko_newton_schulz.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_int32, ctypes.c_void_p]
+        L.ko_vec_lerp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_int64,
+                                  ctypes.c_void_p]
+        L.ko_vec_gc_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        _lib_handle = L
+    return _lib_handle
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------------ bf16 helpers
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even, NaN -> 0x7FC0."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------------ primitives
+def csum(x: np.ndarray) -> np.float32:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return np.float32(lib().ko_csum(_ptr(x), x.size))
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.asarray(ctr, dtype=np.uint32).copy()
+    k = np.asarray(key, dtype=np.uint32).copy()
+    out = np.zeros(4, dtype=np.uint32)
+    lib().ko_philox4x32_10(_ptr(c), _ptr(k), _ptr(out))
+    return out
+
+
+def sr_noise(n: int, seed: int, step: int, tensor_id: int, stream: int) -> np.ndarray:
+    out = np.zeros(max(n, 1), dtype=np.uint16)
+    lib().ko_sr_noise_fill(_ptr(out), n, seed, step, tensor_id, stream)
+    return out[:n]
+
+
+def sr_round(x: np.ndarray, noise: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    noise = np.ascontiguousarray(noise, dtype=np.uint16)
+    out = np.zeros(x.size, dtype=np.uint16)
+    lib().ko_sr_round(_ptr(x), _ptr(noise), x.size, _ptr(out))
+    return out.reshape(x.shape)
+
+
+def quant_int8(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """_quant_int8 (src/kaon/_momentum_codec.py:72-83): per-row for ndim>=2, scalar for 1-D."""
+    m = np.ascontiguousarray(m, dtype=np.float32)
+    rows = m.shape[0] if m.ndim >= 2 else 1
+    cols = m.size // max(rows, 1)
+    q = np.zeros(m.shape, dtype=np.int8)
+    sc = np.zeros(rows, dtype=np.float32)
+    lib().ko_quant_int8(_ptr(m), rows, cols, _ptr(q), _ptr(sc))
+    return q, sc
+
+
+def quant_4bit(m: np.ndarray, block: int) -> tuple[np.ndarray, np.ndarray]:
+    """_quant_4bit (src/kaon/_momentum_codec.py:122-141)."""
+    m = np.ascontiguousarray(m, dtype=np.float32).reshape(-1)
+    n = m.size
+    nb = (n + block - 1) // block
+    pk = np.zeros((n + 1) // 2, dtype=np.uint8)
+    sc = np.zeros(nb, dtype=np.float32)
+    lib().ko_quant_4bit(_ptr(m), n, block, _ptr(pk), _ptr(sc))
+    return pk, sc
+
+
+def dequant(codec: str, m: np.ndarray, scale: np.ndarray | None, shape, block: int = 0) -> np.ndarray:
+    n = int(np.prod(shape)) if len(shape) else 1
+    rows = shape[0] if len(shape) >= 2 else 1
+    cols = n // max(rows, 1)
+    out = np.zeros(max(n, 1), dtype=np.float32)
+    lib().ko_dequant(MOM_CODE[codec], _ptr(np.ascontiguousarray(m)),
+                     _ptr(None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)),
+                     rows, cols, block, _ptr(out))
+    return out[:n].reshape(shape)
+
+
+def lerp(a: np.ndarray, b: np.ndarray, w: float) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.zeros_like(a)
+    lib().ko_vec_lerp(_ptr(a), _ptr(b), float(np.float32(w)), a.size, _ptr(out))
+    return out
+
+
+def gc_bf16(g_bits: np.ndarray) -> np.ndarray:
+    """Gradient centralization of a bf16 [R, C] array (bits), in the grad dtype."""
+    g = np.ascontiguousarray(g_bits, dtype=np.uint16)
+    R = g.shape[0]
+    C = g.size // R
+    out = np.zeros_like(g)
+    lib().ko_vec_gc_bf16(_ptr(g), R, C, _ptr(out))
+    return out
+
+
+def newton_schulz(x: np.ndarray, steps: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    lib().ko_newton_schulz(_ptr(x), x.shape[0], x.shape[1], steps, _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------------ parameters
+def fourbit_block_size(numel: int, bs: int) -> int:
+    """src/kaon/_momentum_codec.py:192-200."""
+    return numel if bs <= 0 else (min(bs, numel) if numel > 0 else 1)
+
+
+@dataclass
+class OParam:
+    """One parameter, its gradient and its optimizer state, as numpy arrays."""
+
+    p: np.ndarray                 # uint16 (bf16 bits) or float32, param shape
+    p_dtype: int
+    shape: tuple[int, ...]
+    tensor_id: int = 0
+    g: np.ndarray | None = None   # uint16 or float32, param shape
+    g_dtype: int = BF16
+    state: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def numel(self) -> int:
+        return int(np.prod(self.shape)) if len(self.shape) else 1
+
+    @property
+    def factored(self) -> bool:
+        return len(self.shape) >= 2
+
+    @property
+    def eff(self) -> tuple[int, int]:
+        if self.factored:
+            return self.shape[0], self.numel // self.shape[0]
+        return 1, self.numel
+
+
+def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
+    st = prm.state
+    R, C = prm.eff
+    n = prm.numel
+    if opt in ("adakaon", "adamuon"):
+        if prm.factored:
+            st["row"] = np.zeros(R, dtype=np.float32)
+            st["col"] = np.zeros(C, dtype=np.float32)
+        else:
+            st["v"] = np.zeros(n, dtype=np.float32)
+    md = group["momentum_dtype"]
+    if group["betas"][0] > 0 or opt == "lion":
+        if md == "float32":
+            st["m"] = np.zeros(prm.shape, dtype=np.float32)
+        elif md == "bfloat16":
+            st["m"] = np.zeros(prm.shape, dtype=np.uint16)
+        elif md == "int8":
+            st["m"] = np.zeros(prm.shape, dtype=np.int8)
+            st["m_scale"] = np.ones(R if prm.factored else 1, dtype=np.float32)
+        else:
+            bs = fourbit_block_size(n, group["momentum_4bit_block"])
+            st["m"] = np.full((n + 1) // 2, 0x88, dtype=np.uint8)
+            st["m_scale"] = np.ones((n + bs - 1) // bs, dtype=np.float32)
+            st["m_numel"] = n
+            st["m_block"] = bs
+    if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+        st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
+
+
+def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) -> KoTensor:
+    st = prm.state
+    R, C = prm.eff
+    t = KoTensor()
+    t.g = _ptr(prm.g)
+    t.p = _ptr(prm.p)
+    t.m = _ptr(st.get("m"))
+    t.m_scale = _ptr(st.get("m_scale"))
+    t.row = _ptr(st.get("row"))
+    t.col = _ptr(st.get("col"))
+    t.v = _ptr(st.get("v"))
+    t.shift = _ptr(st.get("shift"))
+    t.R, t.C = R, C
+    t.g_dtype, t.p_dtype = prm.g_dtype, prm.p_dtype
+    t.codec = MOM_CODE[codec] if "m" in st else 0
+    t.block4 = int(st.get("m_block", 0))
+    t.factored = int(prm.factored)
+    t.tensor_id = prm.tensor_id
+    if noise is not None:
+        for s in range(3):
+            if noise[s] is not None:
+                t.noise[s] = _ptr(noise[s])
+    t.out_m = _ptr(out_m)
+    t.fac_override = _ptr(fac_override)
+    return t
+
+
+def _hyper(group: dict[str, Any], seed: int, step: int) -> KoHyper:
+    h = KoHyper()
+    h.lr = group["lr"]
+    h.beta1, h.beta2 = group["betas"]
+    eps = group.get("eps", (0.0, 0.0))
+    h.eps1 = eps[0]
+    h.wd = group.get("weight_decay", 0.0)
+    h.clip = group.get("clip_threshold", 1.0)
+    h.cautious = int(group.get("cautious", True))
+    h.gc = int(group.get("gradient_centralization", True))
+    h.bf16_method = BF16_METHOD[group.get("bf16_method", "stochastic_rounding")]
+    h.ns_steps = int(group.get("ns_steps", 2))
+    h.seed = seed
+    h.step = step
+    return h
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"oracle returned {rc}")
+
+
+class OracleOptimizer:
+    """Step driver over a list of OParam for one param group.
+
+    ``opt`` is ``"adakaon" | "lion" | "adamuon" | "nekaon"``.  Nekaon is the MSAM
+    ``norm="none"``, ``rho=-k`` preset over Adakaon (src/kaon/nekaon.py:162-171):
+    the removal of the previous climb and the new climb are folded into the
+    per-tensor step exactly where MSAM.step runs them (msam.py:384-403).
+    """
+
+    def __init__(self, params: list[OParam], opt: str, group: dict[str, Any], seed: int = 0) -> None:
+        self.params = params
+        self.opt = opt
+        self.group = dict(group)
+        self.seed = seed
+        self.t = 0
+        self.has_e = False
+        self.bound = 0.0   # frozen climb bound (msam.py:169-188)
+        self.k = float(group.get("k", 0.0))
+        for prm in params:
+            init_state(prm, "adakaon" if opt == "nekaon" else opt, self.group)
+
+    def step(self, noise: dict[int, list] | None = None, fac_override: dict[int, np.ndarray] | None = None) -> None:
+        self.t += 1
+        h = _hyper(self.group, self.seed, self.t)
+        md = self.group["momentum_dtype"]
+        if self.opt == "nekaon":
+            h.nk_remove = int(self.has_e)
+            h.nk_bound_old = self.bound
+            new_bound = abs(self.k) * self.group.get("clip_threshold", 1.0) * self.group["lr"]
+            h.nk_climb = int(self.k != 0.0)
+            h.nk_k = self.k
+            h.nk_bound_new = new_bound
+        for prm in self.params:
+            t = _tensor(prm, md, None if noise is None else noise.get(prm.tensor_id),
+                        fac_override=None if fac_override is None else fac_override.get(prm.tensor_id))
+            if self.opt in ("adakaon", "nekaon"):
+                _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
+            elif self.opt == "lion":
+                _check(lib().ko_lion_tensor(ctypes.byref(t), ctypes.byref(h)))
+            elif self.opt == "adamuon":
+                _check(lib().ko_adamuon_tensor(ctypes.byref(t), ctypes.byref(h)))
+            else:
+                raise ValueError(self.opt)
+        if self.opt == "nekaon" and self.k != 0.0:
+            self.has_e = True
+            self.bound = h.nk_bound_new
+
+    def msam_apply(self, sign: float, noise: dict[int, list] | None = None) -> None:
+        """MSAM._apply(sign) with the frozen bound (eval(): sign=-1; train(): +1)."""
+        h = _hyper(self.group, self.seed, self.t)
+        factor = sign * (-self.k)
+        stream = 0 if sign < 0 else 2
+        for prm in self.params:
+            t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
+            lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), factor, self.bound, stream)
+
+
+def make_param(shape, p_dtype=BF16, g_dtype=BF16, tensor_id=0, *, p_values=None, g_values=None) -> OParam:
+    shape = tuple(int(s) for s in shape)
+    def conv(v, dt):
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(shape)
+        return f32_to_bf16(v).reshape(shape) if dt == BF16 else v.copy()
+    prm = OParam(p=conv(p_values, p_dtype), p_dtype=p_dtype, shape=shape, tensor_id=tensor_id,
+                 g_dtype=g_dtype)
+    if g_values is not None:
+        prm.g = conv(g_values, g_dtype)
+    return prm
+
+
+def values(a: np.ndarray, dtype: int) -> np.ndarray:
+    return bf16_to_f32(a) if dtype == BF16 else a.astype(np.float32)
+
+
+__all__ = [
+    "BF16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "bf16_to_f32", "csum",
+    "dequant", "f32_to_bf16", "fourbit_block_size", "gc_bf16", "init_state", "lerp", "lib", "make_param",
+    "newton_schulz", "philox4x32_10", "quant_4bit", "quant_int8", "sr_noise", "sr_round", "values",
+]
+_ = math

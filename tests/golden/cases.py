@@ -1,0 +1,89 @@
+"""Golden-case definitions and their deterministic inputs.
+
+Shared by ``make_golden.py`` (which steps the reference on them) and the
+oracle tests (which step the oracle / the HIP path on the same bytes).
+Inputs come from numpy's PCG64 keyed by (case seed, tensor index, step):
+weights ~ N(0, 0.02^2) (the reference's ktune convention, src/kaon/tune.py:72),
+gradients ~ N(0, sigma^2) with a per-tensor sigma.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_BASE = dict(steps=5, seed=0, p_dtype="bf16", g_dtype="bf16")
+_SMALL = [[8, 16], [16, 8, 3, 3], [40], [24, 20]]
+_ODD = [[8, 16], [16, 8, 3, 3], [33], [7, 9]]
+
+
+def _case(opt, shapes, kwargs, **kw):
+    c = dict(_BASE)
+    c.update(opt=opt, shapes=shapes, kwargs=kwargs)
+    c.update(kw)
+    return c
+
+
+CASES = {
+    # Adakaon (src/kaon/adakaon.py) -- per-param path for SR, foreach for RN
+    "ada_int8_sr": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01,
+                                                 momentum_dtype="int8", foreach=False)),
+    "ada_4bit_sr": _case("adakaon", _ODD, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="4bit",
+                                               momentum_4bit_block=16, foreach=False)),
+    "ada_bf16_rn": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01,
+                                                 momentum_dtype="bfloat16", bf16_method="none",
+                                                 foreach=True)),
+    "ada_f32_fp32": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.8, 0.99), weight_decay=0.1,
+                                                  momentum_dtype="float32", foreach=True),
+                          p_dtype="f32", g_dtype="f32"),
+    "ada_nomom_sr": _case("adakaon", _SMALL, dict(lr=1e-4, betas=(0.0, 0.999), foreach=False)),
+    "ada_int8_nogc_nocaut": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="int8",
+                                                          cautious=False, gradient_centralization=False,
+                                                          bf16_method="none", foreach=True)),
+    "ada_kahan": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="bfloat16",
+                                               bf16_method="kahan", foreach=False)),
+    # Lion (src/kaon/lion.py)
+    "lion_int8_sr": _case("lion", _SMALL, dict(lr=2e-4, betas=(0.95, 0.98), weight_decay=0.1,
+                                               momentum_dtype="int8", foreach=False)),
+    "lion_4bit_rn": _case("lion", _ODD, dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="4bit",
+                                             momentum_4bit_block=16, bf16_method="none", foreach=True)),
+    "lion_bf16_sr": _case("lion", _SMALL, dict(lr=2e-4, betas=(0.9, 0.99), momentum_dtype="bfloat16",
+                                               foreach=False)),
+    "lion_f32_fp32": _case("lion", _SMALL, dict(lr=1e-3, betas=(0.9, 0.99), weight_decay=0.1,
+                                                momentum_dtype="float32", foreach=True),
+                           p_dtype="f32", g_dtype="f32"),
+    # AdaMuon (src/kaon/adamuon.py) -- bf16 Newton-Schulz: tolerance, not bits
+    "adamuon_int8_sr": _case("adamuon", [[16, 24], [24, 8, 3, 3], [40], [20, 12]],
+                             dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype="int8", ns_steps=2,
+                                  foreach=False)),
+    "adamuon_bf16_rn": _case("adamuon", [[16, 24], [40], [20, 12]],
+                             dict(lr=1e-3, betas=(0.95, 0.999), momentum_dtype="bfloat16", ns_steps=2,
+                                  weight_decay=0.01, bf16_method="none", foreach=False)),
+    # Nekaon = MSAM(norm="none", rho=-k) over Adakaon (src/kaon/nekaon.py, msam.py)
+    "nekaon_4bit_sr": _case("nekaon", _ODD, dict(lr=1e-3, k=1.5, betas=(0.2, 0.999), momentum_dtype="4bit",
+                                                 momentum_4bit_block=64, foreach=False),
+                            eval_train=True),
+    "nekaon_int8_f32": _case("nekaon", _SMALL, dict(lr=1e-3, k=1.5, betas=(0.5, 0.999), momentum_dtype="int8",
+                                                    foreach=False),
+                             p_dtype="f32", g_dtype="f32", eval_train=True),
+}
+
+# Adakaon on a conv [320,320,3,3] and a linear [1280,1280],
+# betas=(0,0.999), lr=1e-4, stochastic rounding, grads N(0, 1e-3^2), 10 steps.
+CFG0 = _case("adakaon", [[320, 320, 3, 3], [1280, 1280]],
+             dict(lr=1e-4, betas=(0.0, 0.999), bf16_method="stochastic_rounding", foreach=False),
+             steps=10, grad_sigma=[1e-3, 1e-3], sample_stride=37)
+
+
+def _sigma(case, i):
+    if "grad_sigma" in case:
+        return case["grad_sigma"][i]
+    return [3e-3, 1e-3, 1e-2, 3e-4, 5e-3][i % 5]
+
+
+def param_values(case, i) -> np.ndarray:
+    rng = np.random.default_rng([case["seed"], i, 0])
+    return (rng.standard_normal(case["shapes"][i]) * 0.02).astype(np.float32)
+
+
+def grad_values(case, i, step) -> np.ndarray:
+    rng = np.random.default_rng([case["seed"], i, step])
+    return (rng.standard_normal(case["shapes"][i]) * _sigma(case, i)).astype(np.float32)

@@ -1,0 +1,156 @@
+"""Pin the oracle's whole-step composition against the reference's own output.
+
+The fixtures under tests/golden/ were written by tests/golden/make_golden.py,
+which steps the reference kaon 0.7.4 (torch CPU, one thread) on seeded inputs
+with the oracle's Philox noise injected into its stochastic-rounding draw.
+
+What must agree:
+* bf16-gradient cases: weights and momentum codes bit-exact except for a tiny
+  fraction of elements where torch's fp32 reduction order differs from the
+  oracle's canonical order (measured: at most 1 element in ~1.2k);
+* fp32 factored / 1-D second-moment state within 1e-6 relative;
+* fp32-gradient cases with gradient centralization: torch's unspecified fp32
+  row-mean order moves the centralized gradient by ulps, so fp32 state and
+  weights agree to 1e-4 relative (cautious-mask flips at |g| ~ 0 dominate);
+* AdaMuon: bf16 Newton-Schulz GEMM accumulation order -> tolerance
+  (the reference's own batched-vs-per-slice tolerance rtol 2e-2, atol 2e-3).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from golden_compare import CASES, CFG0, bf16_mismatch, build_oracle, load_golden, rel_err, run_oracle, set_grads
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+BIT_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "bf16" and c["opt"] != "adamuon"]
+F32_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "f32"]
+MUON_CASES = [k for k, c in CASES.items() if c["opt"] == "adamuon"]
+
+
+def _compare_state(prm, gold, i, tol):
+    for k in ("row", "col", "v"):
+        if f"s{i}_{k}" in gold:
+            assert rel_err(prm.state[k], gold[f"s{i}_{k}"]) <= tol, (k, i)
+
+
+@pytest.mark.parametrize("name", BIT_CASES)
+def test_bf16_cases_match_reference(name):
+    case = CASES[name]
+    gold = load_golden(name)
+    params, _opt, evalp = run_oracle(case)
+    total = diff = 0
+    for i, prm in enumerate(params):
+        nm, _ = bf16_mismatch(prm.p, gold[f"p{i}"])
+        total += prm.p.size
+        diff += nm
+        _compare_state(prm, gold, i, 1e-6)
+        if "m_scale" in prm.state:
+            assert rel_err(prm.state["m_scale"], gold[f"s{i}_m_scale"].reshape(-1)) <= 1e-6
+        if "m" in prm.state:
+            a, b = prm.state["m"].reshape(-1), gold[f"s{i}_m"].reshape(-1)
+            assert (a != b).sum() <= max(1, a.size // 500), (name, i)
+        if evalp is not None:
+            nm2, _ = bf16_mismatch(evalp[i], gold[f"p{i}_eval"])
+            diff += nm2
+            total += prm.p.size
+    assert diff <= max(1, total // 1000), f"{name}: {diff}/{total} weight elements differ"
+
+
+@pytest.mark.parametrize("name", F32_CASES)
+def test_fp32_grad_cases_match_reference(name):
+    case = CASES[name]
+    gold = load_golden(name)
+    params, _opt, evalp = run_oracle(case)
+    for i, prm in enumerate(params):
+        ref = gold[f"p{i}"]
+        assert np.allclose(prm.p, ref, rtol=1e-4, atol=1e-7), (name, i)
+        _compare_state(prm, gold, i, 1e-5)
+        if "m" in prm.state and prm.state["m"].dtype == np.float32:
+            assert np.allclose(prm.state["m"], gold[f"s{i}_m"], rtol=1e-3, atol=1e-8)
+        if evalp is not None:
+            assert np.allclose(evalp[i], gold[f"p{i}_eval"], rtol=1e-4, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", MUON_CASES)
+def test_adamuon_cases_within_ns_tolerance(name):
+    case = CASES[name]
+    gold = load_golden(name)
+    params, _opt, _ = run_oracle(case)
+    for i, prm in enumerate(params):
+        a = O.values(prm.p, prm.p_dtype)
+        b = O.values(gold[f"p{i}"], prm.p_dtype)
+        assert np.allclose(a, b, rtol=2e-2, atol=2e-3)
+        _compare_state(prm, gold, i, 2e-2)
+
+
+def test_cfg0_matches_reference():
+    """10 steps, conv [320,320,3,3] + linear [1280,1280].
+
+    Factored state within 1e-6.  Weights: torch's fp32 ``norm`` (the RMS clip)
+    is off by 1e-5..2.5e-5 relative at these sizes while the canonical order is
+    within 1e-8 of fp64, so the reference's clip factor differs and a small
+    fraction of SR draws land on the other side; each such flip is one bf16 ulp
+    per step.  The sample holds every 37th element.
+    """
+    gold = load_golden("cfg0")
+    params, _opt, _ = run_oracle(CFG0)
+    s = CFG0["sample_stride"]
+    for i, prm in enumerate(params):
+        _compare_state(prm, gold, i, 1e-6)
+        mine = prm.p.reshape(-1)[::s]
+        nm, _ = bf16_mismatch(mine, gold[f"p{i}_sample"])
+        assert nm <= mine.size * 2e-3, (i, nm)
+        a, b = O.bf16_to_f32(mine), O.bf16_to_f32(gold[f"p{i}_sample"])
+        ulp = np.maximum(np.abs(b), 1e-30) * 2.0 ** -7
+        assert np.all(np.abs(a - b) <= CFG0["steps"] * (ulp + 1e-5))
+
+
+def test_cfg0_first_step_exact_given_torch_clip_factor():
+    """With torch's own clip divisor injected, step 1 of configs[0] reproduces the
+    reference's weights (measured: 1 element of 2.56M differs by 1 ulp; the
+    every-37th-element sample must match exactly) -- the remaining composition
+    (bf16 GC, factored EMA, lerp/FMA placement, cautious, SR) is the reference's.
+    Without the injection ~9 sampled elements differ, so the sample separates
+    the two."""
+    import torch
+
+    torch.set_num_threads(1)
+    gold = load_golden("cfg0")
+    case = dict(CFG0)
+    case["steps"] = 1
+    s = CFG0["sample_stride"]
+    for inject in (True, False):
+        params, opt = build_oracle(case)
+        set_grads(case, params, 1)
+        facs = None
+        if inject:
+            facs = {}
+            for prm in params:
+                u = torch.from_numpy(_update_via_torch(prm))
+                rms = u.norm(2) / np.sqrt(u.numel())
+                facs[prm.tensor_id] = np.array([rms.clamp_(min=1.0).item()], dtype=np.float32)
+        opt.step(fac_override=facs)
+        diff = sum(bf16_mismatch(prm.p.reshape(-1)[::s], gold[f"p{i}_step1_sample"])[0]
+                   for i, prm in enumerate(params))
+        if inject:
+            assert diff == 0
+        else:
+            assert 0 < diff <= 40
+
+
+def _update_via_torch(prm):
+    """U = G*r*c at step 1 from zero state, with torch-CPU reductions."""
+    import torch
+
+    g = torch.from_numpy(O.bf16_to_f32(prm.g)).bfloat16()
+    g.sub_(g.mean(dim=tuple(range(1, g.ndim)), keepdim=True))
+    G = g.float().reshape(prm.shape[0], -1)
+    gsq = G * G
+    gsq.add_(1e-30)
+    row = torch.zeros(G.shape[0]).lerp_(gsq.mean(-1), 1 - 0.999)
+    col = torch.zeros(G.shape[1]).lerp_(gsq.mean(-2), 1 - 0.999)
+    return G.mul(row.div(row.mean()).rsqrt_().unsqueeze(-1)).mul_(col.rsqrt().unsqueeze(-2)).numpy()

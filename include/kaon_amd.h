@@ -1,0 +1,224 @@
+/*
+ * kaon_amd.h -- C ABI of the MI355X (gfx950) fused optimizer-step library.
+ *
+ * This is the drop-in boundary for the optimizer-step hot path of
+ * K-Optimizers ("kaon" 0.7.4).  The reference is pure Python: its only
+ * operator boundary for this path is the Triton launch sequence behind
+ * `Adakaon(fused=True)` (src/kaon/adakaon.py:387-738 launching
+ * src/kaon/_fused_triton.py kernels with int64 device pointer arrays
+ * g_addr/p_addr/m_addr/mscale_addr/row_addr/col_addr, int32 Rs/Cs, fp32
+ * scalars lr/beta1/beta2/eps1/clip/wd and the SR seed, plus constexpr flags
+ * LOWP/MOM/CAUTIOUS/WD/GC/SR -- _fused_triton.py:1183-1245, adakaon.py:
+ * 506-513, 533-539), and MSAM's 4-bit perturbation launch
+ * (src/kaon/msam.py:238-290 -> _fused_triton.py:1145-1179).  Lion
+ * (src/kaon/lion.py:322-485) and AdaMuon (src/kaon/adamuon.py:327-615) call
+ * torch ops directly; this ABI covers all four optimizers.
+ *
+ * Conventions
+ *  - Plain C types only.  Every pointer inside KaonTensor / KaonItem points to
+ *    device memory owned by the caller (torch); the library never allocates.
+ *  - Every entry point returns 0 on success or a non-zero status; the text of
+ *    the last error is available from kaon_last_error() (thread-local).
+ *  - Launches are asynchronous on the caller's HIP stream (hipStream_t passed
+ *    as void*); no entry point synchronizes the host.
+ *  - bf16 tensors are 16-bit patterns (uint16), fp32 tensors are float.
+ */
+#ifndef KAON_AMD_H
+#define KAON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KAON_ABI_VERSION 1
+
+/* element types of params / grads (p.dtype, p.grad.dtype) */
+enum { KAON_F32 = 0, KAON_BF16 = 1 };
+
+/* momentum storage ("momentum_dtype"), _momentum_codec.py:253-406 */
+enum { KAON_MOM_NONE = 0, KAON_MOM_F32 = 1, KAON_MOM_BF16 = 2, KAON_MOM_INT8 = 3, KAON_MOM_4BIT = 4 };
+
+/* low-precision weight write ("bf16_method"), _backend.py:82-98; fp32
+ * params always take the plain fp32 subtraction */
+enum { KAON_SR = 0, KAON_RN = 1, KAON_KAHAN = 2 };
+
+/* optimizer selected by a plan / step */
+enum { KAON_OPT_ADAKAON = 0, KAON_OPT_LION = 1, KAON_OPT_ADAMUON = 2 };
+
+/* per-launch flags (KaonHyper.flags) */
+enum {
+  KAON_F_GC = 1,        /* gradient centralization (_backend.py:147-177) */
+  KAON_F_CAUTIOUS = 2,  /* cautious masking (_backend.py:127-142) */
+  KAON_F_WD = 4,        /* weight_decay != 0 */
+  KAON_F_EPS = 8,       /* eps1 > 0 adds eps1 to g^2 (_factored.py:35-39) */
+  KAON_F_MOMENTUM = 16, /* beta1 > 0 and a momentum buffer exists */
+  KAON_F_NK_REMOVE = 32,/* Nekaon: remove the previous climb first (msam.py:386-388) */
+  KAON_F_NK_CLIMB = 64  /* Nekaon: climb along the new momentum (msam.py:395-403) */
+};
+
+/*
+ * One parameter of the multi-tensor launch (the descriptor table entry that
+ * replaces the reference's per-role pointer arrays).  Layout: the param and
+ * grad are viewed as a row-major [R, C] matrix -- R = shape[0], C = numel/R
+ * for ndim >= 2 (conv weights matrixized, adakaon.py:975-981), R = 1 and
+ * C = numel for 1-D params.  State tensors are the reference's own state
+ * entries (adakaon.py:318-335, lion.py:210-241, _momentum_codec.py:293-361).
+ */
+typedef struct KaonTensor {
+  const void* g;          /* grad [R*C], g_dtype (never written) */
+  void* p;                /* param [R*C], p_dtype, updated in place */
+  void* m;                /* momentum codes/values (layout by codec), in place */
+  float* m_scale;         /* int8: [R] per-row (1 for 1-D); 4-bit: [nblocks] */
+  float* row;             /* factored: "row" [R] */
+  float* col;             /* factored: "col" [C] */
+  float* v;               /* 1-D: "v" [C] */
+  void* shift;            /* kahan compensation [R*C] in p_dtype */
+  const uint16_t* noise[3]; /* optional injected SR noise per stream (tests) */
+  int64_t R, C;           /* matrixized shape */
+  int64_t n;              /* R * C */
+  /* workspace offsets, in 4-byte words from the workspace base (kaon_plan) */
+  int64_t ws_row;         /* 5 arrays of R words: mu, rf, rs, amax, oldscale */
+  int64_t ws_col;         /* cf [C] */
+  int64_t ws_part;        /* column partials [ngroups][C] */
+  int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
+  int64_t ws_scal;        /* 4 words: fac, keep-count, spare, spare */
+  int64_t ws_aux;         /* AdaMuon Newton-Schulz scratch (bf16 words) */
+  int32_t tensor_id;      /* SR counter field: index in the optimizer's param list */
+  int32_t block4;         /* 4-bit block size (m_block) */
+  int32_t factored;       /* ndim >= 2 */
+  int32_t ngroups;        /* ceil(R / KAON_COLGROUP) */
+  float sqrt_n;           /* (float)sqrt((double)n), the rms divisor (_backend.py:45-47) */
+  int32_t vec_rows;       /* 16-byte vector path for row-wise chunks (C % 8 == 0, aligned) */
+  int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
+  int32_t pad;
+} KaonTensor;
+
+/* A row-phase work item: rows [row0, row0 + nrows) of tensor `tensor`. */
+typedef struct KaonItem {
+  int32_t tensor;
+  int32_t row0;
+  int32_t nrows;
+  int32_t kind;           /* finalize items: 0 = columns [row0, row0+nrows), 1 = row stats */
+} KaonItem;
+
+/* Rows per row-phase work item; also the column-sum group of the canonical
+ * reduction order (column sums accumulate KAON_COLGROUP rows in row order,
+ * then the group partials in group order). */
+#define KAON_COLGROUP 32
+/* Columns per column-finalize work item. */
+#define KAON_COLITEM 2048
+
+/*
+ * Host-side plan: kaon_plan() fills the workspace offsets of every
+ * descriptor and the work-item arrays.  The caller uploads descriptors and
+ * items to device memory and allocates `ws_words * 4` bytes of workspace.
+ */
+typedef struct KaonPlanInfo {
+  int32_t n_tensors;
+  int32_t n_row_items;    /* row items (phases 1 and 3), sorted by register class */
+  int32_t n_fin_items;    /* finalize items (phase 2) */
+  int32_t n_flat_items;   /* flat items of KAON_FLAT_ITEM elements (phases 5 and 6) */
+  int32_t row_runs[4];    /* row items per register class: rows of <= 2048, 4096, 8192, 16384 elements */
+  int64_t ws_words;       /* workspace size in 4-byte words */
+} KaonPlanInfo;
+
+/* Elements per flat work item. */
+#define KAON_FLAT_ITEM 16384
+/* Longest row (C) of a factored tensor the row kernels accept. */
+#define KAON_MAX_ROW 16384
+
+/* Device-side tables of one planned group, passed to every step entry point. */
+typedef struct KaonLaunch {
+  const KaonTensor* descs;    /* device copy of the planned descriptors */
+  const KaonItem* row_items;  /* device */
+  const KaonItem* fin_items;  /* device */
+  const KaonItem* flat_items; /* device */
+  int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
+  int32_t row_runs[4];
+  void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
+} KaonLaunch;
+
+/* Per-launch hyper-parameters of one param group, rounded to fp32 on the
+ * host exactly as the reference's torch ops see them (python float ->
+ * fp32 scalar):  w1 = 1 - beta1, w2 = 1 - beta2 (lerp weights), wdl = lr*wd
+ * (Adakaon/AdaMuon, adakaon.py:1007-1009) or wd (Lion, lion.py:476-477). */
+typedef struct KaonHyper {
+  float lr;               /* Adakaon/Lion lr; AdaMuon passes 0.2*lr (adamuon.py:88, 588) */
+  float w1, w2;
+  float eps1;
+  float wdl;
+  float clip;
+  float b1, b2, a1, a2;   /* Lion: beta1, beta2, 1-beta1, 1-beta2 */
+  float nk_k;             /* Nekaon k (rho = -k), nekaon.py:162-171 */
+  float nk_bound_old;     /* frozen climb bound of the previous climb (msam.py:169-188) */
+  float nk_bound_new;     /* |k| * clip * lr at this climb */
+  int32_t flags;          /* KAON_F_* */
+  int32_t p_dtype, g_dtype, codec, bf16_method;
+  int32_t ns_steps;       /* AdaMuon Newton-Schulz iterations */
+  uint32_t step;          /* SR key word 1 (the optimizer step count) */
+  uint64_t seed;          /* SR key word 0 (low 32 bits used) */
+} KaonHyper;
+
+int kaon_abi_version(void);
+const char* kaon_last_error(void);
+
+/* Plan a launch group (the host half of the descriptor table; replaces the
+ * pointer-array caches PointerArrayCache / OneDimPointerCache,
+ * _fused_triton.py:1183-1320).  descs: host array of n descriptors with
+ * pointers, shapes, block4 and tensor_id filled; on return their ws_*,
+ * ngroups, sqrt_n and vec_* fields are set.  Item arrays may be NULL to query
+ * sizes; info is always filled.  Returns 0, or non-zero with kaon_last_error()
+ * set (e.g. a factored row longer than KAON_MAX_ROW). */
+int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t n, KaonItem* row_items,
+              KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info);
+
+/* Adakaon step over one planned param group, Nekaon's remove/climb fused in
+ * when the KAON_F_NK_* flags are set.  Replaces Adakaon._fused_step and the
+ * native per-param/foreach step (adakaon.py:339-409, 793-1014) and MSAM.step's
+ * remove/climb around it (msam.py:375-406). */
+int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
+/* Lion step over one planned param group (lion.py:322-352, 416-485). */
+int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
+/* The same steps restricted to the phases whose bit is set in `mask`
+ * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,
+ * 4 clip divisor, 5 keep-count/absmax, 6 apply; Lion uses 1, 5, 6).  For
+ * profiling one kernel at a time; running all phases in order is the step.
+ * No counterpart in the reference, which has no phase boundary to expose. */
+int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
+int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
+
+/* MSAM norm="none" perturbation p += clamp(nan_to_num(factor * dequant(m)), +-bound)
+ * (msam.py:202-235; fused 4-bit twin _fused_triton.py:1145-1179), used by
+ * Nekaon.eval()/train() (msam.py:294-311).  stream_id selects the SR noise
+ * stream (0 = removal, 2 = climb). */
+int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, float bound,
+                    uint32_t stream_id, void* stream);
+
+/* ---------------------------------------------------------- primitives */
+/* _quant_int8 (_momentum_codec.py:72-83): rows x cols fp32 -> int8 codes +
+ * per-row scale (rows = 1 for a 1-D tensor). */
+int kaon_quant_int8(const float* m, int64_t rows, int64_t cols, int8_t* q, float* scale, void* stream);
+/* _quant_4bit (_momentum_codec.py:122-141): n fp32 -> packed nibbles + per-block scale. */
+int kaon_quant_4bit(const float* m, int64_t n, int32_t block, uint8_t* packed, float* scale,
+                    void* stream);
+/* dequant of int8 ([rows, cols], per-row scale) or 4-bit (flat blocks) codes to fp32. */
+int kaon_dequant(int32_t codec, const void* m, const float* scale, int64_t rows, int64_t cols,
+                 int32_t block, float* out, void* stream);
+/* _add_stochastic_bf16_ bit trick (_stochastic_rounding.py:70-103) with explicit noise. */
+int kaon_sr_round(const float* x, const uint16_t* noise, int64_t n, uint16_t* out, void* stream);
+/* Philox4x32-10 SR noise words of (seed, step, tensor id, stream) for elements [0, n). */
+int kaon_sr_noise(uint16_t* out, int64_t n, uint64_t seed, uint32_t step, uint32_t tensor_id,
+                  uint32_t stream_id, void* stream);
+/* Streaming copy (bytes must be a multiple of 16, both pointers 16-B aligned): the
+ * measured HBM read+write ceiling the step is compared against. */
+int kaon_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KAON_AMD_H */

@@ -1,0 +1,219 @@
+// kaon_device.h -- gfx950 device helpers shared by the optimizer-step kernels.
+//
+// Every helper reproduces one rounding step of the reference's torch-CPU
+// arithmetic (K-Optimizers "kaon" 0.7.4) so the HIP step is bit-exact with the
+// CPU restatement under oracle/.  The whole library is compiled with
+// -ffp-contract=off: only the explicit __fmaf_rn calls below fuse.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kaon_amd.h"
+
+#define KAON_WG 256          // threads per workgroup of every step kernel (4 wave64)
+#define KAON_CHUNK 8         // elements per chunk: one 16-byte bf16 vector
+
+namespace kaon {
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 round-to-nearest-even, NaN -> 0x7FC0 (c10::BFloat16 semantics).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// torch.lerp on CPU: self + w*(end-self) if |w| < 0.5 else end - (end-self)*(1-w),
+// each as one fused multiply-add (ATen/native/Lerp.h:22-35).
+__device__ __forceinline__ float klerp(float a, float b, float w) {
+  const float d = b - a;
+  return fabsf(w) < 0.5f ? __fmaf_rn(w, d, a) : __fmaf_rn(w - 1.0f, d, b);
+}
+
+// Correctly rounded a / b from a precomputed r = RN64(1/b).  The fp64 product
+// has relative error < 2^-52 while an fp32 quotient of two fp32 values is at
+// least 2^-49 (relative) away from every fp32 rounding midpoint it is not equal
+// to, so rounding the fp64 product to fp32 gives RN32(a/b) for all finite
+// inputs (exact quotients included); inf and NaN propagate as in IEEE division.
+__device__ __forceinline__ float div_r64(float a, double r) { return (float)((double)a * r); }
+__device__ __forceinline__ double rcp64(float b) { return 1.0 / (double)b; }
+
+__device__ __forceinline__ float ksign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
+
+// ------------------------------------------------------------------ Philox
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11), published multipliers and
+// Weyl increments.  SR noise: key = (seed lo32, step), counter = (chunk lo,
+// chunk hi, tensor id, stream) with chunk = element / 8; the 8 elements of a
+// chunk take the 8 16-bit halves of the output, low half first.
+__device__ __forceinline__ void philox10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    c[1] = (uint32_t)p1;
+    c[3] = (uint32_t)p0;
+    c[0] = n0;
+    c[2] = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// Noise words for the aligned chunk [e0, e0+8) (e0 % 8 == 0).
+__device__ __forceinline__ void noise8(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream,
+                                       int64_t e0, const uint16_t* inj, int cnt, uint32_t w[8]) {
+  if (inj) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = i < cnt ? (uint32_t)inj[e0 + i] : 0u;
+    return;
+  }
+  const uint64_t ch = (uint64_t)e0 >> 3;
+  uint32_t c[4] = {(uint32_t)ch, (uint32_t)(ch >> 32), tid, stream};
+  philox10(c, (uint32_t)seed, step);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[2 * i] = c[i] & 0xFFFFu;
+    w[2 * i + 1] = c[i] >> 16;
+  }
+}
+
+// Noise word of one element (any alignment).
+__device__ __forceinline__ uint32_t noise1(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream,
+                                           int64_t e, const uint16_t* inj) {
+  if (inj) return inj[e];
+  const uint64_t ch = (uint64_t)e >> 3;
+  uint32_t c[4] = {(uint32_t)ch, (uint32_t)(ch >> 32), tid, stream};
+  philox10(c, (uint32_t)seed, step);
+  const int wi = (int)(e & 7);
+  return (c[wi >> 1] >> ((wi & 1) * 16)) & 0xFFFFu;
+}
+
+// _add_stochastic_bf16_ bit trick: int32 add of the 16-bit noise, clear the
+// low half; the cast to bf16 is then exact (NaN -> 0x7FC0).
+__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t noise) {
+  const uint32_t b = (__float_as_uint(x) + noise) & 0xFFFF0000u;
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return b >> 16;
+}
+
+// ------------------------------------------------------------------ loads
+// Chunk loads into fp32 (8 elements, `cnt` valid; vec = 16-byte vector path).
+template <int DT>
+__device__ __forceinline__ void ld8(const void* base, int64_t off, int cnt, bool vec, float o[8]) {
+  if (DT == KAON_BF16) {
+    const uint16_t* b = (const uint16_t*)base + off;
+    if (vec) {
+      const uint4 v = *(const uint4*)b;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = __uint_as_float(w[i] << 16);
+        o[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = i < cnt ? bf2f(b[i]) : 0.0f;
+    }
+  } else {
+    const float* b = (const float*)base + off;
+    if (vec) {
+      const float4 v0 = *(const float4*)b;
+      const float4 v1 = *(const float4*)(b + 4);
+      o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w;
+      o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = i < cnt ? b[i] : 0.0f;
+    }
+  }
+}
+
+// Raw bf16 chunk (bits) load/store.
+__device__ __forceinline__ void ld8_bits(const void* base, int64_t off, int cnt, bool vec, uint32_t o[8]) {
+  const uint16_t* b = (const uint16_t*)base + off;
+  if (vec) {
+    const uint4 v = *(const uint4*)b;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = w[i] & 0xFFFFu;
+      o[2 * i + 1] = w[i] >> 16;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = i < cnt ? (uint32_t)b[i] : 0u;
+  }
+}
+__device__ __forceinline__ void st8_bits(void* base, int64_t off, int cnt, bool vec, const uint32_t o[8]) {
+  uint16_t* b = (uint16_t*)base + off;
+  if (vec) {
+    uint4 v;
+    v.x = (o[0] & 0xFFFFu) | (o[1] << 16);
+    v.y = (o[2] & 0xFFFFu) | (o[3] << 16);
+    v.z = (o[4] & 0xFFFFu) | (o[5] << 16);
+    v.w = (o[6] & 0xFFFFu) | (o[7] << 16);
+    *(uint4*)b = v;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < cnt) b[i] = (uint16_t)o[i];
+  }
+}
+__device__ __forceinline__ void st8_f32(void* base, int64_t off, int cnt, bool vec, const float o[8]) {
+  float* b = (float*)base + off;
+  if (vec) {
+    *(float4*)b = make_float4(o[0], o[1], o[2], o[3]);
+    *(float4*)(b + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < cnt) b[i] = o[i];
+  }
+}
+
+// ------------------------------------------------------------------ reductions
+// Canonical chunked sum (the oracle's CSUM): lane l of 256 accumulates, in
+// order, the 8 elements of its chunks l, l+256, ...; each wave64 is reduced by
+// an xor butterfly (offsets 32..1); the wave totals of the waves that own any
+// chunk are folded left to right.  `a` is this thread's accumulator; lds4
+// holds 4 floats.  Every thread returns the total.  Contains barriers: call
+// from uniform control flow.
+__device__ __forceinline__ float csum_finish(float a, int64_t nch, float* lds4) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) a = a + __shfl_xor(a, o, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds4[wave] = a;
+  __syncthreads();
+  int nw = (int)((nch + 63) / 64);
+  if (nw > 4) nw = 4;
+  float r = lds4[0];
+  for (int w = 1; w < nw; ++w) r = r + lds4[w];
+  __syncthreads();
+  return r;
+}
+
+// Workgroup integer sum (order-free) -> thread 0 gets it.
+__device__ __forceinline__ uint32_t wg_sum_u32(uint32_t a, uint32_t* lds4) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+  if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = a;
+  __syncthreads();
+  uint32_t r = lds4[0] + lds4[1] + lds4[2] + lds4[3];
+  __syncthreads();
+  return r;
+}
+
+// Non-negative float max through its bit pattern (monotone for x >= 0).
+__device__ __forceinline__ uint32_t fmax_bits(uint32_t a, float x) {
+  const uint32_t b = __float_as_uint(x);
+  return b > a ? b : a;
+}
+
+}  // namespace kaon

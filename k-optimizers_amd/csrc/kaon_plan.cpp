@@ -1,0 +1,137 @@
+// kaon_plan.cpp -- host half of the multi-tensor descriptor table.
+//
+// The reference rebuilds int64 device pointer arrays per role (g, p, m,
+// m_scale, row, col) and int32 shape arrays for every fused launch, cached per
+// param set (PointerArrayCache / OneDimPointerCache,
+// src/kaon/_fused_triton.py:1183-1320; built at adakaon.py:489-539, 623-738).
+// Here one descriptor per tensor carries every pointer and shape, and the plan
+// adds what the HIP kernels need: a workspace layout for the per-row /
+// per-column / per-block intermediates and three work-item tables.
+//   row items   KAON_COLGROUP rows of one factored tensor (the whole tensor
+//               for a 1-D param), sorted by register class (row length) so
+//               each class is one launch with a fixed register budget;
+//   fin items   KAON_COLITEM columns of one factored tensor, or its row stats;
+//   flat items  KAON_FLAT_ITEM consecutive elements of one tensor.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kaon_amd.h"
+
+// Error text reported by kaon_last_error() (defined with the kernels).
+void kaon_set_error(const std::string& s);
+
+namespace {
+int plan_fail(const std::string& s) {
+  kaon_set_error(s);
+  return -1;
+}
+
+bool aligned(const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; }
+
+int64_t round4(int64_t x) { return (x + 3) & ~int64_t(3); }
+
+int row_class(const KaonTensor& t) {
+  if (!t.factored) return 0;
+  const int64_t nch = (t.C + 7) / 8;
+  const int64_t cpt = (nch + 255) / 256;
+  if (cpt <= 1) return 0;
+  if (cpt <= 2) return 1;
+  if (cpt <= 4) return 2;
+  return 3;
+}
+}  // namespace
+
+extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t n, KaonItem* row_items,
+                         KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info) {
+  if (!info) return plan_fail("kaon_plan: info is NULL");
+  if (n < 0 || (n > 0 && !descs)) return plan_fail("kaon_plan: bad descriptor array");
+  if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON)
+    return plan_fail("kaon_plan: unknown optimizer");
+  if (codec < KAON_MOM_NONE || codec > KAON_MOM_4BIT) return plan_fail("kaon_plan: unknown codec");
+  std::memset(info, 0, sizeof(*info));
+  info->n_tensors = n;
+
+  int64_t off = 0;
+  struct RowIt {
+    KaonItem it;
+    int cls;
+    int64_t size;
+  };
+  std::vector<RowIt> rows;
+  std::vector<KaonItem> fins, flats;
+  for (int32_t i = 0; i < n; ++i) {
+    KaonTensor& t = descs[i];
+    if (t.R < 1 || t.C < 0) return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has a bad shape");
+    t.n = t.R * t.C;
+    if (t.n >= (int64_t)1 << 31)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has >= 2^31 elements");
+    if (t.factored && t.C > KAON_MAX_ROW)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has rows of " + std::to_string(t.C) +
+                       " elements; the row kernels take at most " + std::to_string(KAON_MAX_ROW));
+    if (!t.factored && t.R != 1) return plan_fail("kaon_plan: a 1-D tensor must have R == 1");
+    if (codec == KAON_MOM_4BIT && t.block4 < 1) return plan_fail("kaon_plan: 4-bit block size must be >= 1");
+    t.sqrt_n = (float)std::sqrt((double)(t.n > 1 ? t.n : 1));
+    t.ngroups = (int32_t)((t.R + KAON_COLGROUP - 1) / KAON_COLGROUP);
+    const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
+                    aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16);
+    t.vec_flat = al ? 1 : 0;
+    t.vec_rows = (al && t.C % 8 == 0) ? 1 : 0;
+    // workspace: 4-word aligned arrays
+    t.ws_row = off;
+    off = round4(off + 5 * t.R);
+    t.ws_col = off;
+    t.ws_part = off;
+    if (t.factored) {
+      off = round4(off + t.C);
+      t.ws_part = off;
+      off = round4(off + (int64_t)t.ngroups * t.C);
+    }
+    t.ws_blk = off;
+    if (codec == KAON_MOM_4BIT) {
+      const int64_t nb = (t.n + t.block4 - 1) / t.block4;
+      off = round4(off + 2 * nb);
+    }
+    t.ws_scal = off;
+    off = round4(off + 4);
+    t.ws_aux = off;
+    if (t.n == 0) continue;
+    // row items
+    const int cls = row_class(t);
+    if (t.factored) {
+      for (int64_t r0 = 0; r0 < t.R; r0 += KAON_COLGROUP) {
+        KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(KAON_COLGROUP, t.R - r0), 0};
+        rows.push_back({it, cls, t.n});
+      }
+    } else {
+      rows.push_back({KaonItem{i, 0, 1, 0}, cls, t.n});
+    }
+    // finalize items (Adakaon / AdaMuon factored second moment)
+    if (t.factored && opt != KAON_OPT_LION) {
+      for (int64_t c0 = 0; c0 < t.C; c0 += KAON_COLITEM)
+        fins.push_back(KaonItem{i, (int32_t)c0, (int32_t)std::min<int64_t>(KAON_COLITEM, t.C - c0), 0});
+      fins.push_back(KaonItem{i, 0, (int32_t)t.R, 1});
+    }
+    for (int64_t e0 = 0; e0 < t.n; e0 += KAON_FLAT_ITEM)
+      flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, t.n - e0), 0});
+  }
+  // register classes in ascending order; inside a class the largest tensors
+  // first so their long runs of items start early
+  std::stable_sort(rows.begin(), rows.end(), [](const RowIt& a, const RowIt& b) {
+    if (a.cls != b.cls) return a.cls < b.cls;
+    return a.size > b.size;
+  });
+  info->n_row_items = (int32_t)rows.size();
+  info->n_fin_items = (int32_t)fins.size();
+  info->n_flat_items = (int32_t)flats.size();
+  for (const RowIt& r : rows) info->row_runs[r.cls]++;
+  info->ws_words = off > 0 ? off : 4;
+  if (row_items)
+    for (size_t k = 0; k < rows.size(); ++k) row_items[k] = rows[k].it;
+  if (fin_items && !fins.empty()) std::memcpy(fin_items, fins.data(), fins.size() * sizeof(KaonItem));
+  if (flat_items && !flats.empty()) std::memcpy(flat_items, flats.data(), flats.size() * sizeof(KaonItem));
+  return 0;
+}

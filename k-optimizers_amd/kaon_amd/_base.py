@@ -1,0 +1,178 @@
+"""Shared optimizer plumbing: state layout, plan cache, checkpoint I/O.
+
+State keys, dtypes and shapes are the reference's (K-Optimizers "kaon"
+0.7.4), so checkpoints move between the two libraries:
+  Adakaon  src/kaon/adakaon.py:318-335    Lion  src/kaon/lion.py:210-241
+  codecs   src/kaon/_momentum_codec.py:253-406 (init_state of each codec)
+  loading  src/kaon/_momentum_codec.py:417-452 (dtype-preserving load)
+"""
+from __future__ import annotations
+
+from typing import Any, Iterable
+
+import torch
+
+from . import _engine as E
+from . import _lib as L
+
+_FOURBIT_BLOCK = 128          # src/kaon/_momentum_codec.py:59
+FOREACH_BATCH_CUTOFF = 2_000_000  # src/kaon/_backend.py:53 (accepted for API compatibility)
+
+
+def fourbit_block_size(numel: int, block: int) -> int:
+    """4-bit absmax block for a tensor of ``numel`` elements (_momentum_codec.py:192-200)."""
+    return numel if block <= 0 else (min(block, numel) if numel > 0 else 1)
+
+
+def init_momentum_state(state: dict[str, Any], grad: torch.Tensor, group: dict[str, Any]) -> None:
+    """Allocate the momentum buffer exactly as the reference codecs do."""
+    md = group["momentum_dtype"]
+    if md in ("bfloat16", "float32"):
+        state["m"] = torch.zeros_like(grad, dtype=torch.bfloat16 if md == "bfloat16" else torch.float32,
+                                      memory_format=torch.contiguous_format)
+    elif md == "int8":
+        state["m"] = torch.zeros_like(grad, dtype=torch.int8, memory_format=torch.contiguous_format)
+        state["m_scale"] = torch.ones((grad.shape[0],) + (1,) * (grad.ndim - 1) if grad.ndim >= 2 else (),
+                                      dtype=torch.float32, device=grad.device)
+    else:
+        numel = grad.numel()
+        bs = fourbit_block_size(numel, group["momentum_4bit_block"])
+        nblocks = (numel + bs - 1) // bs
+        state["m"] = torch.full(((numel + 1) // 2,), 0x88, dtype=torch.uint8, device=grad.device)
+        state["m_scale"] = torch.ones(nblocks, dtype=torch.float32, device=grad.device)
+        state["m_numel"] = numel
+        state["m_block"] = bs
+
+
+def load_state_dict_preserving_dtypes(optimizer: torch.optim.Optimizer, state_dict: dict[str, Any]) -> None:
+    """torch's load_state_dict, then cast every state tensor back to its saved dtype
+    (torch upcasts int8/uint8/bf16 momentum to the param dtype on load)."""
+    saved = state_dict.get("state", {})
+    saved_dtypes = {idx: {k: v.dtype for k, v in s.items() if torch.is_tensor(v)} for idx, s in saved.items()}
+    torch.optim.Optimizer.load_state_dict(optimizer, state_dict)
+    params = [p for group in optimizer.param_groups for p in group["params"]]
+    for i, p in enumerate(params):
+        dtypes = saved_dtypes.get(i)
+        if dtypes is None or p not in optimizer.state:
+            continue
+        st = optimizer.state[p]
+        for key, dtype in dtypes.items():
+            t = st.get(key)
+            if torch.is_tensor(t) and t.dtype != dtype:
+                st[key] = t.to(dtype)
+
+
+def validate_common(lr: float, betas: tuple[float, float], momentum_dtype: str, bf16_method: str,
+                    foreach_batch_cutoff: int, auto_lr: bool) -> tuple[float, float]:
+    beta1, beta2 = float(betas[0]), float(betas[1])
+    if not 0.0 <= beta1 < 1.0:
+        raise ValueError(f"betas[0] must be in [0, 1), got {beta1}")
+    if not 0.0 <= beta2 < 1.0:
+        raise ValueError(f"betas[1] must be in [0, 1), got {beta2}")
+    if lr < 0.0:
+        raise ValueError(f"lr must be >= 0, got {lr}")
+    if momentum_dtype not in ("bfloat16", "float32", "int8", "4bit"):
+        raise ValueError(f"momentum_dtype must be bfloat16/float32/int8/4bit, got {momentum_dtype!r}")
+    if bf16_method not in ("stochastic_rounding", "kahan", "none"):
+        raise ValueError(f"bf16_method must be stochastic_rounding/kahan/none, got {bf16_method!r}")
+    if foreach_batch_cutoff < 1:
+        raise ValueError(f"foreach_batch_cutoff must be >= 1, got {foreach_batch_cutoff}")
+    if auto_lr:
+        raise NotImplementedError("kaon_amd: auto_lr (the DoWG LR controller) is not part of this build")
+    return beta1, beta2
+
+
+class KaonOptimizer(torch.optim.Optimizer):
+    """Base of the HIP-backed optimizers: plan cache, SR key, checkpoint extras.
+
+    Subclasses provide ``_OPT`` (the C-ABI optimizer code), ``_init_state`` and
+    ``_hyper``.  The SR noise key is (``sr_seed``, step count); ``sr_seed``
+    defaults to ``torch.initial_seed()`` at construction, so seeding torch
+    seeds the optimizer's rounding as the reference's global-RNG draw does
+    (src/kaon/_stochastic_rounding.py:88-94).
+    """
+
+    _OPT = L.OPT_ADAKAON
+    _NAME = "kaon"
+
+    def __init__(self, params: Iterable[Any], defaults: dict[str, Any]) -> None:
+        super().__init__(params, defaults)
+        self._t = 0
+        self.sr_seed = int(torch.initial_seed()) & 0xFFFFFFFF
+        self._plans: dict[tuple, tuple[tuple, E.Plan]] = {}
+        self._state_version = 0
+        self._inject_noise: dict[torch.Tensor, list] = {}  # tests: param -> [uint16 noise per stream]
+
+    # ------------------------------------------------------------ helpers
+    def _tensor_ids(self) -> dict[int, int]:
+        return {id(p): i for i, p in enumerate(p for g in self.param_groups for p in g["params"])}
+
+    def _invalidate(self) -> None:
+        self._plans.clear()
+        self._state_version += 1
+
+    def _check_params(self, params: list[torch.Tensor]) -> None:
+        for p in params:
+            if p.grad.is_sparse:
+                raise RuntimeError(f"{self._NAME} does not support sparse gradients")
+            if p.device.type != "cuda":
+                raise RuntimeError(f"kaon_amd: {self._NAME} steps run on a ROCm GPU; got a param on {p.device}")
+            if not p.is_contiguous():
+                raise ValueError("kaon_amd: params must be contiguous")
+            if p.grad.dtype != p.dtype and p.grad.dtype not in (torch.float32, torch.bfloat16):
+                raise NotImplementedError(f"kaon_amd: grad dtype {p.grad.dtype} is not supported")
+
+    def _entries(self, group: dict[str, Any], params: list[torch.Tensor], tids: dict[int, int]) -> list[dict]:
+        out = []
+        for p in params:
+            st = self.state[p]
+            R, C, fac = E.matrixized(p)
+            g = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+            e = dict(p=p, g=g, R=R, C=C, factored=fac, tensor_id=tids[id(p)],
+                     m=st.get("m"), m_scale=st.get("m_scale"), row=st.get("row"), col=st.get("col"),
+                     v=st.get("v"), shift=st.get("shift"), block4=st.get("m_block", 0),
+                     noise=self._inject_noise.get(p))
+            out.append(e)
+        return out
+
+    def _plan(self, key: tuple, group: dict[str, Any], params: list[torch.Tensor], codec: int,
+              tids: dict[int, int]) -> E.Plan:
+        ptrs = (self._state_version,) + tuple(
+            (p.data_ptr(), p.grad.data_ptr()) for p in params)
+        hit = self._plans.get(key)
+        if hit is not None and hit[0] == ptrs:
+            return hit[1]
+        for p in params:
+            if not p.grad.is_contiguous():
+                raise ValueError("kaon_amd: gradients must be contiguous")
+        plan = E.Plan(self._OPT, codec, self._entries(group, params, tids), params[0].device)
+        self._plans[key] = (ptrs, plan)
+        return plan
+
+    def _partitions(self, params: list[torch.Tensor]) -> dict[tuple[int, int], list[torch.Tensor]]:
+        parts: dict[tuple[int, int], list[torch.Tensor]] = {}
+        for p in params:
+            parts.setdefault((E.dtype_code(p.dtype), E.dtype_code(p.grad.dtype)), []).append(p)
+        return parts
+
+    # ------------------------------------------------------------ checkpoint
+    def state_dict(self) -> dict[str, Any]:
+        sd = super().state_dict()
+        sd["kaon_amd"] = {"step": self._t, "sr_seed": self.sr_seed}
+        return sd
+
+    def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        sd = dict(state_dict)
+        extra = sd.pop("kaon_amd", None)
+        sd.pop("_autolr", None)
+        load_state_dict_preserving_dtypes(self, sd)
+        if extra is not None:
+            self._t = int(extra.get("step", self._t))
+            self.sr_seed = int(extra.get("sr_seed", self.sr_seed))
+        self._invalidate()
+
+    def step(self, closure: Any = None) -> Any:
+        return self._step_impl(closure)
+
+    def _step_impl(self, closure: Any = None, nk: Any = None) -> Any:  # pragma: no cover - abstract
+        raise NotImplementedError

@@ -1,0 +1,105 @@
+"""Plans and launches: the host side of the multi-tensor descriptor table.
+
+One :class:`Plan` covers the params of one param group that share (param
+dtype, grad dtype).  It holds the device copy of the descriptor table and the
+work-item tables that ``kaon_plan`` (C++) produced, plus the workspace.  Plans
+are cached by the optimizer and rebuilt when any param or grad pointer changes
+(the stale-pointer hazard the reference guards against in
+src/kaon/_fused_triton.py:1229-1245), when state is (re)initialized or loaded.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Any, Sequence
+
+import torch
+
+from . import _lib as L
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return L.BF16
+    if dt == torch.float32:
+        return L.F32
+    raise NotImplementedError(
+        f"kaon_amd: params/grads of dtype {dt} are not supported (bfloat16 and float32 are)")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _align(n: int, a: int = 256) -> int:
+    return (n + a - 1) // a * a
+
+
+class Plan:
+    """Device tables + workspace of one planned launch group."""
+
+    def __init__(self, opt: int, codec: int, entries: Sequence[dict[str, Any]], device: torch.device) -> None:
+        n = len(entries)
+        descs = (L.KaonTensor * max(n, 1))()
+        for i, e in enumerate(entries):
+            d = descs[i]
+            d.g, d.p = _ptr(e["g"]), _ptr(e["p"])
+            d.m, d.m_scale = _ptr(e.get("m")), _ptr(e.get("m_scale"))
+            d.row, d.col, d.v = _ptr(e.get("row")), _ptr(e.get("col")), _ptr(e.get("v"))
+            d.shift = _ptr(e.get("shift"))
+            noise = e.get("noise") or (None, None, None)
+            for s in range(3):
+                d.noise[s] = _ptr(noise[s])
+            d.R, d.C = e["R"], e["C"]
+            d.factored = 1 if e["factored"] else 0
+            d.block4 = int(e.get("block4", 0))
+            d.tensor_id = int(e["tensor_id"])
+        info = L.KaonPlanInfo()
+        lib = L.lib()
+        L.check(lib.kaon_plan(opt, codec, descs, n, None, None, None, ctypes.byref(info)), "kaon_plan")
+        rows = (L.KaonItem * max(info.n_row_items, 1))()
+        fins = (L.KaonItem * max(info.n_fin_items, 1))()
+        flats = (L.KaonItem * max(info.n_flat_items, 1))()
+        L.check(lib.kaon_plan(opt, codec, descs, n, rows, fins, flats, ctypes.byref(info)), "kaon_plan")
+        self.info = info
+        self.descs = descs
+        parts = [bytes(descs)[: ctypes.sizeof(L.KaonTensor) * n],
+                 bytes(rows)[: 16 * info.n_row_items],
+                 bytes(fins)[: 16 * info.n_fin_items],
+                 bytes(flats)[: 16 * info.n_flat_items]]
+        offs, total = [], 0
+        for b in parts:
+            offs.append(total)
+            total += _align(max(len(b), 1))
+        blob = bytearray(total)
+        for o, b in zip(offs, parts):
+            blob[o:o + len(b)] = b
+        self.table = torch.frombuffer(blob, dtype=torch.uint8).to(device)
+        self.workspace = torch.empty(max(int(info.ws_words), 4), dtype=torch.float32, device=device)
+        base = self.table.data_ptr()
+        la = L.KaonLaunch()
+        la.descs, la.row_items, la.fin_items, la.flat_items = (base + o for o in offs)
+        la.n_tensors, la.n_row_items = n, info.n_row_items
+        la.n_fin_items, la.n_flat_items = info.n_fin_items, info.n_flat_items
+        for k in range(4):
+            la.row_runs[k] = info.row_runs[k]
+        la.workspace = self.workspace.data_ptr()
+        self.launch = la
+
+
+def matrixized(p: torch.Tensor) -> tuple[int, int, bool]:
+    """(R, C, factored): ndim >= 2 -> [shape[0], numel/shape[0]] (conv matrixized,
+    src/kaon/adakaon.py:975-981); otherwise one row of numel elements."""
+    if p.ndim >= 2:
+        r = int(p.shape[0])
+        return r, (p.numel() // r if r else 0), True
+    return 1, p.numel(), False
+
+
+def f32(x: float) -> float:
+    """Round a python float to fp32 as torch does for a scalar operand."""
+    return float(torch.tensor(x, dtype=torch.float32).item()) if math.isfinite(x) else x

@@ -1,0 +1,163 @@
+"""Adakaon on the MI355X HIP step.
+
+Constructor, knobs, param-group keys and state layout follow the reference
+``kaon.Adakaon`` (src/kaon/adakaon.py:195-335).  ``step()`` runs the whole
+update (GC, factored second moment, RMS clip, momentum codec, decoupled WD,
+cautious masking, SR / RN / kahan / fp32 write) as one multi-tensor launch
+sequence per param group and dtype pair (``kaon_adakaon_step``).  The
+reference's ``foreach`` / ``fused`` / stacking knobs are accepted and have no
+effect: there is one path.
+
+Differences from the reference, by design:
+* gradients are read, never written: the reference's native path leaves
+  ``p.grad`` centralized (src/kaon/_backend.py:147-177); here GC happens in
+  registers;
+* stochastic rounding draws Philox4x32-10 noise keyed by (``sr_seed``, step,
+  param index, element) instead of ``torch.randint`` from the global RNG.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Iterable
+
+import torch
+
+from . import _engine as E
+from . import _lib as L
+from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common
+
+
+class Adakaon(KaonOptimizer):
+    _OPT = L.OPT_ADAKAON
+    _NAME = "Adakaon"
+
+    def __init__(
+        self,
+        params: Iterable[Any],
+        lr: float = 1e-3,
+        betas: tuple[float, float] = (0.9, 0.999),
+        eps: tuple[float, float] = (1e-30, 1e-3),
+        weight_decay: float = 0.0,
+        *,
+        clip_threshold: float = 1.0,
+        momentum_dtype: str = "bfloat16",
+        momentum_4bit_block: int = _FOURBIT_BLOCK,
+        cautious: bool = True,
+        gradient_centralization: bool = True,
+        bf16_method: str = "stochastic_rounding",
+        foreach: bool = True,
+        foreach_batch_cutoff: int = FOREACH_BATCH_CUTOFF,
+        foreach_stack_budget: int | None = None,
+        fused: bool = False,
+        fused_tile_cap: int | None = None,
+        auto_lr: bool = False,
+        auto_lr_scale: float = 1.0,
+        auto_lr_fuse_rel: float = 0.0,
+        auto_lr_d0: float | None = None,
+    ) -> None:
+        beta1, beta2 = validate_common(lr, betas, momentum_dtype, bf16_method, foreach_batch_cutoff, auto_lr)
+        if clip_threshold <= 0.0:
+            raise ValueError(f"clip_threshold must be > 0, got {clip_threshold}")
+        defaults = {
+            "lr": lr,
+            "betas": (beta1, beta2),
+            "eps": (float(eps[0]), float(eps[1])),
+            "weight_decay": weight_decay,
+            "clip_threshold": clip_threshold,
+            "momentum_dtype": momentum_dtype,
+            "momentum_4bit_block": momentum_4bit_block,
+            "cautious": cautious,
+            "gradient_centralization": gradient_centralization,
+            "bf16_method": bf16_method,
+        }
+        super().__init__(params, defaults)
+        self._foreach = foreach
+        self._foreach_batch_cutoff = foreach_batch_cutoff
+        self._foreach_stack_budget = foreach_stack_budget
+        self._fused = bool(fused)
+
+    @torch.no_grad()
+    def _init_state(self, p: torch.Tensor, state: dict[str, Any], group: dict[str, Any]) -> None:
+        """adakaon.py:318-335: row/col for ndim >= 2 (conv matrixized), v for 1-D,
+        the codec's momentum buffer when beta1 > 0, kahan shift for bf16 params."""
+        grad = p.grad
+        if p.ndim >= 2:
+            R = grad.shape[0]
+            state["row"] = torch.zeros((R,), dtype=torch.float32, device=p.device)
+            state["col"] = torch.zeros((grad.numel() // R if R else 0,), dtype=torch.float32, device=p.device)
+        else:
+            state["v"] = torch.zeros_like(grad, dtype=torch.float32, memory_format=torch.contiguous_format)
+        if group["betas"][0] > 0:
+            init_momentum_state(state, grad, group)
+        if p.dtype in (torch.bfloat16, torch.float16) and group["bf16_method"] == "kahan":
+            state["shift"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+
+    def _hyper(self, group: dict[str, Any], pdt: int, gdt: int, nk: dict | None, gid: int) -> L.KaonHyper:
+        beta1, beta2 = group["betas"]
+        eps1 = group["eps"][0]
+        lr, wd, clip = group["lr"], group["weight_decay"], group["clip_threshold"]
+        h = L.KaonHyper()
+        h.lr = lr
+        h.w1 = 1.0 - beta1
+        h.w2 = 1.0 - beta2
+        h.eps1 = eps1
+        h.wdl = lr * wd
+        h.clip = clip
+        flags = 0
+        if group["gradient_centralization"]:
+            flags |= L.F_GC
+        if group["cautious"]:
+            flags |= L.F_CAUTIOUS
+        if wd != 0:
+            flags |= L.F_WD
+        if eps1 > 0:
+            flags |= L.F_EPS
+        mom = beta1 > 0
+        if mom:
+            flags |= L.F_MOMENTUM
+        if nk is not None and mom:
+            if nk["remove"] and gid in nk["bound_old"]:
+                flags |= L.F_NK_REMOVE
+                h.nk_bound_old = nk["bound_old"][gid]
+            if nk["k"] != 0.0:
+                flags |= L.F_NK_CLIMB
+                bound = abs(nk["k"]) * group.get("clip_threshold", 1.0) * lr
+                h.nk_bound_new = bound
+                nk["eclamp"][gid] = bound
+            h.nk_k = nk["k"]
+        h.flags = flags
+        h.p_dtype, h.g_dtype = pdt, gdt
+        h.codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
+        h.bf16_method = L.BF16_METHOD[group["bf16_method"]]
+        h.step = self._t & 0xFFFFFFFF
+        h.seed = self.sr_seed
+        return h
+
+    @torch.no_grad()
+    def _step_impl(self, closure: Any = None, nk: dict | None = None) -> Any:
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._t += 1
+        tids = None
+        for gid, group in enumerate(self.param_groups):
+            params = [p for p in group["params"] if p.grad is not None]
+            if not params:
+                continue
+            self._check_params(params)
+            for p in params:
+                state = self.state[p]
+                if not state:
+                    self._init_state(p, state, group)
+                    self._state_version += 1
+            mom = group["betas"][0] > 0
+            codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
+            for (pdt, gdt), plist in self._partitions(params).items():
+                if tids is None:
+                    tids = self._tensor_ids()
+                plan = self._plan((gid, pdt, gdt), group, plist, codec, tids)
+                hp = self._hyper(group, pdt, gdt, nk, gid)
+                L.check(L.lib().kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp),
+                                                  E.stream_handle(plist[0].device)), "kaon_adakaon_step")
+        return loss

@@ -1,0 +1,204 @@
+"""CPU checks of the C-ABI library: exports, struct layout, host-side planning.
+
+No GPU is touched: kaon_plan is host code, and symbol / layout checks only load
+the shared object.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kaon_amd.h")
+
+
+def _lib():
+    from kaon_amd import _lib
+
+    return _lib
+
+
+def test_library_exports_every_declared_symbol():
+    src = open(HEADER).read()
+    names = set(re.findall(r"^\s*(?:int|const char\*)\s+(kaon_\w+)\s*\(", src, re.M))
+    assert {"kaon_plan", "kaon_adakaon_step", "kaon_lion_step", "kaon_msam_apply"} <= names
+    h = ctypes.CDLL(_lib().LIB_PATH)
+    missing = [n for n in sorted(names) if not hasattr(h, n)]
+    assert not missing, missing
+    assert set(_lib().SIGNATURES) >= names
+    assert _lib().lib().kaon_abi_version() == _lib().ABI_VERSION
+
+
+def test_struct_layout_matches_c_compiler(tmp_path):
+    L = _lib()
+    structs = {"KaonTensor": L.KaonTensor, "KaonItem": L.KaonItem, "KaonPlanInfo": L.KaonPlanInfo,
+               "KaonLaunch": L.KaonLaunch, "KaonHyper": L.KaonHyper}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "kaon_amd.h"', "int main(void){"]
+    for sname, cls in structs.items():
+        lines.append(f'printf("{sname} size %zu\\n", sizeof({sname}));')
+        for fname, _t in cls._fields_:
+            lines.append(f'printf("{sname} {fname} %zu\\n", offsetof({sname}, {fname}));')
+    lines.append("return 0;}")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(c), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {}
+    for ln in out:
+        if ln:
+            s, f, v = ln.split()
+            got[(s, f)] = int(v)
+    for sname, cls in structs.items():
+        assert got[(sname, "size")] == ctypes.sizeof(cls), sname
+        for fname, _t in cls._fields_:
+            assert got[(sname, fname)] == getattr(cls, fname).offset, (sname, fname)
+
+
+def _plan(shapes, opt=0, codec=3, block=128):
+    L = _lib()
+    n = len(shapes)
+    descs = (L.KaonTensor * n)()
+    for i, s in enumerate(shapes):
+        d = descs[i]
+        numel = int(np.prod(s))
+        if len(s) >= 2:
+            d.R, d.C, d.factored = s[0], numel // s[0], 1
+        else:
+            d.R, d.C, d.factored = 1, numel, 0
+        d.block4 = min(block, numel) if numel else 1
+        d.tensor_id = i
+        d.g = d.p = d.m = 0x1000 * (i + 1)
+    info = L.KaonPlanInfo()
+    rc = L.lib().kaon_plan(opt, codec, descs, n, None, None, None, ctypes.byref(info))
+    if rc:
+        return rc, None, None, None, None, None
+    rows = (L.KaonItem * max(info.n_row_items, 1))()
+    fins = (L.KaonItem * max(info.n_fin_items, 1))()
+    flats = (L.KaonItem * max(info.n_flat_items, 1))()
+    assert L.lib().kaon_plan(opt, codec, descs, n, rows, fins, flats, ctypes.byref(info)) == 0
+    return 0, descs, info, rows, fins, flats
+
+
+def test_plan_covers_every_row_and_element_once():
+    shapes = [(1280, 1280, 3, 3), (640, 640, 3, 3), (5120, 1280), (1280, 2048), (77, 33), (1280,), (5,), (3, 5, 7),
+              (9, 1), (2, 16384)]
+    rc, descs, info, rows, fins, flats = _plan(shapes, codec=4, block=64)
+    assert rc == 0
+    L = _lib()
+    assert sum(info.row_runs) == info.n_row_items
+    # row items: every row of every tensor exactly once, classes ascending
+    seen = {i: np.zeros(descs[i].R, np.int32) for i in range(len(shapes))}
+    cls_prev = -1
+    off = 0
+    for cls in range(4):
+        for k in range(info.row_runs[cls]):
+            it = rows[off + k]
+            seen[it.tensor][it.row0:it.row0 + it.nrows] += 1
+            assert it.nrows <= L.COLGROUP and it.row0 % L.COLGROUP == 0
+            d = descs[it.tensor]
+            cpt = -(-(-(-d.C // 8)) // 256) if d.factored else 1
+            assert cpt <= (1 << cls)
+        off += info.row_runs[cls]
+        assert cls >= cls_prev
+        cls_prev = cls
+    assert all((v == 1).all() for v in seen.values())
+    # flat items: every element exactly once, 8-aligned starts
+    cover = {i: 0 for i in range(len(shapes))}
+    for k in range(info.n_flat_items):
+        it = flats[k]
+        assert it.row0 % 8 == 0 and it.nrows <= L.FLAT_ITEM
+        cover[it.tensor] += it.nrows
+    assert all(cover[i] == descs[i].n for i in range(len(shapes)))
+    # fin items: columns of factored tensors once + one row-stat item each
+    for i in range(len(shapes)):
+        d = descs[i]
+        cols = sum(fins[k].nrows for k in range(info.n_fin_items) if fins[k].tensor == i and fins[k].kind == 0)
+        rstat = sum(1 for k in range(info.n_fin_items) if fins[k].tensor == i and fins[k].kind == 1)
+        assert (cols, rstat) == ((d.C, 1) if d.factored else (0, 0))
+    # workspace regions are disjoint and in bounds
+    spans = []
+    for i in range(len(shapes)):
+        d = descs[i]
+        nb = -(-d.n // d.block4)
+        spans.append((d.ws_row, d.ws_row + 5 * d.R))
+        if d.factored:
+            spans.append((d.ws_col, d.ws_col + d.C))
+            spans.append((d.ws_part, d.ws_part + d.ngroups * d.C))
+        spans.append((d.ws_blk, d.ws_blk + 2 * nb))
+        spans.append((d.ws_scal, d.ws_scal + 4))
+        assert d.ngroups == -(-d.R // L.COLGROUP)
+        assert d.sqrt_n == np.float32(np.sqrt(float(max(d.n, 1))))
+    spans.sort()
+    for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):
+        assert a1 <= b0
+    assert spans[-1][1] <= info.ws_words
+    # vector flags: rows need C % 8 == 0
+    for i, s in enumerate(shapes):
+        assert descs[i].vec_rows == (1 if descs[i].C % 8 == 0 else 0)
+
+
+def test_plan_rejects_rows_longer_than_the_register_budget():
+    rc, *_ = _plan([(4, 16385)])
+    assert rc != 0
+    msg = _lib().lib().kaon_last_error().decode()
+    assert "16384" in msg
+
+
+def test_constructor_validation_mirrors_reference():
+    from kaon_amd import Adakaon, Lion, Nekaon
+
+    p = [torch.nn.Parameter(torch.zeros(4, 4))]
+    for bad in (dict(betas=(1.0, 0.9)), dict(betas=(0.9, -0.1)), dict(lr=-1.0), dict(clip_threshold=0.0),
+                dict(momentum_dtype="int4"), dict(bf16_method="round"), dict(foreach_batch_cutoff=0)):
+        with pytest.raises(ValueError):
+            Adakaon(p, **bad)
+    with pytest.raises(ValueError):
+        Lion(p, weight_decay=-0.1)
+    with pytest.raises(ValueError):
+        Nekaon(p, k=-1.0)
+    with pytest.raises(ValueError):
+        Nekaon(p, betas=(0.0, 0.999))
+    with pytest.raises(TypeError):
+        Nekaon([{"params": p}], low_vram_above=10)
+
+
+def test_cpu_params_fail_loudly():
+    """There is no CPU fallback: a step on CPU tensors raises."""
+    from kaon_amd import Adakaon
+
+    p = torch.nn.Parameter(torch.zeros(4, 4))
+    p.grad = torch.ones(4, 4)
+    opt = Adakaon([p])
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.step()
+
+
+def test_state_layout_matches_reference_at_init():
+    """_init_state layouts (adakaon.py:318-335, _momentum_codec.py:293-361) on CPU tensors."""
+    from kaon_amd import Adakaon, Lion
+    from kaon_amd._base import init_momentum_state
+
+    conv = torch.nn.Parameter(torch.zeros(8, 4, 3, 3, dtype=torch.bfloat16))
+    conv.grad = torch.zeros_like(conv)
+    vec = torch.nn.Parameter(torch.zeros(10))
+    vec.grad = torch.zeros_like(vec)
+    opt = Adakaon([conv, vec], momentum_dtype="int8", bf16_method="kahan")
+    st, sv = {}, {}
+    opt._init_state(conv, st, opt.param_groups[0])
+    opt._init_state(vec, sv, opt.param_groups[0])
+    assert st["row"].shape == (8,) and st["col"].shape == (36,)
+    assert st["m"].dtype == torch.int8 and st["m"].shape == conv.shape
+    assert st["m_scale"].shape == (8, 1, 1, 1) and st["shift"].dtype == torch.bfloat16
+    assert sv["v"].shape == (10,) and sv["m_scale"].shape == () and "shift" not in sv
+    s4 = {}
+    init_momentum_state(s4, vec.grad, dict(momentum_dtype="4bit", momentum_4bit_block=4))
+    assert s4["m"].tolist() == [0x88] * 5 and s4["m_scale"].shape == (3,) and s4["m_block"] == 4
+    lion = Lion([vec], momentum_dtype="bfloat16")
+    sl = {}
+    lion._init_state(vec, sl, lion.param_groups[0])
+    assert sl["m"].dtype == torch.bfloat16 and set(sl) == {"m"}

@@ -1,0 +1,246 @@
+"""Optimizer-step throughput on a synthetic SDXL-UNet-shaped 2.664B-param bf16 set, 1 GPU.
+
+Metric: Gparam/s and % of the HBM roofline per optimizer step.
+Default workload = BASELINE configs[2]: Adakaon, betas (0.9, 0.999), int8
+momentum, cautious, gradient centralization, stochastic-rounding bf16 writes,
+lr 1e-4 (the north star's target config).  ``--workload lion_int8``
+(configs[1]) and ``nekaon_4bit`` select the others.
+
+A "step" is one ``optimizer.step()`` over all 1,678 tensors with the params,
+grads and optimizer state resident in HBM.  W untimed warmup steps (the first
+one builds the plan and the state), then K steps between two
+``torch.cuda.synchronize()`` calls.
+
+Besides the JSON line's ``value`` (Gparam/s) the line carries
+* ``roofline``: the dominant kernel of the step (largest share of the step
+  time), its algorithmic HBM bytes per launch (bytes/param of that kernel x
+  params) divided by its average duration, measured with HIP events on the
+  launch stream (one phase at a time through ``kaon_adakaon_phases``);
+* ``step_roofline``: the whole step at the algorithmic 2 + 4 + 2*b_m bytes/param
+  (g read, p read+write, momentum read+write), against 8 TB/s and against a
+  copy kernel measured on the same device;
+* ``cpu_baseline``: the CPU oracle (oracle/kaon_oracle.c, one thread) stepping a
+  bounded sample of the same tensors -- a reported baseline, not the target.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "k-optimizers_amd"))
+
+METRIC = "Gparam/s + % HBM roofline per optimizer step, 2.6B bf16 params, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    "adakaon_int8": dict(desc="configs[2]: Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, SR bf16, lr 1e-4",
+                         opt="adakaon", kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8"), bm=1.0),
+    "lion_int8": dict(desc="configs[1]: Lion betas=(0.95,0.98) int8 momentum, cautious, GC, SR bf16, lr 2e-4",
+                      opt="lion", kw=dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="int8"), bm=1.0),
+    "nekaon_4bit": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 128, wd 0.1, cautious, GC, SR bf16, "
+                             "lr 1e-4, 1% Student-t outliers", opt="nekaon",
+                        kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=128),
+                        bm=0.5, outliers=0.01),
+}
+
+# algorithmic HBM bytes per param of each phase kernel (bf16 g/p, b_m momentum bytes)
+PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor", 5: "keep_count", 6: "apply"}
+
+
+def phase_bytes(phase: int, bm: float, wd: bool) -> float:
+    if phase in (1, 3):
+        return 2.0
+    if phase == 5:
+        return 2.0 + bm + (2.0 if wd else 0.0)
+    if phase == 6:
+        return 2.0 + 4.0 + 2.0 * bm
+    return 0.0
+
+
+def make_opt(name, params):
+    from kaon_amd import Adakaon, Lion, Nekaon
+
+    w = WORKLOADS[name]
+    if w["opt"] == "adakaon":
+        return Adakaon(params, **w["kw"])
+    if w["opt"] == "lion":
+        return Lion(params, **w["kw"])
+    return Nekaon(params, **w["kw"])
+
+
+def copy_ceiling_gbs(dev, nbytes=4 << 30, reps=10) -> float:
+    import torch
+    from kaon_amd import _lib
+
+    src = torch.empty(nbytes // 2, dtype=torch.int16, device=dev)
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    lib = _lib.lib()
+    _lib.check(lib.kaon_copy(src.data_ptr(), dst.data_ptr(), nbytes, s), "kaon_copy")
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        lib.kaon_copy(src.data_ptr(), dst.data_ptr(), nbytes, s)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    del src, dst
+    return 2.0 * nbytes / (ms * 1e-3) / 1e9
+
+
+def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
+    """Average duration (ms) of each phase kernel, HIP events on the launch stream."""
+    import torch
+    from kaon_amd import _lib
+
+    inner = getattr(opt, "inner", opt)
+    lib = _lib.lib()
+    out: dict[int, list[float]] = {}
+    for (gid, pdt, gdt), (_key, plan) in inner._plans.items():
+        group = inner.param_groups[gid]
+        if WORKLOADS[name]["opt"] == "lion":
+            hp = inner._hyper(group, pdt, gdt)
+            fn, phases = lib.kaon_lion_phases, (1, 5, 6)
+        else:
+            nk = None
+            if WORKLOADS[name]["opt"] == "nekaon":
+                nk = {"remove": True, "bound_old": dict(opt._eclamp), "k": opt.k, "eclamp": {}}
+            hp = inner._hyper(group, pdt, gdt, nk, gid)
+            fn, phases = lib.kaon_adakaon_phases, (1, 2, 3, 4, 5, 6)
+        s = torch.cuda.current_stream().cuda_stream
+        for _ in range(reps):
+            for ph in phases:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _lib.check(fn(ctypes.byref(plan.launch), ctypes.byref(hp), 1 << ph, s), "phase")
+                e1.record()
+                torch.cuda.synchronize()
+                out.setdefault(ph, []).append(e0.elapsed_time(e1))
+    return {ph: sum(v) / len(v) for ph, v in out.items()}
+
+
+def cpu_baseline(params, name, seconds: float) -> dict:
+    """The CPU oracle (single thread) stepping tensors of the same set until the
+    time budget is spent; Gparam/s over the tensors it finished."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    w = WORKLOADS[name]
+    kw = w["kw"]
+    group = dict(lr=kw["lr"], betas=kw["betas"], eps=(1e-30, 1e-3), weight_decay=0.1 if w["opt"] == "nekaon" else 0.0,
+                 clip_threshold=1.0, momentum_dtype=kw["momentum_dtype"],
+                 momentum_4bit_block=kw.get("momentum_4bit_block", 128), cautious=True,
+                 gradient_centralization=True, bf16_method="stochastic_rounding", k=1.5)
+    order = np.random.default_rng(0).permutation(len(params))
+    done = 0
+    elapsed = 0.0
+    ntens = 0
+    for idx in order:
+        p = params[int(idx)]
+        shape = tuple(p.shape)
+        prm = O.OParam(p=p.detach().view(torch.int16).cpu().numpy().view(np.uint16).copy(), p_dtype=O.BF16,
+                       shape=shape, tensor_id=int(idx),
+                       g=p.grad.view(torch.int16).cpu().numpy().view(np.uint16).copy(), g_dtype=O.BF16)
+        oopt = O.OracleOptimizer([prm], "adakaon" if w["opt"] == "nekaon" else w["opt"], group, seed=0)
+        t0 = time.perf_counter()
+        oopt.step()
+        elapsed += time.perf_counter() - t0
+        done += prm.numel
+        ntens += 1
+        if elapsed >= seconds:
+            break
+    return {"value": done / elapsed / 1e9, "unit": "Gparam/s", "cores": 1, "kind": "port",
+            "sample": f"one {w['opt']} step of {ntens} tensors ({done / 1e6:.1f}M params) drawn at random from "
+                      f"the same set, CPU oracle oracle/kaon_oracle.c, 1 thread, {elapsed:.1f}s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="adakaon_int8", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-breakdown", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the step shards by whole tensors with no exchange inside it, so N GPUs would run this same "
+              "kernel on 1/N of the set", file=sys.stderr)
+        return 2
+
+    import torch
+    from kaon_amd import workloads
+
+    dev = torch.device("cuda:0")
+    w = WORKLOADS[args.workload]
+    shapes = workloads.sdxl_shapes()
+    nparam = workloads.n_params(shapes)
+    print(f"[bench] {args.workload}: {len(shapes)} tensors, {nparam / 1e9:.3f}B params", file=sys.stderr, flush=True)
+    params = workloads.make_params(shapes, dev, seed=0, outlier_frac=w.get("outliers", 0.0))
+    opt = make_opt(args.workload, params)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(args.steps):
+        opt.step()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / args.steps
+    gps = nparam / (ms * 1e-3) / 1e9
+    bm = w["bm"]
+    b_alg = 2.0 + 4.0 + 2.0 * bm
+    step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
+    print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
+          file=sys.stderr, flush=True)
+
+    ceiling = copy_ceiling_gbs(dev)
+    out = {
+        "metric": METRIC, "value": round(gps, 2), "unit": "Gparam/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": w["desc"], "shape_set": "SDXL-UNet-shaped (1678 tensors)", "n_params": nparam,
+                   "params": "bf16", "grads": "bf16",
+                   "momentum": WORKLOADS[args.workload]["kw"]["momentum_dtype"], "parallelism": "none (1 GPU)"},
+        "step_roofline": {"bound": "hbm", "bytes_per_param": b_alg, "achieved": round(step_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                          "copy_ceiling": round(ceiling, 1), "frac_of_copy": round(step_gbs / ceiling, 4)},
+    }
+    if not args.no_breakdown:
+        br = phase_breakdown(opt, args.workload)
+        wd = w["opt"] == "nekaon"
+        dom = max(br, key=lambda k: br[k])
+        bpp = phase_bytes(dom, bm, wd)
+        ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
+        out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                           "kernel": f"phase {dom} ({PHASE_NAMES[dom]})", "bytes_per_param": bpp,
+                           "avg_ms": round(br[dom], 4)}
+        out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

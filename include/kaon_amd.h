@@ -82,32 +82,37 @@ typedef struct KaonTensor {
   /* workspace offsets, in 4-byte words from the workspace base (kaon_plan) */
   int64_t ws_row;         /* 5 arrays of R words: mu, rf, rs, amax, oldscale */
   int64_t ws_col;         /* cf [C] */
-  int64_t ws_part;        /* column partials [ngroups][C] */
+  int64_t ws_part;        /* column partials [ngroups][C], one row per slice */
   int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
   int64_t ws_scal;        /* 4 words: fac, keep-count, spare, spare */
   int64_t ws_aux;         /* AdaMuon Newton-Schulz scratch (bf16 words) */
   int32_t tensor_id;      /* SR counter field: index in the optimizer's param list */
   int32_t block4;         /* 4-bit block size (m_block) */
   int32_t factored;       /* ndim >= 2 */
-  int32_t ngroups;        /* ceil(R / KAON_COLGROUP) */
+  int32_t ngroups;        /* number of slices */
   float sqrt_n;           /* (float)sqrt((double)n), the rms divisor (_backend.py:45-47) */
-  int32_t vec_rows;       /* 16-byte vector path for row-wise chunks (C % 8 == 0, aligned) */
+  int32_t vec_rows;       /* 16-byte vector path for row chunks (C % 8 == 0 or one row, aligned) */
   int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
   int32_t pad;
 } KaonTensor;
 
-/* A row-phase work item: rows [row0, row0 + nrows) of tensor `tensor`. */
+/* A work item.  Slices: rows [row0, row0 + nrows) of tensor `tensor`, kind =
+ * rows per wave group.  Finalize items: kind 0 = columns [row0, row0+nrows),
+ * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows). */
 typedef struct KaonItem {
   int32_t tensor;
   int32_t row0;
   int32_t nrows;
-  int32_t kind;           /* finalize items: 0 = columns [row0, row0+nrows), 1 = row stats */
+  int32_t kind;
 } KaonItem;
 
-/* Rows per row-phase work item; also the column-sum group of the canonical
- * reduction order (column sums accumulate KAON_COLGROUP rows in row order,
- * then the group partials in group order). */
-#define KAON_COLGROUP 32
+/* Work decomposition and canonical reduction order shared with the CPU
+ * oracle.  Row sums: 64 lanes, lane l adds the 8-element chunks l, l+64, ...
+ * in order, then an xor butterfly.  Column sums: wave groups of
+ * RW = max(1, KAON_ROW_BUDGET / chunks-per-lane) consecutive rows (summed in
+ * row order), slices of 4 wave groups (folded in order), slices added in
+ * order.  One slice is one workgroup of 4 wave64. */
+#define KAON_ROW_BUDGET 20
 /* Columns per column-finalize work item. */
 #define KAON_COLITEM 2048
 
@@ -118,12 +123,23 @@ typedef struct KaonItem {
  */
 typedef struct KaonPlanInfo {
   int32_t n_tensors;
-  int32_t n_row_items;    /* row items (phases 1 and 3), sorted by register class */
+  int32_t n_row_items;    /* slices, sorted by phase-1 register class (row_items) */
   int32_t n_fin_items;    /* finalize items (phase 2) */
-  int32_t n_flat_items;   /* flat items of KAON_FLAT_ITEM elements (phases 5 and 6) */
-  int32_t row_runs[4];    /* row items per register class: rows of <= 2048, 4096, 8192, 16384 elements */
+  int32_t n_flat_items;   /* flat items of KAON_FLAT_ITEM elements (MSAM perturbation) */
+  int32_t row_runs[4];    /* slices per phase-1 register class: rows of <= 4, 10, 24 chunks per
+                             lane held in registers, streamed rows */
+  int32_t n_fast;         /* slices of elem_items that take the specialized kernels */
+  int32_t pad;
   int64_t ws_words;       /* workspace size in 4-byte words */
 } KaonPlanInfo;
+
+/* What a plan is built for (one param group and dtype pair). */
+typedef struct KaonPlanArgs {
+  int32_t opt;            /* KAON_OPT_* */
+  int32_t codec;          /* KAON_MOM_* of the group (KAON_MOM_NONE without momentum) */
+  int32_t p_dtype, g_dtype;
+  int32_t bf16_method;    /* KAON_SR / KAON_RN / KAON_KAHAN */
+} KaonPlanArgs;
 
 /* Elements per flat work item. */
 #define KAON_FLAT_ITEM 16384
@@ -133,11 +149,13 @@ typedef struct KaonPlanInfo {
 /* Device-side tables of one planned group, passed to every step entry point. */
 typedef struct KaonLaunch {
   const KaonTensor* descs;    /* device copy of the planned descriptors */
-  const KaonItem* row_items;  /* device */
+  const KaonItem* row_items;  /* device: slices by register class (phase 1) */
+  const KaonItem* elem_items; /* device: the same slices, specialized-kernel ones first */
   const KaonItem* fin_items;  /* device */
   const KaonItem* flat_items; /* device */
   int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
   int32_t row_runs[4];
+  int32_t n_fast, pad;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
 } KaonLaunch;
 
@@ -169,11 +187,12 @@ const char* kaon_last_error(void);
  * pointer-array caches PointerArrayCache / OneDimPointerCache,
  * _fused_triton.py:1183-1320).  descs: host array of n descriptors with
  * pointers, shapes, block4 and tensor_id filled; on return their ws_*,
- * ngroups, sqrt_n and vec_* fields are set.  Item arrays may be NULL to query
- * sizes; info is always filled.  Returns 0, or non-zero with kaon_last_error()
- * set (e.g. a factored row longer than KAON_MAX_ROW). */
-int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t n, KaonItem* row_items,
-              KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info);
+ * ngroups, sqrt_n and vec_* fields are set.  row_items and elem_items hold
+ * n_row_items entries each.  Item arrays may be NULL to query sizes; info is
+ * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
+ * factored row longer than KAON_MAX_ROW). */
+int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
+              KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info);
 
 /* Adakaon step over one planned param group, Nekaon's remove/climb fused in
  * when the KAON_F_NK_* flags are set.  Replaces Adakaon._fused_step and the
@@ -186,7 +205,7 @@ int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
 /* The same steps restricted to the phases whose bit is set in `mask`
  * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,
- * 4 clip divisor, 5 keep-count/absmax, 6 apply; Lion uses 1, 5, 6).  For
+ * 5 clip divisor + keep-count + absmax, 6 apply; Lion uses 1, 5, 6).  For
  * profiling one kernel at a time; running all phases in order is the step.
  * No counterpart in the reference, which has no phase boundary to expose. */
 int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);

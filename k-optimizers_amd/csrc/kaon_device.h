@@ -179,41 +179,50 @@ __device__ __forceinline__ void st8_f32(void* base, int64_t off, int cnt, bool v
 }
 
 // ------------------------------------------------------------------ reductions
-// Canonical chunked sum (the oracle's CSUM): lane l of 256 accumulates, in
-// order, the 8 elements of its chunks l, l+256, ...; each wave64 is reduced by
-// an xor butterfly (offsets 32..1); the wave totals of the waves that own any
-// chunk are folded left to right.  `a` is this thread's accumulator; lds4
-// holds 4 floats.  Every thread returns the total.  Contains barriers: call
-// from uniform control flow.
-__device__ __forceinline__ float csum_finish(float a, int64_t nch, float* lds4) {
+// Canonical 64-lane sum (the oracle's CSUM): every lane has accumulated, in
+// order, the elements of its chunks l, l+64, ...; the lane sums are reduced by
+// an xor butterfly with offsets 32..1 and lane 0's result is the canonical one
+// (other lanes add in other orders).  Call with all 64 lanes active; returns
+// lane 0's value to every lane.
+__device__ __forceinline__ float wave_csum(float a) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) a = a + __shfl_xor(a, o, 64);
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) lds4[wave] = a;
-  __syncthreads();
-  int nw = (int)((nch + 63) / 64);
-  if (nw > 4) nw = 4;
-  float r = lds4[0];
-  for (int w = 1; w < nw; ++w) r = r + lds4[w];
-  __syncthreads();
-  return r;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a)));
 }
 
-// Workgroup integer sum (order-free) -> thread 0 gets it.
-__device__ __forceinline__ uint32_t wg_sum_u32(uint32_t a, uint32_t* lds4) {
+__device__ __forceinline__ float wave_max(float a) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a)));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t a) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
-  if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = a;
-  __syncthreads();
-  uint32_t r = lds4[0] + lds4[1] + lds4[2] + lds4[3];
-  __syncthreads();
-  return r;
+  return __builtin_amdgcn_readfirstlane(a);
+}
+
+__device__ __forceinline__ float uniform_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
 
 // Non-negative float max through its bit pattern (monotone for x >= 0).
 __device__ __forceinline__ uint32_t fmax_bits(uint32_t a, float x) {
   const uint32_t b = __float_as_uint(x);
   return b > a ? b : a;
+}
+
+// Round two floats to bf16 (RNE) and back with the gfx950 conversion
+// instruction.  Matches f2bf() for every non-NaN input (checked exhaustively
+// on the device); a NaN stays NaN with an unspecified payload, so use it only
+// for values that are never stored.
+typedef __bf16 kaon_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float kaon_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+  kaon_f32x2 v = {a, b};
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, kaon_bf16x2));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xFFFF0000u);
 }
 
 }  // namespace kaon

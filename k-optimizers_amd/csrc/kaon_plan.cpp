@@ -7,11 +7,13 @@
 // Here one descriptor per tensor carries every pointer and shape, and the plan
 // adds what the HIP kernels need: a workspace layout for the per-row /
 // per-column / per-block intermediates and three work-item tables.
-//   row items   KAON_COLGROUP rows of one factored tensor (the whole tensor
-//               for a 1-D param), sorted by register class (row length) so
+//   slices      4 wave groups of RW consecutive rows of one tensor (RW =
+//               max(1, 20 / chunks-per-lane); the whole tensor for a 1-D
+//               param), sorted by register class (row length, grad dtype) so
 //               each class is one launch with a fixed register budget;
 //   fin items   KAON_COLITEM columns of one factored tensor, or its row stats;
-//   flat items  KAON_FLAT_ITEM consecutive elements of one tensor.
+//   flat items  KAON_FLAT_ITEM consecutive elements of one tensor (the MSAM
+//               perturbation).
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -34,24 +36,54 @@ bool aligned(const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p 
 
 int64_t round4(int64_t x) { return (x + 3) & ~int64_t(3); }
 
-int row_class(const KaonTensor& t) {
-  if (!t.factored) return 0;
-  const int64_t nch = (t.C + 7) / 8;
-  const int64_t cpt = (nch + 255) / 256;
-  if (cpt <= 1) return 0;
-  if (cpt <= 2) return 1;
-  if (cpt <= 4) return 2;
+int64_t chunks_per_lane(int64_t C) {
+  const int64_t nch = (C + 7) / 8;
+  const int64_t cpl = (nch + 63) / 64;
+  return cpl < 1 ? 1 : cpl;
+}
+
+// rows per wave group (the column-sum order of the CPU oracle)
+int64_t rows_per_wave(int64_t C) {
+  const int64_t rw = KAON_ROW_BUDGET / chunks_per_lane(C);
+  return rw < 1 ? 1 : rw;
+}
+
+// register class of the phase-1 kernel: rows held in registers up to 4, 10
+// and 24 chunks per lane (24 only for bf16 grads), else streamed (class 3)
+int row_class(const KaonTensor& t, int32_t g_dtype) {
+  if (!t.factored) return 3;
+  const int64_t cpl = chunks_per_lane(t.C);
+  if (cpl <= 4) return 0;
+  if (cpl <= 10) return 1;
+  if (cpl <= 24 && g_dtype == KAON_BF16) return 2;
   return 3;
 }
 }  // namespace
 
-extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t n, KaonItem* row_items,
-                         KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info) {
+// Tensors whose slices take the specialized phase-5/6 kernels: bf16 params and
+// grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
+// momentum blocks of 8*G elements (G | 64) that tile the rows.
+bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
+  if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
+  if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
+  if (a.codec == KAON_MOM_F32) return false;
+  if (a.codec == KAON_MOM_4BIT) {
+    const int64_t B = t.block4;
+    if (B % 8 != 0 || t.C % B != 0 || B / 8 > 64 || 64 % (B / 8) != 0) return false;
+  }
+  return true;
+}
+
+extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
+                         KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info) {
   if (!info) return plan_fail("kaon_plan: info is NULL");
+  if (!args) return plan_fail("kaon_plan: args is NULL");
+  const int32_t opt = args->opt, codec = args->codec, g_dtype = args->g_dtype;
   if (n < 0 || (n > 0 && !descs)) return plan_fail("kaon_plan: bad descriptor array");
   if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON)
     return plan_fail("kaon_plan: unknown optimizer");
   if (codec < KAON_MOM_NONE || codec > KAON_MOM_4BIT) return plan_fail("kaon_plan: unknown codec");
+  if (g_dtype != KAON_F32 && g_dtype != KAON_BF16) return plan_fail("kaon_plan: unknown grad dtype");
   std::memset(info, 0, sizeof(*info));
   info->n_tensors = n;
 
@@ -60,6 +92,7 @@ extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t 
     KaonItem it;
     int cls;
     int64_t size;
+    bool fast;
   };
   std::vector<RowIt> rows;
   std::vector<KaonItem> fins, flats;
@@ -75,11 +108,13 @@ extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t 
     if (!t.factored && t.R != 1) return plan_fail("kaon_plan: a 1-D tensor must have R == 1");
     if (codec == KAON_MOM_4BIT && t.block4 < 1) return plan_fail("kaon_plan: 4-bit block size must be >= 1");
     t.sqrt_n = (float)std::sqrt((double)(t.n > 1 ? t.n : 1));
-    t.ngroups = (int32_t)((t.R + KAON_COLGROUP - 1) / KAON_COLGROUP);
+    const int64_t rw = rows_per_wave(t.C);
+    const int64_t slice_rows = 4 * rw;
+    t.ngroups = (int32_t)((t.R + slice_rows - 1) / slice_rows);
     const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
                     aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16);
     t.vec_flat = al ? 1 : 0;
-    t.vec_rows = (al && t.C % 8 == 0) ? 1 : 0;
+    t.vec_rows = (al && (t.C % 8 == 0 || t.R == 1)) ? 1 : 0;
     // workspace: 4-word aligned arrays
     t.ws_row = off;
     off = round4(off + 5 * t.R);
@@ -99,15 +134,12 @@ extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t 
     off = round4(off + 4);
     t.ws_aux = off;
     if (t.n == 0) continue;
-    // row items
-    const int cls = row_class(t);
-    if (t.factored) {
-      for (int64_t r0 = 0; r0 < t.R; r0 += KAON_COLGROUP) {
-        KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(KAON_COLGROUP, t.R - r0), 0};
-        rows.push_back({it, cls, t.n});
-      }
-    } else {
-      rows.push_back({KaonItem{i, 0, 1, 0}, cls, t.n});
+    // slices (row items): kind = rows per wave group
+    const int cls = row_class(t, g_dtype);
+    const bool fast = fast_eligible(*args, t);
+    for (int64_t r0 = 0; r0 < t.R; r0 += slice_rows) {
+      KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(slice_rows, t.R - r0), (int32_t)rw};
+      rows.push_back({it, cls, t.n, fast});
     }
     // finalize items (Adakaon / AdaMuon factored second moment)
     if (t.factored && opt != KAON_OPT_LION) {
@@ -118,6 +150,12 @@ extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t 
     for (int64_t e0 = 0; e0 < t.n; e0 += KAON_FLAT_ITEM)
       flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, t.n - e0), 0});
   }
+  // elem order: specialized-kernel slices first, each part largest tensors first
+  std::vector<RowIt> elems = rows;
+  std::stable_sort(elems.begin(), elems.end(), [](const RowIt& a, const RowIt& b) {
+    if (a.fast != b.fast) return a.fast;
+    return a.size > b.size;
+  });
   // register classes in ascending order; inside a class the largest tensors
   // first so their long runs of items start early
   std::stable_sort(rows.begin(), rows.end(), [](const RowIt& a, const RowIt& b) {
@@ -125,6 +163,9 @@ extern "C" int kaon_plan(int32_t opt, int32_t codec, KaonTensor* descs, int32_t 
     return a.size > b.size;
   });
   info->n_row_items = (int32_t)rows.size();
+  for (const RowIt& r : elems) info->n_fast += r.fast ? 1 : 0;
+  if (elem_items)
+    for (size_t k = 0; k < elems.size(); ++k) elem_items[k] = elems[k].it;
   info->n_fin_items = (int32_t)fins.size();
   info->n_flat_items = (int32_t)flats.size();
   for (const RowIt& r : rows) info->row_runs[r.cls]++;

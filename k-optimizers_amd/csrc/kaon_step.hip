@@ -9,18 +9,22 @@
 //   writes   src/kaon/_backend.py:82-142, _stochastic_rounding.py:70-103
 //   factored src/kaon/_factored.py:26-83; GC src/kaon/_backend.py:147-177
 //
-// One step of one param group runs as a short sequence of multi-tensor
-// launches, each covering every tensor of the group through a work-item table
-// (the descriptor table replaces the reference's per-role pointer arrays):
-//   phase 1  row items   GC row means, row second-moment EMA, column partials
-//   phase 2  fin items   column EMA + column factors; row-mean + row factors
-//   phase 3  row items   per-row sum of U^2 (U = G*r*c) for the RMS clip
-//   phase 4  per tensor  clip divisor
-//   phase 5  flat items  cautious keep-count, momentum absmax, old-scale copy
-//   phase 6  flat items  requant + momentum write, cautious rescale, weight
+// Work decomposition.  A work item is a slice: 4 wave groups of RW
+// consecutive rows of one tensor (RW = max(1, 20 / chunks-per-lane) so a wave
+// group spans about 160 elements per lane).  Each wave64 owns its rows whole:
+// lane l handles the 8-element chunks l, l+64, ... of every row, so every row
+// reduction (GC mean, second-moment row mean, clip sums, int8 absmax) is a
+// wave-local butterfly with no LDS or barrier, and per-row values are
+// wave-uniform.  The tensor-global dependencies (column factors, row-mean,
+// clip divisor, cautious keep-count) split one step into launches:
+//   phase 1  slices      GC row means, row EMA, column partials (LDS fold)
+//   phase 2  fin items   column EMA + column factors; row mean + row factors
+//   phase 3  slices      per-row sums of U^2 (U = G*r*c)
+//   phase 5  slices      clip divisor, cautious keep-count, momentum absmax
+//   phase 6  slices      requant + momentum write, cautious rescale, weight
 //                        write (SR / RN / kahan / fp32), Nekaon remove+climb
-// Reductions follow one fixed order (the canonical order of the CPU oracle);
-// there are no floating-point atomics, so results are deterministic.
+// All reductions follow the CPU oracle's canonical order; there are no
+// floating-point atomics, so results are deterministic and bit-exact.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -74,147 +78,247 @@ __device__ __forceinline__ float round_to(float x) {
   return DT == KAON_BF16 ? rbf(x) : x;
 }
 
-__device__ __forceinline__ int64_t nblocks4(const KaonTensor& T) {
-  return (T.n + T.block4 - 1) / T.block4;
+__device__ __forceinline__ int64_t nblocks4(const KaonTensor& T) { return (T.n + T.block4 - 1) / T.block4; }
+
+// Rows [rb, re) of the calling wave inside slice `it` (RW rows per wave).
+struct WaveRows {
+  int64_t rb, re;
+  int w, lane;
+};
+__device__ __forceinline__ WaveRows wave_rows(const KaonItem& it) {
+  WaveRows wr;
+  wr.w = threadIdx.x >> 6;
+  wr.lane = threadIdx.x & 63;
+  const int64_t end = (int64_t)it.row0 + it.nrows;
+  wr.rb = min((int64_t)it.row0 + (int64_t)wr.w * it.kind, end);
+  wr.re = min(wr.rb + it.kind, end);
+  return wr;
 }
 
-// Zero what later phases accumulate with atomics (keep-count, absmax).  Run by
-// the phase-1 item that owns rows [row0, row0+nrows).
+// Chunks of a row: the element range [8c, 8c+8) clipped to the row length.
+__device__ __forceinline__ int chunk_cnt(int64_t c, int64_t C) {
+  const int64_t j0 = c * 8;
+  return j0 >= C ? 0 : (int)min<int64_t>(8, C - j0);
+}
+
+// Zero what phase 5 accumulates with atomics (keep-count; 4-bit block absmax
+// of blocks that straddle rows).  Run by the phase-1 slice.
 __device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const Ws& ws, int codec) {
   if (it.row0 == 0 && threadIdx.x == 0) ((uint32_t*)ws.scal(T))[1] = 0u;
-  if (codec == KAON_MOM_INT8) {
-    for (int i = threadIdx.x; i < it.nrows; i += KAON_WG) ws.ramax(T)[it.row0 + i] = 0u;
-  } else if (codec == KAON_MOM_4BIT) {
+  if (codec == KAON_MOM_4BIT) {
     const int64_t e_begin = (int64_t)it.row0 * T.C;
     const int64_t e_end = (int64_t)(it.row0 + it.nrows) * T.C;
+    if (e_end <= e_begin) return;
     const int64_t b0 = e_begin / T.block4, b1 = (e_end - 1) / T.block4;
     for (int64_t b = b0 + threadIdx.x; b <= b1; b += KAON_WG) ws.bamax(T)[b] = 0u;
   }
 }
 
 // =============================================================== phase 1
-// Row items.  mode 0 (Adakaon): GC row mean (stored), row EMA of mean_C(G^2),
-// column partial sums of KAON_COLGROUP rows; 1-D tensors: v EMA.  mode 1
-// (Lion): GC row mean only.  KM bounds the chunks per thread kept in
-// registers (C <= 2048*KM).
-template <int GT, int KM>
-__global__ __launch_bounds__(KAON_WG) void k_rows(const KaonTensor* __restrict__ D,
-                                                  const KaonItem* __restrict__ items, Ws ws,
-                                                  KaonHyper hp, int mode) {
-  __shared__ float lds4[4];
+// mode 0 (Adakaon): GC row mean (stored), row EMA of mean_C(G^2), column
+// partial of the slice (wave groups folded in order in LDS); 1-D tensors: v
+// EMA.  mode 1 (Lion): GC row means only.  CPL > 0 keeps a row of up to CPL
+// chunks per lane in registers; CPL == 0 streams the row from memory (used for
+// rows longer than 24 chunks per lane, fp32 grads with long rows, and 1-D).
+template <int GT, int CPL>
+__global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict__ D,
+                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
+                                                   int mode) {
+  extern __shared__ float lds_col[];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   zero_accumulators(T, it, ws, hp.codec);
   const int64_t C = T.C;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec = T.vec_rows != 0;
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  const WaveRows wr = wave_rows(it);
 
   if (!T.factored) {
-    const bool vec = T.vec_flat != 0;
+    // v = lerp(v, g*g (+eps1), 1-beta2) over the single row (adakaon.py:990-995)
     if (mode != 0) return;
-    // v = lerp(v, g*g (+eps1), 1-beta2)  (adakaon.py:990-995)
-    const int64_t nch = (C + 7) >> 3;
     for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
-      const int64_t j0 = c * 8;
-      const int cnt = (int)min<int64_t>(8, C - j0);
+      const int cnt = chunk_cnt(c, C);
       const bool vv = vec && cnt == 8;
       float x[8], v[8];
-      ld8<GT>(T.g, j0, cnt, vv, x);
-      ld8<KAON_F32>(T.v, j0, cnt, vv, v);
+      ld8<GT>(T.g, c * 8, cnt, vv, x);
+      ld8<KAON_F32>(T.v, c * 8, cnt, vv, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float q = x[i] * x[i];
         if (eps) q = q + hp.eps1;
         v[i] = klerp(v[i], q, hp.w2);
       }
-      st8_f32(T.v, j0, cnt, vv, v);
+      st8_f32(T.v, c * 8, cnt, vv, v);
     }
     return;
   }
 
   const bool gc = (hp.flags & KAON_F_GC) != 0;
   if (mode == 1 && !gc) return;
-  const bool vec = T.vec_rows != 0;
-  const int64_t nch = (C + 7) >> 3;
   float* mu_arr = ws.mu(T);
-  float colacc[KM][8];
+  const int RW = it.kind;
+
+  // registers: row buffer (CPL chunks) and the wave-group column partial
+  constexpr int NB = CPL > 0 ? CPL : 1;
+  float xb[NB][8];
+  float colacc[NB][8];
 #pragma unroll
-  for (int k = 0; k < KM; ++k)
+  for (int k = 0; k < NB; ++k)
 #pragma unroll
     for (int i = 0; i < 8; ++i) colacc[k][i] = 0.0f;
 
-  for (int rr = 0; rr < it.nrows; ++rr) {
-    const int64_t r = (int64_t)it.row0 + rr;
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
     const int64_t rowoff = r * C;
-    float x[KM][8];
-    int cntk[KM];
+    float mu = 0.0f;
+    if (CPL > 0) {
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      const int64_t c = threadIdx.x + (int64_t)KAON_WG * k;
-      const int64_t j0 = c * 8;
-      const int cnt = c < nch ? (int)min<int64_t>(8, C - j0) : 0;
-      cntk[k] = cnt;
-      if (cnt > 0) {
-        ld8<GT>(T.g, rowoff + j0, cnt, vec && cnt == 8, x[k]);
-      } else {
+      for (int k = 0; k < NB; ++k) {
+        const int64_t c = wr.lane + 64 * k;
+        const int cnt = k < cpl ? chunk_cnt(c, C) : 0;
+        if (cnt > 0) ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, xb[k]);
+        else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[k][i] = 0.0f;
+          for (int i = 0; i < 8; ++i) xb[k][i] = 0.0f;
       }
-    }
-    if (gc) {
-      float a = 0.0f;
+      if (gc) {
+        float a = 0.0f;
 #pragma unroll
-      for (int k = 0; k < KM; ++k)
+        for (int k = 0; k < NB; ++k) {
+          const int cnt = k < cpl ? chunk_cnt(wr.lane + 64 * k, C) : 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (i < cntk[k]) a = a + x[k][i];
-      const float s = csum_finish(a, nch, lds4);
-      const float mu = round_to<GT>(s / (float)C);
-      if (threadIdx.x == 0) mu_arr[r] = mu;
-#pragma unroll
-      for (int k = 0; k < KM; ++k)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (i < cntk[k]) x[k][i] = round_to<GT>(x[k][i] - mu);
-    }
-    if (mode == 1) continue;
-    float a = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KM; ++k)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (i < cntk[k]) {
-          float q = x[k][i] * x[k][i];
-          if (eps) q = q + hp.eps1;
-          x[k][i] = q;
-          a = a + q;
+          for (int i = 0; i < 8; ++i)
+            if (i < cnt) a = a + xb[k][i];
         }
-    const float s2 = csum_finish(a, nch, lds4);
-    if (threadIdx.x == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
+        mu = round_to<GT>(wave_csum(a) / (float)C);
+        if (wr.lane == 0) mu_arr[r] = mu;
 #pragma unroll
-    for (int k = 0; k < KM; ++k)
+        for (int k = 0; k < NB; ++k) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (i < cntk[k]) colacc[k][i] = colacc[k][i] + x[k][i];
+          for (int i = 0; i < 8; i += 2) {
+            float a0 = xb[k][i] - mu, a1 = xb[k][i + 1] - mu;
+            if (GT == KAON_BF16) rbf2(a0, a1);
+            xb[k][i] = a0;
+            xb[k][i + 1] = a1;
+          }
+        }
+      }
+      if (mode == 1) continue;
+      float a2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const int cnt = k < cpl ? chunk_cnt(wr.lane + 64 * k, C) : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i < cnt) {
+            float q = xb[k][i] * xb[k][i];
+            if (eps) q = q + hp.eps1;
+            a2 = a2 + q;
+            if (RW > 1) colacc[k][i] = colacc[k][i] + q;
+          }
+      }
+      const float s2 = wave_csum(a2);
+      if (wr.lane == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
+    } else {
+      // streaming: sweep A (GC sum), sweep B (q and the row sum)
+      if (gc) {
+        float a = 0.0f;
+        for (int k = 0; k < cpl; ++k) {
+          const int64_t c = wr.lane + 64 * k;
+          const int cnt = chunk_cnt(c, C);
+          if (cnt <= 0) continue;
+          float x[8];
+          ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < cnt) a = a + x[i];
+        }
+        mu = round_to<GT>(wave_csum(a) / (float)C);
+        if (wr.lane == 0) mu_arr[r] = mu;
+      }
+      if (mode == 1) continue;
+      float a2 = 0.0f;
+      for (int k = 0; k < cpl; ++k) {
+        const int64_t c = wr.lane + 64 * k;
+        const int cnt = chunk_cnt(c, C);
+        if (cnt <= 0) continue;
+        float x[8];
+        ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i < cnt) {
+            const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
+            float q = gv * gv;
+            if (eps) q = q + hp.eps1;
+            a2 = a2 + q;
+          }
+      }
+      const float s2 = wave_csum(a2);
+      if (wr.lane == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
+    }
   }
   if (mode == 1) return;
-  float* part = ws.part(T) + (int64_t)(it.row0 / KAON_COLGROUP) * C;
+
+  // fold the wave-group partials in group order into the slice partial
+  const bool has_rows = wr.re > wr.rb;
+  for (int wf = 0; wf < 4; ++wf) {
+    if (wr.w == wf && has_rows) {
+      if (CPL > 0) {
 #pragma unroll
-  for (int k = 0; k < KM; ++k) {
-    const int64_t c = threadIdx.x + (int64_t)KAON_WG * k;
-    if (c >= nch) continue;
-    const int64_t j0 = c * 8;
-    const int cnt = (int)min<int64_t>(8, C - j0);
-    st8_f32(part, j0, cnt, vec && cnt == 8, colacc[k]);
+        for (int k = 0; k < NB; ++k) {
+          const int64_t c = wr.lane + 64 * k;
+          const int cnt = k < cpl ? chunk_cnt(c, C) : 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < cnt) {
+              float v;
+              if (RW > 1) {
+                v = colacc[k][i];
+              } else {
+                v = xb[k][i] * xb[k][i];
+                if (eps) v = v + hp.eps1;
+              }
+              const int64_t j = c * 8 + i;
+              lds_col[j] = wf == 0 ? v : lds_col[j] + v;
+            }
+        }
+      } else {
+        // streaming rows have RW == 1: recompute q of the wave's row
+        const int64_t r = wr.rb;
+        const float mu = gc ? mu_arr[r] : 0.0f;
+        for (int k = 0; k < cpl; ++k) {
+          const int64_t c = wr.lane + 64 * k;
+          const int cnt = chunk_cnt(c, C);
+          if (cnt <= 0) continue;
+          float x[8];
+          ld8<GT>(T.g, r * C + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < cnt) {
+              const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
+              float v = gv * gv;
+              if (eps) v = v + hp.eps1;
+              const int64_t j = c * 8 + i;
+              lds_col[j] = wf == 0 ? v : lds_col[j] + v;
+            }
+        }
+      }
+    }
+    __syncthreads();
   }
+  float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
+  for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = lds_col[j];
 }
 
 // =============================================================== phase 2
 // Finalize items.  kind 0: col = lerp(col, colsum/R, 1-beta2), cf = 1/sqrt(col)
-// for columns [row0, row0+nrows).  kind 1: rm = mean(row) (canonical sum),
-// rf = 1/sqrt(row/rm) (_factored.py:48-52, 76-82).
+// for columns [row0, row0+nrows), colsum = the slice partials added in slice
+// order.  kind 1: rm = mean(row) (canonical sum), rf = 1/sqrt(row/rm)
+// (_factored.py:48-52, 76-82).
 __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ float lds4[4];
+  __shared__ float rm_s;
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const int64_t R = T.R, C = T.C;
@@ -223,99 +327,88 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
     float* cf = ws.cf(T);
     for (int64_t j = it.row0 + threadIdx.x; j < (int64_t)it.row0 + it.nrows; j += KAON_WG) {
       float cs = 0.0f;
-      for (int g = 0; g < T.ngroups; ++g) cs = cs + part[(int64_t)g * C + j];
+      int g = 0;
+      for (; g + 8 <= T.ngroups; g += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(g + u) * C + j];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cs = cs + v[u];
+      }
+      for (; g < T.ngroups; ++g) cs = cs + part[(int64_t)g * C + j];
       const float nc = klerp(T.col[j], cs / (float)R, hp.w2);
       T.col[j] = nc;
       cf[j] = 1.0f / sqrtf(nc);
     }
   } else {
-    const int64_t nch = (R + 7) >> 3;
-    float a = 0.0f;
-    for (int64_t c = threadIdx.x; c < nch; c += KAON_WG)
-      for (int i = 0; i < 8; ++i) {
-        const int64_t j = c * 8 + i;
-        if (j < R) a = a + T.row[j];
-      }
-    const float rm = csum_finish(a, nch, lds4) / (float)R;
+    if (threadIdx.x < 64) {
+      const int64_t nch = (R + 7) >> 3;
+      float a = 0.0f;
+      for (int64_t c = threadIdx.x; c < nch; c += 64)
+        for (int i = 0; i < 8; ++i) {
+          const int64_t j = c * 8 + i;
+          if (j < R) a = a + T.row[j];
+        }
+      const float s = wave_csum(a);
+      if (threadIdx.x == 0) rm_s = s / (float)R;
+    }
+    __syncthreads();
+    const float rm = rm_s;
     float* rf = ws.rf(T);
     for (int64_t i = threadIdx.x; i < R; i += KAON_WG) rf[i] = 1.0f / sqrtf(T.row[i] / rm);
   }
 }
 
 // =============================================================== phase 3
-// Row items: rs[r] = canonical sum over the row of U^2, U = (G*rf)*cf
-// (factored) or G*(1/sqrt(v)) (1-D; the whole tensor is one row).
+// Slices: rs[r] = canonical sum over the row of U^2, U = (G*rf)*cf (factored)
+// or G*(1/sqrt(v)) (1-D: the whole tensor is one row).
 template <int GT>
 __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D,
                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ float lds4[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const int64_t C = T.C;
-  const bool vec = T.factored ? T.vec_rows != 0 : T.vec_flat != 0;
-  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
   const int64_t nch = (C + 7) >> 3;
-  const float* cfa = ws.cf(T);
-  for (int rr = 0; rr < it.nrows; ++rr) {
-    const int64_t r = (int64_t)it.row0 + rr;
-    const float mu = gc ? ws.mu(T)[r] : 0.0f;
-    const float rf = T.factored ? ws.rf(T)[r] : 0.0f;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec = T.vec_rows != 0;
+  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
+  const float* cfa = T.factored ? ws.cf(T) : T.v;
+  const WaveRows wr = wave_rows(it);
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    const float rf = T.factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
     float a = 0.0f;
-    for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
-      const int64_t j0 = c * 8;
-      const int cnt = (int)min<int64_t>(8, C - j0);
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
       const bool vv = vec && cnt == 8;
       float x[8], f[8];
-      ld8<GT>(T.g, r * C + j0, cnt, vv, x);
-      if (T.factored) ld8<KAON_F32>(cfa, j0, cnt, vv, f);
-      else ld8<KAON_F32>(T.v, j0, cnt, vv, f);
+      ld8<GT>(T.g, r * C + c * 8, cnt, vv, x);
+      ld8<KAON_F32>(cfa, c * 8, cnt, vv, f);
+      if (gc) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i >= cnt) break;
-        float g = x[i];
-        if (gc) g = round_to<GT>(g - mu);
-        const float u = T.factored ? (g * rf) * f[i] : g * (1.0f / sqrtf(f[i]));
-        a = a + u * u;
+        for (int i = 0; i < 8; i += 2) {
+          float a0 = x[i] - mu, a1 = x[i + 1] - mu;
+          if (GT == KAON_BF16) rbf2(a0, a1);
+          x[i] = a0;
+          x[i + 1] = a1;
+        }
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < cnt) {
+          const float u = T.factored ? (x[i] * rf) * f[i] : x[i] * (1.0f / sqrtf(f[i]));
+          a = a + u * u;
+        }
     }
-    const float s = csum_finish(a, nch, lds4);
-    if (threadIdx.x == 0) ws.rs(T)[r] = s;
-  }
-}
-
-// =============================================================== phase 4
-// One workgroup per tensor: fac = max(sqrt(sum_r rs[r]) / sqrt(n) / clip, 1)
-// (_backend.py:45-47; adakaon.py:1000-1002).
-__global__ __launch_bounds__(KAON_WG) void k_fac(const KaonTensor* __restrict__ D, Ws ws, KaonHyper hp) {
-  __shared__ float lds4[4];
-  const KaonTensor& T = D[blockIdx.x];
-  const int64_t R = T.R;
-  const float* rs = ws.rs(T);
-  const int64_t nch = (R + 7) >> 3;
-  float a = 0.0f;
-  for (int64_t c = threadIdx.x; c < nch; c += KAON_WG)
-    for (int i = 0; i < 8; ++i) {
-      const int64_t j = c * 8 + i;
-      if (j < R) a = a + rs[j];
-    }
-  const float ss = csum_finish(a, nch, lds4);
-  if (threadIdx.x == 0) {
-    const float rmsv = sqrtf(ss) / T.sqrt_n;
-    ws.scal(T)[0] = fmaxf(rmsv / hp.clip, 1.0f);
+    const float s = wave_csum(a);
+    if (wr.lane == 0) ws.rs(T)[r] = s;
   }
 }
 
 // =============================================================== phases 5/6
-// Per-chunk row/block context resolved once when a chunk lies in one row.
-struct RowCtx {
-  float mu, rf;     // GC mean, row factor
-  float oldsc;      // int8 scale before this step (per row)
-  float newsc;      // int8 scale after requant
-  double rnew;      // RN64(1/newsc)
-};
-
-// Momentum chunk load: fp32 values of the OLD momentum given per-element
-// scales (int8: per-row, 4-bit: per-block).
+// Momentum chunk load (raw codes / bits) and store.
 template <int CODEC>
 __device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, uint32_t q[8]) {
   if (CODEC == KAON_MOM_INT8) {
@@ -332,15 +425,17 @@ __device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int 
       for (int i = 0; i < 8; ++i) q[i] = i < cnt ? (uint32_t)(uint8_t)m[i] : 0u;
     }
   } else if (CODEC == KAON_MOM_4BIT) {
-    const uint8_t* m = (const uint8_t*)T.m + (e0 >> 1);
-    if (vec) {
-      const uint32_t v = *(const uint32_t*)m;
+    // nibble of element e = byte e/2, low nibble for even e (any alignment)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = (v >> (4 * i)) & 0xFu;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = i < cnt ? ((uint32_t)m[i >> 1] >> (4 * (i & 1))) & 0xFu : 8u;
+    for (int i = 0; i < 8; ++i) {
+      if (i < cnt) {
+        const int64_t e = e0 + i;
+        q[i] = ((uint32_t)((const uint8_t*)T.m)[e >> 1] >> (4 * (e & 1))) & 0xFu;
+      } else {
+        q[i] = 8u;
+      }
     }
+    (void)vec;
   } else if (CODEC == KAON_MOM_BF16) {
     ld8_bits(T.m, e0, cnt, vec, q);
   } else if (CODEC == KAON_MOM_F32) {
@@ -366,19 +461,27 @@ __device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int 
         if (i < cnt) m[i] = (int8_t)q[i];
     }
   } else if (CODEC == KAON_MOM_4BIT) {
-    uint8_t* m = (uint8_t*)T.m + (e0 >> 1);
-    if (vec) {
+    uint8_t* m = (uint8_t*)T.m;
+    if (vec && (e0 & 7) == 0) {
       uint32_t v = 0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) v |= (q[i] & 0xFu) << (4 * i);
-      *(uint32_t*)m = v;
+      *(uint32_t*)(m + (e0 >> 1)) = v;
     } else {
-      // the chunk owns bytes e0/2 .. (e0+cnt-1)/2 (e0 even); a dangling high
-      // nibble of an odd-length tensor is written as 0 (_pack_nibbles pads 0)
-      for (int b = 0; 2 * b < cnt; ++b) {
-        const uint32_t lo = q[2 * b] & 0xFu;
-        const uint32_t hi = (2 * b + 1 < cnt) ? (q[2 * b + 1] & 0xFu) : 0u;
-        m[b] = (uint8_t)(lo | (hi << 4));
+      // bytes shared with a neighbouring chunk (odd starts) are merged with an
+      // atomic; the byte of an odd-length tensor's last element keeps 0 in its
+      // high nibble (_pack_nibbles pads with 0)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i >= cnt) break;
+        const int64_t e = e0 + i;
+        const int sh = 4 * (int)(e & 1);
+        uint32_t* word = (uint32_t*)(m + ((e >> 1) & ~(int64_t)3));
+        const int bsh = 8 * (int)((e >> 1) & 3) + sh;
+        // the last element of an odd-length tensor owns its whole byte
+        const uint32_t clear = (e + 1 == T.n && (e & 1) == 0) ? 0xFFu : 0xFu;
+        atomicAnd(word, ~(clear << bsh));
+        atomicOr(word, (q[i] & 0xFu) << bsh);
       }
     }
   } else if (CODEC == KAON_MOM_BF16) {
@@ -398,22 +501,32 @@ __device__ __forceinline__ float msam_e(float x, float bound) {
   return fminf(fmaxf(x, -bound), bound);
 }
 
-// Flat items over [row0, row0 + nrows) elements of one tensor (row0/nrows hold
-// the flat start and length).  OPT: KAON_OPT_ADAKAON (also Nekaon) or
-// KAON_OPT_LION.  PHASE 5: keep-count + absmax + old-scale copy.  PHASE 6:
-// write momentum and weights.
-#define KAON_LDS_AMAX 2048
+// int8 dequant q*sc with q the stored byte: (ub - 128)*sc = fma(ub, sc, -128 sc)
+// with ub = byte ^ 0x80, exact because 128*sc is exact (no overflow below 2^120).
+__device__ __forceinline__ float dq_int8(uint32_t byte, float sc, float m128sc, bool fast) {
+  if (fast) return __fmaf_rn((float)((byte ^ 0x80u) & 0xFFu), sc, m128sc);
+  return (float)(int8_t)(uint8_t)byte * sc;
+}
+
+// Per-chunk body of phases 5 and 6.  Row context (mu, rf, scales) is uniform
+// over the chunk when `one_row`; otherwise it is looked up per element.
+struct RowCtx {
+  float mu, rf, oldsc, newsc, m128, m128n;
+  double rnew;
+  bool fast;
+};
 
 template <int OPT, int PHASE, int PT, int GT, int CODEC>
-__global__ __launch_bounds__(KAON_WG) void k_flat(const KaonTensor* __restrict__ D,
+__global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ uint32_t lds_amax[KAON_LDS_AMAX];
-  __shared__ uint32_t lds4[4];
+  __shared__ float fac_s;
+  __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const int64_t C = T.C, n = T.n;
-  const int64_t e_begin = it.row0, e_end = (int64_t)it.row0 + it.nrows;
-  const bool vecT = T.vec_flat != 0;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec_t = T.vec_rows != 0;
   const bool factored = T.factored != 0;
   const bool gc = (hp.flags & KAON_F_GC) && factored;
   const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
@@ -421,328 +534,652 @@ __global__ __launch_bounds__(KAON_WG) void k_flat(const KaonTensor* __restrict__
   const bool mom = (hp.flags & KAON_F_MOMENTUM) != 0 && CODEC != KAON_MOM_NONE;
   const bool nk_remove = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_REMOVE);
   const bool nk_climb = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_CLIMB);
-  const bool quant = mom && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT);
+  constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
+  const bool quant = mom && QUANT;
+  const bool lowp = PT == KAON_BF16;
   const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 1;
   const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
+  const WaveRows wr = wave_rows(it);
 
-  // per-tensor scalars
+  // clip divisor: phase 5 computes it from the row sums (canonical sum over
+  // the rows) and publishes it for phase 6
   float fac = 1.0f;
-  double rfac = 1.0;
   if (OPT == KAON_OPT_ADAKAON) {
-    fac = ws.scal(T)[0];
-    rfac = rcp64(fac);
+    if (PHASE == 5) {
+      if (wr.w == 0) {
+        const int64_t R = T.R;
+        const int64_t nchr = (R + 7) >> 3;
+        const float* rs = ws.rs(T);
+        float a = 0.0f;
+        for (int64_t c = wr.lane; c < nchr; c += 64)
+          for (int i = 0; i < 8; ++i) {
+            const int64_t j = c * 8 + i;
+            if (j < R) a = a + rs[j];
+          }
+        const float ss = wave_csum(a);
+        if (wr.lane == 0) {
+          const float f = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
+          fac_s = f;
+          if (it.row0 == 0) ws.scal(T)[0] = f;
+        }
+      }
+      __syncthreads();
+      fac = fac_s;
+    } else {
+      fac = ws.scal(T)[0];
+    }
   }
+  const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && cautious) {
     const uint32_t cnt = ((const uint32_t*)ws.scal(T))[1];
-    const float den = fmaxf((float)cnt / (float)n, 1e-8f);
-    rden = rcp64(den);
+    rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
-
-  // absmax bookkeeping (phase 5, quantized codecs): entries are rows (int8) or
-  // blocks (4-bit) touched by this item
-  int64_t a_first = 0, a_last = -1;
-  bool use_lds = false;
-  if (PHASE == 5 && quant) {
-    if (CODEC == KAON_MOM_INT8) {
-      a_first = factored ? e_begin / C : 0;
-      a_last = factored ? (e_end - 1) / C : 0;
-    } else {
-      a_first = e_begin / B;
-      a_last = (e_end - 1) / B;
-    }
-    use_lds = (a_last - a_first + 1) <= KAON_LDS_AMAX;
-    if (use_lds)
-      for (int i = threadIdx.x; i < a_last - a_first + 1; i += KAON_WG) lds_amax[i] = 0u;
-    __syncthreads();
-  }
+  // 4-bit fast path: blocks inside rows, a block = G consecutive chunks = G lanes
+  const int64_t G = CODEC == KAON_MOM_4BIT && B >= 8 ? B / 8 : 1;
+  const bool blk_fast = CODEC == KAON_MOM_4BIT && B % 8 == 0 && C % B == 0 && G <= 64 && (64 % G) == 0 && vec_t;
   uint32_t keep = 0;
 
-  for (int64_t e0 = e_begin + 8 * (int64_t)threadIdx.x; e0 < e_end; e0 += 8 * KAON_WG) {
-    const int cnt = (int)min<int64_t>(8, e_end - e0);
-    const bool vec = vecT && cnt == 8;
-    // row / column of the chunk start
-    int64_t r0 = 0, j0 = e0;
-    if (factored) {
-      if (n < 0xFFFFFFFFll) {
-        r0 = (int64_t)((uint32_t)e0 / (uint32_t)C);
-      } else {
-        r0 = e0 / C;
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    // ---- per-row context (wave-uniform)
+    RowCtx rc;
+    rc.mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    rc.rf = (OPT == KAON_OPT_ADAKAON && factored) ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    rc.oldsc = 1.0f;
+    rc.newsc = 1.0f;
+    rc.rnew = 1.0;
+    if (CODEC == KAON_MOM_INT8 && mom) {
+      rc.oldsc = uniform_f(PHASE == 5 ? T.m_scale[r] : ws.roldsc(T)[r]);
+      if (PHASE == 6) {
+        rc.newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+        rc.rnew = rcp64(rc.newsc);
       }
-      j0 = e0 - r0 * C;
     }
-    const bool one_row = !factored || (j0 + cnt <= C);
+    rc.fast = fabsf(rc.oldsc) < 0x1p120f && fabsf(rc.newsc) < 0x1p120f;
+    rc.m128 = -128.0f * rc.oldsc;
+    float row_amax = 0.0f;
 
-    float g[8], p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    ld8<GT>(T.g, e0, cnt, vec, g);
-    const bool need_p = PHASE == 6 || wd;
-    uint32_t pbits[8];
-    if (need_p) {
-      if (PT == KAON_BF16) {
-        ld8_bits(T.p, e0, cnt, vec, pbits);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = bf2f(pbits[i]);
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      const int64_t j0 = c * 8;
+      const int64_t e0 = r * C + j0;
+      const bool vec = vec_t && cnt == 8;
+      // ---- loads
+      float g[8], p[8], f[8];
+      uint32_t mq[8], pb[8];
+      if (cnt > 0) {
+        ld8<GT>(T.g, e0, cnt, vec, g);
       } else {
-        ld8<KAON_F32>(T.p, e0, cnt, vec, p);
-      }
-    }
-    uint32_t mq[8];
-    if (mom) ld_mom_raw<CODEC>(T, e0, cnt, vec, mq);
-    float cf8[8];
-    if (OPT == KAON_OPT_ADAKAON) {
-      if (factored) {
-        if (one_row && vec && (j0 & 7) == 0) {
-          ld8<KAON_F32>(ws.cf(T), j0, 8, true, cf8);
-        } else {
-          int64_t jj = j0;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            cf8[i] = i < cnt ? ws.cf(T)[jj] : 0.0f;
-            if (++jj == C) jj = 0;
-          }
+        for (int i = 0; i < 8; ++i) g[i] = 0.0f;
+      }
+      const bool need_p = PHASE == 6 || wd;
+      if (need_p && cnt > 0) {
+        if (PT == KAON_BF16) {
+          ld8_bits(T.p, e0, cnt, vec, pb);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+        } else {
+          ld8<KAON_F32>(T.p, e0, cnt, vec, p);
         }
       } else {
-        ld8<KAON_F32>(T.v, e0, cnt, vec, cf8);  // holds v for 1-D
-      }
-    }
-    // noise words (phase 6, bf16 weights)
-    uint32_t nz0[8], nz1[8], nz2[8];
-    const bool lowp = PT == KAON_BF16;
-    if (lowp && nk_remove && need_p)
-      noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 0u, e0, T.noise[0], cnt, nz0);
-    if (PHASE == 6 && lowp) {
-      if (hp.bf16_method == KAON_SR)
-        noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], cnt, nz1);
-      if (nk_climb) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 2u, e0, T.noise[2], cnt, nz2);
-    }
-
-    // row context
-    RowCtx rc{0.0f, 0.0f, 1.0f, 1.0f, 1.0};
-    int64_t rcur = -1;
-    int64_t ri = r0, ji = j0;
-    uint32_t qout[8];
-    float dout[8];
-    float mnew[8];
-    float amax_chunk = 0.0f;
-    int64_t amax_idx = -1;  // entry (row/block) the chunk's running max belongs to
-
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i >= cnt) {
+        for (int i = 0; i < 8; ++i) p[i] = 0.0f;
+      }
+      if (mom && cnt > 0) ld_mom_raw<CODEC>(T, e0, cnt, vec, mq);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mq[i] = CODEC == KAON_MOM_4BIT ? 8u : 0u;
+      if (OPT == KAON_OPT_ADAKAON && cnt > 0) {
+        if (factored) ld8<KAON_F32>(ws.cf(T), j0, cnt, vec, f);
+        else ld8<KAON_F32>(T.v, j0, cnt, vec, f);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = 1.0f;
+      }
+      // 4-bit block scales: one block per chunk on the fast path
+      float b_old = 1.0f, b_new = 1.0f;
+      double b_rnew = 1.0;
+      int64_t blk = 0;
+      if (CODEC == KAON_MOM_4BIT && mom && blk_fast) {
+        blk = e0 / B;
+        if (cnt > 0) {
+          b_old = PHASE == 5 ? T.m_scale[blk] : ws.boldsc(T, nb)[blk];
+          if (PHASE == 6) {
+            b_new = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+            b_rnew = rcp64(b_new);
+          }
+        }
+      }
+      // ---- noise (phase 6, bf16 weights)
+      uint32_t nz0[8], nz1[8], nz2[8];
+      if (lowp && cnt > 0) {
+        const bool aligned = (e0 & 7) == 0;
+        if (nk_remove && need_p) {
+          if (aligned) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 0u, e0, T.noise[0], cnt, nz0);
+          else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nz0[i] = i < cnt ? noise1(hp.seed, hp.step, T.tensor_id, 0u, e0 + i, T.noise[0]) : 0u;
+        }
+        if (PHASE == 6 && hp.bf16_method == KAON_SR) {
+          if (aligned) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], cnt, nz1);
+          else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nz1[i] = i < cnt ? noise1(hp.seed, hp.step, T.tensor_id, 1u, e0 + i, T.noise[1]) : 0u;
+        }
+        if (PHASE == 6 && nk_climb) {
+          if (aligned) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 2u, e0, T.noise[2], cnt, nz2);
+          else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nz2[i] = i < cnt ? noise1(hp.seed, hp.step, T.tensor_id, 2u, e0 + i, T.noise[2]) : 0u;
+        }
+      }
+      // ---- gradient as the step sees it (GC in the grad dtype)
+      if (gc) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          float a0 = g[i] - rc.mu, a1 = g[i + 1] - rc.mu;
+          if (GT == KAON_BF16) rbf2(a0, a1);
+          g[i] = a0;
+          g[i + 1] = a1;
+        }
+      }
+      // ---- per element
+      uint32_t qout[8];
+      float dout[8], mnew[8];
+      float chunk_amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
         qout[i] = mq[i];
         dout[i] = 0.0f;
         mnew[i] = 0.0f;
-        continue;
-      }
-      const int64_t e = e0 + i;
-      if (factored && ri != rcur) {
-        rcur = ri;
-        rc.mu = gc ? ws.mu(T)[ri] : 0.0f;
-        if (OPT == KAON_OPT_ADAKAON) rc.rf = ws.rf(T)[ri];
-        if (CODEC == KAON_MOM_INT8 && mom) {
-          rc.oldsc = PHASE == 5 ? T.m_scale[ri] : ws.roldsc(T)[ri];
+        if (i >= cnt) continue;
+        const int64_t e = e0 + i;
+        float sc4_old = b_old, sc4_new = b_new;
+        double r4 = b_rnew;
+        int64_t blk_e = blk;
+        if (CODEC == KAON_MOM_4BIT && mom && !blk_fast) {
+          blk_e = e / B;
+          sc4_old = PHASE == 5 ? T.m_scale[blk_e] : ws.boldsc(T, nb)[blk_e];
           if (PHASE == 6) {
-            const float am = __uint_as_float(ws.ramax(T)[ri]);
-            rc.newsc = fmaxf(am, 1e-12f) / 127.0f;
-            rc.rnew = rcp64(rc.newsc);
+            sc4_new = fmaxf(__uint_as_float(ws.bamax(T)[blk_e]), 1e-12f) / 7.0f;
+            r4 = rcp64(sc4_new);
           }
         }
-      } else if (!factored && rcur < 0) {
-        rcur = 0;
-        if (CODEC == KAON_MOM_INT8 && mom) {
-          rc.oldsc = PHASE == 5 ? T.m_scale[0] : ws.roldsc(T)[0];
-          if (PHASE == 6) {
-            const float am = __uint_as_float(ws.ramax(T)[0]);
-            rc.newsc = fmaxf(am, 1e-12f) / 127.0f;
-            rc.rnew = rcp64(rc.newsc);
-          }
-        }
-      }
-      // 4-bit block scale context (per element; blocks need not align to chunks)
-      float b_oldsc = 1.0f, b_newsc = 1.0f;
-      double b_rnew = 1.0;
-      int64_t blk = 0;
-      if (CODEC == KAON_MOM_4BIT && mom) {
-        blk = e / B;
-        b_oldsc = PHASE == 5 ? T.m_scale[blk] : ws.boldsc(T, nb)[blk];
-        if (PHASE == 6) {
-          const float am = __uint_as_float(ws.bamax(T)[blk]);
-          b_newsc = fmaxf(am, 1e-12f) / 7.0f;
-          b_rnew = rcp64(b_newsc);
-        }
-      }
-
-      // gradient as the step sees it (GC in the grad dtype)
-      float gv = g[i];
-      if (gc) gv = round_to<GT>(gv - rc.mu);
-
-      float d;       // delta (pre-cautious)
-      float mfv = 0; // new momentum value (fp32, pre-requant)
-      float mold = 0.0f;
-      if (mom) {
-        if (CODEC == KAON_MOM_INT8) mold = (float)(int8_t)(uint8_t)mq[i] * rc.oldsc;
-        else if (CODEC == KAON_MOM_4BIT) mold = ((float)mq[i] - 8.0f) * b_oldsc;
-        else if (CODEC == KAON_MOM_BF16) mold = bf2f(mq[i]);
-        else if (CODEC == KAON_MOM_F32) mold = __uint_as_float(mq[i]);
-      }
-      float pw = p[i];  // weight the inner step sees (after Nekaon removal)
-      if (nk_remove && need_p) {
-        const float ev = msam_e(mold * hp.nk_k, hp.nk_bound_old);
-        if (lowp) pw = bf2f(sr_bf16(p[i] + ev, nz0[i]));
-        else pw = p[i] + ev;
-      }
-
-      if (OPT == KAON_OPT_ADAKAON) {
-        const float u = factored ? (gv * rc.rf) * cf8[i] : gv * (1.0f / sqrtf(cf8[i]));
-        const float ud = (fac == 1.0f ? u : div_r64(u, rfac)) * hp.lr;
+        float mold = 0.0f;
         if (mom) {
-          if (CODEC == KAON_MOM_BF16) {
-            const uint32_t mb = f2bf(klerp(mold, rbf(ud), hp.w1));
-            qout[i] = mb;
-            d = bf2f(mb);
+          if (CODEC == KAON_MOM_INT8) mold = dq_int8(mq[i], rc.oldsc, rc.m128, rc.fast);
+          else if (CODEC == KAON_MOM_4BIT) mold = ((float)mq[i] - 8.0f) * sc4_old;
+          else if (CODEC == KAON_MOM_BF16) mold = bf2f(mq[i]);
+          else if (CODEC == KAON_MOM_F32) mold = __uint_as_float(mq[i]);
+        }
+        float pw = p[i];  // weight the inner step sees (after the Nekaon removal)
+        if (nk_remove && need_p) {
+          const float ev = msam_e(mold * hp.nk_k, hp.nk_bound_old);
+          pw = lowp ? bf2f(sr_bf16(p[i] + ev, nz0[i])) : p[i] + ev;
+        }
+        float d, mfv = 0.0f;
+        const float gv = g[i];
+        if (OPT == KAON_OPT_ADAKAON) {
+          const float u = factored ? (gv * rc.rf) * f[i] : gv * (1.0f / sqrtf(f[i]));
+          const float ud = (fac == 1.0f ? u : div_r64(u, rfac)) * hp.lr;
+          if (mom) {
+            if (CODEC == KAON_MOM_BF16) {
+              const uint32_t mb = f2bf(klerp(mold, rbf(ud), hp.w1));
+              qout[i] = mb;
+              d = bf2f(mb);
+            } else {
+              mfv = klerp(mold, ud, hp.w1);
+              d = mfv;
+              if (CODEC == KAON_MOM_F32) qout[i] = __float_as_uint(mfv);
+            }
           } else {
-            mfv = klerp(mold, ud, hp.w1);
-            d = mfv;
-            if (CODEC == KAON_MOM_F32) qout[i] = __float_as_uint(mfv);
+            d = ud;
+          }
+          if (wd) d = __fmaf_rn(hp.wdl, pw, d);
+        } else {  // Lion
+          const float cdir = __fmaf_rn(hp.a1, gv, mold * hp.b1);
+          d = ksign(cdir);
+          mfv = __fmaf_rn(hp.a2, gv, mold * hp.b2);
+          if (CODEC == KAON_MOM_F32) qout[i] = __float_as_uint(mfv);
+          else if (CODEC == KAON_MOM_BF16) qout[i] = f2bf(mfv);
+          if (wd) d = __fmaf_rn(hp.wdl, pw, d);
+        }
+        const bool kp = d * gv > 0.0f;
+        if (PHASE == 5) {
+          keep += kp ? 1u : 0u;
+          if (quant) {
+            const float ax = fabsf(mfv);
+            if (CODEC == KAON_MOM_4BIT && !blk_fast) {
+              if (ax == ax) atomicMax(&ws.bamax(T)[blk_e], __float_as_uint(ax));
+              if (e == blk_e * B) ws.boldsc(T, nb)[blk_e] = sc4_old;
+            } else {
+              chunk_amax = fmaxf(chunk_amax, ax);
+            }
           }
         } else {
-          d = ud;
+          float mdeq = 0.0f;
+          if (quant) {
+            if (CODEC == KAON_MOM_INT8) {
+              float x = rintf(div_r64(mfv, rc.rnew));
+              x = fminf(fmaxf(x, -127.0f), 127.0f);
+              qout[i] = (uint32_t)(uint8_t)(int8_t)x;
+              mdeq = x * rc.newsc;
+            } else {
+              float x = rintf(div_r64(mfv, r4));
+              x = fminf(fmaxf(x, -7.0f), 7.0f);
+              qout[i] = (uint32_t)((int)x + 8);
+              mdeq = x * sc4_new;
+              if (!blk_fast && e == blk_e * B) T.m_scale[blk_e] = sc4_new;
+            }
+          } else if (mom) {
+            mdeq = CODEC == KAON_MOM_BF16 ? bf2f(qout[i]) : __uint_as_float(qout[i]);
+          }
+          mnew[i] = mdeq;
+          float dd = d;
+          if (cautious) dd = div_r64(d * (kp ? 1.0f : 0.0f), rden);
+          if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
+          dout[i] = dd;
+          p[i] = pw;
         }
-        if (wd) d = __fmaf_rn(hp.wdl, pw, d);
-      } else {  // Lion
-        const float cdir = __fmaf_rn(hp.a1, gv, mold * hp.b1);
-        d = ksign(cdir);
-        mfv = __fmaf_rn(hp.a2, gv, mold * hp.b2);
-        if (CODEC == KAON_MOM_F32) qout[i] = __float_as_uint(mfv);
-        else if (CODEC == KAON_MOM_BF16) qout[i] = f2bf(mfv);
-        if (wd) d = __fmaf_rn(hp.wdl, pw, d);
       }
-      const bool kp = d * gv > 0.0f;
 
       if (PHASE == 5) {
-        keep += kp ? 1u : 0u;
-        if (quant) {
-          const int64_t idx = CODEC == KAON_MOM_INT8 ? (factored ? ri : 0) : blk;
-          const float ax = fabsf(mfv);
-          if (idx != amax_idx) {
-            if (amax_idx >= 0) {
-              if (use_lds) atomicMax(&lds_amax[amax_idx - a_first], __float_as_uint(amax_chunk));
-              else atomicMax(CODEC == KAON_MOM_INT8 ? &ws.ramax(T)[amax_idx] : &ws.bamax(T)[amax_idx],
-                             __float_as_uint(amax_chunk));
-            }
-            amax_idx = idx;
-            amax_chunk = 0.0f;
-          }
-          amax_chunk = fmaxf(amax_chunk, ax);
-          // the element that starts a row/block copies its old scale
+        if (quant && !(CODEC == KAON_MOM_4BIT && !blk_fast)) {
           if (CODEC == KAON_MOM_INT8) {
-            if ((factored ? ji : e) == 0) ws.roldsc(T)[factored ? ri : 0] = rc.oldsc;
-          } else if (e == blk * B) {
-            ws.boldsc(T, nb)[blk] = b_oldsc;
-          }
-        }
-      } else {
-        // requant (_quant_int8 / _quant_4bit)
-        float mdeq = 0.0f;
-        if (quant) {
-          if (CODEC == KAON_MOM_INT8) {
-            float x = rintf(div_r64(mfv, rc.rnew));
-            x = fminf(fmaxf(x, -127.0f), 127.0f);
-            qout[i] = (uint32_t)(uint8_t)(int8_t)x;
-            mdeq = x * rc.newsc;
-            if ((factored ? ji : e) == 0) T.m_scale[factored ? ri : 0] = rc.newsc;
+            row_amax = fmaxf(row_amax, chunk_amax);
           } else {
-            float x = rintf(div_r64(mfv, b_rnew));
-            x = fminf(fmaxf(x, -7.0f), 7.0f);
-            qout[i] = (uint32_t)((int)x + 8);
-            mdeq = x * b_newsc;
-            if (e == blk * B) T.m_scale[blk] = b_newsc;
+            // blocks of G lanes: reduce within the lane group, its first lane stores
+            float a = chunk_amax;
+            for (int o = (int)G / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+            if (cnt > 0 && (wr.lane % G) == 0) {
+              ws.bamax(T)[blk] = __float_as_uint(a);
+              ws.boldsc(T, nb)[blk] = b_old;
+            }
           }
-        } else if (mom) {
-          mdeq = CODEC == KAON_MOM_BF16 ? bf2f(qout[i]) : __uint_as_float(qout[i]);
         }
-        mnew[i] = mdeq;
-        float dd = d;
-        if (cautious) dd = div_r64(d * (kp ? 1.0f : 0.0f), rden);
-        if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
-        dout[i] = dd;
-        p[i] = pw;
+        continue;
       }
-      // advance row/column of the next element
-      if (factored && ++ji == C) {
-        ji = 0;
-        ++ri;
-      }
-    }
-
-    if (PHASE == 5) {
-      if (quant && amax_idx >= 0) {
-        if (use_lds) atomicMax(&lds_amax[amax_idx - a_first], __float_as_uint(amax_chunk));
-        else atomicMax(CODEC == KAON_MOM_INT8 ? &ws.ramax(T)[amax_idx] : &ws.bamax(T)[amax_idx],
-                       __float_as_uint(amax_chunk));
-      }
-      continue;
-    }
-
-    // ---------------- phase 6 writes
-    if (mom) st_mom_raw<CODEC>(T, e0, cnt, vec, qout);
-    if (PT == KAON_F32) {
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float x = p[i] - dout[i];
-        if (nk_climb) x = x + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new);
-        o[i] = x;
-      }
-      st8_f32(T.p, e0, cnt, vec, o);
-    } else {
-      uint32_t o[8];
-      if (hp.bf16_method == KAON_KAHAN) {
-        uint32_t sh[8];
-        ld8_bits(T.shift, e0, cnt, vec, sh);
+      if (cnt <= 0) continue;
+      // ---------------- phase 6 writes
+      if (CODEC == KAON_MOM_4BIT && mom && blk_fast && (wr.lane % G) == 0) T.m_scale[blk] = b_new;
+      if (mom) st_mom_raw<CODEC>(T, e0, cnt, vec, qout);
+      if (PT == KAON_F32) {
+        float o[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          // shift -= bf16(delta); p0 = p; p += shift; shift += p0 - p  (_backend.py:90-94)
-          const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
-          const float p0 = p[i];
-          const float p1 = rbf(p0 + s);
-          o[i] = f2bf(p1);
-          sh[i] = f2bf(s + rbf(p0 - p1));
+          float x = p[i] - dout[i];
+          if (nk_climb) x = x + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new);
+          o[i] = x;
         }
-        st8_bits(T.shift, e0, cnt, vec, sh);
-      } else if (hp.bf16_method == KAON_RN) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+        st8_f32(T.p, e0, cnt, vec, o);
       } else {
+        uint32_t o[8];
+        if (hp.bf16_method == KAON_KAHAN) {
+          uint32_t sh[8];
+          ld8_bits(T.shift, e0, cnt, vec, sh);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz1[i]);
-      }
-      if (nk_climb) {
+          for (int i = 0; i < 8; ++i) {
+            // shift -= bf16(delta); p0 = p; p += shift; shift += p0 - p  (_backend.py:90-94)
+            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            const float p0 = p[i];
+            const float p1 = rbf(p0 + s);
+            o[i] = f2bf(p1);
+            sh[i] = f2bf(s + rbf(p0 - p1));
+          }
+          st8_bits(T.shift, e0, cnt, vec, sh);
+        } else if (hp.bf16_method == KAON_RN) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          o[i] = sr_bf16(bf2f(o[i]) + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz1[i]);
+        }
+        if (nk_climb) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            o[i] = sr_bf16(bf2f(o[i]) + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+        }
+        st8_bits(T.p, e0, cnt, vec, o);
       }
-      st8_bits(T.p, e0, cnt, vec, o);
+    }
+    // ---- end of row
+    if (CODEC == KAON_MOM_INT8 && quant) {
+      if (PHASE == 5) {
+        const float am = wave_max(row_amax);
+        if (wr.lane == 0) {
+          ws.ramax(T)[r] = __float_as_uint(am);
+          ws.roldsc(T)[r] = rc.oldsc;
+        }
+      } else if (wr.lane == 0) {
+        T.m_scale[r] = rc.newsc;
+      }
     }
   }
 
-  if (PHASE == 5) {
-    if (cautious) {
-      const uint32_t tot = wg_sum_u32(keep, lds4);
-      if (threadIdx.x == 0 && tot) atomicAdd(&((uint32_t*)ws.scal(T))[1], tot);
+  if (PHASE == 5 && cautious) {
+    const uint32_t wsum = wave_sum_u32(keep);
+    if (wr.lane == 0) keep_s[wr.w] = wsum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
+      if (tot) atomicAdd(&((uint32_t*)ws.scal(T))[1], tot);
     }
-    if (quant && use_lds) {
-      __syncthreads();
-      for (int64_t a = a_first + threadIdx.x; a <= a_last; a += KAON_WG) {
-        const uint32_t v = lds_amax[a - a_first];
-        bool inside;
-        if (CODEC == KAON_MOM_INT8) inside = !factored ? (e_begin == 0 && e_end == n)
-                                                       : (a * C >= e_begin && (a + 1) * C <= e_end);
-        else inside = a * B >= e_begin && min((a + 1) * B, n) <= e_end;
-        uint32_t* dst = CODEC == KAON_MOM_INT8 ? &ws.ramax(T)[a] : &ws.bamax(T)[a];
-        if (inside) *dst = v;
-        else atomicMax(dst, v);
+  }
+}
+
+// =============================================================== fast path
+// Phases 5 and 6 specialized at compile time for bf16 params and grads,
+// stochastic-rounding writes and 16-byte-aligned rows: every full 8-element
+// chunk runs straight-line code; only a row's partial last chunk takes the
+// generic per-element route.  FLAGS: bit 0 GC, 1 cautious, 2 weight decay,
+// 3 Nekaon removal, 4 Nekaon climb.
+enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16 };
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4 v, float o[8]) {
+  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xFFFF0000u);
+  o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+// int8 requant code (as the stored byte) of mf with r = RN64(1/scale)
+__device__ __forceinline__ uint32_t q_int8(float mf, double r, float& xq) {
+  float x = rintf(div_r64(mf, r));
+  x = fminf(fmaxf(x, -127.0f), 127.0f);
+  xq = x;
+  return (uint32_t)(int)x & 0xFFu;
+}
+
+// FAC1: clip divisor 1 (skip the exact division).  DQX: int8 dequant as
+// q*scale for rows whose old scale is too large for the fma form.
+template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX>
+__device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, int64_t r,
+                                           int64_t e0, int64_t j0, float mu, float rf, float oldsc, float m128,
+                                           float newsc, double rnew, double rfac, double rden, int64_t B,
+                                           int64_t nb, int G, int lane, uint32_t& keep, float& amax,
+                                           const float* cfrow) {
+  constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
+  constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
+  constexpr bool MOM = CODEC != KAON_MOM_NONE;
+  constexpr bool NEEDP = PHASE == 6 || WD;
+  const uint4 gv4 = *(const uint4*)((const uint16_t*)T.g + e0);
+  uint4 pv4 = make_uint4(0, 0, 0, 0);
+  if (NEEDP) pv4 = *(const uint4*)((const uint16_t*)T.p + e0);
+  uint2 mi8 = make_uint2(0, 0);
+  uint32_t m4 = 0;
+  uint4 mb16 = make_uint4(0, 0, 0, 0);
+  if (CODEC == KAON_MOM_INT8) mi8 = *(const uint2*)((const int8_t*)T.m + e0);
+  if (CODEC == KAON_MOM_4BIT) m4 = *(const uint32_t*)((const uint8_t*)T.m + (e0 >> 1));
+  if (CODEC == KAON_MOM_BF16) mb16 = *(const uint4*)((const uint16_t*)T.m + e0);
+  float f[8];
+  if (OPT == KAON_OPT_ADAKAON) {
+    const float* cfp = cfrow + j0;
+    const float4 c0 = *(const float4*)cfp, c1 = *(const float4*)(cfp + 4);
+    f[0] = c0.x; f[1] = c0.y; f[2] = c0.z; f[3] = c0.w; f[4] = c1.x; f[5] = c1.y; f[6] = c1.z; f[7] = c1.w;
+  }
+  // 4-bit: one block per chunk
+  float b_old = 1.0f, b_new = 1.0f;
+  double b_r = 1.0;
+  int64_t blk = 0;
+  if (CODEC == KAON_MOM_4BIT) {
+    blk = e0 / B;
+    b_old = PHASE == 5 ? T.m_scale[blk] : ws.boldsc(T, nb)[blk];
+    if (PHASE == 6) {
+      b_new = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+      b_r = rcp64(b_new);
+    }
+  }
+  float g[8], p[8];
+  unpack_bf16x8(gv4, g);
+  if (NEEDP) unpack_bf16x8(pv4, p);
+  if (GC) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      float a0 = g[i] - mu, a1 = g[i + 1] - mu;
+      rbf2(a0, a1);
+      g[i] = a0;
+      g[i + 1] = a1;
+    }
+  }
+  uint32_t nz0[8], nz1[8], nz2[8];
+  if (NKR && NEEDP) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 0u, e0, T.noise[0], 8, nz0);
+  if (PHASE == 6) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], 8, nz1);
+  if (PHASE == 6 && NKC) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 2u, e0, T.noise[2], 8, nz2);
+
+  float mold[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (CODEC == KAON_MOM_INT8) {
+      const uint32_t w = i < 4 ? mi8.x : mi8.y;
+      if (DQX)
+        mold[i] = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * oldsc;
+      else
+        mold[i] = __fmaf_rn((float)(((w ^ 0x80808080u) >> (8 * (i & 3))) & 0xFFu), oldsc, m128);
+    } else if (CODEC == KAON_MOM_4BIT) {
+      mold[i] = ((float)((m4 >> (4 * i)) & 0xFu) - 8.0f) * b_old;
+    } else if (CODEC == KAON_MOM_BF16) {
+      const uint32_t mw[4] = {mb16.x, mb16.y, mb16.z, mb16.w};
+      const uint32_t w = mw[i >> 1];
+      mold[i] = (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
+    } else {
+      mold[i] = 0.0f;
+    }
+  }
+  float d[8], mf[8];
+  uint32_t mbits[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float pw = p[i];
+    if (NKR && NEEDP) pw = bf2f(sr_bf16(p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old), nz0[i]));
+    p[i] = pw;
+    if (OPT == KAON_OPT_ADAKAON) {
+      const float u = (g[i] * rf) * f[i];
+      const float ud = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
+      if (CODEC == KAON_MOM_BF16) {
+        const uint32_t mb = f2bf(klerp(mold[i], rbf(ud), hp.w1));
+        mbits[i] = mb;
+        mf[i] = bf2f(mb);
+        d[i] = mf[i];
+      } else if (MOM) {
+        mf[i] = klerp(mold[i], ud, hp.w1);
+        d[i] = mf[i];
+      } else {
+        mf[i] = 0.0f;
+        d[i] = ud;
       }
+    } else {
+      d[i] = ksign(__fmaf_rn(hp.a1, g[i], mold[i] * hp.b1));
+      mf[i] = __fmaf_rn(hp.a2, g[i], mold[i] * hp.b2);
+      if (CODEC == KAON_MOM_BF16) mbits[i] = f2bf(mf[i]);
+    }
+    if (WD) d[i] = __fmaf_rn(hp.wdl, pw, d[i]);
+  }
+  if (PHASE == 5) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (CAUT) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
+      if (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) amax = fmaxf(amax, fabsf(mf[i]));
+    }
+    return;
+  }
+  // ---- phase 6: requant, cautious, SR write (+ Nekaon climb)
+  float mdq[8];
+  uint32_t codes[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (CODEC == KAON_MOM_INT8) {
+      float xq;
+      codes[i] = q_int8(mf[i], rnew, xq);
+      mdq[i] = xq * newsc;
+    } else if (CODEC == KAON_MOM_4BIT) {
+      float x = rintf(div_r64(mf[i], b_r));
+      x = fminf(fmaxf(x, -7.0f), 7.0f);
+      codes[i] = (uint32_t)((int)x + 8);
+      mdq[i] = x * b_new;
+    } else if (CODEC == KAON_MOM_BF16) {
+      mdq[i] = mf[i];
+    } else {
+      mdq[i] = 0.0f;
+    }
+  }
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float dd = d[i];
+    if (CAUT) dd = div_r64(d[i] * (d[i] * g[i] > 0.0f ? 1.0f : 0.0f), rden);
+    if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
+    o[i] = sr_bf16(p[i] - dd, nz1[i]);
+    if (NKC) o[i] = sr_bf16(bf2f(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+  }
+  uint4 ov;
+  ov.x = o[0] | (o[1] << 16);
+  ov.y = o[2] | (o[3] << 16);
+  ov.z = o[4] | (o[5] << 16);
+  ov.w = o[6] | (o[7] << 16);
+  *(uint4*)((uint16_t*)T.p + e0) = ov;
+  if (CODEC == KAON_MOM_INT8) {
+    uint2 mv;
+    mv.x = codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
+    mv.y = codes[4] | (codes[5] << 8) | (codes[6] << 16) | (codes[7] << 24);
+    *(uint2*)((int8_t*)T.m + e0) = mv;
+  } else if (CODEC == KAON_MOM_4BIT) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
+    *(uint32_t*)((uint8_t*)T.m + (e0 >> 1)) = v;
+    if ((lane % G) == 0) T.m_scale[blk] = b_new;
+  } else if (CODEC == KAON_MOM_BF16) {
+    uint4 mv;
+    mv.x = mbits[0] | (mbits[1] << 16);
+    mv.y = mbits[2] | (mbits[3] << 16);
+    mv.z = mbits[4] | (mbits[5] << 16);
+    mv.w = mbits[6] | (mbits[7] << 16);
+    *(uint4*)((uint16_t*)T.m + e0) = mv;
+  }
+}
+
+// Fast slices (the planner's fast_eligible tensors): factored, bf16 params and
+// grads, stochastic rounding, 16-byte aligned rows with C % 8 == 0 and, for
+// 4-bit, blocks of 8*G elements with G | 64 that tile the rows.
+template <int OPT, int PHASE, int CODEC, int FLAGS>
+__global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__ D,
+                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  constexpr bool CAUT = FLAGS & FF_CAUT;
+  constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
+  __shared__ float fac_s;
+  __shared__ uint32_t keep_s[4];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C, n = T.n;
+  const int64_t nfull = C >> 3;  // full chunks per row
+  const int cplf = (int)((nfull + 63) >> 6);
+  const WaveRows wr = wave_rows(it);
+  const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 8;
+  const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
+  const int G = CODEC == KAON_MOM_4BIT ? (int)(B / 8) : 1;
+
+  float fac = 1.0f;
+  if (OPT == KAON_OPT_ADAKAON) {
+    if (PHASE == 5) {
+      if (wr.w == 0) {
+        const int64_t R = T.R;
+        const int64_t nchr = (R + 7) >> 3;
+        const float* rs = ws.rs(T);
+        float a = 0.0f;
+        for (int64_t c = wr.lane; c < nchr; c += 64)
+          for (int i = 0; i < 8; ++i) {
+            const int64_t j = c * 8 + i;
+            if (j < R) a = a + rs[j];
+          }
+        const float ss = wave_csum(a);
+        if (wr.lane == 0) {
+          const float fv = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
+          fac_s = fv;
+          if (it.row0 == 0) ws.scal(T)[0] = fv;
+        }
+      }
+      __syncthreads();
+      fac = fac_s;
+    } else {
+      fac = ws.scal(T)[0];
+    }
+  }
+  const double rfac = rcp64(fac);
+  double rden = 1.0;
+  if (PHASE == 6 && CAUT) {
+    const uint32_t cnt = ((const uint32_t*)ws.scal(T))[1];
+    rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
+  }
+  const float* cfrow = ws.cf(T);
+  uint32_t keep = 0;
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float mu = (FLAGS & FF_GC) ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    const float rf = OPT == KAON_OPT_ADAKAON ? uniform_f(ws.rf(T)[r]) : 1.0f;
+    float oldsc = 1.0f, newsc = 1.0f;
+    double rnew = 1.0;
+    if (CODEC == KAON_MOM_INT8) {
+      oldsc = uniform_f(PHASE == 5 ? T.m_scale[r] : ws.roldsc(T)[r]);
+      if (PHASE == 6) {
+        newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+        rnew = rcp64(newsc);
+      }
+    }
+    const float m128 = -128.0f * oldsc;
+    // fma(ub, sc, -128 sc) is the exact product q*sc while 128*sc is finite
+    const bool dqf = CODEC != KAON_MOM_INT8 || fabsf(oldsc) < 0x1p120f;
+    float amax = 0.0f;
+    for (int k = 0; k < cplf; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const bool full = c < nfull;
+      float camax = 0.0f;
+      if (full) {
+        const int64_t j0 = c * 8;
+        const int64_t e0 = r * C + j0;
+        if (fac == 1.0f && dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
+                                                            rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+        else if (dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
+                                                             rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+        else
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
+                                                            rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+      }
+      if (PHASE == 5 && QUANT) {
+        if (CODEC == KAON_MOM_INT8) {
+          amax = fmaxf(amax, camax);
+        } else {
+          float a = camax;
+          for (int o = G / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+          if (full && (wr.lane % G) == 0) {
+            const int64_t blk = (r * C + c * 8) / B;
+            ws.bamax(T)[blk] = __float_as_uint(a);
+            ws.boldsc(T, nb)[blk] = T.m_scale[blk];
+          }
+        }
+      }
+    }
+    if (CODEC == KAON_MOM_INT8) {
+      if (PHASE == 5) {
+        const float am = wave_max(amax);
+        if (wr.lane == 0) {
+          ws.ramax(T)[r] = __float_as_uint(am);
+          ws.roldsc(T)[r] = oldsc;
+        }
+      } else if (wr.lane == 0) {
+        T.m_scale[r] = newsc;
+      }
+    }
+  }
+  if (PHASE == 5 && CAUT) {
+    const uint32_t wsum = wave_sum_u32(keep);
+    if (wr.lane == 0) keep_s[wr.w] = wsum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
+      if (tot) atomicAdd(&((uint32_t*)ws.scal(T))[1], tot);
     }
   }
 }
@@ -886,41 +1323,113 @@ __global__ __launch_bounds__(KAON_WG) void k_copy(const uint4* __restrict__ src,
 }
 
 // ------------------------------------------------------------ dispatch tables
-using FlatFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
+using ElemFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
 
 template <int OPT, int PHASE, int PT, int GT>
-FlatFn flat_by_codec(int codec) {
+ElemFn elem_by_codec(int codec) {
   switch (codec) {
-    case KAON_MOM_NONE: return k_flat<OPT, PHASE, PT, GT, KAON_MOM_NONE>;
-    case KAON_MOM_F32: return k_flat<OPT, PHASE, PT, GT, KAON_MOM_F32>;
-    case KAON_MOM_BF16: return k_flat<OPT, PHASE, PT, GT, KAON_MOM_BF16>;
-    case KAON_MOM_INT8: return k_flat<OPT, PHASE, PT, GT, KAON_MOM_INT8>;
-    case KAON_MOM_4BIT: return k_flat<OPT, PHASE, PT, GT, KAON_MOM_4BIT>;
+    case KAON_MOM_NONE: return k_elem<OPT, PHASE, PT, GT, KAON_MOM_NONE>;
+    case KAON_MOM_F32: return k_elem<OPT, PHASE, PT, GT, KAON_MOM_F32>;
+    case KAON_MOM_BF16: return k_elem<OPT, PHASE, PT, GT, KAON_MOM_BF16>;
+    case KAON_MOM_INT8: return k_elem<OPT, PHASE, PT, GT, KAON_MOM_INT8>;
+    case KAON_MOM_4BIT: return k_elem<OPT, PHASE, PT, GT, KAON_MOM_4BIT>;
   }
   return nullptr;
 }
 
 template <int OPT, int PHASE>
-FlatFn flat_fn(int pt, int gt, int codec) {
-  if (pt == KAON_BF16 && gt == KAON_BF16) return flat_by_codec<OPT, PHASE, KAON_BF16, KAON_BF16>(codec);
-  if (pt == KAON_BF16 && gt == KAON_F32) return flat_by_codec<OPT, PHASE, KAON_BF16, KAON_F32>(codec);
-  if (pt == KAON_F32 && gt == KAON_BF16) return flat_by_codec<OPT, PHASE, KAON_F32, KAON_BF16>(codec);
-  if (pt == KAON_F32 && gt == KAON_F32) return flat_by_codec<OPT, PHASE, KAON_F32, KAON_F32>(codec);
+ElemFn elem_fn(int pt, int gt, int codec) {
+  if (pt == KAON_BF16 && gt == KAON_BF16) return elem_by_codec<OPT, PHASE, KAON_BF16, KAON_BF16>(codec);
+  if (pt == KAON_BF16 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_BF16, KAON_F32>(codec);
+  if (pt == KAON_F32 && gt == KAON_BF16) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_BF16>(codec);
+  if (pt == KAON_F32 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_F32>(codec);
   return nullptr;
 }
 
-using RowsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int);
-template <int GT>
-RowsFn rows_fn_gt(int km) {
-  switch (km) {
-    case 1: return k_rows<GT, 1>;
-    case 2: return k_rows<GT, 2>;
-    case 4: return k_rows<GT, 4>;
-    case 8: return k_rows<GT, 8>;
+// specialized kernels available: (opt, codec, flags) with flags among the
+// defaults of the reference optimizers (GC and cautious on, WD on or off;
+// Nekaon: the climb, plus the removal after the first step, WD on or off)
+template <int OPT, int PHASE, int CODEC>
+ElemFn fast_by_flags(int ff) {
+  switch (ff) {
+    case FF_GC | FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT>;
+    case FF_GC | FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD>;
+  }
+  if (OPT == KAON_OPT_ADAKAON && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT)) {
+    switch (ff) {
+      case FF_GC | FF_CAUT | FF_NKC:
+        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC>;
+      case FF_GC | FF_CAUT | FF_NKC | FF_NKR:
+        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC | FF_NKR>;
+      case FF_GC | FF_CAUT | FF_WD | FF_NKC:
+        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC>;
+      case FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR:
+        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR>;
+    }
   }
   return nullptr;
 }
-RowsFn rows_fn(int gt, int km) { return gt == KAON_BF16 ? rows_fn_gt<KAON_BF16>(km) : rows_fn_gt<KAON_F32>(km); }
+
+template <int OPT, int PHASE>
+ElemFn fast_fn(int codec, int ff) {
+  switch (codec) {
+    case KAON_MOM_NONE: return OPT == KAON_OPT_ADAKAON ? fast_by_flags<OPT, PHASE, KAON_MOM_NONE>(ff) : nullptr;
+    case KAON_MOM_BF16: return fast_by_flags<OPT, PHASE, KAON_MOM_BF16>(ff);
+    case KAON_MOM_INT8: return fast_by_flags<OPT, PHASE, KAON_MOM_INT8>(ff);
+    case KAON_MOM_4BIT: return fast_by_flags<OPT, PHASE, KAON_MOM_4BIT>(ff);
+  }
+  return nullptr;
+}
+
+int fast_flags(const KaonHyper& h) {
+  int ff = 0;
+  if (h.flags & KAON_F_GC) ff |= FF_GC;
+  if (h.flags & KAON_F_CAUTIOUS) ff |= FF_CAUT;
+  if (h.flags & KAON_F_WD) ff |= FF_WD;
+  if (h.flags & KAON_F_NK_REMOVE) ff |= FF_NKR;
+  if (h.flags & KAON_F_NK_CLIMB) ff |= FF_NKC;
+  return ff;
+}
+
+// Phase 5 or 6 over the slices: the specialized kernel over elem_items[0,
+// n_fast) when one exists for the configuration, the generic one over the rest.
+template <int OPT, int PHASE>
+int launch_elem(const KaonLaunch& L, Ws ws, const KaonHyper& h, int codec, hipStream_t st) {
+  int32_t n_fast = L.n_fast;
+  ElemFn ff = nullptr;
+  if (n_fast > 0 && h.bf16_method == KAON_SR && h.p_dtype == KAON_BF16 && h.g_dtype == KAON_BF16)
+    ff = fast_fn<OPT, PHASE>(codec, fast_flags(h));
+  if (!ff) n_fast = 0;
+  if (n_fast > 0) {
+    hipLaunchKernelGGL(ff, dim3(n_fast), dim3(KAON_WG), 0, st, L.descs, L.elem_items, ws, h);
+  }
+  const int32_t rest = L.n_row_items - n_fast;
+  if (rest > 0) {
+    ElemFn fg = elem_fn<OPT, PHASE>(h.p_dtype, h.g_dtype, codec);
+    hipLaunchKernelGGL(fg, dim3(rest), dim3(KAON_WG), 0, st, L.descs, L.elem_items + n_fast, ws, h);
+  }
+  return check_launch(PHASE == 5 ? "kaon: keep-count launch" : "kaon: apply launch");
+}
+
+using StatsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int);
+// register classes of the row kernels: rows of <= 4, 10, 24 chunks per lane,
+// and the streaming kernel; dynamic LDS holds one slice column partial
+constexpr int kClassMaxC[4] = {4 * 512, 10 * 512, 24 * 512, KAON_MAX_ROW};
+
+template <int GT>
+StatsFn stats_fn_gt(int cls) {
+  switch (cls) {
+    case 0: return k_stats<GT, 4>;
+    case 1: return k_stats<GT, 10>;
+    case 2: return k_stats<GT, 24>;
+    case 3: return k_stats<GT, 0>;
+  }
+  return nullptr;
+}
+StatsFn stats_fn(int gt, int cls) { return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls) : stats_fn_gt<KAON_F32>(cls); }
+
+using SsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
+SsFn ss_fn(int gt) { return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : (SsFn)k_ss<KAON_F32>; }
 
 using MsamFn = void (*)(const KaonTensor*, const KaonItem*, KaonHyper, float, float, uint32_t);
 MsamFn msam_fn(int pt, int codec) {
@@ -937,21 +1446,19 @@ MsamFn msam_fn(int pt, int codec) {
   return nullptr;
 }
 
-using SsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
-SsFn ss_fn(int gt) { return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : (SsFn)k_ss<KAON_F32>; }
-
-// Phase-1 launches, one per register class run (items are sorted by class).
-int launch_rows(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipStream_t st) {
+// Phase-1 launches, one per register class run (slices are sorted by class).
+int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipStream_t st) {
   int32_t off = 0;
   for (int cls = 0; cls < 4; ++cls) {
     const int32_t cnt = L.row_runs[cls];
     if (cnt <= 0) continue;
-    RowsFn fn = rows_fn(hp.g_dtype, 1 << cls);
-    hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), 0, st, L.descs, L.row_items + off, ws, hp, mode);
+    StatsFn fn = stats_fn(hp.g_dtype, cls);
+    const size_t lds = mode == 0 ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
+    hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);
     off += cnt;
   }
-  if (off != L.n_row_items) return fail("kaon: row-item class runs do not add up to n_row_items");
-  return check_launch("kaon: k_rows launch");
+  if (off != L.n_row_items) return fail("kaon: slice class runs do not add up to n_row_items");
+  return check_launch("kaon: k_stats launch");
 }
 
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who) {
@@ -976,16 +1483,16 @@ const char* kaon_last_error(void) { return g_err.c_str(); }
 int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
   int rc = validate(L, hp, "kaon_adakaon_phases: null argument");
   if (rc) return rc;
-  if (L->n_tensors <= 0) return 0;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   Ws ws{(float*)L->workspace};
   KaonHyper h = *hp;
   const bool mom = (h.flags & KAON_F_MOMENTUM) && h.codec != KAON_MOM_NONE;
   const int codec = mom ? h.codec : KAON_MOM_NONE;
   if (!mom) h.flags &= ~(KAON_F_MOMENTUM | KAON_F_NK_REMOVE | KAON_F_NK_CLIMB);
-  const bool quant = codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT;
+  h.codec = codec;
   if (mask & (1u << 1)) {
-    if ((rc = launch_rows(*L, ws, h, 0, st))) return rc;
+    if ((rc = launch_stats(*L, ws, h, 0, st))) return rc;
   }
   if ((mask & (1u << 2)) && L->n_fin_items > 0) {
     hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
@@ -996,31 +1503,24 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
                        h);
     if ((rc = check_launch("kaon: k_ss launch"))) return rc;
   }
-  if (mask & (1u << 4)) {
-    hipLaunchKernelGGL(k_fac, dim3(L->n_tensors), dim3(KAON_WG), 0, st, L->descs, ws, h);
-    if ((rc = check_launch("kaon: k_fac launch"))) return rc;
-  }
-  if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {
-    FlatFn f5 = flat_fn<KAON_OPT_ADAKAON, 5>(h.p_dtype, h.g_dtype, codec);
-    hipLaunchKernelGGL(f5, dim3(L->n_flat_items), dim3(KAON_WG), 0, st, L->descs, L->flat_items, ws, h);
-    if ((rc = check_launch("kaon: keep-count launch"))) return rc;
+  // phase 5 always runs for Adakaon: it also publishes the clip divisor
+  if (mask & (1u << 5)) {
+    if ((rc = launch_elem<KAON_OPT_ADAKAON, 5>(*L, ws, h, codec, st))) return rc;
   }
   if (mask & (1u << 6)) {
-    FlatFn f6 = flat_fn<KAON_OPT_ADAKAON, 6>(h.p_dtype, h.g_dtype, codec);
-    hipLaunchKernelGGL(f6, dim3(L->n_flat_items), dim3(KAON_WG), 0, st, L->descs, L->flat_items, ws, h);
-    if ((rc = check_launch("kaon: apply launch"))) return rc;
+    if ((rc = launch_elem<KAON_OPT_ADAKAON, 6>(*L, ws, h, codec, st))) return rc;
   }
   return 0;
 }
 
 int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
-  return kaon_adakaon_phases(L, hp, 0x7Eu, stream);
+  return kaon_adakaon_phases(L, hp, 0x6Eu, stream);
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
   int rc = validate(L, hp, "kaon_lion_phases: null argument");
   if (rc) return rc;
-  if (L->n_tensors <= 0) return 0;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (hp->codec == KAON_MOM_NONE) return fail("kaon_lion_step: Lion always keeps a momentum buffer");
   hipStream_t st = (hipStream_t)stream;
   Ws ws{(float*)L->workspace};
@@ -1029,17 +1529,13 @@ int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, vo
   h.flags &= ~(KAON_F_NK_REMOVE | KAON_F_NK_CLIMB);
   const bool quant = h.codec == KAON_MOM_INT8 || h.codec == KAON_MOM_4BIT;
   if (mask & (1u << 1)) {
-    if ((rc = launch_rows(*L, ws, h, 1, st))) return rc;
+    if ((rc = launch_stats(*L, ws, h, 1, st))) return rc;
   }
   if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {
-    FlatFn f5 = flat_fn<KAON_OPT_LION, 5>(h.p_dtype, h.g_dtype, h.codec);
-    hipLaunchKernelGGL(f5, dim3(L->n_flat_items), dim3(KAON_WG), 0, st, L->descs, L->flat_items, ws, h);
-    if ((rc = check_launch("kaon: lion keep-count launch"))) return rc;
+    if ((rc = launch_elem<KAON_OPT_LION, 5>(*L, ws, h, h.codec, st))) return rc;
   }
   if (mask & (1u << 6)) {
-    FlatFn f6 = flat_fn<KAON_OPT_LION, 6>(h.p_dtype, h.g_dtype, h.codec);
-    hipLaunchKernelGGL(f6, dim3(L->n_flat_items), dim3(KAON_WG), 0, st, L->descs, L->flat_items, ws, h);
-    if ((rc = check_launch("kaon: lion apply launch"))) return rc;
+    if ((rc = launch_elem<KAON_OPT_LION, 6>(*L, ws, h, h.codec, st))) return rc;
   }
   return 0;
 }

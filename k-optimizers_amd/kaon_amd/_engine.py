@@ -42,7 +42,8 @@ def _align(n: int, a: int = 256) -> int:
 class Plan:
     """Device tables + workspace of one planned launch group."""
 
-    def __init__(self, opt: int, codec: int, entries: Sequence[dict[str, Any]], device: torch.device) -> None:
+    def __init__(self, opt: int, codec: int, entries: Sequence[dict[str, Any]], device: torch.device,
+                 p_dtype: int = L.BF16, g_dtype: int = L.BF16, bf16_method: int = L.SR) -> None:
         n = len(entries)
         descs = (L.KaonTensor * max(n, 1))()
         for i, e in enumerate(entries):
@@ -59,16 +60,21 @@ class Plan:
             d.block4 = int(e.get("block4", 0))
             d.tensor_id = int(e["tensor_id"])
         info = L.KaonPlanInfo()
+        args = L.KaonPlanArgs(opt, codec, p_dtype, g_dtype, bf16_method)
         lib = L.lib()
-        L.check(lib.kaon_plan(opt, codec, descs, n, None, None, None, ctypes.byref(info)), "kaon_plan")
+        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, ctypes.byref(info)),
+                "kaon_plan")
         rows = (L.KaonItem * max(info.n_row_items, 1))()
+        elems = (L.KaonItem * max(info.n_row_items, 1))()
         fins = (L.KaonItem * max(info.n_fin_items, 1))()
         flats = (L.KaonItem * max(info.n_flat_items, 1))()
-        L.check(lib.kaon_plan(opt, codec, descs, n, rows, fins, flats, ctypes.byref(info)), "kaon_plan")
+        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, ctypes.byref(info)),
+                "kaon_plan")
         self.info = info
         self.descs = descs
         parts = [bytes(descs)[: ctypes.sizeof(L.KaonTensor) * n],
                  bytes(rows)[: 16 * info.n_row_items],
+                 bytes(elems)[: 16 * info.n_row_items],
                  bytes(fins)[: 16 * info.n_fin_items],
                  bytes(flats)[: 16 * info.n_flat_items]]
         offs, total = [], 0
@@ -82,11 +88,12 @@ class Plan:
         self.workspace = torch.empty(max(int(info.ws_words), 4), dtype=torch.float32, device=device)
         base = self.table.data_ptr()
         la = L.KaonLaunch()
-        la.descs, la.row_items, la.fin_items, la.flat_items = (base + o for o in offs)
+        la.descs, la.row_items, la.elem_items, la.fin_items, la.flat_items = (base + o for o in offs)
         la.n_tensors, la.n_row_items = n, info.n_row_items
         la.n_fin_items, la.n_flat_items = info.n_fin_items, info.n_flat_items
         for k in range(4):
             la.row_runs[k] = info.row_runs[k]
+        la.n_fast = info.n_fast
         la.workspace = self.workspace.data_ptr()
         self.launch = la
 

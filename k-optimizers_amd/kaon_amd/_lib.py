@@ -23,7 +23,7 @@ OPT_ADAKAON, OPT_LION, OPT_ADAMUON = 0, 1, 2
 
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB = 1, 2, 4, 8, 16, 32, 64
 
-COLGROUP = 32
+ROW_BUDGET = 20
 COLITEM = 2048
 FLAT_ITEM = 16384
 MAX_ROW = 16384
@@ -52,14 +52,22 @@ class KaonItem(ctypes.Structure):
 class KaonPlanInfo(ctypes.Structure):
     _fields_ = [("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
-                ("row_runs", ctypes.c_int32 * 4), ("ws_words", ctypes.c_int64)]
+                ("row_runs", ctypes.c_int32 * 4), ("n_fast", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("ws_words", ctypes.c_int64)]
+
+
+class KaonPlanArgs(ctypes.Structure):
+    _fields_ = [("opt", ctypes.c_int32), ("codec", ctypes.c_int32), ("p_dtype", ctypes.c_int32),
+                ("g_dtype", ctypes.c_int32), ("bf16_method", ctypes.c_int32)]
 
 
 class KaonLaunch(ctypes.Structure):
-    _fields_ = [("descs", ctypes.c_void_p), ("row_items", ctypes.c_void_p), ("fin_items", ctypes.c_void_p),
-                ("flat_items", ctypes.c_void_p), ("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
+    _fields_ = [("descs", ctypes.c_void_p), ("row_items", ctypes.c_void_p), ("elem_items", ctypes.c_void_p),
+                ("fin_items", ctypes.c_void_p), ("flat_items", ctypes.c_void_p),
+                ("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
-                ("row_runs", ctypes.c_int32 * 4), ("workspace", ctypes.c_void_p)]
+                ("row_runs", ctypes.c_int32 * 4), ("n_fast", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("workspace", ctypes.c_void_p)]
 
 
 class KaonHyper(ctypes.Structure):
@@ -84,7 +92,8 @@ _VP, _I32, _I64, _U32, _U64, _F = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int
 SIGNATURES = {
     "kaon_abi_version": ([], ctypes.c_int),
     "kaon_last_error": ([], ctypes.c_char_p),
-    "kaon_plan": ([_I32, _I32, _VP, _I32, _VP, _VP, _VP, ctypes.POINTER(KaonPlanInfo)], ctypes.c_int),
+    "kaon_plan": ([ctypes.POINTER(KaonPlanArgs), _VP, _I32, _VP, _VP, _VP, _VP, ctypes.POINTER(KaonPlanInfo)],
+                  ctypes.c_int),
     "kaon_adakaon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adakaon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),

@@ -31,14 +31,16 @@
  *
  * Reduction order.  torch does not specify its fp32 reduction order (it
  * depends on the CPU ISA and thread count).  This restatement fixes one
- * canonical, accurate order, which the HIP kernels implement bit-for-bit:
- *   CSUM(x[0..n)):  256 lanes; lane l accumulates (from +0.0f, in order) the
- *     elements of 8-element chunks l, l+256, l+512, ...; each 64-lane group is
- *     reduced by an xor butterfly (offsets 32,16,8,4,2,1); the group results
- *     of the groups that hold any chunk are folded left to right.
- *   COLSUM_j over R rows: rows are cut into groups of KAON_COLGROUP (32)
- *     consecutive rows; each group is summed in row order, the group partials
- *     are summed in group order.
+ * canonical, accurate order, which the HIP kernels implement bit-for-bit
+ * (one wave64 per row, rows grouped per wave, four waves per workgroup):
+ *   CSUM(x[0..n)):  64 lanes; lane l accumulates (from +0.0f, in order) the
+ *     elements of 8-element chunks l, l+64, l+128, ...; the 64 lane sums are
+ *     reduced by an xor butterfly (offsets 32,16,8,4,2,1): a[l] += a[l+o].
+ *   COLSUM_j over R rows with row length C: cpl = ceil(ceil(C/8)/64) chunks
+ *     per lane, RW = max(1, 20 / cpl) rows per wave group; a wave group sums
+ *     its RW consecutive rows in row order; a slice is 4 consecutive wave
+ *     groups whose sums are folded in group order; the slice sums are added
+ *     in slice order (every partial starts from +0.0f).
  *   Sum of squares for the RMS clip: CSUM over each row (C elements), then
  *     CSUM over the R row results.
  */
@@ -47,9 +49,10 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define KAON_COLGROUP 32
-#define KAON_LANES 256
+#define KAON_LANES 64
 #define KAON_CHUNK 8
+#define KAON_ROW_BUDGET 20   /* chunks per lane a wave group spans */
+#define KAON_WAVES 4         /* wave groups per slice */
 
 /* dtype codes shared with the HIP library and oracle.py */
 enum { KO_F32 = 0, KO_BF16 = 1 };
@@ -143,28 +146,28 @@ static inline uint16_t sr_bf16(float x, uint32_t noise) {
 float ko_csum(const float* x, int64_t n) {
     if (n <= 0) return 0.0f;
     int64_t nch = (n + KAON_CHUNK - 1) / KAON_CHUNK;
-    float acc[KAON_LANES];
+    float a[KAON_LANES];
     for (int l = 0; l < KAON_LANES; ++l) {
-        float a = 0.0f;
+        float acc = 0.0f;
         for (int64_t k = l; k < nch; k += KAON_LANES)
             for (int e = 0; e < KAON_CHUNK; ++e) {
                 int64_t j = KAON_CHUNK * k + e;
-                if (j < n) a = a + x[j];
+                if (j < n) acc = acc + x[j];
             }
-        acc[l] = a;
+        a[l] = acc;
     }
-    float s[4];
-    for (int w = 0; w < 4; ++w) {
-        float* a = acc + 64 * w;
-        for (int o = 32; o >= 1; o >>= 1)
-            for (int l = 0; l < o; ++l) a[l] = a[l] + a[l + o];
-        s[w] = a[0];
-    }
-    int nw = (int)((nch + 63) / 64);
-    if (nw > 4) nw = 4;
-    float r = s[0];
-    for (int w = 1; w < nw; ++w) r = r + s[w];
-    return r;
+    for (int o = KAON_LANES / 2; o >= 1; o >>= 1)
+        for (int l = 0; l < o; ++l) a[l] = a[l] + a[l + o];
+    return a[0];
+}
+
+/* Rows per wave group of the column-sum order (see the header). */
+int64_t ko_rows_per_wave(int64_t C) {
+    int64_t nch = (C + KAON_CHUNK - 1) / KAON_CHUNK;
+    int64_t cpl = (nch + KAON_LANES - 1) / KAON_LANES;
+    if (cpl < 1) cpl = 1;
+    int64_t rw = KAON_ROW_BUDGET / cpl;
+    return rw < 1 ? 1 : rw;
 }
 
 /* ------------------------------------------------------------- tensors */
@@ -409,20 +412,26 @@ int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bou
  * on x [R, C]; returns U = (x * r) * c in `u`. */
 static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u) {
     int64_t R = t->R, C = t->C;
+    int64_t RW = ko_rows_per_wave(C);
     float* q = (float*)malloc(sizeof(float) * (size_t)C);
-    float* colacc = (float*)calloc((size_t)C, sizeof(float));
+    float* pw = (float*)calloc((size_t)C, sizeof(float));  /* wave-group partial */
+    float* ps = (float*)calloc((size_t)C, sizeof(float));  /* slice partial */
     float* colsum = (float*)calloc((size_t)C, sizeof(float));
     for (int64_t r = 0; r < R; ++r) {
         for (int64_t j = 0; j < C; ++j) {
             float v = x[r * C + j] * x[r * C + j];
             if (add_eps) v = v + eps1f;
             q[j] = v;
-            colacc[j] = colacc[j] + v;
+            pw[j] = pw[j] + v;
         }
         float rmean = ko_csum(q, C) / (float)C;
         t->row[r] = ko_lerp(t->row[r], rmean, w2);
-        if ((r + 1) % KAON_COLGROUP == 0 || r + 1 == R) {
-            for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + colacc[j]; colacc[j] = 0.0f; }
+        int end_group = ((r + 1) % RW == 0) || r + 1 == R;
+        if (end_group) {
+            for (int64_t j = 0; j < C; ++j) { ps[j] = ps[j] + pw[j]; pw[j] = 0.0f; }
+            int64_t g = r / RW;
+            if ((g + 1) % KAON_WAVES == 0 || r + 1 == R)
+                for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + ps[j]; ps[j] = 0.0f; }
         }
     }
     float* cf = (float*)malloc(sizeof(float) * (size_t)C);
@@ -435,7 +444,7 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
         float rf = ko_rsqrt(t->row[r] / rm);
         for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf) * cf[j];
     }
-    free(q); free(colacc); free(colsum); free(cf);
+    free(q); free(pw); free(ps); free(colsum); free(cf);
 }
 
 /* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):

@@ -81,6 +81,8 @@ def lib() -> ctypes.CDLL:
                                     ctypes.c_double, ctypes.c_double, ctypes.c_uint32]
         L.ko_csum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
         L.ko_csum.restype = ctypes.c_float
+        L.ko_rows_per_wave.argtypes = [ctypes.c_int64]
+        L.ko_rows_per_wave.restype = ctypes.c_int64
         L.ko_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.ko_sr_noise_fill.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64,
                                        ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
@@ -125,6 +127,11 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
 def csum(x: np.ndarray) -> np.float32:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return np.float32(lib().ko_csum(_ptr(x), x.size))
+
+
+def rows_per_wave(C: int) -> int:
+    """Rows per wave group of the canonical column-sum order."""
+    return int(lib().ko_rows_per_wave(C))
 
 
 def philox4x32_10(ctr, key) -> np.ndarray:
@@ -394,6 +401,7 @@ def values(a: np.ndarray, dtype: int) -> np.ndarray:
 __all__ = [
     "BF16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "bf16_to_f32", "csum",
     "dequant", "f32_to_bf16", "fourbit_block_size", "gc_bf16", "init_state", "lerp", "lib", "make_param",
-    "newton_schulz", "philox4x32_10", "quant_4bit", "quant_int8", "sr_noise", "sr_round", "values",
+    "newton_schulz", "philox4x32_10", "quant_4bit", "quant_int8", "rows_per_wave", "sr_noise", "sr_round",
+    "values",
 ]
 _ = math

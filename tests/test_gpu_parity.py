@@ -75,6 +75,17 @@ EXTRA = {
                                                      cautious=False), p="f32", g="f32"),
     "nekaon_4bit_b256": _case("nekaon", _MIX, dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), momentum_dtype="4bit",
                                                    momentum_4bit_block=256), eval_train=True),
+    # specialized bf16/SR kernels: fac == 1 and fac > 1, each codec, WD on and off
+    "ada_bf16_sr_wd_clip_lo": _case("adakaon", _MIX, dict(lr=1e-3, momentum_dtype="bfloat16", weight_decay=0.05,
+                                                          clip_threshold=0.1)),
+    "ada_4bit_b128_clip_hi": _case("adakaon", _MIX, dict(lr=1e-4, momentum_dtype="4bit", clip_threshold=100.0)),
+    "ada_int8_wd_clip_lo": _case("adakaon", _MIX, dict(lr=1e-4, momentum_dtype="int8", weight_decay=0.1,
+                                                       clip_threshold=0.05)),
+    "lion_bf16_gc_wd": _case("lion", _MIX, dict(lr=2e-4, momentum_dtype="bfloat16", weight_decay=0.1)),
+    "lion_4bit_b64_gc": _case("lion", _MIX, dict(lr=2e-4, momentum_dtype="4bit", momentum_4bit_block=64)),
+    "nekaon_int8_bf16": _case("nekaon", _MIX, dict(lr=1e-4, k=1.5, momentum_dtype="int8"), eval_train=True),
+    "nekaon_4bit_b64_nowd": _case("nekaon", _MIX, dict(lr=1e-4, momentum_dtype="4bit", momentum_4bit_block=64,
+                                                       weight_decay=0.0), eval_train=True),
     "nekaon_int8_f32": _case("nekaon", [[96, 40], [33], [4, 8, 3, 3]],
                              dict(lr=1e-3, k=1.5, momentum_dtype="int8"), p="f32", g="f32", eval_train=True),
 }

@@ -59,7 +59,7 @@ def test_struct_layout_matches_c_compiler(tmp_path):
             assert got[(sname, fname)] == getattr(cls, fname).offset, (sname, fname)
 
 
-def _plan(shapes, opt=0, codec=3, block=128):
+def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
     L = _lib()
     n = len(shapes)
     descs = (L.KaonTensor * n)()
@@ -74,38 +74,59 @@ def _plan(shapes, opt=0, codec=3, block=128):
         d.tensor_id = i
         d.g = d.p = d.m = 0x1000 * (i + 1)
     info = L.KaonPlanInfo()
-    rc = L.lib().kaon_plan(opt, codec, descs, n, None, None, None, ctypes.byref(info))
+    args = L.KaonPlanArgs(opt, codec, 1, g_dtype, 0)
+    rc = L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, ctypes.byref(info))
     if rc:
         return rc, None, None, None, None, None
     rows = (L.KaonItem * max(info.n_row_items, 1))()
+    elems = (L.KaonItem * max(info.n_row_items, 1))()
     fins = (L.KaonItem * max(info.n_fin_items, 1))()
     flats = (L.KaonItem * max(info.n_flat_items, 1))()
-    assert L.lib().kaon_plan(opt, codec, descs, n, rows, fins, flats, ctypes.byref(info)) == 0
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, ctypes.byref(info)) == 0
+    # elem order: the same slices, specialized-kernel ones first
+    key = lambda it: (it.tensor, it.row0, it.nrows, it.kind)  # noqa: E731
+    assert sorted(key(rows[k]) for k in range(info.n_row_items)) == sorted(key(elems[k]) for k in range(info.n_row_items))
+    for k in range(info.n_row_items):
+        d = descs[elems[k].tensor]
+        fast = (g_dtype == 1 and d.factored == 1 and d.vec_rows == 1 and d.C % 8 == 0
+                and (codec != 4 or (d.block4 % 8 == 0 and d.C % d.block4 == 0 and 64 % (d.block4 // 8) == 0)))
+        assert (k < info.n_fast) == fast, (k, d.R, d.C)
     return 0, descs, info, rows, fins, flats
 
 
-def test_plan_covers_every_row_and_element_once():
+def _cpl(C):
+    return max(1, -(-(-(-C // 8)) // 64))
+
+
+@pytest.mark.parametrize("g_dtype", [0, 1])
+def test_plan_covers_every_row_and_element_once(g_dtype):
+    import oracle as O
+
     shapes = [(1280, 1280, 3, 3), (640, 640, 3, 3), (5120, 1280), (1280, 2048), (77, 33), (1280,), (5,), (3, 5, 7),
-              (9, 1), (2, 16384)]
-    rc, descs, info, rows, fins, flats = _plan(shapes, codec=4, block=64)
+              (9, 1), (2, 16384), (50, 12288), (7, 2880)]
+    rc, descs, info, rows, fins, flats = _plan(shapes, codec=4, block=64, g_dtype=g_dtype)
     assert rc == 0
     L = _lib()
     assert sum(info.row_runs) == info.n_row_items
-    # row items: every row of every tensor exactly once, classes ascending
+    # slices: every row of every tensor exactly once, classes ascending, the
+    # rows-per-wave of the oracle's column-sum order
     seen = {i: np.zeros(descs[i].R, np.int32) for i in range(len(shapes))}
-    cls_prev = -1
     off = 0
     for cls in range(4):
         for k in range(info.row_runs[cls]):
             it = rows[off + k]
-            seen[it.tensor][it.row0:it.row0 + it.nrows] += 1
-            assert it.nrows <= L.COLGROUP and it.row0 % L.COLGROUP == 0
             d = descs[it.tensor]
-            cpt = -(-(-(-d.C // 8)) // 256) if d.factored else 1
-            assert cpt <= (1 << cls)
+            seen[it.tensor][it.row0:it.row0 + it.nrows] += 1
+            assert it.kind == O.rows_per_wave(d.C)
+            assert it.nrows <= 4 * it.kind and it.row0 % (4 * it.kind) == 0
+            cpl = _cpl(d.C)
+            if not d.factored:
+                assert cls == 3
+            elif cls < 3:
+                assert cpl <= (4, 10, 24)[cls] and (cls < 2 or g_dtype == 1)
+            else:
+                assert cpl > 24 or (cpl > 10 and g_dtype == 0)
         off += info.row_runs[cls]
-        assert cls >= cls_prev
-        cls_prev = cls
     assert all((v == 1).all() for v in seen.values())
     # flat items: every element exactly once, 8-aligned starts
     cover = {i: 0 for i in range(len(shapes))}
@@ -131,15 +152,15 @@ def test_plan_covers_every_row_and_element_once():
             spans.append((d.ws_part, d.ws_part + d.ngroups * d.C))
         spans.append((d.ws_blk, d.ws_blk + 2 * nb))
         spans.append((d.ws_scal, d.ws_scal + 4))
-        assert d.ngroups == -(-d.R // L.COLGROUP)
+        assert d.ngroups == -(-d.R // (4 * O.rows_per_wave(d.C)))
         assert d.sqrt_n == np.float32(np.sqrt(float(max(d.n, 1))))
     spans.sort()
     for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):
         assert a1 <= b0
     assert spans[-1][1] <= info.ws_words
-    # vector flags: rows need C % 8 == 0
+    # vector flags: rows need C % 8 == 0 (or a single row)
     for i, s in enumerate(shapes):
-        assert descs[i].vec_rows == (1 if descs[i].C % 8 == 0 else 0)
+        assert descs[i].vec_rows == (1 if (descs[i].C % 8 == 0 or descs[i].R == 1) else 0)
 
 
 def test_plan_rejects_rows_longer_than_the_register_budget():

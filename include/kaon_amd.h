@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 1
+#define KAON_ABI_VERSION 2
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -116,6 +116,9 @@ typedef struct KaonItem {
 /* Columns per column-finalize work item. */
 #define KAON_COLITEM 2048
 
+/* Row classes of the slice kernels (KaonPlanInfo.row_runs). */
+#define KAON_ROW_CLASSES 7
+
 /*
  * Host-side plan: kaon_plan() fills the workspace offsets of every
  * descriptor and the work-item arrays.  The caller uploads descriptors and
@@ -126,10 +129,11 @@ typedef struct KaonPlanInfo {
   int32_t n_row_items;    /* slices, sorted by phase-1 register class (row_items) */
   int32_t n_fin_items;    /* finalize items (phase 2) */
   int32_t n_flat_items;   /* flat items of KAON_FLAT_ITEM elements (MSAM perturbation) */
-  int32_t row_runs[4];    /* slices per phase-1 register class: rows of <= 4, 10, 24 chunks per
-                             lane held in registers, streamed rows */
+  int32_t row_runs[KAON_ROW_CLASSES]; /* slices per row class, in row_items order: classes 0-2
+                             bf16 grads with 16-byte rows of <= 4, 10, 24 chunks per lane
+                             (prefetching kernels); 3-5 other rows of <= 4, 10, 24 chunks
+                             held in registers; 6 streamed rows */
   int32_t n_fast;         /* slices of elem_items that take the specialized kernels */
-  int32_t pad;
   int64_t ws_words;       /* workspace size in 4-byte words */
 } KaonPlanInfo;
 
@@ -154,8 +158,8 @@ typedef struct KaonLaunch {
   const KaonItem* fin_items;  /* device */
   const KaonItem* flat_items; /* device */
   int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
-  int32_t row_runs[4];
-  int32_t n_fast, pad;
+  int32_t row_runs[KAON_ROW_CLASSES];
+  int32_t n_fast;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
 } KaonLaunch;
 
@@ -205,7 +209,8 @@ int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
 /* The same steps restricted to the phases whose bit is set in `mask`
  * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,
- * 5 clip divisor + keep-count + absmax, 6 apply; Lion uses 1, 5, 6).  For
+ * 4 clip divisor, 5 keep-count + momentum absmax, 6 apply; Lion uses 1, 5,
+ * 6).  For
  * profiling one kernel at a time; running all phases in order is the step.
  * No counterpart in the reference, which has no phase boundary to expose. */
 int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);

@@ -16,6 +16,21 @@
 
 namespace kaon {
 
+// Global-memory view of a generic pointer.  Descriptor pointers are generic
+// (they are read from the descriptor table), and accesses through generic
+// pointers compile to flat_* instructions, which also count against lgkmcnt
+// and so hold up waits on LDS and scalar loads; through this view they are
+// global_* instructions.
+#define KAON_G __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ KAON_G T* G(T* p) {
+  return (KAON_G T*)p;
+}
+// vector types for 16- and 8-byte accesses through global views
+typedef uint32_t ku4 __attribute__((ext_vector_type(4)));
+typedef uint32_t ku2 __attribute__((ext_vector_type(2)));
+typedef float kf4 __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ bf16
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -71,7 +86,7 @@ __device__ __forceinline__ void noise8(uint64_t seed, uint32_t step, uint32_t ti
                                        int64_t e0, const uint16_t* inj, int cnt, uint32_t w[8]) {
   if (inj) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = i < cnt ? (uint32_t)inj[e0 + i] : 0u;
+    for (int i = 0; i < 8; ++i) w[i] = i < cnt ? (uint32_t)G(inj)[e0 + i] : 0u;
     return;
   }
   const uint64_t ch = (uint64_t)e0 >> 3;
@@ -87,7 +102,7 @@ __device__ __forceinline__ void noise8(uint64_t seed, uint32_t step, uint32_t ti
 // Noise word of one element (any alignment).
 __device__ __forceinline__ uint32_t noise1(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream,
                                            int64_t e, const uint16_t* inj) {
-  if (inj) return inj[e];
+  if (inj) return G(inj)[e];
   const uint64_t ch = (uint64_t)e >> 3;
   uint32_t c[4] = {(uint32_t)ch, (uint32_t)(ch >> 32), tid, stream};
   philox10(c, (uint32_t)seed, step);
@@ -108,9 +123,9 @@ __device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t noise) {
 template <int DT>
 __device__ __forceinline__ void ld8(const void* base, int64_t off, int cnt, bool vec, float o[8]) {
   if (DT == KAON_BF16) {
-    const uint16_t* b = (const uint16_t*)base + off;
+    const KAON_G uint16_t* b = G((const uint16_t*)base + off);
     if (vec) {
-      const uint4 v = *(const uint4*)b;
+      const ku4 v = *(const KAON_G ku4*)b;
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -122,10 +137,10 @@ __device__ __forceinline__ void ld8(const void* base, int64_t off, int cnt, bool
       for (int i = 0; i < 8; ++i) o[i] = i < cnt ? bf2f(b[i]) : 0.0f;
     }
   } else {
-    const float* b = (const float*)base + off;
+    const KAON_G float* b = G((const float*)base + off);
     if (vec) {
-      const float4 v0 = *(const float4*)b;
-      const float4 v1 = *(const float4*)(b + 4);
+      const kf4 v0 = *(const KAON_G kf4*)b;
+      const kf4 v1 = *(const KAON_G kf4*)(b + 4);
       o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w;
       o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
     } else {
@@ -137,9 +152,9 @@ __device__ __forceinline__ void ld8(const void* base, int64_t off, int cnt, bool
 
 // Raw bf16 chunk (bits) load/store.
 __device__ __forceinline__ void ld8_bits(const void* base, int64_t off, int cnt, bool vec, uint32_t o[8]) {
-  const uint16_t* b = (const uint16_t*)base + off;
+  const KAON_G uint16_t* b = G((const uint16_t*)base + off);
   if (vec) {
-    const uint4 v = *(const uint4*)b;
+    const ku4 v = *(const KAON_G ku4*)b;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -152,14 +167,14 @@ __device__ __forceinline__ void ld8_bits(const void* base, int64_t off, int cnt,
   }
 }
 __device__ __forceinline__ void st8_bits(void* base, int64_t off, int cnt, bool vec, const uint32_t o[8]) {
-  uint16_t* b = (uint16_t*)base + off;
+  KAON_G uint16_t* b = G((uint16_t*)base + off);
   if (vec) {
-    uint4 v;
+    ku4 v;
     v.x = (o[0] & 0xFFFFu) | (o[1] << 16);
     v.y = (o[2] & 0xFFFFu) | (o[3] << 16);
     v.z = (o[4] & 0xFFFFu) | (o[5] << 16);
     v.w = (o[6] & 0xFFFFu) | (o[7] << 16);
-    *(uint4*)b = v;
+    *(KAON_G ku4*)b = v;
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -167,10 +182,10 @@ __device__ __forceinline__ void st8_bits(void* base, int64_t off, int cnt, bool 
   }
 }
 __device__ __forceinline__ void st8_f32(void* base, int64_t off, int cnt, bool vec, const float o[8]) {
-  float* b = (float*)base + off;
+  KAON_G float* b = G((float*)base + off);
   if (vec) {
-    *(float4*)b = make_float4(o[0], o[1], o[2], o[3]);
-    *(float4*)(b + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    *(KAON_G kf4*)b = kf4{o[0], o[1], o[2], o[3]};
+    *(KAON_G kf4*)(b + 4) = kf4{o[4], o[5], o[6], o[7]};
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -180,26 +195,60 @@ __device__ __forceinline__ void st8_f32(void* base, int64_t off, int cnt, bool v
 
 // ------------------------------------------------------------------ reductions
 // Canonical 64-lane sum (the oracle's CSUM): every lane has accumulated, in
-// order, the elements of its chunks l, l+64, ...; the lane sums are reduced by
-// an xor butterfly with offsets 32..1 and lane 0's result is the canonical one
-// (other lanes add in other orders).  Call with all 64 lanes active; returns
-// lane 0's value to every lane.
+// order, the elements of its chunks l, l+64, ...; the lane sums are then
+// combined by an xor butterfly with offsets 32, 16, 8, 4, 2, 1: at each step
+// every lane adds its partner's value (a + b == b + a bit for bit, so lanes l
+// and l^o end each step holding the same value and all lanes end with the
+// canonical sum).  The steps run on the VALU: v_permlane32_swap and
+// v_permlane16_swap exchange the halves / rows for offsets 32 and 16; a row
+// rotation by 8 is the xor-8 partner; a rotation by 4 reads lane (i +- 4) mod
+// 16, which after the xor-8 step holds the xor-4 partner's value; quad
+// permutes give offsets 2 and 1.  Call with all 64 lanes active.
+__device__ __forceinline__ uint32_t dpp_ror8(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t dpp_ror4(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x124, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t x) {  // quad_perm [2,3,0,1]
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t x) {  // quad_perm [1,0,3,2]
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);
+}
+
+// Butterfly with a commutative combine: OP(a, partner) at offsets 32..1.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_butterfly(uint32_t a, Op op) {
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    a = op(r[0], r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+    a = op(r[0], r[1]);
+  }
+  a = op(a, dpp_ror8(a));
+  a = op(a, dpp_ror4(a));
+  a = op(a, dpp_xor2(a));
+  a = op(a, dpp_xor1(a));
+  return __builtin_amdgcn_readfirstlane(a);
+}
+
 __device__ __forceinline__ float wave_csum(float a) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) a = a + __shfl_xor(a, o, 64);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a)));
+  return __uint_as_float(wave_butterfly(__float_as_uint(a), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+  }));
 }
 
 __device__ __forceinline__ float wave_max(float a) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a)));
+  return __uint_as_float(wave_butterfly(__float_as_uint(a), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y)));
+  }));
 }
 
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t a) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
-  return __builtin_amdgcn_readfirstlane(a);
+  return wave_butterfly(a, [](uint32_t x, uint32_t y) { return x + y; });
 }
 
 __device__ __forceinline__ float uniform_f(float x) {

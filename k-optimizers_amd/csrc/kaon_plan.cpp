@@ -48,15 +48,18 @@ int64_t rows_per_wave(int64_t C) {
   return rw < 1 ? 1 : rw;
 }
 
-// register class of the phase-1 kernel: rows held in registers up to 4, 10
-// and 24 chunks per lane (24 only for bf16 grads), else streamed (class 3)
+// row class of a slice (phase-1 and phase-3 kernels): 0-2 bf16 grads in
+// 16-byte rows of <= 4, 10, 24 chunks per lane, loaded whole into registers
+// by the prefetching kernels; 3-5 other rows held in registers up to 4, 10
+// and 24 chunks per lane (24 only for bf16 grads); 6 streamed rows
 int row_class(const KaonTensor& t, int32_t g_dtype) {
-  if (!t.factored) return 3;
+  if (!t.factored) return 6;
   const int64_t cpl = chunks_per_lane(t.C);
-  if (cpl <= 4) return 0;
-  if (cpl <= 10) return 1;
-  if (cpl <= 24 && g_dtype == KAON_BF16) return 2;
-  return 3;
+  if (g_dtype == KAON_BF16 && t.vec_rows && t.C % 8 == 0 && cpl <= 24) return cpl <= 4 ? 0 : cpl <= 10 ? 1 : 2;
+  if (cpl <= 4) return 3;
+  if (cpl <= 10) return 4;
+  if (cpl <= 24 && g_dtype == KAON_BF16) return 5;
+  return 6;
 }
 }  // namespace
 

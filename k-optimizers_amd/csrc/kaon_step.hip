@@ -20,7 +20,8 @@
 //   phase 1  slices      GC row means, row EMA, column partials (LDS fold)
 //   phase 2  fin items   column EMA + column factors; row mean + row factors
 //   phase 3  slices      per-row sums of U^2 (U = G*r*c)
-//   phase 5  slices      clip divisor, cautious keep-count, momentum absmax
+//   phase 4  tensors     clip divisor from the row sums
+//   phase 5  slices      cautious keep-count, momentum absmax
 //   phase 6  slices      requant + momentum write, cautious rescale, weight
 //                        write (SR / RN / kahan / fp32), Nekaon remove+climb
 // All reductions follow the CPU oracle's canonical order; there are no
@@ -61,16 +62,20 @@ int check_launch(const char* what) {
 // ------------------------------------------------------------ workspace views
 struct Ws {
   float* base;
-  __device__ float* mu(const KaonTensor& T) const { return base + T.ws_row; }
-  __device__ float* rf(const KaonTensor& T) const { return base + T.ws_row + T.R; }
-  __device__ float* rs(const KaonTensor& T) const { return base + T.ws_row + 2 * T.R; }
-  __device__ uint32_t* ramax(const KaonTensor& T) const { return (uint32_t*)(base + T.ws_row + 3 * T.R); }
-  __device__ float* roldsc(const KaonTensor& T) const { return base + T.ws_row + 4 * T.R; }
-  __device__ float* cf(const KaonTensor& T) const { return base + T.ws_col; }
-  __device__ float* part(const KaonTensor& T) const { return base + T.ws_part; }
-  __device__ uint32_t* bamax(const KaonTensor& T) const { return (uint32_t*)(base + T.ws_blk); }
-  __device__ float* boldsc(const KaonTensor& T, int64_t nb) const { return base + T.ws_blk + nb; }
-  __device__ float* scal(const KaonTensor& T) const { return base + T.ws_scal; }
+  __device__ KAON_G float* mu(const KaonTensor& T) const { return G(base + T.ws_row); }
+  __device__ KAON_G float* rf(const KaonTensor& T) const { return G(base + T.ws_row + T.R); }
+  __device__ KAON_G float* rs(const KaonTensor& T) const { return G(base + T.ws_row + 2 * T.R); }
+  __device__ KAON_G uint32_t* ramax(const KaonTensor& T) const {
+    return G((uint32_t*)(base + T.ws_row + 3 * T.R));
+  }
+  __device__ KAON_G float* roldsc(const KaonTensor& T) const { return G(base + T.ws_row + 4 * T.R); }
+  __device__ KAON_G float* cf(const KaonTensor& T) const { return G(base + T.ws_col); }
+  __device__ KAON_G float* part(const KaonTensor& T) const { return G(base + T.ws_part); }
+  __device__ KAON_G uint32_t* bamax(const KaonTensor& T) const { return G((uint32_t*)(base + T.ws_blk)); }
+  __device__ KAON_G float* boldsc(const KaonTensor& T, int64_t nb) const { return G(base + T.ws_blk + nb); }
+  __device__ KAON_G float* scal(const KaonTensor& T) const { return G(base + T.ws_scal); }
+  // generic address of the keep-count word (for atomics)
+  __device__ uint32_t* keep_ctr(const KaonTensor& T) const { return (uint32_t*)(base + T.ws_scal) + 1; }
 };
 
 template <int DT>
@@ -104,7 +109,7 @@ __device__ __forceinline__ int chunk_cnt(int64_t c, int64_t C) {
 // Zero what phase 5 accumulates with atomics (keep-count; 4-bit block absmax
 // of blocks that straddle rows).  Run by the phase-1 slice.
 __device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const Ws& ws, int codec) {
-  if (it.row0 == 0 && threadIdx.x == 0) ((uint32_t*)ws.scal(T))[1] = 0u;
+  if (it.row0 == 0 && threadIdx.x == 0) ((KAON_G uint32_t*)ws.scal(T))[1] = 0u;
   if (codec == KAON_MOM_4BIT) {
     const int64_t e_begin = (int64_t)it.row0 * T.C;
     const int64_t e_end = (int64_t)(it.row0 + it.nrows) * T.C;
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
 
   const bool gc = (hp.flags & KAON_F_GC) != 0;
   if (mode == 1 && !gc) return;
-  float* mu_arr = ws.mu(T);
+  KAON_G float* mu_arr = ws.mu(T);
   const int RW = it.kind;
 
   // registers: row buffer (CPL chunks) and the wave-group column partial
@@ -307,7 +312,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
     }
     __syncthreads();
   }
-  float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
+  KAON_G float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
   for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = lds_col[j];
 }
 
@@ -323,8 +328,8 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
   const KaonTensor& T = D[it.tensor];
   const int64_t R = T.R, C = T.C;
   if (it.kind == 0) {
-    const float* part = ws.part(T);
-    float* cf = ws.cf(T);
+    const KAON_G float* part = ws.part(T);
+    KAON_G float* cf = ws.cf(T);
     for (int64_t j = it.row0 + threadIdx.x; j < (int64_t)it.row0 + it.nrows; j += KAON_WG) {
       float cs = 0.0f;
       int g = 0;
@@ -354,7 +359,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
     }
     __syncthreads();
     const float rm = rm_s;
-    float* rf = ws.rf(T);
+    KAON_G float* rf = ws.rf(T);
     for (int64_t i = threadIdx.x; i < R; i += KAON_WG) rf[i] = 1.0f / sqrtf(T.row[i] / rm);
   }
 }
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
   const int cpl = (int)((nch + 63) >> 6);
   const bool vec = T.vec_rows != 0;
   const bool gc = (hp.flags & KAON_F_GC) && T.factored;
-  const float* cfa = T.factored ? ws.cf(T) : T.v;
+  const float* cfa = T.factored ? (const float*)ws.cf(T) : T.v;
   const WaveRows wr = wave_rows(it);
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
@@ -407,6 +412,283 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
   }
 }
 
+// =============================================================== phase 4
+// Clip divisor of every tensor: max(RMS(U) / clip, 1), RMS(U) = sqrt(sum of
+// the row sums rs) / sqrt(n), the rows summed in the canonical 64-lane order
+// (_factored.py:84-89 via adakaon.py:1001-1003).  One wave per tensor.
+__global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
+                                                     KaonHyper hp) {
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= n_tensors) return;
+  const KaonTensor& T = D[t];
+  if (T.n == 0) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t R = T.R;
+  const KAON_G float* rs = ws.rs(T);
+  float a = 0.0f;
+  for (int64_t c = lane; c * 8 < R; c += 64) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = rs[min(c * 8 + i, R - 1)];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c * 8 + i < R) a = a + v[i];
+  }
+  const float ss = wave_csum(a);
+  if (lane == 0) ws.scal(T)[0] = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
+}
+
+// =============================================================== prefetching row kernels
+// Phases 1 and 3 for slices of bf16 grads with 16-byte rows (C % 8 == 0) of at
+// most 24 chunks per lane.  A wave loads its whole wave group (RW rows, RW *
+// CPL <= 24 chunks per lane) into registers as packed bf16 with every load
+// issued before the first use, so each lane keeps up to 24 x 16 bytes in
+// flight; the row reductions and the column fold then run from registers.
+// The arithmetic and its order are those of k_stats / k_ss.
+
+__device__ __forceinline__ void unpack8(const ku4 v, float o[8]) {
+  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xFFFF0000u);
+  o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+// Marks packed registers as rewritten (no instruction is emitted), so values
+// derived from them are computed after this point, not hoisted above it or
+// reused from before it.
+template <int CPL, int RW>
+__device__ __forceinline__ void launder(ku4 (&raw)[RW][CPL]) {
+#pragma unroll
+  for (int j = 0; j < RW; ++j)
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+      asm volatile("" : "+v"(raw[j][k].x), "+v"(raw[j][k].y), "+v"(raw[j][k].z), "+v"(raw[j][k].w));
+}
+
+template <int CPL, int RW>
+__device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64_t rb, int nrows, int64_t C,
+                                           int nch, int lane, ku4 (&raw)[RW][CPL]) {
+#pragma unroll
+  for (int j = 0; j < RW; ++j)
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = lane + 64 * k;
+      if (j < nrows && c < nch) raw[j][k] = *(const KAON_G ku4*)G(g + (rb + j) * C + (int64_t)c * 8);
+      else raw[j][k] = ku4{0u, 0u, 0u, 0u};
+    }
+}
+
+// q = (G - mu)^2 + e1 of one chunk, G - mu rounded to bf16 (GC in the grad
+// dtype); e1 = eps1, or 0 without eps (a square plus +0 is the square itself)
+__device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e1, float q[8]) {
+  float x[8];
+  unpack8(v, x);
+  if (gc) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      float a0 = x[i] - mu, a1 = x[i + 1] - mu;
+      rbf2(a0, a1);
+      x[i] = a0;
+      x[i + 1] = a1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = x[i] * x[i] + e1;
+}
+
+template <int CPL, int RW>
+__device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
+                                              const KaonHyper& hp, int mode, float* lds_col) {
+  const int64_t C = T.C;
+  const int nch = (int)(C >> 3);
+  const WaveRows wr = wave_rows(it);
+  const int nrows = (int)(wr.re - wr.rb);
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  const float e1 = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
+  if (mode == 1 && !gc) return;
+  ku4 raw[RW][CPL];
+  load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
+  float mu[RW];
+  KAON_G float* mu_arr = ws.mu(T);
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    mu[j] = 0.0f;
+    if (j >= nrows) continue;
+    const int64_t r = wr.rb + j;
+    if (gc) {
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (wr.lane + 64 * k < nch) {
+          float x[8];
+          unpack8(raw[j][k], x);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a = a + x[i];
+        }
+      }
+      mu[j] = rbf(wave_csum(a) / (float)C);
+      if (wr.lane == 0) mu_arr[r] = mu[j];
+    }
+    if (mode == 1) continue;
+    float a2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      if (wr.lane + 64 * k < nch) {
+        float q[8];
+        sq_chunk(raw[j][k], mu[j], gc, e1, q);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a2 = a2 + q[i];
+      }
+    }
+    const float s2 = wave_csum(a2);
+    if (wr.lane == 0) G(T.row)[r] = klerp(G(T.row)[r], s2 / (float)C, hp.w2);
+  }
+  if (mode == 1) return;
+  // column partial of the slice: each wave group's rows summed in row order,
+  // then the groups folded in order through LDS.  The launder keeps the
+  // compiler from hoisting the partial (CPL x 8 values) out of the loop.
+#pragma unroll 1
+  for (int wf = 0; wf < 4; ++wf) {
+    if (wr.w == wf && nrows > 0) {
+      launder<CPL, RW>(raw);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const int c = wr.lane + 64 * k;
+        if (c < nch) {
+          float v[8];
+          sq_chunk(raw[0][k], mu[0], gc, e1, v);
+#pragma unroll
+          for (int j = 1; j < RW; ++j) {
+            if (j < nrows) {
+              float q[8];
+              sq_chunk(raw[j][k], mu[j], gc, e1, q);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) v[i] = v[i] + q[i];
+            }
+          }
+          float4* l4 = (float4*)(lds_col + (int64_t)c * 8);
+          if (wf > 0) {
+            const float4 o0 = l4[0], o1 = l4[1];
+            v[0] = o0.x + v[0]; v[1] = o0.y + v[1]; v[2] = o0.z + v[2]; v[3] = o0.w + v[3];
+            v[4] = o1.x + v[4]; v[5] = o1.y + v[5]; v[6] = o1.z + v[6]; v[7] = o1.w + v[7];
+          }
+          l4[0] = make_float4(v[0], v[1], v[2], v[3]);
+          l4[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  KAON_G kf4* part = (KAON_G kf4*)(ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C);
+  const kf4* l4 = (const kf4*)lds_col;
+  for (int64_t j = threadIdx.x; j < (C >> 2); j += KAON_WG) part[j] = l4[j];
+}
+
+template <int CPL, int RW>
+__device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
+                                           const KaonHyper& hp) {
+  const int64_t C = T.C;
+  const int nch = (int)(C >> 3);
+  const WaveRows wr = wave_rows(it);
+  const int nrows = (int)(wr.re - wr.rb);
+  if (nrows <= 0) return;
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  float mu[RW], rf[RW];
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    const int64_t r = j < nrows ? wr.rb + j : wr.rb;
+    mu[j] = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    rf[j] = uniform_f(ws.rf(T)[r]);
+  }
+  ku4 raw[RW][CPL];
+  load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
+  const KAON_G float* cf = ws.cf(T);
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    if (j >= nrows) continue;
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = wr.lane + 64 * k;
+      if (c < nch) {
+        const kf4 c0 = *(const KAON_G kf4*)(cf + (int64_t)c * 8), c1 = *(const KAON_G kf4*)(cf + (int64_t)c * 8 + 4);
+        const float f[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        float x[8];
+        unpack8(raw[j][k], x);
+        if (gc) {
+#pragma unroll
+          for (int i = 0; i < 8; i += 2) {
+            float a0 = x[i] - mu[j], a1 = x[i + 1] - mu[j];
+            rbf2(a0, a1);
+            x[i] = a0;
+            x[i + 1] = a1;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float u = (x[i] * rf[j]) * f[i];
+          a = a + u * u;
+        }
+      }
+    }
+    const float s = wave_csum(a);
+    if (wr.lane == 0) ws.rs(T)[wr.rb + j] = s;
+  }
+}
+
+// Row class 0: 1-4 chunks per lane, 1 class 1: 5-10, class 2: 11-24; the
+// body is specialized on the exact chunks per lane and its rows per wave
+// group (RW = max(1, KAON_ROW_BUDGET / CPL)).
+#define KAON_PF_SWITCH(CLS, BODY, ...)                                                         \
+  switch (cpl) {                                                                                \
+    case 1: if (CLS == 0) BODY<1, 20>(__VA_ARGS__); break;                                      \
+    case 2: if (CLS == 0) BODY<2, 10>(__VA_ARGS__); break;                                      \
+    case 3: if (CLS == 0) BODY<3, 6>(__VA_ARGS__); break;                                       \
+    case 4: if (CLS == 0) BODY<4, 5>(__VA_ARGS__); break;                                       \
+    case 5: if (CLS == 1) BODY<5, 4>(__VA_ARGS__); break;                                       \
+    case 6: if (CLS == 1) BODY<6, 3>(__VA_ARGS__); break;                                       \
+    case 7: if (CLS == 1) BODY<7, 2>(__VA_ARGS__); break;                                       \
+    case 8: if (CLS == 1) BODY<8, 2>(__VA_ARGS__); break;                                       \
+    case 9: if (CLS == 1) BODY<9, 2>(__VA_ARGS__); break;                                       \
+    case 10: if (CLS == 1) BODY<10, 2>(__VA_ARGS__); break;                                     \
+    case 11: if (CLS == 2) BODY<11, 1>(__VA_ARGS__); break;                                     \
+    case 12: if (CLS == 2) BODY<12, 1>(__VA_ARGS__); break;                                     \
+    case 13: if (CLS == 2) BODY<13, 1>(__VA_ARGS__); break;                                     \
+    case 14: if (CLS == 2) BODY<14, 1>(__VA_ARGS__); break;                                     \
+    case 15: if (CLS == 2) BODY<15, 1>(__VA_ARGS__); break;                                     \
+    case 16: if (CLS == 2) BODY<16, 1>(__VA_ARGS__); break;                                     \
+    case 17: if (CLS == 2) BODY<17, 1>(__VA_ARGS__); break;                                     \
+    case 18: if (CLS == 2) BODY<18, 1>(__VA_ARGS__); break;                                     \
+    case 19: if (CLS == 2) BODY<19, 1>(__VA_ARGS__); break;                                     \
+    case 20: if (CLS == 2) BODY<20, 1>(__VA_ARGS__); break;                                     \
+    case 21: if (CLS == 2) BODY<21, 1>(__VA_ARGS__); break;                                     \
+    case 22: if (CLS == 2) BODY<22, 1>(__VA_ARGS__); break;                                     \
+    case 23: if (CLS == 2) BODY<23, 1>(__VA_ARGS__); break;                                     \
+    case 24: if (CLS == 2) BODY<24, 1>(__VA_ARGS__); break;                                     \
+  }
+
+template <int CLS>
+__global__ __launch_bounds__(KAON_WG) void k_pf_stats(const KaonTensor* __restrict__ D,
+                                                      const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
+                                                      int mode) {
+  extern __shared__ float lds_col[];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  zero_accumulators(T, it, ws, hp.codec);
+  const int cpl = (int)(((T.C >> 3) + 63) >> 6);
+  KAON_PF_SWITCH(CLS, pf_stats_body, T, it, ws, hp, mode, lds_col)
+}
+
+template <int CLS>
+__global__ __launch_bounds__(KAON_WG) void k_pf_ss(const KaonTensor* __restrict__ D,
+                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const int cpl = (int)(((T.C >> 3) + 63) >> 6);
+  KAON_PF_SWITCH(CLS, pf_ss_body, T, it, ws, hp)
+}
+#undef KAON_PF_SWITCH
+
 // =============================================================== phases 5/6
 // Momentum chunk load (raw codes / bits) and store.
 template <int CODEC>
@@ -414,7 +696,7 @@ __device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int 
   if (CODEC == KAON_MOM_INT8) {
     const int8_t* m = (const int8_t*)T.m + e0;
     if (vec) {
-      const uint2 v = *(const uint2*)m;
+      const ku2 v = *(const KAON_G ku2*)G(m);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         q[i] = (v.x >> (8 * i)) & 0xFFu;
@@ -451,10 +733,10 @@ __device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int 
   if (CODEC == KAON_MOM_INT8) {
     int8_t* m = (int8_t*)T.m + e0;
     if (vec) {
-      uint2 v;
+      ku2 v;
       v.x = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
       v.y = (q[4] & 0xFF) | ((q[5] & 0xFF) << 8) | ((q[6] & 0xFF) << 16) | ((q[7] & 0xFF) << 24);
-      *(uint2*)m = v;
+      *(KAON_G ku2*)G(m) = v;
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -519,7 +801,6 @@ struct RowCtx {
 template <int OPT, int PHASE, int PT, int GT, int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ float fac_s;
   __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
@@ -541,43 +822,17 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
   const WaveRows wr = wave_rows(it);
 
-  // clip divisor: phase 5 computes it from the row sums (canonical sum over
-  // the rows) and publishes it for phase 6
-  float fac = 1.0f;
-  if (OPT == KAON_OPT_ADAKAON) {
-    if (PHASE == 5) {
-      if (wr.w == 0) {
-        const int64_t R = T.R;
-        const int64_t nchr = (R + 7) >> 3;
-        const float* rs = ws.rs(T);
-        float a = 0.0f;
-        for (int64_t c = wr.lane; c < nchr; c += 64)
-          for (int i = 0; i < 8; ++i) {
-            const int64_t j = c * 8 + i;
-            if (j < R) a = a + rs[j];
-          }
-        const float ss = wave_csum(a);
-        if (wr.lane == 0) {
-          const float f = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
-          fac_s = f;
-          if (it.row0 == 0) ws.scal(T)[0] = f;
-        }
-      }
-      __syncthreads();
-      fac = fac_s;
-    } else {
-      fac = ws.scal(T)[0];
-    }
-  }
+  // clip divisor of the tensor (phase 4)
+  const float fac = OPT == KAON_OPT_ADAKAON ? ws.scal(T)[0] : 1.0f;
   const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && cautious) {
-    const uint32_t cnt = ((const uint32_t*)ws.scal(T))[1];
+    const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
     rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
   // 4-bit fast path: blocks inside rows, a block = G consecutive chunks = G lanes
-  const int64_t G = CODEC == KAON_MOM_4BIT && B >= 8 ? B / 8 : 1;
-  const bool blk_fast = CODEC == KAON_MOM_4BIT && B % 8 == 0 && C % B == 0 && G <= 64 && (64 % G) == 0 && vec_t;
+  const int64_t GL = CODEC == KAON_MOM_4BIT && B >= 8 ? B / 8 : 1;
+  const bool blk_fast = CODEC == KAON_MOM_4BIT && B % 8 == 0 && C % B == 0 && GL <= 64 && (64 % GL) == 0 && vec_t;
   uint32_t keep = 0;
 
   for (int64_t r = wr.rb; r < wr.re; ++r) {
@@ -632,7 +887,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
 #pragma unroll
         for (int i = 0; i < 8; ++i) mq[i] = CODEC == KAON_MOM_4BIT ? 8u : 0u;
       if (OPT == KAON_OPT_ADAKAON && cnt > 0) {
-        if (factored) ld8<KAON_F32>(ws.cf(T), j0, cnt, vec, f);
+        if (factored) ld8<KAON_F32>((const float*)ws.cf(T), j0, cnt, vec, f);
         else ld8<KAON_F32>(T.v, j0, cnt, vec, f);
       } else {
 #pragma unroll
@@ -752,7 +1007,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
           if (quant) {
             const float ax = fabsf(mfv);
             if (CODEC == KAON_MOM_4BIT && !blk_fast) {
-              if (ax == ax) atomicMax(&ws.bamax(T)[blk_e], __float_as_uint(ax));
+              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk_e], __float_as_uint(ax));
               if (e == blk_e * B) ws.boldsc(T, nb)[blk_e] = sc4_old;
             } else {
               chunk_amax = fmaxf(chunk_amax, ax);
@@ -792,8 +1047,8 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
           } else {
             // blocks of G lanes: reduce within the lane group, its first lane stores
             float a = chunk_amax;
-            for (int o = (int)G / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-            if (cnt > 0 && (wr.lane % G) == 0) {
+            for (int o = (int)GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+            if (cnt > 0 && (wr.lane % GL) == 0) {
               ws.bamax(T)[blk] = __float_as_uint(a);
               ws.boldsc(T, nb)[blk] = b_old;
             }
@@ -803,7 +1058,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       }
       if (cnt <= 0) continue;
       // ---------------- phase 6 writes
-      if (CODEC == KAON_MOM_4BIT && mom && blk_fast && (wr.lane % G) == 0) T.m_scale[blk] = b_new;
+      if (CODEC == KAON_MOM_4BIT && mom && blk_fast && (wr.lane % GL) == 0) G(T.m_scale)[blk] = b_new;
       if (mom) st_mom_raw<CODEC>(T, e0, cnt, vec, qout);
       if (PT == KAON_F32) {
         float o[8];
@@ -864,7 +1119,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
     __syncthreads();
     if (threadIdx.x == 0) {
       const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
-      if (tot) atomicAdd(&((uint32_t*)ws.scal(T))[1], tot);
+      if (tot) atomicAdd(ws.keep_ctr(T), tot);
     }
   }
 }
@@ -876,13 +1131,6 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
 // generic per-element route.  FLAGS: bit 0 GC, 1 cautious, 2 weight decay,
 // 3 Nekaon removal, 4 Nekaon climb.
 enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16 };
-
-__device__ __forceinline__ void unpack_bf16x8(const uint4 v, float o[8]) {
-  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
-  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
-  o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xFFFF0000u);
-  o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xFFFF0000u);
-}
 
 // int8 requant code (as the stored byte) of mf with r = RN64(1/scale)
 __device__ __forceinline__ uint32_t q_int8(float mf, double r, float& xq) {
@@ -898,25 +1146,25 @@ template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX>
 __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, int64_t r,
                                            int64_t e0, int64_t j0, float mu, float rf, float oldsc, float m128,
                                            float newsc, double rnew, double rfac, double rden, int64_t B,
-                                           int64_t nb, int G, int lane, uint32_t& keep, float& amax,
-                                           const float* cfrow) {
+                                           int64_t nb, int GL, int lane, uint32_t& keep, float& amax,
+                                           const KAON_G float* cfrow) {
   constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
   constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
   constexpr bool MOM = CODEC != KAON_MOM_NONE;
   constexpr bool NEEDP = PHASE == 6 || WD;
-  const uint4 gv4 = *(const uint4*)((const uint16_t*)T.g + e0);
-  uint4 pv4 = make_uint4(0, 0, 0, 0);
-  if (NEEDP) pv4 = *(const uint4*)((const uint16_t*)T.p + e0);
-  uint2 mi8 = make_uint2(0, 0);
+  const ku4 gv4 = *(const KAON_G ku4*)G((const uint16_t*)T.g + e0);
+  ku4 pv4 = ku4{0u, 0u, 0u, 0u};
+  if (NEEDP) pv4 = *(const KAON_G ku4*)G((const uint16_t*)T.p + e0);
+  ku2 mi8 = ku2{0u, 0u};
   uint32_t m4 = 0;
-  uint4 mb16 = make_uint4(0, 0, 0, 0);
-  if (CODEC == KAON_MOM_INT8) mi8 = *(const uint2*)((const int8_t*)T.m + e0);
-  if (CODEC == KAON_MOM_4BIT) m4 = *(const uint32_t*)((const uint8_t*)T.m + (e0 >> 1));
-  if (CODEC == KAON_MOM_BF16) mb16 = *(const uint4*)((const uint16_t*)T.m + e0);
+  ku4 mb16 = ku4{0u, 0u, 0u, 0u};
+  if (CODEC == KAON_MOM_INT8) mi8 = *(const KAON_G ku2*)G((const int8_t*)T.m + e0);
+  if (CODEC == KAON_MOM_4BIT) m4 = *(const KAON_G uint32_t*)G((const uint8_t*)T.m + (e0 >> 1));
+  if (CODEC == KAON_MOM_BF16) mb16 = *(const KAON_G ku4*)G((const uint16_t*)T.m + e0);
   float f[8];
   if (OPT == KAON_OPT_ADAKAON) {
-    const float* cfp = cfrow + j0;
-    const float4 c0 = *(const float4*)cfp, c1 = *(const float4*)(cfp + 4);
+    const KAON_G float* cfp = cfrow + j0;
+    const kf4 c0 = *(const KAON_G kf4*)cfp, c1 = *(const KAON_G kf4*)(cfp + 4);
     f[0] = c0.x; f[1] = c0.y; f[2] = c0.z; f[3] = c0.w; f[4] = c1.x; f[5] = c1.y; f[6] = c1.z; f[7] = c1.w;
   }
   // 4-bit: one block per chunk
@@ -925,15 +1173,15 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
   int64_t blk = 0;
   if (CODEC == KAON_MOM_4BIT) {
     blk = e0 / B;
-    b_old = PHASE == 5 ? T.m_scale[blk] : ws.boldsc(T, nb)[blk];
+    b_old = PHASE == 5 ? G(T.m_scale)[blk] : ws.boldsc(T, nb)[blk];
     if (PHASE == 6) {
       b_new = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
       b_r = rcp64(b_new);
     }
   }
   float g[8], p[8];
-  unpack_bf16x8(gv4, g);
-  if (NEEDP) unpack_bf16x8(pv4, p);
+  unpack8(gv4, g);
+  if (NEEDP) unpack8(pv4, p);
   if (GC) {
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
@@ -1033,30 +1281,30 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
     o[i] = sr_bf16(p[i] - dd, nz1[i]);
     if (NKC) o[i] = sr_bf16(bf2f(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
   }
-  uint4 ov;
+  ku4 ov;
   ov.x = o[0] | (o[1] << 16);
   ov.y = o[2] | (o[3] << 16);
   ov.z = o[4] | (o[5] << 16);
   ov.w = o[6] | (o[7] << 16);
-  *(uint4*)((uint16_t*)T.p + e0) = ov;
+  *(KAON_G ku4*)G((uint16_t*)T.p + e0) = ov;
   if (CODEC == KAON_MOM_INT8) {
-    uint2 mv;
+    ku2 mv;
     mv.x = codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
     mv.y = codes[4] | (codes[5] << 8) | (codes[6] << 16) | (codes[7] << 24);
-    *(uint2*)((int8_t*)T.m + e0) = mv;
+    *(KAON_G ku2*)G((int8_t*)T.m + e0) = mv;
   } else if (CODEC == KAON_MOM_4BIT) {
     uint32_t v = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
-    *(uint32_t*)((uint8_t*)T.m + (e0 >> 1)) = v;
-    if ((lane % G) == 0) T.m_scale[blk] = b_new;
+    *(KAON_G uint32_t*)G((uint8_t*)T.m + (e0 >> 1)) = v;
+    if ((lane % GL) == 0) G(T.m_scale)[blk] = b_new;
   } else if (CODEC == KAON_MOM_BF16) {
-    uint4 mv;
+    ku4 mv;
     mv.x = mbits[0] | (mbits[1] << 16);
     mv.y = mbits[2] | (mbits[3] << 16);
     mv.z = mbits[4] | (mbits[5] << 16);
     mv.w = mbits[6] | (mbits[7] << 16);
-    *(uint4*)((uint16_t*)T.m + e0) = mv;
+    *(KAON_G ku4*)G((uint16_t*)T.m + e0) = mv;
   }
 }
 
@@ -1068,7 +1316,6 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   constexpr bool CAUT = FLAGS & FF_CAUT;
   constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
-  __shared__ float fac_s;
   __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
@@ -1078,41 +1325,17 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   const WaveRows wr = wave_rows(it);
   const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 8;
   const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
-  const int G = CODEC == KAON_MOM_4BIT ? (int)(B / 8) : 1;
+  const int GL = CODEC == KAON_MOM_4BIT ? (int)(B / 8) : 1;
 
-  float fac = 1.0f;
-  if (OPT == KAON_OPT_ADAKAON) {
-    if (PHASE == 5) {
-      if (wr.w == 0) {
-        const int64_t R = T.R;
-        const int64_t nchr = (R + 7) >> 3;
-        const float* rs = ws.rs(T);
-        float a = 0.0f;
-        for (int64_t c = wr.lane; c < nchr; c += 64)
-          for (int i = 0; i < 8; ++i) {
-            const int64_t j = c * 8 + i;
-            if (j < R) a = a + rs[j];
-          }
-        const float ss = wave_csum(a);
-        if (wr.lane == 0) {
-          const float fv = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
-          fac_s = fv;
-          if (it.row0 == 0) ws.scal(T)[0] = fv;
-        }
-      }
-      __syncthreads();
-      fac = fac_s;
-    } else {
-      fac = ws.scal(T)[0];
-    }
-  }
+  // clip divisor of the tensor (phase 4)
+  const float fac = OPT == KAON_OPT_ADAKAON ? ws.scal(T)[0] : 1.0f;
   const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && CAUT) {
-    const uint32_t cnt = ((const uint32_t*)ws.scal(T))[1];
+    const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
     rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
-  const float* cfrow = ws.cf(T);
+  const KAON_G float* cfrow = ws.cf(T);
   uint32_t keep = 0;
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = (FLAGS & FF_GC) ? uniform_f(ws.mu(T)[r]) : 0.0f;
@@ -1120,7 +1343,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     float oldsc = 1.0f, newsc = 1.0f;
     double rnew = 1.0;
     if (CODEC == KAON_MOM_INT8) {
-      oldsc = uniform_f(PHASE == 5 ? T.m_scale[r] : ws.roldsc(T)[r]);
+      oldsc = uniform_f(PHASE == 5 ? G(T.m_scale)[r] : ws.roldsc(T)[r]);
       if (PHASE == 6) {
         newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
         rnew = rcp64(newsc);
@@ -1139,24 +1362,24 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
         const int64_t e0 = r * C + j0;
         if (fac == 1.0f && dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                            rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+                                                            rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
         else if (dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                             rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+                                                             rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
         else
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                            rfac, rden, B, nb, G, wr.lane, keep, camax, cfrow);
+                                                            rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
       }
       if (PHASE == 5 && QUANT) {
         if (CODEC == KAON_MOM_INT8) {
           amax = fmaxf(amax, camax);
         } else {
           float a = camax;
-          for (int o = G / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-          if (full && (wr.lane % G) == 0) {
+          for (int o = GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+          if (full && (wr.lane % GL) == 0) {
             const int64_t blk = (r * C + c * 8) / B;
             ws.bamax(T)[blk] = __float_as_uint(a);
-            ws.boldsc(T, nb)[blk] = T.m_scale[blk];
+            ws.boldsc(T, nb)[blk] = G(T.m_scale)[blk];
           }
         }
       }
@@ -1169,7 +1392,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
           ws.roldsc(T)[r] = oldsc;
         }
       } else if (wr.lane == 0) {
-        T.m_scale[r] = newsc;
+        G(T.m_scale)[r] = newsc;
       }
     }
   }
@@ -1179,7 +1402,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     __syncthreads();
     if (threadIdx.x == 0) {
       const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
-      if (tot) atomicAdd(&((uint32_t*)ws.scal(T))[1], tot);
+      if (tot) atomicAdd(ws.keep_ctr(T), tot);
     }
   }
 }
@@ -1412,17 +1635,22 @@ int launch_elem(const KaonLaunch& L, Ws ws, const KaonHyper& h, int codec, hipSt
 }
 
 using StatsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int);
-// register classes of the row kernels: rows of <= 4, 10, 24 chunks per lane,
-// and the streaming kernel; dynamic LDS holds one slice column partial
-constexpr int kClassMaxC[4] = {4 * 512, 10 * 512, 24 * 512, KAON_MAX_ROW};
+// row classes (slices are sorted by class): 0-2 prefetching kernels, 3-5 rows
+// of <= 4, 10, 24 chunks per lane in registers, 6 streamed rows; dynamic LDS
+// holds one slice column partial
+constexpr int kClassMaxC[KAON_ROW_CLASSES] = {4 * 512, 10 * 512, 24 * 512, 4 * 512, 10 * 512, 24 * 512,
+                                              KAON_MAX_ROW};
 
 template <int GT>
 StatsFn stats_fn_gt(int cls) {
   switch (cls) {
-    case 0: return k_stats<GT, 4>;
-    case 1: return k_stats<GT, 10>;
-    case 2: return k_stats<GT, 24>;
-    case 3: return k_stats<GT, 0>;
+    case 0: return k_pf_stats<0>;
+    case 1: return k_pf_stats<1>;
+    case 2: return k_pf_stats<2>;
+    case 3: return k_stats<GT, 4>;
+    case 4: return k_stats<GT, 10>;
+    case 5: return k_stats<GT, 24>;
+    case 6: return k_stats<GT, 0>;
   }
   return nullptr;
 }
@@ -1449,9 +1677,10 @@ MsamFn msam_fn(int pt, int codec) {
 // Phase-1 launches, one per register class run (slices are sorted by class).
 int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipStream_t st) {
   int32_t off = 0;
-  for (int cls = 0; cls < 4; ++cls) {
+  for (int cls = 0; cls < KAON_ROW_CLASSES; ++cls) {
     const int32_t cnt = L.row_runs[cls];
     if (cnt <= 0) continue;
+    if (cls < 3 && hp.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
     StatsFn fn = stats_fn(hp.g_dtype, cls);
     const size_t lds = mode == 0 ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
     hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);
@@ -1499,12 +1728,27 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
     if ((rc = check_launch("kaon: k_fin launch"))) return rc;
   }
   if (mask & (1u << 3)) {
-    hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3(L->n_row_items), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws,
-                       h);
+    // prefetching kernels over row classes 0-2, k_ss over the rest
+    int32_t off = 0;
+    for (int cls = 0; cls < 3; ++cls) {
+      const int32_t cnt = L->row_runs[cls];
+      if (cnt <= 0) continue;
+      if (h.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
+      SsFn fn = cls == 0 ? (SsFn)k_pf_ss<0> : cls == 1 ? (SsFn)k_pf_ss<1> : (SsFn)k_pf_ss<2>;
+      hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), 0, st, L->descs, L->row_items + off, ws, h);
+      off += cnt;
+    }
+    if (L->n_row_items > off)
+      hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3(L->n_row_items - off), dim3(KAON_WG), 0, st, L->descs,
+                         L->row_items + off, ws, h);
     if ((rc = check_launch("kaon: k_ss launch"))) return rc;
   }
-  // phase 5 always runs for Adakaon: it also publishes the clip divisor
-  if (mask & (1u << 5)) {
+  if (mask & (1u << 4)) {
+    hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, h);
+    if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
+  }
+  const bool quant = codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT;
+  if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {
     if ((rc = launch_elem<KAON_OPT_ADAKAON, 5>(*L, ws, h, codec, st))) return rc;
   }
   if (mask & (1u << 6)) {
@@ -1514,7 +1758,7 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
 }
 
 int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
-  return kaon_adakaon_phases(L, hp, 0x6Eu, stream);
+  return kaon_adakaon_phases(L, hp, 0x7Eu, stream);
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {

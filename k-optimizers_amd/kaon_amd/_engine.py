@@ -91,7 +91,7 @@ class Plan:
         la.descs, la.row_items, la.elem_items, la.fin_items, la.flat_items = (base + o for o in offs)
         la.n_tensors, la.n_row_items = n, info.n_row_items
         la.n_fin_items, la.n_flat_items = info.n_fin_items, info.n_flat_items
-        for k in range(4):
+        for k in range(L.ROW_CLASSES):
             la.row_runs[k] = info.row_runs[k]
         la.n_fast = info.n_fast
         la.workspace = self.workspace.data_ptr()

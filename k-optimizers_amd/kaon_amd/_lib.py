@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -24,6 +24,7 @@ OPT_ADAKAON, OPT_LION, OPT_ADAMUON = 0, 1, 2
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB = 1, 2, 4, 8, 16, 32, 64
 
 ROW_BUDGET = 20
+ROW_CLASSES = 7
 COLITEM = 2048
 FLAT_ITEM = 16384
 MAX_ROW = 16384
@@ -52,7 +53,7 @@ class KaonItem(ctypes.Structure):
 class KaonPlanInfo(ctypes.Structure):
     _fields_ = [("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
-                ("row_runs", ctypes.c_int32 * 4), ("n_fast", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("ws_words", ctypes.c_int64)]
 
 
@@ -66,7 +67,7 @@ class KaonLaunch(ctypes.Structure):
                 ("fin_items", ctypes.c_void_p), ("flat_items", ctypes.c_void_p),
                 ("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
-                ("row_runs", ctypes.c_int32 * 4), ("n_fast", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("workspace", ctypes.c_void_p)]
 
 

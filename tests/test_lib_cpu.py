@@ -112,7 +112,7 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
     # rows-per-wave of the oracle's column-sum order
     seen = {i: np.zeros(descs[i].R, np.int32) for i in range(len(shapes))}
     off = 0
-    for cls in range(4):
+    for cls in range(L.ROW_CLASSES):
         for k in range(info.row_runs[cls]):
             it = rows[off + k]
             d = descs[it.tensor]
@@ -120,10 +120,13 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
             assert it.kind == O.rows_per_wave(d.C)
             assert it.nrows <= 4 * it.kind and it.row0 % (4 * it.kind) == 0
             cpl = _cpl(d.C)
+            prefetch = g_dtype == 1 and d.factored and d.vec_rows and d.C % 8 == 0 and cpl <= 24
             if not d.factored:
-                assert cls == 3
-            elif cls < 3:
-                assert cpl <= (4, 10, 24)[cls] and (cls < 2 or g_dtype == 1)
+                assert cls == 6
+            elif prefetch:
+                assert cls == (0 if cpl <= 4 else 1 if cpl <= 10 else 2)
+            elif cls < 6:
+                assert 3 <= cls and cpl <= (4, 10, 24)[cls - 3] and (cls < 5 or g_dtype == 1)
             else:
                 assert cpl > 24 or (cpl > 10 and g_dtype == 0)
         off += info.row_runs[cls]

@@ -453,16 +453,13 @@ __device__ __forceinline__ void unpack8(const ku4 v, float o[8]) {
   o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
-// Marks packed registers as rewritten (no instruction is emitted), so values
-// derived from them are computed after this point, not hoisted above it or
-// reused from before it.
-template <int CPL, int RW>
-__device__ __forceinline__ void launder(ku4 (&raw)[RW][CPL]) {
-#pragma unroll
-  for (int j = 0; j < RW; ++j)
-#pragma unroll
-    for (int k = 0; k < CPL; ++k)
-      asm volatile("" : "+v"(raw[j][k].x), "+v"(raw[j][k].y), "+v"(raw[j][k].z), "+v"(raw[j][k].w));
+// Per-row values of a wave group: lane j (< nrows) loads row rb + j's value,
+// issued with the chunk loads; lane_val(v, j) hands row j's value to the wave.
+__device__ __forceinline__ int64_t lane_row(int64_t rb, int nrows, int lane) {
+  return rb + (lane < nrows ? lane : 0);
+}
+__device__ __forceinline__ float lane_val(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
 template <int CPL, int RW>
@@ -478,8 +475,9 @@ __device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64
     }
 }
 
-// q = (G - mu)^2 + e1 of one chunk, G - mu rounded to bf16 (GC in the grad
-// dtype); e1 = eps1, or 0 without eps (a square plus +0 is the square itself)
+// q = (G - mu)^2 (+ eps1 with EPS) of one chunk, G - mu rounded to bf16 (GC
+// in the grad dtype)
+template <bool EPS>
 __device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e1, float q[8]) {
   float x[8];
   unpack8(v, x);
@@ -493,95 +491,101 @@ __device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = x[i] * x[i] + e1;
+  for (int i = 0; i < 8; ++i) q[i] = EPS ? x[i] * x[i] + e1 : x[i] * x[i];
 }
 
-template <int CPL, int RW>
+// Column partial of a slice, segment by segment: segment k is chunk k of
+// every lane (columns 512k .. 512k+511).  Each wave writes its wave group's
+// partial for the segment into its LDS slot, and after one barrier every
+// thread forms the ordered sum ((w0 + w1) + w2) + w3 of two columns and
+// stores it (two LDS buffers alternate, so one barrier per segment suffices).
+__device__ __forceinline__ void seg_put(float (*seg)[512], int w, int lane, const float v[8]) {
+  kf4* d = (kf4*)(&seg[w][lane * 8]);
+  d[0] = kf4{v[0], v[1], v[2], v[3]};
+  d[1] = kf4{v[4], v[5], v[6], v[7]};
+}
+__device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0, int64_t C, KAON_G float* part) {
+  const int c = 2 * (int)threadIdx.x;
+  if (col0 + c >= C) return;  // C % 8 == 0: both columns are in range or neither
+  float a0 = seg[0][c], a1 = seg[0][c + 1];
+  for (int w = 1; w < nw; ++w) {
+    a0 = a0 + seg[w][c];
+    a1 = a1 + seg[w][c + 1];
+  }
+  *(KAON_G ku2*)(part + col0 + c) = ku2{__float_as_uint(a0), __float_as_uint(a1)};
+}
+
+template <int CPL, int RW, bool EPS>
 __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
-                                              const KaonHyper& hp, int mode, float* lds_col) {
+                                              const KaonHyper& hp, int mode, float (*seg)[4][512]) {
   const int64_t C = T.C;
   const int nch = (int)(C >> 3);
   const WaveRows wr = wave_rows(it);
   const int nrows = (int)(wr.re - wr.rb);
   const bool gc = (hp.flags & KAON_F_GC) != 0;
-  const float e1 = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
-  if (mode == 1 && !gc) return;
+  const float e1 = hp.eps1;
+  if (mode == 1 && (!gc || nrows <= 0)) return;
+  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
+  const float row_old = (mode == 0 && nrows > 0) ? G(T.row)[rl] : 0.0f;
   ku4 raw[RW][CPL];
   load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
+  // GC means of the wave's rows
   float mu[RW];
   KAON_G float* mu_arr = ws.mu(T);
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
     mu[j] = 0.0f;
-    if (j >= nrows) continue;
-    const int64_t r = wr.rb + j;
-    if (gc) {
-      float a = 0.0f;
-#pragma unroll
-      for (int k = 0; k < CPL; ++k) {
-        if (wr.lane + 64 * k < nch) {
-          float x[8];
-          unpack8(raw[j][k], x);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) a = a + x[i];
-        }
-      }
-      mu[j] = rbf(wave_csum(a) / (float)C);
-      if (wr.lane == 0) mu_arr[r] = mu[j];
-    }
-    if (mode == 1) continue;
-    float a2 = 0.0f;
+    if (j >= nrows || !gc) continue;
+    float a = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       if (wr.lane + 64 * k < nch) {
-        float q[8];
-        sq_chunk(raw[j][k], mu[j], gc, e1, q);
+        float x[8];
+        unpack8(raw[j][k], x);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a2 = a2 + q[i];
+        for (int i = 0; i < 8; ++i) a = a + x[i];
       }
     }
-    const float s2 = wave_csum(a2);
-    if (wr.lane == 0) G(T.row)[r] = klerp(G(T.row)[r], s2 / (float)C, hp.w2);
+    mu[j] = rbf(wave_csum(a) / (float)C);
+    if (wr.lane == 0) mu_arr[wr.rb + j] = mu[j];
   }
   if (mode == 1) return;
-  // column partial of the slice: each wave group's rows summed in row order,
-  // then the groups folded in order through LDS.  The launder keeps the
-  // compiler from hoisting the partial (CPL x 8 values) out of the loop.
-#pragma unroll 1
-  for (int wf = 0; wf < 4; ++wf) {
-    if (wr.w == wf && nrows > 0) {
-      launder<CPL, RW>(raw);
+  // q = (G - mu)^2 (+eps1) once per element: into the row sums (lane order:
+  // chunk by chunk) and the wave group's column partial (row order)
+  const int nw = (int)min<int64_t>(4, ((int64_t)it.nrows + RW - 1) / RW);
+  KAON_G float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
+  float a2[RW];
 #pragma unroll
-      for (int k = 0; k < CPL; ++k) {
-        const int c = wr.lane + 64 * k;
-        if (c < nch) {
-          float v[8];
-          sq_chunk(raw[0][k], mu[0], gc, e1, v);
+  for (int j = 0; j < RW; ++j) a2[j] = 0.0f;
 #pragma unroll
-          for (int j = 1; j < RW; ++j) {
-            if (j < nrows) {
-              float q[8];
-              sq_chunk(raw[j][k], mu[j], gc, e1, q);
+  for (int k = 0; k < CPL; ++k) {
+    if (nrows > 0) {
+      float v[8];
+      const bool in = wr.lane + 64 * k < nch;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = v[i] + q[i];
-            }
+      for (int j = 0; j < RW; ++j) {
+        if (j < nrows) {
+          float q[8];
+          sq_chunk<EPS>(raw[j][k], mu[j], gc, e1, q);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (in) a2[j] = a2[j] + q[i];
+            v[i] = j == 0 ? q[i] : v[i] + q[i];
           }
-          float4* l4 = (float4*)(lds_col + (int64_t)c * 8);
-          if (wf > 0) {
-            const float4 o0 = l4[0], o1 = l4[1];
-            v[0] = o0.x + v[0]; v[1] = o0.y + v[1]; v[2] = o0.z + v[2]; v[3] = o0.w + v[3];
-            v[4] = o1.x + v[4]; v[5] = o1.y + v[5]; v[6] = o1.z + v[6]; v[7] = o1.w + v[7];
-          }
-          l4[0] = make_float4(v[0], v[1], v[2], v[3]);
-          l4[1] = make_float4(v[4], v[5], v[6], v[7]);
         }
       }
+      seg_put(seg[k & 1], wr.w, wr.lane, v);
     }
     __syncthreads();
+    seg_fold(seg[k & 1], nw, (int64_t)k * 512, C, part);
   }
-  KAON_G kf4* part = (KAON_G kf4*)(ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C);
-  const kf4* l4 = (const kf4*)lds_col;
-  for (int64_t j = threadIdx.x; j < (C >> 2); j += KAON_WG) part[j] = l4[j];
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    if (j >= nrows) continue;
+    const float s2 = wave_csum(a2[j]);
+    const float rv = lane_val(row_old, j);
+    if (wr.lane == 0) G(T.row)[wr.rb + j] = klerp(rv, s2 / (float)C, hp.w2);
+  }
 }
 
 template <int CPL, int RW>
@@ -593,19 +597,16 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
   const int nrows = (int)(wr.re - wr.rb);
   if (nrows <= 0) return;
   const bool gc = (hp.flags & KAON_F_GC) != 0;
-  float mu[RW], rf[RW];
-#pragma unroll
-  for (int j = 0; j < RW; ++j) {
-    const int64_t r = j < nrows ? wr.rb + j : wr.rb;
-    mu[j] = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    rf[j] = uniform_f(ws.rf(T)[r]);
-  }
+  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
+  const float mu_l = gc ? ws.mu(T)[rl] : 0.0f;
+  const float rf_l = ws.rf(T)[rl];
   ku4 raw[RW][CPL];
   load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
   const KAON_G float* cf = ws.cf(T);
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
     if (j >= nrows) continue;
+    const float muj = lane_val(mu_l, j), rfj = lane_val(rf_l, j);
     float a = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
@@ -618,7 +619,7 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
         if (gc) {
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            float a0 = x[i] - mu[j], a1 = x[i + 1] - mu[j];
+            float a0 = x[i] - muj, a1 = x[i + 1] - muj;
             rbf2(a0, a1);
             x[i] = a0;
             x[i + 1] = a1;
@@ -626,7 +627,7 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float u = (x[i] * rf[j]) * f[i];
+          const float u = (x[i] * rfj) * f[i];
           a = a + u * u;
         }
       }
@@ -639,44 +640,45 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
 // Row class 0: 1-4 chunks per lane, 1 class 1: 5-10, class 2: 11-24; the
 // body is specialized on the exact chunks per lane and its rows per wave
 // group (RW = max(1, KAON_ROW_BUDGET / CPL)).
-#define KAON_PF_SWITCH(CLS, BODY, ...)                                                         \
+#define KAON_COMMA ,
+#define KAON_PF_SWITCH(CLS, BODY, X, ...)                                                      \
   switch (cpl) {                                                                                \
-    case 1: if (CLS == 0) BODY<1, 20>(__VA_ARGS__); break;                                      \
-    case 2: if (CLS == 0) BODY<2, 10>(__VA_ARGS__); break;                                      \
-    case 3: if (CLS == 0) BODY<3, 6>(__VA_ARGS__); break;                                       \
-    case 4: if (CLS == 0) BODY<4, 5>(__VA_ARGS__); break;                                       \
-    case 5: if (CLS == 1) BODY<5, 4>(__VA_ARGS__); break;                                       \
-    case 6: if (CLS == 1) BODY<6, 3>(__VA_ARGS__); break;                                       \
-    case 7: if (CLS == 1) BODY<7, 2>(__VA_ARGS__); break;                                       \
-    case 8: if (CLS == 1) BODY<8, 2>(__VA_ARGS__); break;                                       \
-    case 9: if (CLS == 1) BODY<9, 2>(__VA_ARGS__); break;                                       \
-    case 10: if (CLS == 1) BODY<10, 2>(__VA_ARGS__); break;                                     \
-    case 11: if (CLS == 2) BODY<11, 1>(__VA_ARGS__); break;                                     \
-    case 12: if (CLS == 2) BODY<12, 1>(__VA_ARGS__); break;                                     \
-    case 13: if (CLS == 2) BODY<13, 1>(__VA_ARGS__); break;                                     \
-    case 14: if (CLS == 2) BODY<14, 1>(__VA_ARGS__); break;                                     \
-    case 15: if (CLS == 2) BODY<15, 1>(__VA_ARGS__); break;                                     \
-    case 16: if (CLS == 2) BODY<16, 1>(__VA_ARGS__); break;                                     \
-    case 17: if (CLS == 2) BODY<17, 1>(__VA_ARGS__); break;                                     \
-    case 18: if (CLS == 2) BODY<18, 1>(__VA_ARGS__); break;                                     \
-    case 19: if (CLS == 2) BODY<19, 1>(__VA_ARGS__); break;                                     \
-    case 20: if (CLS == 2) BODY<20, 1>(__VA_ARGS__); break;                                     \
-    case 21: if (CLS == 2) BODY<21, 1>(__VA_ARGS__); break;                                     \
-    case 22: if (CLS == 2) BODY<22, 1>(__VA_ARGS__); break;                                     \
-    case 23: if (CLS == 2) BODY<23, 1>(__VA_ARGS__); break;                                     \
-    case 24: if (CLS == 2) BODY<24, 1>(__VA_ARGS__); break;                                     \
+    case 1: if (CLS == 0) BODY<1, 20 X>(__VA_ARGS__); break;                                   \
+    case 2: if (CLS == 0) BODY<2, 10 X>(__VA_ARGS__); break;                                   \
+    case 3: if (CLS == 0) BODY<3, 6 X>(__VA_ARGS__); break;                                    \
+    case 4: if (CLS == 0) BODY<4, 5 X>(__VA_ARGS__); break;                                    \
+    case 5: if (CLS == 1) BODY<5, 4 X>(__VA_ARGS__); break;                                    \
+    case 6: if (CLS == 1) BODY<6, 3 X>(__VA_ARGS__); break;                                    \
+    case 7: if (CLS == 1) BODY<7, 2 X>(__VA_ARGS__); break;                                    \
+    case 8: if (CLS == 1) BODY<8, 2 X>(__VA_ARGS__); break;                                    \
+    case 9: if (CLS == 1) BODY<9, 2 X>(__VA_ARGS__); break;                                    \
+    case 10: if (CLS == 1) BODY<10, 2 X>(__VA_ARGS__); break;                                  \
+    case 11: if (CLS == 2) BODY<11, 1 X>(__VA_ARGS__); break;                                  \
+    case 12: if (CLS == 2) BODY<12, 1 X>(__VA_ARGS__); break;                                  \
+    case 13: if (CLS == 2) BODY<13, 1 X>(__VA_ARGS__); break;                                  \
+    case 14: if (CLS == 2) BODY<14, 1 X>(__VA_ARGS__); break;                                  \
+    case 15: if (CLS == 2) BODY<15, 1 X>(__VA_ARGS__); break;                                  \
+    case 16: if (CLS == 2) BODY<16, 1 X>(__VA_ARGS__); break;                                  \
+    case 17: if (CLS == 2) BODY<17, 1 X>(__VA_ARGS__); break;                                  \
+    case 18: if (CLS == 2) BODY<18, 1 X>(__VA_ARGS__); break;                                  \
+    case 19: if (CLS == 2) BODY<19, 1 X>(__VA_ARGS__); break;                                  \
+    case 20: if (CLS == 2) BODY<20, 1 X>(__VA_ARGS__); break;                                  \
+    case 21: if (CLS == 2) BODY<21, 1 X>(__VA_ARGS__); break;                                  \
+    case 22: if (CLS == 2) BODY<22, 1 X>(__VA_ARGS__); break;                                  \
+    case 23: if (CLS == 2) BODY<23, 1 X>(__VA_ARGS__); break;                                  \
+    case 24: if (CLS == 2) BODY<24, 1 X>(__VA_ARGS__); break;                                  \
   }
 
-template <int CLS>
+template <int CLS, bool EPS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_stats(const KaonTensor* __restrict__ D,
                                                       const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                       int mode) {
-  extern __shared__ float lds_col[];
+  __shared__ __attribute__((aligned(16))) float seg[2][4][512];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   zero_accumulators(T, it, ws, hp.codec);
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
-  KAON_PF_SWITCH(CLS, pf_stats_body, T, it, ws, hp, mode, lds_col)
+  KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS, T, it, ws, hp, mode, seg)
 }
 
 template <int CLS>
@@ -685,9 +687,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pf_ss(const KaonTensor* __restrict_
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
-  KAON_PF_SWITCH(CLS, pf_ss_body, T, it, ws, hp)
+  KAON_PF_SWITCH(CLS, pf_ss_body, , T, it, ws, hp)
 }
 #undef KAON_PF_SWITCH
+#undef KAON_COMMA
 
 // =============================================================== phases 5/6
 // Momentum chunk load (raw codes / bits) and store.
@@ -1337,15 +1340,23 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   }
   const KAON_G float* cfrow = ws.cf(T);
   uint32_t keep = 0;
+  // per-row values of the wave's rows, one row per lane
+  const int nrows = (int)(wr.re - wr.rb);
+  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
+  const float mu_l = (FLAGS & FF_GC) && nrows > 0 ? ws.mu(T)[rl] : 0.0f;
+  const float rf_l = OPT == KAON_OPT_ADAKAON && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
+  const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0 ? (PHASE == 5 ? G(T.m_scale)[rl] : ws.roldsc(T)[rl]) : 1.0f;
+  const float am_l = CODEC == KAON_MOM_INT8 && PHASE == 6 && nrows > 0 ? __uint_as_float(ws.ramax(T)[rl]) : 0.0f;
   for (int64_t r = wr.rb; r < wr.re; ++r) {
-    const float mu = (FLAGS & FF_GC) ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    const float rf = OPT == KAON_OPT_ADAKAON ? uniform_f(ws.rf(T)[r]) : 1.0f;
+    const int j = (int)(r - wr.rb);
+    const float mu = (FLAGS & FF_GC) ? lane_val(mu_l, j) : 0.0f;
+    const float rf = OPT == KAON_OPT_ADAKAON ? lane_val(rf_l, j) : 1.0f;
     float oldsc = 1.0f, newsc = 1.0f;
     double rnew = 1.0;
     if (CODEC == KAON_MOM_INT8) {
-      oldsc = uniform_f(PHASE == 5 ? G(T.m_scale)[r] : ws.roldsc(T)[r]);
+      oldsc = lane_val(sc_l, j);
       if (PHASE == 6) {
-        newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+        newsc = fmaxf(lane_val(am_l, j), 1e-12f) / 127.0f;
         rnew = rcp64(newsc);
       }
     }
@@ -1642,11 +1653,11 @@ constexpr int kClassMaxC[KAON_ROW_CLASSES] = {4 * 512, 10 * 512, 24 * 512, 4 * 5
                                               KAON_MAX_ROW};
 
 template <int GT>
-StatsFn stats_fn_gt(int cls) {
+StatsFn stats_fn_gt(int cls, bool eps) {
   switch (cls) {
-    case 0: return k_pf_stats<0>;
-    case 1: return k_pf_stats<1>;
-    case 2: return k_pf_stats<2>;
+    case 0: return eps ? k_pf_stats<0, true> : k_pf_stats<0, false>;
+    case 1: return eps ? k_pf_stats<1, true> : k_pf_stats<1, false>;
+    case 2: return eps ? k_pf_stats<2, true> : k_pf_stats<2, false>;
     case 3: return k_stats<GT, 4>;
     case 4: return k_stats<GT, 10>;
     case 5: return k_stats<GT, 24>;
@@ -1654,7 +1665,9 @@ StatsFn stats_fn_gt(int cls) {
   }
   return nullptr;
 }
-StatsFn stats_fn(int gt, int cls) { return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls) : stats_fn_gt<KAON_F32>(cls); }
+StatsFn stats_fn(int gt, int cls, bool eps) {
+  return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls, eps) : stats_fn_gt<KAON_F32>(cls, eps);
+}
 
 using SsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
 SsFn ss_fn(int gt) { return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : (SsFn)k_ss<KAON_F32>; }
@@ -1681,8 +1694,8 @@ int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipS
     const int32_t cnt = L.row_runs[cls];
     if (cnt <= 0) continue;
     if (cls < 3 && hp.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
-    StatsFn fn = stats_fn(hp.g_dtype, cls);
-    const size_t lds = mode == 0 ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
+    StatsFn fn = stats_fn(hp.g_dtype, cls, (hp.flags & KAON_F_EPS) != 0);
+    const size_t lds = (mode == 0 && cls >= 3) ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
     hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);
     off += cnt;
   }

@@ -62,6 +62,23 @@ def phase_bytes(phase: int, bm: float, wd: bool) -> float:
     return 0.0
 
 
+def measured_traffic(workload: str, phase: int) -> float | None:
+    """HBM bytes per launch of a phase kernel, from the rocprofv3 PMC summaries
+    committed under profiles/ (FETCH_SIZE and WRITE_SIZE, each scaled by what
+    the counter reads for a copy kernel of known size); None when no summary
+    covers this workload and phase."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_pmc.md"))):
+        with open(path) as fh:
+            for line in fh:
+                m = re.match(r"traffic: workload=(\S+) phase=(\d+) kernel=\S+ bytes=(\S+)", line.strip())
+                if m and m.group(1) == workload and int(m.group(2)) == phase:
+                    return float(m.group(3))
+    return None
+
+
 def make_opt(name, params):
     from kaon_amd import Adakaon, Lion, Nekaon
 
@@ -232,7 +249,7 @@ def main() -> int:
         bpp = phase_bytes(dom, bm, wd)
         ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
         out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),
                            "kernel": f"phase {dom} ({PHASE_NAMES[dom]})", "bytes_per_param": bpp,
                            "avg_ms": round(br[dom], 4)}
         out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())}

@@ -1,0 +1,80 @@
+"""Pin the oracle's rounding model against torch CPU (the reference's arithmetic).
+
+The reference computes its step with torch ops; torch is a dependency of the
+reference (pyproject: torch>=2.5), importable here, so its CPU kernels are
+the ground truth for one-op rounding questions the fixtures cannot isolate:
+
+* lerp(a, b, w) with a python-float weight: both branches of |w| < 0.5 and the
+  fused multiply-add in each (src/kaon/_factored.py:51-52,
+  src/kaon/_momentum_codec.py:268, 305, 367);
+* bf16 <-> fp32 conversion, round to nearest even (every bf16 store);
+* GC in the grad dtype: bf16 row mean, bf16 subtraction
+  (src/kaon/_backend.py:147-177) on rows short enough that torch's fp32 sum
+  is exact, so the reduction order cannot matter;
+* the SR bit trick against its three-op torch form
+  (src/kaon/_stochastic_rounding.py:88-103).
+
+A plausible slip -- a lerp without the fma, the branch threshold on the wrong
+side, truncation instead of RNE, an fp32 instead of a bf16 GC -- fails one of
+these on the seeded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+@pytest.mark.parametrize("w", [0.1, 0.001, 0.4999, 0.5, 0.75, 0.999, 1e-30, -0.3, 1.0])
+def test_lerp_matches_torch_cpu(w):
+    rng = np.random.default_rng(1)
+    a = (rng.standard_normal(200_000) * np.exp(rng.uniform(-20, 20, 200_000))).astype(np.float32)
+    b = (rng.standard_normal(200_000) * np.exp(rng.uniform(-20, 20, 200_000))).astype(np.float32)
+    b[:1000] = a[:1000] * np.float32(1.0000001)  # nearly equal operands: cancellation in b - a
+    want = torch.from_numpy(a.copy()).lerp_(torch.from_numpy(b), w).numpy()
+    got = O.lerp(a, b, w)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_lerp_fma_is_observable():
+    """Inputs on which an unfused lerp differs from the fused one (so the test
+    above really pins the fma, not just the formula)."""
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(100_000).astype(np.float32)
+    b = rng.standard_normal(100_000).astype(np.float32)
+    w = np.float32(0.1)
+    unfused = (a + w * (b - a)).astype(np.float32)
+    fused = O.lerp(a, b, float(w))
+    assert (unfused.view(np.uint32) != fused.view(np.uint32)).sum() > 100
+
+
+def test_bf16_conversion_matches_torch():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(300_000) * np.exp(rng.uniform(-80, 80, 300_000))).astype(np.float32)
+    x[:4] = [np.inf, -np.inf, 3.3961e38, -0.0]
+    # exact ties at every mantissa parity
+    ties = (np.arange(1, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16(x), want)
+
+
+@pytest.mark.parametrize("shape", [(7, 16), (33, 40), (5, 128)])
+def test_gc_bf16_matches_torch_on_exact_sum_rows(shape):
+    """Rows of <= 128 bf16 values with a shared exponent range sum exactly in
+    fp32 in any order, so torch's result is order-free and must equal the oracle's."""
+    rng = np.random.default_rng(4)
+    g = torch.from_numpy((rng.integers(-255, 256, shape) / 256.0).astype(np.float32)).to(torch.bfloat16)
+    want = g - g.mean(dim=1, keepdim=True)
+    got = O.gc_bf16(g.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(got, want.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_sr_round_matches_three_op_torch_form():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(100_000) * np.exp(rng.uniform(-30, 30, 100_000))).astype(np.float32)
+    noise = rng.integers(0, 1 << 16, x.size).astype(np.uint16)
+    t = torch.from_numpy(x.copy()).view(torch.int32)
+    t.add_(torch.from_numpy(noise.astype(np.int32))).bitwise_and_(-65536)
+    want = t.view(torch.float32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.sr_round(x, noise), want)

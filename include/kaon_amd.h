@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 2
+#define KAON_ABI_VERSION 3
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -56,7 +56,9 @@ enum {
   KAON_F_EPS = 8,       /* eps1 > 0 adds eps1 to g^2 (_factored.py:35-39) */
   KAON_F_MOMENTUM = 16, /* beta1 > 0 and a momentum buffer exists */
   KAON_F_NK_REMOVE = 32,/* Nekaon: remove the previous climb first (msam.py:386-388) */
-  KAON_F_NK_CLIMB = 64  /* Nekaon: climb along the new momentum (msam.py:395-403) */
+  KAON_F_NK_CLIMB = 64, /* Nekaon: climb along the new momentum (msam.py:395-403) */
+  KAON_F_SRC_O = 128    /* set by the library for AdaMuon's factored passes: the row kernels
+                           read the orthogonalized O from the workspace instead of the grad */
 };
 
 /*
@@ -85,7 +87,8 @@ typedef struct KaonTensor {
   int64_t ws_part;        /* column partials [ngroups][C], one row per slice */
   int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
   int64_t ws_scal;        /* 4 words: fac, keep-count, spare, spare */
-  int64_t ws_aux;         /* AdaMuon Newton-Schulz scratch (bf16 words) */
+  int64_t ws_aux;         /* AdaMuon: Newton-Schulz buffers, bf16: M then O [R*C], the iterate
+                             X and its successor [m_pad*k_pad] each, A and B [m_pad^2] each */
   int32_t tensor_id;      /* SR counter field: index in the optimizer's param list */
   int32_t block4;         /* 4-bit block size (m_block) */
   int32_t factored;       /* ndim >= 2 */
@@ -93,12 +96,16 @@ typedef struct KaonTensor {
   float sqrt_n;           /* (float)sqrt((double)n), the rms divisor (_backend.py:45-47) */
   int32_t vec_rows;       /* 16-byte vector path for row chunks (C % 8 == 0 or one row, aligned) */
   int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
+  int32_t ns_tr;          /* AdaMuon: Newton-Schulz iterates on the transpose (R > C) */
+  int32_t m_pad, k_pad;   /* AdaMuon: min(R,C) and max(R,C) rounded up to KAON_NS_TILE */
   int32_t pad;
 } KaonTensor;
 
 /* A work item.  Slices: rows [row0, row0 + nrows) of tensor `tensor`, kind =
  * rows per wave group.  Finalize items: kind 0 = columns [row0, row0+nrows),
- * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows). */
+ * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows).
+ * Newton-Schulz tiles: row0 = tile row, nrows = tile column (KAON_NS_TILE
+ * square tiles of the padded matrices). */
 typedef struct KaonItem {
   int32_t tensor;
   int32_t row0;
@@ -118,6 +125,8 @@ typedef struct KaonItem {
 
 /* Row classes of the slice kernels (KaonPlanInfo.row_runs). */
 #define KAON_ROW_CLASSES 7
+/* Tile edge of the Newton-Schulz GEMMs; the iterate is zero-padded to it. */
+#define KAON_NS_TILE 128
 
 /*
  * Host-side plan: kaon_plan() fills the workspace offsets of every
@@ -134,6 +143,8 @@ typedef struct KaonPlanInfo {
                              (prefetching kernels); 3-5 other rows of <= 4, 10, 24 chunks
                              held in registers; 6 streamed rows */
   int32_t n_fast;         /* slices of elem_items that take the specialized kernels */
+  int32_t n_ns_sq;        /* AdaMuon: tiles of the m_pad x m_pad products (ns_sq_items) */
+  int32_t n_ns_rect;      /* AdaMuon: tiles of the m_pad x k_pad iterate (ns_rect_items) */
   int64_t ws_words;       /* workspace size in 4-byte words */
 } KaonPlanInfo;
 
@@ -157,9 +168,12 @@ typedef struct KaonLaunch {
   const KaonItem* elem_items; /* device: the same slices, specialized-kernel ones first */
   const KaonItem* fin_items;  /* device */
   const KaonItem* flat_items; /* device */
+  const KaonItem* ns_sq_items;   /* device, AdaMuon */
+  const KaonItem* ns_rect_items; /* device, AdaMuon */
   int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
   int32_t row_runs[KAON_ROW_CLASSES];
   int32_t n_fast;
+  int32_t n_ns_sq, n_ns_rect;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
 } KaonLaunch;
 
@@ -196,7 +210,8 @@ const char* kaon_last_error(void);
  * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
  * factored row longer than KAON_MAX_ROW). */
 int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
-              KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info);
+              KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonItem* ns_sq_items,
+              KaonItem* ns_rect_items, KaonPlanInfo* info);
 
 /* Adakaon step over one planned param group, Nekaon's remove/climb fused in
  * when the KAON_F_NK_* flags are set.  Replaces Adakaon._fused_step and the
@@ -207,6 +222,16 @@ int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 /* Lion step over one planned param group (lion.py:322-352, 416-485). */
 int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
+/* AdaMuon step over one planned group of 2-D / conv params (plan opt =
+ * KAON_OPT_ADAMUON): momentum of the raw grad, Newton-Schulz quintic
+ * iteration as bf16 MFMA GEMMs, factored second moment of the orthogonal
+ * factor, clip, 0.2*lr scale (hp->lr carries 0.2*lr), WD, cautious against
+ * the grad, write.  Replaces AdaMuon._step_one_param / _factored_bucket and
+ * zeropower_via_newtonschulz5(_stacked) (adamuon.py:97-149, 434-501,
+ * 557-593).  1-D params take an Adakaon plan with hp->lr = 0.2*lr
+ * (adamuon.py:594-604). */
+int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
 /* The same steps restricted to the phases whose bit is set in `mask`
  * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,
  * 4 clip divisor, 5 keep-count + momentum absmax, 6 apply; Lion uses 1, 5,
@@ -215,6 +240,10 @@ int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
  * No counterpart in the reference, which has no phase boundary to expose. */
 int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
+/* AdaMuon: bit 8 = momentum pass, norm and Newton-Schulz input; bit 9 =
+ * Newton-Schulz GEMMs and the orthogonal factor O; then bits 1-6 as above on
+ * O.  The step is mask 0x37E. */
+int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
 
 /* MSAM norm="none" perturbation p += clamp(nan_to_num(factor * dequant(m)), +-bound)
  * (msam.py:202-235; fused 4-bit twin _fused_triton.py:1145-1179), used by

@@ -1,0 +1,292 @@
+// kaon_ns.hip -- AdaMuon's Newton-Schulz quintic iteration on gfx950 MFMA.
+//
+// zeropower_via_newtonschulz5 (src/kaon/adamuon.py:97-118), per matrix:
+//   x = bf16(M) (transposed when R > C, so x is m x k with m <= k)
+//   x = x / (||x|| + 1e-7)
+//   repeat steps:  A = x x^T;  B = b*A + c*(A A);  x = a*x + B x
+// with (a, b, c) = (3.4445, -4.7750, 2.0315) and every torch op on bf16
+// tensors rounding its result to bf16 (products accumulate in fp32).
+//
+// Layout: each tensor's iterate lives zero-padded to m_pad x k_pad (multiples
+// of KAON_NS_TILE) in its workspace block.  Zero rows and columns stay zero
+// through all three products, so the GEMMs run on whole tiles with no edge
+// masks and the padding never reaches the result.
+//
+// GEMM: one 128 x 128 output tile per workgroup (4 wave64, each 64 x 64 = 2 x 2
+// v_mfma_f32_32x32x16_bf16 tiles), K in steps of 64 staged through LDS; the
+// next K step's global loads are in flight while the MFMAs run.  Work items
+// list (tensor, tile row, tile column) for every tensor of the plan, so one
+// launch per product covers the whole parameter list.  A = x x^T and A A are
+// "NT" products (both operands row-major along K; A is symmetric); B x reads
+// x along its rows and is transposed into LDS on the way in.
+#include "kaon_ns.h"
+
+#include <string>
+
+#include "kaon_device.h"
+
+using namespace kaon;
+
+void kaon_set_error(const std::string& s);
+
+namespace {
+
+constexpr int TILE = KAON_NS_TILE;  // 128
+constexpr int TK = 64;              // K per LDS stage
+constexpr int LDK = TK + 8;         // LDS row stride (bf16), breaks bank aliasing
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct NsBufs {
+  uint16_t* mo;  // M, then O: [R, C]
+  uint16_t* x0;  // iterate ping
+  uint16_t* x1;  // iterate pong
+  uint16_t* a;   // A = x x^T  [m_pad, m_pad]
+  uint16_t* b;   // B          [m_pad, m_pad]
+};
+
+__device__ __forceinline__ int64_t r4(int64_t x) { return (x + 3) & ~int64_t(3); }
+
+// Word offsets as kaon_plan lays the block out (kaon_plan.cpp ns_words).
+__device__ __forceinline__ NsBufs ns_bufs(float* base, const KaonTensor& T) {
+  float* p = base + T.ws_aux;
+  NsBufs nb;
+  nb.mo = (uint16_t*)p;
+  p += r4((T.R * T.C + 1) / 2);
+  const int64_t xw = r4((int64_t)T.m_pad * T.k_pad / 2), aw = r4((int64_t)T.m_pad * T.m_pad / 2);
+  nb.x0 = (uint16_t*)p;
+  p += xw;
+  nb.x1 = (uint16_t*)p;
+  p += xw;
+  nb.a = (uint16_t*)p;
+  p += aw;
+  nb.b = (uint16_t*)p;
+  return nb;
+}
+
+__device__ __forceinline__ uint32_t half_of(const ku4 v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+// MODE 0: A = x x^T.  MODE 1: B = b*A + c*(A A).  MODE 2: x' = a*x + B x.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, float* ws, int parity,
+                                                 float ca, float cb, float cc) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[TILE * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[TILE * LDK];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const NsBufs nb = ns_bufs(ws, T);
+  const int mp = T.m_pad, kp = T.k_pad;
+  const uint16_t* xc = parity ? nb.x1 : nb.x0;
+  uint16_t* xn = parity ? nb.x0 : nb.x1;
+  const uint16_t* Aop = MODE == 0 ? xc : MODE == 1 ? nb.a : nb.b;
+  const uint16_t* Bop = MODE == 1 ? nb.a : xc;
+  const int lda = MODE == 0 ? kp : mp;
+  const int ldb = MODE == 1 ? mp : kp;
+  const int K = MODE == 0 ? kp : mp;
+  uint16_t* out = MODE == 0 ? nb.a : MODE == 1 ? nb.b : xn;
+  const int ldc = MODE == 2 ? kp : mp;
+  const int row0 = it.row0 * TILE, col0 = it.nrows * TILE;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // staging registers: 4 x 16 B of each operand per thread per K step
+  ku4 ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = tid + 256 * s, r = q >> 3, kc = q & 7;
+      ra[s] = *(const KAON_G ku4*)G(Aop + (int64_t)(row0 + r) * lda + k0 + kc * 8);
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int q = tid + 256 * s, r = q >> 3, kc = q & 7;
+        rb[s] = *(const KAON_G ku4*)G(Bop + (int64_t)(col0 + r) * ldb + k0 + kc * 8);
+      }
+    } else {
+      // x tile: K rows (k0..k0+63) x 128 columns; a thread takes two adjacent
+      // rows of 8 columns so its LDS writes pack row pairs into 32-bit words
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int q = tid + 256 * s, jc = q >> 5, tp = q & 31;
+        const uint16_t* src = Bop + (int64_t)(k0 + 2 * tp) * ldb + col0 + jc * 8;
+        rb[2 * s] = *(const KAON_G ku4*)G(src);
+        rb[2 * s + 1] = *(const KAON_G ku4*)G(src + ldb);
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = tid + 256 * s, r = q >> 3, kc = q & 7;
+      *(ku4*)&As[r * LDK + kc * 8] = ra[s];
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int q = tid + 256 * s, r = q >> 3, kc = q & 7;
+        *(ku4*)&Bs[r * LDK + kc * 8] = rb[s];
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int q = tid + 256 * s, jc = q >> 5, tp = q & 31;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *(uint32_t*)&Bs[(jc * 8 + e) * LDK + 2 * tp] = half_of(rb[2 * s], e) | (half_of(rb[2 * s + 1], e) << 16);
+      }
+    }
+  };
+
+  gload(0);
+  for (int k0 = 0; k0 < K; k0 += TK) {
+    __syncthreads();  // the previous step's MFMAs are done with the LDS tiles
+    lstore();
+    __syncthreads();
+    if (k0 + TK < K) gload(k0 + TK);
+#pragma unroll
+    for (int kk = 0; kk < TK; kk += 16) {
+      bf16x8 af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *(const bf16x8*)&As[(wm * 64 + i * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bfr[j] = *(const bf16x8*)&Bs[(wn * 64 + j * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 8];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // epilogue: lane l of a 32x32 tile holds column l%32, rows (r/4)*8 + (l/32)*4 + r%4
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int col = col0 + wn * 64 + j * 32 + (lane & 31);
+        const float v = acc[i][j][r];
+        uint32_t o;
+        if (MODE == 0) {
+          o = f2bf(v);
+        } else if (MODE == 1) {
+          const float e = bf2f(G(nb.a)[(int64_t)row * mp + col]);
+          o = f2bf(rbf(cb * e) + rbf(cc * rbf(v)));
+        } else {
+          const float e = bf2f(G(xc)[(int64_t)row * kp + col]);
+          o = f2bf(rbf(ca * e) + rbf(v));
+        }
+        G(out)[(int64_t)row * ldc + col] = (uint16_t)o;
+      }
+}
+
+// x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
+// the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
+__global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, float* ws) {
+  __shared__ uint16_t tile[TILE][TILE + 2];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const NsBufs nb = ns_bufs(ws, T);
+  const double rden = rcp64(G(ws)[T.ws_scal + 2]);
+  const int64_t C = T.C;
+  const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
+  const int i0 = it.row0 * TILE, t0 = it.nrows * TILE;
+  const KAON_G uint16_t* mo = G((const uint16_t*)nb.mo);
+  KAON_G uint16_t* x = G(nb.x0);
+  if (!T.ns_tr) {
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int i = i0 + (e >> 7), t = t0 + (e & 127);
+      const float v = (i < m && t < k) ? bf2f(mo[(int64_t)i * C + t]) : 0.0f;
+      x[(int64_t)i * T.k_pad + t] = (uint16_t)f2bf(div_r64(v, rden));
+    }
+  } else {
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int tt = e >> 7, ii = e & 127, t = t0 + tt, i = i0 + ii;
+      tile[tt][ii] = (t < k && i < m) ? mo[(int64_t)t * C + i] : (uint16_t)0;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int ii = e >> 7, tt = e & 127;
+      x[(int64_t)(i0 + ii) * T.k_pad + t0 + tt] = (uint16_t)f2bf(div_r64(bf2f(tile[tt][ii]), rden));
+    }
+  }
+}
+
+// O [R, C] from the final iterate (transposed back when R > C), over M.
+__global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, float* ws, int parity) {
+  __shared__ uint16_t tile[TILE][TILE + 2];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const NsBufs nb = ns_bufs(ws, T);
+  const int64_t C = T.C;
+  const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
+  const int i0 = it.row0 * TILE, t0 = it.nrows * TILE;
+  const KAON_G uint16_t* x = G((const uint16_t*)(parity ? nb.x1 : nb.x0));
+  KAON_G uint16_t* o = G(nb.mo);
+  if (!T.ns_tr) {
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int i = i0 + (e >> 7), t = t0 + (e & 127);
+      if (i < m && t < k) o[(int64_t)i * C + t] = x[(int64_t)i * T.k_pad + t];
+    }
+  } else {
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int ii = e >> 7, tt = e & 127;
+      tile[tt][ii] = x[(int64_t)(i0 + ii) * T.k_pad + t0 + tt];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
+      const int tt = e >> 7, ii = e & 127, t = t0 + tt, i = i0 + ii;
+      if (t < k && i < m) o[(int64_t)t * C + i] = tile[tt][ii];
+    }
+  }
+}
+
+int ns_check(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return 0;
+  kaon_set_error(std::string(what) + ": " + hipGetErrorString(e));
+  return (int)e;
+}
+
+}  // namespace
+
+int kaon_ns_run(const KaonLaunch& L, int steps, hipStream_t st) {
+  if (L.n_ns_rect <= 0) return 0;
+  if (steps < 1) {
+    kaon_set_error("kaon_adamuon: ns_steps must be >= 1");
+    return -1;
+  }
+  float* ws = (float*)L.workspace;
+  const float a = 3.4445f, b = -4.7750f, c = 2.0315f;  // adamuon.py:106
+  hipLaunchKernelGGL(k_ns_prep, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws);
+  int rc = ns_check("kaon: Newton-Schulz input launch");
+  for (int s = 0; s < steps && !rc; ++s) {
+    const int par = s & 1;
+    hipLaunchKernelGGL(k_ns_gemm<0>, dim3(L.n_ns_sq), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
+    hipLaunchKernelGGL(k_ns_gemm<1>, dim3(L.n_ns_sq), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
+    hipLaunchKernelGGL(k_ns_gemm<2>, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, par, a, b,
+                       c);
+    rc = ns_check("kaon: Newton-Schulz GEMM launch");
+  }
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_ns_post, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, steps & 1);
+  return ns_check("kaon: Newton-Schulz output launch");
+}

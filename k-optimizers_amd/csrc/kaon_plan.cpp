@@ -67,6 +67,7 @@ int row_class(const KaonTensor& t, int32_t g_dtype) {
 // grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
 // momentum blocks of 8*G elements (G | 64) that tile the rows.
 bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
+  if (a.opt == KAON_OPT_ADAMUON) return false;
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
   if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
   if (a.codec == KAON_MOM_F32) return false;
@@ -77,8 +78,18 @@ bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
   return true;
 }
 
+// Words of AdaMuon's Newton-Schulz block (bf16 buffers, each 16-byte aligned):
+// M / O [R*C], the iterate and its successor [m_pad*k_pad], A and B [m_pad^2].
+int64_t ns_words(const KaonTensor& t) {
+  const int64_t rc = round4((t.R * t.C + 1) / 2);
+  const int64_t x = round4((int64_t)t.m_pad * t.k_pad / 2);
+  const int64_t a = round4((int64_t)t.m_pad * t.m_pad / 2);
+  return rc + 2 * x + 2 * a;
+}
+
 extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
-                         KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonPlanInfo* info) {
+                         KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonItem* ns_sq_items,
+                         KaonItem* ns_rect_items, KaonPlanInfo* info) {
   if (!info) return plan_fail("kaon_plan: info is NULL");
   if (!args) return plan_fail("kaon_plan: args is NULL");
   const int32_t opt = args->opt, codec = args->codec, g_dtype = args->g_dtype;
@@ -98,7 +109,9 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     bool fast;
   };
   std::vector<RowIt> rows;
-  std::vector<KaonItem> fins, flats;
+  std::vector<KaonItem> fins, flats, ns_sq, ns_rect;
+  // the row kernels of an AdaMuon plan read the bf16 orthogonal factor
+  const int32_t row_dtype = opt == KAON_OPT_ADAMUON ? (int32_t)KAON_BF16 : g_dtype;
   for (int32_t i = 0; i < n; ++i) {
     KaonTensor& t = descs[i];
     if (t.R < 1 || t.C < 0) return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has a bad shape");
@@ -109,6 +122,10 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has rows of " + std::to_string(t.C) +
                        " elements; the row kernels take at most " + std::to_string(KAON_MAX_ROW));
     if (!t.factored && t.R != 1) return plan_fail("kaon_plan: a 1-D tensor must have R == 1");
+    if (opt == KAON_OPT_ADAMUON && !t.factored)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) +
+                       " is 1-D; AdaMuon plans take 2-D / conv params (1-D params step through an Adakaon "
+                       "plan with lr scaled by 0.2)");
     if (codec == KAON_MOM_4BIT && t.block4 < 1) return plan_fail("kaon_plan: 4-bit block size must be >= 1");
     t.sqrt_n = (float)std::sqrt((double)(t.n > 1 ? t.n : 1));
     const int64_t rw = rows_per_wave(t.C);
@@ -136,9 +153,25 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     t.ws_scal = off;
     off = round4(off + 4);
     t.ws_aux = off;
+    t.ns_tr = 0;
+    t.m_pad = t.k_pad = 0;
+    if (opt == KAON_OPT_ADAMUON) {
+      const int64_t m = std::min(t.R, t.C), k = std::max(t.R, t.C);
+      t.ns_tr = t.R > t.C ? 1 : 0;
+      t.m_pad = (int32_t)((m + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE);
+      t.k_pad = (int32_t)((k + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE);
+      off += ns_words(t);
+      if (t.n > 0) {
+        const int32_t tm = t.m_pad / KAON_NS_TILE, tk = t.k_pad / KAON_NS_TILE;
+        for (int32_t a = 0; a < tm; ++a)
+          for (int32_t b = 0; b < tm; ++b) ns_sq.push_back(KaonItem{i, a, b, 0});
+        for (int32_t a = 0; a < tm; ++a)
+          for (int32_t b = 0; b < tk; ++b) ns_rect.push_back(KaonItem{i, a, b, 0});
+      }
+    }
     if (t.n == 0) continue;
     // slices (row items): kind = rows per wave group
-    const int cls = row_class(t, g_dtype);
+    const int cls = row_class(t, row_dtype);
     const bool fast = fast_eligible(*args, t);
     for (int64_t r0 = 0; r0 < t.R; r0 += slice_rows) {
       KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(slice_rows, t.R - r0), (int32_t)rw};
@@ -177,5 +210,10 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     for (size_t k = 0; k < rows.size(); ++k) row_items[k] = rows[k].it;
   if (fin_items && !fins.empty()) std::memcpy(fin_items, fins.data(), fins.size() * sizeof(KaonItem));
   if (flat_items && !flats.empty()) std::memcpy(flat_items, flats.data(), flats.size() * sizeof(KaonItem));
+  info->n_ns_sq = (int32_t)ns_sq.size();
+  info->n_ns_rect = (int32_t)ns_rect.size();
+  if (ns_sq_items && !ns_sq.empty()) std::memcpy(ns_sq_items, ns_sq.data(), ns_sq.size() * sizeof(KaonItem));
+  if (ns_rect_items && !ns_rect.empty())
+    std::memcpy(ns_rect_items, ns_rect.data(), ns_rect.size() * sizeof(KaonItem));
   return 0;
 }

@@ -34,6 +34,7 @@
 #include <string>
 
 #include "kaon_device.h"
+#include "kaon_ns.h"
 
 using namespace kaon;
 
@@ -76,6 +77,13 @@ struct Ws {
   __device__ KAON_G float* scal(const KaonTensor& T) const { return G(base + T.ws_scal); }
   // generic address of the keep-count word (for atomics)
   __device__ uint32_t* keep_ctr(const KaonTensor& T) const { return (uint32_t*)(base + T.ws_scal) + 1; }
+  // AdaMuon: the bf16 momentum, then the orthogonal factor O, [R, C] (first
+  // buffer of the Newton-Schulz block)
+  __device__ uint16_t* mo(const KaonTensor& T) const { return (uint16_t*)(base + T.ws_aux); }
+  // what the row kernels read as "the gradient": O for AdaMuon's factored passes
+  __device__ const void* src(const KaonTensor& T, int flags) const {
+    return (flags & KAON_F_SRC_O) ? (const void*)mo(T) : T.g;
+  }
 };
 
 template <int DT>
@@ -133,6 +141,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   zero_accumulators(T, it, ws, hp.codec);
+  const void* gsrc = ws.src(T, hp.flags);
   const int64_t C = T.C;
   const int64_t nch = (C + 7) >> 3;
   const int cpl = (int)((nch + 63) >> 6);
@@ -147,7 +156,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
       const int cnt = chunk_cnt(c, C);
       const bool vv = vec && cnt == 8;
       float x[8], v[8];
-      ld8<GT>(T.g, c * 8, cnt, vv, x);
+      ld8<GT>(gsrc, c * 8, cnt, vv, x);
       ld8<KAON_F32>(T.v, c * 8, cnt, vv, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
       for (int k = 0; k < NB; ++k) {
         const int64_t c = wr.lane + 64 * k;
         const int cnt = k < cpl ? chunk_cnt(c, C) : 0;
-        if (cnt > 0) ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, xb[k]);
+        if (cnt > 0) ld8<GT>(gsrc, rowoff + c * 8, cnt, vec && cnt == 8, xb[k]);
         else
 #pragma unroll
           for (int i = 0; i < 8; ++i) xb[k][i] = 0.0f;
@@ -234,7 +243,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
           const int cnt = chunk_cnt(c, C);
           if (cnt <= 0) continue;
           float x[8];
-          ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, x);
+          ld8<GT>(gsrc, rowoff + c * 8, cnt, vec && cnt == 8, x);
 #pragma unroll
           for (int i = 0; i < 8; ++i)
             if (i < cnt) a = a + x[i];
@@ -249,7 +258,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
         const int cnt = chunk_cnt(c, C);
         if (cnt <= 0) continue;
         float x[8];
-        ld8<GT>(T.g, rowoff + c * 8, cnt, vec && cnt == 8, x);
+        ld8<GT>(gsrc, rowoff + c * 8, cnt, vec && cnt == 8, x);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           if (i < cnt) {
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
           const int cnt = chunk_cnt(c, C);
           if (cnt <= 0) continue;
           float x[8];
-          ld8<GT>(T.g, r * C + c * 8, cnt, vec && cnt == 8, x);
+          ld8<GT>(gsrc, r * C + c * 8, cnt, vec && cnt == 8, x);
 #pragma unroll
           for (int i = 0; i < 8; ++i)
             if (i < cnt) {
@@ -372,6 +381,7 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
+  const void* gsrc = ws.src(T, hp.flags);
   const int64_t C = T.C;
   const int64_t nch = (C + 7) >> 3;
   const int cpl = (int)((nch + 63) >> 6);
@@ -389,7 +399,7 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
       if (cnt <= 0) continue;
       const bool vv = vec && cnt == 8;
       float x[8], f[8];
-      ld8<GT>(T.g, r * C + c * 8, cnt, vv, x);
+      ld8<GT>(gsrc, r * C + c * 8, cnt, vv, x);
       ld8<KAON_F32>(cfa, c * 8, cnt, vv, f);
       if (gc) {
 #pragma unroll
@@ -527,8 +537,9 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
   if (mode == 1 && (!gc || nrows <= 0)) return;
   const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
   const float row_old = (mode == 0 && nrows > 0) ? G(T.row)[rl] : 0.0f;
+  const void* gsrc = ws.src(T, hp.flags);
   ku4 raw[RW][CPL];
-  load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
+  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, C, nch, wr.lane, raw);
   // GC means of the wave's rows
   float mu[RW];
   KAON_G float* mu_arr = ws.mu(T);
@@ -600,8 +611,9 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
   const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
   const float mu_l = gc ? ws.mu(T)[rl] : 0.0f;
   const float rf_l = ws.rf(T)[rl];
+  const void* gsrc = ws.src(T, hp.flags);
   ku4 raw[RW][CPL];
-  load_group<CPL, RW>((const uint16_t*)T.g, wr.rb, nrows, C, nch, wr.lane, raw);
+  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, C, nch, wr.lane, raw);
   const KAON_G float* cf = ws.cf(T);
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
@@ -793,6 +805,131 @@ __device__ __forceinline__ float dq_int8(uint32_t byte, float sc, float m128sc, 
   return (float)(int8_t)(uint8_t)byte * sc;
 }
 
+// =============================================================== AdaMuon momentum
+// The first moment of the raw gradient (adamuon.py:570-573 via the codecs'
+// ema_one, _momentum_codec.py:266-269, 303-308, 363-371): M = lerp(m, g, 1 -
+// beta1) (g centralized first when GC is on), written as bf16 into the
+// Newton-Schulz block.  Float codecs store m here; int8 / 4-bit record the
+// row / block absmax and the old scales, and phase 6 requantizes M with them.
+// Also: the GC means (phases 5 and 6 use them), and each row's sum of M^2 for
+// the Frobenius norm of the Newton-Schulz input.
+
+// 4-bit block absmax is accumulated with atomics: clear it (one tensor per
+// workgroup) before the momentum pass.
+__global__ __launch_bounds__(KAON_WG) void k_muon_zero(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
+  const KaonTensor& T = D[blockIdx.x];
+  const int64_t nb = nblocks4(T);
+  for (int64_t b = threadIdx.x; b < nb; b += KAON_WG) ws.bamax(T)[b] = 0u;
+}
+
+template <int GT, int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restrict__ D,
+                                                      const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec = T.vec_rows != 0;
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  const bool mom = (hp.flags & KAON_F_MOMENTUM) != 0 && CODEC != KAON_MOM_NONE;
+  const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 1;
+  const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
+  KAON_G uint16_t* mo = G(ws.mo(T));
+  const WaveRows wr = wave_rows(it);
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    float mu = 0.0f;
+    if (gc) {
+      float a = 0.0f;
+      for (int k = 0; k < cpl; ++k) {
+        const int64_t c = wr.lane + 64 * k;
+        const int cnt = chunk_cnt(c, C);
+        if (cnt <= 0) continue;
+        float x[8];
+        ld8<GT>(T.g, r * C + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i < cnt) a = a + x[i];
+      }
+      mu = round_to<GT>(wave_csum(a) / (float)C);
+      if (wr.lane == 0) ws.mu(T)[r] = mu;
+    }
+    const float oldsc = CODEC == KAON_MOM_INT8 && mom ? uniform_f(G(T.m_scale)[r]) : 1.0f;
+    float amax = 0.0f, sq = 0.0f;
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
+      const int64_t e0 = r * C + c * 8;
+      const bool vv = vec && cnt == 8;
+      float g[8];
+      ld8<GT>(T.g, e0, cnt, vv, g);
+      if (gc) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] = round_to<GT>(g[i] - mu);
+      }
+      uint32_t mq[8];
+      if (mom) ld_mom_raw<CODEC>(T, e0, cnt, vv, mq);
+      uint32_t qout[8];
+      float Mv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qout[i] = 0u;
+        Mv[i] = 0.0f;
+        if (i >= cnt) continue;
+        if (!mom) {
+          Mv[i] = g[i];
+        } else if (CODEC == KAON_MOM_BF16) {
+          const uint32_t mb = f2bf(klerp(bf2f(mq[i]), rbf(g[i]), hp.w1));
+          qout[i] = mb;
+          Mv[i] = bf2f(mb);
+        } else if (CODEC == KAON_MOM_F32) {
+          Mv[i] = klerp(__uint_as_float(mq[i]), g[i], hp.w1);
+          qout[i] = __float_as_uint(Mv[i]);
+        } else if (CODEC == KAON_MOM_INT8) {
+          Mv[i] = klerp(dq_int8(mq[i], oldsc, -128.0f * oldsc, fabsf(oldsc) < 0x1p120f), g[i], hp.w1);
+          amax = fmaxf(amax, fabsf(Mv[i]));
+        } else {  // 4-bit: flat blocks, possibly across rows
+          const int64_t e = e0 + i, blk = e / B;
+          const float sc = G(T.m_scale)[blk];
+          Mv[i] = klerp(((float)mq[i] - 8.0f) * sc, g[i], hp.w1);
+          const float ax = fabsf(Mv[i]);
+          if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
+          if (e == blk * B) ws.boldsc(T, nb)[blk] = sc;
+        }
+        const uint32_t xb = f2bf(Mv[i]);
+        const float xf = bf2f(xb);
+        sq = sq + xf * xf;
+        mo[e0 + i] = (uint16_t)xb;
+      }
+      if (mom && (CODEC == KAON_MOM_BF16 || CODEC == KAON_MOM_F32)) st_mom_raw<CODEC>(T, e0, cnt, vv, qout);
+    }
+    if (CODEC == KAON_MOM_INT8 && mom) {
+      const float am = wave_max(amax);
+      if (wr.lane == 0) {
+        ws.ramax(T)[r] = __float_as_uint(am);
+        ws.roldsc(T)[r] = oldsc;
+      }
+    }
+    const float s2 = wave_csum(sq);
+    if (wr.lane == 0) ws.rs(T)[r] = s2;
+  }
+}
+
+// den = bf16(bf16(||M||) + 1e-7) per tensor (x.norm() + 1e-7 on bf16 tensors,
+// adamuon.py:109), one wave per tensor, stored in the tensor's spare scalar.
+__global__ __launch_bounds__(KAON_WG) void k_muon_norm(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= n_tensors) return;
+  const KaonTensor& T = D[t];
+  const int lane = threadIdx.x & 63;
+  const KAON_G float* rs = ws.rs(T);
+  float a = 0.0f;
+  for (int64_t r = lane; r < T.R; r += 64) a = a + rs[r];
+  const float ss = wave_csum(a);
+  if (lane == 0) ws.scal(T)[2] = rbf(rbf(sqrtf(ss)) + 1e-7f);
+}
+
 // Per-chunk body of phases 5 and 6.  Row context (mu, rf, scales) is uniform
 // over the chunk when `one_row`; otherwise it is looked up per element.
 struct RowCtx {
@@ -815,7 +952,11 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const bool gc = (hp.flags & KAON_F_GC) && factored;
   const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
   const bool wd = (hp.flags & KAON_F_WD) != 0;
-  const bool mom = (hp.flags & KAON_F_MOMENTUM) != 0 && CODEC != KAON_MOM_NONE;
+  constexpr bool MUON = OPT == KAON_OPT_ADAMUON;
+  constexpr bool QUANT_C = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
+  // AdaMuon's momentum is the raw grad's: float codecs were stored by the
+  // momentum pass; int8 / 4-bit codes are requantized here in phase 6
+  const bool mom = (hp.flags & KAON_F_MOMENTUM) != 0 && CODEC != KAON_MOM_NONE && (!MUON || (PHASE == 6 && QUANT_C));
   const bool nk_remove = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_REMOVE);
   const bool nk_climb = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_CLIMB);
   constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
@@ -826,7 +967,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const WaveRows wr = wave_rows(it);
 
   // clip divisor of the tensor (phase 4)
-  const float fac = OPT == KAON_OPT_ADAKAON ? ws.scal(T)[0] : 1.0f;
+  const float fac = OPT != KAON_OPT_LION ? ws.scal(T)[0] : 1.0f;
   const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && cautious) {
@@ -842,7 +983,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
     // ---- per-row context (wave-uniform)
     RowCtx rc;
     rc.mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    rc.rf = (OPT == KAON_OPT_ADAKAON && factored) ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    rc.rf = (OPT != KAON_OPT_LION && factored) ? uniform_f(ws.rf(T)[r]) : 0.0f;
     rc.oldsc = 1.0f;
     rc.newsc = 1.0f;
     rc.rnew = 1.0;
@@ -889,7 +1030,9 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       else
 #pragma unroll
         for (int i = 0; i < 8; ++i) mq[i] = CODEC == KAON_MOM_4BIT ? 8u : 0u;
-      if (OPT == KAON_OPT_ADAKAON && cnt > 0) {
+      float ov[8];
+      if (MUON && cnt > 0) ld8<KAON_BF16>(ws.mo(T), e0, cnt, vec, ov);
+      if (OPT != KAON_OPT_LION && cnt > 0) {
         if (factored) ld8<KAON_F32>((const float*)ws.cf(T), j0, cnt, vec, f);
         else ld8<KAON_F32>(T.v, j0, cnt, vec, f);
       } else {
@@ -995,6 +1138,13 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
           } else {
             d = ud;
           }
+          if (wd) d = __fmaf_rn(hp.wdl, pw, d);
+        } else if (MUON) {
+          // U = O * r * c, clipped, times 0.2*lr (hp.lr); the momentum update
+          // is of the grad (requantized below)
+          const float u = (ov[i] * rc.rf) * f[i];
+          d = (fac == 1.0f ? u : div_r64(u, rfac)) * hp.lr;
+          if (mom) mfv = klerp(mold, gv, hp.w1);
           if (wd) d = __fmaf_rn(hp.wdl, pw, d);
         } else {  // Lion
           const float cdir = __fmaf_rn(hp.a1, gv, mold * hp.b1);
@@ -1606,6 +1756,7 @@ ElemFn fast_by_flags(int ff) {
 
 template <int OPT, int PHASE>
 ElemFn fast_fn(int codec, int ff) {
+  if (OPT == KAON_OPT_ADAMUON) return nullptr;
   switch (codec) {
     case KAON_MOM_NONE: return OPT == KAON_OPT_ADAKAON ? fast_by_flags<OPT, PHASE, KAON_MOM_NONE>(ff) : nullptr;
     case KAON_MOM_BF16: return fast_by_flags<OPT, PHASE, KAON_MOM_BF16>(ff);
@@ -1703,6 +1854,36 @@ int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipS
   return check_launch("kaon: k_stats launch");
 }
 
+// Phase 3: prefetching kernels over row classes 0-2, k_ss over the rest.
+int launch_ss(const KaonLaunch& L, Ws ws, const KaonHyper& h, hipStream_t st) {
+  int32_t off = 0;
+  for (int cls = 0; cls < 3; ++cls) {
+    const int32_t cnt = L.row_runs[cls];
+    if (cnt <= 0) continue;
+    if (h.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
+    SsFn fn = cls == 0 ? (SsFn)k_pf_ss<0> : cls == 1 ? (SsFn)k_pf_ss<1> : (SsFn)k_pf_ss<2>;
+    hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), 0, st, L.descs, L.row_items + off, ws, h);
+    off += cnt;
+  }
+  if (L.n_row_items > off)
+    hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3(L.n_row_items - off), dim3(KAON_WG), 0, st, L.descs,
+                       L.row_items + off, ws, h);
+  return check_launch("kaon: k_ss launch");
+}
+
+using MuonMomFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
+template <int GT>
+MuonMomFn muon_mom_gt(int codec) {
+  switch (codec) {
+    case KAON_MOM_NONE: return k_muon_mom<GT, KAON_MOM_NONE>;
+    case KAON_MOM_F32: return k_muon_mom<GT, KAON_MOM_F32>;
+    case KAON_MOM_BF16: return k_muon_mom<GT, KAON_MOM_BF16>;
+    case KAON_MOM_INT8: return k_muon_mom<GT, KAON_MOM_INT8>;
+    case KAON_MOM_4BIT: return k_muon_mom<GT, KAON_MOM_4BIT>;
+  }
+  return nullptr;
+}
+
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who) {
   if (!L || !hp) return fail(who);
   if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16) return fail("kaon: bad p_dtype");
@@ -1741,20 +1922,7 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
     if ((rc = check_launch("kaon: k_fin launch"))) return rc;
   }
   if (mask & (1u << 3)) {
-    // prefetching kernels over row classes 0-2, k_ss over the rest
-    int32_t off = 0;
-    for (int cls = 0; cls < 3; ++cls) {
-      const int32_t cnt = L->row_runs[cls];
-      if (cnt <= 0) continue;
-      if (h.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
-      SsFn fn = cls == 0 ? (SsFn)k_pf_ss<0> : cls == 1 ? (SsFn)k_pf_ss<1> : (SsFn)k_pf_ss<2>;
-      hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), 0, st, L->descs, L->row_items + off, ws, h);
-      off += cnt;
-    }
-    if (L->n_row_items > off)
-      hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3(L->n_row_items - off), dim3(KAON_WG), 0, st, L->descs,
-                         L->row_items + off, ws, h);
-    if ((rc = check_launch("kaon: k_ss launch"))) return rc;
+    if ((rc = launch_ss(*L, ws, h, st))) return rc;
   }
   if (mask & (1u << 4)) {
     hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, h);
@@ -1772,6 +1940,68 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
 
 int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   return kaon_adakaon_phases(L, hp, 0x7Eu, stream);
+}
+
+int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
+  int rc = validate(L, hp, "kaon_adamuon_phases: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
+  if (L->n_ns_rect <= 0) return fail("kaon_adamuon: the launch was not planned for AdaMuon (no Newton-Schulz tiles)");
+  hipStream_t st = (hipStream_t)stream;
+  Ws ws{(float*)L->workspace};
+  KaonHyper h = *hp;
+  const bool mom = (h.flags & KAON_F_MOMENTUM) && h.codec != KAON_MOM_NONE;
+  const int codec = mom ? h.codec : KAON_MOM_NONE;
+  if (!mom) h.flags &= ~KAON_F_MOMENTUM;
+  h.flags &= ~(KAON_F_NK_REMOVE | KAON_F_NK_CLIMB | KAON_F_SRC_O);
+  h.codec = codec;
+  // 8: momentum of the raw grad, its norm
+  if (mask & (1u << 8)) {
+    if (codec == KAON_MOM_4BIT) {
+      hipLaunchKernelGGL(k_muon_zero, dim3(L->n_tensors), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
+      if ((rc = check_launch("kaon: AdaMuon zero launch"))) return rc;
+    }
+    MuonMomFn fm = h.g_dtype == KAON_BF16 ? muon_mom_gt<KAON_BF16>(codec) : muon_mom_gt<KAON_F32>(codec);
+    hipLaunchKernelGGL(fm, dim3(L->n_row_items), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
+    hipLaunchKernelGGL(k_muon_norm, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
+    if ((rc = check_launch("kaon: AdaMuon momentum launch"))) return rc;
+  }
+  // 9: Newton-Schulz -> O
+  if (mask & (1u << 9)) {
+    if ((rc = kaon_ns_run(*L, h.ns_steps, st))) return rc;
+  }
+  // 1-4 on O: bf16 source, no GC (it applies to the grad), nothing of the
+  // momentum codec (its block absmax is already accumulated)
+  KaonHyper ho = h;
+  ho.flags = (h.flags & ~KAON_F_GC) | KAON_F_SRC_O;
+  ho.g_dtype = KAON_BF16;
+  ho.codec = KAON_MOM_NONE;
+  if (mask & (1u << 1)) {
+    if ((rc = launch_stats(*L, ws, ho, 0, st))) return rc;
+  }
+  if ((mask & (1u << 2)) && L->n_fin_items > 0) {
+    hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, ho);
+    if ((rc = check_launch("kaon: k_fin launch"))) return rc;
+  }
+  if (mask & (1u << 3)) {
+    if ((rc = launch_ss(*L, ws, ho, st))) return rc;
+  }
+  if (mask & (1u << 4)) {
+    hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, ho);
+    if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
+  }
+  // 5-6: cautious count against the grad; requant, write
+  if ((mask & (1u << 5)) && (h.flags & KAON_F_CAUTIOUS)) {
+    if ((rc = launch_elem<KAON_OPT_ADAMUON, 5>(*L, ws, h, codec, st))) return rc;
+  }
+  if (mask & (1u << 6)) {
+    if ((rc = launch_elem<KAON_OPT_ADAMUON, 6>(*L, ws, h, codec, st))) return rc;
+  }
+  return 0;
+}
+
+int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  return kaon_adamuon_phases(L, hp, 0x37Eu, stream);
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {

@@ -136,9 +136,10 @@ class KaonOptimizer(torch.optim.Optimizer):
         return out
 
     def _plan(self, key: tuple, group: dict[str, Any], params: list[torch.Tensor], codec: int,
-              tids: dict[int, int]) -> E.Plan:
+              tids: dict[int, int], opt: int | None = None) -> E.Plan:
+        opt = self._OPT if opt is None else opt
         method = L.BF16_METHOD[group["bf16_method"]]
-        ptrs = (self._state_version, codec, method) + tuple(
+        ptrs = (self._state_version, codec, method, opt) + tuple(
             (p.data_ptr(), p.grad.data_ptr()) for p in params)
         hit = self._plans.get(key)
         if hit is not None and hit[0] == ptrs:
@@ -146,7 +147,7 @@ class KaonOptimizer(torch.optim.Optimizer):
         for p in params:
             if not p.grad.is_contiguous():
                 raise ValueError("kaon_amd: gradients must be contiguous")
-        plan = E.Plan(self._OPT, codec, self._entries(group, params, tids), params[0].device,
+        plan = E.Plan(opt, codec, self._entries(group, params, tids), params[0].device,
                       E.dtype_code(params[0].dtype), E.dtype_code(params[0].grad.dtype), method)
         self._plans[key] = (ptrs, plan)
         return plan

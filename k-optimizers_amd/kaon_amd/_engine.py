@@ -62,21 +62,25 @@ class Plan:
         info = L.KaonPlanInfo()
         args = L.KaonPlanArgs(opt, codec, p_dtype, g_dtype, bf16_method)
         lib = L.lib()
-        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, ctypes.byref(info)),
-                "kaon_plan")
+        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None,
+                              ctypes.byref(info)), "kaon_plan")
         rows = (L.KaonItem * max(info.n_row_items, 1))()
         elems = (L.KaonItem * max(info.n_row_items, 1))()
         fins = (L.KaonItem * max(info.n_fin_items, 1))()
         flats = (L.KaonItem * max(info.n_flat_items, 1))()
-        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, ctypes.byref(info)),
-                "kaon_plan")
+        nsq = (L.KaonItem * max(info.n_ns_sq, 1))()
+        nrect = (L.KaonItem * max(info.n_ns_rect, 1))()
+        L.check(lib.kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, nsq, nrect,
+                              ctypes.byref(info)), "kaon_plan")
         self.info = info
         self.descs = descs
         parts = [bytes(descs)[: ctypes.sizeof(L.KaonTensor) * n],
                  bytes(rows)[: 16 * info.n_row_items],
                  bytes(elems)[: 16 * info.n_row_items],
                  bytes(fins)[: 16 * info.n_fin_items],
-                 bytes(flats)[: 16 * info.n_flat_items]]
+                 bytes(flats)[: 16 * info.n_flat_items],
+                 bytes(nsq)[: 16 * info.n_ns_sq],
+                 bytes(nrect)[: 16 * info.n_ns_rect]]
         offs, total = [], 0
         for b in parts:
             offs.append(total)
@@ -88,12 +92,14 @@ class Plan:
         self.workspace = torch.empty(max(int(info.ws_words), 4), dtype=torch.float32, device=device)
         base = self.table.data_ptr()
         la = L.KaonLaunch()
-        la.descs, la.row_items, la.elem_items, la.fin_items, la.flat_items = (base + o for o in offs)
+        (la.descs, la.row_items, la.elem_items, la.fin_items, la.flat_items, la.ns_sq_items,
+         la.ns_rect_items) = (base + o for o in offs)
         la.n_tensors, la.n_row_items = n, info.n_row_items
         la.n_fin_items, la.n_flat_items = info.n_fin_items, info.n_flat_items
         for k in range(L.ROW_CLASSES):
             la.row_runs[k] = info.row_runs[k]
         la.n_fast = info.n_fast
+        la.n_ns_sq, la.n_ns_rect = info.n_ns_sq, info.n_ns_rect
         la.workspace = self.workspace.data_ptr()
         self.launch = la
 

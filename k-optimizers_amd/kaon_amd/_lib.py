@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -21,13 +21,14 @@ SR, RN, KAHAN = 0, 1, 2
 BF16_METHOD = {"stochastic_rounding": SR, "none": RN, "kahan": KAHAN}
 OPT_ADAKAON, OPT_LION, OPT_ADAMUON = 0, 1, 2
 
-F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB = 1, 2, 4, 8, 16, 32, 64
+F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB, F_SRC_O = 1, 2, 4, 8, 16, 32, 64, 128
 
 ROW_BUDGET = 20
 ROW_CLASSES = 7
 COLITEM = 2048
 FLAT_ITEM = 16384
 MAX_ROW = 16384
+NS_TILE = 128
 
 
 class KaonTensor(ctypes.Structure):
@@ -41,7 +42,8 @@ class KaonTensor(ctypes.Structure):
         ("ws_blk", ctypes.c_int64), ("ws_scal", ctypes.c_int64), ("ws_aux", ctypes.c_int64),
         ("tensor_id", ctypes.c_int32), ("block4", ctypes.c_int32), ("factored", ctypes.c_int32),
         ("ngroups", ctypes.c_int32), ("sqrt_n", ctypes.c_float),
-        ("vec_rows", ctypes.c_int32), ("vec_flat", ctypes.c_int32), ("pad", ctypes.c_int32),
+        ("vec_rows", ctypes.c_int32), ("vec_flat", ctypes.c_int32), ("ns_tr", ctypes.c_int32),
+        ("m_pad", ctypes.c_int32), ("k_pad", ctypes.c_int32), ("pad", ctypes.c_int32),
     ]
 
 
@@ -54,7 +56,7 @@ class KaonPlanInfo(ctypes.Structure):
     _fields_ = [("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
-                ("ws_words", ctypes.c_int64)]
+                ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32), ("ws_words", ctypes.c_int64)]
 
 
 class KaonPlanArgs(ctypes.Structure):
@@ -65,9 +67,11 @@ class KaonPlanArgs(ctypes.Structure):
 class KaonLaunch(ctypes.Structure):
     _fields_ = [("descs", ctypes.c_void_p), ("row_items", ctypes.c_void_p), ("elem_items", ctypes.c_void_p),
                 ("fin_items", ctypes.c_void_p), ("flat_items", ctypes.c_void_p),
+                ("ns_sq_items", ctypes.c_void_p), ("ns_rect_items", ctypes.c_void_p),
                 ("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
+                ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
                 ("workspace", ctypes.c_void_p)]
 
 
@@ -83,7 +87,7 @@ class KaonHyper(ctypes.Structure):
     ]
 
 
-assert ctypes.sizeof(KaonTensor) == 192, ctypes.sizeof(KaonTensor)
+assert ctypes.sizeof(KaonTensor) == 208, ctypes.sizeof(KaonTensor)
 assert ctypes.sizeof(KaonItem) == 16
 assert ctypes.sizeof(KaonHyper) == 88, ctypes.sizeof(KaonHyper)
 
@@ -93,12 +97,14 @@ _VP, _I32, _I64, _U32, _U64, _F = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int
 SIGNATURES = {
     "kaon_abi_version": ([], ctypes.c_int),
     "kaon_last_error": ([], ctypes.c_char_p),
-    "kaon_plan": ([ctypes.POINTER(KaonPlanArgs), _VP, _I32, _VP, _VP, _VP, _VP, ctypes.POINTER(KaonPlanInfo)],
-                  ctypes.c_int),
+    "kaon_plan": ([ctypes.POINTER(KaonPlanArgs), _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP,
+                   ctypes.POINTER(KaonPlanInfo)], ctypes.c_int),
     "kaon_adakaon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
+    "kaon_adamuon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adakaon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_lion_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
+    "kaon_adamuon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_msam_apply": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _F, _F, _U32, _VP], ctypes.c_int),
     "kaon_quant_int8": ([_VP, _I64, _I64, _VP, _VP, _VP], ctypes.c_int),
     "kaon_quant_4bit": ([_VP, _I64, _I32, _VP, _VP, _VP], ctypes.c_int),

@@ -22,7 +22,7 @@ def tdtype(name: str) -> torch.dtype:
 
 
 def make_opt(case, params, group=None):
-    from kaon_amd import Adakaon, Lion, Nekaon
+    from kaon_amd import AdaMuon, Adakaon, Lion, Nekaon
 
     g = dict(group or group_for(case))
     name = case["opt"]
@@ -41,6 +41,10 @@ def make_opt(case, params, group=None):
         opt = Nekaon(params, lr=g["lr"], k=g["k"], betas=g["betas"], weight_decay=g["weight_decay"],
                      momentum_dtype=md, eps=g["eps"], clip_threshold=g["clip_threshold"], **common)
         opt.inner.sr_seed = case["seed"]
+    elif name == "adamuon":
+        opt = AdaMuon(params, lr=g["lr"], betas=g["betas"], eps=g["eps"], weight_decay=g["weight_decay"],
+                      ns_steps=g["ns_steps"], clip_threshold=g["clip_threshold"], **common)
+        opt.sr_seed = case["seed"]
     else:
         raise ValueError(name)
     return opt

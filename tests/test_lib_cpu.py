@@ -75,14 +75,15 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
         d.g = d.p = d.m = 0x1000 * (i + 1)
     info = L.KaonPlanInfo()
     args = L.KaonPlanArgs(opt, codec, 1, g_dtype, 0)
-    rc = L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, ctypes.byref(info))
+    rc = L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None, ctypes.byref(info))
     if rc:
         return rc, None, None, None, None, None
     rows = (L.KaonItem * max(info.n_row_items, 1))()
     elems = (L.KaonItem * max(info.n_row_items, 1))()
     fins = (L.KaonItem * max(info.n_fin_items, 1))()
     flats = (L.KaonItem * max(info.n_flat_items, 1))()
-    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, ctypes.byref(info)) == 0
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, None, None,
+                             ctypes.byref(info)) == 0
     # elem order: the same slices, specialized-kernel ones first
     key = lambda it: (it.tensor, it.row0, it.nrows, it.kind)  # noqa: E731
     assert sorted(key(rows[k]) for k in range(info.n_row_items)) == sorted(key(elems[k]) for k in range(info.n_row_items))
@@ -226,3 +227,68 @@ def test_state_layout_matches_reference_at_init():
     sl = {}
     lion._init_state(vec, sl, lion.param_groups[0])
     assert sl["m"].dtype == torch.bfloat16 and set(sl) == {"m"}
+
+
+def test_adamuon_plan_pads_and_tiles_newton_schulz():
+    """AdaMuon plans: m_pad/k_pad round min/max(R, C) up to the GEMM tile, the
+    transposed flag marks R > C, every tile of the padded products is listed
+    once, and the Newton-Schulz blocks do not overlap other workspace."""
+    L = _lib()
+    shapes = [(1280, 1280, 3, 3), (5120, 1280), (77, 33), (320, 2880), (20, 12)]
+    n = len(shapes)
+    descs = (L.KaonTensor * n)()
+    for i, s in enumerate(shapes):
+        d = descs[i]
+        numel = int(np.prod(s))
+        d.R, d.C, d.factored, d.tensor_id = s[0], numel // s[0], 1, i
+        d.g = d.p = d.m = 0x1000 * (i + 1)
+    info = L.KaonPlanInfo()
+    args = L.KaonPlanArgs(L.OPT_ADAMUON, L.MOM_INT8, L.BF16, L.BF16, L.SR)
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None, ctypes.byref(info)) == 0
+    sq = (L.KaonItem * info.n_ns_sq)()
+    rect = (L.KaonItem * info.n_ns_rect)()
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, sq, rect, ctypes.byref(info)) == 0
+    t = L.NS_TILE
+    spans = []
+    for i, s in enumerate(shapes):
+        d = descs[i]
+        m, k = min(d.R, d.C), max(d.R, d.C)
+        assert d.ns_tr == (1 if d.R > d.C else 0)
+        assert d.m_pad == -(-m // t) * t and d.k_pad == -(-k // t) * t
+        got_sq = sorted((it.row0, it.nrows) for it in sq if it.tensor == i)
+        got_rect = sorted((it.row0, it.nrows) for it in rect if it.tensor == i)
+        assert got_sq == [(a, b) for a in range(d.m_pad // t) for b in range(d.m_pad // t)]
+        assert got_rect == [(a, b) for a in range(d.m_pad // t) for b in range(d.k_pad // t)]
+        words = ((d.R * d.C + 1) // 2 + 3) // 4 * 4 + 2 * ((d.m_pad * d.k_pad // 2 + 3) // 4 * 4) \
+            + 2 * ((d.m_pad * d.m_pad // 2 + 3) // 4 * 4)
+        spans += [(d.ws_row, d.ws_row + 5 * d.R), (d.ws_col, d.ws_col + d.C),
+                  (d.ws_part, d.ws_part + d.ngroups * d.C), (d.ws_scal, d.ws_scal + 4), (d.ws_aux, d.ws_aux + words)]
+    spans.sort()
+    for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):
+        assert a1 <= b0
+    assert spans[-1][1] <= info.ws_words
+    assert info.n_fast == 0
+
+
+def test_adamuon_plan_rejects_1d():
+    L = _lib()
+    descs = (L.KaonTensor * 1)()
+    descs[0].R, descs[0].C, descs[0].factored = 1, 40, 0
+    info = L.KaonPlanInfo()
+    args = L.KaonPlanArgs(L.OPT_ADAMUON, L.MOM_BF16, L.BF16, L.BF16, L.SR)
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, 1, None, None, None, None, None, None, ctypes.byref(info)) != 0
+    assert "1-D" in L.lib().kaon_last_error().decode()
+
+
+def test_adamuon_constructor_validation_mirrors_reference():
+    from kaon_amd import AdaMuon
+
+    p = [torch.nn.Parameter(torch.zeros(4, 4))]
+    for bad in (dict(ns_steps=0), dict(betas=(1.0, 0.9)), dict(lr=-1.0), dict(clip_threshold=0.0),
+                dict(momentum_dtype="fp8")):
+        with pytest.raises(ValueError):
+            AdaMuon(p, **bad)
+    opt = AdaMuon(p)
+    g = opt.param_groups[0]
+    assert (g["lr"], g["betas"], g["ns_steps"], g["momentum_dtype"], g["gradient_centralization"]) == \
+        (2e-2, (0.95, 0.999), 2, "bfloat16", False)

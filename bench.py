@@ -46,10 +46,16 @@ WORKLOADS = {
                              "lr 1e-4, 1% Student-t outliers", opt="nekaon",
                         kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=128),
                         bm=0.5, outliers=0.01),
+    "adamuon_int8": dict(desc="configs[4]: AdaMuon ns_steps=2, betas=(0.95,0.999), int8 momentum, factored 2nd "
+                              "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
+                              "params on the Adakaon path", opt="adamuon",
+                         kw=dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype="int8", ns_steps=2), bm=1.0),
 }
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 # algorithmic HBM bytes per param of each phase kernel (bf16 g/p, b_m momentum bytes)
-PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor", 5: "keep_count", 6: "apply"}
+PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor", 5: "keep_count", 6: "apply",
+               8: "momentum", 9: "newton_schulz"}
 
 
 def phase_bytes(phase: int, bm: float, wd: bool) -> float:
@@ -80,14 +86,32 @@ def measured_traffic(workload: str, phase: int) -> float | None:
 
 
 def make_opt(name, params):
-    from kaon_amd import Adakaon, Lion, Nekaon
+    from kaon_amd import AdaMuon, Adakaon, Lion, Nekaon
 
     w = WORKLOADS[name]
     if w["opt"] == "adakaon":
         return Adakaon(params, **w["kw"])
     if w["opt"] == "lion":
         return Lion(params, **w["kw"])
+    if w["opt"] == "adamuon":
+        return AdaMuon(params, **w["kw"])
     return Nekaon(params, **w["kw"])
+
+
+def ns_flops(shapes, steps: int) -> float:
+    """Newton-Schulz FLOPs per optimizer step: sum over 2-D / conv matrices of
+    steps * (4 m^2 n + 2 m^3), m = min(R, C), n = max(R, C) (x x^T, A A, B x)."""
+    tot = 0.0
+    for s in shapes:
+        if len(s) < 2:
+            continue
+        r = s[0]
+        c = 1
+        for d in s[1:]:
+            c *= d
+        m, n = min(r, c), max(r, c)
+        tot += steps * (4.0 * m * m * n + 2.0 * m ** 3)
+    return tot
 
 
 def copy_ceiling_gbs(dev, nbytes=4 << 30, reps=10) -> float:
@@ -120,9 +144,15 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
     inner = getattr(opt, "inner", opt)
     lib = _lib.lib()
     out: dict[int, list[float]] = {}
-    for (gid, pdt, gdt), (_key, plan) in inner._plans.items():
+    for key, (_ptrs, plan) in inner._plans.items():
+        gid, pdt, gdt = key[:3]
         group = inner.param_groups[gid]
-        if WORKLOADS[name]["opt"] == "lion":
+        if WORKLOADS[name]["opt"] == "adamuon":
+            if key[3] != 2:
+                continue  # the 1-D params' Adakaon plan: a few microseconds
+            hp = inner._hyper(group, pdt, gdt)
+            fn, phases = lib.kaon_adamuon_phases, (8, 9, 1, 2, 3, 4, 5, 6)
+        elif WORKLOADS[name]["opt"] == "lion":
             hp = inner._hyper(group, pdt, gdt)
             fn, phases = lib.kaon_lion_phases, (1, 5, 6)
         else:
@@ -157,8 +187,14 @@ def cpu_baseline(params, name, seconds: float) -> dict:
     group = dict(lr=kw["lr"], betas=kw["betas"], eps=(1e-30, 1e-3), weight_decay=0.1 if w["opt"] == "nekaon" else 0.0,
                  clip_threshold=1.0, momentum_dtype=kw["momentum_dtype"],
                  momentum_4bit_block=kw.get("momentum_4bit_block", 128), cautious=True,
-                 gradient_centralization=True, bf16_method="stochastic_rounding", k=1.5)
+                 gradient_centralization=w["opt"] != "adamuon", bf16_method="stochastic_rounding", k=1.5,
+                 ns_steps=kw.get("ns_steps", 2))
     order = np.random.default_rng(0).permutation(len(params))
+    if w["opt"] == "adamuon":
+        # the oracle's scalar GEMMs take minutes on a 1280 x 11520 matrix: sample the
+        # matrices with min(R, C) <= 640 (and the 1-D params)
+        order = [i for i in order if params[int(i)].ndim < 2 or min(params[int(i)].shape[0],
+                 params[int(i)].numel() // params[int(i)].shape[0]) <= 640]
     done = 0
     elapsed = 0.0
     ntens = 0
@@ -178,7 +214,8 @@ def cpu_baseline(params, name, seconds: float) -> dict:
             break
     return {"value": done / elapsed / 1e9, "unit": "Gparam/s", "cores": 1, "kind": "port",
             "sample": f"one {w['opt']} step of {ntens} tensors ({done / 1e6:.1f}M params) drawn at random from "
-                      f"the same set, CPU oracle oracle/kaon_oracle.c, 1 thread, {elapsed:.1f}s"}
+                      f"the same set{' (matrices with min(R, C) <= 640)' if w['opt'] == 'adamuon' else ''}, "
+                      f"CPU oracle oracle/kaon_oracle.c, 1 thread, {elapsed:.1f}s"}
 
 
 def main() -> int:
@@ -246,12 +283,21 @@ def main() -> int:
         br = phase_breakdown(opt, args.workload)
         wd = w["opt"] == "nekaon"
         dom = max(br, key=lambda k: br[k])
-        bpp = phase_bytes(dom, bm, wd)
-        ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
-        out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),
-                           "kernel": f"phase {dom} ({PHASE_NAMES[dom]})", "bytes_per_param": bpp,
-                           "avg_ms": round(br[dom], 4)}
+        if dom == 9:
+            fl = ns_flops(shapes, w["kw"]["ns_steps"])
+            ach = fl / (br[dom] * 1e-3) / 1e12
+            out["roofline"] = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_MFMA_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(ach / BF16_MFMA_PEAK_TFLOPS, 4),
+                               "traffic": measured_traffic(args.workload, dom),
+                               "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
+                               "avg_ms": round(br[dom], 4)}
+        else:
+            bpp = phase_bytes(dom, bm, wd)
+            ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
+            out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),
+                               "kernel": f"phase {dom} ({PHASE_NAMES[dom]})", "bytes_per_param": bpp,
+                               "avg_ms": round(br[dom], 4)}
         out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)

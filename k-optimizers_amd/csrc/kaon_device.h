@@ -49,6 +49,13 @@ __device__ __forceinline__ float klerp(float a, float b, float w) {
   const float d = b - a;
   return fabsf(w) < 0.5f ? __fmaf_rn(w, d, a) : __fmaf_rn(w - 1.0f, d, b);
 }
+// The same with the branch known at compile time (LO: |w| < 0.5); the caller
+// picks LO once per launch from the uniform weight.
+template <bool LO>
+__device__ __forceinline__ float klerp_b(float a, float b, float w) {
+  const float d = b - a;
+  return LO ? __fmaf_rn(w, d, a) : __fmaf_rn(w - 1.0f, d, b);
+}
 
 // Correctly rounded a / b from a precomputed r = RN64(1/b).  The fp64 product
 // has relative error < 2^-52 while an fp32 quotient of two fp32 values is at
@@ -60,18 +67,30 @@ __device__ __forceinline__ double rcp64(float b) { return 1.0 / (double)b; }
 
 __device__ __forceinline__ float ksign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
 
+// An empty asm statement that reads v: the loads producing v complete here.
+// Used where a value loaded before a loop or inside a uniform branch would
+// otherwise make the compiler wait for every load in flight (prefetches
+// included) at the first use after the merge.
+__device__ __forceinline__ void settle(uint32_t v) { asm volatile("" : : "v"(v)); }
+__device__ __forceinline__ void settle(float v) { asm volatile("" : : "v"(v)); }
+
 // ------------------------------------------------------------------ Philox
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11), published multipliers and
 // Weyl increments.  SR noise: key = (seed lo32, step), counter = (chunk lo,
 // chunk hi, tensor id, stream) with chunk = element / 8; the 8 elements of a
 // chunk take the 8 16-bit halves of the output, low half first.
+// a ^ b ^ c in one v_bitop3_b32 (truth table 0x96)
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ void philox10(uint32_t c[4], uint32_t k0, uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
     const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
     const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
-    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
-    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    const uint32_t n0 = xor3((uint32_t)(p1 >> 32), c[1], k0);
+    const uint32_t n2 = xor3((uint32_t)(p0 >> 32), c[3], k1);
     c[1] = (uint32_t)p1;
     c[3] = (uint32_t)p0;
     c[0] = n0;
@@ -112,10 +131,18 @@ __device__ __forceinline__ uint32_t noise1(uint64_t seed, uint32_t step, uint32_
 
 // _add_stochastic_bf16_ bit trick: int32 add of the 16-bit noise, clear the
 // low half; the cast to bf16 is then exact (NaN -> 0x7FC0).
-__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t noise) {
+// The same as a 32-bit word: the bf16 result in the high half, zeros below
+// (so the word is also the fp32 value of the rounded bf16).
+__device__ __forceinline__ uint32_t sr_word(float x, uint32_t noise) {
   const uint32_t b = (__float_as_uint(x) + noise) & 0xFFFF0000u;
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-  return b >> 16;
+  const float f = __uint_as_float(b);
+  return f != f ? 0x7FC00000u : b;
+}
+__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t noise) { return sr_word(x, noise) >> 16; }
+
+// Two words' high halves packed low-first into one word (v_perm_b32).
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 
 // ------------------------------------------------------------------ loads

@@ -71,6 +71,8 @@ bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
   if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
   if (a.codec == KAON_MOM_F32) return false;
+  // the specialized kernel addresses bf16 elements by 32-bit byte offsets
+  if (t.n > (int64_t(1) << 31)) return false;
   if (a.codec == KAON_MOM_4BIT) {
     const int64_t B = t.block4;
     if (B % 8 != 0 || t.C % B != 0 || B / 8 > 64 || 64 % (B / 8) != 0) return false;

@@ -100,7 +100,8 @@ struct WaveRows {
 };
 __device__ __forceinline__ WaveRows wave_rows(const KaonItem& it) {
   WaveRows wr;
-  wr.w = threadIdx.x >> 6;
+  // the wave index is uniform across the wave; readfirstlane tells the compiler
+  wr.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   wr.lane = threadIdx.x & 63;
   const int64_t end = (int64_t)it.row0 + it.nrows;
   wr.rb = min((int64_t)it.row0 + (int64_t)wr.w * it.kind, end);
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
 // (_factored.py:84-89 via adakaon.py:1001-1003).  One wave per tensor.
 __global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
                                                      KaonHyper hp) {
-  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (t >= n_tensors) return;
   const KaonTensor& T = D[t];
   if (T.n == 0) return;
@@ -919,7 +920,7 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
 // den = bf16(bf16(||M||) + 1e-7) per tensor (x.norm() + 1e-7 on bf16 tensors,
 // adamuon.py:109), one wave per tensor, stored in the tensor's spare scalar.
 __global__ __launch_bounds__(KAON_WG) void k_muon_norm(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
-  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (t >= n_tensors) return;
   const KaonTensor& T = D[t];
   const int lane = threadIdx.x & 63;
@@ -1285,50 +1286,146 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
 // 3 Nekaon removal, 4 Nekaon climb.
 enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16 };
 
-// int8 requant code (as the stored byte) of mf with r = RN64(1/scale)
-__device__ __forceinline__ uint32_t q_int8(float mf, double r, float& xq) {
-  float x = rintf(div_r64(mf, r));
-  x = fminf(fmaxf(x, -127.0f), 127.0f);
-  xq = x;
-  return (uint32_t)(int)x & 0xFFu;
+// int8 requant code of mf with r = RN64(1/scale), as a float in [-127, 127]
+__device__ __forceinline__ float q_int8(float mf, double r) {
+  const float x = rintf(div_r64(mf, r));
+  return fminf(fmaxf(x, -127.0f), 127.0f);
+}
+
+// Four int8 codes (floats in [-127, 127]) as the stored little-endian bytes:
+// code + 128 is exact in [1, 255]; v_cvt_pk_u8_f32 inserts each byte and the
+// xor turns offset-binary into two's complement.
+__device__ __forceinline__ uint32_t pack_int8x4(float a, float b, float c, float d) {
+  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(a + 128.0f, 0, 0u);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(b + 128.0f, 1, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.0f, 2, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(d + 128.0f, 3, w);
+  return w ^ 0x80808080u;
+}
+
+// Per-tensor values of a fast slice, read from its descriptor once per
+// workgroup.  Offsets inside the tensor are 32-bit (the planner keeps tensors
+// of more than 2^31 elements off this kernel), so every access is a uniform
+// base plus a 32-bit byte offset, and nothing is reloaded after a store.
+struct FastCtx {
+  const KAON_G uint8_t* g;       // bf16 grads
+  KAON_G uint8_t* p;             // bf16 params
+  KAON_G uint8_t* m;             // momentum codes or bf16 momentum
+  KAON_G uint8_t* msc;           // momentum scales (per row or per block)
+  const KAON_G uint8_t* cf;      // column factors (Adakaon)
+  KAON_G uint8_t* bamax;         // 4-bit: per-block |m| maximum
+  KAON_G uint8_t* boldsc;        // 4-bit: per-block scale before the step
+  const KAON_G uint16_t* nz[3];  // injected noise streams, or null
+  uint32_t tid;                  // Philox tensor id
+  int bsh;                       // 4-bit: log2 of the block size
+  int GL;                        // 4-bit: lanes per block
+};
+
+// noise8 of the chunk at element e0 < 2^31 (the counter's high word is 0).
+__device__ __forceinline__ void noise8_u32(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream, uint32_t e0,
+                                           const KAON_G uint16_t* inj, uint32_t w[8]) {
+  if (inj) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w[i] = inj[e0 + i];
+      settle(w[i]);
+    }
+    return;
+  }
+  uint32_t c[4] = {e0 >> 3, 0u, tid, stream};
+  philox10(c, (uint32_t)seed, step);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[2 * i] = c[i] & 0xFFFFu;
+    w[2 * i + 1] = c[i] >> 16;
+  }
+}
+
+// Global loads of one chunk, issued a chunk ahead of its arithmetic.
+struct FastIn {
+  ku4 g, p, m16;
+  ku2 m8;
+  uint32_t m4;
+  kf4 c0, c1;
+  float bo, ba;  // 4-bit: block scale before the step, block |m| maximum
+};
+
+template <int OPT, int PHASE, int CODEC, int FLAGS>
+__device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t e0, uint32_t j0) {
+  constexpr bool NEEDP = PHASE == 6 || (FLAGS & FF_WD);
+  const ku4 z4 = ku4{0u, 0u, 0u, 0u};
+  in.g = *(const KAON_G ku4*)(X.g + 2u * e0);
+  in.p = NEEDP ? *(const KAON_G ku4*)(X.p + 2u * e0) : z4;
+  in.m8 = CODEC == KAON_MOM_INT8 ? *(const KAON_G ku2*)(X.m + e0) : ku2{0u, 0u};
+  in.m4 = CODEC == KAON_MOM_4BIT ? *(const KAON_G uint32_t*)(X.m + (e0 >> 1)) : 0u;
+  in.m16 = CODEC == KAON_MOM_BF16 ? *(const KAON_G ku4*)(X.m + 2u * e0) : z4;
+  if (OPT == KAON_OPT_ADAKAON) {
+    in.c0 = *(const KAON_G kf4*)(X.cf + 4u * j0);
+    in.c1 = *(const KAON_G kf4*)(X.cf + 4u * j0 + 16u);
+  } else {
+    in.c0 = in.c1 = kf4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  in.bo = in.ba = 0.0f;
+  if (CODEC == KAON_MOM_4BIT) {
+    const uint32_t blk4 = (e0 >> X.bsh) * 4u;
+    in.bo = *(const KAON_G float*)((PHASE == 5 ? X.msc : X.boldsc) + blk4);
+    if (PHASE == 6) in.ba = *(const KAON_G float*)(X.bamax + blk4);
+  }
+}
+
+// Completes the loads of `in` on every path (see settle), so that the
+// branches consuming them leave nothing pending for the next prefetch to wait on.
+template <int OPT, int PHASE, int CODEC, int FLAGS>
+__device__ __forceinline__ void fast_settle(const FastIn& in) {
+  constexpr bool NEEDP = PHASE == 6 || (FLAGS & FF_WD);
+  settle(in.g.x); settle(in.g.y); settle(in.g.z); settle(in.g.w);
+  if (NEEDP) {
+    settle(in.p.x); settle(in.p.y); settle(in.p.z); settle(in.p.w);
+  }
+  if (CODEC == KAON_MOM_INT8) {
+    settle(in.m8.x); settle(in.m8.y);
+  }
+  if (CODEC == KAON_MOM_4BIT) {
+    settle(in.m4); settle(in.bo);
+    if (PHASE == 6) settle(in.ba);
+  }
+  if (CODEC == KAON_MOM_BF16) {
+    settle(in.m16.x); settle(in.m16.y); settle(in.m16.z); settle(in.m16.w);
+  }
+  if (OPT == KAON_OPT_ADAKAON) {
+    settle(in.c0.x); settle(in.c0.y); settle(in.c0.z); settle(in.c0.w);
+    settle(in.c1.x); settle(in.c1.y); settle(in.c1.z); settle(in.c1.w);
+  }
 }
 
 // FAC1: clip divisor 1 (skip the exact division).  DQX: int8 dequant as
-// q*scale for rows whose old scale is too large for the fma form.
-template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX>
-__device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, int64_t r,
-                                           int64_t e0, int64_t j0, float mu, float rf, float oldsc, float m128,
-                                           float newsc, double rnew, double rfac, double rden, int64_t B,
-                                           int64_t nb, int GL, int lane, uint32_t& keep, float& amax,
-                                           const KAON_G float* cfrow) {
+// q*scale for rows whose old scale is too large for the fma form.  WLO: the
+// momentum lerp weight is below 0.5 (its branch of torch's lerp).
+template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX, bool WLO>
+__device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, const KaonHyper& hp, uint32_t e0,
+                                           float mu, float rf, float oldsc, float m128, float newsc, double rnew,
+                                           double rfac, double rden, int lane, uint32_t& keep, float& amax) {
   constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
   constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
   constexpr bool MOM = CODEC != KAON_MOM_NONE;
   constexpr bool NEEDP = PHASE == 6 || WD;
-  const ku4 gv4 = *(const KAON_G ku4*)G((const uint16_t*)T.g + e0);
-  ku4 pv4 = ku4{0u, 0u, 0u, 0u};
-  if (NEEDP) pv4 = *(const KAON_G ku4*)G((const uint16_t*)T.p + e0);
-  ku2 mi8 = ku2{0u, 0u};
-  uint32_t m4 = 0;
-  ku4 mb16 = ku4{0u, 0u, 0u, 0u};
-  if (CODEC == KAON_MOM_INT8) mi8 = *(const KAON_G ku2*)G((const int8_t*)T.m + e0);
-  if (CODEC == KAON_MOM_4BIT) m4 = *(const KAON_G uint32_t*)G((const uint8_t*)T.m + (e0 >> 1));
-  if (CODEC == KAON_MOM_BF16) mb16 = *(const KAON_G ku4*)G((const uint16_t*)T.m + e0);
+  const ku4 gv4 = in.g, pv4 = in.p, mb16 = in.m16;
+  const ku2 mi8 = in.m8;
+  const uint32_t m4 = in.m4;
   float f[8];
   if (OPT == KAON_OPT_ADAKAON) {
-    const KAON_G float* cfp = cfrow + j0;
-    const kf4 c0 = *(const KAON_G kf4*)cfp, c1 = *(const KAON_G kf4*)(cfp + 4);
-    f[0] = c0.x; f[1] = c0.y; f[2] = c0.z; f[3] = c0.w; f[4] = c1.x; f[5] = c1.y; f[6] = c1.z; f[7] = c1.w;
+    f[0] = in.c0.x; f[1] = in.c0.y; f[2] = in.c0.z; f[3] = in.c0.w;
+    f[4] = in.c1.x; f[5] = in.c1.y; f[6] = in.c1.z; f[7] = in.c1.w;
   }
   // 4-bit: one block per chunk
   float b_old = 1.0f, b_new = 1.0f;
   double b_r = 1.0;
-  int64_t blk = 0;
+  uint32_t blk4 = 0;  // byte offset of the chunk's block in the per-block arrays
   if (CODEC == KAON_MOM_4BIT) {
-    blk = e0 / B;
-    b_old = PHASE == 5 ? G(T.m_scale)[blk] : ws.boldsc(T, nb)[blk];
+    blk4 = (e0 >> X.bsh) * 4u;
+    b_old = in.bo;
     if (PHASE == 6) {
-      b_new = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+      b_new = fmaxf(in.ba, 1e-12f) / 7.0f;
       b_r = rcp64(b_new);
     }
   }
@@ -1345,9 +1442,9 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
     }
   }
   uint32_t nz0[8], nz1[8], nz2[8];
-  if (NKR && NEEDP) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 0u, e0, T.noise[0], 8, nz0);
-  if (PHASE == 6) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], 8, nz1);
-  if (PHASE == 6 && NKC) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 2u, e0, T.noise[2], 8, nz2);
+  if (NKR && NEEDP) noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
+  if (PHASE == 6) noise8_u32(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
+  if (PHASE == 6 && NKC) noise8_u32(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
 
   float mold[8];
 #pragma unroll
@@ -1379,12 +1476,12 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
       const float u = (g[i] * rf) * f[i];
       const float ud = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
       if (CODEC == KAON_MOM_BF16) {
-        const uint32_t mb = f2bf(klerp(mold[i], rbf(ud), hp.w1));
+        const uint32_t mb = f2bf(klerp_b<WLO>(mold[i], rbf(ud), hp.w1));
         mbits[i] = mb;
         mf[i] = bf2f(mb);
         d[i] = mf[i];
       } else if (MOM) {
-        mf[i] = klerp(mold[i], ud, hp.w1);
+        mf[i] = klerp_b<WLO>(mold[i], ud, hp.w1);
         d[i] = mf[i];
       } else {
         mf[i] = 0.0f;
@@ -1408,12 +1505,12 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
   // ---- phase 6: requant, cautious, SR write (+ Nekaon climb)
   float mdq[8];
   uint32_t codes[8];
+  float xq[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     if (CODEC == KAON_MOM_INT8) {
-      float xq;
-      codes[i] = q_int8(mf[i], rnew, xq);
-      mdq[i] = xq * newsc;
+      xq[i] = q_int8(mf[i], rnew);
+      mdq[i] = xq[i] * newsc;
     } else if (CODEC == KAON_MOM_4BIT) {
       float x = rintf(div_r64(mf[i], b_r));
       x = fminf(fmaxf(x, -7.0f), 7.0f);
@@ -1431,33 +1528,33 @@ __device__ __forceinline__ void fast_chunk(const KaonTensor& T, const Ws& ws, co
     float dd = d[i];
     if (CAUT) dd = div_r64(d[i] * (d[i] * g[i] > 0.0f ? 1.0f : 0.0f), rden);
     if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
-    o[i] = sr_bf16(p[i] - dd, nz1[i]);
-    if (NKC) o[i] = sr_bf16(bf2f(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+    o[i] = sr_word(p[i] - dd, nz1[i]);
+    if (NKC) o[i] = sr_word(__uint_as_float(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
   }
   ku4 ov;
-  ov.x = o[0] | (o[1] << 16);
-  ov.y = o[2] | (o[3] << 16);
-  ov.z = o[4] | (o[5] << 16);
-  ov.w = o[6] | (o[7] << 16);
-  *(KAON_G ku4*)G((uint16_t*)T.p + e0) = ov;
+  ov.x = pack_hi16(o[0], o[1]);
+  ov.y = pack_hi16(o[2], o[3]);
+  ov.z = pack_hi16(o[4], o[5]);
+  ov.w = pack_hi16(o[6], o[7]);
+  *(KAON_G ku4*)(X.p + 2u * e0) = ov;
   if (CODEC == KAON_MOM_INT8) {
     ku2 mv;
-    mv.x = codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24);
-    mv.y = codes[4] | (codes[5] << 8) | (codes[6] << 16) | (codes[7] << 24);
-    *(KAON_G ku2*)G((int8_t*)T.m + e0) = mv;
+    mv.x = pack_int8x4(xq[0], xq[1], xq[2], xq[3]);
+    mv.y = pack_int8x4(xq[4], xq[5], xq[6], xq[7]);
+    *(KAON_G ku2*)(X.m + e0) = mv;
   } else if (CODEC == KAON_MOM_4BIT) {
     uint32_t v = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
-    *(KAON_G uint32_t*)G((uint8_t*)T.m + (e0 >> 1)) = v;
-    if ((lane % GL) == 0) G(T.m_scale)[blk] = b_new;
+    *(KAON_G uint32_t*)(X.m + (e0 >> 1)) = v;
+    if ((lane & (X.GL - 1)) == 0) *(KAON_G float*)(X.msc + blk4) = b_new;
   } else if (CODEC == KAON_MOM_BF16) {
     ku4 mv;
     mv.x = mbits[0] | (mbits[1] << 16);
     mv.y = mbits[2] | (mbits[3] << 16);
     mv.z = mbits[4] | (mbits[5] << 16);
     mv.w = mbits[6] | (mbits[7] << 16);
-    *(KAON_G ku4*)G((uint16_t*)T.m + e0) = mv;
+    *(KAON_G ku4*)(X.m + 2u * e0) = mv;
   }
 }
 
@@ -1472,13 +1569,25 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
-  const int64_t C = T.C, n = T.n;
-  const int64_t nfull = C >> 3;  // full chunks per row
+  const uint32_t C = (uint32_t)T.C;
+  const int64_t n = T.n;
+  const uint32_t nfull = C >> 3;  // full chunks per row
   const int cplf = (int)((nfull + 63) >> 6);
   const WaveRows wr = wave_rows(it);
-  const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 8;
-  const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
-  const int GL = CODEC == KAON_MOM_4BIT ? (int)(B / 8) : 1;
+  FastCtx X;
+  X.g = (const KAON_G uint8_t*)G(T.g);
+  X.p = (KAON_G uint8_t*)G(T.p);
+  X.m = (KAON_G uint8_t*)G(T.m);
+  X.msc = (KAON_G uint8_t*)G(T.m_scale);
+  X.cf = (const KAON_G uint8_t*)ws.cf(T);
+  X.bamax = (KAON_G uint8_t*)ws.bamax(T);
+  X.boldsc = CODEC == KAON_MOM_4BIT ? (KAON_G uint8_t*)ws.boldsc(T, nblocks4(T)) : X.bamax;
+#pragma unroll
+  for (int s = 0; s < 3; ++s) X.nz[s] = G(T.noise[s]);
+  X.tid = (uint32_t)T.tensor_id;
+  // 4-bit blocks are 8*GL elements with GL | 64, a power of two
+  X.bsh = CODEC == KAON_MOM_4BIT ? __builtin_ctz((uint32_t)T.block4) : 3;
+  X.GL = CODEC == KAON_MOM_4BIT ? (int)(T.block4 >> 3) : 1;
 
   // clip divisor of the tensor (phase 4)
   const float fac = OPT == KAON_OPT_ADAKAON ? ws.scal(T)[0] : 1.0f;
@@ -1488,8 +1597,9 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
     rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
-  const KAON_G float* cfrow = ws.cf(T);
   uint32_t keep = 0;
+  // Adakaon / Nekaon momentum lerp weight 1 - beta1 (Lion has no lerp)
+  const bool wlo = fabsf(hp.w1) < 0.5f;
   // per-row values of the wave's rows, one row per lane
   const int nrows = (int)(wr.re - wr.rb);
   const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
@@ -1497,55 +1607,97 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   const float rf_l = OPT == KAON_OPT_ADAKAON && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
   const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0 ? (PHASE == 5 ? G(T.m_scale)[rl] : ws.roldsc(T)[rl]) : 1.0f;
   const float am_l = CODEC == KAON_MOM_INT8 && PHASE == 6 && nrows > 0 ? __uint_as_float(ws.ramax(T)[rl]) : 0.0f;
-  for (int64_t r = wr.rb; r < wr.re; ++r) {
-    const int j = (int)(r - wr.rb);
-    const float mu = (FLAGS & FF_GC) ? lane_val(mu_l, j) : 0.0f;
-    const float rf = OPT == KAON_OPT_ADAKAON ? lane_val(rf_l, j) : 1.0f;
-    float oldsc = 1.0f, newsc = 1.0f;
-    double rnew = 1.0;
-    if (CODEC == KAON_MOM_INT8) {
-      oldsc = lane_val(sc_l, j);
-      if (PHASE == 6) {
-        newsc = fmaxf(lane_val(am_l, j), 1e-12f) / 127.0f;
-        rnew = rcp64(newsc);
+  settle(mu_l);
+  settle(rf_l);
+  settle(sc_l);
+  settle(am_l);
+  // The wave walks (row, chunk-round) positions in order; the loads of the
+  // next position (possibly in the next row) are issued before the arithmetic
+  // of the current one.  Lanes past the row end load its last chunk again.
+  const int total = nrows * cplf;
+  const uint32_t rowe0 = (uint32_t)wr.rb * C;
+  FastIn buf0, buf1;
+  if (total > 0) {
+    const uint32_t c = min((uint32_t)wr.lane, nfull - 1u);
+    fast_load<OPT, PHASE, CODEC, FLAGS>(buf0, X, rowe0 + 8u * c, 8u * c);
+  }
+  int j = 0, k = 0;
+  float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f;
+  double rnew = 1.0;
+  bool dqf = true;
+  // One position: arithmetic on `cur`, loads of the next position into `nxt`.
+  // Called with the two buffers alternating, so no register copies wait on
+  // the loads in flight.
+  auto step = [&](int t, const FastIn& cur, FastIn& nxt) {
+    const uint32_t rowe = rowe0 + (uint32_t)j * C;
+    if (k == 0) {
+      mu = (FLAGS & FF_GC) ? lane_val(mu_l, j) : 0.0f;
+      rf = OPT == KAON_OPT_ADAKAON ? lane_val(rf_l, j) : 1.0f;
+      if (CODEC == KAON_MOM_INT8) {
+        oldsc = lane_val(sc_l, j);
+        if (PHASE == 6) {
+          newsc = fmaxf(lane_val(am_l, j), 1e-12f) / 127.0f;
+          rnew = rcp64(newsc);
+        }
+      }
+      m128 = -128.0f * oldsc;
+      // fma(ub, sc, -128 sc) is the exact product q*sc while 128*sc is finite
+      dqf = CODEC != KAON_MOM_INT8 || fabsf(oldsc) < 0x1p120f;
+      amax = 0.0f;
+    }
+    int jn = j, kn = k + 1;
+    if (kn == cplf) {
+      kn = 0;
+      ++jn;
+    }
+    {
+      const bool last = t + 1 == total;
+      const uint32_t cn = min((uint32_t)wr.lane + 64u * (uint32_t)(last ? k : kn), nfull - 1u);
+      fast_load<OPT, PHASE, CODEC, FLAGS>(nxt, X, rowe0 + (uint32_t)(last ? j : jn) * C + 8u * cn, 8u * cn);
+    }
+    fast_settle<OPT, PHASE, CODEC, FLAGS>(cur);
+    const uint32_t c = (uint32_t)wr.lane + 64u * (uint32_t)k;
+    const bool full = c < nfull;
+    float camax = 0.0f;
+    if (full) {
+      const uint32_t e0 = rowe + 8u * c;
+      if (wlo) {
+        if (fac == 1.0f && dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, true>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+        else if (dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, true>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+        else
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, true>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+      } else {
+        if (fac == 1.0f && dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, false>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+        else if (dqf)
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, false>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+        else
+          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, false>(
+              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
       }
     }
-    const float m128 = -128.0f * oldsc;
-    // fma(ub, sc, -128 sc) is the exact product q*sc while 128*sc is finite
-    const bool dqf = CODEC != KAON_MOM_INT8 || fabsf(oldsc) < 0x1p120f;
-    float amax = 0.0f;
-    for (int k = 0; k < cplf; ++k) {
-      const int64_t c = wr.lane + 64 * k;
-      const bool full = c < nfull;
-      float camax = 0.0f;
-      if (full) {
-        const int64_t j0 = c * 8;
-        const int64_t e0 = r * C + j0;
-        if (fac == 1.0f && dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                            rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
-        else if (dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                             rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
-        else
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true>(T, ws, hp, r, e0, j0, mu, rf, oldsc, m128, newsc, rnew,
-                                                            rfac, rden, B, nb, GL, wr.lane, keep, camax, cfrow);
-      }
-      if (PHASE == 5 && QUANT) {
-        if (CODEC == KAON_MOM_INT8) {
-          amax = fmaxf(amax, camax);
-        } else {
-          float a = camax;
-          for (int o = GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-          if (full && (wr.lane % GL) == 0) {
-            const int64_t blk = (r * C + c * 8) / B;
-            ws.bamax(T)[blk] = __float_as_uint(a);
-            ws.boldsc(T, nb)[blk] = G(T.m_scale)[blk];
-          }
+    if (PHASE == 5 && QUANT) {
+      if (CODEC == KAON_MOM_INT8) {
+        amax = fmaxf(amax, camax);
+      } else {
+        float a = camax;
+        for (int o = X.GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        if (full && (wr.lane & (X.GL - 1)) == 0) {
+          const uint32_t blk4 = ((rowe + c * 8u) >> X.bsh) * 4u;
+          *(KAON_G uint32_t*)(X.bamax + blk4) = __float_as_uint(a);
+          *(KAON_G float*)(X.boldsc + blk4) = *(const KAON_G float*)(X.msc + blk4);
         }
       }
     }
-    if (CODEC == KAON_MOM_INT8) {
+    if (kn == 0 && CODEC == KAON_MOM_INT8) {
+      const int64_t r = wr.rb + j;
       if (PHASE == 5) {
         const float am = wave_max(amax);
         if (wr.lane == 0) {
@@ -1556,6 +1708,12 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
         G(T.m_scale)[r] = newsc;
       }
     }
+    j = jn;
+    k = kn;
+  };
+  for (int t = 0; t < total; t += 2) {
+    step(t, buf0, buf1);
+    if (t + 1 < total) step(t + 1, buf1, buf0);
   }
   if (PHASE == 5 && CAUT) {
     const uint32_t wsum = wave_sum_u32(keep);

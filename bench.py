@@ -143,7 +143,7 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
 
     inner = getattr(opt, "inner", opt)
     lib = _lib.lib()
-    out: dict[int, list[float]] = {}
+    out: dict[int, list[float]] = {}  # per phase: [sum over plans] per rep
     for key, (_ptrs, plan) in inner._plans.items():
         gid, pdt, gdt = key[:3]
         group = inner.param_groups[gid]
@@ -162,14 +162,15 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
             hp = inner._hyper(group, pdt, gdt, nk, gid)
             fn, phases = lib.kaon_adakaon_phases, (1, 2, 3, 4, 5, 6)
         s = torch.cuda.current_stream().cuda_stream
-        for _ in range(reps):
+        for r in range(reps):
             for ph in phases:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
                 _lib.check(fn(ctypes.byref(plan.launch), ctypes.byref(hp), 1 << ph, s), "phase")
                 e1.record()
                 torch.cuda.synchronize()
-                out.setdefault(ph, []).append(e0.elapsed_time(e1))
+                acc = out.setdefault(ph, [0.0] * reps)
+                acc[r] += e0.elapsed_time(e1)
     return {ph: sum(v) / len(v) for ph, v in out.items()}
 
 

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 3
+#define KAON_ABI_VERSION 4
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -98,7 +98,7 @@ typedef struct KaonTensor {
   int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
   int32_t ns_tr;          /* AdaMuon: Newton-Schulz iterates on the transpose (R > C) */
   int32_t m_pad, k_pad;   /* AdaMuon: min(R,C) and max(R,C) rounded up to KAON_NS_TILE */
-  int32_t pad;
+  int32_t fast_lanes;     /* set by kaon_plan: lanes per row of the phase-5/6 fast kernel (8..64) */
 } KaonTensor;
 
 /* A work item.  Slices: rows [row0, row0 + nrows) of tensor `tensor`, kind =
@@ -142,7 +142,8 @@ typedef struct KaonPlanInfo {
                              bf16 grads with 16-byte rows of <= 4, 10, 24 chunks per lane
                              (prefetching kernels); 3-5 other rows of <= 4, 10, 24 chunks
                              held in registers; 6 streamed rows */
-  int32_t n_fast;         /* slices of elem_items that take the specialized kernels */
+  int32_t n_fast;         /* items at the head of elem_items that take the specialized kernels */
+  int32_t n_elem_items;   /* phase-5/6 items (elem_items) */
   int32_t n_ns_sq;        /* AdaMuon: tiles of the m_pad x m_pad products (ns_sq_items) */
   int32_t n_ns_rect;      /* AdaMuon: tiles of the m_pad x k_pad iterate (ns_rect_items) */
   int64_t ws_words;       /* workspace size in 4-byte words */
@@ -165,14 +166,14 @@ typedef struct KaonPlanArgs {
 typedef struct KaonLaunch {
   const KaonTensor* descs;    /* device copy of the planned descriptors */
   const KaonItem* row_items;  /* device: slices by register class (phase 1) */
-  const KaonItem* elem_items; /* device: the same slices, specialized-kernel ones first */
+  const KaonItem* elem_items; /* device: phase-5/6 items, specialized-kernel ones first */
   const KaonItem* fin_items;  /* device */
   const KaonItem* flat_items; /* device */
   const KaonItem* ns_sq_items;   /* device, AdaMuon */
   const KaonItem* ns_rect_items; /* device, AdaMuon */
   int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
   int32_t row_runs[KAON_ROW_CLASSES];
-  int32_t n_fast;
+  int32_t n_fast, n_elem_items;
   int32_t n_ns_sq, n_ns_rect;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
 } KaonLaunch;
@@ -205,8 +206,11 @@ const char* kaon_last_error(void);
  * pointer-array caches PointerArrayCache / OneDimPointerCache,
  * _fused_triton.py:1183-1320).  descs: host array of n descriptors with
  * pointers, shapes, block4 and tensor_id filled; on return their ws_*,
- * ngroups, sqrt_n and vec_* fields are set.  row_items and elem_items hold
- * n_row_items entries each.  Item arrays may be NULL to query sizes; info is
+ * ngroups, sqrt_n, vec_* and fast_lanes fields are set.  row_items holds
+ * n_row_items slices; elem_items holds n_elem_items phase-5/6 items: the
+ * slices of the generic kernel, and for the specialized kernel slices of
+ * 4 * kind rows whose kind (rows per wave) is a multiple of 64 / fast_lanes.
+ * Item arrays may be NULL to query sizes; info is
  * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
  * factored row longer than KAON_MAX_ROW). */
 int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,

@@ -10,7 +10,9 @@
 //   slices      4 wave groups of RW consecutive rows of one tensor (RW =
 //               max(1, 20 / chunks-per-lane); the whole tensor for a 1-D
 //               param), sorted by register class (row length, grad dtype) so
-//               each class is one launch with a fixed register budget;
+//               each class is one launch with a fixed register budget; the
+//               phase-5/6 items of the specialized kernel round RW up to a
+//               multiple of the rows it works on at once;
 //   fin items   KAON_COLITEM columns of one factored tensor, or its row stats;
 //   flat items  KAON_FLAT_ITEM consecutive elements of one tensor (the MSAM
 //               perturbation).
@@ -46,6 +48,24 @@ int64_t chunks_per_lane(int64_t C) {
 int64_t rows_per_wave(int64_t C) {
   const int64_t rw = KAON_ROW_BUDGET / chunks_per_lane(C);
   return rw < 1 ? 1 : rw;
+}
+
+// Lanes per row of the specialized phase-5/6 kernel: a power of two in
+// [max(8, G), 64] (G = 4-bit lanes per block) whose rounds of chunks cover the
+// row's C/8 chunks with the fewest idle lanes (ties: more lanes).  A wave
+// then works on 64/L rows at a time.
+int32_t fast_lanes(int64_t C, int64_t gl) {
+  const int64_t nfull = C / 8;
+  int32_t best = 64;
+  double best_use = 0.0;
+  for (int32_t L = 64; L >= 8 && L >= gl; L >>= 1) {
+    const double use = (double)nfull / (double)(L * ((nfull + L - 1) / L));
+    if (use > best_use + 1e-12) {
+      best_use = use;
+      best = L;
+    }
+  }
+  return best;
 }
 
 // row class of a slice (phase-1 and phase-3 kernels): 0-2 bf16 grads in
@@ -110,7 +130,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     int64_t size;
     bool fast;
   };
-  std::vector<RowIt> rows;
+  std::vector<RowIt> rows, elems;
   std::vector<KaonItem> fins, flats, ns_sq, ns_rect;
   // the row kernels of an AdaMuon plan read the bf16 orthogonal factor
   const int32_t row_dtype = opt == KAON_OPT_ADAMUON ? (int32_t)KAON_BF16 : g_dtype;
@@ -175,9 +195,24 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     // slices (row items): kind = rows per wave group
     const int cls = row_class(t, row_dtype);
     const bool fast = fast_eligible(*args, t);
+    const size_t first_row_item = rows.size();
     for (int64_t r0 = 0; r0 < t.R; r0 += slice_rows) {
       KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(slice_rows, t.R - r0), (int32_t)rw};
       rows.push_back({it, cls, t.n, fast});
+    }
+    // phase-5/6 items: the slices, except for the specialized kernel, whose
+    // waves take a multiple of 64/L rows (L = fast_lanes)
+    t.fast_lanes = 64;
+    if (fast) {
+      t.fast_lanes = fast_lanes(t.C, codec == KAON_MOM_4BIT ? t.block4 / 8 : 1);
+      const int64_t per = 64 / t.fast_lanes;
+      const int64_t frw = (rw + per - 1) / per * per;
+      for (int64_t r0 = 0; r0 < t.R; r0 += 4 * frw) {
+        KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(4 * frw, t.R - r0), (int32_t)frw};
+        elems.push_back({it, cls, t.n, true});
+      }
+    } else {
+      elems.insert(elems.end(), rows.begin() + (std::ptrdiff_t)first_row_item, rows.end());
     }
     // finalize items (Adakaon / AdaMuon factored second moment)
     if (t.factored && opt != KAON_OPT_LION) {
@@ -189,7 +224,6 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, t.n - e0), 0});
   }
   // elem order: specialized-kernel slices first, each part largest tensors first
-  std::vector<RowIt> elems = rows;
   std::stable_sort(elems.begin(), elems.end(), [](const RowIt& a, const RowIt& b) {
     if (a.fast != b.fast) return a.fast;
     return a.size > b.size;
@@ -201,7 +235,9 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     return a.size > b.size;
   });
   info->n_row_items = (int32_t)rows.size();
+  info->n_fast = 0;
   for (const RowIt& r : elems) info->n_fast += r.fast ? 1 : 0;
+  info->n_elem_items = (int32_t)elems.size();
   if (elem_items)
     for (size_t k = 0; k < elems.size(); ++k) elem_items[k] = elems[k].it;
   info->n_fin_items = (int32_t)fins.size();

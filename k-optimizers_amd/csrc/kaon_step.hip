@@ -1572,7 +1572,6 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   const uint32_t C = (uint32_t)T.C;
   const int64_t n = T.n;
   const uint32_t nfull = C >> 3;  // full chunks per row
-  const int cplf = (int)((nfull + 63) >> 6);
   const WaveRows wr = wave_rows(it);
   FastCtx X;
   X.g = (const KAON_G uint8_t*)G(T.g);
@@ -1611,17 +1610,31 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   settle(rf_l);
   settle(sc_l);
   settle(am_l);
-  // The wave walks (row, chunk-round) positions in order; the loads of the
-  // next position (possibly in the next row) are issued before the arithmetic
-  // of the current one.  Lanes past the row end load its last chunk again.
-  const int total = nrows * cplf;
-  const uint32_t rowe0 = (uint32_t)wr.rb * C;
+  // Each row is worked on by L = T.fast_lanes consecutive lanes (a power of
+  // two), so a wave covers P = 64 / L rows at a time (a row set); chunk
+  // round k of a row is chunks [L k, L k + L) with lane group member cl
+  // taking chunk cl + L k.  The wave walks (row set, round) positions in
+  // order, issuing the loads of the next position before the arithmetic of
+  // the current one.  Lanes of rows past the slice, and of chunks past the
+  // row end, load a valid chunk of their row again and skip the arithmetic.
+  const int lsh = __builtin_ctz((uint32_t)T.fast_lanes);
+  const uint32_t L = 1u << lsh;
+  const int P = 64 >> lsh;
+  const int rounds = (int)((nfull + L - 1) >> lsh);
+  const int nsets = (nrows + P - 1) / P;
+  const int total = nsets * rounds;
+  const int grp = wr.lane >> lsh;             // the lane's row inside a row set
+  const uint32_t cl = (uint32_t)wr.lane & (L - 1u);
   FastIn buf0, buf1;
   if (total > 0) {
-    const uint32_t c = min((uint32_t)wr.lane, nfull - 1u);
-    fast_load<OPT, PHASE, CODEC, FLAGS>(buf0, X, rowe0 + 8u * c, 8u * c);
+    const uint32_t c = min(cl, nfull - 1u);
+    const uint32_t re = (uint32_t)(wr.rb + min(grp, nrows - 1)) * C;
+    fast_load<OPT, PHASE, CODEC, FLAGS>(buf0, X, re + 8u * c, 8u * c);
   }
-  int j = 0, k = 0;
+  int s = 0, k = 0;
+  int rj = 0;        // the lane's row (index into the wave's rows), clamped
+  bool valid = false;
+  uint32_t rowe = 0;
   float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f;
   double rnew = 1.0;
   bool dqf = true;
@@ -1629,15 +1642,19 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   // Called with the two buffers alternating, so no register copies wait on
   // the loads in flight.
   auto step = [&](int t, const FastIn& cur, FastIn& nxt) {
-    const uint32_t rowe = rowe0 + (uint32_t)j * C;
     if (k == 0) {
-      mu = (FLAGS & FF_GC) ? lane_val(mu_l, j) : 0.0f;
-      rf = OPT == KAON_OPT_ADAKAON ? lane_val(rf_l, j) : 1.0f;
+      const int ri = s * P + grp;
+      valid = ri < nrows;
+      rj = min(ri, nrows - 1);
+      rowe = (uint32_t)(wr.rb + rj) * C;
+      mu = (FLAGS & FF_GC) ? __shfl(mu_l, rj) : 0.0f;
+      rf = OPT == KAON_OPT_ADAKAON ? __shfl(rf_l, rj) : 1.0f;
       if (CODEC == KAON_MOM_INT8) {
-        oldsc = lane_val(sc_l, j);
+        oldsc = __shfl(sc_l, rj);
         if (PHASE == 6) {
-          newsc = fmaxf(lane_val(am_l, j), 1e-12f) / 127.0f;
+          newsc = fmaxf(__shfl(am_l, rj), 1e-12f) / 127.0f;
           rnew = rcp64(newsc);
+          if (valid && cl == 0) G(T.m_scale)[wr.rb + rj] = newsc;
         }
       }
       m128 = -128.0f * oldsc;
@@ -1645,19 +1662,20 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
       dqf = CODEC != KAON_MOM_INT8 || fabsf(oldsc) < 0x1p120f;
       amax = 0.0f;
     }
-    int jn = j, kn = k + 1;
-    if (kn == cplf) {
+    int sn = s, kn = k + 1;
+    if (kn == rounds) {
       kn = 0;
-      ++jn;
+      ++sn;
     }
     {
       const bool last = t + 1 == total;
-      const uint32_t cn = min((uint32_t)wr.lane + 64u * (uint32_t)(last ? k : kn), nfull - 1u);
-      fast_load<OPT, PHASE, CODEC, FLAGS>(nxt, X, rowe0 + (uint32_t)(last ? j : jn) * C + 8u * cn, 8u * cn);
+      const int rn = last ? rj : min((sn * P) + grp, nrows - 1);
+      const uint32_t cn = min(cl + L * (uint32_t)(last ? k : kn), nfull - 1u);
+      fast_load<OPT, PHASE, CODEC, FLAGS>(nxt, X, (uint32_t)(wr.rb + rn) * C + 8u * cn, 8u * cn);
     }
     fast_settle<OPT, PHASE, CODEC, FLAGS>(cur);
-    const uint32_t c = (uint32_t)wr.lane + 64u * (uint32_t)k;
-    const bool full = c < nfull;
+    const uint32_t c = cl + L * (uint32_t)k;
+    const bool full = valid && c < nfull;
     float camax = 0.0f;
     if (full) {
       const uint32_t e0 = rowe + 8u * c;
@@ -1687,6 +1705,8 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
       if (CODEC == KAON_MOM_INT8) {
         amax = fmaxf(amax, camax);
       } else {
+        // 4-bit: a block is GL consecutive chunks, GL | L, so its lanes are
+        // one aligned group of GL lanes
         float a = camax;
         for (int o = X.GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
         if (full && (wr.lane & (X.GL - 1)) == 0) {
@@ -1696,19 +1716,16 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
         }
       }
     }
-    if (kn == 0 && CODEC == KAON_MOM_INT8) {
-      const int64_t r = wr.rb + j;
-      if (PHASE == 5) {
-        const float am = wave_max(amax);
-        if (wr.lane == 0) {
-          ws.ramax(T)[r] = __float_as_uint(am);
-          ws.roldsc(T)[r] = oldsc;
-        }
-      } else if (wr.lane == 0) {
-        G(T.m_scale)[r] = newsc;
+    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && kn == 0) {
+      // row maxima of the set: reduce over each row's L lanes
+      float a = amax;
+      for (int o = (int)L / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+      if (valid && cl == 0) {
+        ws.ramax(T)[wr.rb + rj] = __float_as_uint(a);
+        ws.roldsc(T)[wr.rb + rj] = oldsc;
       }
     }
-    j = jn;
+    s = sn;
     k = kn;
   };
   for (int t = 0; t < total; t += 2) {
@@ -1946,7 +1963,7 @@ int launch_elem(const KaonLaunch& L, Ws ws, const KaonHyper& h, int codec, hipSt
   if (n_fast > 0) {
     hipLaunchKernelGGL(ff, dim3(n_fast), dim3(KAON_WG), 0, st, L.descs, L.elem_items, ws, h);
   }
-  const int32_t rest = L.n_row_items - n_fast;
+  const int32_t rest = L.n_elem_items - n_fast;
   if (rest > 0) {
     ElemFn fg = elem_fn<OPT, PHASE>(h.p_dtype, h.g_dtype, codec);
     hipLaunchKernelGGL(fg, dim3(rest), dim3(KAON_WG), 0, st, L.descs, L.elem_items + n_fast, ws, h);

@@ -65,7 +65,7 @@ class Plan:
         L.check(lib.kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None,
                               ctypes.byref(info)), "kaon_plan")
         rows = (L.KaonItem * max(info.n_row_items, 1))()
-        elems = (L.KaonItem * max(info.n_row_items, 1))()
+        elems = (L.KaonItem * max(info.n_elem_items, 1))()
         fins = (L.KaonItem * max(info.n_fin_items, 1))()
         flats = (L.KaonItem * max(info.n_flat_items, 1))()
         nsq = (L.KaonItem * max(info.n_ns_sq, 1))()
@@ -76,7 +76,7 @@ class Plan:
         self.descs = descs
         parts = [bytes(descs)[: ctypes.sizeof(L.KaonTensor) * n],
                  bytes(rows)[: 16 * info.n_row_items],
-                 bytes(elems)[: 16 * info.n_row_items],
+                 bytes(elems)[: 16 * info.n_elem_items],
                  bytes(fins)[: 16 * info.n_fin_items],
                  bytes(flats)[: 16 * info.n_flat_items],
                  bytes(nsq)[: 16 * info.n_ns_sq],
@@ -98,7 +98,7 @@ class Plan:
         la.n_fin_items, la.n_flat_items = info.n_fin_items, info.n_flat_items
         for k in range(L.ROW_CLASSES):
             la.row_runs[k] = info.row_runs[k]
-        la.n_fast = info.n_fast
+        la.n_fast, la.n_elem_items = info.n_fast, info.n_elem_items
         la.n_ns_sq, la.n_ns_rect = info.n_ns_sq, info.n_ns_rect
         la.workspace = self.workspace.data_ptr()
         self.launch = la

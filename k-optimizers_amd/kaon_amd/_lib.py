@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -43,7 +43,7 @@ class KaonTensor(ctypes.Structure):
         ("tensor_id", ctypes.c_int32), ("block4", ctypes.c_int32), ("factored", ctypes.c_int32),
         ("ngroups", ctypes.c_int32), ("sqrt_n", ctypes.c_float),
         ("vec_rows", ctypes.c_int32), ("vec_flat", ctypes.c_int32), ("ns_tr", ctypes.c_int32),
-        ("m_pad", ctypes.c_int32), ("k_pad", ctypes.c_int32), ("pad", ctypes.c_int32),
+        ("m_pad", ctypes.c_int32), ("k_pad", ctypes.c_int32), ("fast_lanes", ctypes.c_int32),
     ]
 
 
@@ -56,7 +56,8 @@ class KaonPlanInfo(ctypes.Structure):
     _fields_ = [("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
-                ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32), ("ws_words", ctypes.c_int64)]
+                ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
+                ("ws_words", ctypes.c_int64)]
 
 
 class KaonPlanArgs(ctypes.Structure):
@@ -71,7 +72,7 @@ class KaonLaunch(ctypes.Structure):
                 ("n_tensors", ctypes.c_int32), ("n_row_items", ctypes.c_int32),
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
-                ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
+                ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
                 ("workspace", ctypes.c_void_p)]
 
 

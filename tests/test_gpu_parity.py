@@ -52,7 +52,8 @@ def _case(opt, shapes, kwargs, steps=3, p="bf16", g="bf16", **kw):
     return c
 
 
-_MIX = [[640, 640, 3, 3], [1280, 2048], [5120, 640], [1280], [77, 33], [3, 5, 7], [1], [9, 1], [2, 2048 * 8]]
+_MIX = [[640, 640, 3, 3], [1280, 2048], [5120, 640], [1280], [77, 33], [3, 5, 7], [1], [9, 1], [2, 2048 * 8],
+        [13, 2880]]
 EXTRA = {
     "ada_int8_mix": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8")),
     "ada_4bit_mix_b64": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="4bit",

@@ -79,20 +79,47 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
     if rc:
         return rc, None, None, None, None, None
     rows = (L.KaonItem * max(info.n_row_items, 1))()
-    elems = (L.KaonItem * max(info.n_row_items, 1))()
+    elems = (L.KaonItem * max(info.n_elem_items, 1))()
     fins = (L.KaonItem * max(info.n_fin_items, 1))()
     flats = (L.KaonItem * max(info.n_flat_items, 1))()
     assert L.lib().kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, None, None,
                              ctypes.byref(info)) == 0
-    # elem order: the same slices, specialized-kernel ones first
+    # phase-5/6 items: specialized-kernel ones first; every row of every
+    # tensor exactly once; the generic kernel's are the slices themselves
     key = lambda it: (it.tensor, it.row0, it.nrows, it.kind)  # noqa: E731
-    assert sorted(key(rows[k]) for k in range(info.n_row_items)) == sorted(key(elems[k]) for k in range(info.n_row_items))
-    for k in range(info.n_row_items):
-        d = descs[elems[k].tensor]
+    slices = sorted(key(rows[k]) for k in range(info.n_row_items))
+    covered = {i: np.zeros(descs[i].R, np.int32) for i in range(n) if descs[i].R * descs[i].C > 0}
+    for k in range(info.n_elem_items):
+        it = elems[k]
+        d = descs[it.tensor]
         fast = (g_dtype == 1 and d.factored == 1 and d.vec_rows == 1 and d.C % 8 == 0
                 and (codec != 4 or (d.block4 % 8 == 0 and d.C % d.block4 == 0 and 64 % (d.block4 // 8) == 0)))
         assert (k < info.n_fast) == fast, (k, d.R, d.C)
+        covered[it.tensor][it.row0:it.row0 + it.nrows] += 1
+        if fast:
+            gl = d.block4 // 8 if codec == 4 else 1
+            assert d.fast_lanes == _fast_lanes(d.C, gl), (d.C, d.fast_lanes)
+            per = 64 // d.fast_lanes
+            assert it.kind % per == 0 and it.kind >= _rows_per_wave(d.C) > it.kind - per
+            assert it.row0 % (4 * it.kind) == 0 and 0 < it.nrows <= 4 * it.kind
+        else:
+            assert key(it) in slices
+    assert all((v == 1).all() for v in covered.values())
     return 0, descs, info, rows, fins, flats
+
+
+def _rows_per_wave(C):
+    return max(1, 20 // _cpl(C))
+
+
+def _fast_lanes(C, gl):
+    """Lanes per row of the specialized phase-5/6 kernel: the power of two in
+    [max(8, gl), 64] with the fewest idle lanes over a row's C/8 chunks, ties
+    to the larger (checked by brute force over the candidates)."""
+    nfull = C // 8
+    use = {L: nfull / (L * -(-nfull // L)) for L in (64, 32, 16, 8) if L >= gl}
+    best = max(use.values())
+    return max(L for L, u in use.items() if u >= best - 1e-12)
 
 
 def _cpl(C):
@@ -292,3 +319,20 @@ def test_adamuon_constructor_validation_mirrors_reference():
     g = opt.param_groups[0]
     assert (g["lr"], g["betas"], g["ns_steps"], g["momentum_dtype"], g["gradient_centralization"]) == \
         (2e-2, (0.95, 0.999), 2, "bfloat16", False)
+
+
+def test_fast_lanes_fill_every_lane_on_sdxl_rows():
+    """Lanes per row of the phase-5/6 specialized kernel for the SDXL row
+    lengths: every chunk round of these rows is full (C/8 = L * rounds)."""
+    want = {1280: 32, 640: 16, 2048: 64, 5120: 64, 11520: 32, 5760: 16, 2880: 8, 320: 8}
+    shapes = [(64, C) for C in want]
+    rc, descs, info, _, _, _ = _plan(shapes, codec=3)
+    assert rc == 0
+    for i, C in enumerate(want):
+        assert descs[i].fast_lanes == want[C], (C, descs[i].fast_lanes)
+        assert (C // 8) % want[C] == 0
+    # 4-bit blocks of 128 (16 chunks) keep at least 16 lanes per row
+    rc, descs, info, _, _, _ = _plan([(64, 2880), (64, 1280)], codec=4, block=128)
+    assert rc == 0
+    assert descs[0].fast_lanes == 64 or descs[0].C % 128 != 0
+    assert descs[1].fast_lanes == 32

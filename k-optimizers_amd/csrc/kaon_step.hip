@@ -473,17 +473,24 @@ __device__ __forceinline__ float lane_val(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
+// Chunk k of the lane in each of the wave group's rows.  Every load is
+// issued unconditionally from a valid address (rows past the group and
+// chunks past the row end load the last ones again, and a wave without rows
+// loads row `rsafe`), so no load waits behind a divergent branch; the caller
+// ignores the extra values.
 template <int CPL, int RW>
-__device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64_t rb, int nrows, int64_t C,
-                                           int nch, int lane, ku4 (&raw)[RW][CPL]) {
+__device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64_t rb, int nrows, int64_t rsafe,
+                                           int64_t C, int nch, int lane, ku4 (&raw)[RW][CPL]) {
+  uint32_t off[CPL];
 #pragma unroll
-  for (int j = 0; j < RW; ++j)
+  for (int k = 0; k < CPL; ++k) off[k] = 16u * (uint32_t)min(lane + 64 * k, nch - 1);
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) {
-      const int c = lane + 64 * k;
-      if (j < nrows && c < nch) raw[j][k] = *(const KAON_G ku4*)G(g + (rb + j) * C + (int64_t)c * 8);
-      else raw[j][k] = ku4{0u, 0u, 0u, 0u};
-    }
+  for (int j = 0; j < RW; ++j) {
+    const int64_t r = nrows > 0 ? rb + min(j, nrows - 1) : rsafe;
+    const KAON_G uint8_t* rowp = (const KAON_G uint8_t*)G(g + r * C);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) raw[j][k] = *(const KAON_G ku4*)(rowp + off[k]);
+  }
 }
 
 // q = (G - mu)^2 (+ eps1 with EPS) of one chunk, G - mu rounded to bf16 (GC
@@ -540,7 +547,7 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
   const float row_old = (mode == 0 && nrows > 0) ? G(T.row)[rl] : 0.0f;
   const void* gsrc = ws.src(T, hp.flags);
   ku4 raw[RW][CPL];
-  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, C, nch, wr.lane, raw);
+  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, it.row0, C, nch, wr.lane, raw);
   // GC means of the wave's rows
   float mu[RW];
   KAON_G float* mu_arr = ws.mu(T);
@@ -613,26 +620,45 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
   const float mu_l = gc ? ws.mu(T)[rl] : 0.0f;
   const float rf_l = ws.rf(T)[rl];
   const void* gsrc = ws.src(T, hp.flags);
+  // chunk-outer: each chunk's column factors are loaded once for the wave's
+  // rows (all up front for short rows, else one chunk ahead); every row
+  // still sums its chunks in lane order
+  const KAON_G uint8_t* cfb = (const KAON_G uint8_t*)ws.cf(T);
+  constexpr int CFD = CPL <= 4 ? CPL : 1;
+  kf4 cfv[CPL][2];
+  auto load_cf = [&](int k) {
+    const uint32_t cb = 32u * (uint32_t)min(wr.lane + 64 * k, nch - 1);
+    cfv[k][0] = *(const KAON_G kf4*)(cfb + cb);
+    cfv[k][1] = *(const KAON_G kf4*)(cfb + cb + 16u);
+  };
+#pragma unroll
+  for (int k = 0; k < CFD; ++k) load_cf(k);
   ku4 raw[RW][CPL];
-  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, C, nch, wr.lane, raw);
-  const KAON_G float* cf = ws.cf(T);
+  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, it.row0, C, nch, wr.lane, raw);
+  float muj[RW], rfj[RW], a[RW];
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
-    if (j >= nrows) continue;
-    const float muj = lane_val(mu_l, j), rfj = lane_val(rf_l, j);
-    float a = 0.0f;
+    const int jj = min(j, nrows - 1);
+    muj[j] = lane_val(mu_l, jj);
+    rfj[j] = lane_val(rf_l, jj);
+    a[j] = 0.0f;
+  }
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) {
-      const int c = wr.lane + 64 * k;
-      if (c < nch) {
-        const kf4 c0 = *(const KAON_G kf4*)(cf + (int64_t)c * 8), c1 = *(const KAON_G kf4*)(cf + (int64_t)c * 8 + 4);
-        const float f[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  for (int k = 0; k < CPL; ++k) {
+    const int c = wr.lane + 64 * k;
+    if (k + CFD < CPL) load_cf(k + CFD);
+    const kf4 c0 = cfv[k][0], c1 = cfv[k][1];
+    const float f[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    if (c < nch) {
+#pragma unroll
+      for (int j = 0; j < RW; ++j) {
+        if (j >= nrows) continue;
         float x[8];
         unpack8(raw[j][k], x);
         if (gc) {
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            float a0 = x[i] - muj, a1 = x[i + 1] - muj;
+            float a0 = x[i] - muj[j], a1 = x[i + 1] - muj[j];
             rbf2(a0, a1);
             x[i] = a0;
             x[i + 1] = a1;
@@ -640,12 +666,16 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float u = (x[i] * rfj) * f[i];
-          a = a + u * u;
+          const float u = (x[i] * rfj[j]) * f[i];
+          a[j] = a[j] + u * u;
         }
       }
     }
-    const float s = wave_csum(a);
+  }
+#pragma unroll
+  for (int j = 0; j < RW; ++j) {
+    if (j >= nrows) continue;
+    const float s = wave_csum(a[j]);
     if (wr.lane == 0) ws.rs(T)[wr.rb + j] = s;
   }
 }

@@ -84,7 +84,7 @@ typedef struct KaonTensor {
   /* workspace offsets, in 4-byte words from the workspace base (kaon_plan) */
   int64_t ws_row;         /* 5 arrays of R words: mu, rf, rs, amax, oldscale */
   int64_t ws_col;         /* cf [C] */
-  int64_t ws_part;        /* column partials [ngroups][C], one row per slice */
+  int64_t ws_part;        /* column partials [ngroups][C], one row per run */
   int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
   int64_t ws_scal;        /* 4 words: fac, keep-count, spare, spare */
   int64_t ws_aux;         /* AdaMuon: Newton-Schulz buffers, bf16: M then O [R*C], the iterate
@@ -92,7 +92,7 @@ typedef struct KaonTensor {
   int32_t tensor_id;      /* SR counter field: index in the optimizer's param list */
   int32_t block4;         /* 4-bit block size (m_block) */
   int32_t factored;       /* ndim >= 2 */
-  int32_t ngroups;        /* number of slices */
+  int32_t ngroups;        /* number of runs (column partials) */
   float sqrt_n;           /* (float)sqrt((double)n), the rms divisor (_backend.py:45-47) */
   int32_t vec_rows;       /* 16-byte vector path for row chunks (C % 8 == 0 or one row, aligned) */
   int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
@@ -101,8 +101,9 @@ typedef struct KaonTensor {
   int32_t fast_lanes;     /* set by kaon_plan: lanes per row of the phase-5/6 fast kernel (8..64) */
 } KaonTensor;
 
-/* A work item.  Slices: rows [row0, row0 + nrows) of tensor `tensor`, kind =
- * rows per wave group.  Finalize items: kind 0 = columns [row0, row0+nrows),
+/* A work item.  Runs and slices: rows [row0, row0 + nrows) of tensor
+ * `tensor`, kind = rows per wave group (RW); a slice is at most 4 * RW rows, a
+ * run at most KAON_RUN slices.  Finalize items: kind 0 = columns [row0, row0+nrows),
  * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows).
  * Newton-Schulz tiles: row0 = tile row, nrows = tile column (KAON_NS_TILE
  * square tiles of the padded matrices). */
@@ -117,9 +118,11 @@ typedef struct KaonItem {
  * oracle.  Row sums: 64 lanes, lane l adds the 8-element chunks l, l+64, ...
  * in order, then an xor butterfly.  Column sums: wave groups of
  * RW = max(1, KAON_ROW_BUDGET / chunks-per-lane) consecutive rows (summed in
- * row order), slices of 4 wave groups (folded in order), slices added in
- * order.  One slice is one workgroup of 4 wave64. */
+ * row order), slices of 4 wave groups (folded in order), runs of KAON_RUN
+ * slices (added in order, one column partial per run), runs added in order.
+ * A slice is one pass of a workgroup of 4 wave64; a run is one workgroup. */
 #define KAON_ROW_BUDGET 20
+#define KAON_RUN 4
 /* Columns per column-finalize work item. */
 #define KAON_COLITEM 2048
 
@@ -135,10 +138,10 @@ typedef struct KaonItem {
  */
 typedef struct KaonPlanInfo {
   int32_t n_tensors;
-  int32_t n_row_items;    /* slices, sorted by phase-1 register class (row_items) */
+  int32_t n_row_items;    /* runs, sorted by phase-1 register class (row_items) */
   int32_t n_fin_items;    /* finalize items (phase 2) */
   int32_t n_flat_items;   /* flat items of KAON_FLAT_ITEM elements (MSAM perturbation) */
-  int32_t row_runs[KAON_ROW_CLASSES]; /* slices per row class, in row_items order: classes 0-2
+  int32_t row_runs[KAON_ROW_CLASSES]; /* runs per row class, in row_items order: classes 0-2
                              bf16 grads with 16-byte rows of <= 4, 10, 24 chunks per lane
                              (prefetching kernels); 3-5 other rows of <= 4, 10, 24 chunks
                              held in registers; 6 streamed rows */
@@ -165,7 +168,7 @@ typedef struct KaonPlanArgs {
 /* Device-side tables of one planned group, passed to every step entry point. */
 typedef struct KaonLaunch {
   const KaonTensor* descs;    /* device copy of the planned descriptors */
-  const KaonItem* row_items;  /* device: slices by register class (phase 1) */
+  const KaonItem* row_items;  /* device: runs by register class (phases 1, 3, AdaMuon momentum) */
   const KaonItem* elem_items; /* device: phase-5/6 items, specialized-kernel ones first */
   const KaonItem* fin_items;  /* device */
   const KaonItem* flat_items; /* device */
@@ -207,9 +210,9 @@ const char* kaon_last_error(void);
  * _fused_triton.py:1183-1320).  descs: host array of n descriptors with
  * pointers, shapes, block4 and tensor_id filled; on return their ws_*,
  * ngroups, sqrt_n, vec_* and fast_lanes fields are set.  row_items holds
- * n_row_items slices; elem_items holds n_elem_items phase-5/6 items: the
- * slices of the generic kernel, and for the specialized kernel slices of
- * 4 * kind rows whose kind (rows per wave) is a multiple of 64 / fast_lanes.
+ * n_row_items runs; elem_items holds n_elem_items phase-5/6 items: slices for
+ * the generic kernel, and for the specialized kernel slices of 4 * kind rows
+ * whose kind (rows per wave) is a multiple of 64 / fast_lanes.
  * Item arrays may be NULL to query sizes; info is
  * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
  * factored row longer than KAON_MAX_ROW). */

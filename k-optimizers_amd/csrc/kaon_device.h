@@ -74,6 +74,16 @@ __device__ __forceinline__ float ksign(float x) { return x > 0.0f ? 1.0f : (x < 
 __device__ __forceinline__ void settle(uint32_t v) { asm volatile("" : : "v"(v)); }
 __device__ __forceinline__ void settle(float v) { asm volatile("" : : "v"(v)); }
 
+// The same pointer, opaque to the optimizer: loads through it are not hoisted
+// out of the enclosing loop (used where keeping a loop-invariant load's result
+// live across iterations would cost more registers than loading it again).
+template <class T>
+__device__ __forceinline__ T* opaque(T* p) {
+  uint64_t v = (uint64_t)p;
+  asm volatile("" : "+s"(v));
+  return (T*)v;
+}
+
 // ------------------------------------------------------------------ Philox
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11), published multipliers and
 // Weyl increments.  SR noise: key = (seed lo32, step), counter = (chunk lo,

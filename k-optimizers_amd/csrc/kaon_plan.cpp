@@ -7,12 +7,13 @@
 // Here one descriptor per tensor carries every pointer and shape, and the plan
 // adds what the HIP kernels need: a workspace layout for the per-row /
 // per-column / per-block intermediates and three work-item tables.
-//   slices      4 wave groups of RW consecutive rows of one tensor (RW =
-//               max(1, 20 / chunks-per-lane); the whole tensor for a 1-D
-//               param), sorted by register class (row length, grad dtype) so
-//               each class is one launch with a fixed register budget; the
-//               phase-5/6 items of the specialized kernel round RW up to a
-//               multiple of the rows it works on at once;
+//   runs        KAON_RUN slices of 4 wave groups of RW consecutive rows of
+//               one tensor (RW = max(1, 20 / chunks-per-lane); the whole
+//               tensor for a 1-D param), sorted by register class (row
+//               length, grad dtype) so each class is one launch with a fixed
+//               register budget;
+//   elem items  phase-5/6 slices; those of the specialized kernel round RW up
+//               to a multiple of the rows it works on at once;
 //   fin items   KAON_COLITEM columns of one factored tensor, or its row stats;
 //   flat items  KAON_FLAT_ITEM consecutive elements of one tensor (the MSAM
 //               perturbation).
@@ -152,7 +153,8 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     t.sqrt_n = (float)std::sqrt((double)(t.n > 1 ? t.n : 1));
     const int64_t rw = rows_per_wave(t.C);
     const int64_t slice_rows = 4 * rw;
-    t.ngroups = (int32_t)((t.R + slice_rows - 1) / slice_rows);
+    const int64_t run_rows = KAON_RUN * slice_rows;
+    t.ngroups = (int32_t)((t.R + run_rows - 1) / run_rows);
     const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
                     aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16);
     t.vec_flat = al ? 1 : 0;
@@ -192,12 +194,11 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       }
     }
     if (t.n == 0) continue;
-    // slices (row items): kind = rows per wave group
+    // runs (row items): kind = rows per wave group
     const int cls = row_class(t, row_dtype);
     const bool fast = fast_eligible(*args, t);
-    const size_t first_row_item = rows.size();
-    for (int64_t r0 = 0; r0 < t.R; r0 += slice_rows) {
-      KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(slice_rows, t.R - r0), (int32_t)rw};
+    for (int64_t r0 = 0; r0 < t.R; r0 += run_rows) {
+      KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(run_rows, t.R - r0), (int32_t)rw};
       rows.push_back({it, cls, t.n, fast});
     }
     // phase-5/6 items: the slices, except for the specialized kernel, whose
@@ -212,7 +213,10 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
         elems.push_back({it, cls, t.n, true});
       }
     } else {
-      elems.insert(elems.end(), rows.begin() + (std::ptrdiff_t)first_row_item, rows.end());
+      for (int64_t r0 = 0; r0 < t.R; r0 += slice_rows) {
+        KaonItem it{i, (int32_t)r0, (int32_t)std::min<int64_t>(slice_rows, t.R - r0), (int32_t)rw};
+        elems.push_back({it, cls, t.n, false});
+      }
     }
     // finalize items (Adakaon / AdaMuon factored second moment)
     if (t.factored && opt != KAON_OPT_LION) {

@@ -109,6 +109,23 @@ __device__ __forceinline__ WaveRows wave_rows(const KaonItem& it) {
   return wr;
 }
 
+// Slice sl of a run item (rows [row0 + 4 RW sl, ...), RW = kind) and the
+// number of slices in the run.
+__device__ __forceinline__ KaonItem slice_item(const KaonItem& run, int sl) {
+  KaonItem s = run;
+  const int span = 4 * run.kind;
+  s.row0 = run.row0 + sl * span;
+  s.nrows = min(span, run.nrows - sl * span);
+  return s;
+}
+__device__ __forceinline__ int run_slices(const KaonItem& run) {
+  return (run.nrows + 4 * run.kind - 1) / (4 * run.kind);
+}
+// Column partial of a run: one row of C floats per run.
+__device__ __forceinline__ KAON_G float* run_part(const Ws& ws, const KaonTensor& T, const KaonItem& run) {
+  return ws.part(T) + (int64_t)(run.row0 / (KAON_RUN * 4 * run.kind)) * T.C;
+}
+
 // Chunks of a row: the element range [8c, 8c+8) clipped to the row length.
 __device__ __forceinline__ int chunk_cnt(int64_t c, int64_t C) {
   const int64_t j0 = c * 8;
@@ -148,7 +165,6 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const int cpl = (int)((nch + 63) >> 6);
   const bool vec = T.vec_rows != 0;
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
-  const WaveRows wr = wave_rows(it);
 
   if (!T.factored) {
     // v = lerp(v, g*g (+eps1), 1-beta2) over the single row (adakaon.py:990-995)
@@ -174,6 +190,11 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   if (mode == 1 && !gc) return;
   KAON_G float* mu_arr = ws.mu(T);
   const int RW = it.kind;
+  KAON_G float* part = run_part(ws, T, it);
+  const int nsl = run_slices(it);
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nsl; ++sl) {
+  const WaveRows wr = wave_rows(slice_item(it, sl));
 
   // registers: row buffer (CPL chunks) and the wave-group column partial
   constexpr int NB = CPL > 0 ? CPL : 1;
@@ -273,7 +294,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
       if (wr.lane == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
     }
   }
-  if (mode == 1) return;
+  if (mode == 1) continue;
 
   // fold the wave-group partials in group order into the slice partial
   const bool has_rows = wr.re > wr.rb;
@@ -322,8 +343,10 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
     }
     __syncthreads();
   }
-  KAON_G float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
-  for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = lds_col[j];
+  // the run partial: the slice partials added in slice order
+  for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = sl == 0 ? lds_col[j] : part[j] + lds_col[j];
+  __syncthreads();  // lds_col is reused by the next slice
+  }
 }
 
 // =============================================================== phase 2
@@ -380,7 +403,10 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
 template <int GT>
 __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D,
                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  const KaonItem it = items[blockIdx.x];
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
   const KaonTensor& T = D[it.tensor];
   const void* gsrc = ws.src(T, hp.flags);
   const int64_t C = T.C;
@@ -522,23 +548,51 @@ __device__ __forceinline__ void seg_put(float (*seg)[512], int w, int lane, cons
   d[0] = kf4{v[0], v[1], v[2], v[3]};
   d[1] = kf4{v[4], v[5], v[6], v[7]};
 }
-__device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0, int64_t C, KAON_G float* part) {
-  const int c = 2 * (int)threadIdx.x;
+// The run partial (the slice partials added in slice order) is kept in
+// `racc` (LDS, C floats; each thread owns its two columns) and stored to
+// `part` after the last slice, or, with racc == nullptr, accumulated in
+// `part` itself.
+__device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0, int64_t C, KAON_G float* part,
+                                         bool acc, bool last, int tid, float* racc) {
+  const int c = 2 * tid;
   if (col0 + c >= C) return;  // C % 8 == 0: both columns are in range or neither
   float a0 = seg[0][c], a1 = seg[0][c + 1];
   for (int w = 1; w < nw; ++w) {
     a0 = a0 + seg[w][c];
     a1 = a1 + seg[w][c + 1];
   }
-  *(KAON_G ku2*)(part + col0 + c) = ku2{__float_as_uint(a0), __float_as_uint(a1)};
+  KAON_G ku2* dst = (KAON_G ku2*)(part + col0 + c);
+  if (racc) {
+    float* r = racc + col0 + c;
+    if (acc) {
+      a0 = r[0] + a0;
+      a1 = r[1] + a1;
+    }
+    if (!last) {
+      r[0] = a0;
+      r[1] = a1;
+      return;
+    }
+  } else if (acc) {
+    const ku2 o = *dst;
+    a0 = __uint_as_float(o.x) + a0;
+    a1 = __uint_as_float(o.y) + a1;
+  }
+  *dst = ku2{__float_as_uint(a0), __float_as_uint(a1)};
 }
 
 template <int CPL, int RW, bool EPS>
 __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
-                                              const KaonHyper& hp, int mode, float (*seg)[4][512]) {
+                                              const KaonHyper& hp, int mode, float (*seg)[4][512],
+                                              KAON_G float* part, bool acc, bool last, float* racc) {
   const int64_t C = T.C;
   const int nch = (int)(C >> 3);
-  const WaveRows wr = wave_rows(it);
+  WaveRows wr = wave_rows(it);
+  // recomputed per slice: values derived from the lane are not kept live
+  // across the slice loop
+  asm volatile("" : "+v"(wr.lane));
+  int tid = (int)threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int nrows = (int)(wr.re - wr.rb);
   const bool gc = (hp.flags & KAON_F_GC) != 0;
   const float e1 = hp.eps1;
@@ -572,7 +626,6 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
   // q = (G - mu)^2 (+eps1) once per element: into the row sums (lane order:
   // chunk by chunk) and the wave group's column partial (row order)
   const int nw = (int)min<int64_t>(4, ((int64_t)it.nrows + RW - 1) / RW);
-  KAON_G float* part = ws.part(T) + (int64_t)(it.row0 / (4 * RW)) * C;
   float a2[RW];
 #pragma unroll
   for (int j = 0; j < RW; ++j) a2[j] = 0.0f;
@@ -596,7 +649,7 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
       seg_put(seg[k & 1], wr.w, wr.lane, v);
     }
     __syncthreads();
-    seg_fold(seg[k & 1], nw, (int64_t)k * 512, C, part);
+    seg_fold(seg[k & 1], nw, (int64_t)k * 512, C, part, acc, last, tid, racc);
   }
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
@@ -680,6 +733,7 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
   }
 }
 
+
 // Row class 0: 1-4 chunks per lane, 1 class 1: 5-10, class 2: 11-24; the
 // body is specialized on the exact chunks per lane and its rows per wave
 // group (RW = max(1, KAON_ROW_BUDGET / CPL)).
@@ -713,21 +767,52 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
   }
 
 template <int CLS, bool EPS>
-__global__ __launch_bounds__(KAON_WG) void k_pf_stats(const KaonTensor* __restrict__ D,
-                                                      const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
-                                                      int mode) {
-  __shared__ __attribute__((aligned(16))) float seg[2][4][512];
+__device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, const KaonItem* __restrict__ items,
+                                             const Ws& ws, const KaonHyper& hp, int mode, float (*seg)[4][512],
+                                             float* racc) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   zero_accumulators(T, it, ws, hp.codec);
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
-  KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS, T, it, ws, hp, mode, seg)
+  KAON_G float* part = run_part(ws, T, it);
+  const int nsl = run_slices(it);
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nsl; ++sl) {
+    if (sl > 0) __syncthreads();  // the LDS fold buffers are reused
+    const KaonItem si = slice_item(it, sl);
+    KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS, T, si, ws, hp, mode, seg, part, sl > 0, sl + 1 == nsl,
+                   racc)
+  }
 }
 
+// Classes 0 and 1 are held to 4 waves per SIMD (128 VGPRs), which their
+// bodies fit without spilling, and keep the run partial in LDS (rows of at
+// most 2048 and 5120 elements); class 2 rows take more registers and
+// accumulate the run partial in the workspace.
+template <int CLS, bool EPS>
+__global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __restrict__ D,
+                                                         const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
+                                                         int mode) {
+  __shared__ __attribute__((aligned(16))) float seg[2][4][512];
+  __shared__ __attribute__((aligned(16))) float racc[CLS == 0 ? 4 * 512 : 10 * 512];
+  pf_stats_run<CLS, EPS>(D, items, ws, hp, mode, seg, racc);
+}
+template <bool EPS>
+__global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __restrict__ D,
+                                                           const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
+                                                           int mode) {
+  __shared__ __attribute__((aligned(16))) float seg[2][4][512];
+  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, nullptr);
+}
+
+// One slice per workgroup: workgroup b takes slice b % KAON_RUN of run b / KAON_RUN.
 template <int CLS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_ss(const KaonTensor* __restrict__ D,
                                                    const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  const KaonItem it = items[blockIdx.x];
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
   const KaonTensor& T = D[it.tensor];
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
   KAON_PF_SWITCH(CLS, pf_ss_body, , T, it, ws, hp)
@@ -867,7 +952,10 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
   const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 1;
   const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
   KAON_G uint16_t* mo = G(ws.mo(T));
-  const WaveRows wr = wave_rows(it);
+  const int nsl = run_slices(it);
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nsl; ++sl) {
+  const WaveRows wr = wave_rows(slice_item(it, sl));
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     float mu = 0.0f;
     if (gc) {
@@ -944,6 +1032,7 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
     }
     const float s2 = wave_csum(sq);
     if (wr.lane == 0) ws.rs(T)[r] = s2;
+  }
   }
 }
 
@@ -2013,7 +2102,7 @@ StatsFn stats_fn_gt(int cls, bool eps) {
   switch (cls) {
     case 0: return eps ? k_pf_stats<0, true> : k_pf_stats<0, false>;
     case 1: return eps ? k_pf_stats<1, true> : k_pf_stats<1, false>;
-    case 2: return eps ? k_pf_stats<2, true> : k_pf_stats<2, false>;
+    case 2: return eps ? k_pf_stats_wide<true> : k_pf_stats_wide<false>;
     case 3: return k_stats<GT, 4>;
     case 4: return k_stats<GT, 10>;
     case 5: return k_stats<GT, 24>;
@@ -2067,11 +2156,11 @@ int launch_ss(const KaonLaunch& L, Ws ws, const KaonHyper& h, hipStream_t st) {
     if (cnt <= 0) continue;
     if (h.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
     SsFn fn = cls == 0 ? (SsFn)k_pf_ss<0> : cls == 1 ? (SsFn)k_pf_ss<1> : (SsFn)k_pf_ss<2>;
-    hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), 0, st, L.descs, L.row_items + off, ws, h);
+    hipLaunchKernelGGL(fn, dim3(cnt * KAON_RUN), dim3(KAON_WG), 0, st, L.descs, L.row_items + off, ws, h);
     off += cnt;
   }
   if (L.n_row_items > off)
-    hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3(L.n_row_items - off), dim3(KAON_WG), 0, st, L.descs,
+    hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3((L.n_row_items - off) * KAON_RUN), dim3(KAON_WG), 0, st, L.descs,
                        L.row_items + off, ws, h);
   return check_launch("kaon: k_ss launch");
 }

@@ -39,8 +39,9 @@
  *   COLSUM_j over R rows with row length C: cpl = ceil(ceil(C/8)/64) chunks
  *     per lane, RW = max(1, 20 / cpl) rows per wave group; a wave group sums
  *     its RW consecutive rows in row order; a slice is 4 consecutive wave
- *     groups whose sums are folded in group order; the slice sums are added
- *     in slice order (every partial starts from +0.0f).
+ *     groups whose sums are folded in group order; a run is 4 consecutive
+ *     slices whose sums are added in slice order; the run sums are added in
+ *     run order (every partial starts from +0.0f).
  *   Sum of squares for the RMS clip: CSUM over each row (C elements), then
  *     CSUM over the R row results.
  */
@@ -53,6 +54,7 @@
 #define KAON_CHUNK 8
 #define KAON_ROW_BUDGET 20   /* chunks per lane a wave group spans */
 #define KAON_WAVES 4         /* wave groups per slice */
+#define KAON_RUN 4           /* slices per run (one column partial per run) */
 
 /* dtype codes shared with the HIP library and oracle.py */
 enum { KO_F32 = 0, KO_BF16 = 1 };
@@ -416,6 +418,7 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
     float* q = (float*)malloc(sizeof(float) * (size_t)C);
     float* pw = (float*)calloc((size_t)C, sizeof(float));  /* wave-group partial */
     float* ps = (float*)calloc((size_t)C, sizeof(float));  /* slice partial */
+    float* pr = (float*)calloc((size_t)C, sizeof(float));  /* run partial */
     float* colsum = (float*)calloc((size_t)C, sizeof(float));
     for (int64_t r = 0; r < R; ++r) {
         for (int64_t j = 0; j < C; ++j) {
@@ -430,8 +433,12 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
         if (end_group) {
             for (int64_t j = 0; j < C; ++j) { ps[j] = ps[j] + pw[j]; pw[j] = 0.0f; }
             int64_t g = r / RW;
-            if ((g + 1) % KAON_WAVES == 0 || r + 1 == R)
-                for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + ps[j]; ps[j] = 0.0f; }
+            if ((g + 1) % KAON_WAVES == 0 || r + 1 == R) {
+                for (int64_t j = 0; j < C; ++j) { pr[j] = pr[j] + ps[j]; ps[j] = 0.0f; }
+                int64_t s = g / KAON_WAVES;
+                if ((s + 1) % KAON_RUN == 0 || r + 1 == R)
+                    for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + pr[j]; pr[j] = 0.0f; }
+            }
         }
     }
     float* cf = (float*)malloc(sizeof(float) * (size_t)C);
@@ -444,7 +451,7 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
         float rf = ko_rsqrt(t->row[r] / rm);
         for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf) * cf[j];
     }
-    free(q); free(pw); free(ps); free(colsum); free(cf);
+    free(q); free(pw); free(ps); free(pr); free(colsum); free(cf);
 }
 
 /* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):

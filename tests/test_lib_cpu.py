@@ -85,9 +85,7 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
     assert L.lib().kaon_plan(ctypes.byref(args), descs, n, rows, elems, fins, flats, None, None,
                              ctypes.byref(info)) == 0
     # phase-5/6 items: specialized-kernel ones first; every row of every
-    # tensor exactly once; the generic kernel's are the slices themselves
-    key = lambda it: (it.tensor, it.row0, it.nrows, it.kind)  # noqa: E731
-    slices = sorted(key(rows[k]) for k in range(info.n_row_items))
+    # tensor exactly once; the generic kernel's are slices of 4 wave groups
     covered = {i: np.zeros(descs[i].R, np.int32) for i in range(n) if descs[i].R * descs[i].C > 0}
     for k in range(info.n_elem_items):
         it = elems[k]
@@ -103,7 +101,8 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
             assert it.kind % per == 0 and it.kind >= _rows_per_wave(d.C) > it.kind - per
             assert it.row0 % (4 * it.kind) == 0 and 0 < it.nrows <= 4 * it.kind
         else:
-            assert key(it) in slices
+            assert it.kind == _rows_per_wave(d.C) if d.factored else it.nrows == 1
+            assert it.row0 % (4 * it.kind) == 0 and 0 < it.nrows <= 4 * it.kind
     assert all((v == 1).all() for v in covered.values())
     return 0, descs, info, rows, fins, flats
 
@@ -145,8 +144,9 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
             it = rows[off + k]
             d = descs[it.tensor]
             seen[it.tensor][it.row0:it.row0 + it.nrows] += 1
+            # runs of KAON_RUN = 4 slices of 4 wave groups of RW rows
             assert it.kind == O.rows_per_wave(d.C)
-            assert it.nrows <= 4 * it.kind and it.row0 % (4 * it.kind) == 0
+            assert it.nrows <= 16 * it.kind and it.row0 % (16 * it.kind) == 0
             cpl = _cpl(d.C)
             prefetch = g_dtype == 1 and d.factored and d.vec_rows and d.C % 8 == 0 and cpl <= 24
             if not d.factored:
@@ -183,7 +183,7 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
             spans.append((d.ws_part, d.ws_part + d.ngroups * d.C))
         spans.append((d.ws_blk, d.ws_blk + 2 * nb))
         spans.append((d.ws_scal, d.ws_scal + 4))
-        assert d.ngroups == -(-d.R // (4 * O.rows_per_wave(d.C)))
+        assert d.ngroups == -(-d.R // (16 * O.rows_per_wave(d.C)))
         assert d.sqrt_n == np.float32(np.sqrt(float(max(d.n, 1))))
     spans.sort()
     for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):

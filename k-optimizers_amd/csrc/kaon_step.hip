@@ -86,6 +86,19 @@ struct Ws {
   }
 };
 
+// Streaming accesses: the gradient, parameter and momentum streams of a
+// 2.6B-param step are far larger than the caches, so they are loaded and
+// stored as non-temporal accesses (NT); small reused arrays (column
+// factors, per-row values) are not.
+template <bool NT, class V>
+__device__ __forceinline__ V ld_stream(const KAON_G V* p) {
+  return NT ? __builtin_nontemporal_load(p) : *p;
+}
+template <class V>
+__device__ __forceinline__ void st_stream(KAON_G V* p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 template <int DT>
 __device__ __forceinline__ float round_to(float x) {
   return DT == KAON_BF16 ? rbf(x) : x;
@@ -515,7 +528,7 @@ __device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64
     const int64_t r = nrows > 0 ? rb + min(j, nrows - 1) : rsafe;
     const KAON_G uint8_t* rowp = (const KAON_G uint8_t*)G(g + r * C);
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) raw[j][k] = *(const KAON_G ku4*)(rowp + off[k]);
+    for (int k = 0; k < CPL; ++k) raw[j][k] = ld_stream<true>((const KAON_G ku4*)(rowp + off[k]));
   }
 }
 
@@ -1473,11 +1486,11 @@ template <int OPT, int PHASE, int CODEC, int FLAGS>
 __device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t e0, uint32_t j0) {
   constexpr bool NEEDP = PHASE == 6 || (FLAGS & FF_WD);
   const ku4 z4 = ku4{0u, 0u, 0u, 0u};
-  in.g = *(const KAON_G ku4*)(X.g + 2u * e0);
-  in.p = NEEDP ? *(const KAON_G ku4*)(X.p + 2u * e0) : z4;
-  in.m8 = CODEC == KAON_MOM_INT8 ? *(const KAON_G ku2*)(X.m + e0) : ku2{0u, 0u};
-  in.m4 = CODEC == KAON_MOM_4BIT ? *(const KAON_G uint32_t*)(X.m + (e0 >> 1)) : 0u;
-  in.m16 = CODEC == KAON_MOM_BF16 ? *(const KAON_G ku4*)(X.m + 2u * e0) : z4;
+  in.g = ld_stream<true>((const KAON_G ku4*)(X.g + 2u * e0));
+  in.p = NEEDP ? ld_stream<true>((const KAON_G ku4*)(X.p + 2u * e0)) : z4;
+  in.m8 = CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m + e0)) : ku2{0u, 0u};
+  in.m4 = CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m + (e0 >> 1))) : 0u;
+  in.m16 = CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m + 2u * e0)) : z4;
   if (OPT == KAON_OPT_ADAKAON) {
     in.c0 = *(const KAON_G kf4*)(X.cf + 4u * j0);
     in.c1 = *(const KAON_G kf4*)(X.cf + 4u * j0 + 16u);
@@ -1655,12 +1668,12 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   ov.y = pack_hi16(o[2], o[3]);
   ov.z = pack_hi16(o[4], o[5]);
   ov.w = pack_hi16(o[6], o[7]);
-  *(KAON_G ku4*)(X.p + 2u * e0) = ov;
+  st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
   if (CODEC == KAON_MOM_INT8) {
     ku2 mv;
     mv.x = pack_int8x4(xq[0], xq[1], xq[2], xq[3]);
     mv.y = pack_int8x4(xq[4], xq[5], xq[6], xq[7]);
-    *(KAON_G ku2*)(X.m + e0) = mv;
+    st_stream((KAON_G ku2*)(X.m + e0), mv);
   } else if (CODEC == KAON_MOM_4BIT) {
     uint32_t v = 0;
 #pragma unroll
@@ -1673,7 +1686,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     mv.y = mbits[2] | (mbits[3] << 16);
     mv.z = mbits[4] | (mbits[5] << 16);
     mv.w = mbits[6] | (mbits[7] << 16);
-    *(KAON_G ku4*)(X.m + 2u * e0) = mv;
+    st_stream((KAON_G ku4*)(X.m + 2u * e0), mv);
   }
 }
 

@@ -2000,17 +2000,20 @@ __global__ void k_sr_noise(uint16_t* __restrict__ out, int64_t n, uint64_t seed,
   }
 }
 
-__global__ __launch_bounds__(KAON_WG) void k_copy(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n16) {
+__global__ __launch_bounds__(KAON_WG) void k_copy(const ku4* __restrict__ src_, ku4* __restrict__ dst_, int64_t n16) {
+  const KAON_G ku4* src = G(src_);
+  KAON_G ku4* dst = G(dst_);
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (; i + 3 * stride < n16; i += 4 * stride) {
-    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-    dst[i] = a;
-    dst[i + stride] = b;
-    dst[i + 2 * stride] = c;
-    dst[i + 3 * stride] = d;
+    const ku4 a = ld_stream<true>(src + i), b = ld_stream<true>(src + i + stride);
+    const ku4 c = ld_stream<true>(src + i + 2 * stride), d = ld_stream<true>(src + i + 3 * stride);
+    st_stream(dst + i, a);
+    st_stream(dst + i + stride, b);
+    st_stream(dst + i + 2 * stride, c);
+    st_stream(dst + i + 3 * stride, d);
   }
-  for (; i < n16; i += stride) dst[i] = src[i];
+  for (; i < n16; i += stride) st_stream(dst + i, ld_stream<true>(src + i));
 }
 
 // ------------------------------------------------------------ dispatch tables
@@ -2405,9 +2408,11 @@ int kaon_copy(const void* src, void* dst, int64_t bytes, void* stream) {
   if (bytes <= 0) return 0;
   if ((bytes & 15) || (((uintptr_t)src | (uintptr_t)dst) & 15)) return fail("kaon_copy: needs 16-byte alignment");
   const int64_t n16 = bytes / 16;
+  // the fastest configuration of a size sweep on gfx950: 4 vectors per thread
+  // per round, up to 65536 workgroups, non-temporal accesses
   int64_t g = (n16 + KAON_WG * 4 - 1) / (KAON_WG * 4);
-  if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(k_copy, dim3((unsigned)g), dim3(KAON_WG), 0, (hipStream_t)stream, (const uint4*)src, (uint4*)dst,
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(k_copy, dim3((unsigned)g), dim3(KAON_WG), 0, (hipStream_t)stream, (const ku4*)src, (ku4*)dst,
                      n16);
   return check_launch("kaon_copy");
 }

@@ -45,21 +45,28 @@ def init_momentum_state(state: dict[str, Any], grad: torch.Tensor, group: dict[s
 
 
 def load_state_dict_preserving_dtypes(optimizer: torch.optim.Optimizer, state_dict: dict[str, Any]) -> None:
-    """torch's load_state_dict, then cast every state tensor back to its saved dtype
-    (torch upcasts int8/uint8/bf16 momentum to the param dtype on load)."""
+    """torch's load_state_dict with every state tensor kept as saved
+    (_momentum_codec.py:417-452).
+
+    torch casts each state tensor to the param's dtype on load.  The reference
+    casts it back afterwards, which is exact for fp32 params; with bf16 params
+    the fp32 row/col/v/scale state would come back rounded to bf16.  Here a
+    tensor whose dtype torch changed is replaced by the saved tensor itself,
+    moved to the param's device, so a resume is byte-identical for any param
+    dtype.  Keys and layout are the reference's, so checkpoints move both ways.
+    """
     saved = state_dict.get("state", {})
-    saved_dtypes = {idx: {k: v.dtype for k, v in s.items() if torch.is_tensor(v)} for idx, s in saved.items()}
     torch.optim.Optimizer.load_state_dict(optimizer, state_dict)
     params = [p for group in optimizer.param_groups for p in group["params"]]
     for i, p in enumerate(params):
-        dtypes = saved_dtypes.get(i)
-        if dtypes is None or p not in optimizer.state:
+        s = saved.get(i)
+        if s is None or p not in optimizer.state:
             continue
         st = optimizer.state[p]
-        for key, dtype in dtypes.items():
+        for key, v in s.items():
             t = st.get(key)
-            if torch.is_tensor(t) and t.dtype != dtype:
-                st[key] = t.to(dtype)
+            if torch.is_tensor(v) and torch.is_tensor(t) and t.dtype != v.dtype:
+                st[key] = v.detach().to(device=p.device, copy=True)
 
 
 def validate_common(lr: float, betas: tuple[float, float], momentum_dtype: str, bf16_method: str,

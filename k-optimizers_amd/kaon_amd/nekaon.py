@@ -169,11 +169,16 @@ class Nekaon(torch.optim.Optimizer):
         return sd
 
     def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        """MSAM.load_state_dict (msam.py:409-421): restore the inner optimizer;
+        MSAM keeps no persistent state, checkpoints are saved in eval mode
+        (unperturbed weights), so no climb is active after loading."""
         sd = dict(state_dict)
         sd.pop("msam", None)
         sd.pop("_autolr", None)
         self.inner.load_state_dict(sd)
         self.param_groups = self.inner.param_groups
         self._train_mode = True
+        self._has_e = False
+        self._eclamp = {}
         self._has_e = False
         self._eclamp = {}

@@ -1,0 +1,167 @@
+"""Checkpoint interop with the reference layout (CPU: layout and loading only).
+
+The golden fixtures hold the reference's own state after its steps
+(tests/golden/make_golden.py ran kaon 0.7.4): per param the keys, dtypes and
+shapes of ``optimizer.state`` (adakaon.py:318-335, lion.py:210-241,
+_momentum_codec.py:253-406).  These tests check that
+
+* kaon_amd's fresh state has the reference's keys and dtypes, and its shapes
+  except where the reference's own two paths differ (the 1-D int8 ``m_scale``:
+  ``()`` at init and on the foreach path, ``(1,)`` after the per-param requant,
+  tests/test_fused_triton.py:906-908 of the reference);
+* a reference-layout checkpoint loads with every tensor byte-identical, both
+  shapes of the 1-D scale included, for bf16 and fp32 params;
+* kaon_amd's own state_dict round-trips through torch.save / torch.load
+  (weights_only) with its SR key.
+
+Stepping from a loaded checkpoint runs in tests/test_gpu_checkpoint.py.
+"""
+import io
+
+import numpy as np
+import pytest
+import torch
+
+from cases import CASES, grad_values, param_values
+from golden_compare import load_golden
+from gpu_cases import make_opt
+
+INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion")]
+
+
+def _tdt(name):
+    return torch.bfloat16 if name == "bf16" else torch.float32
+
+
+def _cpu_opt(case):
+    pdt = _tdt(case["p_dtype"])
+    params = []
+    for i, _ in enumerate(case["shapes"]):
+        p = torch.nn.Parameter(torch.from_numpy(param_values(case, i)).to(pdt))
+        p.grad = torch.from_numpy(grad_values(case, i, 1)).to(_tdt(case["g_dtype"]))
+        params.append(p)
+    opt = make_opt(case, params)
+    for g in opt.param_groups:
+        for p in g["params"]:
+            opt._init_state(p, opt.state[p], g)
+    return opt, params
+
+
+def _golden_state(gold, i):
+    out = {}
+    pre = f"s{i}_"
+    for k, a in gold.items():
+        if not k.startswith(pre):
+            continue
+        key = k[len(pre):]
+        if key in ("m_numel", "m_block"):
+            out[key] = int(a)
+        elif a.dtype == np.uint16:  # bf16 bits
+            out[key] = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        else:
+            out[key] = torch.from_numpy(a.copy())
+    return out
+
+
+def _bytes(t):
+    return t.detach().contiguous().reshape(-1).view(torch.uint8).numpy()
+
+
+def _reference_sd(name, opt):
+    gold = load_golden(name)
+    sd = opt.state_dict()
+    sd["state"] = {i: _golden_state(gold, i) for i in range(len(CASES[name]["shapes"]))}
+    sd.pop("kaon_amd", None)
+    return sd, gold
+
+
+@pytest.mark.parametrize("name", INTEROP)
+def test_fresh_state_has_the_reference_layout(name):
+    case = CASES[name]
+    opt, params = _cpu_opt(case)
+    gold = load_golden(name)
+    for i, p in enumerate(params):
+        ref = _golden_state(gold, i)
+        st = opt.state[p]
+        assert sorted(st) == sorted(ref), (name, i, sorted(st), sorted(ref))
+        for k, v in ref.items():
+            if not torch.is_tensor(v):
+                assert int(st[k]) == v, (name, i, k)
+                continue
+            assert st[k].dtype == v.dtype, (name, i, k, st[k].dtype, v.dtype)
+            if k == "m_scale" and p.ndim == 1 and v.dtype == torch.float32 and case["kwargs"].get(
+                    "momentum_dtype") == "int8":
+                assert tuple(st[k].shape) == () and tuple(v.shape) in ((), (1,)), (name, i, v.shape)
+            else:
+                assert st[k].shape == v.shape, (name, i, k, tuple(st[k].shape), tuple(v.shape))
+
+
+@pytest.mark.parametrize("name", INTEROP)
+def test_reference_checkpoint_loads_byte_identical(name):
+    case = CASES[name]
+    opt, params = _cpu_opt(case)
+    sd, gold = _reference_sd(name, opt)
+    opt.load_state_dict(sd)
+    for i, p in enumerate(params):
+        ref = _golden_state(gold, i)
+        st = opt.state[p]
+        for k, v in ref.items():
+            if not torch.is_tensor(v):
+                assert int(st[k]) == v
+                continue
+            assert st[k].dtype == v.dtype and st[k].shape == v.shape, (name, i, k)
+            assert np.array_equal(_bytes(st[k]), _bytes(v)), (name, i, k)
+
+
+def test_bf16_params_keep_fp32_state_exact():
+    """torch's load rounds floating state to the param dtype; the loader restores
+    the saved fp32 row/col/v/scales rather than casting the rounded values back."""
+    name = "ada_int8_sr"
+    opt, params = _cpu_opt(CASES[name])
+    assert params[0].dtype == torch.bfloat16
+    sd, gold = _reference_sd(name, opt)
+    opt.load_state_dict(sd)
+    row = opt.state[params[0]]["row"]
+    assert row.dtype == torch.float32
+    assert np.array_equal(row.numpy(), gold["s0_row"])
+    # the values are not all bf16-representable, so a lossy round trip would show
+    assert not np.array_equal(gold["s0_row"], torch.from_numpy(gold["s0_row"]).bfloat16().float().numpy())
+
+
+@pytest.mark.parametrize("name", ["ada_int8_sr", "ada_4bit_sr", "lion_bf16_sr"])
+def test_state_dict_round_trip_through_torch_save(name):
+    case = CASES[name]
+    opt, params = _cpu_opt(case)
+    sd0, _ = _reference_sd(name, opt)
+    opt.load_state_dict(sd0)
+    opt._t, opt.sr_seed = 7, 1234
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    buf.seek(0)
+    sd = torch.load(buf, weights_only=True)
+    assert sd["kaon_amd"] == {"step": 7, "sr_seed": 1234}
+    opt2, params2 = _cpu_opt(case)
+    opt2.load_state_dict(sd)
+    assert (opt2._t, opt2.sr_seed) == (7, 1234)
+    for p, q in zip(params, params2):
+        a, b = opt.state[p], opt2.state[q]
+        assert sorted(a) == sorted(b)
+        for k in a:
+            if torch.is_tensor(a[k]):
+                assert a[k].dtype == b[k].dtype and a[k].shape == b[k].shape
+                assert np.array_equal(_bytes(a[k]), _bytes(b[k])), (name, k)
+            else:
+                assert a[k] == b[k]
+
+
+def test_nekaon_load_clears_the_climb():
+    """MSAM.load_state_dict (msam.py:409-421): checkpoints are saved in eval mode,
+    so no climb is active after loading."""
+    from kaon_amd import Nekaon
+
+    p = torch.nn.Parameter(torch.zeros(8, 16, dtype=torch.bfloat16))
+    opt = Nekaon([p], lr=1e-3)
+    sd = opt.state_dict()
+    opt._has_e, opt._eclamp = True, {0: 0.1}
+    opt.load_state_dict(sd)
+    assert opt._has_e is False and opt._eclamp == {}

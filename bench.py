@@ -50,7 +50,14 @@ WORKLOADS = {
                               "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
                               "params on the Adakaon path", opt="adamuon",
                          kw=dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype="int8", ns_steps=2), bm=1.0),
+    # the launch-bound regime: the reference's LoRA proxy bag (benchmarks/proxy/harness.py:117-127:
+    # 512 tensors [8, 16], fp32) stepped by Adakaon with bf16 momentum, the configuration its
+    # control ranking lists as "Adakaon-bf16-fused" (benchmarks/control/RANKINGS.md:83)
+    "lora_bag": dict(desc="LoRA bag: 512 x [8,16] fp32 params and grads, Adakaon bf16 momentum, cautious, GC, "
+                          "lr 1e-4", opt="adakaon", kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="bfloat16"),
+                     bm=2.0, shapes=[(8, 16)] * 512, pdtype="f32"),
 }
+LORA_METRIC = "ms per optimizer step, LoRA bag 512 x [8,16] fp32, 1 GPU"
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 # algorithmic HBM bytes per param of each phase kernel (bf16 g/p, b_m momentum bytes)
@@ -241,10 +248,11 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     w = WORKLOADS[args.workload]
-    shapes = workloads.sdxl_shapes()
+    shapes = w.get("shapes") or workloads.sdxl_shapes()
+    pdt = torch.float32 if w.get("pdtype") == "f32" else torch.bfloat16
     nparam = workloads.n_params(shapes)
     print(f"[bench] {args.workload}: {len(shapes)} tensors, {nparam / 1e9:.3f}B params", file=sys.stderr, flush=True)
-    params = workloads.make_params(shapes, dev, seed=0, outlier_frac=w.get("outliers", 0.0))
+    params = workloads.make_params(shapes, dev, seed=0, dtype=pdt, outlier_frac=w.get("outliers", 0.0))
     opt = make_opt(args.workload, params)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
@@ -263,11 +271,26 @@ def main() -> int:
     ms = t0.elapsed_time(t1) / args.steps
     gps = nparam / (ms * 1e-3) / 1e9
     bm = w["bm"]
-    b_alg = 2.0 + 4.0 + 2.0 * bm
+    eb = 4.0 if pdt == torch.float32 else 2.0   # param and grad element bytes
+    b_alg = eb + 2.0 * eb + 2.0 * bm
     step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
     print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
           file=sys.stderr, flush=True)
 
+    if "shapes" in w:
+        # a launch-bound configuration: the step time is the metric
+        out = {"metric": LORA_METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+               "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+               "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": {"workload": w["desc"], "n_tensors": len(shapes), "n_params": nparam, "params": "f32",
+                          "grads": "f32", "momentum": w["kw"]["momentum_dtype"], "parallelism": "none (1 GPU)",
+                          "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+                          "launches_per_step": "6 kernels"}}
+        if not args.no_breakdown:
+            out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(phase_breakdown(opt, args.workload)
+                                                                                 .items())}
+        print(json.dumps(out), flush=True)
+        return 0
     ceiling = copy_ceiling_gbs(dev)
     out = {
         "metric": METRIC, "value": round(gps, 2), "unit": "Gparam/s", "n_gpus": 1, "steps": args.steps,

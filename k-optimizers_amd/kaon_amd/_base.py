@@ -8,6 +8,7 @@ State keys, dtypes and shapes are the reference's (K-Optimizers "kaon"
 """
 from __future__ import annotations
 
+import operator
 from typing import Any, Iterable
 
 import torch
@@ -16,6 +17,11 @@ from . import _engine as E
 from . import _lib as L
 
 _FOURBIT_BLOCK = 128          # src/kaon/_momentum_codec.py:59
+# per-tensor accessors mapped over a param group each step (C-level map, no Python loop)
+_DP = torch.Tensor.data_ptr
+_CONTIG = torch.Tensor.is_contiguous
+_GRAD = operator.attrgetter("grad")
+_DTYPE = operator.attrgetter("dtype")
 FOREACH_BATCH_CUTOFF = 2_000_000  # src/kaon/_backend.py:53 (accepted for API compatibility)
 
 
@@ -107,6 +113,7 @@ class KaonOptimizer(torch.optim.Optimizer):
         self._t = 0
         self.sr_seed = int(torch.initial_seed()) & 0xFFFFFFFF
         self._plans: dict[tuple, tuple[tuple, E.Plan]] = {}
+        self._launch_cache: dict[int, tuple[tuple, list]] = {}  # param group -> (key, launches)
         self._state_version = 0
         self._inject_noise: dict[torch.Tensor, list] = {}  # tests: param -> [uint16 noise per stream]
 
@@ -116,7 +123,46 @@ class KaonOptimizer(torch.optim.Optimizer):
 
     def _invalidate(self) -> None:
         self._plans.clear()
+        self._launch_cache.clear()
         self._state_version += 1
+
+    def add_param_group(self, param_group: dict[str, Any]) -> None:
+        super().add_param_group(param_group)
+        if hasattr(self, "_plans"):  # tensor ids (the SR counter field) shift
+            self._invalidate()
+
+    def _group_key(self, group: dict[str, Any], params: list[torch.Tensor]) -> tuple:
+        """What a group's launches depend on: state version, codec settings, and the
+        param and grad pointers (grad dtype and contiguity included)."""
+        grads = list(map(_GRAD, params))
+        return (self._state_version, group["momentum_dtype"], group["bf16_method"], group["betas"][0] > 0,
+                tuple(map(_DP, params)), tuple(map(_DP, grads)), tuple(map(_DTYPE, grads)),
+                tuple(map(_CONTIG, grads)))
+
+    def _launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor]) -> list:
+        """The group's launches (plan, p dtype, g dtype, device, ...), reused while
+        ``_group_key`` is unchanged; otherwise checks the params, creates missing state
+        and plans again (``_build_launches``).  The stream is looked up per step."""
+        try:
+            key = self._group_key(group, params)
+        except RuntimeError:  # e.g. a sparse grad: the checks below raise the proper error
+            key = None
+        hit = self._launch_cache.get(gid)
+        if key is not None and hit is not None and hit[0] == key:
+            return hit[1]
+        self._check_params(params)
+        for p in params:
+            state = self.state[p]
+            if not state:
+                self._init_state(p, state, group)
+                self._state_version += 1
+        out = self._build_launches(gid, group, params, self._tensor_ids())
+        self._launch_cache[gid] = (self._group_key(group, params), out)
+        return out
+
+    def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],
+                        tids: dict[int, int]) -> list:  # pragma: no cover - abstract
+        raise NotImplementedError
 
     def _check_params(self, params: list[torch.Tensor]) -> None:
         for p in params:

@@ -140,24 +140,23 @@ class Adakaon(KaonOptimizer):
             with torch.enable_grad():
                 loss = closure()
         self._t += 1
-        tids = None
+        lib = L.lib()
         for gid, group in enumerate(self.param_groups):
             params = [p for p in group["params"] if p.grad is not None]
             if not params:
                 continue
-            self._check_params(params)
-            for p in params:
-                state = self.state[p]
-                if not state:
-                    self._init_state(p, state, group)
-                    self._state_version += 1
-            mom = group["betas"][0] > 0
-            codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
-            for (pdt, gdt), plist in self._partitions(params).items():
-                if tids is None:
-                    tids = self._tensor_ids()
-                plan = self._plan((gid, pdt, gdt), group, plist, codec, tids)
+            for plan, pdt, gdt, dev in self._launches(gid, group, params):
                 hp = self._hyper(group, pdt, gdt, nk, gid)
-                L.check(L.lib().kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp),
-                                                  E.stream_handle(plist[0].device)), "kaon_adakaon_step")
+                L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
+                        "kaon_adakaon_step")
         return loss
+
+    def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],
+                        tids: dict[int, int]) -> list:
+        mom = group["betas"][0] > 0
+        codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
+        out = []
+        for (pdt, gdt), plist in self._partitions(params).items():
+            plan = self._plan((gid, pdt, gdt), group, plist, codec, tids)
+            out.append((plan, pdt, gdt, plist[0].device))
+        return out

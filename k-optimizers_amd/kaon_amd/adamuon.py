@@ -136,33 +136,31 @@ class AdaMuon(KaonOptimizer):
             with torch.enable_grad():
                 loss = closure()
         self._t += 1
-        tids = None
         lib = L.lib()
         for gid, group in enumerate(self.param_groups):
             params = [p for p in group["params"] if p.grad is not None]
             if not params:
                 continue
-            self._check_params(params)
-            for p in params:
-                state = self.state[p]
-                if not state:
-                    self._init_state(p, state, group)
-                    self._state_version += 1
-            mom = group["betas"][0] > 0
-            codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
-            for (pdt, gdt), plist in self._partitions(params).items():
-                if tids is None:
-                    tids = self._tensor_ids()
+            for fn, plan, pdt, gdt, dev in self._launches(gid, group, params):
                 hp = self._hyper(group, pdt, gdt)
-                stream = E.stream_handle(plist[0].device)
-                mats = [p for p in plist if p.ndim >= 2]
-                vecs = [p for p in plist if p.ndim < 2]
-                if mats:
-                    plan = self._plan((gid, pdt, gdt, 2), group, mats, codec, tids, L.OPT_ADAMUON)
-                    L.check(lib.kaon_adamuon_step(ctypes.byref(plan.launch), ctypes.byref(hp), stream),
-                            "kaon_adamuon_step")
-                if vecs:
-                    plan = self._plan((gid, pdt, gdt, 1), group, vecs, codec, tids, L.OPT_ADAKAON)
-                    L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), stream),
-                            "kaon_adakaon_step")
+                L.check(getattr(lib, fn)(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)), fn)
         return loss
+
+    def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],
+                        tids: dict[int, int]) -> list:
+        """The matrices through an AdaMuon plan, the 1-D params through an Adakaon plan
+        (hp.lr is already 0.2 * lr, adamuon.py:88, 588)."""
+        mom = group["betas"][0] > 0
+        codec = L.MOM_CODE[group["momentum_dtype"]] if mom else L.MOM_NONE
+        out = []
+        for (pdt, gdt), plist in self._partitions(params).items():
+            dev = plist[0].device
+            mats = [p for p in plist if p.ndim >= 2]
+            vecs = [p for p in plist if p.ndim < 2]
+            if mats:
+                plan = self._plan((gid, pdt, gdt, 2), group, mats, codec, tids, L.OPT_ADAMUON)
+                out.append(("kaon_adamuon_step", plan, pdt, gdt, dev))
+            if vecs:
+                plan = self._plan((gid, pdt, gdt, 1), group, vecs, codec, tids, L.OPT_ADAKAON)
+                out.append(("kaon_adakaon_step", plan, pdt, gdt, dev))
+        return out

@@ -97,23 +97,22 @@ class Lion(KaonOptimizer):
             with torch.enable_grad():
                 loss = closure()
         self._t += 1
-        tids = None
+        lib = L.lib()
         for gid, group in enumerate(self.param_groups):
             params = [p for p in group["params"] if p.grad is not None]
             if not params:
                 continue
-            self._check_params(params)
-            for p in params:
-                state = self.state[p]
-                if not state:
-                    self._init_state(p, state, group)
-                    self._state_version += 1
-            codec = L.MOM_CODE[group["momentum_dtype"]]
-            for (pdt, gdt), plist in self._partitions(params).items():
-                if tids is None:
-                    tids = self._tensor_ids()
-                plan = self._plan((gid, pdt, gdt), group, plist, codec, tids)
+            for plan, pdt, gdt, dev in self._launches(gid, group, params):
                 hp = self._hyper(group, pdt, gdt)
-                L.check(L.lib().kaon_lion_step(ctypes.byref(plan.launch), ctypes.byref(hp),
-                                               E.stream_handle(plist[0].device)), "kaon_lion_step")
+                L.check(lib.kaon_lion_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
+                        "kaon_lion_step")
         return loss
+
+    def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],
+                        tids: dict[int, int]) -> list:
+        codec = L.MOM_CODE[group["momentum_dtype"]]
+        out = []
+        for (pdt, gdt), plist in self._partitions(params).items():
+            plan = self._plan((gid, pdt, gdt), group, plist, codec, tids)
+            out.append((plan, pdt, gdt, plist[0].device))
+        return out

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 4
+#define KAON_ABI_VERSION 5
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -97,7 +97,8 @@ typedef struct KaonTensor {
   int32_t vec_rows;       /* 16-byte vector path for row chunks (C % 8 == 0 or one row, aligned) */
   int32_t vec_flat;       /* 16-byte vector path for flat chunks (all bases aligned) */
   int32_t ns_tr;          /* AdaMuon: Newton-Schulz iterates on the transpose (R > C) */
-  int32_t m_pad, k_pad;   /* AdaMuon: min(R,C) and max(R,C) rounded up to KAON_NS_TILE */
+  int32_t m_pad, k_pad;   /* AdaMuon: min(R,C) and max(R,C) rounded up to the tile (KAON_NS_TILE,
+                             or twice that for big matrices) */
   int32_t fast_lanes;     /* set by kaon_plan: lanes per row of the phase-5/6 fast kernel (8..64) */
 } KaonTensor;
 
@@ -105,8 +106,9 @@ typedef struct KaonTensor {
  * `tensor`, kind = rows per wave group (RW); a slice is at most 4 * RW rows, a
  * run at most KAON_RUN slices.  Finalize items: kind 0 = columns [row0, row0+nrows),
  * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows).
- * Newton-Schulz tiles: row0 = tile row, nrows = tile column (KAON_NS_TILE
- * square tiles of the padded matrices). */
+ * Newton-Schulz tiles: row0 = tile row, nrows = tile column of the padded
+ * matrices, kind = 0 for KAON_NS_TILE tiles, 1 for 2 * KAON_NS_TILE tiles (the
+ * symmetric products list only row <= column for those). */
 typedef struct KaonItem {
   int32_t tensor;
   int32_t row0;
@@ -149,6 +151,8 @@ typedef struct KaonPlanInfo {
   int32_t n_elem_items;   /* phase-5/6 items (elem_items) */
   int32_t n_ns_sq;        /* AdaMuon: tiles of the m_pad x m_pad products (ns_sq_items) */
   int32_t n_ns_rect;      /* AdaMuon: tiles of the m_pad x k_pad iterate (ns_rect_items) */
+  int32_t n_ns_sq_big;    /* of which the leading big-tile items (kind 1) */
+  int32_t n_ns_rect_big;
   int64_t ws_words;       /* workspace size in 4-byte words */
 } KaonPlanInfo;
 
@@ -178,6 +182,7 @@ typedef struct KaonLaunch {
   int32_t row_runs[KAON_ROW_CLASSES];
   int32_t n_fast, n_elem_items;
   int32_t n_ns_sq, n_ns_rect;
+  int32_t n_ns_sq_big, n_ns_rect_big;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
 } KaonLaunch;
 

@@ -196,18 +196,201 @@ __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ 
       }
 }
 
-// x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
-// the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
-__global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ D,
-                                                 const KaonItem* __restrict__ items, float* ws) {
-  __shared__ uint16_t tile[TILE][TILE + 2];
+// Big tiles: one 256 x 256 output tile per workgroup, 4 wave64 of 128 x 128
+// (4 x 4 v_mfma_f32_32x32x16_bf16 tiles accumulating in AGPRs), K in steps of
+// 32 through two LDS stages: the next step's global loads and LDS stores
+// overlap the current step's MFMAs, one barrier per step.  Per step a wave
+// reads 16 KiB of fragments for 32 MFMAs, so LDS stays below its bandwidth at
+// full MFMA rate (a 64 x 64 wave tile needs more than LDS provides).  The
+// symmetric products (MODE 0, 1) run on tiles with row <= column and also store
+// the transposed tile: its elements are the same products summed in the same
+// order, so the mirror is exact.  The epilogue goes through LDS so that every
+// global access is 16 bytes.
+constexpr int BT = 2 * TILE;     // 256
+constexpr int BK = 32;           // K per stage
+constexpr int BLD = BK + 8;      // LDS row stride (bf16): 80 B, 16-B aligned rows, no bank aliasing
+constexpr int WLD = 128 + 8;     // epilogue staging row stride (bf16): a wave's 128 x 128 tile
+constexpr int NS_LDS = (2 * 2 * BT * BLD > 4 * 128 * WLD) ? 2 * 2 * BT * BLD : 4 * 128 * WLD;
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__ D,
+                                                  const KaonItem* __restrict__ items, float* ws, int parity,
+                                                  float ca, float cb, float cc) {
+  // K loop: [stage][A, B][BT][BLD]; epilogue: [wave][128][WLD]
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NS_LDS];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
-  const double rden = rcp64(G(ws)[T.ws_scal + 2]);
+  const int mp = T.m_pad, kp = T.k_pad;
+  const uint16_t* xc = parity ? nb.x1 : nb.x0;
+  uint16_t* xn = parity ? nb.x0 : nb.x1;
+  const uint16_t* Aop = MODE == 0 ? xc : MODE == 1 ? nb.a : nb.b;
+  const uint16_t* Bop = MODE == 1 ? nb.a : xc;
+  const int lda = MODE == 0 ? kp : mp;
+  const int ldb = MODE == 1 ? mp : kp;
+  const int K = MODE == 0 ? kp : mp;
+  uint16_t* out = MODE == 0 ? nb.a : MODE == 1 ? nb.b : xn;
+  const int ldc = MODE == 2 ? kp : mp;
+  const int row0 = it.row0 * BT, col0 = it.nrows * BT;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+  auto As = [&](int st) { return lds + (st * 2 + 0) * BT * BLD; };
+  auto Bs = [&](int st) { return lds + (st * 2 + 1) * BT * BLD; };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // staging: 4 x 16 B of each operand per thread per step
+  ku4 ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+      ra[s] = *(const KAON_G ku4*)G(Aop + (int64_t)(row0 + r) * lda + k0 + kc * 8);
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+        rb[s] = *(const KAON_G ku4*)G(Bop + (int64_t)(col0 + r) * ldb + k0 + kc * 8);
+      }
+    } else {
+      // x: 32 K rows x 256 columns; a thread takes two adjacent K rows of 8
+      // columns, so its transposed LDS writes pack K pairs into 32-bit words
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int q = tid + 256 * s, jc = q >> 4, tp = q & 15;
+        const uint16_t* src = Bop + (int64_t)(k0 + 2 * tp) * ldb + col0 + jc * 8;
+        rb[2 * s] = *(const KAON_G ku4*)G(src);
+        rb[2 * s + 1] = *(const KAON_G ku4*)G(src + ldb);
+      }
+    }
+  };
+  auto lstore = [&](int st) {
+    uint16_t* as = As(st);
+    uint16_t* bs = Bs(st);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+      *(ku4*)&as[r * BLD + kc * 8] = ra[s];
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+        *(ku4*)&bs[r * BLD + kc * 8] = rb[s];
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int q = tid + 256 * s, jc = q >> 4, tp = q & 15;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *(uint32_t*)&bs[(jc * 8 + e) * BLD + 2 * tp] = half_of(rb[2 * s], e) | (half_of(rb[2 * s + 1], e) << 16);
+      }
+    }
+  };
+
+  const int nk = K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ++ks) {
+    const int cur = ks & 1;
+    if (ks + 1 < nk) gload((ks + 1) * BK);
+    const uint16_t* as = As(cur);
+    const uint16_t* bs = Bs(cur);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      bf16x8 af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *(const bf16x8*)&as[(wm * 128 + i * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bfr[j] = *(const bf16x8*)&bs[(wn * 128 + j * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (ks + 1 < nk) lstore(cur ^ 1);  // that stage was last read before the previous barrier
+    __syncthreads();
+  }
+
+  // epilogue: bf16(v) of the wave's whole 128 x 128 tile goes to its own LDS
+  // region (the stages are free after the last barrier) in one unrolled pass,
+  // then a loop that never touches the accumulators reads it back 32 x 32 at a
+  // time as 16-byte row chunks (normal store) or 8-row column chunks (mirror)
+  uint16_t* stg = lds + w * (128 * WLD);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        stg[(i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * WLD + j * 32 + (lane & 31)] =
+            (uint16_t)f2bf(acc[i][j][r]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  const bool mirror = MODE != 2 && it.row0 != it.nrows;
+  const KAON_G uint16_t* eop = G((const uint16_t*)(MODE == 1 ? nb.a : xc));
+  const int lde = MODE == 1 ? mp : kp;
+#pragma clang loop unroll(disable)
+  for (int sub = 0; sub < 16; ++sub) {
+    const int i = sub >> 2, j = sub & 3;
+    const int R0 = row0 + wm * 128 + i * 32, C0 = col0 + wn * 128 + j * 32;
+    const uint16_t* t = stg + (i * 32) * WLD + j * 32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = lane + 64 * h, rr = q >> 2, c8 = (q & 3) * 8;
+      const ku4 xv = *(const ku4*)&t[rr * WLD + c8];
+      ku4 ov = xv;
+      if (MODE != 0) {
+        const ku4 ev = *(const KAON_G ku4*)(eop + (int64_t)(R0 + rr) * lde + C0 + c8);
+        uint32_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = __uint_as_float(half_of(xv, e) << 16), ef = __uint_as_float(half_of(ev, e) << 16);
+          o[e] = MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * x)) : f2bf(rbf(ca * ef) + x);
+        }
+        ov = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+      }
+      *(KAON_G ku4*)G(out + (int64_t)(R0 + rr) * ldc + C0 + c8) = ov;
+      if (mirror) {
+        // out[C0 + cr][R0 + r8 .. + 8] = the same values read down column cr
+        const int cr = q >> 2, r8 = (q & 3) * 8;
+        uint32_t xs[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[e] = t[(r8 + e) * WLD + cr];
+        ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
+        if (MODE == 1) {
+          // B[c][r] = b A[r][c] + c (AA)[r][c]; A is symmetric, so A[r][c] = A[c][r]
+          const ku4 ev = *(const KAON_G ku4*)(eop + (int64_t)(C0 + cr) * lde + R0 + r8);
+          uint32_t o[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = __uint_as_float(xs[e] << 16), ef = __uint_as_float(half_of(ev, e) << 16);
+            o[e] = f2bf(rbf(cb * ef) + rbf(cc * x));
+          }
+          mv = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+        }
+        *(KAON_G ku4*)G(out + (int64_t)(C0 + cr) * ldc + R0 + r8) = mv;
+      }
+    }
+  }
+}
+
+// x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
+// the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
+__device__ __forceinline__ void ns_prep_tile(const KaonTensor& T, const NsBufs& nb, double rden, int i0, int t0,
+                                             uint16_t (*tile)[TILE + 2]) {
   const int64_t C = T.C;
   const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
-  const int i0 = it.row0 * TILE, t0 = it.nrows * TILE;
   const KAON_G uint16_t* mo = G((const uint16_t*)nb.mo);
   KAON_G uint16_t* x = G(nb.x0);
   if (!T.ns_tr) {
@@ -229,16 +412,26 @@ __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ 
   }
 }
 
-// O [R, C] from the final iterate (transposed back when R > C), over M.
-__global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ D,
-                                                 const KaonItem* __restrict__ items, float* ws, int parity) {
+// One item = one tile (kind 0) or 2 x 2 tiles (kind 1, a big-tile item).
+__global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, float* ws) {
   __shared__ uint16_t tile[TILE][TILE + 2];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
+  const double rden = rcp64(G(ws)[T.ws_scal + 2]);
+  const int sub = it.kind ? 2 : 1;
+  for (int s = 0; s < sub * sub; ++s) {
+    if (s) __syncthreads();  // the transpose tile is reused
+    ns_prep_tile(T, nb, rden, (it.row0 * sub + s / sub) * TILE, (it.nrows * sub + s % sub) * TILE, tile);
+  }
+}
+
+// O [R, C] from the final iterate (transposed back when R > C), over M.
+__device__ __forceinline__ void ns_post_tile(const KaonTensor& T, const NsBufs& nb, int parity, int i0, int t0,
+                                             uint16_t (*tile)[TILE + 2]) {
   const int64_t C = T.C;
   const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
-  const int i0 = it.row0 * TILE, t0 = it.nrows * TILE;
   const KAON_G uint16_t* x = G((const uint16_t*)(parity ? nb.x1 : nb.x0));
   KAON_G uint16_t* o = G(nb.mo);
   if (!T.ns_tr) {
@@ -256,6 +449,19 @@ __global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ 
       const int tt = e >> 7, ii = e & 127, t = t0 + tt, i = i0 + ii;
       if (t < k && i < m) o[(int64_t)t * C + i] = tile[tt][ii];
     }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, float* ws, int parity) {
+  __shared__ uint16_t tile[TILE][TILE + 2];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const NsBufs nb = ns_bufs(ws, T);
+  const int sub = it.kind ? 2 : 1;
+  for (int s = 0; s < sub * sub; ++s) {
+    if (s) __syncthreads();
+    ns_post_tile(T, nb, parity, (it.row0 * sub + s / sub) * TILE, (it.nrows * sub + s % sub) * TILE, tile);
   }
 }
 
@@ -278,12 +484,24 @@ int kaon_ns_run(const KaonLaunch& L, int steps, hipStream_t st) {
   const float a = 3.4445f, b = -4.7750f, c = 2.0315f;  // adamuon.py:106
   hipLaunchKernelGGL(k_ns_prep, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws);
   int rc = ns_check("kaon: Newton-Schulz input launch");
+  // big-tile items lead both lists
+  const int nsq_b = L.n_ns_sq_big, nrect_b = L.n_ns_rect_big;
+  const int nsq_s = L.n_ns_sq - nsq_b, nrect_s = L.n_ns_rect - nrect_b;
+  if (nsq_b < 0 || nrect_b < 0 || nsq_s < 0 || nrect_s < 0) {
+    kaon_set_error("kaon_adamuon: inconsistent Newton-Schulz item counts");
+    return -1;
+  }
+  const KaonItem* sq_s = L.ns_sq_items + nsq_b;
+  const KaonItem* rect_s = L.ns_rect_items + nrect_b;
   for (int s = 0; s < steps && !rc; ++s) {
     const int par = s & 1;
-    hipLaunchKernelGGL(k_ns_gemm<0>, dim3(L.n_ns_sq), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
-    hipLaunchKernelGGL(k_ns_gemm<1>, dim3(L.n_ns_sq), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
-    hipLaunchKernelGGL(k_ns_gemm<2>, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, par, a, b,
-                       c);
+    if (nsq_b) hipLaunchKernelGGL(k_ns_gemm2<0>, dim3(nsq_b), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
+    if (nsq_s) hipLaunchKernelGGL(k_ns_gemm<0>, dim3(nsq_s), dim3(256), 0, st, L.descs, sq_s, ws, par, a, b, c);
+    if (nsq_b) hipLaunchKernelGGL(k_ns_gemm2<1>, dim3(nsq_b), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
+    if (nsq_s) hipLaunchKernelGGL(k_ns_gemm<1>, dim3(nsq_s), dim3(256), 0, st, L.descs, sq_s, ws, par, a, b, c);
+    if (nrect_b)
+      hipLaunchKernelGGL(k_ns_gemm2<2>, dim3(nrect_b), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, par, a, b, c);
+    if (nrect_s) hipLaunchKernelGGL(k_ns_gemm<2>, dim3(nrect_s), dim3(256), 0, st, L.descs, rect_s, ws, par, a, b, c);
     rc = ns_check("kaon: Newton-Schulz GEMM launch");
   }
   if (rc) return rc;

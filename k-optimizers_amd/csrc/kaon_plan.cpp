@@ -132,7 +132,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     bool fast;
   };
   std::vector<RowIt> rows, elems;
-  std::vector<KaonItem> fins, flats, ns_sq, ns_rect;
+  std::vector<KaonItem> fins, flats, ns_sq, ns_rect, ns_sq_big, ns_rect_big;
   // the row kernels of an AdaMuon plan read the bf16 orthogonal factor
   const int32_t row_dtype = opt == KAON_OPT_ADAMUON ? (int32_t)KAON_BF16 : g_dtype;
   for (int32_t i = 0; i < n; ++i) {
@@ -182,15 +182,21 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     if (opt == KAON_OPT_ADAMUON) {
       const int64_t m = std::min(t.R, t.C), k = std::max(t.R, t.C);
       t.ns_tr = t.R > t.C ? 1 : 0;
-      t.m_pad = (int32_t)((m + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE);
-      t.k_pad = (int32_t)((k + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE);
+      // big matrices take 2*KAON_NS_TILE tiles when that adds no row padding
+      const int64_t m128 = (m + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE;
+      const bool big = m128 >= 4 * KAON_NS_TILE && m128 % (2 * KAON_NS_TILE) == 0;
+      const int64_t tile = big ? 2 * KAON_NS_TILE : KAON_NS_TILE;
+      t.m_pad = (int32_t)((m + tile - 1) / tile * tile);
+      t.k_pad = (int32_t)((k + tile - 1) / tile * tile);
       off += ns_words(t);
       if (t.n > 0) {
-        const int32_t tm = t.m_pad / KAON_NS_TILE, tk = t.k_pad / KAON_NS_TILE;
+        const int32_t tm = (int32_t)(t.m_pad / tile), tk = (int32_t)(t.k_pad / tile);
+        // A = x x^T and B = b A + c A A are symmetric: big tiles cover a <= b
+        // only, their mirror is written with them
         for (int32_t a = 0; a < tm; ++a)
-          for (int32_t b = 0; b < tm; ++b) ns_sq.push_back(KaonItem{i, a, b, 0});
+          for (int32_t b = big ? a : 0; b < tm; ++b) (big ? ns_sq_big : ns_sq).push_back(KaonItem{i, a, b, big});
         for (int32_t a = 0; a < tm; ++a)
-          for (int32_t b = 0; b < tk; ++b) ns_rect.push_back(KaonItem{i, a, b, 0});
+          for (int32_t b = 0; b < tk; ++b) (big ? ns_rect_big : ns_rect).push_back(KaonItem{i, a, b, big});
       }
     }
     if (t.n == 0) continue;
@@ -252,6 +258,11 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     for (size_t k = 0; k < rows.size(); ++k) row_items[k] = rows[k].it;
   if (fin_items && !fins.empty()) std::memcpy(fin_items, fins.data(), fins.size() * sizeof(KaonItem));
   if (flat_items && !flats.empty()) std::memcpy(flat_items, flats.data(), flats.size() * sizeof(KaonItem));
+  // Newton-Schulz tiles: the big-tile items first
+  info->n_ns_sq_big = (int32_t)ns_sq_big.size();
+  info->n_ns_rect_big = (int32_t)ns_rect_big.size();
+  ns_sq.insert(ns_sq.begin(), ns_sq_big.begin(), ns_sq_big.end());
+  ns_rect.insert(ns_rect.begin(), ns_rect_big.begin(), ns_rect_big.end());
   info->n_ns_sq = (int32_t)ns_sq.size();
   info->n_ns_rect = (int32_t)ns_rect.size();
   if (ns_sq_items && !ns_sq.empty()) std::memcpy(ns_sq_items, ns_sq.data(), ns_sq.size() * sizeof(KaonItem));

@@ -100,6 +100,7 @@ class Plan:
             la.row_runs[k] = info.row_runs[k]
         la.n_fast, la.n_elem_items = info.n_fast, info.n_elem_items
         la.n_ns_sq, la.n_ns_rect = info.n_ns_sq, info.n_ns_rect
+        la.n_ns_sq_big, la.n_ns_rect_big = info.n_ns_sq_big, info.n_ns_rect_big
         la.workspace = self.workspace.data_ptr()
         self.launch = la
 

@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -57,7 +57,7 @@ class KaonPlanInfo(ctypes.Structure):
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
-                ("ws_words", ctypes.c_int64)]
+                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("ws_words", ctypes.c_int64)]
 
 
 class KaonPlanArgs(ctypes.Structure):
@@ -73,7 +73,7 @@ class KaonLaunch(ctypes.Structure):
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
-                ("workspace", ctypes.c_void_p)]
+                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("workspace", ctypes.c_void_p)]
 
 
 class KaonHyper(ctypes.Structure):

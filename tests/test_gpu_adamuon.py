@@ -84,7 +84,10 @@ def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     return O.bf16_to_f32(o).reshape(g.shape)
 
 
-@pytest.mark.parametrize("shape", [(64, 96), (96, 64), (77, 33), (130, 300), (256, 640), (640, 256), (320, 2880)])
+# the last four take the 256-tile GEMMs (m = min(R, C) a multiple of 256, >= 512):
+# symmetric products on row <= column tiles with mirrored stores
+@pytest.mark.parametrize("shape", [(64, 96), (96, 64), (77, 33), (130, 300), (256, 640), (640, 256), (320, 2880),
+                                   (512, 1024), (1024, 512), (512, 2000), (768, 1280)])
 def test_newton_schulz_matches_oracle(shape):
     print(f"[gpu] newton-schulz {shape}", flush=True)
     rng = np.random.default_rng(sum(shape))

@@ -257,11 +257,14 @@ def test_state_layout_matches_reference_at_init():
 
 
 def test_adamuon_plan_pads_and_tiles_newton_schulz():
-    """AdaMuon plans: m_pad/k_pad round min/max(R, C) up to the GEMM tile, the
-    transposed flag marks R > C, every tile of the padded products is listed
-    once, and the Newton-Schulz blocks do not overlap other workspace."""
+    """AdaMuon plans: m_pad/k_pad round min/max(R, C) up to the GEMM tile (twice
+    KAON_NS_TILE when m rounds to a multiple of it with no extra padding and is at
+    least 4 tiles), the transposed flag marks R > C, every tile of the padded
+    products is listed once (big symmetric products: row <= column only, big
+    items first), and the Newton-Schulz blocks do not overlap other workspace."""
     L = _lib()
-    shapes = [(1280, 1280, 3, 3), (5120, 1280), (77, 33), (320, 2880), (20, 12)]
+    shapes = [(1280, 1280, 3, 3), (5120, 1280), (77, 33), (320, 2880), (20, 12), (640, 640), (512, 2000),
+              (1024, 5760)]
     n = len(shapes)
     descs = (L.KaonTensor * n)()
     for i, s in enumerate(shapes):
@@ -275,17 +278,24 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
     sq = (L.KaonItem * info.n_ns_sq)()
     rect = (L.KaonItem * info.n_ns_rect)()
     assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, sq, rect, ctypes.byref(info)) == 0
-    t = L.NS_TILE
     spans = []
+    nbig_sq = nbig_rect = 0
     for i, s in enumerate(shapes):
         d = descs[i]
         m, k = min(d.R, d.C), max(d.R, d.C)
+        m128 = -(-m // L.NS_TILE) * L.NS_TILE
+        big = m128 >= 4 * L.NS_TILE and m128 % (2 * L.NS_TILE) == 0
+        assert big == (m in (1280, 512, 1024)), (s, big)
+        t = 2 * L.NS_TILE if big else L.NS_TILE
         assert d.ns_tr == (1 if d.R > d.C else 0)
         assert d.m_pad == -(-m // t) * t and d.k_pad == -(-k // t) * t
-        got_sq = sorted((it.row0, it.nrows) for it in sq if it.tensor == i)
-        got_rect = sorted((it.row0, it.nrows) for it in rect if it.tensor == i)
-        assert got_sq == [(a, b) for a in range(d.m_pad // t) for b in range(d.m_pad // t)]
-        assert got_rect == [(a, b) for a in range(d.m_pad // t) for b in range(d.k_pad // t)]
+        got_sq = sorted((it.row0, it.nrows, it.kind) for it in sq if it.tensor == i)
+        got_rect = sorted((it.row0, it.nrows, it.kind) for it in rect if it.tensor == i)
+        tm, tk = d.m_pad // t, d.k_pad // t
+        assert got_sq == [(a, b, int(big)) for a in range(tm) for b in range(tm) if not big or a <= b]
+        assert got_rect == [(a, b, int(big)) for a in range(tm) for b in range(tk)]
+        nbig_sq += len(got_sq) if big else 0
+        nbig_rect += len(got_rect) if big else 0
         words = ((d.R * d.C + 1) // 2 + 3) // 4 * 4 + 2 * ((d.m_pad * d.k_pad // 2 + 3) // 4 * 4) \
             + 2 * ((d.m_pad * d.m_pad // 2 + 3) // 4 * 4)
         spans += [(d.ws_row, d.ws_row + 5 * d.R), (d.ws_col, d.ws_col + d.C),
@@ -295,6 +305,10 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
         assert a1 <= b0
     assert spans[-1][1] <= info.ws_words
     assert info.n_fast == 0
+    # big-tile items lead both lists
+    assert (info.n_ns_sq_big, info.n_ns_rect_big) == (nbig_sq, nbig_rect)
+    assert all(sq[j].kind == (j < nbig_sq) for j in range(info.n_ns_sq))
+    assert all(rect[j].kind == (j < nbig_rect) for j in range(info.n_ns_rect))
 
 
 def test_adamuon_plan_rejects_1d():

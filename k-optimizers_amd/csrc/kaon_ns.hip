@@ -198,17 +198,17 @@ __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ 
 
 // Big tiles: one 256 x 256 output tile per workgroup, 4 wave64 of 128 x 128
 // (4 x 4 v_mfma_f32_32x32x16_bf16 tiles accumulating in AGPRs), K in steps of
-// 32 through two LDS stages: the next step's global loads and LDS stores
+// 64 through two LDS stages: the next step's global loads and LDS stores
 // overlap the current step's MFMAs, one barrier per step.  Per step a wave
-// reads 16 KiB of fragments for 32 MFMAs, so LDS stays below its bandwidth at
+// reads 32 KiB of fragments for 64 MFMAs, so LDS stays below its bandwidth at
 // full MFMA rate (a 64 x 64 wave tile needs more than LDS provides).  The
 // symmetric products (MODE 0, 1) run on tiles with row <= column and also store
 // the transposed tile: its elements are the same products summed in the same
 // order, so the mirror is exact.  The epilogue goes through LDS so that every
 // global access is 16 bytes.
 constexpr int BT = 2 * TILE;     // 256
-constexpr int BK = 32;           // K per stage
-constexpr int BLD = BK + 8;      // LDS row stride (bf16): 80 B, 16-B aligned rows, no bank aliasing
+constexpr int BK = 64;           // K per stage
+constexpr int BLD = BK + 8;      // LDS row stride (bf16): 144 B, 16-B aligned rows, no bank aliasing
 constexpr int WLD = 128 + 8;     // epilogue staging row stride (bf16): a wave's 128 x 128 tile
 constexpr int NS_LDS = (2 * 2 * BT * BLD > 4 * 128 * WLD) ? 2 * 2 * BT * BLD : 4 * 128 * WLD;
 
@@ -244,26 +244,28 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // staging: 4 x 16 B of each operand per thread per step
-  ku4 ra[4], rb[4];
+  // staging: 8 x 16 B of each operand per thread per step (256 rows x 64 K)
+  constexpr int KC = BK / 8;     // 16-byte chunks per row per step
+  constexpr int NS = BT * KC / 256;
+  ku4 ra[NS], rb[NS];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+    for (int s = 0; s < NS; ++s) {
+      const int q = tid + 256 * s, r = q / KC, kc = q % KC;
       ra[s] = *(const KAON_G ku4*)G(Aop + (int64_t)(row0 + r) * lda + k0 + kc * 8);
     }
     if (MODE != 2) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+      for (int s = 0; s < NS; ++s) {
+        const int q = tid + 256 * s, r = q / KC, kc = q % KC;
         rb[s] = *(const KAON_G ku4*)G(Bop + (int64_t)(col0 + r) * ldb + k0 + kc * 8);
       }
     } else {
-      // x: 32 K rows x 256 columns; a thread takes two adjacent K rows of 8
+      // x: BK K rows x 256 columns; a thread takes two adjacent K rows of 8
       // columns, so its transposed LDS writes pack K pairs into 32-bit words
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int q = tid + 256 * s, jc = q >> 4, tp = q & 15;
+      for (int s = 0; s < NS / 2; ++s) {
+        const int q = tid + 256 * s, jc = q / (BK / 2), tp = q % (BK / 2);
         const uint16_t* src = Bop + (int64_t)(k0 + 2 * tp) * ldb + col0 + jc * 8;
         rb[2 * s] = *(const KAON_G ku4*)G(src);
         rb[2 * s + 1] = *(const KAON_G ku4*)G(src + ldb);
@@ -274,20 +276,20 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     uint16_t* as = As(st);
     uint16_t* bs = Bs(st);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+    for (int s = 0; s < NS; ++s) {
+      const int q = tid + 256 * s, r = q / KC, kc = q % KC;
       *(ku4*)&as[r * BLD + kc * 8] = ra[s];
     }
     if (MODE != 2) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int q = tid + 256 * s, r = q >> 2, kc = q & 3;
+      for (int s = 0; s < NS; ++s) {
+        const int q = tid + 256 * s, r = q / KC, kc = q % KC;
         *(ku4*)&bs[r * BLD + kc * 8] = rb[s];
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int q = tid + 256 * s, jc = q >> 4, tp = q & 15;
+      for (int s = 0; s < NS / 2; ++s) {
+        const int q = tid + 256 * s, jc = q / (BK / 2), tp = q % (BK / 2);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           *(uint32_t*)&bs[(jc * 8 + e) * BLD + 2 * tp] = half_of(rb[2 * s], e) | (half_of(rb[2 * s + 1], e) << 16);
@@ -295,30 +297,72 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     }
   };
 
+  // Fragments are double-buffered across the four 16-K sub-steps of a stage:
+  // sub-step t's MFMAs run while t + 1's fragments load, and the scheduling
+  // groups below pin that interleave (left alone, the compiler loads each
+  // fragment right before its MFMAs and one wave per SIMD exposes every LDS
+  // latency).  The next stage's global loads are spread over sub-step 0 and
+  // its LDS stores over sub-step 3; the last step re-loads its own K range so
+  // that the step stays one basic block.
+  bf16x8 fa[2][4], fb[2][4];
+  auto lfrag = [&](int buf, const uint16_t* as, const uint16_t* bs, int kk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[buf][i] = *(const bf16x8*)&as[(wm * 128 + i * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      fb[buf][j] = *(const bf16x8*)&bs[(wn * 128 + j * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+  };
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int SG_MFMA = 0x008, SG_VMEM_RD = 0x020, SG_DS_RD = 0x100, SG_DS_WR = 0x200;
+  constexpr int NWR = MODE == 2 ? NS + NS / 2 * 8 / 2 : 2 * NS;  // LDS store instructions per step
+
   const int nk = K / BK;
   gload(0);
   lstore(0);
   __syncthreads();
   for (int ks = 0; ks < nk; ++ks) {
     const int cur = ks & 1;
-    if (ks + 1 < nk) gload((ks + 1) * BK);
     const uint16_t* as = As(cur);
     const uint16_t* bs = Bs(cur);
+    lfrag(0, as, bs, 0);
+    gload(min(ks + 1, nk - 1) * BK);
+    lfrag(1, as, bs, 16);
+    mma(0);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 8, 0);  // sub-step 0's fragments
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      bf16x8 af[4], bfr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *(const bf16x8*)&as[(wm * 128 + i * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bfr[j] = *(const bf16x8*)&bs[(wn * 128 + j * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, 2 * NS / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
-    if (ks + 1 < nk) lstore(cur ^ 1);  // that stage was last read before the previous barrier
+    lfrag(0, as, bs, 32);
+    mma(1);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+    lfrag(1, as, bs, 48);
+    mma(0);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+    lstore(cur ^ 1);  // that stage was last read before the previous barrier
+    mma(1);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_WR, NWR / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
     __syncthreads();
   }
 
@@ -385,37 +429,91 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   }
 }
 
-// x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
-// the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
-__device__ __forceinline__ void ns_prep_tile(const KaonTensor& T, const NsBufs& nb, double rden, int i0, int t0,
-                                             uint16_t (*tile)[TILE + 2]) {
-  const int64_t C = T.C;
-  const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
-  const KAON_G uint16_t* mo = G((const uint16_t*)nb.mo);
-  KAON_G uint16_t* x = G(nb.x0);
-  if (!T.ns_tr) {
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int i = i0 + (e >> 7), t = t0 + (e & 127);
-      const float v = (i < m && t < k) ? bf2f(mo[(int64_t)i * C + t]) : 0.0f;
-      x[(int64_t)i * T.k_pad + t] = (uint16_t)f2bf(div_r64(v, rden));
+// 8 consecutive bf16 of a row-major matrix from column c of row r; zeros
+// outside rows x cols.  ALN: the row stride is a multiple of 8 (every chunk is
+// 16-byte aligned).
+__device__ __forceinline__ ku4 ns_ld8(const uint16_t* p, int64_t ld, int r, int c, int rows, int cols, bool aln) {
+  if (r >= rows) return ku4{0u, 0u, 0u, 0u};
+  const KAON_G uint16_t* q = G(p) + (int64_t)r * ld + c;
+  if (aln && c + 8 <= cols) return *(const KAON_G ku4*)q;
+  uint32_t h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = c + e < cols ? (uint32_t)q[e] : 0u;
+  return ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
+__device__ __forceinline__ void ns_st8(uint16_t* p, int64_t ld, int r, int c, int rows, int cols, bool aln, ku4 v) {
+  if (r >= rows) return;
+  KAON_G uint16_t* q = G(p) + (int64_t)r * ld + c;
+  if (aln && c + 8 <= cols) {
+    *(KAON_G ku4*)q = v;
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (c + e < cols) q[e] = (uint16_t)half_of(v, e);
+}
+
+// x = bf16(v / den) on 8 packed bf16 (torch's bf16 division: fp32 quotient,
+// rounded to bf16), or v itself
+template <bool SCALE>
+__device__ __forceinline__ ku4 ns_map8(ku4 v, double rden) {
+  if (!SCALE) return v;
+  uint32_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f2bf(div_r64(__uint_as_float(half_of(v, e) << 16), rden));
+  return ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+}
+
+// One 128 x 128 tile from src to dst, dst(r0 + i, c0 + j) = f(src(r0 + i, c0 + j))
+// or, transposed, f(src(c0 + j, r0 + i)); source elements outside its
+// srows x scols read as 0 (the iterate's zero padding), destination writes stay
+// inside drows x dcols.  16-byte global accesses wherever rows are aligned.
+// The transpose goes through an LDS tile of 256-byte rows whose 16-byte chunks
+// are XOR-swizzled by row / 8: row chunk writes and 8-row column reads both
+// touch 16 distinct chunks per 16 lanes.
+template <bool TR, bool SCALE>
+__device__ __forceinline__ void ns_move_tile(const uint16_t* src, int64_t lds_, int srows, int scols, uint16_t* dst,
+                                             int64_t ldd, int drows, int dcols, int r0, int c0, double rden,
+                                             uint16_t* tile) {
+  const bool sa = (lds_ & 7) == 0, da = (ldd & 7) == 0;
+  const int tid = threadIdx.x;
+  if (!TR) {
+#pragma unroll 2
+    for (int q = tid; q < TILE * TILE / 8; q += 256) {
+      const int i = r0 + (q >> 4), j = c0 + (q & 15) * 8;
+      if (i >= drows || j >= dcols) continue;
+      ns_st8(dst, ldd, i, j, drows, dcols, da, ns_map8<SCALE>(ns_ld8(src, lds_, i, j, srows, scols, sa), rden));
     }
-  } else {
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int tt = e >> 7, ii = e & 127, t = t0 + tt, i = i0 + ii;
-      tile[tt][ii] = (t < k && i < m) ? mo[(int64_t)t * C + i] : (uint16_t)0;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int ii = e >> 7, tt = e & 127;
-      x[(int64_t)(i0 + ii) * T.k_pad + t0 + tt] = (uint16_t)f2bf(div_r64(bf2f(tile[tt][ii]), rden));
-    }
+    return;
+  }
+  // source rows c0 .. c0 + 127 (tile rows tt), columns r0 .. r0 + 127
+#pragma unroll 2
+  for (int q = tid; q < TILE * TILE / 8; q += 256) {
+    const int tt = q >> 4, ch = q & 15;
+    const ku4 v = ns_ld8(src, lds_, c0 + tt, r0 + ch * 8, srows, scols, sa);
+    *(ku4*)&tile[tt * TILE + ((ch ^ ((tt >> 3) & 15)) << 3)] = v;
+  }
+  __syncthreads();
+#pragma unroll 2
+  for (int q = tid; q < TILE * TILE / 8; q += 256) {
+    const int ii = q >> 4, g = q & 15;  // destination row r0 + ii, columns c0 + 8 g ..
+    if (r0 + ii >= drows || c0 + g * 8 >= dcols) continue;
+    const int off = (((ii >> 3) ^ g) << 3) + (ii & 7);
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = tile[(g * 8 + e) * TILE + off];
+    const ku4 v = ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    ns_st8(dst, ldd, r0 + ii, c0 + g * 8, drows, dcols, da, ns_map8<SCALE>(v, rden));
   }
 }
 
+// x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
+// the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
 // One item = one tile (kind 0) or 2 x 2 tiles (kind 1, a big-tile item).
 __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, float* ws) {
-  __shared__ uint16_t tile[TILE][TILE + 2];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[TILE * TILE];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
@@ -423,45 +521,30 @@ __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ 
   const int sub = it.kind ? 2 : 1;
   for (int s = 0; s < sub * sub; ++s) {
     if (s) __syncthreads();  // the transpose tile is reused
-    ns_prep_tile(T, nb, rden, (it.row0 * sub + s / sub) * TILE, (it.nrows * sub + s % sub) * TILE, tile);
+    const int i0 = (it.row0 * sub + s / sub) * TILE, t0 = (it.nrows * sub + s % sub) * TILE;
+    if (T.ns_tr)
+      ns_move_tile<true, true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, T.m_pad, T.k_pad, i0, t0, rden, tile);
+    else
+      ns_move_tile<false, true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, T.m_pad, T.k_pad, i0, t0, rden, tile);
   }
 }
 
 // O [R, C] from the final iterate (transposed back when R > C), over M.
-__device__ __forceinline__ void ns_post_tile(const KaonTensor& T, const NsBufs& nb, int parity, int i0, int t0,
-                                             uint16_t (*tile)[TILE + 2]) {
-  const int64_t C = T.C;
-  const int m = (int)(T.R < T.C ? T.R : T.C), k = (int)(T.R < T.C ? T.C : T.R);
-  const KAON_G uint16_t* x = G((const uint16_t*)(parity ? nb.x1 : nb.x0));
-  KAON_G uint16_t* o = G(nb.mo);
-  if (!T.ns_tr) {
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int i = i0 + (e >> 7), t = t0 + (e & 127);
-      if (i < m && t < k) o[(int64_t)i * C + t] = x[(int64_t)i * T.k_pad + t];
-    }
-  } else {
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int ii = e >> 7, tt = e & 127;
-      tile[tt][ii] = x[(int64_t)(i0 + ii) * T.k_pad + t0 + tt];
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < TILE * TILE; e += 256) {
-      const int tt = e >> 7, ii = e & 127, t = t0 + tt, i = i0 + ii;
-      if (t < k && i < m) o[(int64_t)t * C + i] = tile[tt][ii];
-    }
-  }
-}
-
 __global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, float* ws, int parity) {
-  __shared__ uint16_t tile[TILE][TILE + 2];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[TILE * TILE];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
+  const uint16_t* x = parity ? nb.x1 : nb.x0;
   const int sub = it.kind ? 2 : 1;
   for (int s = 0; s < sub * sub; ++s) {
     if (s) __syncthreads();
-    ns_post_tile(T, nb, parity, (it.row0 * sub + s / sub) * TILE, (it.nrows * sub + s % sub) * TILE, tile);
+    const int i0 = (it.row0 * sub + s / sub) * TILE, t0 = (it.nrows * sub + s % sub) * TILE;
+    if (T.ns_tr)  // O(t, i) = x(i, t)
+      ns_move_tile<true, false>(x, T.k_pad, T.m_pad, T.k_pad, nb.mo, T.C, (int)T.R, (int)T.C, t0, i0, 0.0, tile);
+    else
+      ns_move_tile<false, false>(x, T.k_pad, T.m_pad, T.k_pad, nb.mo, T.C, (int)T.R, (int)T.C, i0, t0, 0.0, tile);
   }
 }
 

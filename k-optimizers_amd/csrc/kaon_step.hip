@@ -1002,11 +1002,12 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
       }
       uint32_t mq[8];
       if (mom) ld_mom_raw<CODEC>(T, e0, cnt, vv, mq);
-      uint32_t qout[8];
+      uint32_t qout[8], mob[8];
       float Mv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qout[i] = 0u;
+        mob[i] = 0u;
         Mv[i] = 0.0f;
         if (i >= cnt) continue;
         if (!mom) {
@@ -1032,7 +1033,13 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
         const uint32_t xb = f2bf(Mv[i]);
         const float xf = bf2f(xb);
         sq = sq + xf * xf;
-        mo[e0 + i] = (uint16_t)xb;
+        mob[i] = xb;
+      }
+      if (vv) {
+        *(KAON_G ku4*)(mo + e0) = ku4{mob[0] | (mob[1] << 16), mob[2] | (mob[3] << 16), mob[4] | (mob[5] << 16),
+                                      mob[6] | (mob[7] << 16)};
+      } else {
+        for (int i = 0; i < cnt; ++i) mo[e0 + i] = (uint16_t)mob[i];
       }
       if (mom && (CODEC == KAON_MOM_BF16 || CODEC == KAON_MOM_F32)) st_mom_raw<CODEC>(T, e0, cnt, vv, qout);
     }

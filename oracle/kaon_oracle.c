@@ -18,11 +18,13 @@
  *   - Lion          src/kaon/lion.py:454-485 (== batched :416-451)
  *   - AdaMuon       src/kaon/adamuon.py:97-149, 557-615 (== batched :434-555)
  *   - MSAM/Nekaon   src/kaon/msam.py:169-235, 375-406 ; src/kaon/nekaon.py:162-171
+ *   - AdaPNM        src/kaon/adapnm.py:998-1016, 1209-1275 (== batched :1069-1200)
  *
  * Rounding model (measured against torch 2.10 CPU in this image, see
  * tests/test_oracle_torch_semantics.py):
  *   - lerp(a,b,w): |w|<0.5 -> fma(w, b-a, a), else fma(w-1, b-a, b)
  *   - add_(x, alpha=s): fma(s, x, self)
+ *   - addcmul_(t1, t2, value=s): fma(s * t1, t2, self)
  *   - rsqrt(x): 1/sqrt(x) (two correctly rounded ops)
  *   - x / python_scalar: true fp32 division by (float)scalar
  *   - bf16 mean: bf16(fp32_sum / C) (one rounding); bf16 a-b: bf16(fp32(a-b))
@@ -190,6 +192,10 @@ typedef struct {
     float* out_m;        /* optional: AdaMuon NS output O [R*C] (fp32), diagnostics */
     const float* fac_override; /* optional: clip divisor to use instead of the computed
                                   one (lets a test inject torch's own norm value) */
+    void* m2;            /* AdaPNM: the negative momentum buffer (read only); m is the
+                            positive one, which takes the gradient this step */
+    float* m2_scale;
+    float* max_v;        /* AdaPNM ams_bound: running max of v (1-D) */
 } KoTensor;
 
 typedef struct {
@@ -201,6 +207,9 @@ typedef struct {
     /* Nekaon lookahead fused into the Adakaon step */
     int32_t nk_remove, nk_climb;
     double nk_k, nk_bound_old, nk_bound_new;
+    /* AdaPNM */
+    double beta0;
+    int32_t ams_bound;
 } KoHyper;
 
 static inline float load_g(const KoTensor* t, int64_t i) {
@@ -411,8 +420,10 @@ int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bou
 
 /* ------------------------------------------------ factored second moment */
 /* update_factored_state + factored_inv_sqrt_factors (src/kaon/_factored.py)
- * on x [R, C]; returns U = (x * r) * c in `u`. */
-static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u) {
+ * on x [R, C]: the row/col EMAs, then r = rsqrt(row / mean(row)) into rf [R]
+ * and c = rsqrt(col) into cf [C]. */
+static void factored_state(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* rf,
+                           float* cf) {
     int64_t R = t->R, C = t->C;
     int64_t RW = ko_rows_per_wave(C);
     float* q = (float*)malloc(sizeof(float) * (size_t)C);
@@ -441,17 +452,24 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
             }
         }
     }
-    float* cf = (float*)malloc(sizeof(float) * (size_t)C);
     for (int64_t j = 0; j < C; ++j) {
         t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
         cf[j] = ko_rsqrt(t->col[j]);
     }
     float rm = ko_csum(t->row, R) / (float)R;
-    for (int64_t r = 0; r < R; ++r) {
-        float rf = ko_rsqrt(t->row[r] / rm);
-        for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf) * cf[j];
-    }
-    free(q); free(pw); free(ps); free(pr); free(colsum); free(cf);
+    for (int64_t r = 0; r < R; ++r) rf[r] = ko_rsqrt(t->row[r] / rm);
+    free(q); free(pw); free(ps); free(pr); free(colsum);
+}
+
+/* The factored step's U = (x * r) * c. */
+static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u) {
+    int64_t R = t->R, C = t->C;
+    float* rf = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
+    float* cf = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+    factored_state(t, x, w2, eps1f, add_eps, rf, cf);
+    for (int64_t r = 0; r < R; ++r)
+        for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf[r]) * cf[j];
+    free(rf); free(cf);
 }
 
 /* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):
@@ -542,6 +560,84 @@ int ko_lion_tensor(const KoTensor* t, const KoHyper* h) {
     for (int64_t i = 0; i < n; ++i) d[i] = d[i] * lr;
     write_sub(t, d, h, 1);
     free(g); free(m); free(d);
+    return 0;
+}
+
+/* ------------------------------------------------------------- AdaPNM */
+/* One AdaPNM step (_step_one_param, adapnm.py:1209-1275; coefficients
+ * _coeffs :998-1016).  t->m is the positive buffer of this step (the one the
+ * gradient goes into), t->m2 the negative one; the caller alternates them by
+ * step parity (_pos_neg_prefixes :588-596).  h->step is the group's step
+ * count after its increment (bias corrections). */
+int ko_adapnm_tensor(const KoTensor* t, const KoHyper* h) {
+    int64_t n = t->R * t->C;
+    if (n <= 0) return 0;
+    const double b1 = h->beta1, b2 = h->beta2, b0 = h->beta0;
+    const double b1sq = b1 * b1;
+    const double noise_norm = sqrt((1.0 + b0) * (1.0 + b0) + b0 * b0);
+    const double bc1 = 1.0 - pow(b1, (double)h->step);
+    const double bc2_sq = sqrt(1.0 - pow(b2, (double)h->step));
+    const float fb1sq = (float)b1sq, fa1 = (float)(1.0 - b1sq);
+    const float fpos = (float)(1.0 + b0), fneg = (float)(-b0), frn = (float)(1.0 / noise_norm);
+    const float fbc2 = (float)bc2_sq, fstep = (float)(h->lr / bc1);
+    const float fb2 = (float)b2, fa2 = (float)(1.0 - b2), feps = (float)h->eps1;
+
+    float* g = centralized_grad(t, h->gc);
+    /* decoupled weight decay first, in the param dtype: p *= (1 - lr*wd) */
+    if (h->wd != 0) {
+        const float f = (float)(1.0 - h->lr * h->wd);
+        if (t->p_dtype == KO_BF16) {
+            uint16_t* p = (uint16_t*)t->p;
+            for (int64_t i = 0; i < n; ++i) p[i] = f_to_bf16(bf16_to_f(p[i]) * f);
+        } else {
+            float* p = (float*)t->p;
+            for (int64_t i = 0; i < n; ++i) p[i] = p[i] * f;
+        }
+    }
+    float* u = (float*)malloc(sizeof(float) * (size_t)n);
+    float* mp = (float*)malloc(sizeof(float) * (size_t)n);
+    float* mn = (float*)malloc(sizeof(float) * (size_t)n);
+    /* second moment: factored r, c or the 1-D denominator */
+    float* rf = NULL;
+    float* cf = NULL;
+    if (t->factored) {
+        rf = (float*)malloc(sizeof(float) * (size_t)t->R);
+        cf = (float*)malloc(sizeof(float) * (size_t)t->C);
+        factored_state(t, g, fa2, feps, h->eps1 > 0, rf, cf);
+    }
+    /* both momenta as fp32; EMA of the positive one with the raw gradient
+     * (mul_(beta1^2).add_(g, alpha=1-beta1^2)), stored back through its codec */
+    mom_dequant(t, mp);
+    KoTensor neg = *t;
+    neg.m = t->m2;
+    neg.m_scale = t->m2_scale;
+    mom_dequant(&neg, mn);
+    for (int64_t i = 0; i < n; ++i) mp[i] = fmaf(fa1, g[i], mp[i] * fb1sq);
+    mom_store_quant(t, mp);
+    /* pn = ((1+b0) m_pos - b0 m_neg) / noise_norm, times 1/sqrt(v_hat) */
+    for (int64_t i = 0; i < n; ++i) {
+        const float pn = fmaf(fneg, mn[i], mp[i] * fpos) * frn;
+        if (t->factored) {
+            const int64_t r = i / t->C, j = i % t->C;
+            u[i] = pn * ((rf[r] * cf[j]) * fbc2);
+        } else {
+            /* v.mul_(beta2).addcmul_(g, g, value=1-beta2); denominator
+             * (sqrt(v + 1e-15) + eps) / bc2, from max_v under ams_bound */
+            t->v[i] = fmaf(fa2 * g[i], g[i], t->v[i] * fb2);
+            float vv = t->v[i];
+            if (h->ams_bound && t->max_v) {
+                t->max_v[i] = fmaxf(t->max_v[i], t->v[i]);
+                vv = t->max_v[i];
+            }
+            const float de = (sqrtf(vv + 1e-15f) + feps) / fbc2;
+            u[i] = pn / de;
+        }
+    }
+    if (h->clip > 0) clip_scale(t, u, h->clip, fstep);
+    else for (int64_t i = 0; i < n; ++i) u[i] = u[i] * fstep;
+    if (h->cautious) cautious(u, g, n);
+    write_sub(t, u, h, 1);
+    free(g); free(u); free(mp); free(mn); free(rf); free(cf);
     return 0;
 }
 

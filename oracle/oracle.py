@@ -16,6 +16,8 @@ reference's per-parameter state layout:
 * AdaMuon ``_init_state``  -- src/kaon/adamuon.py:297-316
 * codec ``init_state``     -- src/kaon/_momentum_codec.py:263-264, 296-301, 351-361
 * MSAM / Nekaon lookahead  -- src/kaon/msam.py:169-188, 375-406; src/kaon/nekaon.py:162-171
+* AdaPNM ``_init_state`` / ``_alloc_momentum`` -- src/kaon/adapnm.py:451-500 (two momenta,
+  ``m_pos`` / ``m_neg``, whose roles alternate by step parity, :588-596)
 
 Arrays: bf16 tensors are ``np.uint16`` bit patterns, fp32 are ``np.float32``.
 """
@@ -49,6 +51,7 @@ class KoTensor(ctypes.Structure):
         ("noise", ctypes.c_void_p * 3),
         ("out_m", ctypes.c_void_p),
         ("fac_override", ctypes.c_void_p),
+        ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
     ]
 
 
@@ -61,6 +64,7 @@ class KoHyper(ctypes.Structure):
         ("seed", ctypes.c_uint64), ("step", ctypes.c_uint32),
         ("nk_remove", ctypes.c_int32), ("nk_climb", ctypes.c_int32),
         ("nk_k", ctypes.c_double), ("nk_bound_old", ctypes.c_double), ("nk_bound_new", ctypes.c_double),
+        ("beta0", ctypes.c_double), ("ams_bound", ctypes.c_int32),
     ]
 
 
@@ -74,7 +78,7 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(_LIB_PATH):
             raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run `make -C oracle`)")
         L = ctypes.CDLL(_LIB_PATH)
-        for name in ("ko_adakaon_tensor", "ko_lion_tensor", "ko_adamuon_tensor"):
+        for name in ("ko_adakaon_tensor", "ko_lion_tensor", "ko_adamuon_tensor", "ko_adapnm_tensor"):
             getattr(L, name).argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper)]
             getattr(L, name).restype = ctypes.c_int
         L.ko_msam_apply.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
@@ -247,10 +251,44 @@ class OParam:
         return 1, self.numel
 
 
+def _alloc_momentum(st: dict[str, Any], prefix: str, prm: OParam, group: dict[str, Any]) -> None:
+    """One momentum buffer under ``prefix`` (src/kaon/adapnm.py:451-479; the codec
+    layouts of src/kaon/_momentum_codec.py:263-264, 296-301, 351-361)."""
+    R, _ = prm.eff
+    n = prm.numel
+    md = group["momentum_dtype"]
+    if md == "float32":
+        st[prefix] = np.zeros(prm.shape, dtype=np.float32)
+    elif md == "bfloat16":
+        st[prefix] = np.zeros(prm.shape, dtype=np.uint16)
+    elif md == "int8":
+        st[prefix] = np.zeros(prm.shape, dtype=np.int8)
+        st[f"{prefix}_scale"] = np.ones(R if prm.factored else 1, dtype=np.float32)
+    else:
+        bs = fourbit_block_size(n, group["momentum_4bit_block"])
+        st[prefix] = np.full((n + 1) // 2, 0x88, dtype=np.uint8)
+        st[f"{prefix}_scale"] = np.ones((n + bs - 1) // bs, dtype=np.float32)
+        st[f"{prefix}_numel"] = n
+        st[f"{prefix}_block"] = bs
+
+
 def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
     st = prm.state
     R, C = prm.eff
     n = prm.numel
+    if opt == "adapnm":
+        if prm.factored:
+            st["row"] = np.zeros(R, dtype=np.float32)
+            st["col"] = np.zeros(C, dtype=np.float32)
+        else:
+            st["v"] = np.zeros(n, dtype=np.float32)
+            if group.get("ams_bound"):
+                st["max_v"] = np.zeros(n, dtype=np.float32)
+        _alloc_momentum(st, "m_pos", prm, group)
+        _alloc_momentum(st, "m_neg", prm, group)
+        if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+            st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
+        return
     if opt in ("adakaon", "adamuon"):
         if prm.factored:
             st["row"] = np.zeros(R, dtype=np.float32)
@@ -303,12 +341,26 @@ def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) 
     return t
 
 
+def _pnm_tensor(prm: OParam, codec: str, step: int, noise=None) -> KoTensor:
+    """AdaPNM: m = this step's positive buffer, m2 = the negative one
+    (_pos_neg_prefixes, src/kaon/adapnm.py:588-596: m_pos on odd steps)."""
+    st = prm.state
+    pos, neg = ("m_pos", "m_neg") if step % 2 == 1 else ("m_neg", "m_pos")
+    t = _tensor(prm, codec, noise)
+    t.m, t.m_scale = _ptr(st[pos]), _ptr(st.get(f"{pos}_scale"))
+    t.m2, t.m2_scale = _ptr(st[neg]), _ptr(st.get(f"{neg}_scale"))
+    t.max_v = _ptr(st.get("max_v"))
+    t.codec = MOM_CODE[codec]
+    t.block4 = int(st.get("m_pos_block", 0))
+    return t
+
+
 def _hyper(group: dict[str, Any], seed: int, step: int) -> KoHyper:
     h = KoHyper()
     h.lr = group["lr"]
     h.beta1, h.beta2 = group["betas"]
     eps = group.get("eps", (0.0, 0.0))
-    h.eps1 = eps[0]
+    h.eps1 = eps if isinstance(eps, float) else eps[0]
     h.wd = group.get("weight_decay", 0.0)
     h.clip = group.get("clip_threshold", 1.0)
     h.cautious = int(group.get("cautious", True))
@@ -317,6 +369,8 @@ def _hyper(group: dict[str, Any], seed: int, step: int) -> KoHyper:
     h.ns_steps = int(group.get("ns_steps", 2))
     h.seed = seed
     h.step = step
+    h.beta0 = float(group.get("beta0", 0.0))
+    h.ams_bound = int(bool(group.get("ams_bound", False)))
     return h
 
 
@@ -328,7 +382,7 @@ def _check(rc: int) -> None:
 class OracleOptimizer:
     """Step driver over a list of OParam for one param group.
 
-    ``opt`` is ``"adakaon" | "lion" | "adamuon" | "nekaon"``.  Nekaon is the MSAM
+    ``opt`` is ``"adakaon" | "lion" | "adamuon" | "nekaon" | "adapnm"``.  Nekaon is the MSAM
     ``norm="none"``, ``rho=-k`` preset over Adakaon (src/kaon/nekaon.py:162-171):
     the removal of the previous climb and the new climb are folded into the
     per-tensor step exactly where MSAM.step runs them (msam.py:384-403).
@@ -358,6 +412,10 @@ class OracleOptimizer:
             h.nk_k = self.k
             h.nk_bound_new = new_bound
         for prm in self.params:
+            if self.opt == "adapnm":
+                t = _pnm_tensor(prm, md, self.t, None if noise is None else noise.get(prm.tensor_id))
+                _check(lib().ko_adapnm_tensor(ctypes.byref(t), ctypes.byref(h)))
+                continue
             t = _tensor(prm, md, None if noise is None else noise.get(prm.tensor_id),
                         fac_override=None if fac_override is None else fac_override.get(prm.tensor_id))
             if self.opt in ("adakaon", "nekaon"):

@@ -64,6 +64,19 @@ CASES = {
     "nekaon_int8_f32": _case("nekaon", _SMALL, dict(lr=1e-3, k=1.5, betas=(0.5, 0.999), momentum_dtype="int8",
                                                     foreach=False),
                              p_dtype="f32", g_dtype="f32", eval_train=True),
+    # AdaPNM (src/kaon/adapnm.py) -- two momenta alternating by step parity
+    "pnm_bf16_sr": _case("adapnm", _SMALL, dict(lr=1e-3, betas=(0.8, 0.999), beta0=0.5,
+                                                momentum_dtype="bfloat16", foreach=False)),
+    "pnm_int8_sr": _case("adapnm", _SMALL, dict(lr=1e-3, betas=(0.8, 0.999), beta0=1.0, weight_decay=0.01,
+                                                momentum_dtype="int8", foreach=False)),
+    "pnm_4bit_rn": _case("adapnm", _ODD, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="4bit",
+                                              momentum_4bit_block=16, bf16_method="none", foreach=True)),
+    "pnm_f32_ams": _case("adapnm", _SMALL, dict(lr=1e-3, betas=(0.8, 0.99), weight_decay=0.1,
+                                                momentum_dtype="float32", ams_bound=True, clip_threshold=0.0,
+                                                cautious=False, foreach=True),
+                         p_dtype="f32", g_dtype="f32"),
+    "pnm_kahan": _case("adapnm", _SMALL, dict(lr=1e-3, momentum_dtype="bfloat16", bf16_method="kahan",
+                                              foreach=False)),
 }
 
 # Adakaon on a conv [320,320,3,3] and a linear [1280,1280],

@@ -2,10 +2,10 @@
 
 Run in the build container only (the reference is not present on the GPU box):
 
-    python tests/golden/make_golden.py /root/reference/src
+    python tests/golden/make_golden.py /root/reference/src [case ...]
 
 It imports the reference ``kaon`` package (pure Python + torch CPU) and steps
-its Adakaon / Lion / AdaMuon / Nekaon on small seeded inputs.  The codecs, the
+its Adakaon / Lion / AdaMuon / Nekaon / AdaPNM on small seeded inputs.  The codecs, the
 SR bit trick, the cautious rule and the Philox stream are pinned by closed
 forms and known-answer tests elsewhere; what only the reference itself can pin
 is the composition of torch-CPU ops (lerp/FMA placement, bf16-rounded GC,
@@ -116,6 +116,8 @@ def make_opt(kaon, case, params):
         return kaon.AdaMuon(params, **kw)
     if name == "nekaon":
         return kaon.Nekaon(params, **kw)
+    if name == "adapnm":
+        return kaon.AdaPNM(params, **kw)
     raise ValueError(name)
 
 
@@ -162,19 +164,27 @@ def run_case(kaon, case):
 
 
 def main() -> None:
+    """argv: [reference src dir] [case names ...]; no names = every case."""
     ref_src = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src"
+    only = set(sys.argv[2:])
     sys.path.insert(0, ref_src)
     import kaon  # the reference package (this container only)
 
     _install_noise_hooks(kaon)
     meta = {"torch": torch.__version__, "cpu_capability": torch.backends.cpu.get_cpu_capability(),
             "threads": torch.get_num_threads(), "kaon_version": kaon.__version__, "cases": {}}
+    meta_path = os.path.join(HERE, "golden_meta.json")
+    if only and os.path.exists(meta_path):
+        with open(meta_path) as fh:
+            meta["cases"] = json.load(fh).get("cases", {})
     for name, case in list(CASES.items()) + [("cfg0", CFG0)]:
+        if only and name not in only:
+            continue
         out = run_case(kaon, case)
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **{k: v for k, v in out.items() if k != "hashes"})
         meta["cases"][name] = {"hashes": out["hashes"]}
         print(name, out["hashes"][-1][:16], flush=True)
-    with open(os.path.join(HERE, "golden_meta.json"), "w") as fh:
+    with open(meta_path, "w") as fh:
         json.dump(meta, fh, indent=1, sort_keys=True)
 
 

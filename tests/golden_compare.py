@@ -18,7 +18,8 @@ from cases import CASES, CFG0, grad_values, param_values  # noqa: E402
 
 # Constructor defaults of each reference optimizer (what the case kwargs do not set):
 # Adakaon src/kaon/adakaon.py:195-218, Lion src/kaon/lion.py:152-171,
-# AdaMuon src/kaon/adamuon.py:216-239, Nekaon src/kaon/nekaon.py:122-137.
+# AdaMuon src/kaon/adamuon.py:216-239, Nekaon src/kaon/nekaon.py:122-137,
+# AdaPNM src/kaon/adapnm.py:344-370.
 DEFAULTS = {
     "adakaon": dict(lr=1e-3, betas=(0.9, 0.999), eps=(1e-30, 1e-3), weight_decay=0.0, clip_threshold=1.0,
                     momentum_dtype="bfloat16", momentum_4bit_block=128, cautious=True,
@@ -32,6 +33,9 @@ DEFAULTS = {
     "nekaon": dict(lr=1e-3, k=1.5, betas=(0.5, 0.999), eps=(1e-30, 1e-3), weight_decay=0.1,
                    clip_threshold=1.0, momentum_dtype="4bit", momentum_4bit_block=128, cautious=True,
                    gradient_centralization=True, bf16_method="stochastic_rounding"),
+    "adapnm": dict(lr=1e-3, betas=(0.8, 0.999), beta0=0.5, eps=1e-8, weight_decay=0.0, clip_threshold=1.0,
+                   cautious=True, gradient_centralization=True, ams_bound=False, momentum_dtype="bfloat16",
+                   momentum_4bit_block=128, bf16_method="stochastic_rounding"),
 }
 _IGNORED = ("foreach", "foreach_batch_cutoff", "foreach_stack_budget", "fused")
 

@@ -14,6 +14,9 @@ What must agree:
   weights agree to 1e-4 relative (cautious-mask flips at |g| ~ 0 dominate);
 * AdaMuon: bf16 Newton-Schulz GEMM accumulation order -> tolerance
   (the reference's own batched-vs-per-slice tolerance rtol 2e-2, atol 2e-3).
+* AdaPNM (pnm_* cases): both momentum buffers (codes and scales) under the same
+  bars as the single buffer of the other optimizers, over five steps, so each
+  buffer is the positive one at least twice.
 """
 import json
 import os
@@ -31,8 +34,11 @@ F32_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "f32"]
 MUON_CASES = [k for k, c in CASES.items() if c["opt"] == "adamuon"]
 
 
+_MOM = ("m", "m_pos", "m_neg")  # Adakaon / Lion / AdaMuon / Nekaon, AdaPNM's two buffers
+
+
 def _compare_state(prm, gold, i, tol):
-    for k in ("row", "col", "v"):
+    for k in ("row", "col", "v", "max_v"):
         if f"s{i}_{k}" in gold:
             assert rel_err(prm.state[k], gold[f"s{i}_{k}"]) <= tol, (k, i)
 
@@ -48,11 +54,12 @@ def test_bf16_cases_match_reference(name):
         total += prm.p.size
         diff += nm
         _compare_state(prm, gold, i, 1e-6)
-        if "m_scale" in prm.state:
-            assert rel_err(prm.state["m_scale"], gold[f"s{i}_m_scale"].reshape(-1)) <= 1e-6
-        if "m" in prm.state:
-            a, b = prm.state["m"].reshape(-1), gold[f"s{i}_m"].reshape(-1)
-            assert (a != b).sum() <= max(1, a.size // 500), (name, i)
+        for k in _MOM:
+            if f"{k}_scale" in prm.state:
+                assert rel_err(prm.state[f"{k}_scale"], gold[f"s{i}_{k}_scale"].reshape(-1)) <= 1e-6
+            if k in prm.state:
+                a, b = prm.state[k].reshape(-1), gold[f"s{i}_{k}"].reshape(-1)
+                assert (a != b).sum() <= max(1, a.size // 500), (name, i, k)
         if evalp is not None:
             nm2, _ = bf16_mismatch(evalp[i], gold[f"p{i}_eval"])
             diff += nm2
@@ -69,8 +76,10 @@ def test_fp32_grad_cases_match_reference(name):
         ref = gold[f"p{i}"]
         assert np.allclose(prm.p, ref, rtol=1e-4, atol=1e-7), (name, i)
         _compare_state(prm, gold, i, 1e-5)
-        if "m" in prm.state and prm.state["m"].dtype == np.float32:
-            assert np.allclose(prm.state["m"], gold[f"s{i}_m"], rtol=1e-3, atol=1e-8)
+        for k in _MOM:
+            if k in prm.state and prm.state[k].dtype == np.float32:
+                assert np.allclose(prm.state[k], gold[f"s{i}_{k}"].reshape(prm.state[k].shape), rtol=1e-3,
+                                   atol=1e-8), (name, i, k)
         if evalp is not None:
             assert np.allclose(evalp[i], gold[f"p{i}_eval"], rtol=1e-4, atol=1e-7)
 

@@ -12,7 +12,9 @@ the ground truth for one-op rounding questions the fixtures cannot isolate:
   (src/kaon/_backend.py:147-177) on rows short enough that torch's fp32 sum
   is exact, so the reduction order cannot matter;
 * the SR bit trick against its three-op torch form
-  (src/kaon/_stochastic_rounding.py:88-103).
+  (src/kaon/_stochastic_rounding.py:88-103);
+* addcmul_(g, g, value=s) after mul_(beta2): AdaPNM's 1-D second moment
+  (src/kaon/adapnm.py:1243-1244), one fma of (s * g) and g into v * beta2.
 
 A plausible slip -- a lerp without the fma, the branch threshold on the wrong
 side, truncation instead of RNE, an fp32 instead of a bf16 GC -- fails one of
@@ -78,3 +80,28 @@ def test_sr_round_matches_three_op_torch_form():
     t.add_(torch.from_numpy(noise.astype(np.int32))).bitwise_and_(-65536)
     want = t.view(torch.float32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(O.sr_round(x, noise), want)
+
+
+def test_pnm_addcmul_second_moment_matches_torch():
+    """The oracle's AdaPNM 1-D ``v`` after three steps equals torch CPU's
+    ``v.mul_(beta2).addcmul_(g, g, value=1 - beta2)`` bit for bit; the unfused
+    form (two products and an add) differs on these inputs, so the fma is pinned."""
+    from golden_compare import DEFAULTS
+
+    n, b2 = 4096, 0.99
+    group = dict(DEFAULTS["adapnm"], betas=(0.8, b2), momentum_dtype="float32")
+    rng = np.random.default_rng(7)
+    prm = O.make_param((n,), O.F32, O.F32, p_values=np.zeros(n, dtype=np.float32))
+    opt = O.OracleOptimizer([prm], "adapnm", group)
+    v = torch.zeros(n)
+    unfused = np.zeros(n, dtype=np.float32)
+    fb2, fa2 = np.float32(b2), np.float32(1.0 - b2)
+    for _ in range(3):
+        g = (rng.standard_normal(n) * np.exp(rng.uniform(-6, 0, n))).astype(np.float32)
+        prm.g = g.copy()
+        opt.step()
+        v.mul_(b2).addcmul_(torch.from_numpy(g), torch.from_numpy(g), value=1.0 - b2)
+        unfused = (unfused * fb2 + ((fa2 * g) * g).astype(np.float32)).astype(np.float32)
+    want = v.numpy()
+    assert np.array_equal(prm.state["v"].view(np.uint32), want.view(np.uint32))
+    assert (unfused.view(np.uint32) != want.view(np.uint32)).sum() > 10

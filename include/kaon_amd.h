@@ -12,7 +12,9 @@
  * 506-513, 533-539), and MSAM's 4-bit perturbation launch
  * (src/kaon/msam.py:238-290 -> _fused_triton.py:1145-1179).  Lion
  * (src/kaon/lion.py:322-485) and AdaMuon (src/kaon/adamuon.py:327-615) call
- * torch ops directly; this ABI covers all four optimizers.
+ * torch ops directly; this ABI covers all four optimizers, and AdaPNM
+ * (src/kaon/adapnm.py, whose Triton path _fused_triton.py:724-1143 is launched
+ * from adapnm.py:647-980).
  *
  * Conventions
  *  - Plain C types only.  Every pointer inside KaonTensor / KaonItem points to
@@ -33,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 5
+#define KAON_ABI_VERSION 6
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -46,7 +48,7 @@ enum { KAON_MOM_NONE = 0, KAON_MOM_F32 = 1, KAON_MOM_BF16 = 2, KAON_MOM_INT8 = 3
 enum { KAON_SR = 0, KAON_RN = 1, KAON_KAHAN = 2 };
 
 /* optimizer selected by a plan / step */
-enum { KAON_OPT_ADAKAON = 0, KAON_OPT_LION = 1, KAON_OPT_ADAMUON = 2 };
+enum { KAON_OPT_ADAKAON = 0, KAON_OPT_LION = 1, KAON_OPT_ADAMUON = 2, KAON_OPT_ADAPNM = 3 };
 
 /* per-launch flags (KaonHyper.flags) */
 enum {
@@ -57,8 +59,11 @@ enum {
   KAON_F_MOMENTUM = 16, /* beta1 > 0 and a momentum buffer exists */
   KAON_F_NK_REMOVE = 32,/* Nekaon: remove the previous climb first (msam.py:386-388) */
   KAON_F_NK_CLIMB = 64, /* Nekaon: climb along the new momentum (msam.py:395-403) */
-  KAON_F_SRC_O = 128    /* set by the library for AdaMuon's factored passes: the row kernels
+  KAON_F_SRC_O = 128,   /* set by the library for AdaMuon's factored passes: the row kernels
                            read the orthogonalized O from the workspace instead of the grad */
+  KAON_F_PNM = 256,     /* set by the library for AdaPNM: the 1-D second moment is
+                           v*beta2 + (1-beta2)*g*g (adapnm.py:1243-1244) */
+  KAON_F_AMS = 512      /* AdaPNM ams_bound: 1-D denominators from the running max of v */
 };
 
 /*
@@ -78,6 +83,9 @@ typedef struct KaonTensor {
   float* col;             /* factored: "col" [C] */
   float* v;               /* 1-D: "v" [C] */
   void* shift;            /* kahan compensation [R*C] in p_dtype */
+  void* m2;               /* AdaPNM: "m_neg", layout as m ("m_pos"); adapnm.py:451-500 */
+  float* m2_scale;        /* AdaPNM: "m_neg_scale" */
+  float* max_v;           /* AdaPNM ams_bound, 1-D: "max_v" [C] */
   const uint16_t* noise[3]; /* optional injected SR noise per stream (tests) */
   int64_t R, C;           /* matrixized shape */
   int64_t n;              /* R * C */
@@ -189,7 +197,13 @@ typedef struct KaonLaunch {
 /* Per-launch hyper-parameters of one param group, rounded to fp32 on the
  * host exactly as the reference's torch ops see them (python float ->
  * fp32 scalar):  w1 = 1 - beta1, w2 = 1 - beta2 (lerp weights), wdl = lr*wd
- * (Adakaon/AdaMuon, adakaon.py:1007-1009) or wd (Lion, lion.py:476-477). */
+ * (Adakaon/AdaMuon, adakaon.py:1007-1009) or wd (Lion, lion.py:476-477).
+ * AdaPNM (_coeffs, adapnm.py:998-1016; step t = the group's step count after
+ * its increment): lr = lr / (1 - beta1^t); b1 = beta1^2, a1 = 1 - beta1^2;
+ * b2 = beta2, a2 = w2 = 1 - beta2; eps1 = eps; wdl = 1 - lr*wd (the decoupled
+ * decay multiplier, :1231-1232); pn_pos = 1 + beta0, pn_neg = -beta0,
+ * pn_rnorm = 1 / sqrt((1+beta0)^2 + beta0^2); bc2 = sqrt(1 - beta2^t);
+ * clip 0 = no clip. */
 typedef struct KaonHyper {
   float lr;               /* Adakaon/Lion lr; AdaMuon passes 0.2*lr (adamuon.py:88, 588) */
   float w1, w2;
@@ -200,6 +214,7 @@ typedef struct KaonHyper {
   float nk_k;             /* Nekaon k (rho = -k), nekaon.py:162-171 */
   float nk_bound_old;     /* frozen climb bound of the previous climb (msam.py:169-188) */
   float nk_bound_new;     /* |k| * clip * lr at this climb */
+  float pn_pos, pn_neg, pn_rnorm, bc2; /* AdaPNM */
   int32_t flags;          /* KAON_F_* */
   int32_t p_dtype, g_dtype, codec, bf16_method;
   int32_t ns_steps;       /* AdaMuon Newton-Schulz iterations */
@@ -244,6 +259,17 @@ int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
  * (adamuon.py:594-604). */
 int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
+/* AdaPNM step over one planned param group (plan opt = KAON_OPT_ADAPNM):
+ * decoupled WD, factored (or 1-D, optionally AMSBound) second moment with
+ * bias correction, EMA of this step's positive momentum with the raw grad
+ * (decay beta1^2), positive-negative mix, RMS clip, lr / (1 - beta1^t),
+ * cautious against the grad, write.  m is "m_pos" and m2 "m_neg": odd steps
+ * (hp->step) take m as the positive buffer, even steps m2
+ * (_pos_neg_prefixes, adapnm.py:588-596).  Replaces AdaPNM._step_one_param /
+ * _factored_bucket / _nonfactored_bucket (adapnm.py:1069-1275) and the fused
+ * launches of adapnm.py:647-980. */
+int kaon_adapnm_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
 /* The same steps restricted to the phases whose bit is set in `mask`
  * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,
  * 4 clip divisor, 5 keep-count + momentum absmax, 6 apply; Lion uses 1, 5,
@@ -256,6 +282,9 @@ int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, vo
  * Newton-Schulz GEMMs and the orthogonal factor O; then bits 1-6 as above on
  * O.  The step is mask 0x37E. */
 int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
+/* AdaPNM: bits 1-6; phase 3 also records the new positive momentum's int8 row /
+ * 4-bit block absmax, phase 5 is the cautious keep count. */
+int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream);
 
 /* MSAM norm="none" perturbation p += clamp(nan_to_num(factor * dequant(m)), +-bound)
  * (msam.py:202-235; fused 4-bit twin _fused_triton.py:1145-1179), used by

@@ -366,10 +366,24 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     __syncthreads();
   }
 
-  // epilogue: bf16(v) of the wave's whole 128 x 128 tile goes to its own LDS
-  // region (the stages are free after the last barrier) in one unrolled pass,
-  // then a loop that never touches the accumulators reads it back 32 x 32 at a
-  // time as 16-byte row chunks (normal store) or 8-row column chunks (mirror)
+  // Epilogue.  bf16(v) of the wave's whole 128 x 128 tile goes to its own LDS
+  // region (the stages are free after the last barrier); it is read back as
+  // 16-byte row chunks (normal store) or 8-row column chunks (mirror).  The
+  // a x / b A term of a pass is loaded whole (32 x 16 B per lane) before the
+  // pass starts, the normal pass's before the staging, so each pass waits for
+  // global memory once rather than once per 32 x 32 sub-tile.
+  const bool mirror = MODE != 2 && it.row0 != it.nrows;
+  const KAON_G uint16_t* eop = G((const uint16_t*)(MODE == 1 ? nb.a : xc));
+  const int lde = MODE == 1 ? mp : kp;
+  const int wr0 = row0 + wm * 128, wc0 = col0 + wn * 128;
+  ku4 ev[32];
+  if (MODE != 0) {
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
+      ev[u] = *(const KAON_G ku4*)(eop + (int64_t)(wr0 + i * 32 + (q >> 2)) * lde + wc0 + j * 32 + (q & 3) * 8);
+    }
+  }
   uint16_t* stg = lds + w * (128 * WLD);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -381,51 +395,50 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
             (uint16_t)f2bf(acc[i][j][r]);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
-  const bool mirror = MODE != 2 && it.row0 != it.nrows;
-  const KAON_G uint16_t* eop = G((const uint16_t*)(MODE == 1 ? nb.a : xc));
-  const int lde = MODE == 1 ? mp : kp;
-#pragma clang loop unroll(disable)
-  for (int sub = 0; sub < 16; ++sub) {
-    const int i = sub >> 2, j = sub & 3;
-    const int R0 = row0 + wm * 128 + i * 32, C0 = col0 + wn * 128 + j * 32;
-    const uint16_t* t = stg + (i * 32) * WLD + j * 32;
+  // u = (32 x 32 sub-tile i, j) x half h: rows rr = q / 4, 8 columns from c8
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int q = lane + 64 * h, rr = q >> 2, c8 = (q & 3) * 8;
-      const ku4 xv = *(const ku4*)&t[rr * WLD + c8];
-      ku4 ov = xv;
-      if (MODE != 0) {
-        const ku4 ev = *(const KAON_G ku4*)(eop + (int64_t)(R0 + rr) * lde + C0 + c8);
-        uint32_t o[8];
+  for (int u = 0; u < 32; ++u) {
+    const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), rr = q >> 2, c8 = (q & 3) * 8;
+    const ku4 xv = *(const ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8];
+    ku4 ov = xv;
+    if (MODE != 0) {
+      uint32_t o[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = __uint_as_float(half_of(xv, e) << 16), ef = __uint_as_float(half_of(ev, e) << 16);
-          o[e] = MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * x)) : f2bf(rbf(ca * ef) + x);
-        }
-        ov = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+      for (int e = 0; e < 8; ++e) {
+        const float x = __uint_as_float(half_of(xv, e) << 16), ef = __uint_as_float(half_of(ev[u], e) << 16);
+        o[e] = MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * x)) : f2bf(rbf(ca * ef) + x);
       }
-      *(KAON_G ku4*)G(out + (int64_t)(R0 + rr) * ldc + C0 + c8) = ov;
-      if (mirror) {
-        // out[C0 + cr][R0 + r8 .. + 8] = the same values read down column cr
-        const int cr = q >> 2, r8 = (q & 3) * 8;
-        uint32_t xs[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xs[e] = t[(r8 + e) * WLD + cr];
-        ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
-        if (MODE == 1) {
-          // B[c][r] = b A[r][c] + c (AA)[r][c]; A is symmetric, so A[r][c] = A[c][r]
-          const ku4 ev = *(const KAON_G ku4*)(eop + (int64_t)(C0 + cr) * lde + R0 + r8);
-          uint32_t o[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = __uint_as_float(xs[e] << 16), ef = __uint_as_float(half_of(ev, e) << 16);
-            o[e] = f2bf(rbf(cb * ef) + rbf(cc * x));
-          }
-          mv = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
-        }
-        *(KAON_G ku4*)G(out + (int64_t)(C0 + cr) * ldc + R0 + r8) = mv;
-      }
+      ov = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
     }
+    *(KAON_G ku4*)G(out + (int64_t)(wr0 + i * 32 + rr) * ldc + wc0 + j * 32 + c8) = ov;
+  }
+  if (!mirror) return;
+  // out[c][r] for this tile's (r, c): 8-row column chunks; for B, the b A term
+  // is read at the transposed position (A is symmetric, A[r][c] = A[c][r])
+  if (MODE == 1) {
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
+      ev[u] = *(const KAON_G ku4*)(eop + (int64_t)(wc0 + j * 32 + (q >> 2)) * lde + wr0 + i * 32 + (q & 3) * 8);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 32; ++u) {
+    const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), cr = q >> 2, r8 = (q & 3) * 8;
+    uint32_t xs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xs[e] = stg[(i * 32 + r8 + e) * WLD + j * 32 + cr];
+    ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
+    if (MODE == 1) {
+      uint32_t o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = __uint_as_float(xs[e] << 16), ef = __uint_as_float(half_of(ev[u], e) << 16);
+        o[e] = f2bf(rbf(cb * ef) + rbf(cc * x));
+      }
+      mv = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+    }
+    *(KAON_G ku4*)G(out + (int64_t)(wc0 + j * 32 + cr) * ldc + wr0 + i * 32 + r8) = mv;
   }
 }
 

@@ -88,7 +88,7 @@ int row_class(const KaonTensor& t, int32_t g_dtype) {
 // grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
 // momentum blocks of 8*G elements (G | 64) that tile the rows.
 bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
-  if (a.opt == KAON_OPT_ADAMUON) return false;
+  if (a.opt == KAON_OPT_ADAMUON || a.opt == KAON_OPT_ADAPNM) return false;
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
   if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
   if (a.codec == KAON_MOM_F32) return false;
@@ -117,7 +117,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
   if (!args) return plan_fail("kaon_plan: args is NULL");
   const int32_t opt = args->opt, codec = args->codec, g_dtype = args->g_dtype;
   if (n < 0 || (n > 0 && !descs)) return plan_fail("kaon_plan: bad descriptor array");
-  if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON)
+  if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM)
     return plan_fail("kaon_plan: unknown optimizer");
   if (codec < KAON_MOM_NONE || codec > KAON_MOM_4BIT) return plan_fail("kaon_plan: unknown codec");
   if (g_dtype != KAON_F32 && g_dtype != KAON_BF16) return plan_fail("kaon_plan: unknown grad dtype");
@@ -155,8 +155,11 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     const int64_t slice_rows = 4 * rw;
     const int64_t run_rows = KAON_RUN * slice_rows;
     t.ngroups = (int32_t)((t.R + run_rows - 1) / run_rows);
+    if (opt == KAON_OPT_ADAPNM && (!t.m || !t.m2))
+      return plan_fail("kaon_plan: AdaPNM tensor " + std::to_string(i) + " needs both momentum buffers (m, m2)");
     const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
-                    aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16);
+                    aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16) && aligned(t.m2, 16) &&
+                    aligned(t.max_v, 16);
     t.vec_flat = al ? 1 : 0;
     t.vec_rows = (al && (t.C % 8 == 0 || t.R == 1)) ? 1 : 0;
     // workspace: 4-word aligned arrays

@@ -180,19 +180,35 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
 
   if (!T.factored) {
-    // v = lerp(v, g*g (+eps1), 1-beta2) over the single row (adakaon.py:990-995)
+    // v = lerp(v, g*g (+eps1), 1-beta2) over the single row (adakaon.py:990-995);
+    // AdaPNM: v = v*beta2 + (1-beta2)*g*g, mul_ then addcmul_ (one fma in torch),
+    // and the running max under ams_bound (adapnm.py:1243-1248)
     if (mode != 0) return;
+    const bool pnm = (hp.flags & KAON_F_PNM) != 0;
+    const bool ams = pnm && (hp.flags & KAON_F_AMS) != 0 && T.max_v;
     for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
       const int cnt = chunk_cnt(c, C);
       const bool vv = vec && cnt == 8;
       float x[8], v[8];
       ld8<GT>(gsrc, c * 8, cnt, vv, x);
       ld8<KAON_F32>(T.v, c * 8, cnt, vv, v);
+      if (pnm) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float q = x[i] * x[i];
-        if (eps) q = q + hp.eps1;
-        v[i] = klerp(v[i], q, hp.w2);
+        for (int i = 0; i < 8; ++i) v[i] = __fmaf_rn(hp.a2 * x[i], x[i], v[i] * hp.b2);
+        if (ams) {
+          float mx[8];
+          ld8<KAON_F32>(T.max_v, c * 8, cnt, vv, mx);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], v[i]);
+          st8_f32(T.max_v, c * 8, cnt, vv, mx);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float q = x[i] * x[i];
+          if (eps) q = q + hp.eps1;
+          v[i] = klerp(v[i], q, hp.w2);
+        }
       }
       st8_f32(T.v, c * 8, cnt, vv, v);
     }
@@ -485,7 +501,8 @@ __global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restric
       if (c * 8 + i < R) a = a + v[i];
   }
   const float ss = wave_csum(a);
-  if (lane == 0) ws.scal(T)[0] = fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f);
+  // clip_threshold 0 (AdaPNM) leaves the update unclipped (adapnm.py:157-161)
+  if (lane == 0) ws.scal(T)[0] = hp.clip > 0.0f ? fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f) : 1.0f;
 }
 
 // =============================================================== prefetching row kernels
@@ -836,9 +853,9 @@ __global__ __launch_bounds__(KAON_WG) void k_pf_ss(const KaonTensor* __restrict_
 // =============================================================== phases 5/6
 // Momentum chunk load (raw codes / bits) and store.
 template <int CODEC>
-__device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, uint32_t q[8]) {
+__device__ __forceinline__ void ld_mom_at(const void* mbuf, int64_t e0, int cnt, bool vec, uint32_t q[8]) {
   if (CODEC == KAON_MOM_INT8) {
-    const int8_t* m = (const int8_t*)T.m + e0;
+    const int8_t* m = (const int8_t*)mbuf + e0;
     if (vec) {
       const ku2 v = *(const KAON_G ku2*)G(m);
 #pragma unroll
@@ -856,26 +873,32 @@ __device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int 
     for (int i = 0; i < 8; ++i) {
       if (i < cnt) {
         const int64_t e = e0 + i;
-        q[i] = ((uint32_t)((const uint8_t*)T.m)[e >> 1] >> (4 * (e & 1))) & 0xFu;
+        q[i] = ((uint32_t)((const uint8_t*)mbuf)[e >> 1] >> (4 * (e & 1))) & 0xFu;
       } else {
         q[i] = 8u;
       }
     }
     (void)vec;
   } else if (CODEC == KAON_MOM_BF16) {
-    ld8_bits(T.m, e0, cnt, vec, q);
+    ld8_bits(mbuf, e0, cnt, vec, q);
   } else if (CODEC == KAON_MOM_F32) {
     float f[8];
-    ld8<KAON_F32>(T.m, e0, cnt, vec, f);
+    ld8<KAON_F32>(mbuf, e0, cnt, vec, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) q[i] = __float_as_uint(f[i]);
   }
 }
 
 template <int CODEC>
-__device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, const uint32_t q[8]) {
+__device__ __forceinline__ void ld_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, uint32_t q[8]) {
+  ld_mom_at<CODEC>(T.m, e0, cnt, vec, q);
+}
+
+// n = the tensor's element count (the last byte of an odd-length 4-bit buffer)
+template <int CODEC>
+__device__ __forceinline__ void st_mom_at(void* mbuf, int64_t n, int64_t e0, int cnt, bool vec, const uint32_t q[8]) {
   if (CODEC == KAON_MOM_INT8) {
-    int8_t* m = (int8_t*)T.m + e0;
+    int8_t* m = (int8_t*)mbuf + e0;
     if (vec) {
       ku2 v;
       v.x = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
@@ -887,7 +910,7 @@ __device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int 
         if (i < cnt) m[i] = (int8_t)q[i];
     }
   } else if (CODEC == KAON_MOM_4BIT) {
-    uint8_t* m = (uint8_t*)T.m;
+    uint8_t* m = (uint8_t*)mbuf;
     if (vec && (e0 & 7) == 0) {
       uint32_t v = 0;
 #pragma unroll
@@ -905,19 +928,24 @@ __device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int 
         uint32_t* word = (uint32_t*)(m + ((e >> 1) & ~(int64_t)3));
         const int bsh = 8 * (int)((e >> 1) & 3) + sh;
         // the last element of an odd-length tensor owns its whole byte
-        const uint32_t clear = (e + 1 == T.n && (e & 1) == 0) ? 0xFFu : 0xFu;
+        const uint32_t clear = (e + 1 == n && (e & 1) == 0) ? 0xFFu : 0xFu;
         atomicAnd(word, ~(clear << bsh));
         atomicOr(word, (q[i] & 0xFu) << bsh);
       }
     }
   } else if (CODEC == KAON_MOM_BF16) {
-    st8_bits(T.m, e0, cnt, vec, q);
+    st8_bits(mbuf, e0, cnt, vec, q);
   } else if (CODEC == KAON_MOM_F32) {
     float f[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(q[i]);
-    st8_f32(T.m, e0, cnt, vec, f);
+    st8_f32(mbuf, e0, cnt, vec, f);
   }
+}
+
+template <int CODEC>
+__device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, const uint32_t q[8]) {
+  st_mom_at<CODEC>(T.m, T.n, e0, cnt, vec, q);
 }
 
 // MSAM perturbation value: clamp(nan_to_num(x, 0, +b, -b), -b, b) (msam.py:222-230).
@@ -1403,6 +1431,254 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       } else if (wr.lane == 0) {
         T.m_scale[r] = rc.newsc;
       }
+    }
+  }
+
+  if (PHASE == 5 && cautious) {
+    const uint32_t wsum = wave_sum_u32(keep);
+    if (wr.lane == 0) keep_s[wr.w] = wsum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
+      if (tot) atomicAdd(ws.keep_ctr(T), tot);
+    }
+  }
+}
+
+// =============================================================== AdaPNM
+// Phases 3, 5 and 6 of AdaPNM (_step_one_param, adapnm.py:1209-1275), per
+// element with g the (centralized) gradient:
+//   m_pos' = fma(1 - b1^2, g, m_pos * b1^2)       this step's positive buffer
+//   pn     = fma(-b0, m_neg, m_pos' * (1 + b0)) * (1 / noise_norm)
+//   u      = pn * ((r * c) * bc2)                   factored
+//          = pn / ((sqrt(v + 1e-15) + eps) / bc2)   1-D (max_v under ams_bound)
+//   d      = (u / fac) * lr / (1 - b1^t)
+// Phase 3 (slices of row runs): the row sums of u^2 for the clip, and the
+// absmax of m_pos' per int8 row / 4-bit block with the old scales.  Phase 5:
+// the cautious keep count of d * g > 0.  Phase 6: requantize or store m_pos',
+// write p after the decoupled decay p * (1 - lr*wd).  The negative buffer is
+// only read.  Odd steps take m as the positive buffer, even steps m2.
+template <int PHASE, int PT, int GT, int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  __shared__ uint32_t keep_s[4];
+  KaonItem it;
+  if (PHASE == 3) {
+    const KaonItem run = items[blockIdx.x / KAON_RUN];
+    const int sl = (int)(blockIdx.x % KAON_RUN);
+    if (sl >= run_slices(run)) return;
+    it = slice_item(run, sl);
+  } else {
+    it = items[blockIdx.x];
+  }
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C, n = T.n;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec_t = T.vec_rows != 0;
+  const bool factored = T.factored != 0;
+  const bool gc = (hp.flags & KAON_F_GC) && factored;
+  const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
+  const bool wd = (hp.flags & KAON_F_WD) != 0;
+  const bool ams = (hp.flags & KAON_F_AMS) && !factored && T.max_v;
+  const bool lowp = PT == KAON_BF16;
+  constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
+  const bool swap = (hp.step & 1u) == 0u;
+  void* mpos = swap ? T.m2 : T.m;
+  const void* mneg = swap ? T.m : T.m2;
+  float* spos = swap ? T.m2_scale : T.m_scale;
+  const float* sneg = swap ? T.m_scale : T.m2_scale;
+  const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 1;
+  const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
+  const WaveRows wr = wave_rows(it);
+  const float fac = PHASE == 3 ? 1.0f : ws.scal(T)[0];
+  const double rfac = rcp64(fac);
+  double rden = 1.0;
+  if (PHASE == 6 && cautious) {
+    const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
+    rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
+  }
+  const float* fsrc = factored ? (const float*)ws.cf(T) : (ams ? T.max_v : T.v);
+  uint32_t keep = 0;
+
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    const float rf = factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    // int8 per-row scales (one for a 1-D tensor): the positive buffer's old one
+    // (phase 6: as phase 3 recorded it), its new one (phase 6), the negative one
+    const int64_t sr = factored ? r : 0;
+    float oldsc = 1.0f, newsc = 1.0f, negsc = 1.0f;
+    double rnew = 1.0;
+    if (CODEC == KAON_MOM_INT8) {
+      oldsc = uniform_f(PHASE == 6 ? ws.roldsc(T)[r] : G(spos)[sr]);
+      negsc = uniform_f(G(sneg)[sr]);
+      if (PHASE == 6) {
+        newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+        rnew = rcp64(newsc);
+      }
+    }
+    const bool dqf = fabsf(oldsc) < 0x1p120f && fabsf(negsc) < 0x1p120f;
+    const float m128o = -128.0f * oldsc, m128n = -128.0f * negsc;
+    float ss = 0.0f, row_amax = 0.0f;
+
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
+      const int64_t j0 = c * 8;
+      const int64_t e0 = r * C + j0;
+      const bool vec = vec_t && cnt == 8;
+      float g[8], f[8], p[8];
+      uint32_t mq[8], nq[8], pb[8];
+      ld8<GT>(T.g, e0, cnt, vec, g);
+      ld_mom_at<CODEC>(mpos, e0, cnt, vec, mq);
+      ld_mom_at<CODEC>(mneg, e0, cnt, vec, nq);
+      ld8<KAON_F32>(fsrc, j0, cnt, vec, f);
+      if (PHASE == 6) {
+        if (PT == KAON_BF16) {
+          ld8_bits(T.p, e0, cnt, vec, pb);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+        } else {
+          ld8<KAON_F32>(T.p, e0, cnt, vec, p);
+        }
+      }
+      uint32_t nz[8];
+      if (PHASE == 6 && lowp && hp.bf16_method == KAON_SR) {
+        if ((e0 & 7) == 0) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], cnt, nz);
+        else
+#pragma unroll
+          for (int i = 0; i < 8; ++i) nz[i] = i < cnt ? noise1(hp.seed, hp.step, T.tensor_id, 1u, e0 + i, T.noise[1]) : 0u;
+      }
+      if (gc) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          float a0 = g[i] - mu, a1 = g[i + 1] - mu;
+          if (GT == KAON_BF16) rbf2(a0, a1);
+          g[i] = a0;
+          g[i + 1] = a1;
+        }
+      }
+      uint32_t qout[8];
+      float dout[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qout[i] = mq[i];
+        dout[i] = 0.0f;
+        if (i >= cnt) continue;
+        const int64_t e = e0 + i;
+        // 4-bit block scales of the element
+        int64_t blk = 0;
+        float sc4o = 1.0f, sc4n = 1.0f, sc4g = 1.0f;
+        double r4 = 1.0;
+        if (CODEC == KAON_MOM_4BIT) {
+          blk = e / B;
+          sc4o = PHASE == 6 ? ws.boldsc(T, nb)[blk] : G(spos)[blk];
+          sc4g = G(sneg)[blk];
+          if (PHASE == 6) {
+            sc4n = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+            r4 = rcp64(sc4n);
+          }
+        }
+        float mold, mng;
+        if (CODEC == KAON_MOM_INT8) {
+          mold = dq_int8(mq[i], oldsc, m128o, dqf);
+          mng = dq_int8(nq[i], negsc, m128n, dqf);
+        } else if (CODEC == KAON_MOM_4BIT) {
+          mold = ((float)mq[i] - 8.0f) * sc4o;
+          mng = ((float)nq[i] - 8.0f) * sc4g;
+        } else if (CODEC == KAON_MOM_BF16) {
+          mold = bf2f(mq[i]);
+          mng = bf2f(nq[i]);
+        } else {
+          mold = __uint_as_float(mq[i]);
+          mng = __uint_as_float(nq[i]);
+        }
+        const float gv = g[i];
+        const float mfv = __fmaf_rn(hp.a1, gv, mold * hp.b1);
+        const float pn = __fmaf_rn(hp.pn_neg, mng, mfv * hp.pn_pos) * hp.pn_rnorm;
+        const float u = factored ? pn * ((rf * f[i]) * hp.bc2) : pn / ((sqrtf(f[i] + 1e-15f) + hp.eps1) / hp.bc2);
+        if (PHASE == 3) {
+          ss = ss + u * u;
+          if (QUANT) {
+            const float ax = fabsf(mfv);
+            if (CODEC == KAON_MOM_INT8) {
+              row_amax = fmaxf(row_amax, ax);
+            } else {
+              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
+              if (e == blk * B) ws.boldsc(T, nb)[blk] = sc4o;
+            }
+          }
+          continue;
+        }
+        const float d = (fac == 1.0f ? u : div_r64(u, rfac)) * hp.lr;
+        const bool kp = d * gv > 0.0f;
+        if (PHASE == 5) {
+          keep += kp ? 1u : 0u;
+          continue;
+        }
+        if (CODEC == KAON_MOM_INT8) {
+          float x = rintf(div_r64(mfv, rnew));
+          x = fminf(fmaxf(x, -127.0f), 127.0f);
+          qout[i] = (uint32_t)(uint8_t)(int8_t)x;
+        } else if (CODEC == KAON_MOM_4BIT) {
+          float x = rintf(div_r64(mfv, r4));
+          x = fminf(fmaxf(x, -7.0f), 7.0f);
+          qout[i] = (uint32_t)((int)x + 8);
+          if (e == blk * B) G(spos)[blk] = sc4n;
+        } else if (CODEC == KAON_MOM_BF16) {
+          qout[i] = f2bf(mfv);
+        } else {
+          qout[i] = __float_as_uint(mfv);
+        }
+        dout[i] = cautious ? div_r64(d * (kp ? 1.0f : 0.0f), rden) : d;
+        if (wd) p[i] = lowp ? rbf(p[i] * hp.wdl) : p[i] * hp.wdl;
+      }
+      if (PHASE != 6) continue;
+      // ---------------- phase 6 writes
+      st_mom_at<CODEC>(mpos, n, e0, cnt, vec, qout);
+      if (PT == KAON_F32) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = p[i] - dout[i];
+        st8_f32(T.p, e0, cnt, vec, o);
+      } else {
+        uint32_t o[8];
+        if (hp.bf16_method == KAON_KAHAN) {
+          uint32_t sh[8];
+          ld8_bits(T.shift, e0, cnt, vec, sh);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            const float p0 = p[i];
+            const float p1 = rbf(p0 + s);
+            o[i] = f2bf(p1);
+            sh[i] = f2bf(s + rbf(p0 - p1));
+          }
+          st8_bits(T.shift, e0, cnt, vec, sh);
+        } else if (hp.bf16_method == KAON_RN) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz[i]);
+        }
+        st8_bits(T.p, e0, cnt, vec, o);
+      }
+    }
+    // ---- end of row
+    if (PHASE == 3) {
+      const float s2 = wave_csum(ss);
+      if (CODEC == KAON_MOM_INT8) {
+        const float am = wave_max(row_amax);
+        if (wr.lane == 0) {
+          ws.ramax(T)[r] = __float_as_uint(am);
+          ws.roldsc(T)[r] = oldsc;
+        }
+      }
+      if (wr.lane == 0) ws.rs(T)[r] = s2;
+    } else if (PHASE == 6 && CODEC == KAON_MOM_INT8 && wr.lane == 0) {
+      G(spos)[sr] = newsc;
     }
   }
 
@@ -2201,6 +2477,26 @@ MuonMomFn muon_mom_gt(int codec) {
   return nullptr;
 }
 
+using PnmFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
+template <int PHASE, int PT, int GT>
+PnmFn pnm_by_codec(int codec) {
+  switch (codec) {
+    case KAON_MOM_F32: return k_pnm<PHASE, PT, GT, KAON_MOM_F32>;
+    case KAON_MOM_BF16: return k_pnm<PHASE, PT, GT, KAON_MOM_BF16>;
+    case KAON_MOM_INT8: return k_pnm<PHASE, PT, GT, KAON_MOM_INT8>;
+    case KAON_MOM_4BIT: return k_pnm<PHASE, PT, GT, KAON_MOM_4BIT>;
+  }
+  return nullptr;
+}
+template <int PHASE>
+PnmFn pnm_fn(int pt, int gt, int codec) {
+  if (pt == KAON_BF16 && gt == KAON_BF16) return pnm_by_codec<PHASE, KAON_BF16, KAON_BF16>(codec);
+  if (pt == KAON_BF16 && gt == KAON_F32) return pnm_by_codec<PHASE, KAON_BF16, KAON_F32>(codec);
+  if (pt == KAON_F32 && gt == KAON_BF16) return pnm_by_codec<PHASE, KAON_F32, KAON_BF16>(codec);
+  if (pt == KAON_F32 && gt == KAON_F32) return pnm_by_codec<PHASE, KAON_F32, KAON_F32>(codec);
+  return nullptr;
+}
+
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who) {
   if (!L || !hp) return fail(who);
   if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16) return fail("kaon: bad p_dtype");
@@ -2319,6 +2615,50 @@ int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
 
 int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   return kaon_adamuon_phases(L, hp, 0x37Eu, stream);
+}
+
+int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
+  int rc = validate(L, hp, "kaon_adapnm_phases: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
+  if (hp->codec == KAON_MOM_NONE) return fail("kaon_adapnm_step: AdaPNM keeps two momentum buffers; pass their codec");
+  hipStream_t st = (hipStream_t)stream;
+  Ws ws{(float*)L->workspace};
+  KaonHyper h = *hp;
+  h.flags |= KAON_F_PNM | KAON_F_MOMENTUM;
+  h.flags &= ~(KAON_F_NK_REMOVE | KAON_F_NK_CLIMB | KAON_F_SRC_O);
+  PnmFn f3 = pnm_fn<3>(h.p_dtype, h.g_dtype, h.codec);
+  PnmFn f5 = pnm_fn<5>(h.p_dtype, h.g_dtype, h.codec);
+  PnmFn f6 = pnm_fn<6>(h.p_dtype, h.g_dtype, h.codec);
+  if (!f3 || !f5 || !f6) return fail("kaon_adapnm_step: unsupported dtype / codec combination");
+  if (mask & (1u << 1)) {
+    if ((rc = launch_stats(*L, ws, h, 0, st))) return rc;
+  }
+  if ((mask & (1u << 2)) && L->n_fin_items > 0) {
+    hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
+    if ((rc = check_launch("kaon: k_fin launch"))) return rc;
+  }
+  if (mask & (1u << 3)) {
+    hipLaunchKernelGGL(f3, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
+    if ((rc = check_launch("kaon: AdaPNM clip-sum launch"))) return rc;
+  }
+  if (mask & (1u << 4)) {
+    hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, h);
+    if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
+  }
+  if ((mask & (1u << 5)) && (h.flags & KAON_F_CAUTIOUS) && L->n_elem_items > 0) {
+    hipLaunchKernelGGL(f5, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
+    if ((rc = check_launch("kaon: AdaPNM keep-count launch"))) return rc;
+  }
+  if ((mask & (1u << 6)) && L->n_elem_items > 0) {
+    hipLaunchKernelGGL(f6, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
+    if ((rc = check_launch("kaon: AdaPNM apply launch"))) return rc;
+  }
+  return 0;
+}
+
+int kaon_adapnm_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  return kaon_adapnm_phases(L, hp, 0x7Eu, stream);
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {

@@ -30,24 +30,26 @@ def fourbit_block_size(numel: int, block: int) -> int:
     return numel if block <= 0 else (min(block, numel) if numel > 0 else 1)
 
 
-def init_momentum_state(state: dict[str, Any], grad: torch.Tensor, group: dict[str, Any]) -> None:
-    """Allocate the momentum buffer exactly as the reference codecs do."""
+def init_momentum_state(state: dict[str, Any], grad: torch.Tensor, group: dict[str, Any], prefix: str = "m") -> None:
+    """Allocate a momentum buffer exactly as the reference codecs do, under the keys
+    ``prefix``, ``prefix_scale``, ``prefix_numel``, ``prefix_block`` (AdaPNM's two
+    buffers use "m_pos" and "m_neg", src/kaon/adapnm.py:451-479)."""
     md = group["momentum_dtype"]
     if md in ("bfloat16", "float32"):
-        state["m"] = torch.zeros_like(grad, dtype=torch.bfloat16 if md == "bfloat16" else torch.float32,
-                                      memory_format=torch.contiguous_format)
+        state[prefix] = torch.zeros_like(grad, dtype=torch.bfloat16 if md == "bfloat16" else torch.float32,
+                                         memory_format=torch.contiguous_format)
     elif md == "int8":
-        state["m"] = torch.zeros_like(grad, dtype=torch.int8, memory_format=torch.contiguous_format)
-        state["m_scale"] = torch.ones((grad.shape[0],) + (1,) * (grad.ndim - 1) if grad.ndim >= 2 else (),
-                                      dtype=torch.float32, device=grad.device)
+        state[prefix] = torch.zeros_like(grad, dtype=torch.int8, memory_format=torch.contiguous_format)
+        state[f"{prefix}_scale"] = torch.ones((grad.shape[0],) + (1,) * (grad.ndim - 1) if grad.ndim >= 2 else (),
+                                              dtype=torch.float32, device=grad.device)
     else:
         numel = grad.numel()
         bs = fourbit_block_size(numel, group["momentum_4bit_block"])
         nblocks = (numel + bs - 1) // bs
-        state["m"] = torch.full(((numel + 1) // 2,), 0x88, dtype=torch.uint8, device=grad.device)
-        state["m_scale"] = torch.ones(nblocks, dtype=torch.float32, device=grad.device)
-        state["m_numel"] = numel
-        state["m_block"] = bs
+        state[prefix] = torch.full(((numel + 1) // 2,), 0x88, dtype=torch.uint8, device=grad.device)
+        state[f"{prefix}_scale"] = torch.ones(nblocks, dtype=torch.float32, device=grad.device)
+        state[f"{prefix}_numel"] = numel
+        state[f"{prefix}_block"] = bs
 
 
 def load_state_dict_preserving_dtypes(optimizer: torch.optim.Optimizer, state_dict: dict[str, Any]) -> None:

@@ -52,6 +52,7 @@ class Plan:
             d.m, d.m_scale = _ptr(e.get("m")), _ptr(e.get("m_scale"))
             d.row, d.col, d.v = _ptr(e.get("row")), _ptr(e.get("col")), _ptr(e.get("v"))
             d.shift = _ptr(e.get("shift"))
+            d.m2, d.m2_scale, d.max_v = _ptr(e.get("m2")), _ptr(e.get("m2_scale")), _ptr(e.get("max_v"))
             noise = e.get("noise") or (None, None, None)
             for s in range(3):
                 d.noise[s] = _ptr(noise[s])

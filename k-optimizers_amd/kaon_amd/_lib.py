@@ -12,16 +12,17 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
 MOM_CODE = {"none": MOM_NONE, "float32": MOM_F32, "bfloat16": MOM_BF16, "int8": MOM_INT8, "4bit": MOM_4BIT}
 SR, RN, KAHAN = 0, 1, 2
 BF16_METHOD = {"stochastic_rounding": SR, "none": RN, "kahan": KAHAN}
-OPT_ADAKAON, OPT_LION, OPT_ADAMUON = 0, 1, 2
+OPT_ADAKAON, OPT_LION, OPT_ADAMUON, OPT_ADAPNM = 0, 1, 2, 3
 
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB, F_SRC_O = 1, 2, 4, 8, 16, 32, 64, 128
+F_PNM, F_AMS = 256, 512
 
 ROW_BUDGET = 20
 ROW_CLASSES = 7
@@ -36,6 +37,7 @@ class KaonTensor(ctypes.Structure):
         ("g", ctypes.c_void_p), ("p", ctypes.c_void_p), ("m", ctypes.c_void_p),
         ("m_scale", ctypes.c_void_p), ("row", ctypes.c_void_p), ("col", ctypes.c_void_p),
         ("v", ctypes.c_void_p), ("shift", ctypes.c_void_p),
+        ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
         ("noise", ctypes.c_void_p * 3),
         ("R", ctypes.c_int64), ("C", ctypes.c_int64), ("n", ctypes.c_int64),
         ("ws_row", ctypes.c_int64), ("ws_col", ctypes.c_int64), ("ws_part", ctypes.c_int64),
@@ -82,15 +84,17 @@ class KaonHyper(ctypes.Structure):
         ("wdl", ctypes.c_float), ("clip", ctypes.c_float), ("b1", ctypes.c_float), ("b2", ctypes.c_float),
         ("a1", ctypes.c_float), ("a2", ctypes.c_float), ("nk_k", ctypes.c_float),
         ("nk_bound_old", ctypes.c_float), ("nk_bound_new", ctypes.c_float),
+        ("pn_pos", ctypes.c_float), ("pn_neg", ctypes.c_float), ("pn_rnorm", ctypes.c_float),
+        ("bc2", ctypes.c_float),
         ("flags", ctypes.c_int32), ("p_dtype", ctypes.c_int32), ("g_dtype", ctypes.c_int32),
         ("codec", ctypes.c_int32), ("bf16_method", ctypes.c_int32), ("ns_steps", ctypes.c_int32),
         ("step", ctypes.c_uint32), ("seed", ctypes.c_uint64),
     ]
 
 
-assert ctypes.sizeof(KaonTensor) == 208, ctypes.sizeof(KaonTensor)
+assert ctypes.sizeof(KaonTensor) == 232, ctypes.sizeof(KaonTensor)
 assert ctypes.sizeof(KaonItem) == 16
-assert ctypes.sizeof(KaonHyper) == 88, ctypes.sizeof(KaonHyper)
+assert ctypes.sizeof(KaonHyper) == 104, ctypes.sizeof(KaonHyper)
 
 # entry points: name -> (argtypes, restype)
 _VP, _I32, _I64, _U32, _U64, _F = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32,
@@ -103,9 +107,11 @@ SIGNATURES = {
     "kaon_adakaon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adamuon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
+    "kaon_adapnm_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adakaon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_lion_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_adamuon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
+    "kaon_adapnm_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_msam_apply": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _F, _F, _U32, _VP], ctypes.c_int),
     "kaon_quant_int8": ([_VP, _I64, _I64, _VP, _VP, _VP], ctypes.c_int),
     "kaon_quant_4bit": ([_VP, _I64, _I32, _VP, _VP, _VP], ctypes.c_int),

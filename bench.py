@@ -50,6 +50,15 @@ WORKLOADS = {
                               "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
                               "params on the Adakaon path", opt="adamuon",
                          kw=dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype="int8", ns_steps=2), bm=1.0),
+    # AdaPNM (src/kaon/adapnm.py, SURVEY's next row 3): two momenta, the positive one read and
+    # written, the negative one read (b_neg), on the same SDXL set
+    "adapnm_int8": dict(desc="AdaPNM betas=(0.8,0.999) beta0=0.5, two int8 momenta, factored 2nd moment, cautious, "
+                             "GC, SR bf16, lr 1e-4", opt="adapnm",
+                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="int8"), bm=1.0, b_neg=1.0),
+    "adapnm_bf16": dict(desc="AdaPNM defaults: betas=(0.8,0.999) beta0=0.5, two bf16 momenta, factored 2nd moment, "
+                             "cautious, GC, SR bf16, lr 1e-4", opt="adapnm",
+                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="bfloat16"), bm=2.0,
+                        b_neg=2.0),
     # the launch-bound regime: the reference's LoRA proxy bag (benchmarks/proxy/harness.py:117-127:
     # 512 tensors [8, 16], fp32) stepped by Adakaon with bf16 momentum, the configuration its
     # control ranking lists as "Adakaon-bf16-fused" (benchmarks/control/RANKINGS.md:83)
@@ -65,7 +74,10 @@ PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor",
                8: "momentum", 9: "newton_schulz"}
 
 
-def phase_bytes(phase: int, bm: float, wd: bool) -> float:
+def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon") -> float:
+    if opt == "adapnm":
+        # both momenta are read by the clip-sum, keep-count and apply passes
+        return {1: 2.0, 3: 2.0 + 2.0 * bm, 5: 2.0 + 2.0 * bm, 6: 6.0 + 3.0 * bm}.get(phase, 0.0)
     if phase in (1, 3):
         return 2.0
     if phase == 5:
@@ -93,9 +105,11 @@ def measured_traffic(workload: str, phase: int) -> float | None:
 
 
 def make_opt(name, params):
-    from kaon_amd import AdaMuon, Adakaon, Lion, Nekaon
+    from kaon_amd import AdaMuon, AdaPNM, Adakaon, Lion, Nekaon
 
     w = WORKLOADS[name]
+    if w["opt"] == "adapnm":
+        return AdaPNM(params, **w["kw"])
     if w["opt"] == "adakaon":
         return Adakaon(params, **w["kw"])
     if w["opt"] == "lion":
@@ -162,6 +176,9 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
         elif WORKLOADS[name]["opt"] == "lion":
             hp = inner._hyper(group, pdt, gdt)
             fn, phases = lib.kaon_lion_phases, (1, 5, 6)
+        elif WORKLOADS[name]["opt"] == "adapnm":
+            hp = inner._hyper(group, pdt, gdt)
+            fn, phases = lib.kaon_adapnm_phases, (1, 2, 3, 4, 5, 6)
         else:
             nk = None
             if WORKLOADS[name]["opt"] == "nekaon":
@@ -197,6 +214,8 @@ def cpu_baseline(params, name, seconds: float) -> dict:
                  momentum_4bit_block=kw.get("momentum_4bit_block", 128), cautious=True,
                  gradient_centralization=w["opt"] != "adamuon", bf16_method="stochastic_rounding", k=1.5,
                  ns_steps=kw.get("ns_steps", 2))
+    if w["opt"] == "adapnm":
+        group.update(eps=1e-8, beta0=kw["beta0"], ams_bound=False)
     order = np.random.default_rng(0).permutation(len(params))
     if w["opt"] == "adamuon":
         # the oracle's scalar GEMMs take minutes on a 1280 x 11520 matrix: sample the
@@ -272,7 +291,7 @@ def main() -> int:
     gps = nparam / (ms * 1e-3) / 1e9
     bm = w["bm"]
     eb = 4.0 if pdt == torch.float32 else 2.0   # param and grad element bytes
-    b_alg = eb + 2.0 * eb + 2.0 * bm
+    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0)
     step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
     print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
           file=sys.stderr, flush=True)
@@ -298,7 +317,8 @@ def main() -> int:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": w["desc"], "shape_set": "SDXL-UNet-shaped (1678 tensors)", "n_params": nparam,
                    "params": "bf16", "grads": "bf16",
-                   "momentum": WORKLOADS[args.workload]["kw"]["momentum_dtype"], "parallelism": "none (1 GPU)"},
+                   "momentum": w["kw"]["momentum_dtype"] + (" x2 (m_pos, m_neg)" if w["opt"] == "adapnm" else ""),
+                   "parallelism": "none (1 GPU)"},
         "step_roofline": {"bound": "hbm", "bytes_per_param": b_alg, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                           "copy_ceiling": round(ceiling, 1), "frac_of_copy": round(step_gbs / ceiling, 4)},
@@ -316,7 +336,7 @@ def main() -> int:
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
                                "avg_ms": round(br[dom], 4)}
         else:
-            bpp = phase_bytes(dom, bm, wd)
+            bpp = phase_bytes(dom, bm, wd, w["opt"])
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
             out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),

@@ -3,10 +3,10 @@
 The golden fixtures hold the reference's own state after its steps
 (tests/golden/make_golden.py ran kaon 0.7.4): per param the keys, dtypes and
 shapes of ``optimizer.state`` (adakaon.py:318-335, lion.py:210-241,
-_momentum_codec.py:253-406).  These tests check that
+adapnm.py:451-500, _momentum_codec.py:253-406).  These tests check that
 
 * kaon_amd's fresh state has the reference's keys and dtypes, and its shapes
-  except where the reference's own two paths differ (the 1-D int8 ``m_scale``:
+  except where the reference's own two paths differ (the 1-D int8 scales:
   ``()`` at init and on the foreach path, ``(1,)`` after the per-param requant,
   tests/test_fused_triton.py:906-908 of the reference);
 * a reference-layout checkpoint loads with every tensor byte-identical, both
@@ -26,7 +26,7 @@ from cases import CASES, grad_values, param_values
 from golden_compare import load_golden
 from gpu_cases import make_opt
 
-INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion")]
+INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion", "adapnm")]
 
 
 def _tdt(name):
@@ -54,7 +54,7 @@ def _golden_state(gold, i):
         if not k.startswith(pre):
             continue
         key = k[len(pre):]
-        if key in ("m_numel", "m_block"):
+        if key.endswith("_numel") or key.endswith("_block"):  # the 4-bit codec's ints
             out[key] = int(a)
         elif a.dtype == np.uint16:  # bf16 bits
             out[key] = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
@@ -89,7 +89,7 @@ def test_fresh_state_has_the_reference_layout(name):
                 assert int(st[k]) == v, (name, i, k)
                 continue
             assert st[k].dtype == v.dtype, (name, i, k, st[k].dtype, v.dtype)
-            if k == "m_scale" and p.ndim == 1 and v.dtype == torch.float32 and case["kwargs"].get(
+            if k.endswith("_scale") and p.ndim == 1 and v.dtype == torch.float32 and case["kwargs"].get(
                     "momentum_dtype") == "int8":
                 assert tuple(st[k].shape) == () and tuple(v.shape) in ((), (1,)), (name, i, v.shape)
             else:

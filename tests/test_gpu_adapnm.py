@@ -19,9 +19,10 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-from golden_compare import CASES  # noqa: E402
-from gpu_cases import assert_same_as_oracle, make_opt, oracle_case_run, run_gpu, tdtype, DEV  # noqa: E402
+import oracle as O  # noqa: E402
 from cases import grad_values  # noqa: E402
+from golden_compare import CASES, group_for, load_golden  # noqa: E402
+from gpu_cases import DEV, assert_same_as_oracle, make_opt, oracle_case_run, run_gpu, tdtype  # noqa: E402
 
 GOLDEN = [k for k, c in CASES.items() if c["opt"] == "adapnm"]
 
@@ -116,3 +117,63 @@ def test_save_load_resume_matches_uninterrupted():
                 assert torch.equal(sa[k].reshape(-1).view(torch.uint8), sb[k].reshape(-1).view(torch.uint8)), (i, k)
             else:
                 assert sa[k] == sb[k], (i, k)
+
+
+def _golden_state(gold, i):
+    pre = f"s{i}_"
+    return {k[len(pre):]: a for k, a in gold.items() if k.startswith(pre)}
+
+
+@pytest.mark.parametrize("name", GOLDEN)
+def test_resume_from_reference_checkpoint(name):
+    """The reference's own state after its steps (the golden fixture), loaded in
+    the reference's layout with the group's step count, then one more step on
+    the GPU and in the oracle from the same params and state: identical.  The
+    step count decides which buffer is positive and the bias corrections."""
+    case = CASES[name]
+    print(f"[gpu] adapnm resume from reference checkpoint {name}", flush=True)
+    gold = load_golden(name)
+    pdt, gdt = tdtype(case["p_dtype"]), tdtype(case["g_dtype"])
+    steps, nxt = case["steps"], case["steps"] + 1
+
+    def tensor_of(a, dt):
+        if dt == torch.bfloat16:
+            return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        return torch.from_numpy(a.astype(np.float32) if a.dtype == np.float32 else a.copy())
+
+    params = [torch.nn.Parameter(tensor_of(gold[f"p{i}"], pdt).to(DEV)) for i in range(len(case["shapes"]))]
+    opt = make_opt(case, params)
+    sd = opt.state_dict()
+    sd.pop("kaon_amd", None)
+    sd["param_groups"][0]["step"] = steps
+    st = {}
+    for i in range(len(params)):
+        st[i] = {}
+        for k, a in _golden_state(gold, i).items():
+            if k.endswith("_numel") or k.endswith("_block"):
+                st[i][k] = int(a)
+            else:
+                st[i][k] = tensor_of(a, torch.bfloat16 if a.dtype == np.uint16 else None)
+    sd["state"] = st
+    opt.load_state_dict(sd)
+    for i, p in enumerate(params):
+        p.grad = torch.from_numpy(grad_values(case, i, nxt)).to(DEV, gdt)
+    opt.step()
+    torch.cuda.synchronize()
+    dt = O.BF16 if case["p_dtype"] == "bf16" else O.F32
+    gt = O.BF16 if case["g_dtype"] == "bf16" else O.F32
+    oparams = [O.make_param(shape, dt, gt, tensor_id=i, p_values=O.values(gold[f"p{i}"], dt))
+               for i, shape in enumerate(case["shapes"])]
+    oopt = O.OracleOptimizer(oparams, "adapnm", group_for(case), seed=case["seed"])
+    oopt.t = steps
+    for i, prm in enumerate(oparams):
+        for k, a in _golden_state(gold, i).items():
+            if k.endswith("_numel") or k.endswith("_block"):
+                prm.state[k] = int(a)
+            else:
+                prm.state[k] = np.ascontiguousarray(a).reshape(np.shape(prm.state[k])).copy()
+        g = grad_values(case, i, nxt)
+        prm.g = O.f32_to_bf16(g).reshape(prm.shape) if gt == O.BF16 else g.copy()
+    oopt.step()
+    assert opt.param_groups[0]["step"] == nxt
+    assert_same_as_oracle(case, oparams, params, opt, label=f"resume {name}")

@@ -19,6 +19,7 @@
  *   - AdaMuon       src/kaon/adamuon.py:97-149, 557-615 (== batched :434-555)
  *   - MSAM/Nekaon   src/kaon/msam.py:169-235, 375-406 ; src/kaon/nekaon.py:162-171
  *   - AdaPNM        src/kaon/adapnm.py:998-1016, 1209-1275 (== batched :1069-1200)
+ *   - KProdigy      src/kaon/kprodigy.py:337-441 (pass 1), 768-808 (pass 2), 723-741 (momentum)
  *
  * Rounding model (measured against torch 2.10 CPU in this image, see
  * tests/test_oracle_torch_semantics.py):
@@ -46,6 +47,9 @@
  *     run order (every partial starts from +0.0f).
  *   Sum of squares for the RMS clip: CSUM over each row (C elements), then
  *     CSUM over the R row results.
+ *   FSUM(x[0..n)) (KProdigy's per-tensor D statistics over the sliced
+ *     elements): blocks of 16384 consecutive elements, each summed in CSUM
+ *     order, then CSUM over the block sums.
  */
 #include <math.h>
 #include <stdint.h>
@@ -166,6 +170,20 @@ float ko_csum(const float* x, int64_t n) {
 }
 
 /* Rows per wave group of the column-sum order (see the header). */
+#define KAON_FLAT 16384
+float ko_fsum(const float* x, int64_t n) {
+    if (n <= 0) return 0.0f;
+    int64_t nb = (n + KAON_FLAT - 1) / KAON_FLAT;
+    float* bs = (float*)malloc(sizeof(float) * (size_t)nb);
+    for (int64_t b = 0; b < nb; ++b) {
+        int64_t len = n - b * KAON_FLAT < KAON_FLAT ? n - b * KAON_FLAT : KAON_FLAT;
+        bs[b] = ko_csum(x + b * KAON_FLAT, len);
+    }
+    float r = ko_csum(bs, nb);
+    free(bs);
+    return r;
+}
+
 int64_t ko_rows_per_wave(int64_t C) {
     int64_t nch = (C + KAON_CHUNK - 1) / KAON_CHUNK;
     int64_t cpl = (nch + KAON_LANES - 1) / KAON_LANES;
@@ -196,6 +214,12 @@ typedef struct {
                             positive one, which takes the gradient this step */
     float* m2_scale;
     float* max_v;        /* AdaPNM ams_bound: running max of v (1-D) */
+    /* KProdigy */
+    float* pd_s;         /* "s" [ceil(n / slice)] */
+    const float* pd_p0;  /* "p0" [ceil(n / slice)], or one 0.0 when pd_np0 == 1 */
+    int64_t pd_np0;
+    int32_t pd_slice;    /* slice_p */
+    int32_t full_v;      /* per-element second moment v although the tensor is a matrix */
 } KoTensor;
 
 typedef struct {
@@ -210,6 +234,11 @@ typedef struct {
     /* AdaPNM */
     double beta0;
     int32_t ams_bound;
+    /* KProdigy: d and dlr of this step (the values before its D update), the s
+     * EMA weight alpha_s, beta3, the denominator floor eps; wd decoupled or
+     * folded into the gradient; whether this step updates the D statistics */
+    double pd_d, pd_dlr, pd_alpha_s, pd_beta3, pd_eps;
+    int32_t pd_decouple, pd_stats;
 } KoHyper;
 
 static inline float load_g(const KoTensor* t, int64_t i) {
@@ -419,9 +448,16 @@ int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bou
 }
 
 /* ------------------------------------------------ factored second moment */
+/* factored_inv_sqrt_factors (src/kaon/_factored.py:62-83): r = rsqrt(row /
+ * mean(row)) into rf [R], c = rsqrt(col) into cf [C]. */
+static void factored_factors(const KoTensor* t, float* rf, float* cf) {
+    for (int64_t j = 0; j < t->C; ++j) cf[j] = ko_rsqrt(t->col[j]);
+    float rm = ko_csum(t->row, t->R) / (float)t->R;
+    for (int64_t r = 0; r < t->R; ++r) rf[r] = ko_rsqrt(t->row[r] / rm);
+}
+
 /* update_factored_state + factored_inv_sqrt_factors (src/kaon/_factored.py)
- * on x [R, C]: the row/col EMAs, then r = rsqrt(row / mean(row)) into rf [R]
- * and c = rsqrt(col) into cf [C]. */
+ * on x [R, C]: the row/col EMAs, then the factors into rf / cf when given. */
 static void factored_state(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* rf,
                            float* cf) {
     int64_t R = t->R, C = t->C;
@@ -452,13 +488,9 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
             }
         }
     }
-    for (int64_t j = 0; j < C; ++j) {
-        t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
-        cf[j] = ko_rsqrt(t->col[j]);
-    }
-    float rm = ko_csum(t->row, R) / (float)R;
-    for (int64_t r = 0; r < R; ++r) rf[r] = ko_rsqrt(t->row[r] / rm);
+    for (int64_t j = 0; j < C; ++j) t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
     free(q); free(pw); free(ps); free(pr); free(colsum);
+    if (rf && cf) factored_factors(t, rf, cf);
 }
 
 /* The factored step's U = (x * r) * c. */
@@ -638,6 +670,123 @@ int ko_adapnm_tensor(const KoTensor* t, const KoHyper* h) {
     if (h->cautious) cautious(u, g, n);
     write_sub(t, u, h, 1);
     free(g); free(u); free(mp); free(mn); free(rf); free(cf);
+    return 0;
+}
+
+/* ------------------------------------------------------------ KProdigy */
+/* The gradient pass 1 sees (_collect_grad, kprodigy.py:342-349): GC'd, plus
+ * wd * p when the decay is not decoupled (add(p, alpha=wd): one fma). */
+static float* pd_grad(const KoTensor* t, const KoHyper* h) {
+    float* g = centralized_grad(t, h->gc);
+    if (h->wd != 0 && !h->pd_decouple) {
+        const float a = (float)h->wd;
+        for (int64_t i = 0; i < t->R * t->C; ++i) g[i] = fmaf(a, load_p(t, i), g[i]);
+    }
+    return g;
+}
+
+/* Pass 1 of one tensor (_pass1_per_param body, kprodigy.py:392-441): the D
+ * statistics over every pd_slice-th element (num = FSUM(g * (p0 - p)), the s
+ * EMA s*beta3 + alpha_s*g, den = FSUM(|s|)), the first moment of d*g in its
+ * codec (_update_momentum :723-741), the second moment (full: v*beta2 +
+ * d^2(1-beta2) g g; factored: the row/col EMAs of g^2 + eps_factored). */
+int ko_kprodigy_pass1_tensor(const KoTensor* t, const KoHyper* h, float* num_out, float* den_out) {
+    int64_t n = t->R * t->C;
+    if (num_out) *num_out = 0.0f;
+    if (den_out) *den_out = 0.0f;
+    if (n <= 0) return 0;
+    float* g = pd_grad(t, h);
+    if (h->pd_stats) {
+        const int64_t sp = t->pd_slice > 0 ? t->pd_slice : 1, ns = (n + sp - 1) / sp;
+        float* prod = (float*)malloc(sizeof(float) * (size_t)ns);
+        float* sa = (float*)malloc(sizeof(float) * (size_t)ns);
+        const float as = (float)h->pd_alpha_s, b3 = (float)h->pd_beta3;
+        for (int64_t j = 0; j < ns; ++j) {
+            const int64_t e = j * sp;
+            const float p0 = t->pd_np0 == 1 ? t->pd_p0[0] : t->pd_p0[j];
+            prod[j] = g[e] * (p0 - load_p(t, e));
+            t->pd_s[j] = fmaf(as, g[e], t->pd_s[j] * b3);
+            sa[j] = fabsf(t->pd_s[j]);
+        }
+        if (num_out) *num_out = ko_fsum(prod, ns);
+        if (den_out) *den_out = ko_fsum(sa, ns);
+        free(prod); free(sa);
+    }
+    if (h->beta1 > 0 && t->codec != KO_MOM_NONE) {
+        const float b1 = (float)h->beta1, tg = (float)(h->pd_d * (1.0 - h->beta1));
+        if (t->codec == KO_MOM_F32) {
+            float* m = (float*)t->m;
+            for (int64_t i = 0; i < n; ++i) m[i] = fmaf(tg, g[i], m[i] * b1);
+        } else if (t->codec == KO_MOM_BF16) {
+            /* bf16 storage: mul_ rounds to bf16; add_(g.to(bf16), alpha) of torch's
+             * vectorized bf16 kernel rounds alpha to bf16 as well (torch CPU's scalar
+             * tail of n % 32 elements keeps it fp32; torch CUDA keeps it fp32 throughout) */
+            uint16_t* m = (uint16_t*)t->m;
+            const float tgb = round_bf16(tg);
+            for (int64_t i = 0; i < n; ++i) {
+                const float mb = round_bf16(bf16_to_f(m[i]) * b1);
+                m[i] = f_to_bf16(fmaf(tgb, round_bf16(g[i]), mb));
+            }
+        } else {
+            float* mf = (float*)malloc(sizeof(float) * (size_t)n);
+            mom_dequant(t, mf);
+            if (t->codec == KO_MOM_INT8) {
+                for (int64_t i = 0; i < n; ++i) mf[i] = fmaf(tg, g[i], mf[i] * b1);
+            } else { /* 4-bit: lerp toward d * g (ema_one, _momentum_codec.py:363-371) */
+                const float w = (float)(1.0 - h->beta1), df = (float)h->pd_d;
+                for (int64_t i = 0; i < n; ++i) mf[i] = ko_lerp(mf[i], h->pd_d == 1.0 ? g[i] : g[i] * df, w);
+            }
+            mom_store_quant(t, mf);
+            free(mf);
+        }
+    }
+    if (t->full_v || !t->factored) {
+        const float val = (float)(h->pd_d * h->pd_d * (1.0 - h->beta2)), b2 = (float)h->beta2;
+        for (int64_t i = 0; i < n; ++i) t->v[i] = fmaf(val * g[i], g[i], t->v[i] * b2);
+    } else {
+        factored_state(t, g, (float)(1.0 - h->beta2), (float)h->eps1, h->eps1 > 0, NULL, NULL);
+    }
+    free(g);
+    return 0;
+}
+
+/* Pass 2 of one tensor (_update_one_param, kprodigy.py:768-808): numerator =
+ * the stored momentum (or the gradient at beta1 = 0), over max(sqrt(v), d*eps)
+ * or times min(r c / d, 1/(d eps)); times dlr; decoupled WD; cautious; write.
+ * h->pd_d is the d after this step's D update, h->pd_dlr the dlr of the d
+ * before it (kprodigy.py:366-386). */
+int ko_kprodigy_pass2_tensor(const KoTensor* t, const KoHyper* h) {
+    int64_t n = t->R * t->C;
+    if (n <= 0) return 0;
+    float* g = centralized_grad(t, h->gc);
+    float* d = (float*)malloc(sizeof(float) * (size_t)n);
+    if (h->beta1 > 0 && t->codec != KO_MOM_NONE) mom_dequant(t, d);
+    else memcpy(d, g, sizeof(float) * (size_t)n);
+    const float df = (float)h->pd_d;
+    if (t->full_v || !t->factored) {
+        const float floor = (float)(h->pd_d * h->pd_eps);
+        for (int64_t i = 0; i < n; ++i) d[i] = d[i] / fmaxf(sqrtf(t->v[i]), floor);
+    } else {
+        float* rf = (float*)malloc(sizeof(float) * (size_t)t->R);
+        float* cf = (float*)malloc(sizeof(float) * (size_t)t->C);
+        factored_factors(t, rf, cf);
+        const float cap = (float)(1.0 / (h->pd_d * h->pd_eps));
+        for (int64_t r = 0; r < t->R; ++r)
+            for (int64_t j = 0; j < t->C; ++j) {
+                const float inv = fminf((rf[r] * cf[j]) / df, cap);
+                d[r * t->C + j] = d[r * t->C + j] * inv;
+            }
+        free(rf); free(cf);
+    }
+    const float dlr = (float)h->pd_dlr;
+    for (int64_t i = 0; i < n; ++i) d[i] = d[i] * dlr;
+    if (h->wd != 0 && h->pd_decouple) {
+        const float a = (float)(h->wd * h->pd_dlr);
+        for (int64_t i = 0; i < n; ++i) d[i] = fmaf(a, load_p(t, i), d[i]);
+    }
+    if (h->cautious) cautious(d, g, n);
+    write_sub(t, d, h, 1);
+    free(g); free(d);
     return 0;
 }
 

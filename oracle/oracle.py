@@ -18,6 +18,8 @@ reference's per-parameter state layout:
 * MSAM / Nekaon lookahead  -- src/kaon/msam.py:169-188, 375-406; src/kaon/nekaon.py:162-171
 * AdaPNM ``_init_state`` / ``_alloc_momentum`` -- src/kaon/adapnm.py:451-500 (two momenta,
   ``m_pos`` / ``m_neg``, whose roles alternate by step parity, :588-596)
+* KProdigy ``_init_state`` / ``_step_scope`` -- src/kaon/kprodigy.py:262-291, 306-386 (the D
+  update folds the per-tensor statistics in param order in fp32, then runs in double)
 
 Arrays: bf16 tensors are ``np.uint16`` bit patterns, fp32 are ``np.float32``.
 """
@@ -52,6 +54,8 @@ class KoTensor(ctypes.Structure):
         ("out_m", ctypes.c_void_p),
         ("fac_override", ctypes.c_void_p),
         ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
+        ("pd_s", ctypes.c_void_p), ("pd_p0", ctypes.c_void_p), ("pd_np0", ctypes.c_int64),
+        ("pd_slice", ctypes.c_int32), ("full_v", ctypes.c_int32),
     ]
 
 
@@ -65,6 +69,9 @@ class KoHyper(ctypes.Structure):
         ("nk_remove", ctypes.c_int32), ("nk_climb", ctypes.c_int32),
         ("nk_k", ctypes.c_double), ("nk_bound_old", ctypes.c_double), ("nk_bound_new", ctypes.c_double),
         ("beta0", ctypes.c_double), ("ams_bound", ctypes.c_int32),
+        ("pd_d", ctypes.c_double), ("pd_dlr", ctypes.c_double), ("pd_alpha_s", ctypes.c_double),
+        ("pd_beta3", ctypes.c_double), ("pd_eps", ctypes.c_double),
+        ("pd_decouple", ctypes.c_int32), ("pd_stats", ctypes.c_int32),
     ]
 
 
@@ -81,6 +88,13 @@ def lib() -> ctypes.CDLL:
         for name in ("ko_adakaon_tensor", "ko_lion_tensor", "ko_adamuon_tensor", "ko_adapnm_tensor"):
             getattr(L, name).argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper)]
             getattr(L, name).restype = ctypes.c_int
+        L.ko_kprodigy_pass1_tensor.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
+                                               ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+        L.ko_kprodigy_pass1_tensor.restype = ctypes.c_int
+        L.ko_kprodigy_pass2_tensor.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper)]
+        L.ko_kprodigy_pass2_tensor.restype = ctypes.c_int
+        L.ko_fsum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        L.ko_fsum.restype = ctypes.c_float
         L.ko_msam_apply.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
                                     ctypes.c_double, ctypes.c_double, ctypes.c_uint32]
         L.ko_csum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
@@ -276,6 +290,23 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
     st = prm.state
     R, C = prm.eff
     n = prm.numel
+    if opt == "kprodigy":
+        # src/kaon/kprodigy.py:262-291
+        sliced = values(prm.p, prm.p_dtype).reshape(-1)[:: group["slice_p"]].astype(np.float32)
+        st["step"] = 0
+        st["s"] = np.zeros(sliced.size, dtype=np.float32)
+        st["p0"] = sliced.copy() if float(np.sqrt(np.sum(sliced.astype(np.float64) ** 2))) > 0 else \
+            np.zeros((), dtype=np.float32)
+        if group["betas"][0] > 0:
+            _alloc_momentum(st, "m", prm, group)
+        if group["second_moment"] == "factored" and prm.factored:
+            st["row"] = np.zeros(R, dtype=np.float32)
+            st["col"] = np.zeros(C, dtype=np.float32)
+        else:
+            st["v"] = np.zeros(prm.shape, dtype=np.float32)
+        if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+            st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
+        return
     if opt == "adapnm":
         if prm.factored:
             st["row"] = np.zeros(R, dtype=np.float32)
@@ -341,6 +372,21 @@ def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) 
     return t
 
 
+def _pd_tensor(prm: OParam, group: dict[str, Any], noise=None) -> KoTensor:
+    st = prm.state
+    t = _tensor(prm, group["momentum_dtype"], noise)
+    t.pd_s = _ptr(st["s"])
+    p0 = st["p0"]
+    if p0.ndim == 0:
+        st["_p0_1"] = p0.reshape(1).copy()
+        t.pd_p0, t.pd_np0 = _ptr(st["_p0_1"]), 1
+    else:
+        t.pd_p0, t.pd_np0 = _ptr(p0), p0.size
+    t.pd_slice = int(group["slice_p"])
+    t.full_v = int("v" in st)
+    return t
+
+
 def _pnm_tensor(prm: OParam, codec: str, step: int, noise=None) -> KoTensor:
     """AdaPNM: m = this step's positive buffer, m2 = the negative one
     (_pos_neg_prefixes, src/kaon/adapnm.py:588-596: m_pos on odd steps)."""
@@ -382,7 +428,7 @@ def _check(rc: int) -> None:
 class OracleOptimizer:
     """Step driver over a list of OParam for one param group.
 
-    ``opt`` is ``"adakaon" | "lion" | "adamuon" | "nekaon" | "adapnm"``.  Nekaon is the MSAM
+    ``opt`` is ``"adakaon" | "lion" | "adamuon" | "nekaon" | "adapnm" | "kprodigy"``.  Nekaon is the MSAM
     ``norm="none"``, ``rho=-k`` preset over Adakaon (src/kaon/nekaon.py:162-171):
     the removal of the previous climb and the new climb are folded into the
     per-tensor step exactly where MSAM.step runs them (msam.py:384-403).
@@ -400,8 +446,58 @@ class OracleOptimizer:
         for prm in params:
             init_state(prm, "adakaon" if opt == "nekaon" else opt, self.group)
 
+    def _kprodigy_step(self, noise: dict[int, list] | None) -> None:
+        """KProdigy._step_scope (src/kaon/kprodigy.py:306-386) for one group."""
+        g = self.group
+        beta1, beta2 = g["betas"]
+        beta3 = g["beta3"] if g.get("beta3") is not None else math.sqrt(beta2)
+        k, d, d_max, d0 = g["k"], g["d"], g["d_max"], g["d0"]
+        lr = g["lr"]
+        bias_correction = (((1 - beta2 ** (k + 1)) ** 0.5) / (1 - beta1 ** (k + 1))
+                           if g["use_bias_correction"] else 1.0)
+        dlr = d * lr * bias_correction
+        should_update_d = (k % g["d_update_freq"]) == 0
+        d_over_d0 = d / d0
+        d_numerator = g["d_numerator"] * beta3
+        stats = lr > 0.0 and should_update_d
+        h = _hyper(g, self.seed, self.t)
+        h.eps1 = g["eps_factored"]
+        h.pd_d, h.pd_dlr, h.pd_beta3, h.pd_eps = d, dlr, beta3, g["eps"]
+        h.pd_alpha_s = d_over_d0 * d if g["safeguard_warmup"] else d_over_d0 * dlr
+        h.pd_decouple, h.pd_stats = int(g["decouple"]), int(stats)
+        num_f32, den_f32 = np.float32(0.0), np.float32(0.0)
+        const = np.float32(d_over_d0 * dlr)
+        for prm in self.params:
+            t = _pd_tensor(prm, g, None if noise is None else noise.get(prm.tensor_id))
+            num, den = ctypes.c_float(0.0), ctypes.c_float(0.0)
+            _check(lib().ko_kprodigy_pass1_tensor(ctypes.byref(t), ctypes.byref(h), ctypes.byref(num),
+                                                  ctypes.byref(den)))
+            if stats:
+                num_f32 = np.float32(num_f32 + np.float32(const * np.float32(num.value)))
+                den_f32 = np.float32(den_f32 + np.float32(den.value))
+        if should_update_d and lr > 0.0:
+            if float(den_f32) > 0.0:
+                global_num = d_numerator + float(num_f32)
+                d_hat = g["d_coef"] * global_num / float(den_f32)
+                if d == d0:
+                    d = max(d, d_hat)
+                d_max = max(d_max, d_hat)
+                d = min(d_max, d * g["growth_rate"])
+                g.update(d_numerator=global_num, d=d, d_max=d_max, d_hat=d_hat)
+        # pass 2 takes the updated d (the denominator floor d*eps, and r*c/d) with the
+        # dlr of the old d (kprodigy.py:366-386)
+        h.pd_d = d
+        for prm in self.params:
+            prm.state["step"] += 1
+            t = _pd_tensor(prm, g, None if noise is None else noise.get(prm.tensor_id))
+            _check(lib().ko_kprodigy_pass2_tensor(ctypes.byref(t), ctypes.byref(h)))
+        g["k"] = k + 1
+
     def step(self, noise: dict[int, list] | None = None, fac_override: dict[int, np.ndarray] | None = None) -> None:
         self.t += 1
+        if self.opt == "kprodigy":
+            self._kprodigy_step(noise)
+            return
         h = _hyper(self.group, self.seed, self.t)
         md = self.group["momentum_dtype"]
         if self.opt == "nekaon":

@@ -77,6 +77,22 @@ CASES = {
                          p_dtype="f32", g_dtype="f32"),
     "pnm_kahan": _case("adapnm", _SMALL, dict(lr=1e-3, momentum_dtype="bfloat16", bf16_method="kahan",
                                               foreach=False)),
+    # KProdigy (src/kaon/kprodigy.py) -- D adaptation over six steps
+    "pd_bf16_sr": _case("kprodigy", _SMALL, dict(lr=1.0, momentum_dtype="bfloat16", foreach=False), steps=6),
+    "pd_int8_factored": _case("kprodigy", _SMALL, dict(lr=1.0, momentum_dtype="int8", second_moment="factored",
+                                                       cautious=True, weight_decay=0.01, slice_p=3,
+                                                       foreach=False), steps=6),
+    "pd_4bit_rn": _case("kprodigy", _ODD, dict(lr=1.0, momentum_dtype="4bit", momentum_4bit_block=16,
+                                               bf16_method="none", use_bias_correction=True,
+                                               safeguard_warmup=True, foreach=True), steps=6),
+    "pd_f32_coupled": _case("kprodigy", _SMALL, dict(lr=1.0, betas=(0.9, 0.99), momentum_dtype="float32",
+                                                     weight_decay=0.1, decouple=False, slice_p=2, growth_rate=1.02,
+                                                     d_coef=0.5, foreach=True), steps=6,
+                            p_dtype="f32", g_dtype="f32"),
+    "pd_nomom_caut": _case("kprodigy", _SMALL, dict(lr=1.0, betas=(0.0, 0.999), cautious=True, d_update_freq=2,
+                                                    foreach=False), steps=6),
+    "pd_kahan": _case("kprodigy", _SMALL, dict(lr=1.0, momentum_dtype="bfloat16", bf16_method="kahan",
+                                               second_moment="factored", foreach=False), steps=6),
 }
 
 # Adakaon on a conv [320,320,3,3] and a linear [1280,1280],

@@ -5,7 +5,7 @@ Run in the build container only (the reference is not present on the GPU box):
     python tests/golden/make_golden.py /root/reference/src [case ...]
 
 It imports the reference ``kaon`` package (pure Python + torch CPU) and steps
-its Adakaon / Lion / AdaMuon / Nekaon / AdaPNM on small seeded inputs.  The codecs, the
+its Adakaon / Lion / AdaMuon / Nekaon / AdaPNM / KProdigy on small seeded inputs.  The codecs, the
 SR bit trick, the cautious rule and the Philox stream are pinned by closed
 forms and known-answer tests elsewhere; what only the reference itself can pin
 is the composition of torch-CPU ops (lerp/FMA placement, bf16-rounded GC,
@@ -118,7 +118,13 @@ def make_opt(kaon, case, params):
         return kaon.Nekaon(params, **kw)
     if name == "adapnm":
         return kaon.AdaPNM(params, **kw)
+    if name == "kprodigy":
+        return kaon.KProdigy(params, **kw)
     raise ValueError(name)
+
+
+def name_of(case) -> str:
+    return case["opt"]
 
 
 def run_case(kaon, case):
@@ -127,6 +133,7 @@ def run_case(kaon, case):
     _CTX["seed"] = case["seed"]
     _CTX["ids"] = {p.data_ptr(): i for i, p in enumerate(params)}
     hashes = []
+    d_traj = []
     for step in range(1, case["steps"] + 1):
         for i, p in enumerate(params):
             g = grad_values(case, i, step)
@@ -134,6 +141,8 @@ def run_case(kaon, case):
             p.grad = torch.from_numpy(g).to(gdt)
         _CTX["step"] = step
         opt.step()
+        if name_of(case) == "kprodigy":
+            d_traj.append(opt.param_groups[0]["d"])
         if step == 1 and case.get("sample_stride"):
             step1 = [_bits(p).reshape(-1)[::case["sample_stride"]] for p in params]
         hashes.append(hashlib.sha256(b"".join(_bits(p).tobytes() for p in params)).hexdigest())
@@ -143,6 +152,13 @@ def run_case(kaon, case):
         eval_p = [_bits(p) for p in params]
         opt.train()
     out = {"hashes": hashes}
+    if name_of(case) == "kprodigy":
+        # the group's D state (kprodigy.py:365-380): d after every step, and the final scalars
+        grp = opt.param_groups[0]
+        out["d_traj"] = np.array(d_traj, dtype=np.float64)
+        for key in ("d", "d_max", "d_numerator"):
+            out[f"g_{key}"] = np.array(grp[key], dtype=np.float64)
+        out["g_k"] = np.array(grp["k"], dtype=np.int64)
     inner = getattr(opt, "inner", opt)
     for i, p in enumerate(params):
         st = inner.state[p]

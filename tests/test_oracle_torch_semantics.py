@@ -14,7 +14,9 @@ the ground truth for one-op rounding questions the fixtures cannot isolate:
 * the SR bit trick against its three-op torch form
   (src/kaon/_stochastic_rounding.py:88-103);
 * addcmul_(g, g, value=s) after mul_(beta2): AdaPNM's 1-D second moment
-  (src/kaon/adapnm.py:1243-1244), one fma of (s * g) and g into v * beta2.
+  (src/kaon/adapnm.py:1243-1244), one fma of (s * g) and g into v * beta2;
+* add_(x, alpha) on bf16 tensors: KProdigy's bf16 momentum
+  (src/kaon/kprodigy.py:738-740) -- torch CPU's vector loop rounds alpha to bf16.
 
 A plausible slip -- a lerp without the fma, the branch threshold on the wrong
 side, truncation instead of RNE, an fp32 instead of a bf16 GC -- fails one of
@@ -105,3 +107,26 @@ def test_pnm_addcmul_second_moment_matches_torch():
     want = v.numpy()
     assert np.array_equal(prm.state["v"].view(np.uint32), want.view(np.uint32))
     assert (unfused.view(np.uint32) != want.view(np.uint32)).sum() > 10
+
+
+def test_bf16_add_alpha_is_rounded_to_bf16_by_torch_cpu():
+    """KProdigy's bf16 momentum is m.mul_(beta1).add_(g.to(bf16), alpha=d*(1-beta1))
+    (kprodigy.py:738-740).  torch CPU's 32-wide vector loop rounds alpha to bf16
+    (an fp32 alpha differs on most elements; the oracle's KProdigy pass 1 uses the
+    bf16 one).  On a length that is a multiple of 32 (no scalar tail) the bf16-alpha
+    form matches every element; the fp32-alpha form does not."""
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(9)
+    n = 32 * 4096
+    g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).bfloat16()
+    m0 = torch.from_numpy((rng.standard_normal(n) * 1e-9).astype(np.float32)).bfloat16()
+    alpha, b1 = 3.3e-5 * 0.1, 0.9
+    want = m0.clone().mul_(b1).add_(g, alpha=alpha).float().numpy()
+    mb = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(O.f32_to_bf16(m0.float().numpy())) * np.float32(b1)))
+    gf = g.float().numpy()
+    ab = O.bf16_to_f32(O.f32_to_bf16(np.array([alpha], dtype=np.float32)))[0]
+    exact = mb.astype(np.float64) + np.float64(ab) * gf.astype(np.float64)  # exact product of two bf16
+    got = O.bf16_to_f32(O.f32_to_bf16(exact.astype(np.float32)))
+    assert np.array_equal(got, want)
+    f32a = O.bf16_to_f32(O.f32_to_bf16((mb + np.float32(alpha) * gf).astype(np.float32)))
+    assert (f32a != want).sum() > n // 10

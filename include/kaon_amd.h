@@ -12,9 +12,10 @@
  * 506-513, 533-539), and MSAM's 4-bit perturbation launch
  * (src/kaon/msam.py:238-290 -> _fused_triton.py:1145-1179).  Lion
  * (src/kaon/lion.py:322-485) and AdaMuon (src/kaon/adamuon.py:327-615) call
- * torch ops directly; this ABI covers all four optimizers, and AdaPNM
+ * torch ops directly; this ABI covers all four optimizers, AdaPNM
  * (src/kaon/adapnm.py, whose Triton path _fused_triton.py:724-1143 is launched
- * from adapnm.py:647-980).
+ * from adapnm.py:647-980) and KProdigy's two passes (src/kaon/kprodigy.py:306-441,
+ * 744-960).
  *
  * Conventions
  *  - Plain C types only.  Every pointer inside KaonTensor / KaonItem points to
@@ -35,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 6
+#define KAON_ABI_VERSION 7
 
 /* element types of params / grads (p.dtype, p.grad.dtype) */
 enum { KAON_F32 = 0, KAON_BF16 = 1 };
@@ -48,7 +49,7 @@ enum { KAON_MOM_NONE = 0, KAON_MOM_F32 = 1, KAON_MOM_BF16 = 2, KAON_MOM_INT8 = 3
 enum { KAON_SR = 0, KAON_RN = 1, KAON_KAHAN = 2 };
 
 /* optimizer selected by a plan / step */
-enum { KAON_OPT_ADAKAON = 0, KAON_OPT_LION = 1, KAON_OPT_ADAMUON = 2, KAON_OPT_ADAPNM = 3 };
+enum { KAON_OPT_ADAKAON = 0, KAON_OPT_LION = 1, KAON_OPT_ADAMUON = 2, KAON_OPT_ADAPNM = 3, KAON_OPT_KPRODIGY = 4 };
 
 /* per-launch flags (KaonHyper.flags) */
 enum {
@@ -63,7 +64,10 @@ enum {
                            read the orthogonalized O from the workspace instead of the grad */
   KAON_F_PNM = 256,     /* set by the library for AdaPNM: the 1-D second moment is
                            v*beta2 + (1-beta2)*g*g (adapnm.py:1243-1244) */
-  KAON_F_AMS = 512      /* AdaPNM ams_bound: 1-D denominators from the running max of v */
+  KAON_F_AMS = 512,     /* AdaPNM ams_bound: 1-D denominators from the running max of v */
+  KAON_F_PD_COUPLED = 1024, /* KProdigy pass 1: weight decay folded into the gradient
+                               (decouple=False, kprodigy.py:342-349) */
+  KAON_F_PD_STATS = 2048    /* KProdigy pass 1: update s and the D statistics this step */
 };
 
 /*
@@ -86,6 +90,14 @@ typedef struct KaonTensor {
   void* m2;               /* AdaPNM: "m_neg", layout as m ("m_pos"); adapnm.py:451-500 */
   float* m2_scale;        /* AdaPNM: "m_neg_scale" */
   float* max_v;           /* AdaPNM ams_bound, 1-D: "max_v" [C] */
+  float* pd_s;            /* KProdigy: "s" [pd_ns] */
+  const float* pd_p0;     /* KProdigy: "p0" [pd_ns], or its single 0.0 when pd_p0_scalar */
+  int64_t pd_ns;          /* KProdigy: ceil(n / pd_slice), the sliced length */
+  int32_t pd_slice;       /* KProdigy: slice_p */
+  int32_t pd_p0_scalar;   /* KProdigy: "p0" is the 0-dim zero (the initial slice had norm 0) */
+  int32_t full_v;         /* KProdigy: per-element second moment "v" on a matrix (second_moment
+                             "full"); 1-D KProdigy tensors always set it */
+  int32_t pd_pad;
   const uint16_t* noise[3]; /* optional injected SR noise per stream (tests) */
   int64_t R, C;           /* matrixized shape */
   int64_t n;              /* R * C */
@@ -94,9 +106,10 @@ typedef struct KaonTensor {
   int64_t ws_col;         /* cf [C] */
   int64_t ws_part;        /* column partials [ngroups][C], one row per run */
   int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
-  int64_t ws_scal;        /* 4 words: fac, keep-count, spare, spare */
+  int64_t ws_scal;        /* 4 words: fac, keep-count, KProdigy num, KProdigy den */
   int64_t ws_aux;         /* AdaMuon: Newton-Schulz buffers, bf16: M then O [R*C], the iterate
-                             X and its successor [m_pad*k_pad] each, A and B [m_pad^2] each */
+                             X and its successor [m_pad*k_pad] each, A and B [m_pad^2] each;
+                             KProdigy: the D statistics' block sums, [2][ceil(pd_ns / KAON_FLAT_ITEM)] */
   int32_t tensor_id;      /* SR counter field: index in the optimizer's param list */
   int32_t block4;         /* 4-bit block size (m_block) */
   int32_t factored;       /* ndim >= 2 */
@@ -215,6 +228,13 @@ typedef struct KaonHyper {
   float nk_bound_old;     /* frozen climb bound of the previous climb (msam.py:169-188) */
   float nk_bound_new;     /* |k| * clip * lr at this climb */
   float pn_pos, pn_neg, pn_rnorm, bc2; /* AdaPNM */
+  /* KProdigy (kprodigy.py:306-386, 723-808; b1 = beta1, w1 = 1 - beta1, b2 = beta2,
+   * w2 = 1 - beta2, eps1 = eps_factored, wdl = wd for the pass-1 coupled decay):
+   * pd_tg = d*(1 - beta1), pd_vval = d*d*(1 - beta2), pd_alpha_s, pd_beta3 of the s EMA,
+   * pd_d = d before this step's D update (the momentum's d), pd_dn = d after it,
+   * pd_floor = dn*eps, pd_cap = 1/(dn*eps) (pass 2), pd_dlr = dlr of the old d, pd_wdl =
+   * wd*dlr (decoupled decay) */
+  float pd_tg, pd_vval, pd_alpha_s, pd_beta3, pd_d, pd_dn, pd_floor, pd_cap, pd_dlr, pd_wdl;
   int32_t flags;          /* KAON_F_* */
   int32_t p_dtype, g_dtype, codec, bf16_method;
   int32_t ns_steps;       /* AdaMuon Newton-Schulz iterations */
@@ -269,6 +289,22 @@ int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
  * _factored_bucket / _nonfactored_bucket (adapnm.py:1069-1275) and the fused
  * launches of adapnm.py:647-980. */
 int kaon_adapnm_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
+/* KProdigy over one planned param group (plan opt = KAON_OPT_KPRODIGY).  Pass 1:
+ * the factored row/col EMAs (second_moment "factored"), the GC row means, the
+ * first moment of d*g in its codec and the full v, and when KAON_F_PD_STATS is
+ * set the s EMA and each tensor's D statistics num = FSUM(g (p0 - p)) and den =
+ * FSUM(|s|) over its sliced elements (FSUM: blocks of KAON_FLAT_ITEM elements in
+ * the 64-lane order, then the 64-lane order over the blocks), left in the
+ * tensor's scalar words 2 and 3 of the workspace.  The caller folds them over
+ * every tensor of the D scope in param order and updates D as
+ * KProdigy._step_scope does (kprodigy.py:355-380).  Pass 2: the update with the
+ * new d and the old dlr (kprodigy.py:383-386, 768-808): cautious count, then the
+ * apply (int8 / 4-bit momenta are requantized here, as pass 1's absmax left them).
+ * Replaces KProdigy._pass1_per_param / _pass1_foreach and _update_one_param /
+ * _update_foreach (kprodigy.py:392-441, 443-674, 744-960). */
+int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+int kaon_kprodigy_pass2(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
 /* The same steps restricted to the phases whose bit is set in `mask`
  * (bit k = phase k: 1 row statistics, 2 column/row finalize, 3 clip sums,

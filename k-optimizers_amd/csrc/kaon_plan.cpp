@@ -88,7 +88,7 @@ int row_class(const KaonTensor& t, int32_t g_dtype) {
 // grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
 // momentum blocks of 8*G elements (G | 64) that tile the rows.
 bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
-  if (a.opt == KAON_OPT_ADAMUON || a.opt == KAON_OPT_ADAPNM) return false;
+  if (a.opt == KAON_OPT_ADAMUON || a.opt == KAON_OPT_ADAPNM || a.opt == KAON_OPT_KPRODIGY) return false;
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
   if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
   if (a.codec == KAON_MOM_F32) return false;
@@ -117,7 +117,8 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
   if (!args) return plan_fail("kaon_plan: args is NULL");
   const int32_t opt = args->opt, codec = args->codec, g_dtype = args->g_dtype;
   if (n < 0 || (n > 0 && !descs)) return plan_fail("kaon_plan: bad descriptor array");
-  if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM)
+  if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM &&
+      opt != KAON_OPT_KPRODIGY)
     return plan_fail("kaon_plan: unknown optimizer");
   if (codec < KAON_MOM_NONE || codec > KAON_MOM_4BIT) return plan_fail("kaon_plan: unknown codec");
   if (g_dtype != KAON_F32 && g_dtype != KAON_BF16) return plan_fail("kaon_plan: unknown grad dtype");
@@ -155,6 +156,17 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     const int64_t slice_rows = 4 * rw;
     const int64_t run_rows = KAON_RUN * slice_rows;
     t.ngroups = (int32_t)((t.R + run_rows - 1) / run_rows);
+    if (opt == KAON_OPT_KPRODIGY) {
+      if (!t.factored && !t.full_v)
+        return plan_fail("kaon_plan: KProdigy 1-D tensor " + std::to_string(i) + " needs full_v (a per-element v)");
+      if (t.pd_slice < 1) return plan_fail("kaon_plan: KProdigy slice_p must be >= 1");
+      if (t.pd_ns != (t.R * t.C + t.pd_slice - 1) / t.pd_slice)
+        return plan_fail("kaon_plan: KProdigy tensor " + std::to_string(i) + " has pd_ns != ceil(n / slice_p)");
+      if (t.R * t.C > 0 && (!t.pd_s || !t.pd_p0))
+        return plan_fail("kaon_plan: KProdigy tensor " + std::to_string(i) + " needs s and p0");
+    } else {
+      t.full_v = 0;
+    }
     if (opt == KAON_OPT_ADAPNM && (!t.m || !t.m2))
       return plan_fail("kaon_plan: AdaPNM tensor " + std::to_string(i) + " needs both momentum buffers (m, m2)");
     const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
@@ -167,7 +179,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     off = round4(off + 5 * t.R);
     t.ws_col = off;
     t.ws_part = off;
-    if (t.factored) {
+    if (t.factored && !t.full_v) {
       off = round4(off + t.C);
       t.ws_part = off;
       off = round4(off + (int64_t)t.ngroups * t.C);
@@ -202,6 +214,11 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
           for (int32_t b = 0; b < tk; ++b) (big ? ns_rect_big : ns_rect).push_back(KaonItem{i, a, b, big});
       }
     }
+    if (opt == KAON_OPT_KPRODIGY) {
+      // the D statistics' block sums (num, den) per KAON_FLAT_ITEM sliced elements
+      const int64_t nfb = (t.pd_ns + KAON_FLAT_ITEM - 1) / KAON_FLAT_ITEM;
+      off = round4(off + 2 * nfb);
+    }
     if (t.n == 0) continue;
     // runs (row items): kind = rows per wave group
     const int cls = row_class(t, row_dtype);
@@ -227,14 +244,17 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
         elems.push_back({it, cls, t.n, false});
       }
     }
-    // finalize items (Adakaon / AdaMuon factored second moment)
-    if (t.factored && opt != KAON_OPT_LION) {
+    // finalize items (the factored second moment of every optimizer but Lion)
+    if (t.factored && !t.full_v && opt != KAON_OPT_LION) {
       for (int64_t c0 = 0; c0 < t.C; c0 += KAON_COLITEM)
         fins.push_back(KaonItem{i, (int32_t)c0, (int32_t)std::min<int64_t>(KAON_COLITEM, t.C - c0), 0});
       fins.push_back(KaonItem{i, 0, (int32_t)t.R, 1});
     }
-    for (int64_t e0 = 0; e0 < t.n; e0 += KAON_FLAT_ITEM)
-      flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, t.n - e0), 0});
+    // flat items: blocks of the elements (MSAM perturbation), or for KProdigy of
+    // the sliced elements (the D statistics)
+    const int64_t nflat = opt == KAON_OPT_KPRODIGY ? t.pd_ns : t.n;
+    for (int64_t e0 = 0; e0 < nflat; e0 += KAON_FLAT_ITEM)
+      flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, nflat - e0), 0});
   }
   // elem order: specialized-kernel slices first, each part largest tensors first
   std::stable_sort(elems.begin(), elems.end(), [](const RowIt& a, const RowIt& b) {

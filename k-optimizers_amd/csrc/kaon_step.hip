@@ -171,6 +171,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   extern __shared__ float lds_col[];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
+  if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
   zero_accumulators(T, it, ws, hp.codec);
   const void* gsrc = ws.src(T, hp.flags);
   const int64_t C = T.C;
@@ -802,6 +803,7 @@ __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, c
                                              float* racc) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
+  if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
   zero_accumulators(T, it, ws, hp.codec);
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
   KAON_G float* part = run_part(ws, T, it);
@@ -1693,6 +1695,383 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
   }
 }
 
+// =============================================================== KProdigy
+// The two passes of KProdigy (src/kaon/kprodigy.py).  Pass 1 sees the gradient
+// g' = GC(g), plus wd * p when the decay is coupled (_collect_grad, :342-349);
+// pass 2 reads the GC'd gradient (:768-808).
+
+// Clear the keep count and the 4-bit block absmax of every tensor.
+__global__ __launch_bounds__(KAON_WG) void k_pd_zero(const KaonTensor* __restrict__ D, Ws ws, int codec) {
+  const KaonTensor& T = D[blockIdx.x];
+  if (threadIdx.x == 0) ((KAON_G uint32_t*)ws.scal(T))[1] = 0u;
+  if (codec == KAON_MOM_4BIT) {
+    const int64_t nb = nblocks4(T);
+    for (int64_t b = threadIdx.x; b < nb; b += KAON_WG) ws.bamax(T)[b] = 0u;
+  }
+}
+
+// Pass 1 over rows (_pass1_per_param, kprodigy.py:392-441; _update_momentum
+// :723-741): the GC row means (kept for the later kernels), the first moment of
+// d*g' in its codec -- fp32 m*beta1 + d(1-beta1) g'; bf16 storage rounds after
+// mul_ and after add_, whose alpha torch rounds to bf16; int8 and 4-bit (a lerp
+// toward d*g') leave the row / block absmax and the old scales, pass 2
+// requantizes -- and the full second moment v*beta2 + d^2(1-beta2) g' g'.
+template <int GT, int PT, int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec = T.vec_rows != 0;
+  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
+  const bool coupled = (hp.flags & KAON_F_PD_COUPLED) != 0;
+  const float tgb = rbf(hp.pd_tg);
+  const int nsl = run_slices(it);
+#pragma clang loop unroll(disable)
+  for (int sl = 0; sl < nsl; ++sl) {
+  const WaveRows wr = wave_rows(slice_item(it, sl));
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    float mu = 0.0f;
+    if (gc) {
+      float a = 0.0f;
+      for (int k = 0; k < cpl; ++k) {
+        const int64_t c = wr.lane + 64 * k;
+        const int cnt = chunk_cnt(c, C);
+        if (cnt <= 0) continue;
+        float x[8];
+        ld8<GT>(T.g, r * C + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i < cnt) a = a + x[i];
+      }
+      mu = round_to<GT>(wave_csum(a) / (float)C);
+      if (wr.lane == 0) ws.mu(T)[r] = mu;
+    }
+    const int64_t sr = T.factored ? r : 0;
+    const float oldsc = CODEC == KAON_MOM_INT8 ? uniform_f(G(T.m_scale)[sr]) : 1.0f;
+    const bool dqf = fabsf(oldsc) < 0x1p120f;
+    float amax = 0.0f;
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
+      const int64_t e0 = r * C + c * 8;
+      const bool vv = vec && cnt == 8;
+      float g[8];
+      ld8<GT>(T.g, e0, cnt, vv, g);
+      if (gc) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          float a0 = g[i] - mu, a1 = g[i + 1] - mu;
+          if (GT == KAON_BF16) rbf2(a0, a1);
+          g[i] = a0;
+          g[i + 1] = a1;
+        }
+      }
+      if (coupled) {
+        float p[8];
+        ld8<PT>(T.p, e0, cnt, vv, p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] = __fmaf_rn(hp.wdl, p[i], g[i]);
+      }
+      if (CODEC != KAON_MOM_NONE) {
+        uint32_t mq[8];
+        ld_mom_at<CODEC>(T.m, e0, cnt, vv, mq);
+        if (CODEC == KAON_MOM_F32 || CODEC == KAON_MOM_BF16) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (CODEC == KAON_MOM_F32) {
+              mq[i] = __float_as_uint(__fmaf_rn(hp.pd_tg, g[i], __uint_as_float(mq[i]) * hp.b1));
+            } else {
+              const float mb = rbf(bf2f(mq[i]) * hp.b1);
+              mq[i] = f2bf(__fmaf_rn(tgb, rbf(g[i]), mb));
+            }
+          }
+          st_mom_at<CODEC>(T.m, T.n, e0, cnt, vv, mq);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (i >= cnt) continue;
+            if (CODEC == KAON_MOM_INT8) {
+              const float mf = __fmaf_rn(hp.pd_tg, g[i], dq_int8(mq[i], oldsc, -128.0f * oldsc, dqf) * hp.b1);
+              amax = fmaxf(amax, fabsf(mf));
+            } else {
+              const int64_t e = e0 + i, blk = e / T.block4;
+              const float sc = G(T.m_scale)[blk];
+              const float mf = klerp(((float)mq[i] - 8.0f) * sc, g[i] * hp.pd_d, hp.w1);
+              const float ax = fabsf(mf);
+              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
+              if (e == blk * (int64_t)T.block4) ws.boldsc(T, nblocks4(T))[blk] = sc;
+            }
+          }
+        }
+      }
+      if (T.full_v) {
+        float v[8];
+        ld8<KAON_F32>(T.v, e0, cnt, vv, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __fmaf_rn(hp.pd_vval * g[i], g[i], v[i] * hp.b2);
+        st8_f32(T.v, e0, cnt, vv, v);
+      }
+    }
+    if (CODEC == KAON_MOM_INT8) {
+      const float am = wave_max(amax);
+      if (wr.lane == 0) {
+        ws.ramax(T)[r] = __float_as_uint(am);
+        ws.roldsc(T)[r] = oldsc;
+      }
+    }
+  }
+  }
+}
+
+// Pass 1, D statistics: one wave per flat item of KAON_FLAT_ITEM sliced
+// elements j (element j * slice_p): s_j = fma(alpha_s, g', s_j * beta3), and the
+// item's sums of g' (p0 - p) and |s| in the 64-lane order (lane l adds chunks
+// l, l+64, ... of 8 sliced elements), stored per item for k_pd_sfin.
+template <int GT, int PT>
+__global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restrict__ D,
+                                                      const KaonItem* __restrict__ items, int32_t n_items, Ws ws,
+                                                      KaonHyper hp) {
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int64_t idx = (int64_t)blockIdx.x * 4 + w;
+  if (idx >= n_items) return;
+  const KaonItem it = items[idx];
+  const KaonTensor& T = D[it.tensor];
+  const int64_t sp = T.pd_slice, C = T.C, j0 = it.row0, len = it.nrows;
+  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
+  const bool coupled = (hp.flags & KAON_F_PD_COUPLED) != 0;
+  const KAON_G float* p0 = G(T.pd_p0);
+  KAON_G float* sv = G(T.pd_s);
+  float an = 0.0f, ad = 0.0f;
+  const int64_t nch = (len + 7) >> 3;
+  for (int64_t c = lane; c < nch; c += 64) {
+    for (int i = 0; i < 8; ++i) {
+      const int64_t jj = c * 8 + i;
+      if (jj >= len) break;
+      const int64_t j = j0 + jj, e = j * sp;
+      float gv, pv;
+      if (GT == KAON_BF16) gv = bf2f(G((const uint16_t*)T.g)[e]);
+      else gv = G((const float*)T.g)[e];
+      if (PT == KAON_BF16) pv = bf2f(G((const uint16_t*)T.p)[e]);
+      else pv = G((const float*)T.p)[e];
+      if (gc) gv = round_to<GT>(gv - ws.mu(T)[e / C]);
+      if (coupled) gv = __fmaf_rn(hp.wdl, pv, gv);
+      const float pz = T.pd_p0_scalar ? p0[0] : p0[j];
+      an = an + gv * (pz - pv);
+      const float snew = __fmaf_rn(hp.pd_alpha_s, gv, sv[j] * hp.pd_beta3);
+      sv[j] = snew;
+      ad = ad + fabsf(snew);
+    }
+  }
+  const float num = wave_csum(an), den = wave_csum(ad);
+  if (lane == 0) {
+    const int64_t nfb = (T.pd_ns + KAON_FLAT_ITEM - 1) / KAON_FLAT_ITEM, blk = j0 / KAON_FLAT_ITEM;
+    KAON_G float* bs = G(ws.base + T.ws_aux);
+    bs[blk] = num;
+    bs[nfb + blk] = den;
+  }
+}
+
+// Each tensor's D statistics from its item sums, in the 64-lane order, into
+// its scalar words 2 (num) and 3 (den).  One wave per tensor.
+__global__ __launch_bounds__(KAON_WG) void k_pd_sfin(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
+  const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (t >= n_tensors) return;
+  const KaonTensor& T = D[t];
+  const int lane = threadIdx.x & 63;
+  const int64_t nfb = (T.pd_ns + KAON_FLAT_ITEM - 1) / KAON_FLAT_ITEM;
+  const KAON_G float* bs = G(ws.base + T.ws_aux);
+  float a = 0.0f, b = 0.0f;
+  for (int64_t c = lane; c * 8 < nfb; c += 64)
+    for (int i = 0; i < 8; ++i) {
+      const int64_t k = c * 8 + i;
+      if (k < nfb) {
+        a = a + bs[k];
+        b = b + bs[nfb + k];
+      }
+    }
+  const float sa = wave_csum(a), sb = wave_csum(b);
+  if (lane == 0) {
+    ws.scal(T)[2] = sa;
+    ws.scal(T)[3] = sb;
+  }
+}
+
+// Pass 2 (_update_one_param, kprodigy.py:768-808), phase 5 (cautious keep count)
+// or 6 (apply): numerator = the momentum (float codecs as pass 1 stored it; int8 /
+// 4-bit requantized here from the old codes with pass 1's absmax) or g; over
+// max(sqrt(v), dn*eps), or times min(r c / dn, 1/(dn*eps)); times dlr; decoupled
+// WD; cautious; write.
+template <int PHASE, int PT, int GT, int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  __shared__ uint32_t keep_s[4];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C, n = T.n;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec_t = T.vec_rows != 0;
+  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
+  const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
+  const bool decoupled_wd = (hp.flags & KAON_F_WD) != 0;
+  const bool coupled = (hp.flags & KAON_F_PD_COUPLED) != 0;
+  const bool lowp = PT == KAON_BF16;
+  const bool factored = T.factored && !T.full_v;
+  const int64_t B = CODEC == KAON_MOM_4BIT ? (int64_t)T.block4 : 1;
+  const int64_t nb = CODEC == KAON_MOM_4BIT ? nblocks4(T) : 0;
+  const WaveRows wr = wave_rows(it);
+  double rden = 1.0;
+  if (PHASE == 6 && cautious) {
+    const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
+    rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
+  }
+  uint32_t keep = 0;
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
+    const float rf = factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    float oldsc = 1.0f, newsc = 1.0f;
+    double rnew = 1.0;
+    if (CODEC == KAON_MOM_INT8) {
+      oldsc = uniform_f(ws.roldsc(T)[r]);
+      newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+      rnew = rcp64(newsc);
+    }
+    const bool dqf = fabsf(oldsc) < 0x1p120f;
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
+      const int64_t j0 = c * 8;
+      const int64_t e0 = r * C + j0;
+      const bool vec = vec_t && cnt == 8;
+      float g[8], p[8], f[8];
+      uint32_t mq[8], pb[8];
+      ld8<GT>(T.g, e0, cnt, vec, g);
+      const bool need_p = PHASE == 6 || decoupled_wd || (coupled && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT));
+      if (need_p) {
+        if (PT == KAON_BF16) {
+          ld8_bits(T.p, e0, cnt, vec, pb);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+        } else {
+          ld8<KAON_F32>(T.p, e0, cnt, vec, p);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = 0.0f;
+      }
+      if (CODEC != KAON_MOM_NONE) ld_mom_at<CODEC>(T.m, e0, cnt, vec, mq);
+      if (factored) ld8<KAON_F32>((const float*)ws.cf(T), j0, cnt, vec, f);
+      else ld8<KAON_F32>(T.v, e0, cnt, vec, f);
+      uint32_t nz[8];
+      if (PHASE == 6 && lowp && hp.bf16_method == KAON_SR) {
+        if ((e0 & 7) == 0) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], cnt, nz);
+        else
+#pragma unroll
+          for (int i = 0; i < 8; ++i) nz[i] = i < cnt ? noise1(hp.seed, hp.step, T.tensor_id, 1u, e0 + i, T.noise[1]) : 0u;
+      }
+      if (gc) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          float a0 = g[i] - mu, a1 = g[i + 1] - mu;
+          if (GT == KAON_BF16) rbf2(a0, a1);
+          g[i] = a0;
+          g[i + 1] = a1;
+        }
+      }
+      uint32_t qout[8];
+      float dout[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qout[i] = mq[i];
+        dout[i] = 0.0f;
+        if (i >= cnt) continue;
+        const int64_t e = e0 + i;
+        const float gq = coupled ? __fmaf_rn(hp.wdl, p[i], g[i]) : g[i];
+        float numer;
+        if (CODEC == KAON_MOM_NONE) {
+          numer = g[i];
+        } else if (CODEC == KAON_MOM_F32) {
+          numer = __uint_as_float(mq[i]);
+        } else if (CODEC == KAON_MOM_BF16) {
+          numer = bf2f(mq[i]);
+        } else if (CODEC == KAON_MOM_INT8) {
+          const float mf = __fmaf_rn(hp.pd_tg, gq, dq_int8(mq[i], oldsc, -128.0f * oldsc, dqf) * hp.b1);
+          float x = rintf(div_r64(mf, rnew));
+          x = fminf(fmaxf(x, -127.0f), 127.0f);
+          qout[i] = (uint32_t)(uint8_t)(int8_t)x;
+          numer = x * newsc;
+        } else {
+          const int64_t blk = e / B;
+          const float sco = ws.boldsc(T, nb)[blk];
+          const float scn = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+          const float mf = klerp(((float)mq[i] - 8.0f) * sco, gq * hp.pd_d, hp.w1);
+          float x = rintf(div_r64(mf, rcp64(scn)));
+          x = fminf(fmaxf(x, -7.0f), 7.0f);
+          qout[i] = (uint32_t)((int)x + 8);
+          numer = x * scn;
+          if (PHASE == 6 && e == blk * B) G(T.m_scale)[blk] = scn;
+        }
+        const float u = factored ? numer * fminf((rf * f[i]) / hp.pd_dn, hp.pd_cap)
+                                 : numer / fmaxf(sqrtf(f[i]), hp.pd_floor);
+        float d = u * hp.pd_dlr;
+        if (decoupled_wd) d = __fmaf_rn(hp.pd_wdl, p[i], d);
+        const bool kp = d * g[i] > 0.0f;
+        if (PHASE == 5) {
+          keep += kp ? 1u : 0u;
+          continue;
+        }
+        dout[i] = cautious ? div_r64(d * (kp ? 1.0f : 0.0f), rden) : d;
+      }
+      if (PHASE != 6) continue;
+      if (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) st_mom_at<CODEC>(T.m, n, e0, cnt, vec, qout);
+      if (PT == KAON_F32) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = p[i] - dout[i];
+        st8_f32(T.p, e0, cnt, vec, o);
+      } else {
+        uint32_t o[8];
+        if (hp.bf16_method == KAON_KAHAN) {
+          uint32_t sh[8];
+          ld8_bits(T.shift, e0, cnt, vec, sh);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            const float p0 = p[i];
+            const float p1 = rbf(p0 + s);
+            o[i] = f2bf(p1);
+            sh[i] = f2bf(s + rbf(p0 - p1));
+          }
+          st8_bits(T.shift, e0, cnt, vec, sh);
+        } else if (hp.bf16_method == KAON_RN) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz[i]);
+        }
+        st8_bits(T.p, e0, cnt, vec, o);
+      }
+    }
+    if (PHASE == 6 && CODEC == KAON_MOM_INT8 && wr.lane == 0) G(T.m_scale)[T.factored ? r : 0] = newsc;
+  }
+  if (PHASE == 5 && cautious) {
+    const uint32_t wsum = wave_sum_u32(keep);
+    if (wr.lane == 0) keep_s[wr.w] = wsum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
+      if (tot) atomicAdd(ws.keep_ctr(T), tot);
+    }
+  }
+}
+
 // =============================================================== fast path
 // Phases 5 and 6 specialized at compile time for bf16 params and grads,
 // stochastic-rounding writes and 16-byte-aligned rows: every full 8-element
@@ -2497,6 +2876,53 @@ PnmFn pnm_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
+using PdFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
+using PdStatsFn = void (*)(const KaonTensor*, const KaonItem*, int32_t, Ws, KaonHyper);
+template <int GT, int PT>
+PdFn pd1_by_codec(int codec) {
+  switch (codec) {
+    case KAON_MOM_NONE: return k_pd1<GT, PT, KAON_MOM_NONE>;
+    case KAON_MOM_F32: return k_pd1<GT, PT, KAON_MOM_F32>;
+    case KAON_MOM_BF16: return k_pd1<GT, PT, KAON_MOM_BF16>;
+    case KAON_MOM_INT8: return k_pd1<GT, PT, KAON_MOM_INT8>;
+    case KAON_MOM_4BIT: return k_pd1<GT, PT, KAON_MOM_4BIT>;
+  }
+  return nullptr;
+}
+PdFn pd1_fn(int pt, int gt, int codec) {
+  if (gt == KAON_BF16 && pt == KAON_BF16) return pd1_by_codec<KAON_BF16, KAON_BF16>(codec);
+  if (gt == KAON_BF16 && pt == KAON_F32) return pd1_by_codec<KAON_BF16, KAON_F32>(codec);
+  if (gt == KAON_F32 && pt == KAON_BF16) return pd1_by_codec<KAON_F32, KAON_BF16>(codec);
+  if (gt == KAON_F32 && pt == KAON_F32) return pd1_by_codec<KAON_F32, KAON_F32>(codec);
+  return nullptr;
+}
+PdStatsFn pd_stats_fn(int pt, int gt) {
+  if (gt == KAON_BF16 && pt == KAON_BF16) return k_pd_stats<KAON_BF16, KAON_BF16>;
+  if (gt == KAON_BF16 && pt == KAON_F32) return k_pd_stats<KAON_BF16, KAON_F32>;
+  if (gt == KAON_F32 && pt == KAON_BF16) return k_pd_stats<KAON_F32, KAON_BF16>;
+  if (gt == KAON_F32 && pt == KAON_F32) return k_pd_stats<KAON_F32, KAON_F32>;
+  return nullptr;
+}
+template <int PHASE, int PT, int GT>
+PdFn pd2_by_codec(int codec) {
+  switch (codec) {
+    case KAON_MOM_NONE: return k_pd2<PHASE, PT, GT, KAON_MOM_NONE>;
+    case KAON_MOM_F32: return k_pd2<PHASE, PT, GT, KAON_MOM_F32>;
+    case KAON_MOM_BF16: return k_pd2<PHASE, PT, GT, KAON_MOM_BF16>;
+    case KAON_MOM_INT8: return k_pd2<PHASE, PT, GT, KAON_MOM_INT8>;
+    case KAON_MOM_4BIT: return k_pd2<PHASE, PT, GT, KAON_MOM_4BIT>;
+  }
+  return nullptr;
+}
+template <int PHASE>
+PdFn pd2_fn(int pt, int gt, int codec) {
+  if (pt == KAON_BF16 && gt == KAON_BF16) return pd2_by_codec<PHASE, KAON_BF16, KAON_BF16>(codec);
+  if (pt == KAON_BF16 && gt == KAON_F32) return pd2_by_codec<PHASE, KAON_BF16, KAON_F32>(codec);
+  if (pt == KAON_F32 && gt == KAON_BF16) return pd2_by_codec<PHASE, KAON_F32, KAON_BF16>(codec);
+  if (pt == KAON_F32 && gt == KAON_F32) return pd2_by_codec<PHASE, KAON_F32, KAON_F32>(codec);
+  return nullptr;
+}
+
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who) {
   if (!L || !hp) return fail(who);
   if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16) return fail("kaon: bad p_dtype");
@@ -2659,6 +3085,59 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
 
 int kaon_adapnm_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   return kaon_adapnm_phases(L, hp, 0x7Eu, stream);
+}
+
+int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  int rc = validate(L, hp, "kaon_kprodigy_pass1: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  Ws ws{(float*)L->workspace};
+  KaonHyper h = *hp;
+  const bool mom = (h.flags & KAON_F_MOMENTUM) && h.codec != KAON_MOM_NONE;
+  const int codec = mom ? h.codec : KAON_MOM_NONE;
+  h.codec = codec;
+  h.flags &= ~(KAON_F_NK_REMOVE | KAON_F_NK_CLIMB | KAON_F_SRC_O | KAON_F_PNM);
+  PdFn f1 = pd1_fn(h.p_dtype, h.g_dtype, codec);
+  PdStatsFn fs = pd_stats_fn(h.p_dtype, h.g_dtype);
+  if (!f1 || !fs) return fail("kaon_kprodigy_pass1: unsupported dtype / codec combination");
+  hipLaunchKernelGGL(k_pd_zero, dim3(L->n_tensors), dim3(KAON_WG), 0, st, L->descs, ws, codec);
+  if ((rc = check_launch("kaon: KProdigy zero launch"))) return rc;
+  // the factored row/col EMAs (tensors with a per-element v return at once)
+  if ((rc = launch_stats(*L, ws, h, 0, st))) return rc;
+  if (L->n_fin_items > 0) {
+    hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
+    if ((rc = check_launch("kaon: k_fin launch"))) return rc;
+  }
+  hipLaunchKernelGGL(f1, dim3(L->n_row_items), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
+  if ((rc = check_launch("kaon: KProdigy pass-1 launch"))) return rc;
+  if ((h.flags & KAON_F_PD_STATS) && L->n_flat_items > 0) {
+    hipLaunchKernelGGL(fs, dim3((L->n_flat_items + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->flat_items,
+                       L->n_flat_items, ws, h);
+    hipLaunchKernelGGL(k_pd_sfin, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
+    if ((rc = check_launch("kaon: KProdigy statistics launch"))) return rc;
+  }
+  return 0;
+}
+
+int kaon_kprodigy_pass2(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  int rc = validate(L, hp, "kaon_kprodigy_pass2: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0 || L->n_elem_items <= 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  Ws ws{(float*)L->workspace};
+  KaonHyper h = *hp;
+  const bool mom = (h.flags & KAON_F_MOMENTUM) && h.codec != KAON_MOM_NONE;
+  const int codec = mom ? h.codec : KAON_MOM_NONE;
+  h.codec = codec;
+  PdFn f5 = pd2_fn<5>(h.p_dtype, h.g_dtype, codec), f6 = pd2_fn<6>(h.p_dtype, h.g_dtype, codec);
+  if (!f5 || !f6) return fail("kaon_kprodigy_pass2: unsupported dtype / codec combination");
+  if (h.flags & KAON_F_CAUTIOUS) {
+    hipLaunchKernelGGL(f5, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
+    if ((rc = check_launch("kaon: KProdigy keep-count launch"))) return rc;
+  }
+  hipLaunchKernelGGL(f6, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
+  return check_launch("kaon: KProdigy apply launch");
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {

@@ -53,6 +53,11 @@ class Plan:
             d.row, d.col, d.v = _ptr(e.get("row")), _ptr(e.get("col")), _ptr(e.get("v"))
             d.shift = _ptr(e.get("shift"))
             d.m2, d.m2_scale, d.max_v = _ptr(e.get("m2")), _ptr(e.get("m2_scale")), _ptr(e.get("max_v"))
+            if e.get("pd_s") is not None:
+                d.pd_s, d.pd_p0 = _ptr(e["pd_s"]), _ptr(e["pd_p0"])
+                d.pd_ns, d.pd_slice = e["pd_s"].numel(), int(e["pd_slice"])
+                d.pd_p0_scalar = 1 if e["pd_p0"].dim() == 0 else 0
+                d.full_v = 1 if e.get("full_v") else 0
             noise = e.get("noise") or (None, None, None)
             for s in range(3):
                 d.noise[s] = _ptr(noise[s])

@@ -12,17 +12,17 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, BF16 = 0, 1
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
 MOM_CODE = {"none": MOM_NONE, "float32": MOM_F32, "bfloat16": MOM_BF16, "int8": MOM_INT8, "4bit": MOM_4BIT}
 SR, RN, KAHAN = 0, 1, 2
 BF16_METHOD = {"stochastic_rounding": SR, "none": RN, "kahan": KAHAN}
-OPT_ADAKAON, OPT_LION, OPT_ADAMUON, OPT_ADAPNM = 0, 1, 2, 3
+OPT_ADAKAON, OPT_LION, OPT_ADAMUON, OPT_ADAPNM, OPT_KPRODIGY = 0, 1, 2, 3, 4
 
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB, F_SRC_O = 1, 2, 4, 8, 16, 32, 64, 128
-F_PNM, F_AMS = 256, 512
+F_PNM, F_AMS, F_PD_COUPLED, F_PD_STATS = 256, 512, 1024, 2048
 
 ROW_BUDGET = 20
 ROW_CLASSES = 7
@@ -38,6 +38,9 @@ class KaonTensor(ctypes.Structure):
         ("m_scale", ctypes.c_void_p), ("row", ctypes.c_void_p), ("col", ctypes.c_void_p),
         ("v", ctypes.c_void_p), ("shift", ctypes.c_void_p),
         ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
+        ("pd_s", ctypes.c_void_p), ("pd_p0", ctypes.c_void_p), ("pd_ns", ctypes.c_int64),
+        ("pd_slice", ctypes.c_int32), ("pd_p0_scalar", ctypes.c_int32), ("full_v", ctypes.c_int32),
+        ("pd_pad", ctypes.c_int32),
         ("noise", ctypes.c_void_p * 3),
         ("R", ctypes.c_int64), ("C", ctypes.c_int64), ("n", ctypes.c_int64),
         ("ws_row", ctypes.c_int64), ("ws_col", ctypes.c_int64), ("ws_part", ctypes.c_int64),
@@ -86,15 +89,19 @@ class KaonHyper(ctypes.Structure):
         ("nk_bound_old", ctypes.c_float), ("nk_bound_new", ctypes.c_float),
         ("pn_pos", ctypes.c_float), ("pn_neg", ctypes.c_float), ("pn_rnorm", ctypes.c_float),
         ("bc2", ctypes.c_float),
+        ("pd_tg", ctypes.c_float), ("pd_vval", ctypes.c_float), ("pd_alpha_s", ctypes.c_float),
+        ("pd_beta3", ctypes.c_float), ("pd_d", ctypes.c_float), ("pd_dn", ctypes.c_float),
+        ("pd_floor", ctypes.c_float),
+        ("pd_cap", ctypes.c_float), ("pd_dlr", ctypes.c_float), ("pd_wdl", ctypes.c_float),
         ("flags", ctypes.c_int32), ("p_dtype", ctypes.c_int32), ("g_dtype", ctypes.c_int32),
         ("codec", ctypes.c_int32), ("bf16_method", ctypes.c_int32), ("ns_steps", ctypes.c_int32),
         ("step", ctypes.c_uint32), ("seed", ctypes.c_uint64),
     ]
 
 
-assert ctypes.sizeof(KaonTensor) == 232, ctypes.sizeof(KaonTensor)
+assert ctypes.sizeof(KaonTensor) == 272, ctypes.sizeof(KaonTensor)
 assert ctypes.sizeof(KaonItem) == 16
-assert ctypes.sizeof(KaonHyper) == 104, ctypes.sizeof(KaonHyper)
+assert ctypes.sizeof(KaonHyper) == 144, ctypes.sizeof(KaonHyper)
 
 # entry points: name -> (argtypes, restype)
 _VP, _I32, _I64, _U32, _U64, _F = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32,
@@ -108,6 +115,8 @@ SIGNATURES = {
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adamuon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adapnm_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
+    "kaon_kprodigy_pass1": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
+    "kaon_kprodigy_pass2": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adakaon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_lion_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_adamuon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),

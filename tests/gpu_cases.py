@@ -22,7 +22,7 @@ def tdtype(name: str) -> torch.dtype:
 
 
 def make_opt(case, params, group=None):
-    from kaon_amd import AdaMuon, AdaPNM, Adakaon, Lion, Nekaon
+    from kaon_amd import AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
 
     g = dict(group or group_for(case))
     name = case["opt"]
@@ -44,6 +44,13 @@ def make_opt(case, params, group=None):
     elif name == "adamuon":
         opt = AdaMuon(params, lr=g["lr"], betas=g["betas"], eps=g["eps"], weight_decay=g["weight_decay"],
                       ns_steps=g["ns_steps"], clip_threshold=g["clip_threshold"], **common)
+        opt.sr_seed = case["seed"]
+    elif name == "kprodigy":
+        kw = {k: g[k] for k in ("lr", "betas", "beta3", "eps", "weight_decay", "decouple", "use_bias_correction",
+                                "safeguard_warmup", "d0", "d_coef", "growth_rate", "d_update_freq", "slice_p",
+                                "momentum_dtype", "momentum_4bit_block", "second_moment", "eps_factored", "cautious",
+                                "gradient_centralization", "bf16_method")}
+        opt = KProdigy(params, **kw)
         opt.sr_seed = case["seed"]
     elif name == "adapnm":
         opt = AdaPNM(params, lr=g["lr"], betas=g["betas"], beta0=g["beta0"], eps=g["eps"],
@@ -101,7 +108,9 @@ def assert_same_as_oracle(case, oparams, params, opt, evalp=None, oeval=None, la
         assert nbad == 0, f"{label} param {i} {tuple(p.shape)}: {nbad}/{got.size} weights differ"
         st = state_of(opt, p)
         for k, ov in op.state.items():
-            if k.endswith("_numel") or k.endswith("_block"):  # the 4-bit codec's ints
+            if k.startswith("_"):  # the oracle's own scratch
+                continue
+            if k.endswith("_numel") or k.endswith("_block") or k == "step":  # ints
                 assert int(st[k]) == int(ov), (label, i, k)
                 continue
             gv = to_bits(st[k]).reshape(-1)

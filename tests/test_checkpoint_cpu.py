@@ -3,7 +3,7 @@
 The golden fixtures hold the reference's own state after its steps
 (tests/golden/make_golden.py ran kaon 0.7.4): per param the keys, dtypes and
 shapes of ``optimizer.state`` (adakaon.py:318-335, lion.py:210-241,
-adapnm.py:451-500, _momentum_codec.py:253-406).  These tests check that
+adapnm.py:451-500, kprodigy.py:262-291, _momentum_codec.py:253-406).  These tests check that
 
 * kaon_amd's fresh state has the reference's keys and dtypes, and its shapes
   except where the reference's own two paths differ (the 1-D int8 scales:
@@ -26,7 +26,7 @@ from cases import CASES, grad_values, param_values
 from golden_compare import load_golden
 from gpu_cases import make_opt
 
-INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion", "adapnm")]
+INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion", "adapnm", "kprodigy")]
 
 
 def _tdt(name):
@@ -54,7 +54,7 @@ def _golden_state(gold, i):
         if not k.startswith(pre):
             continue
         key = k[len(pre):]
-        if key.endswith("_numel") or key.endswith("_block"):  # the 4-bit codec's ints
+        if key.endswith("_numel") or key.endswith("_block") or key == "step":  # ints
             out[key] = int(a)
         elif a.dtype == np.uint16:  # bf16 bits
             out[key] = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
@@ -85,6 +85,9 @@ def test_fresh_state_has_the_reference_layout(name):
         st = opt.state[p]
         assert sorted(st) == sorted(ref), (name, i, sorted(st), sorted(ref))
         for k, v in ref.items():
+            if k == "step":  # KProdigy's per-param step count: an int, 0 when fresh
+                assert isinstance(st[k], int) and st[k] == 0, (name, i, k)
+                continue
             if not torch.is_tensor(v):
                 assert int(st[k]) == v, (name, i, k)
                 continue

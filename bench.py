@@ -59,6 +59,17 @@ WORKLOADS = {
                              "cautious, GC, SR bf16, lr 1e-4", opt="adapnm",
                         kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="bfloat16"), bm=2.0,
                         b_neg=2.0),
+    # KProdigy (src/kaon/kprodigy.py, SURVEY's next row 4): two passes around a cross-tensor D
+    # estimate; b_extra = the fp32 v (read + write) and the sliced s (read + write) and p0 (read)
+    "kprodigy_bf16": dict(desc="KProdigy defaults: lr 1.0, d0 1e-6, betas=(0.9,0.999), bf16 momentum, full fp32 "
+                               "second moment, slice_p 1, GC, SR bf16", opt="kprodigy",
+                          kw=dict(lr=1.0, betas=(0.9, 0.999), momentum_dtype="bfloat16"), bm=2.0,
+                          b_extra=8.0 + 12.0, pd_slice=1, pd_full_v=True),
+    "kprodigy_int8_factored": dict(desc="KProdigy memory-lean: lr 1.0, int8 momentum, factored second moment, "
+                                        "slice_p 11, GC, SR bf16", opt="kprodigy",
+                                   kw=dict(lr=1.0, betas=(0.9, 0.999), momentum_dtype="int8",
+                                           second_moment="factored", slice_p=11), bm=1.0,
+                                   b_extra=12.0 / 11.0, pd_slice=11, pd_full_v=False),
     # the launch-bound regime: the reference's LoRA proxy bag (benchmarks/proxy/harness.py:117-127:
     # 512 tensors [8, 16], fp32) stepped by Adakaon with bf16 momentum, the configuration its
     # control ranking lists as "Adakaon-bf16-fused" (benchmarks/control/RANKINGS.md:83)
@@ -71,10 +82,16 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 # algorithmic HBM bytes per param of each phase kernel (bf16 g/p, b_m momentum bytes)
 PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor", 5: "keep_count", 6: "apply",
-               8: "momentum", 9: "newton_schulz"}
+               8: "momentum", 9: "newton_schulz", 11: "pass1_moments_and_d_stats", 12: "pass2_update"}
 
 
-def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon") -> float:
+def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict | None = None) -> float:
+    if opt == "kprodigy":
+        # pass 1: g, m (read + write), v (read + write) and the sliced s (r + w), p0, p;
+        # pass 2: g, m, v, p (read + write)
+        full = 1.0 if w and w.get("pd_full_v") else 0.0
+        sl = (w or {}).get("pd_slice", 1)
+        return {11: 2.0 + 2.0 * bm + 8.0 * full + 14.0 / sl, 12: 2.0 + bm + 4.0 * full + 4.0}.get(phase, 0.0)
     if opt == "adapnm":
         # both momenta are read by the clip-sum, keep-count and apply passes
         return {1: 2.0, 3: 2.0 + 2.0 * bm, 5: 2.0 + 2.0 * bm, 6: 6.0 + 3.0 * bm}.get(phase, 0.0)
@@ -105,11 +122,13 @@ def measured_traffic(workload: str, phase: int) -> float | None:
 
 
 def make_opt(name, params):
-    from kaon_amd import AdaMuon, AdaPNM, Adakaon, Lion, Nekaon
+    from kaon_amd import AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
 
     w = WORKLOADS[name]
     if w["opt"] == "adapnm":
         return AdaPNM(params, **w["kw"])
+    if w["opt"] == "kprodigy":
+        return KProdigy(params, **w["kw"])
     if w["opt"] == "adakaon":
         return Adakaon(params, **w["kw"])
     if w["opt"] == "lion":
@@ -168,6 +187,25 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
     for key, (_ptrs, plan) in inner._plans.items():
         gid, pdt, gdt = key[:3]
         group = inner.param_groups[gid]
+        if WORKLOADS[name]["opt"] == "kprodigy":
+            # the two passes with the group's current d (the host D update between them is a
+            # fold of two floats per tensor)
+            import math as _m
+            d = group["d"]
+            c = {"d": d, "dlr": d * group["lr"], "beta3": _m.sqrt(group["betas"][1]), "should_update_d": True,
+                 "alpha_s": d * group["lr"] * d / group["d0"], "d_new": d}
+            hp = inner._hyper(group, pdt, gdt, c)
+            s = torch.cuda.current_stream().cuda_stream
+            for r in range(reps):
+                for ph, fn in ((11, lib.kaon_kprodigy_pass1), (12, lib.kaon_kprodigy_pass2)):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    _lib.check(fn(ctypes.byref(plan.launch), ctypes.byref(hp), s), "pass")
+                    e1.record()
+                    torch.cuda.synchronize()
+                    acc = out.setdefault(ph, [0.0] * reps)
+                    acc[r] += e0.elapsed_time(e1)
+            continue
         if WORKLOADS[name]["opt"] == "adamuon":
             if key[3] != 2:
                 continue  # the 1-D params' Adakaon plan: a few microseconds
@@ -216,6 +254,12 @@ def cpu_baseline(params, name, seconds: float) -> dict:
                  ns_steps=kw.get("ns_steps", 2))
     if w["opt"] == "adapnm":
         group.update(eps=1e-8, beta0=kw["beta0"], ams_bound=False)
+    if w["opt"] == "kprodigy":
+        group.update(beta3=None, eps=1e-8, decouple=True, use_bias_correction=False, safeguard_warmup=False,
+                     d=1e-6, d0=1e-6, d_max=1e-6, d_numerator=0.0, d_coef=1.0, growth_rate=float("inf"),
+                     d_update_freq=1, slice_p=kw.get("slice_p", 1), k=0,
+                     second_moment=kw.get("second_moment", "full"), eps_factored=1e-30, cautious=False,
+                     factor_conv_as_matrix=True)
     order = np.random.default_rng(0).permutation(len(params))
     if w["opt"] == "adamuon":
         # the oracle's scalar GEMMs take minutes on a 1280 x 11520 matrix: sample the
@@ -291,7 +335,7 @@ def main() -> int:
     gps = nparam / (ms * 1e-3) / 1e9
     bm = w["bm"]
     eb = 4.0 if pdt == torch.float32 else 2.0   # param and grad element bytes
-    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0)
+    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0) + w.get("b_extra", 0.0)
     step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
     print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
           file=sys.stderr, flush=True)
@@ -336,7 +380,7 @@ def main() -> int:
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
                                "avg_ms": round(br[dom], 4)}
         else:
-            bpp = phase_bytes(dom, bm, wd, w["opt"])
+            bpp = phase_bytes(dom, bm, wd, w["opt"], w)
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
             out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),

@@ -329,6 +329,15 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
 int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, float bound,
                     uint32_t stream_id, void* stream);
 
+/* Each tensor's sum of squares of its dequantized momentum into its scalar word
+ * 2 of the workspace (rows in the 64-lane order, then the rows in that order),
+ * for MSAM norm="global", whose climb is rho * m / (||m|| + eps) with ||m|| over
+ * every momentum of the net (_global_mnorm, msam.py:191-199; the caller adds
+ * the tensors in param order in fp32 and takes the fp32 square root).  The
+ * climb and its removal then run through kaon_msam_apply with that factor and
+ * an infinite bound. */
+int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
 /* ---------------------------------------------------------- primitives */
 /* _quant_int8 (_momentum_codec.py:72-83): rows x cols fp32 -> int8 codes +
  * per-row scale (rows = 1 for a 1-D tensor). */

@@ -171,7 +171,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       return plan_fail("kaon_plan: AdaPNM tensor " + std::to_string(i) + " needs both momentum buffers (m, m2)");
     const bool al = aligned(t.g, 16) && aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) &&
                     aligned(t.shift, 16) && aligned(t.row, 16) && aligned(t.col, 16) && aligned(t.m2, 16) &&
-                    aligned(t.max_v, 16);
+                    aligned(t.max_v, 16) && aligned(t.pd_s, 16) && (t.pd_p0_scalar || aligned(t.pd_p0, 16));
     t.vec_flat = al ? 1 : 0;
     t.vec_rows = (al && (t.C % 8 == 0 || t.R == 1)) ? 1 : 0;
     // workspace: 4-word aligned arrays

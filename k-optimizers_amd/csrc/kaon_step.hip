@@ -1695,6 +1695,64 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
   }
 }
 
+// =============================================================== MSAM norm="global"
+// Sum of squares of the dequantized momentum (_global_mnorm, msam.py:191-199):
+// each row in the 64-lane order into rs[r] (a 1-D tensor is one row); k_msq_fin
+// adds the rows in the 64-lane order into the tensor's scalar word 2.
+template <int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_msq(const KaonTensor* __restrict__ D,
+                                                 const KaonItem* __restrict__ items, Ws ws) {
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
+  const KaonTensor& T = D[it.tensor];
+  const int64_t C = T.C;
+  const int64_t nch = (C + 7) >> 3;
+  const int cpl = (int)((nch + 63) >> 6);
+  const bool vec = T.vec_rows != 0;
+  const WaveRows wr = wave_rows(it);
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float sc = CODEC == KAON_MOM_INT8 ? uniform_f(G(T.m_scale)[T.factored ? r : 0]) : 1.0f;
+    float a = 0.0f;
+    for (int k = 0; k < cpl; ++k) {
+      const int64_t c = wr.lane + 64 * k;
+      const int cnt = chunk_cnt(c, C);
+      if (cnt <= 0) continue;
+      const int64_t e0 = r * C + c * 8;
+      uint32_t mq[8];
+      ld_mom_at<CODEC>(T.m, e0, cnt, vec && cnt == 8, mq);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i >= cnt) continue;
+        float m;
+        if (CODEC == KAON_MOM_INT8) m = (float)(int8_t)(uint8_t)mq[i] * sc;
+        else if (CODEC == KAON_MOM_4BIT) m = ((float)mq[i] - 8.0f) * G(T.m_scale)[(e0 + i) / T.block4];
+        else if (CODEC == KAON_MOM_BF16) m = bf2f(mq[i]);
+        else m = __uint_as_float(mq[i]);
+        a = a + m * m;
+      }
+    }
+    const float s = wave_csum(a);
+    if (wr.lane == 0) ws.rs(T)[r] = s;
+  }
+}
+
+__global__ __launch_bounds__(KAON_WG) void k_msq_fin(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
+  const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (t >= n_tensors) return;
+  const KaonTensor& T = D[t];
+  const int lane = threadIdx.x & 63;
+  const int64_t R = T.n > 0 ? T.R : 0;
+  const KAON_G float* rs = ws.rs(T);
+  float a = 0.0f;
+  for (int64_t c = lane; c * 8 < R; c += 64)
+    for (int i = 0; i < 8; ++i)
+      if (c * 8 + i < R) a = a + rs[c * 8 + i];
+  const float ss = wave_csum(a);
+  if (lane == 0) ws.scal(T)[2] = ss;
+}
+
 // =============================================================== KProdigy
 // The two passes of KProdigy (src/kaon/kprodigy.py).  Pass 1 sees the gradient
 // g' = GC(g), plus wd * p when the decay is coupled (_collect_grad, :342-349);
@@ -1848,23 +1906,52 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
   KAON_G float* sv = G(T.pd_s);
   float an = 0.0f, ad = 0.0f;
   const int64_t nch = (len + 7) >> 3;
-  for (int64_t c = lane; c < nch; c += 64) {
-    for (int i = 0; i < 8; ++i) {
-      const int64_t jj = c * 8 + i;
-      if (jj >= len) break;
-      const int64_t j = j0 + jj, e = j * sp;
-      float gv, pv;
-      if (GT == KAON_BF16) gv = bf2f(G((const uint16_t*)T.g)[e]);
-      else gv = G((const float*)T.g)[e];
-      if (PT == KAON_BF16) pv = bf2f(G((const uint16_t*)T.p)[e]);
-      else pv = G((const float*)T.p)[e];
-      if (gc) gv = round_to<GT>(gv - ws.mu(T)[e / C]);
-      if (coupled) gv = __fmaf_rn(hp.wdl, pv, gv);
-      const float pz = T.pd_p0_scalar ? p0[0] : p0[j];
-      an = an + gv * (pz - pv);
-      const float snew = __fmaf_rn(hp.pd_alpha_s, gv, sv[j] * hp.pd_beta3);
-      sv[j] = snew;
-      ad = ad + fabsf(snew);
+  if (sp == 1) {
+    // contiguous: 16-byte accesses for whole chunks (j0 and the chunks are 8-aligned)
+    const bool vec = T.vec_flat != 0;
+    for (int64_t c = lane; c < nch; c += 64) {
+      const int64_t jj = c * 8, j = j0 + jj;
+      const int cnt = (int)min<int64_t>(8, len - jj);
+      const bool vv = vec && cnt == 8;
+      float g[8], p[8], z[8], sc[8];
+      ld8<GT>(T.g, j, cnt, vv, g);
+      ld8<PT>(T.p, j, cnt, vv, p);
+      ld8<KAON_F32>(T.pd_s, j, cnt, vv, sc);
+      if (!T.pd_p0_scalar) ld8<KAON_F32>(T.pd_p0, j, cnt, vv, z);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) z[i] = p0[0];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i >= cnt) continue;
+        float gv = g[i];
+        if (gc) gv = round_to<GT>(gv - ws.mu(T)[(j + i) / C]);
+        if (coupled) gv = __fmaf_rn(hp.wdl, p[i], gv);
+        an = an + gv * (z[i] - p[i]);
+        sc[i] = __fmaf_rn(hp.pd_alpha_s, gv, sc[i] * hp.pd_beta3);
+        ad = ad + fabsf(sc[i]);
+      }
+      st8_f32(T.pd_s, j, cnt, vv, sc);
+    }
+  } else {
+    for (int64_t c = lane; c < nch; c += 64) {
+      for (int i = 0; i < 8; ++i) {
+        const int64_t jj = c * 8 + i;
+        if (jj >= len) break;
+        const int64_t j = j0 + jj, e = j * sp;
+        float gv, pv;
+        if (GT == KAON_BF16) gv = bf2f(G((const uint16_t*)T.g)[e]);
+        else gv = G((const float*)T.g)[e];
+        if (PT == KAON_BF16) pv = bf2f(G((const uint16_t*)T.p)[e]);
+        else pv = G((const float*)T.p)[e];
+        if (gc) gv = round_to<GT>(gv - ws.mu(T)[e / C]);
+        if (coupled) gv = __fmaf_rn(hp.wdl, pv, gv);
+        const float pz = T.pd_p0_scalar ? p0[0] : p0[j];
+        an = an + gv * (pz - pv);
+        const float snew = __fmaf_rn(hp.pd_alpha_s, gv, sv[j] * hp.pd_beta3);
+        sv[j] = snew;
+        ad = ad + fabsf(snew);
+      }
     }
   }
   const float num = wave_csum(an), den = wave_csum(ad);
@@ -3085,6 +3172,27 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
 
 int kaon_adapnm_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   return kaon_adapnm_phases(L, hp, 0x7Eu, stream);
+}
+
+int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  int rc = validate(L, hp, "kaon_momentum_sumsq: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  Ws ws{(float*)L->workspace};
+  using MsqFn = void (*)(const KaonTensor*, const KaonItem*, Ws);
+  MsqFn f = nullptr;
+  switch (hp->codec) {
+    case KAON_MOM_F32: f = k_msq<KAON_MOM_F32>; break;
+    case KAON_MOM_BF16: f = k_msq<KAON_MOM_BF16>; break;
+    case KAON_MOM_INT8: f = k_msq<KAON_MOM_INT8>; break;
+    case KAON_MOM_4BIT: f = k_msq<KAON_MOM_4BIT>; break;
+  }
+  if (!f) return fail("kaon_momentum_sumsq: needs a momentum codec");
+  if (L->n_row_items > 0)
+    hipLaunchKernelGGL(f, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws);
+  hipLaunchKernelGGL(k_msq_fin, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
+  return check_launch("kaon: momentum sum-of-squares launch");
 }
 
 int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) {

@@ -2,7 +2,7 @@
 
 Drop-in classes with the reference ``kaon`` API (constructors, ``step()``,
 ``state_dict`` layout, ``momentum_dtype`` / ``bf16_method`` knobs):
-``Adakaon``, ``Lion``, ``Nekaon``, ``AdaMuon``, ``AdaPNM``, ``KProdigy``.  Every step runs hand-written HIP kernels
+``Adakaon``, ``Lion``, ``Nekaon``, ``AdaMuon``, ``AdaPNM``, ``KProdigy``, ``MSAM``.  Every step runs hand-written HIP kernels
 from ``libkaon_amd.so`` (C ABI in ``include/kaon_amd.h``); importing this
 package does not load the library, the first step does, and fails loudly if it
 has not been built.
@@ -13,7 +13,8 @@ from .adamuon import AdaMuon
 from .adapnm import AdaPNM
 from .kprodigy import KProdigy
 from .lion import Lion
+from .msam import MSAM
 from .nekaon import Nekaon
 
 __version__ = "0.1.0"
-__all__ = ["AdaMuon", "AdaPNM", "Adakaon", "KProdigy", "Lion", "Nekaon", "fourbit_block_size", "load_state_dict_preserving_dtypes"]
+__all__ = ["AdaMuon", "AdaPNM", "Adakaon", "KProdigy", "MSAM", "Lion", "Nekaon", "fourbit_block_size", "load_state_dict_preserving_dtypes"]

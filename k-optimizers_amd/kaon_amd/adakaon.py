@@ -119,7 +119,7 @@ class Adakaon(KaonOptimizer):
             if nk["remove"] and gid in nk["bound_old"]:
                 flags |= L.F_NK_REMOVE
                 h.nk_bound_old = nk["bound_old"][gid]
-            if nk["k"] != 0.0:
+            if nk["k"] != 0.0 and nk.get("climb", True):
                 flags |= L.F_NK_CLIMB
                 bound = abs(nk["k"]) * group.get("clip_threshold", 1.0) * lr
                 h.nk_bound_new = bound

@@ -1,0 +1,236 @@
+"""MSAM (Momentum-SAM) over a kaon_amd optimizer on the MI355X HIP step.
+
+Reference: src/kaon/msam.py:73-421.  Each step removes the previous climb,
+runs the inner step at the true weights, and climbs along the refreshed
+momentum for the next forward/backward:
+
+* ``norm="global"`` (the default): ``e = rho * m / (||m|| + eps)`` with ``||m||``
+  over every momentum of the net (``_global_mnorm``, :191-199) -- a
+  cross-tensor reduction between the inner step and the climb
+  (``kaon_momentum_sumsq``, the tensors added in param order in fp32);
+* ``norm="none"``: ``e = clamp(nan_to_num(rho * m), +-|rho| * clip * lr)`` with the
+  bound frozen at climb time (:169-188, Nekaon's form).
+
+Over a plain :class:`Adakaon` the removal (and for ``norm="none"`` the climb)
+is folded into the Adakaon apply pass, as three stochastic roundings of one
+register value (SR noise streams 0, 1, 2); over any other kaon_amd optimizer
+with a momentum buffer they are separate ``kaon_msam_apply`` passes, as in the
+reference.  ``norm="tensor"`` is not part of this build (it raises).  In the
+global norm a NaN momentum coordinate contributes no climb (the reference
+would carry the NaN into the weights).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from collections import defaultdict
+from typing import Any, Iterable
+
+import numpy as np
+import torch
+
+from . import _engine as E
+from . import _lib as L
+from .adakaon import Adakaon
+
+
+def _ptr_or0(t: torch.Tensor | None) -> int:
+    return t.data_ptr() if t is not None else 0
+
+
+class MSAM(torch.optim.Optimizer):
+    def __init__(
+        self,
+        params: Iterable[Any],
+        base_optimizer: type | None = None,
+        rho: float = 0.3,
+        norm: str = "global",
+        eps: float = 1e-12,
+        **kwargs: Any,
+    ) -> None:
+        if eps < 0.0:
+            raise ValueError(f"eps must be >= 0, got {eps}")
+        if norm not in ("global", "tensor", "none"):
+            raise ValueError(f"norm must be 'global', 'tensor' or 'none', got {norm!r}")
+        if norm == "tensor":
+            raise NotImplementedError("kaon_amd: MSAM norm='tensor' is not part of this build")
+        base = Adakaon if base_optimizer is None else base_optimizer
+        inner = base(params, **kwargs)
+        super().__init__([p for g in inner.param_groups for p in g["params"]], dict(inner.defaults))
+        self.inner = inner
+        self.base_optimizer = inner
+        self.param_groups = self.inner.param_groups
+        self.defaults = self.inner.defaults
+        self.state = defaultdict(dict)   # no per-param state of its own
+        self.rho = float(rho)
+        self.norm = norm
+        self.eps = float(eps)
+        self._train_mode = True
+        self._has_e = False
+        self._mnorm = 0.0
+        self._eclamp: dict[int, float] = {}
+        self._fused = type(inner) is Adakaon
+        self._mplans: dict[tuple, tuple[tuple, E.Plan, list[int], torch.Tensor]] = {}
+
+    # ---------------------------------------------------------------- plans
+    def _momentum_plans(self) -> list[tuple[int, int, E.Plan, list[int], torch.Tensor]]:
+        """(gid, p dtype, plan, param positions, stat word index) over the params with a
+        momentum buffer, cached while the param and state pointers hold."""
+        tids = self.inner._tensor_ids()
+        by_key: dict[tuple[int, int], list[torch.Tensor]] = {}
+        for gid, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                st = self.inner.state.get(p)
+                if st and "m" in st:
+                    by_key.setdefault((gid, E.dtype_code(p.dtype)), []).append(p)
+        out = []
+        for (gid, pdt), plist in by_key.items():
+            ptrs = tuple((p.data_ptr(), self.inner.state[p]["m"].data_ptr(),
+                          _ptr_or0(self.inner.state[p].get("m_scale")),
+                          tuple(_ptr_or0(t) for t in (self.inner._inject_noise.get(p) or ())))
+                         for p in plist)
+            hit = self._mplans.get((gid, pdt))
+            if hit is None or hit[0] != ptrs:
+                entries = []
+                for p in plist:
+                    st = self.inner.state[p]
+                    R, C, fac = E.matrixized(p)
+                    entries.append(dict(p=p, g=p, R=R, C=C, factored=fac, tensor_id=tids[id(p)], m=st["m"],
+                                        m_scale=st.get("m_scale"), block4=st.get("m_block", 0),
+                                        noise=self.inner._inject_noise.get(p)))
+                group = self.param_groups[gid]
+                plan = E.Plan(L.OPT_ADAKAON, L.MOM_CODE[group["momentum_dtype"]], entries, plist[0].device, pdt,
+                              pdt)
+                idx = torch.tensor([plan.descs[i].ws_scal + 2 for i in range(len(plist))], dtype=torch.int64,
+                                   device=plist[0].device)
+                hit = (ptrs, plan, [tids[id(p)] for p in plist], idx)
+                self._mplans[(gid, pdt)] = hit
+            out.append((gid, pdt, hit[1], hit[2], hit[3]))
+        return out
+
+    def _hyper(self, gid: int, pdt: int, step: int | None = None) -> L.KaonHyper:
+        h = L.KaonHyper()
+        h.p_dtype = h.g_dtype = pdt
+        h.codec = L.MOM_CODE[self.param_groups[gid]["momentum_dtype"]]
+        h.step = (self.inner._t if step is None else step) & 0xFFFFFFFF
+        h.seed = self.inner.sr_seed
+        return h
+
+    # ---------------------------------------------------------- perturbation
+    @torch.no_grad()
+    def _global_mnorm(self) -> float:
+        """||m|| over every momentum: per-tensor sums of squares on the GPU, added in
+        param order in fp32, fp32 square root (msam.py:191-199)."""
+        lib = L.lib()
+        rows = []
+        for gid, pdt, plan, tids, idx in self._momentum_plans():
+            dev = plan.workspace.device
+            L.check(lib.kaon_momentum_sumsq(ctypes.byref(plan.launch), ctypes.byref(self._hyper(gid, pdt)),
+                                            E.stream_handle(dev)), "kaon_momentum_sumsq")
+            vals = plan.workspace.index_select(0, idx).cpu().numpy()
+            rows += list(zip(tids, vals))
+        rows.sort(key=lambda x: x[0])
+        sq = np.float32(0.0)
+        for _t, v in rows:
+            sq = np.float32(sq + np.float32(v))
+        return float(np.sqrt(sq, dtype=np.float32))
+
+    @torch.no_grad()
+    def _apply(self, sign: float, step: int | None = None) -> None:
+        """Add the perturbation sign * e to every weight with a momentum (msam.py:202-235).
+        The SR noise is keyed on ``step`` (default: the inner step count) and stream 0
+        for a removal, 2 for a climb."""
+        lib = L.lib()
+        sid = 0 if sign < 0 else 2
+        for gid, pdt, plan, _tids, _idx in self._momentum_plans():
+            group = self.param_groups[gid]
+            if self.norm == "global":
+                factor, bound = sign * self.rho / (self._mnorm + self.eps), math.inf
+            else:
+                if sign > 0 and gid not in self._eclamp:
+                    self._eclamp[gid] = abs(self.rho) * group.get("clip_threshold", 1.0) * group["lr"]
+                factor, bound = sign * self.rho, self._eclamp.get(gid, 0.0)
+            h = self._hyper(gid, pdt, step)
+            L.check(lib.kaon_msam_apply(ctypes.byref(plan.launch), ctypes.byref(h), factor, bound, sid,
+                                        E.stream_handle(plan.workspace.device)), "kaon_msam_apply")
+
+    # ---------------------------------------------------------------- step
+    @torch.no_grad()
+    def step(self, closure: Any = None) -> Any:
+        if not self._train_mode:
+            raise RuntimeError(
+                "MSAM.step() called outside train mode. Call optimizer.train() before the "
+                "training step (and optimizer.eval() before sampling / checkpointing).")
+        if self._fused:
+            if self.norm == "global":
+                nk = {"remove": self._has_e, "bound_old": {g: math.inf for g in range(len(self.param_groups))},
+                      "k": -self.rho / (self._mnorm + self.eps), "climb": False, "eclamp": {}}
+            else:  # rho = -k in the fused removal / climb (Nekaon's form)
+                nk = {"remove": self._has_e, "bound_old": dict(self._eclamp), "k": -self.rho, "eclamp": {}}
+            self._has_e = False
+            self._eclamp = {}
+            loss = self.inner._step_impl(closure, nk=nk)
+            if self.norm == "none":
+                if self.rho != 0.0 and self._momentum_plans():
+                    self._eclamp = nk["eclamp"]
+                    self._has_e = True
+                return loss
+        else:
+            if self._has_e:  # keyed on the coming step, as the fused removal is
+                self._apply(-1.0, self.inner._t + 1)
+                self._has_e = False
+            self._eclamp = {}
+            loss = self.inner.step(closure)
+            if self.norm == "none":
+                if self.rho != 0.0 and self._momentum_plans():
+                    self._apply(+1.0)
+                    self._has_e = True
+                return loss
+        if self.rho != 0.0:
+            self._mnorm = self._global_mnorm()
+            if self._mnorm > 0.0:
+                self._apply(+1.0)
+                self._has_e = True
+        return loss
+
+    # ------------------------------------------------------------ eval/train
+    @torch.no_grad()
+    def eval(self) -> None:  # noqa: A003 - mirrors MSAM.eval()
+        if self._train_mode and self._has_e:
+            self._apply(-1.0)
+        self._train_mode = False
+
+    @torch.no_grad()
+    def train(self) -> None:
+        if not self._train_mode and self._has_e:
+            self._apply(+1.0)
+        self._train_mode = True
+
+    # ------------------------------------------------------------ delegation
+    def zero_grad(self, set_to_none: bool = True) -> None:  # noqa: FBT001, FBT002
+        self.inner.zero_grad(set_to_none=set_to_none)
+
+    def add_param_group(self, param_group: dict[str, Any]) -> None:
+        if not hasattr(self, "inner"):
+            return super().add_param_group(param_group)
+        self.inner.add_param_group(param_group)
+        self._mplans.clear()
+
+    def state_dict(self) -> dict[str, Any]:
+        sd = self.inner.state_dict()
+        sd["msam"] = {}
+        return sd
+
+    def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        """msam.py:409-421: checkpoints are saved in eval mode, so no climb is
+        active after loading."""
+        sd = dict(state_dict)
+        sd.pop("msam", None)
+        sd.pop("_autolr", None)
+        self.inner.load_state_dict(sd)
+        self.param_groups = self.inner.param_groups
+        self._train_mode = True
+        self._has_e = False
+        self._mnorm = 0.0
+        self._eclamp = {}
+        self._mplans.clear()

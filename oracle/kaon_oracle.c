@@ -18,6 +18,7 @@
  *   - Lion          src/kaon/lion.py:454-485 (== batched :416-451)
  *   - AdaMuon       src/kaon/adamuon.py:97-149, 557-615 (== batched :434-555)
  *   - MSAM/Nekaon   src/kaon/msam.py:169-235, 375-406 ; src/kaon/nekaon.py:162-171
+ *                   (norm "none" and "global": the momentum norm, msam.py:191-199)
  *   - AdaPNM        src/kaon/adapnm.py:998-1016, 1209-1275 (== batched :1069-1200)
  *   - KProdigy      src/kaon/kprodigy.py:337-441 (pass 1), 768-808 (pass 2), 723-741 (momentum)
  *
@@ -440,6 +441,22 @@ static void msam_apply(const KoTensor* t, const KoHyper* h, float factor, float 
     }
     write_add(t, e, h, stream);
     free(e);
+}
+
+/* Sum of squares of the dequantized momentum, for MSAM norm="global"
+ * (_global_mnorm, msam.py:191-199: (m*m).sum() per bucket): CSUM over each
+ * row, then CSUM over the R row sums (a 1-D tensor is one row). */
+float ko_momentum_sumsq(const KoTensor* t) {
+    int64_t R = t->R, C = t->C, n = R * C;
+    if (n <= 0) return 0.0f;
+    float* m = (float*)malloc(sizeof(float) * (size_t)n);
+    float* rs = (float*)malloc(sizeof(float) * (size_t)R);
+    mom_dequant(t, m);
+    for (int64_t i = 0; i < n; ++i) m[i] = m[i] * m[i];
+    for (int64_t r = 0; r < R; ++r) rs[r] = ko_csum(m + r * C, C);
+    float s = ko_csum(rs, R);
+    free(m); free(rs);
+    return s;
 }
 
 int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bound, uint32_t stream) {

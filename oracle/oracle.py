@@ -93,6 +93,8 @@ def lib() -> ctypes.CDLL:
         L.ko_kprodigy_pass1_tensor.restype = ctypes.c_int
         L.ko_kprodigy_pass2_tensor.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper)]
         L.ko_kprodigy_pass2_tensor.restype = ctypes.c_int
+        L.ko_momentum_sumsq.argtypes = [ctypes.POINTER(KoTensor)]
+        L.ko_momentum_sumsq.restype = ctypes.c_float
         L.ko_fsum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
         L.ko_fsum.restype = ctypes.c_float
         L.ko_msam_apply.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
@@ -443,8 +445,15 @@ class OracleOptimizer:
         self.has_e = False
         self.bound = 0.0   # frozen climb bound (msam.py:169-188)
         self.k = float(group.get("k", 0.0))
+        self.mnorm = 0.0   # MSAM norm="global": ||m|| cached at climb time
+        self.mnorm_log: list[float] = []           # the norm this oracle computed, per step
+        self.mnorm_feed: list[float] | None = None  # tests: norms to use instead (another sum order)
+        self.rho, self.norm, self.meps = -self.k, "none", 1e-12
+        if opt == "msam":  # MSAM(norm=...) over Adakaon; norm "none" is Nekaon's rho = -k form
+            self.rho, self.norm, self.meps = float(group["rho"]), group["norm"], float(group.get("msam_eps", 1e-12))
+            self.k = -self.rho
         for prm in params:
-            init_state(prm, "adakaon" if opt == "nekaon" else opt, self.group)
+            init_state(prm, "adakaon" if opt in ("nekaon", "msam") else opt, self.group)
 
     def _kprodigy_step(self, noise: dict[int, list] | None) -> None:
         """KProdigy._step_scope (src/kaon/kprodigy.py:306-386) for one group."""
@@ -493,14 +502,47 @@ class OracleOptimizer:
             _check(lib().ko_kprodigy_pass2_tensor(ctypes.byref(t), ctypes.byref(h)))
         g["k"] = k + 1
 
+    def global_mnorm(self) -> float:
+        """msam.py:191-199 in the canonical order: each tensor's sum of squares
+        (ko_momentum_sumsq), added in param order in fp32, fp32 sqrt."""
+        sq = np.float32(0.0)
+        for prm in self.params:
+            t = _tensor(prm, self.group["momentum_dtype"])
+            sq = np.float32(sq + np.float32(lib().ko_momentum_sumsq(ctypes.byref(t))))
+        return float(np.sqrt(sq, dtype=np.float32))
+
+    def _msam_global_step(self, noise: dict[int, list] | None) -> None:
+        """MSAM.step with norm="global" (msam.py:375-406): remove the previous climb
+        (folded into the Adakaon step, factor -rho/(||m||+eps) with the cached norm,
+        no bound), the inner step, then climb along the new momentum with its norm."""
+        h = _hyper(self.group, self.seed, self.t)
+        h.nk_remove = int(self.has_e)
+        h.nk_k = -self.rho / (self.mnorm + self.meps)
+        h.nk_bound_old = math.inf
+        h.nk_climb = 0
+        for prm in self.params:
+            t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
+            _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
+        self.has_e = False
+        if self.rho != 0.0:
+            own = self.global_mnorm()
+            self.mnorm_log.append(own)
+            self.mnorm = self.mnorm_feed.pop(0) if self.mnorm_feed else own
+            if self.mnorm > 0.0:
+                self.msam_apply(+1.0, noise)
+                self.has_e = True
+
     def step(self, noise: dict[int, list] | None = None, fac_override: dict[int, np.ndarray] | None = None) -> None:
         self.t += 1
         if self.opt == "kprodigy":
             self._kprodigy_step(noise)
             return
+        if self.opt == "msam" and self.norm == "global":
+            self._msam_global_step(noise)
+            return
         h = _hyper(self.group, self.seed, self.t)
         md = self.group["momentum_dtype"]
-        if self.opt == "nekaon":
+        if self.opt in ("nekaon", "msam"):
             h.nk_remove = int(self.has_e)
             h.nk_bound_old = self.bound
             new_bound = abs(self.k) * self.group.get("clip_threshold", 1.0) * self.group["lr"]
@@ -514,7 +556,7 @@ class OracleOptimizer:
                 continue
             t = _tensor(prm, md, None if noise is None else noise.get(prm.tensor_id),
                         fac_override=None if fac_override is None else fac_override.get(prm.tensor_id))
-            if self.opt in ("adakaon", "nekaon"):
+            if self.opt in ("adakaon", "nekaon", "msam"):
                 _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
             elif self.opt == "lion":
                 _check(lib().ko_lion_tensor(ctypes.byref(t), ctypes.byref(h)))
@@ -522,18 +564,25 @@ class OracleOptimizer:
                 _check(lib().ko_adamuon_tensor(ctypes.byref(t), ctypes.byref(h)))
             else:
                 raise ValueError(self.opt)
-        if self.opt == "nekaon" and self.k != 0.0:
+        if self.opt in ("nekaon", "msam") and self.k != 0.0:
             self.has_e = True
             self.bound = h.nk_bound_new
 
-    def msam_apply(self, sign: float, noise: dict[int, list] | None = None) -> None:
-        """MSAM._apply(sign) with the frozen bound (eval(): sign=-1; train(): +1)."""
-        h = _hyper(self.group, self.seed, self.t)
+    def msam_apply(self, sign: float, noise: dict[int, list] | None = None, step: int | None = None) -> None:
+        """MSAM._apply(sign) with the frozen bound (eval(): sign=-1; train(): +1).
+
+        ``step`` keys the SR noise (default: the current step count).  A caller
+        that drives MSAM over another optimizer by hand sets ``rho``, ``norm``,
+        ``meps`` (and ``mnorm`` from :meth:`global_mnorm`) on this object."""
+        h = _hyper(self.group, self.seed, self.t if step is None else step)
         factor = sign * (-self.k)
+        bound = self.bound
+        if self.norm == "global":
+            factor, bound = sign * self.rho / (self.mnorm + self.meps), math.inf
         stream = 0 if sign < 0 else 2
         for prm in self.params:
             t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
-            lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), factor, self.bound, stream)
+            lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), factor, bound, stream)
 
 
 def make_param(shape, p_dtype=BF16, g_dtype=BF16, tensor_id=0, *, p_values=None, g_values=None) -> OParam:

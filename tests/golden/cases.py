@@ -64,6 +64,17 @@ CASES = {
     "nekaon_int8_f32": _case("nekaon", _SMALL, dict(lr=1e-3, k=1.5, betas=(0.5, 0.999), momentum_dtype="int8",
                                                     foreach=False),
                              p_dtype="f32", g_dtype="f32", eval_train=True),
+    # MSAM (src/kaon/msam.py) over Adakaon: norm="global" scales the climb by one
+    # momentum norm over the whole net; norm="none" is the raw-momentum lookahead
+    "msam_global_int8": _case("msam", _SMALL, dict(lr=1e-3, rho=0.3, betas=(0.9, 0.999), weight_decay=0.01,
+                                                   momentum_dtype="int8", foreach=False), eval_train=True),
+    "msam_global_bf16_rn": _case("msam", _ODD, dict(lr=1e-3, rho=-0.2, betas=(0.8, 0.999), momentum_dtype="bfloat16",
+                                                    bf16_method="none", foreach=True), eval_train=True),
+    "msam_global_4bit_f32": _case("msam", _SMALL, dict(lr=1e-3, rho=0.05, momentum_dtype="4bit",
+                                                       momentum_4bit_block=32, foreach=False),
+                                  p_dtype="f32", g_dtype="f32", eval_train=True),
+    "msam_none_int8": _case("msam", _SMALL, dict(lr=1e-3, rho=0.5, norm="none", betas=(0.5, 0.999),
+                                                 momentum_dtype="int8", foreach=False), eval_train=True),
     # AdaPNM (src/kaon/adapnm.py) -- two momenta alternating by step parity
     "pnm_bf16_sr": _case("adapnm", _SMALL, dict(lr=1e-3, betas=(0.8, 0.999), beta0=0.5,
                                                 momentum_dtype="bfloat16", foreach=False)),

@@ -5,7 +5,7 @@ Run in the build container only (the reference is not present on the GPU box):
     python tests/golden/make_golden.py /root/reference/src [case ...]
 
 It imports the reference ``kaon`` package (pure Python + torch CPU) and steps
-its Adakaon / Lion / AdaMuon / Nekaon / AdaPNM / KProdigy on small seeded inputs.  The codecs, the
+its Adakaon / Lion / AdaMuon / Nekaon / MSAM / AdaPNM / KProdigy on small seeded inputs.  The codecs, the
 SR bit trick, the cautious rule and the Philox stream are pinned by closed
 forms and known-answer tests elsewhere; what only the reference itself can pin
 is the composition of torch-CPU ops (lerp/FMA placement, bf16-rounded GC,
@@ -120,6 +120,8 @@ def make_opt(kaon, case, params):
         return kaon.AdaPNM(params, **kw)
     if name == "kprodigy":
         return kaon.KProdigy(params, **kw)
+    if name == "msam":
+        return kaon.MSAM(params, **kw)
     raise ValueError(name)
 
 
@@ -134,6 +136,8 @@ def run_case(kaon, case):
     _CTX["ids"] = {p.data_ptr(): i for i, p in enumerate(params)}
     hashes = []
     d_traj = []
+    mnorm_traj = []
+    out_steps = {}
     for step in range(1, case["steps"] + 1):
         for i, p in enumerate(params):
             g = grad_values(case, i, step)
@@ -143,6 +147,12 @@ def run_case(kaon, case):
         opt.step()
         if name_of(case) == "kprodigy":
             d_traj.append(opt.param_groups[0]["d"])
+        if name_of(case) == "msam":
+            mnorm_traj.append(opt._mnorm)
+            for i, p in enumerate(params):  # the momentum the norm was taken over
+                for k in ("m", "m_scale"):
+                    if k in opt.inner.state[p]:
+                        out_steps[f"t{step}_s{i}_{k}"] = _bits(opt.inner.state[p][k])
         if step == 1 and case.get("sample_stride"):
             step1 = [_bits(p).reshape(-1)[::case["sample_stride"]] for p in params]
         hashes.append(hashlib.sha256(b"".join(_bits(p).tobytes() for p in params)).hexdigest())
@@ -159,6 +169,10 @@ def run_case(kaon, case):
         for key in ("d", "d_max", "d_numerator"):
             out[f"g_{key}"] = np.array(grp[key], dtype=np.float64)
         out["g_k"] = np.array(grp["k"], dtype=np.int64)
+    if name_of(case) == "msam":
+        # MSAM's cached ||m|| after every step (msam.py:191-199, 395-397)
+        out["mnorm_traj"] = np.array(mnorm_traj, dtype=np.float64)
+        out.update(out_steps)
     inner = getattr(opt, "inner", opt)
     for i, p in enumerate(params):
         st = inner.state[p]

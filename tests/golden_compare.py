@@ -18,7 +18,8 @@ from cases import CASES, CFG0, grad_values, param_values  # noqa: E402
 
 # Constructor defaults of each reference optimizer (what the case kwargs do not set):
 # Adakaon src/kaon/adakaon.py:195-218, Lion src/kaon/lion.py:152-171,
-# AdaMuon src/kaon/adamuon.py:216-239, Nekaon src/kaon/nekaon.py:122-137,
+# AdaMuon src/kaon/adamuon.py:216-239, Nekaon src/kaon/nekaon.py:122-137, MSAM src/kaon/msam.py:101-108
+# over Adakaon's (its eps is msam_eps here: Adakaon has an eps of its own),
 # AdaPNM src/kaon/adapnm.py:344-370, KProdigy src/kaon/kprodigy.py:155-235 (the group keys d, d_max,
 # d_numerator, k are its per-group D state).
 DEFAULTS = {
@@ -34,6 +35,10 @@ DEFAULTS = {
     "nekaon": dict(lr=1e-3, k=1.5, betas=(0.5, 0.999), eps=(1e-30, 1e-3), weight_decay=0.1,
                    clip_threshold=1.0, momentum_dtype="4bit", momentum_4bit_block=128, cautious=True,
                    gradient_centralization=True, bf16_method="stochastic_rounding"),
+    "msam": dict(lr=1e-3, betas=(0.9, 0.999), eps=(1e-30, 1e-3), weight_decay=0.0, clip_threshold=1.0,
+                 momentum_dtype="bfloat16", momentum_4bit_block=128, cautious=True,
+                 gradient_centralization=True, bf16_method="stochastic_rounding", rho=0.3, norm="global",
+                 msam_eps=1e-12),
     "kprodigy": dict(lr=1.0, betas=(0.9, 0.999), beta3=None, eps=1e-8, weight_decay=0.0, decouple=True,
                      use_bias_correction=False, safeguard_warmup=False, d=1e-6, d0=1e-6, d_max=1e-6,
                      d_numerator=0.0, d_coef=1.0, growth_rate=float("inf"), d_update_freq=1, slice_p=1, k=0,

@@ -22,7 +22,7 @@ def tdtype(name: str) -> torch.dtype:
 
 
 def make_opt(case, params, group=None):
-    from kaon_amd import AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
+    from kaon_amd import MSAM, AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
 
     g = dict(group or group_for(case))
     name = case["opt"]
@@ -40,6 +40,11 @@ def make_opt(case, params, group=None):
         md = common.pop("momentum_dtype")
         opt = Nekaon(params, lr=g["lr"], k=g["k"], betas=g["betas"], weight_decay=g["weight_decay"],
                      momentum_dtype=md, eps=g["eps"], clip_threshold=g["clip_threshold"], **common)
+        opt.inner.sr_seed = case["seed"]
+    elif name == "msam":
+        # MSAM takes ``eps`` for itself; the Adakaon base keeps its default eps
+        opt = MSAM(params, rho=g["rho"], norm=g["norm"], eps=g["msam_eps"], lr=g["lr"], betas=g["betas"],
+                   weight_decay=g["weight_decay"], clip_threshold=g["clip_threshold"], **common)
         opt.inner.sr_seed = case["seed"]
     elif name == "adamuon":
         opt = AdaMuon(params, lr=g["lr"], betas=g["betas"], eps=g["eps"], weight_decay=g["weight_decay"],

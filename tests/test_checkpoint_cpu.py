@@ -168,3 +168,23 @@ def test_nekaon_load_clears_the_climb():
     opt._has_e, opt._eclamp = True, {0: 0.1}
     opt.load_state_dict(sd)
     assert opt._has_e is False and opt._eclamp == {}
+
+
+def test_msam_load_clears_the_climb_and_validates():
+    """MSAM.load_state_dict (msam.py:409-421) clears the climb and the cached norm;
+    the constructor checks follow msam.py:101-108 (norm="tensor" is not built here)."""
+    from kaon_amd import MSAM
+
+    p = torch.nn.Parameter(torch.zeros(8, 16, dtype=torch.bfloat16))
+    opt = MSAM([p], rho=0.3, lr=1e-3)
+    sd = opt.state_dict()
+    assert "msam" in sd
+    opt._has_e, opt._mnorm, opt._eclamp = True, 0.5, {0: 0.1}
+    opt.load_state_dict(sd)
+    assert opt._has_e is False and opt._mnorm == 0.0 and opt._eclamp == {}
+    with pytest.raises(ValueError):
+        MSAM([p], norm="layer")
+    with pytest.raises(ValueError):
+        MSAM([p], eps=-1.0)
+    with pytest.raises(NotImplementedError):
+        MSAM([p], norm="tensor")

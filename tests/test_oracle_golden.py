@@ -23,6 +23,15 @@ What must agree:
   momentum exact except, for bf16 storage, the last numel % 32 elements of a
   tensor: torch CPU's scalar tail loop keeps add_'s alpha in fp32 where its
   32-wide vector loop rounds it to bf16 (the oracle follows the vector loop).
+* MSAM norm="global" (msam_global_* cases): the norm is a cross-tensor fp32
+  sum, so the two halves are pinned apart.  The fixtures hold the reference's
+  momentum after every step and the norm it took over it: the oracle's norm of
+  that same momentum is within 4 fp32 ulps of the reference's.  With the
+  reference's norms fed in, the whole step (removal folded into Adakaon, inner
+  step, climb, eval/train swaps) gives the reference's weights bit for bit.
+  Left to its own norms the oracle drifts by a few SR flips: a momentum code
+  that torch's reduction order moves by one (the bf16-case allowance above)
+  moves the norm by ~1e-5.
 """
 import json
 import os
@@ -35,8 +44,10 @@ from golden_compare import CASES, CFG0, bf16_mismatch, build_oracle, load_golden
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-BIT_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "bf16" and c["opt"] not in ("adamuon", "kprodigy")]
-F32_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "f32" and c["opt"] != "kprodigy"]
+MSAM_GLOBAL = [k for k, c in CASES.items() if c["opt"] == "msam" and c["kwargs"].get("norm", "global") == "global"]
+BIT_CASES = [k for k, c in CASES.items()
+             if c["g_dtype"] == "bf16" and c["opt"] not in ("adamuon", "kprodigy") and k not in MSAM_GLOBAL]
+F32_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "f32" and c["opt"] != "kprodigy" and k not in MSAM_GLOBAL]
 PD_CASES = [k for k, c in CASES.items() if c["opt"] == "kprodigy"]
 MUON_CASES = [k for k, c in CASES.items() if c["opt"] == "adamuon"]
 
@@ -89,6 +100,57 @@ def test_fp32_grad_cases_match_reference(name):
                                    atol=1e-8), (name, i, k)
         if evalp is not None:
             assert np.allclose(evalp[i], gold[f"p{i}_eval"], rtol=1e-4, atol=1e-7)
+
+
+def _oracle_with_reference_momentum(case, gold, step):
+    """An oracle optimizer over the case whose momentum is the reference's after ``step``."""
+    params, opt = build_oracle(case)
+    for i, prm in enumerate(params):
+        for k in ("m", "m_scale"):
+            key = f"t{step}_s{i}_{k}"
+            if key in gold:
+                prm.state[k] = np.ascontiguousarray(gold[key]).reshape(np.shape(prm.state[k])).copy()
+    return opt
+
+
+@pytest.mark.parametrize("name", MSAM_GLOBAL)
+def test_msam_global_norm_of_reference_momentum(name):
+    """_global_mnorm (msam.py:191-199) over the reference's own momentum after each
+    step: the canonical order (per-tensor 64-lane sums, added in param order, fp32
+    sqrt) is within 4 fp32 ulps of torch's."""
+    case = CASES[name]
+    gold = load_golden(name)
+    for step in range(1, case["steps"] + 1):
+        mine = _oracle_with_reference_momentum(case, gold, step).global_mnorm()
+        ref = float(gold["mnorm_traj"][step - 1])
+        assert ref > 0.0
+        assert abs(mine - ref) <= 4 * float(np.spacing(np.float32(ref))), (name, step, mine, ref)
+
+
+@pytest.mark.parametrize("name", MSAM_GLOBAL)
+def test_msam_global_step_exact_given_reference_norm(name):
+    """MSAM.step (msam.py:375-406) with norm="global", the reference's norms fed in."""
+    case = CASES[name]
+    gold = load_golden(name)
+    params, opt = build_oracle(case)
+    opt.mnorm_feed = [float(x) for x in gold["mnorm_traj"]]
+    for step in range(1, case["steps"] + 1):
+        set_grads(case, params, step)
+        opt.step()
+    opt.msam_apply(-1.0)
+    evalp = [prm.p.copy() for prm in params]
+    opt.msam_apply(+1.0)
+    # the oracle's own norm of its own momentum stays close to the reference's
+    assert rel_err(opt.mnorm_log, gold["mnorm_traj"]) <= 1e-4
+    for i, prm in enumerate(params):
+        a, b = prm.state["m"].reshape(-1), gold[f"s{i}_m"].reshape(-1)
+        assert (a != b).sum() <= max(1, a.size // 500), (name, i)
+        if case["g_dtype"] == "bf16":
+            assert bf16_mismatch(prm.p, gold[f"p{i}"])[0] == 0, (name, i)
+            assert bf16_mismatch(evalp[i], gold[f"p{i}_eval"])[0] == 0, (name, i)
+        else:
+            assert np.allclose(prm.p, gold[f"p{i}"], rtol=1e-4, atol=1e-7), (name, i)
+            assert np.allclose(evalp[i], gold[f"p{i}_eval"], rtol=1e-4, atol=1e-7), (name, i)
 
 
 @pytest.mark.parametrize("name", MUON_CASES)

@@ -70,6 +70,12 @@ WORKLOADS = {
                                    kw=dict(lr=1.0, betas=(0.9, 0.999), momentum_dtype="int8",
                                            second_moment="factored", slice_p=11), bm=1.0,
                                    b_extra=12.0 / 11.0, pd_slice=11, pd_full_v=False),
+    # MSAM norm="global" over Adakaon (src/kaon/msam.py, SURVEY's next row 4): the removal rides in
+    # Adakaon's apply; b_extra = the norm pass (m read) and the climb pass (m read, p read + write)
+    "msam_int8": dict(desc="MSAM rho=0.3 norm='global' over Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, "
+                           "SR bf16, lr 1e-4", opt="msam",
+                      kw=dict(lr=1e-4, rho=0.3, betas=(0.9, 0.999), momentum_dtype="int8"), bm=1.0,
+                      b_extra=1.0 + 4.0 + 1.0),
     # the launch-bound regime: the reference's LoRA proxy bag (benchmarks/proxy/harness.py:117-127:
     # 512 tensors [8, 16], fp32) stepped by Adakaon with bf16 momentum, the configuration its
     # control ranking lists as "Adakaon-bf16-fused" (benchmarks/control/RANKINGS.md:83)
@@ -82,7 +88,8 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 # algorithmic HBM bytes per param of each phase kernel (bf16 g/p, b_m momentum bytes)
 PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor", 5: "keep_count", 6: "apply",
-               8: "momentum", 9: "newton_schulz", 11: "pass1_moments_and_d_stats", 12: "pass2_update"}
+               8: "momentum", 9: "newton_schulz", 11: "pass1_moments_and_d_stats", 12: "pass2_update",
+               13: "momentum_sumsq", 14: "climb"}
 
 
 def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict | None = None) -> float:
@@ -92,6 +99,11 @@ def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict |
         full = 1.0 if w and w.get("pd_full_v") else 0.0
         sl = (w or {}).get("pd_slice", 1)
         return {11: 2.0 + 2.0 * bm + 8.0 * full + 14.0 / sl, 12: 2.0 + bm + 4.0 * full + 4.0}.get(phase, 0.0)
+    if opt == "msam":
+        # the Adakaon phases (the removal reads the momentum the update reads anyway), then
+        # the norm (m read) and the climb (m read, p read + write)
+        if phase in (13, 14):
+            return {13: bm, 14: 4.0 + bm}[phase]
     if opt == "adapnm":
         # both momenta are read by the clip-sum, keep-count and apply passes
         return {1: 2.0, 3: 2.0 + 2.0 * bm, 5: 2.0 + 2.0 * bm, 6: 6.0 + 3.0 * bm}.get(phase, 0.0)
@@ -122,9 +134,11 @@ def measured_traffic(workload: str, phase: int) -> float | None:
 
 
 def make_opt(name, params):
-    from kaon_amd import AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
+    from kaon_amd import MSAM, AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
 
     w = WORKLOADS[name]
+    if w["opt"] == "msam":
+        return MSAM(params, **w["kw"])
     if w["opt"] == "adapnm":
         return AdaPNM(params, **w["kw"])
     if w["opt"] == "kprodigy":
@@ -221,6 +235,9 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
             nk = None
             if WORKLOADS[name]["opt"] == "nekaon":
                 nk = {"remove": True, "bound_old": dict(opt._eclamp), "k": opt.k, "eclamp": {}}
+            if WORKLOADS[name]["opt"] == "msam":
+                nk = {"remove": True, "bound_old": {gid: float("inf")}, "k": -opt.rho / (opt._mnorm + opt.eps),
+                      "climb": False, "eclamp": {}}
             hp = inner._hyper(group, pdt, gdt, nk, gid)
             fn, phases = lib.kaon_adakaon_phases, (1, 2, 3, 4, 5, 6)
         s = torch.cuda.current_stream().cuda_stream
@@ -233,6 +250,25 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
                 torch.cuda.synchronize()
                 acc = out.setdefault(ph, [0.0] * reps)
                 acc[r] += e0.elapsed_time(e1)
+    if WORKLOADS[name]["opt"] == "msam":
+        # the norm and the climb passes over the momentum plans
+        s = torch.cuda.current_stream().cuda_stream
+        for gid, pdt, plan, _tids, _idx in opt._momentum_plans():
+            h = opt._hyper(gid, pdt)
+            f = opt.rho / (opt._mnorm + opt.eps)
+            for r in range(reps):
+                for ph in (13, 14):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    if ph == 13:
+                        rc = lib.kaon_momentum_sumsq(ctypes.byref(plan.launch), ctypes.byref(h), s)
+                    else:
+                        rc = lib.kaon_msam_apply(ctypes.byref(plan.launch), ctypes.byref(h), f, float("inf"), 2, s)
+                    _lib.check(rc, "msam pass")
+                    e1.record()
+                    torch.cuda.synchronize()
+                    acc = out.setdefault(ph, [0.0] * reps)
+                    acc[r] += e0.elapsed_time(e1)
     return {ph: sum(v) / len(v) for ph, v in out.items()}
 
 
@@ -254,6 +290,8 @@ def cpu_baseline(params, name, seconds: float) -> dict:
                  ns_steps=kw.get("ns_steps", 2))
     if w["opt"] == "adapnm":
         group.update(eps=1e-8, beta0=kw["beta0"], ams_bound=False)
+    if w["opt"] == "msam":
+        group.update(rho=kw["rho"], norm="global", msam_eps=1e-12)
     if w["opt"] == "kprodigy":
         group.update(beta3=None, eps=1e-8, decouple=True, use_bias_correction=False, safeguard_warmup=False,
                      d=1e-6, d0=1e-6, d_max=1e-6, d_numerator=0.0, d_coef=1.0, growth_rate=float("inf"),

@@ -1722,14 +1722,29 @@ __global__ __launch_bounds__(KAON_WG) void k_msq(const KaonTensor* __restrict__ 
       const int64_t e0 = r * C + c * 8;
       uint32_t mq[8];
       ld_mom_at<CODEC>(T.m, e0, cnt, vec && cnt == 8, mq);
+      // 4-bit: walk the blocks from the chunk's first element (32-bit: n < 2^31)
+      uint32_t blk = 0u, boff = 0u;
+      if (CODEC == KAON_MOM_4BIT) {
+        blk = (uint32_t)e0 / (uint32_t)T.block4;
+        boff = (uint32_t)e0 - blk * (uint32_t)T.block4;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (i >= cnt) continue;
         float m;
-        if (CODEC == KAON_MOM_INT8) m = (float)(int8_t)(uint8_t)mq[i] * sc;
-        else if (CODEC == KAON_MOM_4BIT) m = ((float)mq[i] - 8.0f) * G(T.m_scale)[(e0 + i) / T.block4];
-        else if (CODEC == KAON_MOM_BF16) m = bf2f(mq[i]);
-        else m = __uint_as_float(mq[i]);
+        if (CODEC == KAON_MOM_INT8) {
+          m = (float)(int8_t)(uint8_t)mq[i] * sc;
+        } else if (CODEC == KAON_MOM_4BIT) {
+          m = ((float)mq[i] - 8.0f) * G(T.m_scale)[blk];
+          if (++boff == (uint32_t)T.block4) {
+            boff = 0u;
+            ++blk;
+          }
+        } else if (CODEC == KAON_MOM_BF16) {
+          m = bf2f(mq[i]);
+        } else {
+          m = __uint_as_float(mq[i]);
+        }
         a = a + m * m;
       }
     }
@@ -2631,22 +2646,50 @@ __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__
                                                   float factor, float bound, uint32_t sid) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
-  const int64_t C = T.C;
-  const int64_t e_begin = it.row0, e_end = (int64_t)it.row0 + it.nrows;
+  // tensors hold < 2^31 elements: 32-bit element and row arithmetic
+  const uint32_t e_begin = (uint32_t)it.row0, e_end = (uint32_t)it.row0 + (uint32_t)it.nrows;
   const bool vecT = T.vec_flat != 0;
-  for (int64_t e0 = e_begin + 8 * (int64_t)threadIdx.x; e0 < e_end; e0 += 8 * KAON_WG) {
-    const int cnt = (int)min<int64_t>(8, e_end - e0);
+  // the scale of element e is scale[e / span] (int8: span C per row, or the whole 1-D tensor;
+  // 4-bit: the block); chunks start at multiples of 8, so a span that is a multiple of 8
+  // gives one scale per chunk, and any other span is walked element by element
+  const uint32_t span = CODEC == KAON_MOM_4BIT ? (uint32_t)T.block4
+                        : (CODEC == KAON_MOM_INT8 && T.factored) ? (uint32_t)T.C : 0u;
+  const bool span8 = span % 8u == 0u;
+  const KAON_G float* msc = G(T.m_scale);
+  for (uint32_t e0 = e_begin + 8u * threadIdx.x; e0 < e_end; e0 += 8u * KAON_WG) {
+    const int cnt = (int)min(8u, e_end - e0);
     const bool vec = vecT && cnt == 8;
     uint32_t mq[8];
     ld_mom_raw<CODEC>(T, e0, cnt, vec, mq);
+    float sc[8];
+    if (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) {
+      if (span == 0u) {
+        const float s0 = msc[0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = s0;
+      } else if (span8) {
+        const float s0 = msc[e0 / span];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = s0;
+      } else {
+        uint32_t r = e0 / span, c = e0 - r * span;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          sc[i] = i < cnt ? msc[r] : 0.0f;
+          if (++c == span) {
+            c = 0u;
+            ++r;
+          }
+        }
+      }
+    }
     float ev[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t e = e0 + i;
       float mold = 0.0f;
       if (i < cnt) {
-        if (CODEC == KAON_MOM_INT8) mold = (float)(int8_t)(uint8_t)mq[i] * T.m_scale[T.factored ? e / C : 0];
-        else if (CODEC == KAON_MOM_4BIT) mold = ((float)mq[i] - 8.0f) * T.m_scale[e / T.block4];
+        if (CODEC == KAON_MOM_INT8) mold = (float)(int8_t)(uint8_t)mq[i] * sc[i];
+        else if (CODEC == KAON_MOM_4BIT) mold = ((float)mq[i] - 8.0f) * sc[i];
         else if (CODEC == KAON_MOM_BF16) mold = bf2f(mq[i]);
         else mold = __uint_as_float(mq[i]);
       }
@@ -2791,23 +2834,36 @@ ElemFn elem_fn(int pt, int gt, int codec) {
 
 // specialized kernels available: (opt, codec, flags) with flags among the
 // defaults of the reference optimizers (GC and cautious on, WD on or off;
-// Nekaon: the climb, plus the removal after the first step, WD on or off)
+// Nekaon: the climb, plus the removal after the first step, WD on or off;
+// MSAM norm="global": the removal alone)
 template <int OPT, int PHASE, int CODEC>
 ElemFn fast_by_flags(int ff) {
   switch (ff) {
     case FF_GC | FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT>;
     case FF_GC | FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD>;
   }
-  if (OPT == KAON_OPT_ADAKAON && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT)) {
+  if constexpr (OPT == KAON_OPT_ADAKAON && CODEC != KAON_MOM_NONE) {
+    // phase 5 reads the weights (and so the removal) only under weight decay
     switch (ff) {
-      case FF_GC | FF_CAUT | FF_NKC:
-        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC>;
-      case FF_GC | FF_CAUT | FF_NKC | FF_NKR:
-        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC | FF_NKR>;
-      case FF_GC | FF_CAUT | FF_WD | FF_NKC:
-        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC>;
-      case FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR:
-        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR>;
+      case FF_GC | FF_CAUT | FF_WD | FF_NKR:
+        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKR>;
+    }
+    if constexpr (PHASE == 6) {
+      switch (ff) {
+        case FF_GC | FF_CAUT | FF_NKR: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKR>;
+      }
+      if constexpr (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) {
+        switch (ff) {
+          case FF_GC | FF_CAUT | FF_NKC:
+            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC>;
+          case FF_GC | FF_CAUT | FF_NKC | FF_NKR:
+            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC | FF_NKR>;
+          case FF_GC | FF_CAUT | FF_WD | FF_NKC:
+            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC>;
+          case FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR:
+            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR>;
+        }
+      }
     }
   }
   return nullptr;
@@ -2816,6 +2872,12 @@ ElemFn fast_by_flags(int ff) {
 template <int OPT, int PHASE>
 ElemFn fast_fn(int codec, int ff) {
   if (OPT == KAON_OPT_ADAMUON) return nullptr;
+  if (PHASE == 5) {
+    // the climb is a phase-6 write; the removal matters to phase 5 only where it reads
+    // the weights (weight decay): drop the flags phase 5 does not look at
+    ff &= ~FF_NKC;
+    if (!(ff & FF_WD)) ff &= ~FF_NKR;
+  }
   switch (codec) {
     case KAON_MOM_NONE: return OPT == KAON_OPT_ADAKAON ? fast_by_flags<OPT, PHASE, KAON_MOM_NONE>(ff) : nullptr;
     case KAON_MOM_BF16: return fast_by_flags<OPT, PHASE, KAON_MOM_BF16>(ff);

@@ -252,16 +252,17 @@ class KProdigy(KaonOptimizer):
         # D update: the per-tensor statistics folded in param order in fp32, then
         # the scalar recurrence in double (kprodigy.py:355-380)
         if should_update_d and lr > 0.0 and stats:
-            rows = []
+            orders, poss, vals = [], [], []
             for order, positions, t in stats:
-                v = t.cpu().numpy().reshape(-1, 2)
-                rows += [(order, pos, v[i, 0], v[i, 1]) for i, pos in enumerate(positions)]
-            rows.sort(key=lambda x: (x[0], x[1]))
+                orders.append(np.full(len(positions), order))
+                poss.append(np.asarray(positions))
+                vals.append(t.cpu().numpy().reshape(-1, 2))
+            perm = np.lexsort((np.concatenate(poss), np.concatenate(orders)))
+            v = np.concatenate(vals)[perm].astype(np.float32)
             const = np.float32(d_over_d0 * dlr)
-            num, den = np.float32(0.0), np.float32(0.0)
-            for _o, _p, n_i, d_i in rows:
-                num = np.float32(num + np.float32(const * np.float32(n_i)))
-                den = np.float32(den + np.float32(d_i))
+            # add.accumulate adds left to right in float32: the sequential fold
+            num = np.add.accumulate(const * v[:, 0], dtype=np.float32)[-1]
+            den = np.add.accumulate(v[:, 1], dtype=np.float32)[-1]
             if float(den) > 0.0:
                 global_num = d_numerator + float(num)
                 d_hat = lead["d_coef"] * global_num / float(den)

@@ -118,31 +118,32 @@ class MSAM(torch.optim.Optimizer):
 
     # ---------------------------------------------------------- perturbation
     @torch.no_grad()
-    def _global_mnorm(self) -> float:
+    def _global_mnorm(self, plans: list | None = None) -> float:
         """||m|| over every momentum: per-tensor sums of squares on the GPU, added in
         param order in fp32, fp32 square root (msam.py:191-199)."""
         lib = L.lib()
-        rows = []
-        for gid, pdt, plan, tids, idx in self._momentum_plans():
+        tids, vals = [], []
+        for gid, pdt, plan, ptids, idx in (self._momentum_plans() if plans is None else plans):
             dev = plan.workspace.device
             L.check(lib.kaon_momentum_sumsq(ctypes.byref(plan.launch), ctypes.byref(self._hyper(gid, pdt)),
                                             E.stream_handle(dev)), "kaon_momentum_sumsq")
-            vals = plan.workspace.index_select(0, idx).cpu().numpy()
-            rows += list(zip(tids, vals))
-        rows.sort(key=lambda x: x[0])
-        sq = np.float32(0.0)
-        for _t, v in rows:
-            sq = np.float32(sq + np.float32(v))
+            vals.append(plan.workspace.index_select(0, idx))
+            tids.append(np.asarray(ptids))
+        if not vals:
+            return 0.0
+        v = np.concatenate([t.cpu().numpy() for t in vals])[np.argsort(np.concatenate(tids), kind="stable")]
+        # add.accumulate adds left to right in float32: the sequential fold
+        sq = np.add.accumulate(v.astype(np.float32), dtype=np.float32)[-1]
         return float(np.sqrt(sq, dtype=np.float32))
 
     @torch.no_grad()
-    def _apply(self, sign: float, step: int | None = None) -> None:
+    def _apply(self, sign: float, step: int | None = None, plans: list | None = None) -> None:
         """Add the perturbation sign * e to every weight with a momentum (msam.py:202-235).
         The SR noise is keyed on ``step`` (default: the inner step count) and stream 0
         for a removal, 2 for a climb."""
         lib = L.lib()
         sid = 0 if sign < 0 else 2
-        for gid, pdt, plan, _tids, _idx in self._momentum_plans():
+        for gid, pdt, plan, _tids, _idx in (self._momentum_plans() if plans is None else plans):
             group = self.param_groups[gid]
             if self.norm == "global":
                 factor, bound = sign * self.rho / (self._mnorm + self.eps), math.inf
@@ -187,9 +188,10 @@ class MSAM(torch.optim.Optimizer):
                     self._has_e = True
                 return loss
         if self.rho != 0.0:
-            self._mnorm = self._global_mnorm()
+            plans = self._momentum_plans()
+            self._mnorm = self._global_mnorm(plans)
             if self._mnorm > 0.0:
-                self._apply(+1.0)
+                self._apply(+1.0, plans=plans)
                 self._has_e = True
         return loss
 

@@ -69,6 +69,12 @@ EXTRA = {
     "none_4bit": _case([[160, 40], [33], [7, 9]], dict(lr=1e-3, rho=0.8, norm="none", momentum_dtype="4bit",
                                                        momentum_4bit_block=16)),
     "rho_zero": _case([[24, 32], [40]], dict(lr=1e-3, rho=0.0, momentum_dtype="int8")),
+    # rows the specialized apply kernel takes (bf16 p and g, SR, GC, cautious): the removal
+    # alone in its phase 6, and under weight decay in its phase 5 too
+    "fast_bf16": _case([[320, 1280], [640, 640], [1280]], dict(lr=1e-3, rho=0.3, momentum_dtype="bfloat16")),
+    "fast_int8_wd": _case([[320, 1280], [96, 64, 3, 3], [640]], dict(lr=1e-3, rho=-0.5, momentum_dtype="int8",
+                                                                     weight_decay=0.1)),
+    "fast_4bit_wd": _case([[256, 2048], [1280]], dict(lr=1e-3, rho=0.2, momentum_dtype="4bit", weight_decay=0.05)),
 }
 
 

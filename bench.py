@@ -94,11 +94,11 @@ PHASE_NAMES = {1: "row_stats", 2: "finalize", 3: "clip_sums", 4: "clip_divisor",
 
 def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict | None = None) -> float:
     if opt == "kprodigy":
-        # pass 1: g, m (read + write), v (read + write) and the sliced s (r + w), p0, p;
-        # pass 2: g, m, v, p (read + write)
+        # pass 1: g, m (read + write), v (read + write); then the sliced g, p, fp32 p0 and the
+        # fp32 s (read + write) for the D statistics; pass 2: g, m, v, p (read + write)
         full = 1.0 if w and w.get("pd_full_v") else 0.0
         sl = (w or {}).get("pd_slice", 1)
-        return {11: 2.0 + 2.0 * bm + 8.0 * full + 14.0 / sl, 12: 2.0 + bm + 4.0 * full + 4.0}.get(phase, 0.0)
+        return {11: 2.0 + 2.0 * bm + 8.0 * full + 16.0 / sl, 12: 2.0 + bm + 4.0 * full + 4.0}.get(phase, 0.0)
     if opt == "msam":
         # the Adakaon phases (the removal reads the momentum the update reads anyway), then
         # the norm (m read) and the climb (m read, p read + write)

@@ -1936,11 +1936,25 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
       else
 #pragma unroll
         for (int i = 0; i < 8; ++i) z[i] = p0[0];
+      // the GC row means of the chunk's elements: one 32-bit division per chunk, then a
+      // walk along the row (n < 2^31)
+      float mu[8];
+      if (gc) {
+        uint32_t r = (uint32_t)j / (uint32_t)C, c = (uint32_t)j - r * (uint32_t)C;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          mu[i] = i < cnt ? ws.mu(T)[r] : 0.0f;
+          if (++c == (uint32_t)C) {
+            c = 0u;
+            ++r;
+          }
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (i >= cnt) continue;
         float gv = g[i];
-        if (gc) gv = round_to<GT>(gv - ws.mu(T)[(j + i) / C]);
+        if (gc) gv = round_to<GT>(gv - mu[i]);
         if (coupled) gv = __fmaf_rn(hp.wdl, p[i], gv);
         an = an + gv * (z[i] - p[i]);
         sc[i] = __fmaf_rn(hp.pd_alpha_s, gv, sc[i] * hp.pd_beta3);
@@ -1950,6 +1964,9 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
     }
   } else {
     for (int64_t c = lane; c < nch; c += 64) {
+      // row of the chunk's first element, then walked by slice_p per element
+      const uint32_t e_first = (uint32_t)((j0 + c * 8) * sp);
+      uint32_t row = gc ? e_first / (uint32_t)C : 0u, col = gc ? e_first - row * (uint32_t)C : 0u;
       for (int i = 0; i < 8; ++i) {
         const int64_t jj = c * 8 + i;
         if (jj >= len) break;
@@ -1959,7 +1976,14 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
         else gv = G((const float*)T.g)[e];
         if (PT == KAON_BF16) pv = bf2f(G((const uint16_t*)T.p)[e]);
         else pv = G((const float*)T.p)[e];
-        if (gc) gv = round_to<GT>(gv - ws.mu(T)[e / C]);
+        if (gc) {
+          gv = round_to<GT>(gv - ws.mu(T)[row]);
+          col += (uint32_t)sp;
+          while (col >= (uint32_t)C) {
+            col -= (uint32_t)C;
+            ++row;
+          }
+        }
         if (coupled) gv = __fmaf_rn(hp.wdl, pv, gv);
         const float pz = T.pd_p0_scalar ? p0[0] : p0[j];
         an = an + gv * (pz - pv);

@@ -55,7 +55,14 @@ class MSAM(torch.optim.Optimizer):
         if norm == "tensor":
             raise NotImplementedError("kaon_amd: MSAM norm='tensor' is not part of this build")
         base = Adakaon if base_optimizer is None else base_optimizer
-        inner = base(params, **kwargs)
+        self._bind(base(params, **kwargs), rho, norm, eps)
+
+    def _bind(self, inner: torch.optim.Optimizer, rho: float, norm: str, eps: float) -> None:
+        """Wrap ``inner``: the param groups and defaults are its own; MSAM keeps no
+        per-param state (torch.optim.Optimizer bookkeeping: hooks, LR schedulers)."""
+        if not hasattr(inner, "_tensor_ids"):
+            raise TypeError("kaon_amd: MSAM wraps a kaon_amd optimizer that owns the momentum "
+                            f"(Adakaon, Lion, AdaMuon, AdaPNM, KProdigy), got {type(inner).__name__}")
         super().__init__([p for g in inner.param_groups for p in g["params"]], dict(inner.defaults))
         self.inner = inner
         self.base_optimizer = inner
@@ -73,6 +80,10 @@ class MSAM(torch.optim.Optimizer):
         self._mplans: dict[tuple, tuple[tuple, E.Plan, list[int], torch.Tensor]] = {}
 
     # ---------------------------------------------------------------- plans
+    def _has_momentum(self) -> bool:
+        return any("m" in self.inner.state.get(p, ())
+                   for g in self.param_groups for p in g["params"])
+
     def _momentum_plans(self) -> list[tuple[int, int, E.Plan, list[int], torch.Tensor]]:
         """(gid, p dtype, plan, param positions, stat word index) over the params with a
         momentum buffer, cached while the param and state pointers hold."""
@@ -172,7 +183,7 @@ class MSAM(torch.optim.Optimizer):
             self._eclamp = {}
             loss = self.inner._step_impl(closure, nk=nk)
             if self.norm == "none":
-                if self.rho != 0.0 and self._momentum_plans():
+                if self.rho != 0.0 and self._has_momentum():
                     self._eclamp = nk["eclamp"]
                     self._has_e = True
                 return loss
@@ -183,7 +194,7 @@ class MSAM(torch.optim.Optimizer):
             self._eclamp = {}
             loss = self.inner.step(closure)
             if self.norm == "none":
-                if self.rho != 0.0 and self._momentum_plans():
+                if self.rho != 0.0 and self._has_momentum():
                     self._apply(+1.0)
                     self._has_e = True
                 return loss

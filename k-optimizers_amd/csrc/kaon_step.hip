@@ -2236,6 +2236,8 @@ struct FastCtx {
   KAON_G uint8_t* bamax;         // 4-bit: per-block |m| maximum
   KAON_G uint8_t* boldsc;        // 4-bit: per-block scale before the step
   const KAON_G uint16_t* nz[3];  // injected noise streams, or null
+  const KAON_G uint8_t* m2;      // AdaPNM: the negative buffer (read only)
+  const KAON_G uint8_t* m2sc;    // AdaPNM: its scales
   uint32_t tid;                  // Philox tensor id
   int bsh;                       // 4-bit: log2 of the block size
   int GL;                        // 4-bit: lanes per block
@@ -2268,28 +2270,45 @@ struct FastIn {
   uint32_t m4;
   kf4 c0, c1;
   float bo, ba;  // 4-bit: block scale before the step, block |m| maximum
+  ku4 n16;       // AdaPNM: the negative buffer (bf16, int8, 4-bit) and its 4-bit block scale
+  ku2 n8;
+  uint32_t n4;
+  float bn;
 };
+
+// Which passes of the specialized kernel read the weights: the apply, and for
+// Adakaon's coupled form of weight decay also the keep count (AdaPNM decays p
+// in the apply only).
+template <int OPT, int PHASE, int FLAGS>
+constexpr bool fast_needs_p() {
+  return PHASE == 6 || ((FLAGS & FF_WD) && OPT != KAON_OPT_ADAPNM);
+}
 
 template <int OPT, int PHASE, int CODEC, int FLAGS>
 __device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t e0, uint32_t j0) {
-  constexpr bool NEEDP = PHASE == 6 || (FLAGS & FF_WD);
+  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
   const ku4 z4 = ku4{0u, 0u, 0u, 0u};
   in.g = ld_stream<true>((const KAON_G ku4*)(X.g + 2u * e0));
   in.p = NEEDP ? ld_stream<true>((const KAON_G ku4*)(X.p + 2u * e0)) : z4;
   in.m8 = CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m + e0)) : ku2{0u, 0u};
   in.m4 = CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m + (e0 >> 1))) : 0u;
   in.m16 = CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m + 2u * e0)) : z4;
-  if (OPT == KAON_OPT_ADAKAON) {
+  in.n8 = PNM && CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m2 + e0)) : ku2{0u, 0u};
+  in.n4 = PNM && CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m2 + (e0 >> 1))) : 0u;
+  in.n16 = PNM && CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m2 + 2u * e0)) : z4;
+  if (OPT == KAON_OPT_ADAKAON || PNM) {
     in.c0 = *(const KAON_G kf4*)(X.cf + 4u * j0);
     in.c1 = *(const KAON_G kf4*)(X.cf + 4u * j0 + 16u);
   } else {
     in.c0 = in.c1 = kf4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  in.bo = in.ba = 0.0f;
+  in.bo = in.ba = in.bn = 0.0f;
   if (CODEC == KAON_MOM_4BIT) {
     const uint32_t blk4 = (e0 >> X.bsh) * 4u;
     in.bo = *(const KAON_G float*)((PHASE == 5 ? X.msc : X.boldsc) + blk4);
     if (PHASE == 6) in.ba = *(const KAON_G float*)(X.bamax + blk4);
+    if (PNM) in.bn = *(const KAON_G float*)(X.m2sc + blk4);
   }
 }
 
@@ -2297,7 +2316,8 @@ __device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t
 // branches consuming them leave nothing pending for the next prefetch to wait on.
 template <int OPT, int PHASE, int CODEC, int FLAGS>
 __device__ __forceinline__ void fast_settle(const FastIn& in) {
-  constexpr bool NEEDP = PHASE == 6 || (FLAGS & FF_WD);
+  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
   settle(in.g.x); settle(in.g.y); settle(in.g.z); settle(in.g.w);
   if (NEEDP) {
     settle(in.p.x); settle(in.p.y); settle(in.p.z); settle(in.p.w);
@@ -2312,28 +2332,42 @@ __device__ __forceinline__ void fast_settle(const FastIn& in) {
   if (CODEC == KAON_MOM_BF16) {
     settle(in.m16.x); settle(in.m16.y); settle(in.m16.z); settle(in.m16.w);
   }
-  if (OPT == KAON_OPT_ADAKAON) {
+  if (PNM) {
+    if (CODEC == KAON_MOM_INT8) {
+      settle(in.n8.x); settle(in.n8.y);
+    }
+    if (CODEC == KAON_MOM_4BIT) {
+      settle(in.n4); settle(in.bn);
+    }
+    if (CODEC == KAON_MOM_BF16) {
+      settle(in.n16.x); settle(in.n16.y); settle(in.n16.z); settle(in.n16.w);
+    }
+  }
+  if (OPT == KAON_OPT_ADAKAON || PNM) {
     settle(in.c0.x); settle(in.c0.y); settle(in.c0.z); settle(in.c0.w);
     settle(in.c1.x); settle(in.c1.y); settle(in.c1.z); settle(in.c1.w);
   }
 }
 
 // FAC1: clip divisor 1 (skip the exact division).  DQX: int8 dequant as
-// q*scale for rows whose old scale is too large for the fma form.  WLO: the
-// momentum lerp weight is below 0.5 (its branch of torch's lerp).
+// q*scale for rows whose old scale (AdaPNM: either buffer's) is too large for
+// the fma form.  WLO: the momentum lerp weight is below 0.5 (its branch of
+// torch's lerp).
 template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX, bool WLO>
 __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, const KaonHyper& hp, uint32_t e0,
-                                           float mu, float rf, float oldsc, float m128, float newsc, double rnew,
-                                           double rfac, double rden, int lane, uint32_t& keep, float& amax) {
+                                           float mu, float rf, float oldsc, float m128, float negsc, float m128n,
+                                           float newsc, double rnew, double rfac, double rden, int lane,
+                                           uint32_t& keep, float& amax) {
   constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
   constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
   constexpr bool MOM = CODEC != KAON_MOM_NONE;
-  constexpr bool NEEDP = PHASE == 6 || WD;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
+  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
   const ku4 gv4 = in.g, pv4 = in.p, mb16 = in.m16;
   const ku2 mi8 = in.m8;
   const uint32_t m4 = in.m4;
   float f[8];
-  if (OPT == KAON_OPT_ADAKAON) {
+  if (OPT == KAON_OPT_ADAKAON || PNM) {
     f[0] = in.c0.x; f[1] = in.c0.y; f[2] = in.c0.z; f[3] = in.c0.w;
     f[4] = in.c1.x; f[5] = in.c1.y; f[6] = in.c1.z; f[7] = in.c1.w;
   }
@@ -2385,6 +2419,26 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
       mold[i] = 0.0f;
     }
   }
+  // AdaPNM: the negative buffer, dequantized as the positive one
+  float mng[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mng[i] = 0.0f;
+    if (!PNM) continue;
+    if (CODEC == KAON_MOM_INT8) {
+      const uint32_t w = i < 4 ? in.n8.x : in.n8.y;
+      if (DQX)
+        mng[i] = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * negsc;
+      else
+        mng[i] = __fmaf_rn((float)(((w ^ 0x80808080u) >> (8 * (i & 3))) & 0xFFu), negsc, m128n);
+    } else if (CODEC == KAON_MOM_4BIT) {
+      mng[i] = ((float)((in.n4 >> (4 * i)) & 0xFu) - 8.0f) * in.bn;
+    } else if (CODEC == KAON_MOM_BF16) {
+      const uint32_t nw[4] = {in.n16.x, in.n16.y, in.n16.z, in.n16.w};
+      const uint32_t w = nw[i >> 1];
+      mng[i] = (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
+    }
+  }
   float d[8], mf[8];
   uint32_t mbits[8];
 #pragma unroll
@@ -2392,7 +2446,16 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     float pw = p[i];
     if (NKR && NEEDP) pw = bf2f(sr_bf16(p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old), nz0[i]));
     p[i] = pw;
-    if (OPT == KAON_OPT_ADAKAON) {
+    if (PNM) {
+      // this step's positive buffer (decay beta1^2), the pos-neg mix, the
+      // factored preconditioner with the bias correction, clip and lr
+      const float mfv = __fmaf_rn(hp.a1, g[i], mold[i] * hp.b1);
+      const float pn = __fmaf_rn(hp.pn_neg, mng[i], mfv * hp.pn_pos) * hp.pn_rnorm;
+      const float u = pn * ((rf * f[i]) * hp.bc2);
+      d[i] = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
+      mf[i] = mfv;
+      if (CODEC == KAON_MOM_BF16) mbits[i] = f2bf(mfv);
+    } else if (OPT == KAON_OPT_ADAKAON) {
       const float u = (g[i] * rf) * f[i];
       const float ud = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
       if (CODEC == KAON_MOM_BF16) {
@@ -2412,13 +2475,14 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
       mf[i] = __fmaf_rn(hp.a2, g[i], mold[i] * hp.b2);
       if (CODEC == KAON_MOM_BF16) mbits[i] = f2bf(mf[i]);
     }
-    if (WD) d[i] = __fmaf_rn(hp.wdl, pw, d[i]);
+    if (WD && !PNM) d[i] = __fmaf_rn(hp.wdl, pw, d[i]);
   }
   if (PHASE == 5) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (CAUT) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
-      if (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) amax = fmaxf(amax, fabsf(mf[i]));
+      // AdaPNM's absmax of the new positive buffer comes from its clip-sum pass
+      if ((CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM) amax = fmaxf(amax, fabsf(mf[i]));
     }
     return;
   }
@@ -2448,7 +2512,9 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     float dd = d[i];
     if (CAUT) dd = div_r64(d[i] * (d[i] * g[i] > 0.0f ? 1.0f : 0.0f), rden);
     if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
-    o[i] = sr_word(p[i] - dd, nz1[i]);
+    // AdaPNM's decoupled decay p * (1 - lr wd), rounded to the param dtype
+    const float pd = PNM && WD ? rbf(p[i] * hp.wdl) : p[i];
+    o[i] = sr_word(pd - dd, nz1[i]);
     if (NKC) o[i] = sr_word(__uint_as_float(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
   }
   ku4 ov;
@@ -2486,6 +2552,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   constexpr bool CAUT = FLAGS & FF_CAUT;
   constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
   __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
@@ -2496,8 +2563,12 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   FastCtx X;
   X.g = (const KAON_G uint8_t*)G(T.g);
   X.p = (KAON_G uint8_t*)G(T.p);
-  X.m = (KAON_G uint8_t*)G(T.m);
-  X.msc = (KAON_G uint8_t*)G(T.m_scale);
+  // AdaPNM: m is this step's positive buffer (m on odd steps, m2 on even ones)
+  const bool swap = PNM && (hp.step & 1u) == 0u;
+  X.m = (KAON_G uint8_t*)G(swap ? T.m2 : T.m);
+  X.msc = (KAON_G uint8_t*)G(swap ? T.m2_scale : T.m_scale);
+  X.m2 = (const KAON_G uint8_t*)G(swap ? T.m : T.m2);
+  X.m2sc = (const KAON_G uint8_t*)G(swap ? T.m_scale : T.m2_scale);
   X.cf = (const KAON_G uint8_t*)ws.cf(T);
   X.bamax = (KAON_G uint8_t*)ws.bamax(T);
   X.boldsc = CODEC == KAON_MOM_4BIT ? (KAON_G uint8_t*)ws.boldsc(T, nblocks4(T)) : X.bamax;
@@ -2509,7 +2580,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   X.GL = CODEC == KAON_MOM_4BIT ? (int)(T.block4 >> 3) : 1;
 
   // clip divisor of the tensor (phase 4)
-  const float fac = OPT == KAON_OPT_ADAKAON ? ws.scal(T)[0] : 1.0f;
+  const float fac = OPT == KAON_OPT_ADAKAON || PNM ? ws.scal(T)[0] : 1.0f;
   const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && CAUT) {
@@ -2517,18 +2588,23 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
   uint32_t keep = 0;
-  // Adakaon / Nekaon momentum lerp weight 1 - beta1 (Lion has no lerp)
+  // Adakaon / Nekaon momentum lerp weight 1 - beta1 (Lion has no lerp, AdaPNM an fma)
   const bool wlo = fabsf(hp.w1) < 0.5f;
   // per-row values of the wave's rows, one row per lane
   const int nrows = (int)(wr.re - wr.rb);
   const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
   const float mu_l = (FLAGS & FF_GC) && nrows > 0 ? ws.mu(T)[rl] : 0.0f;
-  const float rf_l = OPT == KAON_OPT_ADAKAON && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
-  const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0 ? (PHASE == 5 ? G(T.m_scale)[rl] : ws.roldsc(T)[rl]) : 1.0f;
+  const float rf_l = (OPT == KAON_OPT_ADAKAON || PNM) && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
+  const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0
+                         ? (PHASE == 5 ? *(const KAON_G float*)(X.msc + 4u * (uint32_t)rl) : ws.roldsc(T)[rl])
+                         : 1.0f;
+  const float ng_l = PNM && CODEC == KAON_MOM_INT8 && nrows > 0 ? *(const KAON_G float*)(X.m2sc + 4u * (uint32_t)rl)
+                                                                : 1.0f;
   const float am_l = CODEC == KAON_MOM_INT8 && PHASE == 6 && nrows > 0 ? __uint_as_float(ws.ramax(T)[rl]) : 0.0f;
   settle(mu_l);
   settle(rf_l);
   settle(sc_l);
+  settle(ng_l);
   settle(am_l);
   // Each row is worked on by L = T.fast_lanes consecutive lanes (a power of
   // two), so a wave covers P = 64 / L rows at a time (a row set); chunk
@@ -2555,7 +2631,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   int rj = 0;        // the lane's row (index into the wave's rows), clamped
   bool valid = false;
   uint32_t rowe = 0;
-  float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f;
+  float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f, negsc = 1.0f, m128n = 0.0f;
   double rnew = 1.0;
   bool dqf = true;
   // One position: arithmetic on `cur`, loads of the next position into `nxt`.
@@ -2568,18 +2644,20 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
       rj = min(ri, nrows - 1);
       rowe = (uint32_t)(wr.rb + rj) * C;
       mu = (FLAGS & FF_GC) ? __shfl(mu_l, rj) : 0.0f;
-      rf = OPT == KAON_OPT_ADAKAON ? __shfl(rf_l, rj) : 1.0f;
+      rf = OPT == KAON_OPT_ADAKAON || PNM ? __shfl(rf_l, rj) : 1.0f;
       if (CODEC == KAON_MOM_INT8) {
         oldsc = __shfl(sc_l, rj);
+        if (PNM) negsc = __shfl(ng_l, rj);
         if (PHASE == 6) {
           newsc = fmaxf(__shfl(am_l, rj), 1e-12f) / 127.0f;
           rnew = rcp64(newsc);
-          if (valid && cl == 0) G(T.m_scale)[wr.rb + rj] = newsc;
+          if (valid && cl == 0) *(KAON_G float*)(X.msc + 4u * (uint32_t)(wr.rb + rj)) = newsc;
         }
       }
       m128 = -128.0f * oldsc;
+      m128n = -128.0f * negsc;
       // fma(ub, sc, -128 sc) is the exact product q*sc while 128*sc is finite
-      dqf = CODEC != KAON_MOM_INT8 || fabsf(oldsc) < 0x1p120f;
+      dqf = CODEC != KAON_MOM_INT8 || (fabsf(oldsc) < 0x1p120f && (!PNM || fabsf(negsc) < 0x1p120f));
       amax = 0.0f;
     }
     int sn = s, kn = k + 1;
@@ -2602,26 +2680,26 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
       if (wlo) {
         if (fac == 1.0f && dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
         else if (dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
         else
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
       } else {
         if (fac == 1.0f && dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
         else if (dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
         else
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
       }
     }
-    if (PHASE == 5 && QUANT) {
+    if (PHASE == 5 && QUANT && !PNM) {
       if (CODEC == KAON_MOM_INT8) {
         amax = fmaxf(amax, camax);
       } else {
@@ -2636,7 +2714,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
         }
       }
     }
-    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && kn == 0) {
+    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && !PNM && kn == 0) {
       // row maxima of the set: reduce over each row's L lanes
       float a = amax;
       for (int o = (int)L / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
@@ -3245,13 +3323,26 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
     hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, h);
     if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
   }
+  // phases 5 and 6: the specialized kernel over the fast slices when one exists
+  // for the configuration, the generic one over the rest
+  const bool fast_cfg = L->n_fast > 0 && h.bf16_method == KAON_SR && h.p_dtype == KAON_BF16 &&
+                        h.g_dtype == KAON_BF16;
+  auto launch_pnm = [&](ElemFn ff, PnmFn fg, const char* what) {
+    const int32_t n_fast = ff ? L->n_fast : 0;
+    if (n_fast > 0)
+      hipLaunchKernelGGL(ff, dim3(n_fast), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
+    if (L->n_elem_items > n_fast)
+      hipLaunchKernelGGL(fg, dim3(L->n_elem_items - n_fast), dim3(KAON_WG), 0, st, L->descs,
+                         L->elem_items + n_fast, ws, h);
+    return check_launch(what);
+  };
   if ((mask & (1u << 5)) && (h.flags & KAON_F_CAUTIOUS) && L->n_elem_items > 0) {
-    hipLaunchKernelGGL(f5, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
-    if ((rc = check_launch("kaon: AdaPNM keep-count launch"))) return rc;
+    ElemFn ff = fast_cfg ? fast_fn<KAON_OPT_ADAPNM, 5>(h.codec, fast_flags(h)) : nullptr;
+    if ((rc = launch_pnm(ff, f5, "kaon: AdaPNM keep-count launch"))) return rc;
   }
   if ((mask & (1u << 6)) && L->n_elem_items > 0) {
-    hipLaunchKernelGGL(f6, dim3(L->n_elem_items), dim3(KAON_WG), 0, st, L->descs, L->elem_items, ws, h);
-    if ((rc = check_launch("kaon: AdaPNM apply launch"))) return rc;
+    ElemFn ff = fast_cfg ? fast_fn<KAON_OPT_ADAPNM, 6>(h.codec, fast_flags(h)) : nullptr;
+    if ((rc = launch_pnm(ff, f6, "kaon: AdaPNM apply launch"))) return rc;
   }
   return 0;
 }

@@ -8,8 +8,9 @@ factored / 1-D second moment, max_v and the kahan shift, over several steps
 so that each buffer is the positive one more than once.  Extra cases cover
 what the golden ones do not: rows long enough for several runs, ragged rows
 (C % 8 != 0, the scalar path), 4-bit blocks spanning rows, fp32 params with
-bf16 grads and the reverse, AMSBound, clip 0, no cautious / no GC, and the
-SDXL set's largest conv.
+bf16 grads and the reverse, AMSBound, clip 0, no cautious / no GC, rows the
+specialized keep-count / apply kernel takes (every codec, with and without
+weight decay), and the SDXL set's largest conv.
 """
 import io
 
@@ -65,6 +66,13 @@ EXTRA = {
                                                      gradient_centralization=False)),
     "kahan_int8": _case([[40, 24], [56]], dict(lr=1e-3, momentum_dtype="int8", bf16_method="kahan")),
     "beta1_zero": _case([[32, 16], [20]], dict(lr=1e-3, betas=(0.0, 0.99), momentum_dtype="bfloat16")),
+    # rows the specialized keep-count / apply kernel takes (bf16 p and g, SR, C % 8 == 0,
+    # 4-bit blocks tiling the rows), each buffer positive twice
+    "fast_4bit_b128": _case([[256, 2048], [128, 128, 3, 3], [96]], dict(lr=1e-3, momentum_dtype="4bit",
+                                                                        momentum_4bit_block=128)),
+    "fast_bf16_wd": _case([[320, 1280], [64, 640]], dict(lr=1e-3, momentum_dtype="bfloat16", weight_decay=0.1)),
+    "fast_int8_noclip": _case([[200, 512], [48, 32, 3, 3]], dict(lr=2e-3, momentum_dtype="int8", clip_threshold=0.0,
+                                                                 beta0=1.0)),
 }
 
 

@@ -4,7 +4,10 @@ Metric: Gparam/s and % of the HBM roofline per optimizer step.
 Default workload = BASELINE configs[2]: Adakaon, betas (0.9, 0.999), int8
 momentum, cautious, gradient centralization, stochastic-rounding bf16 writes,
 lr 1e-4 (the north star's target config).  ``--workload lion_int8``
-(configs[1]) and ``nekaon_4bit`` select the others.
+(configs[1]), ``nekaon_4bit_b64`` / ``nekaon_4bit_b256`` (configs[3]'s two block
+sizes; ``nekaon_4bit`` keeps Nekaon's default 128), ``adamuon_int8``
+(configs[4]) and the adjacent optimizers (``adapnm_*``, ``kprodigy_*``,
+``msam_int8``, ``lora_bag``) select the others.
 
 A "step" is one ``optimizer.step()`` over all 1,678 tensors with the params,
 grads and optimizer state resident in HBM.  W untimed warmup steps (the first
@@ -46,6 +49,15 @@ WORKLOADS = {
                              "lr 1e-4, 1% Student-t outliers", opt="nekaon",
                         kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=128),
                         bm=0.5, outliers=0.01),
+    # configs[3] names block sizes 64 and 256 (the default workload above keeps Nekaon's default 128)
+    "nekaon_4bit_b64": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 64, wd 0.1, cautious, GC, SR bf16, "
+                                 "lr 1e-4, 1% Student-t outliers", opt="nekaon",
+                            kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=64),
+                            bm=0.5, outliers=0.01),
+    "nekaon_4bit_b256": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 256, wd 0.1, cautious, GC, SR "
+                                  "bf16, lr 1e-4, 1% Student-t outliers", opt="nekaon",
+                             kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=256),
+                             bm=0.5, outliers=0.01),
     "adamuon_int8": dict(desc="configs[4]: AdaMuon ns_steps=2, betas=(0.95,0.999), int8 momentum, factored 2nd "
                               "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
                               "params on the Adakaon path", opt="adamuon",

@@ -964,6 +964,26 @@ __device__ __forceinline__ float dq_int8(uint32_t byte, float sc, float m128sc, 
   return (float)(int8_t)(uint8_t)byte * sc;
 }
 
+// The |m| maxima of 4-bit blocks that cross chunks or rows: the elements a
+// thread visits in one block are reduced in registers and stored with one
+// atomic per run (NaN never enters: fmaxf keeps its other operand, as the
+// per-element form skipped NaN).
+struct BlkMax {
+  uint32_t blk = 0xFFFFFFFFu;
+  float mx = 0.0f;
+  __device__ __forceinline__ void flush(KAON_G uint32_t* bamax) {
+    if (blk != 0xFFFFFFFFu && mx > 0.0f) atomicMax((uint32_t*)&bamax[blk], __float_as_uint(mx));
+  }
+  __device__ __forceinline__ void add(KAON_G uint32_t* bamax, uint32_t b, float ax) {
+    if (b != blk) {
+      flush(bamax);
+      blk = b;
+      mx = 0.0f;
+    }
+    mx = fmaxf(mx, ax);
+  }
+};
+
 // =============================================================== AdaMuon momentum
 // The first moment of the raw gradient (adamuon.py:570-573 via the codecs'
 // ema_one, _momentum_codec.py:266-269, 303-308, 363-371): M = lerp(m, g, 1 -
@@ -1018,6 +1038,7 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
     }
     const float oldsc = CODEC == KAON_MOM_INT8 && mom ? uniform_f(G(T.m_scale)[r]) : 1.0f;
     float amax = 0.0f, sq = 0.0f;
+    BlkMax bm4;
     for (int k = 0; k < cpl; ++k) {
       const int64_t c = wr.lane + 64 * k;
       const int cnt = chunk_cnt(c, C);
@@ -1052,13 +1073,12 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
         } else if (CODEC == KAON_MOM_INT8) {
           Mv[i] = klerp(dq_int8(mq[i], oldsc, -128.0f * oldsc, fabsf(oldsc) < 0x1p120f), g[i], hp.w1);
           amax = fmaxf(amax, fabsf(Mv[i]));
-        } else {  // 4-bit: flat blocks, possibly across rows
-          const int64_t e = e0 + i, blk = e / B;
+        } else {  // 4-bit: flat blocks, possibly across rows (32-bit: n < 2^31)
+          const uint32_t e = (uint32_t)e0 + (uint32_t)i, blk = e / (uint32_t)B;
           const float sc = G(T.m_scale)[blk];
           Mv[i] = klerp(((float)mq[i] - 8.0f) * sc, g[i], hp.w1);
-          const float ax = fabsf(Mv[i]);
-          if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
-          if (e == blk * B) ws.boldsc(T, nb)[blk] = sc;
+          bm4.add(ws.bamax(T), blk, fabsf(Mv[i]));
+          if (e == blk * (uint32_t)B) ws.boldsc(T, nb)[blk] = sc;
         }
         const uint32_t xb = f2bf(Mv[i]);
         const float xf = bf2f(xb);
@@ -1073,6 +1093,7 @@ __global__ __launch_bounds__(KAON_WG) void k_muon_mom(const KaonTensor* __restri
       }
       if (mom && (CODEC == KAON_MOM_BF16 || CODEC == KAON_MOM_F32)) st_mom_raw<CODEC>(T, e0, cnt, vv, qout);
     }
+    if (CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
     if (CODEC == KAON_MOM_INT8 && mom) {
       const float am = wave_max(amax);
       if (wr.lane == 0) {
@@ -1148,6 +1169,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const int64_t GL = CODEC == KAON_MOM_4BIT && B >= 8 ? B / 8 : 1;
   const bool blk_fast = CODEC == KAON_MOM_4BIT && B % 8 == 0 && C % B == 0 && GL <= 64 && (64 % GL) == 0 && vec_t;
   uint32_t keep = 0;
+  BlkMax bm4;  // 4-bit blocks across chunks or rows (phase 5)
 
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     // ---- per-row context (wave-uniform)
@@ -1260,18 +1282,30 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       uint32_t qout[8];
       float dout[8], mnew[8];
       float chunk_amax = 0.0f;
+      // 4-bit blocks that cross chunks or rows: the chunk's first block and offset
+      // (one 32-bit division, n < 2^31), then walked element by element
+      uint32_t wblk = 0u, woff = 0u;
+      if (CODEC == KAON_MOM_4BIT && mom && !blk_fast) {
+        wblk = (uint32_t)e0 / (uint32_t)B;
+        woff = (uint32_t)e0 - wblk * (uint32_t)B;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qout[i] = mq[i];
         dout[i] = 0.0f;
         mnew[i] = 0.0f;
         if (i >= cnt) continue;
-        const int64_t e = e0 + i;
         float sc4_old = b_old, sc4_new = b_new;
         double r4 = b_rnew;
         int64_t blk_e = blk;
+        bool blk_first = false;  // the element opens its block
         if (CODEC == KAON_MOM_4BIT && mom && !blk_fast) {
-          blk_e = e / B;
+          blk_e = wblk;
+          blk_first = woff == 0u;
+          if (++woff == (uint32_t)B) {
+            woff = 0u;
+            ++wblk;
+          }
           sc4_old = PHASE == 5 ? T.m_scale[blk_e] : ws.boldsc(T, nb)[blk_e];
           if (PHASE == 6) {
             sc4_new = fmaxf(__uint_as_float(ws.bamax(T)[blk_e]), 1e-12f) / 7.0f;
@@ -1330,8 +1364,8 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
           if (quant) {
             const float ax = fabsf(mfv);
             if (CODEC == KAON_MOM_4BIT && !blk_fast) {
-              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk_e], __float_as_uint(ax));
-              if (e == blk_e * B) ws.boldsc(T, nb)[blk_e] = sc4_old;
+              bm4.add(ws.bamax(T), (uint32_t)blk_e, ax);
+              if (blk_first) ws.boldsc(T, nb)[blk_e] = sc4_old;
             } else {
               chunk_amax = fmaxf(chunk_amax, ax);
             }
@@ -1349,7 +1383,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
               x = fminf(fmaxf(x, -7.0f), 7.0f);
               qout[i] = (uint32_t)((int)x + 8);
               mdeq = x * sc4_new;
-              if (!blk_fast && e == blk_e * B) T.m_scale[blk_e] = sc4_new;
+              if (!blk_fast && blk_first) T.m_scale[blk_e] = sc4_new;
             }
           } else if (mom) {
             mdeq = CODEC == KAON_MOM_BF16 ? bf2f(qout[i]) : __uint_as_float(qout[i]);
@@ -1436,6 +1470,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
     }
   }
 
+  if (PHASE == 5 && CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
   if (PHASE == 5 && cautious) {
     const uint32_t wsum = wave_sum_u32(keep);
     if (wr.lane == 0) keep_s[wr.w] = wsum;
@@ -1502,6 +1537,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
   }
   const float* fsrc = factored ? (const float*)ws.cf(T) : (ams ? T.max_v : T.v);
   uint32_t keep = 0;
+  BlkMax bm4;  // 4-bit blocks across chunks or rows (phase 3)
 
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
@@ -1563,18 +1599,30 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
       }
       uint32_t qout[8];
       float dout[8];
+      // 4-bit: the chunk's first block and offset (one 32-bit division, n < 2^31),
+      // then walked element by element
+      uint32_t wblk = 0u, woff = 0u;
+      if (CODEC == KAON_MOM_4BIT) {
+        wblk = (uint32_t)e0 / (uint32_t)B;
+        woff = (uint32_t)e0 - wblk * (uint32_t)B;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qout[i] = mq[i];
         dout[i] = 0.0f;
         if (i >= cnt) continue;
-        const int64_t e = e0 + i;
         // 4-bit block scales of the element
         int64_t blk = 0;
+        bool blk_first = false;  // the element opens its block
         float sc4o = 1.0f, sc4n = 1.0f, sc4g = 1.0f;
         double r4 = 1.0;
         if (CODEC == KAON_MOM_4BIT) {
-          blk = e / B;
+          blk = wblk;
+          blk_first = woff == 0u;
+          if (++woff == (uint32_t)B) {
+            woff = 0u;
+            ++wblk;
+          }
           sc4o = PHASE == 6 ? ws.boldsc(T, nb)[blk] : G(spos)[blk];
           sc4g = G(sneg)[blk];
           if (PHASE == 6) {
@@ -1607,8 +1655,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
             if (CODEC == KAON_MOM_INT8) {
               row_amax = fmaxf(row_amax, ax);
             } else {
-              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
-              if (e == blk * B) ws.boldsc(T, nb)[blk] = sc4o;
+              bm4.add(ws.bamax(T), (uint32_t)blk, ax);
+              if (blk_first) ws.boldsc(T, nb)[blk] = sc4o;
             }
           }
           continue;
@@ -1627,7 +1675,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
           float x = rintf(div_r64(mfv, r4));
           x = fminf(fmaxf(x, -7.0f), 7.0f);
           qout[i] = (uint32_t)((int)x + 8);
-          if (e == blk * B) G(spos)[blk] = sc4n;
+          if (blk_first) G(spos)[blk] = sc4n;
         } else if (CODEC == KAON_MOM_BF16) {
           qout[i] = f2bf(mfv);
         } else {
@@ -1684,6 +1732,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
     }
   }
 
+  if (PHASE == 3 && CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
   if (PHASE == 5 && cautious) {
     const uint32_t wsum = wave_sum_u32(keep);
     if (wr.lane == 0) keep_s[wr.w] = wsum;
@@ -1802,6 +1851,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
   const bool coupled = (hp.flags & KAON_F_PD_COUPLED) != 0;
   const float tgb = rbf(hp.pd_tg);
   const int nsl = run_slices(it);
+  BlkMax bm4;  // 4-bit blocks across chunks or rows
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nsl; ++sl) {
   const WaveRows wr = wave_rows(slice_item(it, sl));
@@ -1864,6 +1914,12 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
           }
           st_mom_at<CODEC>(T.m, T.n, e0, cnt, vv, mq);
         } else {
+          // 4-bit: the chunk's first block and offset (32-bit, n < 2^31), then walked
+          uint32_t wblk = 0u, woff = 0u;
+          if (CODEC == KAON_MOM_4BIT) {
+            wblk = (uint32_t)e0 / (uint32_t)T.block4;
+            woff = (uint32_t)e0 - wblk * (uint32_t)T.block4;
+          }
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             if (i >= cnt) continue;
@@ -1871,12 +1927,16 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
               const float mf = __fmaf_rn(hp.pd_tg, g[i], dq_int8(mq[i], oldsc, -128.0f * oldsc, dqf) * hp.b1);
               amax = fmaxf(amax, fabsf(mf));
             } else {
-              const int64_t e = e0 + i, blk = e / T.block4;
+              const uint32_t blk = wblk;
+              const bool blk_first = woff == 0u;
+              if (++woff == (uint32_t)T.block4) {
+                woff = 0u;
+                ++wblk;
+              }
               const float sc = G(T.m_scale)[blk];
               const float mf = klerp(((float)mq[i] - 8.0f) * sc, g[i] * hp.pd_d, hp.w1);
-              const float ax = fabsf(mf);
-              if (ax == ax) atomicMax((uint32_t*)&ws.bamax(T)[blk], __float_as_uint(ax));
-              if (e == blk * (int64_t)T.block4) ws.boldsc(T, nblocks4(T))[blk] = sc;
+              bm4.add(ws.bamax(T), blk, fabsf(mf));
+              if (blk_first) ws.boldsc(T, nblocks4(T))[blk] = sc;
             }
           }
         }
@@ -1898,6 +1958,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
     }
   }
   }
+  if (CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
 }
 
 // Pass 1, D statistics: one wave per flat item of KAON_FLAT_ITEM sliced
@@ -2112,12 +2173,17 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
       }
       uint32_t qout[8];
       float dout[8];
+      // 4-bit: the chunk's first block and offset, walked element by element
+      uint32_t wblk = 0u, woff = 0u;
+      if (CODEC == KAON_MOM_4BIT) {
+        wblk = (uint32_t)e0 / (uint32_t)B;
+        woff = (uint32_t)e0 - wblk * (uint32_t)B;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qout[i] = mq[i];
         dout[i] = 0.0f;
         if (i >= cnt) continue;
-        const int64_t e = e0 + i;
         const float gq = coupled ? __fmaf_rn(hp.wdl, p[i], g[i]) : g[i];
         float numer;
         if (CODEC == KAON_MOM_NONE) {
@@ -2133,7 +2199,12 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
           qout[i] = (uint32_t)(uint8_t)(int8_t)x;
           numer = x * newsc;
         } else {
-          const int64_t blk = e / B;
+          const int64_t blk = wblk;
+          const bool blk_first = woff == 0u;
+          if (++woff == (uint32_t)B) {
+            woff = 0u;
+            ++wblk;
+          }
           const float sco = ws.boldsc(T, nb)[blk];
           const float scn = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
           const float mf = klerp(((float)mq[i] - 8.0f) * sco, gq * hp.pd_d, hp.w1);
@@ -2141,7 +2212,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
           x = fminf(fmaxf(x, -7.0f), 7.0f);
           qout[i] = (uint32_t)((int)x + 8);
           numer = x * scn;
-          if (PHASE == 6 && e == blk * B) G(T.m_scale)[blk] = scn;
+          if (PHASE == 6 && blk_first) G(T.m_scale)[blk] = scn;
         }
         const float u = factored ? numer * fminf((rf * f[i]) / hp.pd_dn, hp.pd_cap)
                                  : numer / fmaxf(sqrtf(f[i]), hp.pd_floor);

@@ -88,7 +88,7 @@ int row_class(const KaonTensor& t, int32_t g_dtype) {
 // grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
 // momentum blocks of 8*G elements (G | 64) that tile the rows.
 bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
-  if (a.opt == KAON_OPT_ADAMUON || a.opt == KAON_OPT_KPRODIGY) return false;
+  if (a.opt == KAON_OPT_KPRODIGY) return false;
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
   if (!t.factored || !t.vec_rows || t.C % 8 != 0) return false;
   if (a.codec == KAON_MOM_F32) return false;

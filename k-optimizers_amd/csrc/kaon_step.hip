@@ -2309,6 +2309,7 @@ struct FastCtx {
   const KAON_G uint16_t* nz[3];  // injected noise streams, or null
   const KAON_G uint8_t* m2;      // AdaPNM: the negative buffer (read only)
   const KAON_G uint8_t* m2sc;    // AdaPNM: its scales
+  const KAON_G uint8_t* o;       // AdaMuon: the orthogonal factor O (bf16, row-major like g)
   uint32_t tid;                  // Philox tensor id
   int bsh;                       // 4-bit: log2 of the block size
   int GL;                        // 4-bit: lanes per block
@@ -2345,7 +2346,15 @@ struct FastIn {
   ku2 n8;
   uint32_t n4;
   float bn;
+  ku4 o;         // AdaMuon: O
 };
+
+// AdaMuon's keep count reads no momentum (the update is O's; the momentum of
+// the raw grad was stepped and its absmax taken by the momentum pass)
+template <int OPT, int PHASE>
+constexpr bool fast_reads_m() {
+  return !(OPT == KAON_OPT_ADAMUON && PHASE == 5);
+}
 
 // Which passes of the specialized kernel read the weights: the apply, and for
 // Adakaon's coupled form of weight decay also the keep count (AdaPNM decays p
@@ -2358,24 +2367,26 @@ constexpr bool fast_needs_p() {
 template <int OPT, int PHASE, int CODEC, int FLAGS>
 __device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t e0, uint32_t j0) {
   constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
+  constexpr bool RM = fast_reads_m<OPT, PHASE>();
   const ku4 z4 = ku4{0u, 0u, 0u, 0u};
   in.g = ld_stream<true>((const KAON_G ku4*)(X.g + 2u * e0));
   in.p = NEEDP ? ld_stream<true>((const KAON_G ku4*)(X.p + 2u * e0)) : z4;
-  in.m8 = CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m + e0)) : ku2{0u, 0u};
-  in.m4 = CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m + (e0 >> 1))) : 0u;
-  in.m16 = CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m + 2u * e0)) : z4;
+  in.o = MUON ? *(const KAON_G ku4*)(X.o + 2u * e0) : z4;
+  in.m8 = RM && CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m + e0)) : ku2{0u, 0u};
+  in.m4 = RM && CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m + (e0 >> 1))) : 0u;
+  in.m16 = RM && CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m + 2u * e0)) : z4;
   in.n8 = PNM && CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m2 + e0)) : ku2{0u, 0u};
   in.n4 = PNM && CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m2 + (e0 >> 1))) : 0u;
   in.n16 = PNM && CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m2 + 2u * e0)) : z4;
-  if (OPT == KAON_OPT_ADAKAON || PNM) {
+  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
     in.c0 = *(const KAON_G kf4*)(X.cf + 4u * j0);
     in.c1 = *(const KAON_G kf4*)(X.cf + 4u * j0 + 16u);
   } else {
     in.c0 = in.c1 = kf4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   in.bo = in.ba = in.bn = 0.0f;
-  if (CODEC == KAON_MOM_4BIT) {
+  if (CODEC == KAON_MOM_4BIT && RM) {
     const uint32_t blk4 = (e0 >> X.bsh) * 4u;
     in.bo = *(const KAON_G float*)((PHASE == 5 ? X.msc : X.boldsc) + blk4);
     if (PHASE == 6) in.ba = *(const KAON_G float*)(X.bamax + blk4);
@@ -2388,19 +2399,23 @@ __device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t
 template <int OPT, int PHASE, int CODEC, int FLAGS>
 __device__ __forceinline__ void fast_settle(const FastIn& in) {
   constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
+  constexpr bool RM = fast_reads_m<OPT, PHASE>();
   settle(in.g.x); settle(in.g.y); settle(in.g.z); settle(in.g.w);
+  if (MUON) {
+    settle(in.o.x); settle(in.o.y); settle(in.o.z); settle(in.o.w);
+  }
   if (NEEDP) {
     settle(in.p.x); settle(in.p.y); settle(in.p.z); settle(in.p.w);
   }
-  if (CODEC == KAON_MOM_INT8) {
+  if (RM && CODEC == KAON_MOM_INT8) {
     settle(in.m8.x); settle(in.m8.y);
   }
-  if (CODEC == KAON_MOM_4BIT) {
+  if (RM && CODEC == KAON_MOM_4BIT) {
     settle(in.m4); settle(in.bo);
     if (PHASE == 6) settle(in.ba);
   }
-  if (CODEC == KAON_MOM_BF16) {
+  if (RM && CODEC == KAON_MOM_BF16) {
     settle(in.m16.x); settle(in.m16.y); settle(in.m16.z); settle(in.m16.w);
   }
   if (PNM) {
@@ -2414,7 +2429,7 @@ __device__ __forceinline__ void fast_settle(const FastIn& in) {
       settle(in.n16.x); settle(in.n16.y); settle(in.n16.z); settle(in.n16.w);
     }
   }
-  if (OPT == KAON_OPT_ADAKAON || PNM) {
+  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
     settle(in.c0.x); settle(in.c0.y); settle(in.c0.z); settle(in.c0.w);
     settle(in.c1.x); settle(in.c1.y); settle(in.c1.z); settle(in.c1.w);
   }
@@ -2432,13 +2447,13 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
   constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
   constexpr bool MOM = CODEC != KAON_MOM_NONE;
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
   constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
   const ku4 gv4 = in.g, pv4 = in.p, mb16 = in.m16;
   const ku2 mi8 = in.m8;
   const uint32_t m4 = in.m4;
   float f[8];
-  if (OPT == KAON_OPT_ADAKAON || PNM) {
+  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
     f[0] = in.c0.x; f[1] = in.c0.y; f[2] = in.c0.z; f[3] = in.c0.w;
     f[4] = in.c1.x; f[5] = in.c1.y; f[6] = in.c1.z; f[7] = in.c1.w;
   }
@@ -2510,14 +2525,21 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
       mng[i] = (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
     }
   }
-  float d[8], mf[8];
+  float d[8], mf[8], of[8];
   uint32_t mbits[8];
+  if (MUON) unpack8(in.o, of);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float pw = p[i];
     if (NKR && NEEDP) pw = bf2f(sr_bf16(p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old), nz0[i]));
     p[i] = pw;
-    if (PNM) {
+    if (MUON) {
+      // the update is O's (factored, clipped, lr = 0.2 lr); the momentum of the
+      // raw grad is requantized in the apply
+      const float u = (of[i] * rf) * f[i];
+      d[i] = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
+      mf[i] = PHASE == 6 ? klerp_b<WLO>(mold[i], g[i], hp.w1) : 0.0f;
+    } else if (PNM) {
       // this step's positive buffer (decay beta1^2), the pos-neg mix, the
       // factored preconditioner with the bias correction, clip and lr
       const float mfv = __fmaf_rn(hp.a1, g[i], mold[i] * hp.b1);
@@ -2552,8 +2574,9 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (CAUT) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
-      // AdaPNM's absmax of the new positive buffer comes from its clip-sum pass
-      if ((CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM) amax = fmaxf(amax, fabsf(mf[i]));
+      // AdaPNM's absmax of the new positive buffer comes from its clip-sum pass,
+      // AdaMuon's from its momentum pass
+      if ((CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON) amax = fmaxf(amax, fabsf(mf[i]));
     }
     return;
   }
@@ -2623,7 +2646,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   constexpr bool CAUT = FLAGS & FF_CAUT;
   constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM;
+  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
   __shared__ uint32_t keep_s[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
@@ -2640,6 +2663,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   X.msc = (KAON_G uint8_t*)G(swap ? T.m2_scale : T.m_scale);
   X.m2 = (const KAON_G uint8_t*)G(swap ? T.m : T.m2);
   X.m2sc = (const KAON_G uint8_t*)G(swap ? T.m_scale : T.m2_scale);
+  X.o = MUON ? (const KAON_G uint8_t*)G(ws.mo(T)) : nullptr;
   X.cf = (const KAON_G uint8_t*)ws.cf(T);
   X.bamax = (KAON_G uint8_t*)ws.bamax(T);
   X.boldsc = CODEC == KAON_MOM_4BIT ? (KAON_G uint8_t*)ws.boldsc(T, nblocks4(T)) : X.bamax;
@@ -2651,7 +2675,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   X.GL = CODEC == KAON_MOM_4BIT ? (int)(T.block4 >> 3) : 1;
 
   // clip divisor of the tensor (phase 4)
-  const float fac = OPT == KAON_OPT_ADAKAON || PNM ? ws.scal(T)[0] : 1.0f;
+  const float fac = OPT == KAON_OPT_ADAKAON || PNM || MUON ? ws.scal(T)[0] : 1.0f;
   const double rfac = rcp64(fac);
   double rden = 1.0;
   if (PHASE == 6 && CAUT) {
@@ -2665,7 +2689,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   const int nrows = (int)(wr.re - wr.rb);
   const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
   const float mu_l = (FLAGS & FF_GC) && nrows > 0 ? ws.mu(T)[rl] : 0.0f;
-  const float rf_l = (OPT == KAON_OPT_ADAKAON || PNM) && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
+  const float rf_l = (OPT == KAON_OPT_ADAKAON || PNM || MUON) && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
   const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0
                          ? (PHASE == 5 ? *(const KAON_G float*)(X.msc + 4u * (uint32_t)rl) : ws.roldsc(T)[rl])
                          : 1.0f;
@@ -2715,7 +2739,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
       rj = min(ri, nrows - 1);
       rowe = (uint32_t)(wr.rb + rj) * C;
       mu = (FLAGS & FF_GC) ? __shfl(mu_l, rj) : 0.0f;
-      rf = OPT == KAON_OPT_ADAKAON || PNM ? __shfl(rf_l, rj) : 1.0f;
+      rf = OPT == KAON_OPT_ADAKAON || PNM || MUON ? __shfl(rf_l, rj) : 1.0f;
       if (CODEC == KAON_MOM_INT8) {
         oldsc = __shfl(sc_l, rj);
         if (PNM) negsc = __shfl(ng_l, rj);
@@ -2770,7 +2794,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
               X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
       }
     }
-    if (PHASE == 5 && QUANT && !PNM) {
+    if (PHASE == 5 && QUANT && !PNM && !MUON) {
       if (CODEC == KAON_MOM_INT8) {
         amax = fmaxf(amax, camax);
       } else {
@@ -2785,7 +2809,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
         }
       }
     }
-    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && !PNM && kn == 0) {
+    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && !PNM && !MUON && kn == 0) {
       // row maxima of the set: reduce over each row's L lanes
       float a = amax;
       for (int o = (int)L / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
@@ -3011,6 +3035,14 @@ ElemFn elem_fn(int pt, int gt, int codec) {
 // MSAM norm="global": the removal alone)
 template <int OPT, int PHASE, int CODEC>
 ElemFn fast_by_flags(int ff) {
+  if constexpr (OPT == KAON_OPT_ADAMUON) {
+    // int8 / 4-bit momenta (requantized in the apply); GC is off by default
+    if constexpr (CODEC != KAON_MOM_INT8 && CODEC != KAON_MOM_4BIT) return nullptr;
+    switch (ff) {
+      case FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_CAUT>;
+      case FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_CAUT | FF_WD>;
+    }
+  }
   switch (ff) {
     case FF_GC | FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT>;
     case FF_GC | FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD>;
@@ -3044,7 +3076,6 @@ ElemFn fast_by_flags(int ff) {
 
 template <int OPT, int PHASE>
 ElemFn fast_fn(int codec, int ff) {
-  if (OPT == KAON_OPT_ADAMUON) return nullptr;
   if (PHASE == 5) {
     // the climb is a phase-6 write; the removal matters to phase 5 only where it reads
     // the weights (weight decay): drop the flags phase 5 does not look at

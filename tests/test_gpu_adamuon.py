@@ -107,3 +107,47 @@ def test_newton_schulz_orthogonalizes():
     o = _ns_on_gpu(g, 5)
     sv = np.linalg.svd(o.astype(np.float64), compute_uv=False)
     assert sv.min() > 0.5 and sv.max() < 1.3, (sv.min(), sv.max())
+
+
+@pytest.mark.parametrize("md,wd", [("int8", 0.0), ("int8", 0.01), ("4bit", 0.0)])
+def test_specialized_apply_matches_generic_kernel(md, wd):
+    """The keep count and apply on the specialized row-set kernel (bf16 p and g, SR,
+    C % 8 == 0) against the generic kernel on the same inputs: two optimizers over
+    identical params and grads, the second with its plans' fast slices handed to
+    the generic kernel (KaonLaunch.n_fast = 0).  Newton-Schulz runs the same
+    kernels on the same bytes in both, so weights, codes and scales must agree
+    bit for bit."""
+    from kaon_amd import AdaMuon
+
+    print(f"[gpu] adamuon fast vs generic apply {md} wd={wd}", flush=True)
+    shapes = [(320, 1280), (256, 256, 3, 3), (640, 640)]
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    init = [(torch.randn(*s, generator=gen) * 0.02).bfloat16() for s in shapes]
+    grads = [[(torch.randn(*s, generator=gen) * 1e-3).bfloat16() for s in shapes] for _ in range(3)]
+    kw = dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype=md, ns_steps=2, weight_decay=wd)
+    runs = []
+    for generic in (False, True):
+        params = [torch.nn.Parameter(t.clone().cuda()) for t in init]
+        opt = AdaMuon(params, **kw)
+        opt.sr_seed = 17
+        for step, gs in enumerate(grads):
+            # grads copied into the same tensors, so the cached plans stay in use
+            for p, g in zip(params, gs):
+                if p.grad is None:
+                    p.grad = g.clone().cuda()
+                else:
+                    p.grad.copy_(g)
+            if generic and step == 1:
+                for _key, (_ptrs, plan) in opt._plans.items():
+                    assert plan.launch.n_fast > 0
+                    plan.launch.n_fast = 0
+            opt.step()
+        if generic:
+            assert all(plan.launch.n_fast == 0 for _k, (_p, plan) in opt._plans.items())
+        torch.cuda.synchronize()
+        runs.append((params, opt))
+    (pa, oa), (pb, ob) = runs
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert np.array_equal(to_bits(a), to_bits(b)), (md, i, "weights")
+        for k in ("m", "m_scale"):
+            assert np.array_equal(to_bits(oa.state[a][k]).reshape(-1), to_bits(ob.state[b][k]).reshape(-1)), (md, i, k)

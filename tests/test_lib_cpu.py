@@ -304,7 +304,14 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
     for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):
         assert a1 <= b0
     assert spans[-1][1] <= info.ws_words
-    assert info.n_fast == 0
+    # the keep-count / apply slices of tensors with C % 8 == 0 (bf16, SR) go to the
+    # specialized kernel and lead the list
+    elems = (L.KaonItem * info.n_elem_items)()
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, elems, None, None, sq, rect,
+                             ctypes.byref(info)) == 0
+    assert info.n_fast > 0
+    for j in range(info.n_elem_items):
+        assert (j < info.n_fast) == (descs[elems[j].tensor].C % 8 == 0), (j, descs[elems[j].tensor].C)
     # big-tile items lead both lists
     assert (info.n_ns_sq_big, info.n_ns_rect_big) == (nbig_sq, nbig_rect)
     assert all(sq[j].kind == (j < nbig_sq) for j in range(info.n_ns_sq))

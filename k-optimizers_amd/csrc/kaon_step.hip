@@ -1744,6 +1744,145 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
   }
 }
 
+// AdaPNM phase 3 on row class 0 (factored, bf16 g, 16-byte rows with
+// C % 8 == 0, at most 4 chunks per lane) with int8 or bf16 momenta: the same
+// arithmetic and 64-lane row order as k_pnm<3>, with all loads of a group of
+// GR rows (g and both momenta, every chunk of the lane) issued before the
+// group's arithmetic, and the per-row values read once per wave (one row per
+// lane, then read across lanes).  Addresses are clamped to valid rows and
+// chunks, so every load is unconditional.
+template <int CPL, int GR, int CODEC>
+__device__ __forceinline__ void pnm_ss_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
+                                            const KaonHyper& hp) {
+  constexpr bool I8 = CODEC == KAON_MOM_INT8;
+  const uint32_t C = (uint32_t)T.C;
+  const int nch = (int)(C >> 3);
+  const WaveRows wr = wave_rows(it);
+  const int nrows = (int)(wr.re - wr.rb);
+  if (nrows <= 0) return;
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  const bool swap = (hp.step & 1u) == 0u;
+  const KAON_G uint8_t* mpos = (const KAON_G uint8_t*)G(swap ? T.m2 : T.m);
+  const KAON_G uint8_t* mneg = (const KAON_G uint8_t*)G(swap ? T.m : T.m2);
+  const KAON_G float* spos = G(swap ? T.m2_scale : T.m_scale);
+  const KAON_G float* sneg = G(swap ? T.m_scale : T.m2_scale);
+  const KAON_G uint8_t* gb = (const KAON_G uint8_t*)G(T.g);
+  const KAON_G uint8_t* cfb = (const KAON_G uint8_t*)ws.cf(T);
+  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
+  const float mu_l = gc ? ws.mu(T)[rl] : 0.0f;
+  const float rf_l = ws.rf(T)[rl];
+  const float so_l = I8 ? spos[rl] : 1.0f;
+  const float sn_l = I8 ? sneg[rl] : 1.0f;
+  kf4 cfv[CPL][2];  // the column factors of the lane's chunks, held for the wave
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const uint32_t cb = 32u * (uint32_t)min(wr.lane + 64 * k, nch - 1);
+    cfv[k][0] = *(const KAON_G kf4*)(cfb + cb);
+    cfv[k][1] = *(const KAON_G kf4*)(cfb + cb + 16u);
+  }
+  for (int j0 = 0; j0 < nrows; j0 += GR) {
+    ku4 graw[GR][CPL], m16[GR][CPL], n16[GR][CPL];
+    ku2 m8[GR][CPL], n8[GR][CPL];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+      const uint32_t rowe = (uint32_t)(wr.rb + min(j0 + j, nrows - 1)) * C;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const uint32_t e0 = rowe + 8u * (uint32_t)min(wr.lane + 64 * k, nch - 1);
+        graw[j][k] = ld_stream<true>((const KAON_G ku4*)(gb + 2u * e0));
+        if (I8) {
+          m8[j][k] = ld_stream<true>((const KAON_G ku2*)(mpos + e0));
+          n8[j][k] = ld_stream<true>((const KAON_G ku2*)(mneg + e0));
+        } else {
+          m16[j][k] = ld_stream<true>((const KAON_G ku4*)(mpos + 2u * e0));
+          n16[j][k] = ld_stream<true>((const KAON_G ku4*)(mneg + 2u * e0));
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+      const int jj = j0 + j;
+      if (jj >= nrows) continue;
+      const float mu = lane_val(mu_l, jj), rf = lane_val(rf_l, jj);
+      const float oldsc = lane_val(so_l, jj), negsc = lane_val(sn_l, jj);
+      const bool dqf = fabsf(oldsc) < 0x1p120f && fabsf(negsc) < 0x1p120f;
+      const float m128o = -128.0f * oldsc, m128n = -128.0f * negsc;
+      float ss = 0.0f, amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (wr.lane + 64 * k >= nch) continue;
+        float g[8], mo[8], mn[8];
+        unpack8(graw[j][k], g);
+        if (gc) {
+#pragma unroll
+          for (int i = 0; i < 8; i += 2) {
+            float a0 = g[i] - mu, a1 = g[i + 1] - mu;
+            rbf2(a0, a1);
+            g[i] = a0;
+            g[i + 1] = a1;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (I8) {
+            const uint32_t wm = i < 4 ? m8[j][k].x : m8[j][k].y, wn = i < 4 ? n8[j][k].x : n8[j][k].y;
+            mo[i] = dq_int8((wm >> (8 * (i & 3))) & 0xFFu, oldsc, m128o, dqf);
+            mn[i] = dq_int8((wn >> (8 * (i & 3))) & 0xFFu, negsc, m128n, dqf);
+          } else {
+            const uint32_t wm[4] = {m16[j][k].x, m16[j][k].y, m16[j][k].z, m16[j][k].w};
+            const uint32_t wn[4] = {n16[j][k].x, n16[j][k].y, n16[j][k].z, n16[j][k].w};
+            mo[i] = (i & 1) ? __uint_as_float(wm[i >> 1] & 0xFFFF0000u) : __uint_as_float(wm[i >> 1] << 16);
+            mn[i] = (i & 1) ? __uint_as_float(wn[i >> 1] & 0xFFFF0000u) : __uint_as_float(wn[i >> 1] << 16);
+          }
+        }
+        const kf4 c0 = cfv[k][0], c1 = cfv[k][1];
+        const float f[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float mfv = __fmaf_rn(hp.a1, g[i], mo[i] * hp.b1);
+          const float pn = __fmaf_rn(hp.pn_neg, mn[i], mfv * hp.pn_pos) * hp.pn_rnorm;
+          const float u = pn * ((rf * f[i]) * hp.bc2);
+          ss = ss + u * u;
+          if (I8) amax = fmaxf(amax, fabsf(mfv));
+        }
+      }
+      const float s2 = wave_csum(ss);
+      const int64_t r = wr.rb + jj;
+      if (I8) {
+        const float am = wave_max(amax);
+        if (wr.lane == 0) {
+          ws.ramax(T)[r] = __float_as_uint(am);
+          ws.roldsc(T)[r] = oldsc;
+        }
+      }
+      if (wr.lane == 0) ws.rs(T)[r] = s2;
+    }
+  }
+}
+
+// One slice per workgroup, as k_pf_ss.
+template <int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_pnm_ss(const KaonTensor* __restrict__ D,
+                                                    const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
+  const KaonTensor& T = D[it.tensor];
+  const int cpl = (int)(((T.C >> 3) + 63) >> 6);
+  constexpr int W = CODEC == KAON_MOM_INT8 ? 10 : 6;  // rows x chunks held per group
+#define KAON_PNM_SS(N)                                                                 \
+  case N: {                                                                            \
+    constexpr int GR = W / N > 0 ? W / N : 1;                                          \
+    pnm_ss_body<N, GR, CODEC>(T, it, ws, hp);                                          \
+    break;                                                                             \
+  }
+  switch (cpl) {
+    KAON_PNM_SS(1) KAON_PNM_SS(2) KAON_PNM_SS(3) KAON_PNM_SS(4)
+  }
+#undef KAON_PNM_SS
+}
+
 // =============================================================== MSAM norm="global"
 // Sum of squares of the dequantized momentum (_global_mnorm, msam.py:191-199):
 // each row in the 64-lane order into rs[r] (a 1-D tensor is one row); k_msq_fin
@@ -3418,7 +3557,17 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
     if ((rc = check_launch("kaon: k_fin launch"))) return rc;
   }
   if (mask & (1u << 3)) {
-    hipLaunchKernelGGL(f3, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
+    // row class 0 (the leading row items) with int8 / bf16 momenta: the prefetching kernel
+    // (on the longer rows of class 1 it measured slower than the generic one with int8)
+    PnmFn f3p = h.g_dtype != KAON_BF16 ? nullptr
+                : h.codec == KAON_MOM_INT8 ? (PnmFn)k_pnm_ss<KAON_MOM_INT8>
+                : h.codec == KAON_MOM_BF16 ? (PnmFn)k_pnm_ss<KAON_MOM_BF16> : nullptr;
+    const int32_t n0 = f3p ? L->row_runs[0] : 0;
+    if (n0 > 0)
+      hipLaunchKernelGGL(f3p, dim3(n0 * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
+    if (L->n_row_items > n0)
+      hipLaunchKernelGGL(f3, dim3((L->n_row_items - n0) * KAON_RUN), dim3(KAON_WG), 0, st, L->descs,
+                         L->row_items + n0, ws, h);
     if ((rc = check_launch("kaon: AdaPNM clip-sum launch"))) return rc;
   }
   if (mask & (1u << 4)) {

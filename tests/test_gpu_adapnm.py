@@ -73,6 +73,9 @@ EXTRA = {
     "fast_bf16_wd": _case([[320, 1280], [64, 640]], dict(lr=1e-3, momentum_dtype="bfloat16", weight_decay=0.1)),
     "fast_int8_noclip": _case([[200, 512], [48, 32, 3, 3]], dict(lr=2e-3, momentum_dtype="int8", clip_threshold=0.0,
                                                                  beta0=1.0)),
+    # rows of 5 to 10 chunks per lane (the prefetching clip-sum kernel's second row class)
+    "class1_int8": _case([[96, 5120], [64, 320, 3, 3], [40, 2056]], dict(lr=1e-3, momentum_dtype="int8")),
+    "class1_bf16": _case([[48, 4096], [32, 2880]], dict(lr=1e-3, momentum_dtype="bfloat16", weight_decay=0.01)),
 }
 
 

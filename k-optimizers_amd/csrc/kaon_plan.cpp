@@ -86,7 +86,7 @@ int row_class(const KaonTensor& t, int32_t g_dtype) {
 
 // Tensors whose slices take the specialized phase-5/6 kernels: bf16 params and
 // grads, stochastic rounding, factored, 16-byte aligned rows, and for 4-bit
-// momentum blocks of 8*G elements (G | 64) that tile the rows.
+// momentum blocks of 8*G elements (G | 64): whole chunks, inside rows or across them.
 bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
   if (a.opt == KAON_OPT_KPRODIGY) return false;
   if (a.p_dtype != KAON_BF16 || a.g_dtype != KAON_BF16 || a.bf16_method != KAON_SR) return false;
@@ -96,7 +96,7 @@ bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
   if (t.n > (int64_t(1) << 31)) return false;
   if (a.codec == KAON_MOM_4BIT) {
     const int64_t B = t.block4;
-    if (B % 8 != 0 || t.C % B != 0 || B / 8 > 64 || 64 % (B / 8) != 0) return false;
+    if (B % 8 != 0 || B / 8 > 64 || 64 % (B / 8) != 0) return false;
   }
   return true;
 }

@@ -1170,6 +1170,11 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const bool blk_fast = CODEC == KAON_MOM_4BIT && B % 8 == 0 && C % B == 0 && GL <= 64 && (64 % GL) == 0 && vec_t;
   uint32_t keep = 0;
   BlkMax bm4;  // 4-bit blocks across chunks or rows (phase 5)
+  // the scales of the last 4-bit block visited (blocks across chunks or rows):
+  // read once per run of a block's elements
+  uint32_t c_blk = 0xFFFFFFFFu;
+  float c_old = 1.0f, c_new = 1.0f;
+  double c_r = 1.0;
 
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     // ---- per-row context (wave-uniform)
@@ -1306,11 +1311,17 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
             woff = 0u;
             ++wblk;
           }
-          sc4_old = PHASE == 5 ? T.m_scale[blk_e] : ws.boldsc(T, nb)[blk_e];
-          if (PHASE == 6) {
-            sc4_new = fmaxf(__uint_as_float(ws.bamax(T)[blk_e]), 1e-12f) / 7.0f;
-            r4 = rcp64(sc4_new);
+          if ((uint32_t)blk_e != c_blk) {
+            c_blk = (uint32_t)blk_e;
+            c_old = PHASE == 5 ? T.m_scale[blk_e] : ws.boldsc(T, nb)[blk_e];
+            if (PHASE == 6) {
+              c_new = fmaxf(__uint_as_float(ws.bamax(T)[blk_e]), 1e-12f) / 7.0f;
+              c_r = rcp64(c_new);
+            }
           }
+          sc4_old = c_old;
+          sc4_new = c_new;
+          r4 = c_r;
         }
         float mold = 0.0f;
         if (mom) {
@@ -1538,6 +1549,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
   const float* fsrc = factored ? (const float*)ws.cf(T) : (ams ? T.max_v : T.v);
   uint32_t keep = 0;
   BlkMax bm4;  // 4-bit blocks across chunks or rows (phase 3)
+  // the scales of the last 4-bit block visited: read once per run of its elements
+  uint32_t c_blk = 0xFFFFFFFFu;
+  float c_o = 1.0f, c_g = 1.0f, c_n = 1.0f;
+  double c_r = 1.0;
 
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
@@ -1623,12 +1638,19 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
             woff = 0u;
             ++wblk;
           }
-          sc4o = PHASE == 6 ? ws.boldsc(T, nb)[blk] : G(spos)[blk];
-          sc4g = G(sneg)[blk];
-          if (PHASE == 6) {
-            sc4n = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
-            r4 = rcp64(sc4n);
+          if ((uint32_t)blk != c_blk) {
+            c_blk = (uint32_t)blk;
+            c_o = PHASE == 6 ? ws.boldsc(T, nb)[blk] : G(spos)[blk];
+            c_g = G(sneg)[blk];
+            if (PHASE == 6) {
+              c_n = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+              c_r = rcp64(c_n);
+            }
           }
+          sc4o = c_o;
+          sc4g = c_g;
+          sc4n = c_n;
+          r4 = c_r;
         }
         float mold, mng;
         if (CODEC == KAON_MOM_INT8) {
@@ -2257,6 +2279,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
     rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
   }
   uint32_t keep = 0;
+  // the scales of the last 4-bit block visited: read once per run of its elements
+  uint32_t c_blk = 0xFFFFFFFFu;
+  float c_o = 1.0f, c_n = 1.0f;
+  double c_r = 1.0;
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
     const float rf = factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
@@ -2344,10 +2370,15 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
             woff = 0u;
             ++wblk;
           }
-          const float sco = ws.boldsc(T, nb)[blk];
-          const float scn = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+          if ((uint32_t)blk != c_blk) {  // the block's scales, once per run of its elements
+            c_blk = (uint32_t)blk;
+            c_o = ws.boldsc(T, nb)[blk];
+            c_n = fmaxf(__uint_as_float(ws.bamax(T)[blk]), 1e-12f) / 7.0f;
+            c_r = rcp64(c_n);
+          }
+          const float sco = c_o, scn = c_n;
           const float mf = klerp(((float)mq[i] - 8.0f) * sco, gq * hp.pd_d, hp.w1);
-          float x = rintf(div_r64(mf, rcp64(scn)));
+          float x = rintf(div_r64(mf, c_r));
           x = fminf(fmaxf(x, -7.0f), 7.0f);
           qout[i] = (uint32_t)((int)x + 8);
           numer = x * scn;
@@ -2452,6 +2483,7 @@ struct FastCtx {
   uint32_t tid;                  // Philox tensor id
   int bsh;                       // 4-bit: log2 of the block size
   int GL;                        // 4-bit: lanes per block
+  bool xrow;                     // 4-bit: blocks cross rows (C % block != 0)
 };
 
 // noise8 of the chunk at element e0 < 2^31 (the counter's high word is 0).
@@ -2766,7 +2798,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
 #pragma unroll
     for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
     *(KAON_G uint32_t*)(X.m + (e0 >> 1)) = v;
-    if ((lane & (X.GL - 1)) == 0) *(KAON_G float*)(X.msc + blk4) = b_new;
+    if ((e0 & ((1u << X.bsh) - 1u)) == 0u) *(KAON_G float*)(X.msc + blk4) = b_new;  // the block's first chunk
   } else if (CODEC == KAON_MOM_BF16) {
     ku4 mv;
     mv.x = mbits[0] | (mbits[1] << 16);
@@ -2779,7 +2811,8 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
 
 // Fast slices (the planner's fast_eligible tensors): factored, bf16 params and
 // grads, stochastic rounding, 16-byte aligned rows with C % 8 == 0 and, for
-// 4-bit, blocks of 8*G elements with G | 64 that tile the rows.
+// 4-bit, blocks of 8*G elements with G | 64 (blocks that cross rows take one
+// atomic maximum per chunk instead of the lane-group reduction).
 template <int OPT, int PHASE, int CODEC, int FLAGS>
 __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
@@ -2812,6 +2845,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   // 4-bit blocks are 8*GL elements with GL | 64, a power of two
   X.bsh = CODEC == KAON_MOM_4BIT ? __builtin_ctz((uint32_t)T.block4) : 3;
   X.GL = CODEC == KAON_MOM_4BIT ? (int)(T.block4 >> 3) : 1;
+  X.xrow = CODEC == KAON_MOM_4BIT && (T.C % T.block4) != 0;
 
   // clip divisor of the tensor (phase 4)
   const float fac = OPT == KAON_OPT_ADAKAON || PNM || MUON ? ws.scal(T)[0] : 1.0f;
@@ -2936,6 +2970,16 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     if (PHASE == 5 && QUANT && !PNM && !MUON) {
       if (CODEC == KAON_MOM_INT8) {
         amax = fmaxf(amax, camax);
+      } else if (X.xrow) {
+        // 4-bit blocks across rows (a block is still whole chunks): one atomic
+        // maximum per chunk into the block's |m| maximum (zeroed by phase 1)
+        if (full) {
+          const uint32_t e0c = rowe + c * 8u;
+          const uint32_t blk4 = (e0c >> X.bsh) * 4u;
+          if (camax > 0.0f) atomicMax((uint32_t*)(X.bamax + blk4), __float_as_uint(camax));
+          if ((e0c & ((1u << X.bsh) - 1u)) == 0u)
+            *(KAON_G float*)(X.boldsc + blk4) = *(const KAON_G float*)(X.msc + blk4);
+        }
       } else {
         // 4-bit: a block is GL consecutive chunks, GL | L, so its lanes are
         // one aligned group of GL lanes

@@ -91,7 +91,7 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
         it = elems[k]
         d = descs[it.tensor]
         fast = (g_dtype == 1 and d.factored == 1 and d.vec_rows == 1 and d.C % 8 == 0
-                and (codec != 4 or (d.block4 % 8 == 0 and d.C % d.block4 == 0 and 64 % (d.block4 // 8) == 0)))
+                and (codec != 4 or (d.block4 % 8 == 0 and 64 % (d.block4 // 8) == 0)))
         assert (k < info.n_fast) == fast, (k, d.R, d.C)
         covered[it.tensor][it.row0:it.row0 + it.nrows] += 1
         if fast:

@@ -51,6 +51,9 @@
  *   FSUM(x[0..n)) (KProdigy's per-tensor D statistics over the sliced
  *     elements): blocks of 16384 consecutive elements, each summed in CSUM
  *     order, then CSUM over the block sums.
+ *   MSAM's momentum sum of squares (ko_momentum_sumsq): CSUM of m^2 over each
+ *     row, then CSUM over the R row results.  Cross-tensor sums (KProdigy's D
+ *     statistics, MSAM's norm) are added by the caller in param order, fp32.
  */
 #include <math.h>
 #include <stdint.h>

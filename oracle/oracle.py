@@ -22,6 +22,21 @@ reference's per-parameter state layout:
   update folds the per-tensor statistics in param order in fp32, then runs in double)
 
 Arrays: bf16 tensors are ``np.uint16`` bit patterns, fp32 are ``np.float32``.
+
+How it is pinned (tests/):
+
+* the reference's own output on seeded inputs with the oracle's SR noise
+  injected (``tests/golden/``, written by ``tests/golden/make_golden.py``):
+  every optimizer above, bit-exact up to torch's unspecified fp32 reduction
+  order (``test_oracle_golden.py``); KProdigy also per-step D; MSAM's global
+  norm from the reference's per-step momentum, and its step with the
+  reference's norms fed in (``mnorm_feed``), bit-exact;
+* known answers and closed forms: Philox4x32-10 vectors, the SR bit trick,
+  the int8 / 4-bit codecs, CSUM (``test_oracle_kat.py``);
+* torch-CPU arithmetic it mirrors: lerp, add_/addcmul_ fma forms, bf16 GC
+  (``test_oracle_torch_semantics.py``).
+
+Parity unpinned: NaN payload bits (positions are compared).
 """
 from __future__ import annotations
 

@@ -36,6 +36,8 @@ constexpr int TK = 64;              // K per LDS stage
 constexpr int LDK = TK + 8;         // LDS row stride (bf16), breaks bank aliasing
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct NsBufs {
@@ -210,6 +212,11 @@ constexpr int BT = 2 * TILE;     // 256
 constexpr int BK = 64;           // K per stage
 constexpr int BLD = BK + 8;      // LDS row stride (bf16): 144 B, 16-B aligned rows, no bank aliasing
 constexpr int WLD = 128 + 8;     // epilogue staging row stride (bf16): a wave's 128 x 128 tile
+// MODE 2 keeps x as it lies in memory, BK rows of K by BT columns, and reads its
+// MFMA fragments with the LDS transpose read (ds_read_b64_tr_b16): row stride
+// 544 B puts consecutive rows 8 banks apart
+constexpr int XLD = BT + 16;
+static_assert(BK * XLD <= BT * BLD, "the x tile fits the B stage");
 constexpr int NS_LDS = (2 * 2 * BT * BLD > 4 * 128 * WLD) ? 2 * 2 * BT * BLD : 4 * 128 * WLD;
 
 template <int MODE>
@@ -261,14 +268,11 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
         rb[s] = *(const KAON_G ku4*)G(Bop + (int64_t)(col0 + r) * ldb + k0 + kc * 8);
       }
     } else {
-      // x: BK K rows x 256 columns; a thread takes two adjacent K rows of 8
-      // columns, so its transposed LDS writes pack K pairs into 32-bit words
+      // x: BK K rows x 256 columns, 16-byte chunks along its rows
 #pragma unroll
-      for (int s = 0; s < NS / 2; ++s) {
-        const int q = tid + 256 * s, jc = q / (BK / 2), tp = q % (BK / 2);
-        const uint16_t* src = Bop + (int64_t)(k0 + 2 * tp) * ldb + col0 + jc * 8;
-        rb[2 * s] = *(const KAON_G ku4*)G(src);
-        rb[2 * s + 1] = *(const KAON_G ku4*)G(src + ldb);
+      for (int s = 0; s < NS; ++s) {
+        const int q = tid + 256 * s, kr = q / (BT / 8), nc = q % (BT / 8);
+        rb[s] = *(const KAON_G ku4*)G(Bop + (int64_t)(k0 + kr) * ldb + col0 + nc * 8);
       }
     }
   };
@@ -288,11 +292,9 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < NS / 2; ++s) {
-        const int q = tid + 256 * s, jc = q / (BK / 2), tp = q % (BK / 2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *(uint32_t*)&bs[(jc * 8 + e) * BLD + 2 * tp] = half_of(rb[2 * s], e) | (half_of(rb[2 * s + 1], e) << 16);
+      for (int s = 0; s < NS; ++s) {
+        const int q = tid + 256 * s, kr = q / (BT / 8), nc = q % (BT / 8);
+        *(ku4*)&bs[kr * XLD + nc * 8] = rb[s];
       }
     }
   };
@@ -309,9 +311,27 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       fa[buf][i] = *(const bf16x8*)&as[(wm * 128 + i * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+    if (MODE != 2) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      fb[buf][j] = *(const bf16x8*)&bs[(wn * 128 + j * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+      for (int j = 0; j < 4; ++j)
+        fb[buf][j] = *(const bf16x8*)&bs[(wn * 128 + j * 32 + (lane & 31)) * BLD + kk + (lane >> 5) * 8];
+    } else {
+      // Lane l needs x[kk + 8 (l / 32) + 0..7][n0 + l % 32].  In each group of 16
+      // lanes the transpose read gives lane i element i % 4 of the 8-byte chunks
+      // of lanes i / 4 + 4 t (t = 0..3); lane s of the group points at row
+      // kbase + s / 4, columns nbase + 4 (s % 4) .. + 3, so lane i receives
+      // x[kbase + t][nbase + i]: four K values of its column per read, two reads.
+      const int g = lane >> 4, sl = lane & 15;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nbase = wn * 128 + j * 32 + 16 * (g & 1), kbase = kk + 8 * (g >> 1);
+        const uint16_t* p = bs + (kbase + (sl >> 2)) * XLD + nbase + 4 * (sl & 3);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p + 4 * XLD));
+        const v8s c = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        fb[buf][j] = __builtin_bit_cast(bf16x8, c);
+      }
+    }
   };
   auto mma = [&](int buf) {
 #pragma unroll
@@ -321,7 +341,8 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
   };
   constexpr int SG_MFMA = 0x008, SG_VMEM_RD = 0x020, SG_DS_RD = 0x100, SG_DS_WR = 0x200;
-  constexpr int NWR = MODE == 2 ? NS + NS / 2 * 8 / 2 : 2 * NS;  // LDS store instructions per step
+  constexpr int NWR = 2 * NS;  // LDS store instructions per step
+  constexpr int RD2 = MODE == 2 ? 2 : 1;  // MODE 2: 12 fragment reads per sub-step, else 8
 
   const int nk = K / BK;
   gload(0);
@@ -335,25 +356,32 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     gload(min(ks + 1, nk - 1) * BK);
     lfrag(1, as, bs, 16);
     mma(0);
-    __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 8, 0);  // sub-step 0's fragments
+    __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 4 + 4 * RD2, 0);  // sub-step 0's fragments
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
+    for (int g = 0; g < 4; ++g) {
       __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, 2 * NS / 8, 0);
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, 2 * NS / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
     lfrag(0, as, bs, 32);
     mma(1);
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
+    for (int g = 0; g < 4; ++g) {
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
     lfrag(1, as, bs, 48);
     mma(0);
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
+    for (int g = 0; g < 4; ++g) {
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
     lstore(cur ^ 1);  // that stage was last read before the previous barrier

@@ -2130,6 +2130,10 @@ template <int GT, int PT>
 __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restrict__ D,
                                                       const KaonItem* __restrict__ items, int32_t n_items, Ws ws,
                                                       KaonHyper hp) {
+  // sliced tensors (slice_p > 1): each wave stages one round of 512 sliced g
+  // and p values here, loaded lane-interleaved (coalesced), then read back as
+  // the lanes' 8-element chunks; only the wave itself touches its region
+  __shared__ float stage[4][2][512];
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int64_t idx = (int64_t)blockIdx.x * 4 + w;
@@ -2185,19 +2189,35 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
       st8_f32(T.pd_s, j, cnt, vv, sc);
     }
   } else {
-    for (int64_t c = lane; c < nch; c += 64) {
+    float* sg = stage[w][0];
+    float* spv = stage[w][1];
+    for (int64_t t = 0; 64 * t < nch; ++t) {
+      // round t: chunks lane + 64 t, i.e. sliced elements 512 t .. 512 t + 511 of the item
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t jj = 512 * t + lane + 64 * u;
+        float gv = 0.0f, pv = 0.0f;
+        if (jj < len) {
+          const int64_t e = (j0 + jj) * sp;
+          gv = GT == KAON_BF16 ? bf2f(G((const uint16_t*)T.g)[e]) : G((const float*)T.g)[e];
+          pv = PT == KAON_BF16 ? bf2f(G((const uint16_t*)T.p)[e]) : G((const float*)T.p)[e];
+        }
+        sg[lane + 64 * u] = gv;
+        spv[lane + 64 * u] = pv;
+      }
+      // the wave's LDS writes before its reads of other lanes' values
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int64_t c = lane + 64 * t;
       // row of the chunk's first element, then walked by slice_p per element
       const uint32_t e_first = (uint32_t)((j0 + c * 8) * sp);
       uint32_t row = gc ? e_first / (uint32_t)C : 0u, col = gc ? e_first - row * (uint32_t)C : 0u;
       for (int i = 0; i < 8; ++i) {
         const int64_t jj = c * 8 + i;
         if (jj >= len) break;
-        const int64_t j = j0 + jj, e = j * sp;
-        float gv, pv;
-        if (GT == KAON_BF16) gv = bf2f(G((const uint16_t*)T.g)[e]);
-        else gv = G((const float*)T.g)[e];
-        if (PT == KAON_BF16) pv = bf2f(G((const uint16_t*)T.p)[e]);
-        else pv = G((const float*)T.p)[e];
+        const int64_t j = j0 + jj;
+        float gv = sg[8 * lane + i], pv = spv[8 * lane + i];
         if (gc) {
           gv = round_to<GT>(gv - ws.mu(T)[row]);
           col += (uint32_t)sp;
@@ -2213,6 +2233,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
         sv[j] = snew;
         ad = ad + fabsf(snew);
       }
+      // every lane's reads of this round before the next round's writes
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
   const float num = wave_csum(an), den = wave_csum(ad);

@@ -201,6 +201,9 @@ typedef struct KaonLaunch {
   const KaonItem* ns_rect_items; /* device, AdaMuon */
   int32_t n_tensors, n_row_items, n_fin_items, n_flat_items;
   int32_t row_runs[KAON_ROW_CLASSES];
+  /* n_fast: the leading elem_items that take the specialized phase-5/6 kernel;
+   * a caller may lower it to 0 to send every item to the generic kernel (same
+   * results, bit for bit; the GPU tests use this to check the two kernels) */
   int32_t n_fast, n_elem_items;
   int32_t n_ns_sq, n_ns_rect;
   int32_t n_ns_sq_big, n_ns_rect_big;

@@ -1963,6 +1963,77 @@ __global__ __launch_bounds__(KAON_WG) void k_msq(const KaonTensor* __restrict__ 
   }
 }
 
+// k_msq on row class 0 (factored, 16-byte rows with C % 8 == 0, at most 4
+// chunks per lane) with int8 or bf16 momenta: the same sums in the same order,
+// with the chunks of GR rows loaded before their arithmetic and the int8 row
+// scales read once per wave (one row per lane, then read across lanes).
+template <int CPL, int GR, int CODEC>
+__device__ __forceinline__ void msq_pf_body(const KaonTensor& T, const KaonItem& it, const Ws& ws) {
+  constexpr bool I8 = CODEC == KAON_MOM_INT8;
+  const uint32_t C = (uint32_t)T.C;
+  const int nch = (int)(C >> 3);
+  const WaveRows wr = wave_rows(it);
+  const int nrows = (int)(wr.re - wr.rb);
+  if (nrows <= 0) return;
+  const KAON_G uint8_t* mb = (const KAON_G uint8_t*)G(T.m);
+  const float sc_l = I8 ? G(T.m_scale)[lane_row(wr.rb, nrows, wr.lane)] : 1.0f;
+  for (int j0 = 0; j0 < nrows; j0 += GR) {
+    ku2 m8[GR][CPL];
+    ku4 m16[GR][CPL];
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+      const uint32_t rowe = (uint32_t)(wr.rb + min(j0 + j, nrows - 1)) * C;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const uint32_t e0 = rowe + 8u * (uint32_t)min(wr.lane + 64 * k, nch - 1);
+        if (I8) m8[j][k] = ld_stream<true>((const KAON_G ku2*)(mb + e0));
+        else m16[j][k] = ld_stream<true>((const KAON_G ku4*)(mb + 2u * e0));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GR; ++j) {
+      const int jj = j0 + j;
+      if (jj >= nrows) continue;
+      const float sc = lane_val(sc_l, jj);
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        if (wr.lane + 64 * k >= nch) continue;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float m;
+          if (I8) {
+            const uint32_t w = i < 4 ? m8[j][k].x : m8[j][k].y;
+            m = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * sc;
+          } else {
+            const uint32_t wv[4] = {m16[j][k].x, m16[j][k].y, m16[j][k].z, m16[j][k].w};
+            m = (i & 1) ? __uint_as_float(wv[i >> 1] & 0xFFFF0000u) : __uint_as_float(wv[i >> 1] << 16);
+          }
+          a = a + m * m;
+        }
+      }
+      const float s2 = wave_csum(a);
+      if (wr.lane == 0) ws.rs(T)[wr.rb + jj] = s2;
+    }
+  }
+}
+
+template <int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_msq_pf(const KaonTensor* __restrict__ D,
+                                                    const KaonItem* __restrict__ items, Ws ws) {
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
+  const KaonTensor& T = D[it.tensor];
+  switch ((int)(((T.C >> 3) + 63) >> 6)) {
+    case 1: msq_pf_body<1, CODEC == KAON_MOM_INT8 ? 16 : 8, CODEC>(T, it, ws); break;
+    case 2: msq_pf_body<2, CODEC == KAON_MOM_INT8 ? 8 : 4, CODEC>(T, it, ws); break;
+    case 3: msq_pf_body<3, CODEC == KAON_MOM_INT8 ? 5 : 3, CODEC>(T, it, ws); break;
+    case 4: msq_pf_body<4, CODEC == KAON_MOM_INT8 ? 4 : 2, CODEC>(T, it, ws); break;
+  }
+}
+
 __global__ __launch_bounds__(KAON_WG) void k_msq_fin(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws) {
   const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (t >= n_tensors) return;
@@ -3685,8 +3756,14 @@ int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
     case KAON_MOM_4BIT: f = k_msq<KAON_MOM_4BIT>; break;
   }
   if (!f) return fail("kaon_momentum_sumsq: needs a momentum codec");
-  if (L->n_row_items > 0)
-    hipLaunchKernelGGL(f, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws);
+  // row class 0 (the leading row items) with int8 / bf16 momenta: the prefetching form
+  MsqFn fp = hp->codec == KAON_MOM_INT8 ? k_msq_pf<KAON_MOM_INT8>
+             : hp->codec == KAON_MOM_BF16 ? k_msq_pf<KAON_MOM_BF16> : nullptr;
+  const int32_t n0 = fp ? L->row_runs[0] : 0;
+  if (n0 > 0) hipLaunchKernelGGL(fp, dim3(n0 * KAON_RUN), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws);
+  if (L->n_row_items > n0)
+    hipLaunchKernelGGL(f, dim3((L->n_row_items - n0) * KAON_RUN), dim3(KAON_WG), 0, st, L->descs,
+                       L->row_items + n0, ws);
   hipLaunchKernelGGL(k_msq_fin, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
   return check_launch("kaon: momentum sum-of-squares launch");
 }

@@ -62,7 +62,7 @@ WORKLOADS = {
                               "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
                               "params on the Adakaon path", opt="adamuon",
                          kw=dict(lr=2e-2, betas=(0.95, 0.999), momentum_dtype="int8", ns_steps=2), bm=1.0),
-    # AdaPNM (src/kaon/adapnm.py, SURVEY's next row 3): two momenta, the positive one read and
+    # AdaPNM (src/kaon/adapnm.py): two momenta, the positive one read and
     # written, the negative one read (b_neg), on the same SDXL set
     "adapnm_int8": dict(desc="AdaPNM betas=(0.8,0.999) beta0=0.5, two int8 momenta, factored 2nd moment, cautious, "
                              "GC, SR bf16, lr 1e-4", opt="adapnm",
@@ -71,7 +71,7 @@ WORKLOADS = {
                              "cautious, GC, SR bf16, lr 1e-4", opt="adapnm",
                         kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="bfloat16"), bm=2.0,
                         b_neg=2.0),
-    # KProdigy (src/kaon/kprodigy.py, SURVEY's next row 4): two passes around a cross-tensor D
+    # KProdigy (src/kaon/kprodigy.py): two passes around a cross-tensor D
     # estimate; b_extra = the fp32 v (read + write) and the sliced s (read + write) and p0 (read)
     "kprodigy_bf16": dict(desc="KProdigy defaults: lr 1.0, d0 1e-6, betas=(0.9,0.999), bf16 momentum, full fp32 "
                                "second moment, slice_p 1, GC, SR bf16", opt="kprodigy",
@@ -82,7 +82,7 @@ WORKLOADS = {
                                    kw=dict(lr=1.0, betas=(0.9, 0.999), momentum_dtype="int8",
                                            second_moment="factored", slice_p=11), bm=1.0,
                                    b_extra=12.0 / 11.0, pd_slice=11, pd_full_v=False),
-    # MSAM norm="global" over Adakaon (src/kaon/msam.py, SURVEY's next row 4): the removal rides in
+    # MSAM norm="global" over Adakaon (src/kaon/msam.py): the removal rides in
     # Adakaon's apply; b_extra = the norm pass (m read) and the climb pass (m read, p read + write)
     "msam_int8": dict(desc="MSAM rho=0.3 norm='global' over Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, "
                            "SR bf16, lr 1e-4", opt="msam",

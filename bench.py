@@ -3,7 +3,7 @@
 Metric: Gparam/s and % of the HBM roofline per optimizer step.
 Default workload = BASELINE configs[2]: Adakaon, betas (0.9, 0.999), int8
 momentum, cautious, gradient centralization, stochastic-rounding bf16 writes,
-lr 1e-4 (the north star's target config).  ``--workload lion_int8``
+lr 1e-4 (the configuration the metric is quoted on).  ``--workload lion_int8``
 (configs[1]), ``nekaon_4bit_b64`` / ``nekaon_4bit_b256`` (configs[3]'s two block
 sizes; ``nekaon_4bit`` keeps Nekaon's default 128), ``adamuon_int8``
 (configs[4]) and the adjacent optimizers (``adapnm_*``, ``kprodigy_*``,

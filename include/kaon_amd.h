@@ -269,6 +269,22 @@ int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* 
  * remove/climb around it (msam.py:375-406). */
 int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
+/* Size of the static workspace of kaon_adakaon_step_noalloc, per device. */
+#define KAON_NOALLOC_WS_BYTES (32u * 1024u * 1024u)
+
+/* kaon_adakaon_step without the caller's workspace: the same kernels and
+ * results, with the workspace taken from a device array of
+ * KAON_NOALLOC_WS_BYTES that the library holds on every device it runs on
+ * until the process ends (L->workspace is ignored).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * ws_words is the plan's KaonPlanInfo.ws_words; a plan that needs more than
+ * KAON_NOALLOC_WS_BYTES / 4 words is rejected with an error.  Allocates
+ * nothing.  Every call on a device shares that device's array, so calls that
+ * overlap on one device (two streams or two host threads) race; the device
+ * the stream belongs to must be current. */
+int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* hp, int64_t ws_words, void* stream);
+
 /* Lion step over one planned param group (lion.py:322-352, 416-485). */
 int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 

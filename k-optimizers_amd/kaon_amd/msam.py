@@ -84,13 +84,16 @@ class MSAM(torch.optim.Optimizer):
         return any("m" in self.inner.state.get(p, ())
                    for g in self.param_groups for p in g["params"])
 
-    def _momentum_plans(self) -> list[tuple[int, int, E.Plan, list[int], torch.Tensor]]:
+    def _momentum_plans(self, gradless: bool = False) -> list[tuple[int, int, E.Plan, list[int], torch.Tensor]]:
         """(gid, p dtype, plan, param positions, stat word index) over the params with a
-        momentum buffer, cached while the param and state pointers hold."""
+        momentum buffer (with ``gradless``: only those without a gradient now), cached
+        while the param and state pointers hold."""
         tids = self.inner._tensor_ids()
         by_key: dict[tuple[int, int], list[torch.Tensor]] = {}
         for gid, group in enumerate(self.param_groups):
             for p in group["params"]:
+                if gradless and p.grad is not None:
+                    continue
                 st = self.inner.state.get(p)
                 if st and "m" in st:
                     by_key.setdefault((gid, E.dtype_code(p.dtype)), []).append(p)
@@ -100,7 +103,7 @@ class MSAM(torch.optim.Optimizer):
                           _ptr_or0(self.inner.state[p].get("m_scale")),
                           tuple(_ptr_or0(t) for t in (self.inner._inject_noise.get(p) or ())))
                          for p in plist)
-            hit = self._mplans.get((gid, pdt))
+            hit = self._mplans.get((gid, pdt, gradless))
             if hit is None or hit[0] != ptrs:
                 entries = []
                 for p in plist:
@@ -115,7 +118,7 @@ class MSAM(torch.optim.Optimizer):
                 idx = torch.tensor([plan.descs[i].ws_scal + 2 for i in range(len(plist))], dtype=torch.int64,
                                    device=plist[0].device)
                 hit = (ptrs, plan, [tids[id(p)] for p in plist], idx)
-                self._mplans[(gid, pdt)] = hit
+                self._mplans[(gid, pdt, gradless)] = hit
             out.append((gid, pdt, hit[1], hit[2], hit[3]))
         return out
 
@@ -174,6 +177,14 @@ class MSAM(torch.optim.Optimizer):
                 "MSAM.step() called outside train mode. Call optimizer.train() before the "
                 "training step (and optimizer.eval() before sampling / checkpointing).")
         if self._fused:
+            # The removal and the climb are folded into the Adakaon apply of the params
+            # that step.  A param with a momentum but no gradient this step is not
+            # stepped; MSAM still removes its climb and climbs again along its
+            # (unchanged) momentum (msam.py:384-403), in passes of their own keyed on
+            # the same step.
+            idle = self._momentum_plans(gradless=True) if self.rho != 0.0 else []
+            if self._has_e and idle:
+                self._apply(-1.0, self.inner._t + 1, plans=idle)
             if self.norm == "global":
                 nk = {"remove": self._has_e, "bound_old": {g: math.inf for g in range(len(self.param_groups))},
                       "k": -self.rho / (self._mnorm + self.eps), "climb": False, "eclamp": {}}
@@ -184,7 +195,11 @@ class MSAM(torch.optim.Optimizer):
             loss = self.inner._step_impl(closure, nk=nk)
             if self.norm == "none":
                 if self.rho != 0.0 and self._has_momentum():
+                    # bounds frozen at this climb: the stepped groups' from the fused climb,
+                    # the others' by _apply below
                     self._eclamp = nk["eclamp"]
+                    if idle:
+                        self._apply(+1.0, plans=idle)
                     self._has_e = True
                 return loss
         else:

@@ -146,12 +146,19 @@ def _ptr(a: np.ndarray | None) -> int | None:
 
 # ------------------------------------------------------------------ bf16 helpers
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:
-    """fp32 -> bf16 bits, round to nearest even, NaN -> 0x7FC0."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r[nan] = 0x7FC0
-    return r
+    """fp32 -> bf16 bits, round to nearest even, NaN -> 0x7FC0.
+
+    u + 0x7FFF + lsb fits in 32 bits for every non-NaN pattern (the largest,
+    0xFF7FFFFF + 0x8000, rounds to -inf); only negative NaNs wrap, and they are
+    replaced below."""
+    u = np.ascontiguousarray(x, dtype=np.float32).reshape(-1).view(np.uint32)
+    t = (u >> 16) & np.uint32(1)
+    t += u
+    t += np.uint32(0x7FFF)
+    t >>= 16
+    r = t.astype(np.uint16)
+    r[(u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)] = 0x7FC0
+    return r.reshape(np.shape(x))
 
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:
@@ -537,6 +544,12 @@ class OracleOptimizer:
         h.nk_climb = 0
         for prm in self.params:
             t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
+            if prm.g is None:
+                # no gradient this step: the param is not stepped, but MSAM removes the
+                # climb from every param with a momentum (msam.py:155-167, 384-388)
+                if h.nk_remove and "m" in prm.state:
+                    lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), h.nk_k, math.inf, 0)
+                continue
             _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
         self.has_e = False
         if self.rho != 0.0:
@@ -565,6 +578,16 @@ class OracleOptimizer:
             h.nk_k = self.k
             h.nk_bound_new = new_bound
         for prm in self.params:
+            if prm.g is None:
+                # the reference skips a param without a gradient; MSAM still removes and
+                # re-adds the climb on every param with a momentum (msam.py:384-403)
+                if self.opt in ("nekaon", "msam") and "m" in prm.state:
+                    t = _tensor(prm, md, None if noise is None else noise.get(prm.tensor_id))
+                    if h.nk_remove:
+                        lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), h.nk_k, h.nk_bound_old, 0)
+                    if h.nk_climb:
+                        lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), -h.nk_k, h.nk_bound_new, 2)
+                continue
             if self.opt == "adapnm":
                 t = _pnm_tensor(prm, md, self.t, None if noise is None else noise.get(prm.tensor_id))
                 _check(lib().ko_adapnm_tensor(ctypes.byref(t), ctypes.byref(h)))

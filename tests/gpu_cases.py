@@ -86,7 +86,11 @@ def run_gpu(case, group=None, values=None):
         params.append(prm)
     opt = make_opt(case, params, group)
     for step in range(1, case["steps"] + 1):
+        idle = case.get("no_grad", {}).get(step, ())
         for i, p in enumerate(params):
+            if i in idle:  # no gradient for this param this step
+                p.grad = None
+                continue
             g = grad_values(case, i, step)
             p.grad = torch.from_numpy(g).to(DEV, gdt)
         opt.step()
@@ -139,7 +143,11 @@ def oracle_case_run(case, group=None, values=None):
         params.append(O.make_param(shape, dt(case["p_dtype"]), dt(case["g_dtype"]), tensor_id=i, p_values=v))
     opt = O.OracleOptimizer(params, case["opt"], g, seed=case["seed"])
     for step in range(1, case["steps"] + 1):
+        idle = case.get("no_grad", {}).get(step, ())
         for i, prm in enumerate(params):
+            if i in idle:
+                prm.g = None
+                continue
             gv = grad_values(case, i, step)
             prm.g = O.f32_to_bf16(gv).reshape(prm.shape) if prm.g_dtype == O.BF16 else gv.copy()
         opt.step()

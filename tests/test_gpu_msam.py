@@ -75,6 +75,16 @@ EXTRA = {
     "fast_int8_wd": _case([[320, 1280], [96, 64, 3, 3], [640]], dict(lr=1e-3, rho=-0.5, momentum_dtype="int8",
                                                                      weight_decay=0.1)),
     "fast_4bit_wd": _case([[256, 2048], [1280]], dict(lr=1e-3, rho=0.2, momentum_dtype="4bit", weight_decay=0.05)),
+    # params with a momentum but no gradient on some steps: not stepped, but their climb
+    # is removed and added again (msam.py:384-403); on step 3 of the Nekaon-form case no
+    # param of the group has a gradient
+    "gradless_global_int8": dict(_case([[320, 1280], [96, 64, 3, 3], [640], [24, 32]],
+                                       dict(lr=1e-3, rho=0.3, momentum_dtype="int8")),
+                                 no_grad={2: (1,), 3: (0, 2)}),
+    "gradless_none_4bit": dict(_case([[160, 40], [33], [7, 9], [256, 64]],
+                                     dict(lr=1e-3, rho=0.8, norm="none", momentum_dtype="4bit",
+                                          momentum_4bit_block=16)),
+                               no_grad={2: (0, 3), 3: (0, 1, 2, 3)}),
 }
 
 

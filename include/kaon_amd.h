@@ -187,8 +187,6 @@ typedef struct KaonPlanArgs {
 
 /* Elements per flat work item. */
 #define KAON_FLAT_ITEM 16384
-/* Longest row (C) of a factored tensor the row kernels accept. */
-#define KAON_MAX_ROW 16384
 
 /* Device-side tables of one planned group, passed to every step entry point. */
 typedef struct KaonLaunch {
@@ -258,7 +256,7 @@ const char* kaon_last_error(void);
  * whose kind (rows per wave) is a multiple of 64 / fast_lanes.
  * Item arrays may be NULL to query sizes; info is
  * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
- * factored row longer than KAON_MAX_ROW). */
+ * tensor of 2^31 or more elements, or a momentum codec without its buffer). */
 int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
               KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonItem* ns_sq_items,
               KaonItem* ns_rect_items, KaonPlanInfo* info);

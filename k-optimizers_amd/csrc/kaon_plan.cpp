@@ -142,15 +142,16 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     t.n = t.R * t.C;
     if (t.n >= (int64_t)1 << 31)
       return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has >= 2^31 elements");
-    if (t.factored && t.C > KAON_MAX_ROW)
-      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has rows of " + std::to_string(t.C) +
-                       " elements; the row kernels take at most " + std::to_string(KAON_MAX_ROW));
     if (!t.factored && t.R != 1) return plan_fail("kaon_plan: a 1-D tensor must have R == 1");
     if (opt == KAON_OPT_ADAMUON && !t.factored)
       return plan_fail("kaon_plan: tensor " + std::to_string(i) +
                        " is 1-D; AdaMuon plans take 2-D / conv params (1-D params step through an Adakaon "
                        "plan with lr scaled by 0.2)");
     if (codec == KAON_MOM_4BIT && t.block4 < 1) return plan_fail("kaon_plan: 4-bit block size must be >= 1");
+    if (codec != KAON_MOM_NONE && t.R * t.C > 0 && !t.m)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has no momentum buffer for the planned codec");
+    if ((codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT) && t.R * t.C > 0 && !t.m_scale)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has no momentum scales for the planned codec");
     t.sqrt_n = (float)std::sqrt((double)(t.n > 1 ? t.n : 1));
     const int64_t rw = rows_per_wave(t.C);
     const int64_t slice_rows = 4 * rw;

@@ -158,6 +158,9 @@ __device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const
   }
 }
 
+// Columns per LDS segment of the streamed rows' column fold (phase 1).
+constexpr int kSeg = 4096;
+
 // =============================================================== phase 1
 // mode 0 (Adakaon): GC row mean (stored), row EMA of mean_C(G^2), column
 // partial of the slice (wave groups folded in order in LDS); 1-D tensors: v
@@ -328,6 +331,39 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
 
   // fold the wave-group partials in group order into the slice partial
   const bool has_rows = wr.re > wr.rb;
+  if (CPL == 0) {
+    // streamed rows (RW == 1, any length): the slice partial is folded kSeg
+    // columns at a time through LDS.  Per column the order is the one below:
+    // wave 0 + wave 1 + wave 2 + wave 3, then the slice added to the run partial.
+    for (int64_t c0 = 0; c0 < C; c0 += kSeg) {
+      const int64_t c1 = min(C, c0 + (int64_t)kSeg);
+      for (int wf = 0; wf < 4; ++wf) {
+        if (wr.w == wf && has_rows) {
+          const int64_t r = wr.rb;
+          const float mu = gc ? mu_arr[r] : 0.0f;
+          for (int64_t c = (c0 >> 3) + wr.lane; c * 8 < c1; c += 64) {
+            const int cnt = chunk_cnt(c, C);
+            float x[8];
+            ld8<GT>(gsrc, r * C + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              if (i < cnt) {
+                const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
+                float v = gv * gv;
+                if (eps) v = v + hp.eps1;
+                const int64_t j = c * 8 + i - c0;
+                lds_col[j] = wf == 0 ? v : lds_col[j] + v;
+              }
+          }
+        }
+        __syncthreads();
+      }
+      for (int64_t j = c0 + threadIdx.x; j < c1; j += KAON_WG)
+        part[j] = sl == 0 ? lds_col[j - c0] : part[j] + lds_col[j - c0];
+      __syncthreads();  // lds_col is reused by the next segment
+    }
+    continue;
+  }
   for (int wf = 0; wf < 4; ++wf) {
     if (wr.w == wf && has_rows) {
       if (CPL > 0) {
@@ -345,26 +381,6 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
                 v = xb[k][i] * xb[k][i];
                 if (eps) v = v + hp.eps1;
               }
-              const int64_t j = c * 8 + i;
-              lds_col[j] = wf == 0 ? v : lds_col[j] + v;
-            }
-        }
-      } else {
-        // streaming rows have RW == 1: recompute q of the wave's row
-        const int64_t r = wr.rb;
-        const float mu = gc ? mu_arr[r] : 0.0f;
-        for (int k = 0; k < cpl; ++k) {
-          const int64_t c = wr.lane + 64 * k;
-          const int cnt = chunk_cnt(c, C);
-          if (cnt <= 0) continue;
-          float x[8];
-          ld8<GT>(gsrc, r * C + c * 8, cnt, vec && cnt == 8, x);
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (i < cnt) {
-              const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
-              float v = gv * gv;
-              if (eps) v = v + hp.eps1;
               const int64_t j = c * 8 + i;
               lds_col[j] = wf == 0 ? v : lds_col[j] + v;
             }
@@ -3403,8 +3419,7 @@ using StatsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int)
 // row classes (slices are sorted by class): 0-2 prefetching kernels, 3-5 rows
 // of <= 4, 10, 24 chunks per lane in registers, 6 streamed rows; dynamic LDS
 // holds one slice column partial
-constexpr int kClassMaxC[KAON_ROW_CLASSES] = {4 * 512, 10 * 512, 24 * 512, 4 * 512, 10 * 512, 24 * 512,
-                                              KAON_MAX_ROW};
+constexpr int kClassMaxC[KAON_ROW_CLASSES] = {4 * 512, 10 * 512, 24 * 512, 4 * 512, 10 * 512, 24 * 512, kSeg};
 
 template <int GT>
 StatsFn stats_fn_gt(int cls, bool eps) {

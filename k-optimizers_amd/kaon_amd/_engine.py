@@ -39,12 +39,64 @@ def _align(n: int, a: int = 256) -> int:
     return (n + a - 1) // a * a
 
 
+_MOM_DTYPE = {L.MOM_F32: torch.float32, L.MOM_BF16: torch.bfloat16, L.MOM_INT8: torch.int8,
+              L.MOM_4BIT: torch.uint8}
+
+
+def _check_state(e: dict[str, Any], codec: int, i: int) -> None:
+    """The state tensors of entry ``e`` hold what the kernels will read and write for
+    ``codec``: a momentum buffer (and its scales) of the codec's dtype and size, and
+    second-moment buffers of the param's matrixized shape.  State created for another
+    ``momentum_dtype`` or ``betas`` (the group changed after the first step) or loaded
+    for another shape raises here instead of being overrun on the device."""
+    p = e["p"]
+    n, R, C = p.numel(), e["R"], e["C"]
+
+    def bad(key: str, why: str) -> None:
+        raise ValueError(f"kaon_amd: param {i} {tuple(p.shape)}: state '{key}' {why}; the state does not match "
+                         "the group's settings (momentum_dtype / betas changed after the state was created, or "
+                         "a checkpoint of another shape was loaded)")
+
+    def need(key: str, t: torch.Tensor | None, dtype: torch.dtype, numel: int) -> None:
+        if t is None:
+            bad(key, "is missing")
+        if t.dtype != dtype:
+            bad(key, f"has dtype {t.dtype}, expected {dtype}")
+        if t.numel() != numel:
+            bad(key, f"has {t.numel()} elements, expected {numel}")
+        if not t.is_contiguous() or t.device != p.device:
+            bad(key, "must be a contiguous tensor on the param's device")
+
+    for key, skey in (("m", "m_scale"), ("m2", "m2_scale")):
+        if key == "m2" and e.get("m2") is None:
+            continue
+        if codec == L.MOM_NONE:
+            continue
+        m = e.get(key)
+        if codec == L.MOM_4BIT:
+            need(key, m, torch.uint8, (n + 1) // 2)
+            blk = int(e.get("block4", 0))
+            if blk < 1:
+                bad(key, "has no 4-bit block size")
+            need(skey, e.get(skey), torch.float32, (n + blk - 1) // blk)
+        else:
+            need(key, m, _MOM_DTYPE[codec], n)
+            if codec == L.MOM_INT8:
+                need(skey, e.get(skey), torch.float32, R if e["factored"] else 1)
+    for key, numel in (("row", R), ("col", C), ("v", n), ("max_v", n)):
+        t = e.get(key)
+        if t is not None:
+            need(key, t, torch.float32, numel)
+
+
 class Plan:
     """Device tables + workspace of one planned launch group."""
 
     def __init__(self, opt: int, codec: int, entries: Sequence[dict[str, Any]], device: torch.device,
                  p_dtype: int = L.BF16, g_dtype: int = L.BF16, bf16_method: int = L.SR) -> None:
         n = len(entries)
+        for i, e in enumerate(entries):
+            _check_state(e, codec, i)
         descs = (L.KaonTensor * max(n, 1))()
         for i, e in enumerate(entries):
             d = descs[i]

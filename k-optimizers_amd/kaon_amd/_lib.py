@@ -28,7 +28,6 @@ ROW_BUDGET = 20
 ROW_CLASSES = 7
 COLITEM = 2048
 FLAT_ITEM = 16384
-MAX_ROW = 16384
 NS_TILE = 128
 
 

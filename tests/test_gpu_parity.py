@@ -54,6 +54,10 @@ def _case(opt, shapes, kwargs, steps=3, p="bf16", g="bf16", **kw):
 
 _MIX = [[640, 640, 3, 3], [1280, 2048], [5120, 640], [1280], [77, 33], [3, 5, 7], [1], [9, 1], [2, 2048 * 8],
         [13, 2880]]
+# SDXL-shaped tensors of every row length of the benchmark set (640, 1280, 2048, 2880,
+# 5120, 5760) plus 1-D, at sizes the oracle steps in about a second
+_SDXL = [[640, 640, 3, 3], [1280, 1280], [256, 2048], [96, 5120], [320, 320, 3, 3], [64, 640, 3, 3], [5120, 640],
+         [1280], [640], [77, 33]]
 EXTRA = {
     "ada_int8_mix": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8")),
     "ada_4bit_mix_b64": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="4bit",
@@ -89,6 +93,24 @@ EXTRA = {
                                                        weight_decay=0.0), eval_train=True),
     "nekaon_int8_f32": _case("nekaon", [[96, 40], [33], [4, 8, 3, 3]],
                              dict(lr=1e-3, k=1.5, momentum_dtype="int8"), p="f32", g="f32", eval_train=True),
+    # BASELINE configs[3] as given: Nekaon k=1.5, beta1=0.2, wd 0.1, 4-bit blocks of 64 and
+    # 256 (the 256-element blocks of the 640-, 2880- and 5760-element rows cross rows), grads
+    # with 1 % Student-t(3) outliers that set the block absmax and drive the climb clamp;
+    # eval/train at the end
+    "cfg3_nekaon_4bit_b64": _case("nekaon", _SDXL, dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), weight_decay=0.1,
+                                                         momentum_dtype="4bit", momentum_4bit_block=64),
+                                  outlier_frac=0.01, eval_train=True),
+    "cfg3_nekaon_4bit_b256": _case("nekaon", _SDXL, dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), weight_decay=0.1,
+                                                          momentum_dtype="4bit", momentum_4bit_block=256),
+                                   outlier_frac=0.01, eval_train=True),
+    # Nekaon with a param without a gradient on some steps (its climb is still removed and
+    # re-added), all three on step 3
+    "nekaon_gradless": _case("nekaon", [[320, 1280], [13, 2880], [640]],
+                             dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=64),
+                             steps=4, no_grad={2: (1,), 3: (0, 1, 2)}, eval_train=True),
+    # BASELINE configs[1] as given: Lion int8, betas=(0.95, 0.98), lr 2e-4, wd 0 (the
+    # specialized kernel without weight decay), cautious, GC, SR
+    "cfg1_lion_int8": _case("lion", _SDXL, dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="int8"), steps=4),
 }
 
 
@@ -99,6 +121,46 @@ def test_extra_case_bit_exact(name):
     oparams, _, oeval = oracle_case_run(case)
     params, opt, evalp = run_gpu(case)
     assert_same_as_oracle(case, oparams, params, opt, evalp, oeval, label=name)
+
+
+def test_lora_bag_launch_bound_regime():
+    """The reference's launch-bound proxy (benchmarks/proxy/harness.py:117-127): 512 fp32
+    LoRA factors of [8, 16], Adakaon defaults (bf16 momentum, GC, cautious), three steps,
+    bit for bit against the oracle."""
+    case = _case("adakaon", [[8, 16]] * 512, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="bfloat16"),
+                 p="f32", g="f32")
+    print("[gpu] lora bag 512 x [8, 16]", flush=True)
+    oparams, _, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case)
+    assert_same_as_oracle(case, oparams, params, opt, label="lora_bag")
+
+
+@pytest.mark.parametrize("variant", ["bf16_int8", "f32g_4bit"])
+def test_rows_longer_than_16384(variant):
+    """Factored rows of 17280, 23040 and 28672 elements (SDXL up-block convs [640,1920,3,3]
+    and [1280,2560,3,3], a linear with 28672 inputs): the streamed-row kernels fold the
+    column partial in LDS segments.  bf16 grads + int8 take the specialized phase-5/6
+    kernel; fp32 grads + 4-bit (blocks crossing rows) the generic ones."""
+    shapes = [[640, 1920, 3, 3], [1280, 2560, 3, 3], [96, 28672], [1920]]
+    if variant == "bf16_int8":
+        case = _case("adakaon", shapes, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8"), steps=2)
+    else:
+        case = _case("adakaon", shapes,
+                     dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="4bit", momentum_4bit_block=96,
+                          weight_decay=0.01), steps=2, g="f32")
+    print(f"[gpu] long rows {variant}", flush=True)
+    oparams, _, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case)
+    assert_same_as_oracle(case, oparams, params, opt, label=f"long_rows_{variant}")
+
+
+def test_linear_of_28672_inputs():
+    """A [4096, 28672] linear (117M elements, rows of 28672) through Adakaon int8, one step."""
+    case = _case("adakaon", [[4096, 28672]], dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8"), steps=1)
+    print("[gpu] linear [4096, 28672]", flush=True)
+    oparams, _, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case)
+    assert_same_as_oracle(case, oparams, params, opt, label="linear_28672")
 
 
 def test_sdxl_largest_conv_two_steps():

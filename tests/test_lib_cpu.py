@@ -72,7 +72,7 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
             d.R, d.C, d.factored = 1, numel, 0
         d.block4 = min(block, numel) if numel else 1
         d.tensor_id = i
-        d.g = d.p = d.m = 0x1000 * (i + 1)
+        d.g = d.p = d.m = d.m_scale = 0x1000 * (i + 1)
     info = L.KaonPlanInfo()
     args = L.KaonPlanArgs(opt, codec, 1, g_dtype, 0)
     rc = L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None, ctypes.byref(info))
@@ -194,11 +194,16 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
         assert descs[i].vec_rows == (1 if (descs[i].C % 8 == 0 or descs[i].R == 1) else 0)
 
 
-def test_plan_rejects_rows_longer_than_the_register_budget():
-    rc, *_ = _plan([(4, 16385)])
-    assert rc != 0
-    msg = _lib().lib().kaon_last_error().decode()
-    assert "16384" in msg
+def test_plan_takes_rows_of_any_length():
+    """Rows longer than any register class (SDXL up-block convs [640,1920,3,3] and
+    [1280,2560,3,3], rows of 17280 and 23040; a 28672-input linear) are planned as
+    streamed rows (class 6) with one run per 4 slices of 4 rows."""
+    shapes = [(640, 1920, 3, 3), (1280, 2560, 3, 3), (4096, 28672), (4, 16385)]
+    rc, descs, info, rows, _fins, _flats = _plan(shapes)
+    assert rc == 0
+    assert info.row_runs[6] == sum(-(-s[0] // 16) for s in shapes)
+    for i in range(len(shapes)):
+        assert descs[i].ngroups == -(-descs[i].R // 16)
 
 
 def test_constructor_validation_mirrors_reference():
@@ -271,7 +276,7 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
         d = descs[i]
         numel = int(np.prod(s))
         d.R, d.C, d.factored, d.tensor_id = s[0], numel // s[0], 1, i
-        d.g = d.p = d.m = 0x1000 * (i + 1)
+        d.g = d.p = d.m = d.m_scale = 0x1000 * (i + 1)
     info = L.KaonPlanInfo()
     args = L.KaonPlanArgs(L.OPT_ADAMUON, L.MOM_INT8, L.BF16, L.BF16, L.SR)
     assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None, ctypes.byref(info)) == 0
@@ -357,3 +362,45 @@ def test_fast_lanes_fill_every_lane_on_sdxl_rows():
     assert rc == 0
     assert descs[0].fast_lanes == 64 or descs[0].C % 128 != 0
     assert descs[1].fast_lanes == 32
+
+
+def test_state_that_does_not_match_the_codec_is_refused():
+    """State created for another momentum_dtype / betas, or for another shape, raises
+    ValueError before anything is planned (the kernels would otherwise write past the
+    buffer or read a missing one)."""
+    from kaon_amd import _engine as E
+    from kaon_amd import _lib as L
+
+    p = torch.zeros(6, 10, dtype=torch.bfloat16)
+    base = dict(p=p, g=p, R=6, C=10, factored=True, tensor_id=0, row=torch.zeros(6), col=torch.zeros(10))
+    int8 = dict(base, m=torch.zeros(6, 10, dtype=torch.int8), m_scale=torch.ones(6, 1))
+    E._check_state(int8, L.MOM_INT8, 0)                       # matches
+    with pytest.raises(ValueError, match="dtype torch.int8"):  # momentum_dtype int8 -> bfloat16
+        E._check_state(int8, L.MOM_BF16, 0)
+    with pytest.raises(ValueError, match="'m' is missing"):   # betas[0] 0 -> 0.9
+        E._check_state(dict(base), L.MOM_INT8, 0)
+    four = dict(base, m=torch.full((30,), 0x88, dtype=torch.uint8), m_scale=torch.ones(1), block4=60)
+    E._check_state(four, L.MOM_4BIT, 0)
+    with pytest.raises(ValueError, match="'m_scale' has 1 elements"):  # block size changed to 16
+        E._check_state(dict(four, block4=16), L.MOM_4BIT, 0)
+    with pytest.raises(ValueError, match="'col' has 9 elements"):      # state of another shape
+        E._check_state(dict(int8, col=torch.zeros(9)), L.MOM_INT8, 0)
+    E._check_state(dict(base), L.MOM_NONE, 0)                 # beta1 = 0: no momentum needed
+
+
+def test_plan_refuses_a_missing_momentum_buffer():
+    L = _lib()
+    descs = (L.KaonTensor * 1)()
+    d = descs[0]
+    d.R, d.C, d.factored, d.block4 = 8, 16, 1, 128
+    d.g = d.p = 0x1000
+    info = L.KaonPlanInfo()
+    for codec in (1, 2, 3, 4):
+        d.m, d.m_scale = None, None
+        args = L.KaonPlanArgs(0, codec, 1, 1, 0)
+        assert L.lib().kaon_plan(ctypes.byref(args), descs, 1, None, None, None, None, None, None,
+                                 ctypes.byref(info)) != 0
+        assert b"momentum" in L.lib().kaon_last_error()
+    args = L.KaonPlanArgs(0, 0, 1, 1, 0)
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, 1, None, None, None, None, None, None,
+                             ctypes.byref(info)) == 0

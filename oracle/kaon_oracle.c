@@ -224,6 +224,12 @@ typedef struct {
     int64_t pd_np0;
     int32_t pd_slice;    /* slice_p */
     int32_t full_v;      /* per-element second moment v although the tensor is a matrix */
+    /* 1: the GC mean, the row / column means of the factored second moment,
+     * the row factors' mean and the RMS clip's norm are summed in torch CPU's
+     * order (ko_torch_inner_sum, ko_torch_outer_sum, ko_torch_sumsq) instead of
+     * the canonical one.  For pinning the oracle against the reference's own
+     * output only; the GPU follows the canonical order. */
+    int32_t torch_order;
 } KoTensor;
 
 typedef struct {
@@ -255,6 +261,95 @@ static inline float round_g(const KoTensor* t, float x) {
     return t->g_dtype == KO_BF16 ? round_bf16(x) : x;
 }
 
+/* torch CPU's fp32 sum order (aten/src/ATen/native/cpu/SumKernel.cpp as
+ * measured against torch 2.10 on x86-64, tests/test_oracle_torch_semantics.py):
+ * 8-float vectors, four of them accumulated side by side, in a cascade of four
+ * levels whose first level takes 2^max(4, ceil(log2(size))/4) rows before it is
+ * added into the next.  torch_msum is that cascade over `size` rows of `ns`
+ * slots of `nl` lanes, element (i, k, l) at base[i*rs + k*ss + l]; out holds the
+ * ns*nl sums. */
+static int ceil_log2_i64(int64_t x) {
+    int k = 0;
+    for (int64_t v = x - 1; x > 1 && v > 0; v >>= 1) ++k;
+    return k;
+}
+static void torch_msum(const float* base, int64_t rs, int64_t ss, int ns, int nl, int64_t size, float* out) {
+    enum { LV = 4 };
+    float acc[LV][4][8];
+    memset(acc, 0, sizeof(acc));
+    const int lp0 = ceil_log2_i64(size) / LV;
+    const int lp = lp0 > 4 ? lp0 : 4;
+    const int64_t step = (int64_t)1 << lp, mask = step - 1;
+    int64_t i = 0;
+    while (i + step <= size) {
+        for (int64_t j = 0; j < step; ++j, ++i)
+            for (int k = 0; k < ns; ++k)
+                for (int l = 0; l < nl; ++l) acc[0][k][l] = acc[0][k][l] + base[i * rs + k * ss + l];
+        for (int v = 1; v < LV; ++v) {
+            for (int k = 0; k < ns; ++k)
+                for (int l = 0; l < nl; ++l) {
+                    acc[v][k][l] = acc[v][k][l] + acc[v - 1][k][l];
+                    acc[v - 1][k][l] = 0.0f;
+                }
+            if ((i & (mask << (v * lp))) != 0) break;
+        }
+    }
+    for (; i < size; ++i)
+        for (int k = 0; k < ns; ++k)
+            for (int l = 0; l < nl; ++l) acc[0][k][l] = acc[0][k][l] + base[i * rs + k * ss + l];
+    for (int v = 1; v < LV; ++v)
+        for (int k = 0; k < ns; ++k)
+            for (int l = 0; l < nl; ++l) acc[0][k][l] = acc[0][k][l] + acc[v][k][l];
+    for (int k = 0; k < ns; ++k)
+        for (int l = 0; l < nl; ++l) out[k * nl + l] = acc[0][k][l];
+}
+/* row_sum: `size` vectors of nl lanes, vector i at base + i*vs, in torch_msum
+ * over rows of four vectors, the leftover vectors and then the other three
+ * partials added into the first. */
+static void torch_row_sum(const float* base, int64_t vs, int nl, int64_t size, float* out) {
+    float ps[4 * 8];
+    const int64_t size_ilp = size / 4;
+    torch_msum(base, 4 * vs, vs, 4, nl, size_ilp, ps);
+    for (int64_t i = size_ilp * 4; i < size; ++i)
+        for (int l = 0; l < nl; ++l) ps[l] = ps[l] + base[i * vs + l];
+    for (int k = 1; k < 4; ++k)
+        for (int l = 0; l < nl; ++l) ps[l] = ps[l] + ps[k * nl + l];
+    for (int l = 0; l < nl; ++l) out[l] = ps[l];
+}
+/* torch's sum of a contiguous fp32 row: rows of at least 8 elements take
+ * vectorized_inner_sum (the scalar tail first, then the 8 lanes of the vector
+ * sum in order), shorter ones scalar_inner_sum (row_sum of single lanes). */
+float ko_torch_inner_sum(const float* x, int64_t n) {
+    if (n < 8) {
+        float s = 0.0f;
+        if (n > 0) torch_row_sum(x, 1, 1, n, &s);
+        return s;
+    }
+    const int64_t nv = n / 8;
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (nv > 0) torch_row_sum(x, 8, 8, nv, v);
+    float f = 0.0f;
+    for (int64_t k = nv * 8; k < n; ++k) f = f + x[k];
+    for (int l = 0; l < 8; ++l) f = f + v[l];
+    return f;
+}
+/* torch's sums over the rows of a contiguous [R, C] fp32 matrix into out [C]
+ * (vectorized_outer_sum): blocks of 32 columns in torch_msum, then blocks of 8
+ * and single columns in torch_row_sum over the rows; matrices narrower than 8
+ * columns take scalar_outer_sum. */
+void ko_torch_outer_sum(const float* x, int64_t R, int64_t C, float* out) {
+    int64_t j = 0;
+    if (C < 8) {
+        /* scalar_outer_sum: blocks of 4 columns in torch_msum, then row_sum */
+        for (; j + 4 <= C; j += 4) torch_msum(x + j, C, 1, 4, 1, R, out + j);
+        for (; j < C; ++j) torch_row_sum(x + j, C, 1, R, out + j);
+        return;
+    }
+    for (; j + 32 <= C; j += 32) torch_msum(x + j, C, 8, 4, 8, R, out + j);
+    for (; j + 8 <= C; j += 8) torch_row_sum(x + j, C, 8, R, out + j);
+    for (; j < C; ++j) torch_row_sum(x + j, C, 1, R, out + j);
+}
+
 /* Gradient as the step sees it: GC'd in the grad dtype when enabled and
  * ndim >= 2 (src/kaon/_backend.py:147-177; the mean is torch's bf16 mean,
  * i.e. one rounding of fp32_sum / C). */
@@ -265,7 +360,8 @@ static float* centralized_grad(const KoTensor* t, int gc) {
     if (gc && t->factored) {
         for (int64_t r = 0; r < t->R; ++r) {
             float* gr = g + r * t->C;
-            float mu = round_g(t, ko_csum(gr, t->C) / (float)t->C);
+            const float sum = t->torch_order ? ko_torch_inner_sum(gr, t->C) : ko_csum(gr, t->C);
+            float mu = round_g(t, sum / (float)t->C);
             for (int64_t j = 0; j < t->C; ++j) gr[j] = round_g(t, gr[j] - mu);
         }
     }
@@ -472,7 +568,7 @@ int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bou
  * mean(row)) into rf [R], c = rsqrt(col) into cf [C]. */
 static void factored_factors(const KoTensor* t, float* rf, float* cf) {
     for (int64_t j = 0; j < t->C; ++j) cf[j] = ko_rsqrt(t->col[j]);
-    float rm = ko_csum(t->row, t->R) / (float)t->R;
+    float rm = (t->torch_order ? ko_torch_inner_sum(t->row, t->R) : ko_csum(t->row, t->R)) / (float)t->R;
     for (int64_t r = 0; r < t->R; ++r) rf[r] = ko_rsqrt(t->row[r] / rm);
 }
 
@@ -487,6 +583,8 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
     float* ps = (float*)calloc((size_t)C, sizeof(float));  /* slice partial */
     float* pr = (float*)calloc((size_t)C, sizeof(float));  /* run partial */
     float* colsum = (float*)calloc((size_t)C, sizeof(float));
+    float* rowold = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
+    for (int64_t r = 0; r < R; ++r) rowold[r] = t->row[r];
     for (int64_t r = 0; r < R; ++r) {
         for (int64_t j = 0; j < C; ++j) {
             float v = x[r * C + j] * x[r * C + j];
@@ -508,8 +606,24 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
             }
         }
     }
+    if (t->torch_order) {
+        /* torch: grad_sq.mean(-1) and grad_sq.mean(-2) of the whole [R, C] square */
+        float* sq = (float*)malloc(sizeof(float) * (size_t)(R * C > 0 ? R * C : 1));
+        for (int64_t r = 0; r < R; ++r)
+            for (int64_t j = 0; j < C; ++j) {
+                float v = x[r * C + j] * x[r * C + j];
+                if (add_eps) v = v + eps1f;
+                sq[r * C + j] = v;
+            }
+        /* undo the canonical row EMAs taken above from the same old state: redo them */
+        for (int64_t r = 0; r < R; ++r) t->row[r] = rowold[r];
+        for (int64_t r = 0; r < R; ++r)
+            t->row[r] = ko_lerp(t->row[r], ko_torch_inner_sum(sq + r * C, C) / (float)C, w2);
+        ko_torch_outer_sum(sq, R, C, colsum);
+        free(sq);
+    }
     for (int64_t j = 0; j < C; ++j) t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
-    free(q); free(pw); free(ps); free(pr); free(colsum);
+    free(q); free(pw); free(ps); free(pr); free(colsum); free(rowold);
     if (rf && cf) factored_factors(t, rf, cf);
 }
 
@@ -524,8 +638,26 @@ static void factored_update(const KoTensor* t, const float* x, float w2, float e
     free(rf); free(cf);
 }
 
+/* The squared fp32 norm as torch CPU computes t.norm(2) of a contiguous fp32
+ * tensor (rms, _backend.py:45-47), measured against torch 2.10 on x86-64
+ * (tests/test_oracle_torch_semantics.py): its 8-float vector kernel keeps 8
+ * lanes, lane k a sequential fused multiply-add chain over elements k, k+8,
+ * k+16, ... of the largest multiple of 8; the lanes are added in order 0..7
+ * and the remaining elements fma'd in one by one. */
+float ko_torch_sumsq(const float* u, int64_t n) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t body = n - n % 8;
+    for (int64_t i = 0; i < body; i += 8)
+        for (int k = 0; k < 8; ++k) acc[k] = fmaf(u[i + k], u[i + k], acc[k]);
+    float b = acc[0];
+    for (int k = 1; k < 8; ++k) b = b + acc[k];
+    for (int64_t i = body; i < n; ++i) b = fmaf(u[i], u[i], b);
+    return b;
+}
+
 /* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):
- * u /= max((||u|| / sqrt(n)) / clip, 1); u *= scale. */
+ * u /= max((||u|| / sqrt(n)) / clip, 1); u *= scale.  The sum of squares is
+ * canonical (CSUM of the rows' CSUMs), or torch's order with torch_order. */
 static void clip_scale(const KoTensor* t, float* u, double clip, float scale) {
     int64_t R = t->R, C = t->C, n = R * C;
     float* rs = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
@@ -534,7 +666,7 @@ static void clip_scale(const KoTensor* t, float* u, double clip, float scale) {
         for (int64_t j = 0; j < C; ++j) sq[j] = u[r * C + j] * u[r * C + j];
         rs[r] = ko_csum(sq, C);
     }
-    float ss = ko_csum(rs, R);
+    float ss = t->torch_order ? ko_torch_sumsq(u, n) : ko_csum(rs, R);
     float rmsv = sqrtf(ss) / (float)sqrt((double)(n > 1 ? n : 1));
     float fac = fmaxf(rmsv / (float)clip, 1.0f);
     if (t->fac_override) fac = *t->fac_override;

@@ -40,6 +40,7 @@ Parity unpinned: NaN payload bits (positions are compared).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 import os
@@ -71,6 +72,7 @@ class KoTensor(ctypes.Structure):
         ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
         ("pd_s", ctypes.c_void_p), ("pd_p0", ctypes.c_void_p), ("pd_np0", ctypes.c_int64),
         ("pd_slice", ctypes.c_int32), ("full_v", ctypes.c_int32),
+        ("torch_order", ctypes.c_int32),
     ]
 
 
@@ -116,6 +118,11 @@ def lib() -> ctypes.CDLL:
                                     ctypes.c_double, ctypes.c_double, ctypes.c_uint32]
         L.ko_csum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
         L.ko_csum.restype = ctypes.c_float
+        for name in ("ko_torch_inner_sum", "ko_torch_sumsq"):
+            getattr(L, name).argtypes = [ctypes.c_void_p, ctypes.c_int64]
+            getattr(L, name).restype = ctypes.c_float
+        L.ko_torch_outer_sum.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        L.ko_torch_outer_sum.restype = None
         L.ko_rows_per_wave.argtypes = [ctypes.c_int64]
         L.ko_rows_per_wave.restype = ctypes.c_int64
         L.ko_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
@@ -169,6 +176,37 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
 def csum(x: np.ndarray) -> np.float32:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return np.float32(lib().ko_csum(_ptr(x), x.size))
+
+
+def torch_inner_sum(x: np.ndarray) -> np.float32:
+    """torch CPU's fp32 sum of a contiguous row (ko_torch_inner_sum)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return np.float32(lib().ko_torch_inner_sum(_ptr(x), x.size))
+
+
+def torch_outer_sum(x: np.ndarray) -> np.ndarray:
+    """torch CPU's fp32 sums over the rows of a contiguous [R, C] matrix (ko_torch_outer_sum)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    R, C = x.shape
+    out = np.zeros(C, dtype=np.float32)
+    lib().ko_torch_outer_sum(_ptr(x), R, C, _ptr(out))
+    return out
+
+
+def torch_sumsq(x: np.ndarray) -> np.float32:
+    """torch CPU's fp32 sum of squares inside t.norm(2) (ko_torch_sumsq)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return np.float32(lib().ko_torch_sumsq(_ptr(x), x.size))
+
+
+@contextlib.contextmanager
+def torch_order():
+    """Within the block every oracle step sums in torch CPU's order (tests only)."""
+    TORCH_ORDER[0] = True
+    try:
+        yield
+    finally:
+        TORCH_ORDER[0] = False
 
 
 def rows_per_wave(C: int) -> int:
@@ -369,6 +407,11 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
         st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
 
 
+# Tests only: TORCH_ORDER[0] = True makes every tensor of the following steps sum
+# in torch CPU's order (KoTensor.torch_order) instead of the canonical one.
+TORCH_ORDER = [False]
+
+
 def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) -> KoTensor:
     st = prm.state
     R, C = prm.eff
@@ -393,6 +436,7 @@ def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) 
                 t.noise[s] = _ptr(noise[s])
     t.out_m = _ptr(out_m)
     t.fac_override = _ptr(fac_override)
+    t.torch_order = int(TORCH_ORDER[0])
     return t
 
 
@@ -640,9 +684,9 @@ def values(a: np.ndarray, dtype: int) -> np.ndarray:
 
 
 __all__ = [
-    "BF16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "bf16_to_f32", "csum",
+    "BF16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "TORCH_ORDER", "bf16_to_f32", "csum",
     "dequant", "f32_to_bf16", "fourbit_block_size", "gc_bf16", "init_state", "lerp", "lib", "make_param",
     "newton_schulz", "philox4x32_10", "quant_4bit", "quant_int8", "rows_per_wave", "sr_noise", "sr_round",
-    "values",
+    "torch_inner_sum", "torch_order", "torch_outer_sum", "torch_sumsq", "values",
 ]
 _ = math

@@ -18,9 +18,16 @@ the ground truth for one-op rounding questions the fixtures cannot isolate:
 * add_(x, alpha) on bf16 tensors: KProdigy's bf16 momentum
   (src/kaon/kprodigy.py:738-740) -- torch CPU's vector loop rounds alpha to bf16.
 
+* the fp32 reduction orders of the five sums in a step (the oracle's
+  torch-order mode, KoTensor.torch_order): x.sum() / x.mean(-1) of a contiguous
+  row, x.mean(-2) over the rows, the bf16 GC mean, and t.norm(2) -- each
+  reproduced bit for bit (ko_torch_inner_sum, ko_torch_outer_sum,
+  ko_torch_sumsq) on sizes that cross every cascade level and vector tail.
+
 A plausible slip -- a lerp without the fma, the branch threshold on the wrong
-side, truncation instead of RNE, an fp32 instead of a bf16 GC -- fails one of
-these on the seeded inputs.
+side, truncation instead of RNE, an fp32 instead of a bf16 GC, a 16-lane
+instead of an 8-lane norm, a cascade level too few -- fails one of these on the
+seeded inputs.
 """
 import numpy as np
 import pytest
@@ -130,3 +137,59 @@ def test_bf16_add_alpha_is_rounded_to_bf16_by_torch_cpu():
     assert np.array_equal(got, want)
     f32a = O.bf16_to_f32(O.f32_to_bf16((mb + np.float32(alpha) * gf).astype(np.float32)))
     assert (f32a != want).sum() > n // 10
+
+
+_SIZES = [1, 7, 8, 9, 31, 32, 33, 64, 100, 255, 256, 257, 640, 1280, 2048, 2880, 4097, 5760, 11520, 65536 + 17,
+          300_000]
+
+
+def test_torch_row_sum_order_reproduced():
+    """torch CPU's fp32 x.sum() and row sums (the inner cascade with 8-float vectors)."""
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(21)
+    for n in _SIZES:
+        x = (rng.standard_normal(n) * np.exp(rng.uniform(-8, 8, n))).astype(np.float32)
+        want = np.float32(torch.from_numpy(x).sum().item())
+        assert O.torch_inner_sum(x).view(np.uint32) == want.view(np.uint32), n
+    for C in (1280, 5, 3):
+        x = (rng.standard_normal((37, C)) ** 2 * 1e-6).astype(np.float32)
+        want = torch.from_numpy(x).mean(dim=-1).numpy()
+        got = np.array([O.torch_inner_sum(r) for r in x], np.float32) / np.float32(C)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), C
+
+
+@pytest.mark.parametrize("shape", [(320, 2880), (1280, 1280), (17, 40), (640, 5760), (100, 13), (5, 300), (9, 1),
+                                   (33, 6), (70, 4), (3, 7)])
+def test_torch_column_sum_order_reproduced(shape):
+    """torch CPU's x.mean(dim=-2) of an fp32 matrix (the outer cascade: 32-column blocks,
+    then 8-column blocks and single columns through the 4-way row split)."""
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal(shape) ** 2 * np.exp(rng.uniform(-6, 6, shape))).astype(np.float32)
+    want = torch.from_numpy(x).mean(dim=-2).numpy()
+    got = O.torch_outer_sum(x) / np.float32(shape[0])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_torch_norm_order_reproduced():
+    """torch CPU's fp32 t.norm(2): 8 lanes of sequential fused multiply-adds, lanes
+    added in order, then the tail.  A 16-lane model or an unfused one fails."""
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(23)
+    for n in _SIZES:
+        x = (rng.standard_normal(n) * np.exp(rng.uniform(-6, 6, n))).astype(np.float32)
+        want = np.float32(torch.from_numpy(x).norm(2).item())
+        got = np.sqrt(O.torch_sumsq(x), dtype=np.float32)
+        assert got.view(np.uint32) == want.view(np.uint32), n
+
+
+def test_torch_bf16_mean_is_one_rounding_of_the_fp32_cascade_sum():
+    """g.mean(dims) on bf16: the bf16 rounding of (fp32 cascade sum of the upcast row) / C."""
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(24)
+    for C in (640, 1280, 2048, 2880, 5760):
+        g = torch.from_numpy((rng.standard_normal((200, C)) * np.exp(rng.uniform(-4, 4, (200, 1))))
+                             .astype(np.float32)).bfloat16()
+        want = g.mean(dim=1).view(torch.int16).numpy().view(np.uint16)
+        sums = np.array([O.torch_inner_sum(r) for r in g.float().numpy()], np.float32)
+        assert np.array_equal(O.f32_to_bf16(sums / np.float32(C)), want), C

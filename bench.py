@@ -19,11 +19,21 @@ Besides the JSON line's ``value`` (Gparam/s) the line carries
   time), its algorithmic HBM bytes per launch (bytes/param of that kernel x
   params) divided by its average duration, measured with HIP events on the
   launch stream (one phase at a time through ``kaon_adakaon_phases``);
+  ``traffic`` is the HBM bytes per launch that rocprofv3's FETCH_SIZE and
+  WRITE_SIZE counters measured for that kernel, read from the committed
+  profiles/*_pmc.md summary only when the summary's source hash matches the
+  current kernel sources (null otherwise);
 * ``step_roofline``: the whole step at the algorithmic 2 + 4 + 2*b_m bytes/param
-  (g read, p read+write, momentum read+write), against 8 TB/s and against a
-  copy kernel measured on the same device;
-* ``cpu_baseline``: the CPU oracle (oracle/kaon_oracle.c, one thread) stepping a
-  bounded sample of the same tensors -- a reported baseline, not the target.
+  (g read, p read+write, momentum read+write), against 8 TB/s, against a copy
+  kernel measured on the same device (1:1 read:write) and against a kernel
+  with the apply's own access mix (``kaon_apply_ceiling``: bf16 g and p and
+  int8 m read, p and m written, 5:3);
+* ``lora_bag`` (default workload): ms per step of the launch-bound regime, the
+  reference's LoRA proxy bag of 512 fp32 [8, 16] tensors;
+* ``cpu_baseline``: the CPU oracle (oracle/kaon_oracle.c) stepping the same
+  tensors on the host's cores (at most 16 threads), the median of three steps
+  after a warmup, the whole set when a step fits the time budget -- a reported
+  baseline, not the target.
 """
 from __future__ import annotations
 
@@ -128,19 +138,36 @@ def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict |
     return 0.0
 
 
+KERNEL_SOURCES = ("k-optimizers_amd/csrc/kaon_step.hip", "k-optimizers_amd/csrc/kaon_device.h")
+
+
+def kernel_source_hash() -> str:
+    """sha256 (first 16 hex digits) of the step kernels' source files, the key a
+    committed PMC summary records for the build it measured."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(workload: str, phase: int) -> float | None:
     """HBM bytes per launch of a phase kernel, from the rocprofv3 PMC summaries
     committed under profiles/ (FETCH_SIZE and WRITE_SIZE, each scaled by what
-    the counter reads for a copy kernel of known size); None when no summary
-    covers this workload and phase."""
+    the counter reads for a copy kernel of known size).  Only a summary taken
+    with the current kernel sources counts (its ``source=`` hash must equal
+    kernel_source_hash()); otherwise None."""
     import glob
     import re
 
+    src = kernel_source_hash()
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_pmc.md"))):
         with open(path) as fh:
             for line in fh:
-                m = re.match(r"traffic: workload=(\S+) phase=(\d+) kernel=\S+ bytes=(\S+)", line.strip())
-                if m and m.group(1) == workload and int(m.group(2)) == phase:
+                m = re.match(r"traffic: workload=(\S+) phase=(\d+) kernel=\S+ bytes=(\S+) source=(\w+)", line.strip())
+                if m and m.group(1) == workload and int(m.group(2)) == phase and m.group(4) == src:
                     return float(m.group(3))
     return None
 
@@ -200,6 +227,51 @@ def copy_ceiling_gbs(dev, nbytes=4 << 30, reps=10) -> float:
     ms = t0.elapsed_time(t1) / reps
     del src, dst
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
+
+
+def apply_mix_ceiling_gbs(dev, n=512 << 20, reps=10) -> float:
+    """kaon_apply_ceiling: the apply's streams (bf16 g and p read, int8 m read,
+    p and m written; 8 B per element) without its arithmetic, n elements."""
+    import torch
+    from kaon_amd import _lib
+
+    g = torch.ones(n, dtype=torch.int16, device=dev)
+    p = torch.ones(n, dtype=torch.int16, device=dev)
+    m = torch.zeros(n, dtype=torch.int8, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    lib = _lib.lib()
+    _lib.check(lib.kaon_apply_ceiling(g.data_ptr(), p.data_ptr(), m.data_ptr(), n, s), "kaon_apply_ceiling")
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        lib.kaon_apply_ceiling(g.data_ptr(), p.data_ptr(), m.data_ptr(), n, s)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    del g, p, m
+    return 8.0 * n / (ms * 1e-3) / 1e9
+
+
+def lora_bag_ms(dev, steps=50, warmup=5) -> float:
+    """ms per step of the launch-bound regime: the reference's LoRA proxy bag
+    (512 fp32 [8, 16] tensors, Adakaon with bf16 momentum), HIP events."""
+    import torch
+    from kaon_amd import workloads
+
+    w = WORKLOADS["lora_bag"]
+    params = workloads.make_params(w["shapes"], dev, seed=0, dtype=torch.float32)
+    opt = make_opt("lora_bag", params)
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        opt.step()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
 
 
 def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
@@ -284,9 +356,27 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
     return {ph: sum(v) / len(v) for ph, v in out.items()}
 
 
-def cpu_baseline(params, name, seconds: float) -> dict:
-    """The CPU oracle (single thread) stepping tensors of the same set until the
-    time budget is spent; Gparam/s over the tensors it finished."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(params, name, budget_s: float) -> dict:
+    """The CPU oracle (oracle/kaon_oracle.c, the C restatement of the reference's
+    per-element step) over the same tensors on the host's cores: one oracle
+    optimizer per tensor, the tensors spread over a thread pool (the C calls run
+    outside the GIL), one warmup step, then the median of three timed steps.
+    The whole set is timed when a step fits the budget; otherwise the largest
+    prefix of a fixed random order of the tensors that does."""
+    import statistics
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
     import torch
 
@@ -310,33 +400,63 @@ def cpu_baseline(params, name, seconds: float) -> dict:
                      d_update_freq=1, slice_p=kw.get("slice_p", 1), k=0,
                      second_moment=kw.get("second_moment", "full"), eps_factored=1e-30, cautious=False,
                      factor_conv_as_matrix=True)
-    order = np.random.default_rng(0).permutation(len(params))
+    order = [int(i) for i in np.random.default_rng(0).permutation(len(params))]
     if w["opt"] == "adamuon":
-        # the oracle's scalar GEMMs take minutes on a 1280 x 11520 matrix: sample the
+        # the oracle's scalar GEMMs take minutes on a 1280 x 11520 matrix: the
         # matrices with min(R, C) <= 640 (and the 1-D params)
-        order = [i for i in order if params[int(i)].ndim < 2 or min(params[int(i)].shape[0],
-                 params[int(i)].numel() // params[int(i)].shape[0]) <= 640]
-    done = 0
-    elapsed = 0.0
-    ntens = 0
-    for idx in order:
-        p = params[int(idx)]
-        shape = tuple(p.shape)
+        order = [i for i in order if params[i].ndim < 2 or min(params[i].shape[0],
+                                                               params[i].numel() // params[i].shape[0]) <= 640]
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    oopt_name = "adakaon" if w["opt"] == "nekaon" else ("adakaon" if w["opt"] == "msam" else w["opt"])
+
+    def build(i):
+        p = params[i]
         prm = O.OParam(p=p.detach().view(torch.int16).cpu().numpy().view(np.uint16).copy(), p_dtype=O.BF16,
-                       shape=shape, tensor_id=int(idx),
+                       shape=tuple(p.shape), tensor_id=i,
                        g=p.grad.view(torch.int16).cpu().numpy().view(np.uint16).copy(), g_dtype=O.BF16)
-        oopt = O.OracleOptimizer([prm], "adakaon" if w["opt"] == "nekaon" else w["opt"], group, seed=0)
+        return O.OracleOptimizer([prm], oopt_name, group, seed=0), prm.numel
+
+    with ThreadPoolExecutor(threads) as pool:
+        # warmup on the whole candidate set, timed per tensor to size the timed set
+        opts, sizes, secs = [], [], []
+        t_all = 0.0
+        for i in order:
+            o, n = build(i)
+            opts.append(o)
+            sizes.append(n)
+        def step_one(o):
+            t = time.perf_counter()
+            o.step()
+            return time.perf_counter() - t
         t0 = time.perf_counter()
-        oopt.step()
-        elapsed += time.perf_counter() - t0
-        done += prm.numel
-        ntens += 1
-        if elapsed >= seconds:
-            break
-    return {"value": done / elapsed / 1e9, "unit": "Gparam/s", "cores": 1, "kind": "port",
-            "sample": f"one {w['opt']} step of {ntens} tensors ({done / 1e6:.1f}M params) drawn at random from "
-                      f"the same set{' (matrices with min(R, C) <= 640)' if w['opt'] == 'adamuon' else ''}, "
-                      f"CPU oracle oracle/kaon_oracle.c, 1 thread, {elapsed:.1f}s"}
+        secs = list(pool.map(step_one, opts))
+        warm = time.perf_counter() - t0
+        # the timed set: everything if a step fits the budget, else a prefix of the order
+        k = len(opts)
+        if warm > budget_s:
+            acc, k = 0.0, 0
+            for s_ in secs:
+                if acc + s_ / threads > budget_s:
+                    break
+                acc += s_ / threads
+                k += 1
+            k = max(k, 1)
+        timed = opts[:k]
+        nparam = sum(sizes[:k])
+        walls = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            list(pool.map(lambda o: o.step(), timed))
+            walls.append(time.perf_counter() - t0)
+    med = statistics.median(walls)
+    what = "the whole set" if k == len(order) and w["opt"] != "adamuon" else f"{k} of the tensors"
+    return {"value": nparam / med / 1e9, "unit": "Gparam/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": f"one {w['opt']} step of {what} ({k} tensors, {nparam / 1e6:.1f}M params"
+                      f"{'; matrices with min(R, C) <= 640' if w['opt'] == 'adamuon' else ''}), CPU oracle "
+                      f"oracle/kaon_oracle.c over {threads} threads (one oracle optimizer per tensor), "
+                      f"median of 3 steps after 1 warmup: {med:.2f} s/step (warmup {warm:.1f} s)",
+            "steps_s": [round(x, 3) for x in walls]}
 
 
 def main() -> int:
@@ -345,7 +465,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="adakaon_int8", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="time budget of one CPU-baseline step (the whole set is timed when it fits)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
     args = ap.parse_args()
@@ -405,6 +526,7 @@ def main() -> int:
         print(json.dumps(out), flush=True)
         return 0
     ceiling = copy_ceiling_gbs(dev)
+    mix = apply_mix_ceiling_gbs(dev)
     out = {
         "metric": METRIC, "value": round(gps, 2), "unit": "Gparam/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -415,7 +537,8 @@ def main() -> int:
                    "parallelism": "none (1 GPU)"},
         "step_roofline": {"bound": "hbm", "bytes_per_param": b_alg, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                          "copy_ceiling": round(ceiling, 1), "frac_of_copy": round(step_gbs / ceiling, 4)},
+                          "copy_ceiling": round(ceiling, 1), "frac_of_copy": round(step_gbs / ceiling, 4),
+                          "apply_mix_ceiling": round(mix, 1), "frac_of_apply_mix": round(step_gbs / mix, 4)},
     }
     if not args.no_breakdown:
         br = phase_breakdown(opt, args.workload)
@@ -435,9 +558,16 @@ def main() -> int:
             out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),
                                "kernel": f"phase {dom} ({PHASE_NAMES[dom]})", "bytes_per_param": bpp,
-                               "avg_ms": round(br[dom], 4)}
+                               "avg_ms": round(br[dom], 4), "frac_of_apply_mix": round(ach / mix, 4),
+                               "source": kernel_source_hash()}
         out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())}
+    if args.workload == "adakaon_int8" and not args.no_breakdown:
+        # the launch-bound regime beside the headline (reference: 0.24 ms for its fused Adakaon
+        # on this bag, benchmarks/control/RANKINGS.md:83, on its own hardware)
+        out["lora_bag"] = {"ms_per_step": round(lora_bag_ms(dev), 4), "unit": "ms", "config": WORKLOADS["lora_bag"]["desc"]}
     if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        del opt
         out["cpu_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0

@@ -373,6 +373,11 @@ int kaon_sr_noise(uint16_t* out, int64_t n, uint64_t seed, uint32_t step, uint32
 /* Streaming copy (bytes must be a multiple of 16, both pointers 16-B aligned): the
  * measured HBM read+write ceiling the step is compared against. */
 int kaon_copy(const void* src, void* dst, int64_t bytes, void* stream);
+/* The apply's access mix as a measured ceiling: per element read 2 B of bf16 g,
+ * 2 B of bf16 p and 1 B of int8 m, write p and m back (5:3 read:write, 8 B per
+ * element, n % 8 == 0).  No counterpart in the reference: it bounds what the
+ * phase-6 apply (the same streams plus its arithmetic) can reach on the device. */
+int kaon_apply_ceiling(const void* g, void* p, void* m, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

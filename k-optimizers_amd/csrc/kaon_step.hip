@@ -3926,6 +3926,52 @@ int kaon_sr_noise(uint16_t* out, int64_t n, uint64_t seed, uint32_t step, uint32
   return check_launch("kaon_sr_noise");
 }
 
+// The apply's HBM access mix without its arithmetic: per 8-element chunk, read
+// 16 B of bf16 g, 16 B of bf16 p and 8 B of int8 m, write p and m back (5:3
+// read:write, 8 B per element), non-temporal like the apply's streams.  p and m
+// are changed by an integer add so no access can be dropped.
+__global__ __launch_bounds__(KAON_WG) void k_apply_mix(const ku4* __restrict__ g_, ku4* __restrict__ p_,
+                                                       ku2* __restrict__ m_, int64_t nch) {
+  const KAON_G ku4* g = G(g_);
+  KAON_G ku4* p = G(p_);
+  KAON_G ku2* m = G(m_);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + stride < nch; i += 2 * stride) {
+    const ku4 ga = ld_stream<true>(g + i), gb = ld_stream<true>(g + i + stride);
+    ku4 pa = ld_stream<true>(p + i), pb = ld_stream<true>(p + i + stride);
+    ku2 ma = ld_stream<true>(m + i), mb = ld_stream<true>(m + i + stride);
+    pa.x += ga.x; pa.y += ga.y; pa.z += ga.z; pa.w += ga.w;
+    pb.x += gb.x; pb.y += gb.y; pb.z += gb.z; pb.w += gb.w;
+    ma.x += 1u; ma.y += 1u; mb.x += 1u; mb.y += 1u;
+    st_stream(p + i, pa);
+    st_stream(p + i + stride, pb);
+    st_stream(m + i, ma);
+    st_stream(m + i + stride, mb);
+  }
+  for (; i < nch; i += stride) {
+    const ku4 ga = ld_stream<true>(g + i);
+    ku4 pa = ld_stream<true>(p + i);
+    ku2 ma = ld_stream<true>(m + i);
+    pa.x += ga.x; pa.y += ga.y; pa.z += ga.z; pa.w += ga.w;
+    ma.x += 1u; ma.y += 1u;
+    st_stream(p + i, pa);
+    st_stream(m + i, ma);
+  }
+}
+
+int kaon_apply_ceiling(const void* g, void* p, void* m, int64_t n, void* stream) {
+  if (n <= 0) return 0;
+  if ((n & 7) || (((uintptr_t)g | (uintptr_t)p) & 15) || ((uintptr_t)m & 7))
+    return fail("kaon_apply_ceiling: needs n % 8 == 0, 16-byte aligned g and p, 8-byte aligned m");
+  const int64_t nch = n / 8;
+  int64_t grid = (nch + KAON_WG * 2 - 1) / (KAON_WG * 2);
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(k_apply_mix, dim3((unsigned)grid), dim3(KAON_WG), 0, (hipStream_t)stream, (const ku4*)g,
+                     (ku4*)p, (ku2*)m, nch);
+  return check_launch("kaon_apply_ceiling");
+}
+
 int kaon_copy(const void* src, void* dst, int64_t bytes, void* stream) {
   if (bytes <= 0) return 0;
   if ((bytes & 15) || (((uintptr_t)src | (uintptr_t)dst) & 15)) return fail("kaon_copy: needs 16-byte alignment");

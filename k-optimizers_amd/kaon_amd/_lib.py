@@ -130,6 +130,7 @@ SIGNATURES = {
     "kaon_sr_round": ([_VP, _VP, _I64, _VP, _VP], ctypes.c_int),
     "kaon_sr_noise": ([_VP, _I64, _U64, _U32, _U32, _U32, _VP], ctypes.c_int),
     "kaon_copy": ([_VP, _VP, _I64, _VP], ctypes.c_int),
+    "kaon_apply_ceiling": ([_VP, _VP, _VP, _I64, _VP], ctypes.c_int),
 }
 
 _handle: ctypes.CDLL | None = None

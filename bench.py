@@ -138,7 +138,8 @@ def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict |
     return 0.0
 
 
-KERNEL_SOURCES = ("k-optimizers_amd/csrc/kaon_step.hip", "k-optimizers_amd/csrc/kaon_device.h")
+KERNEL_SOURCES = ("k-optimizers_amd/csrc/kaon_step.hip", "k-optimizers_amd/csrc/kaon_fast.hip",
+                  "k-optimizers_amd/csrc/kaon_common.h", "k-optimizers_amd/csrc/kaon_device.h")
 
 
 def kernel_source_hash() -> str:

@@ -33,6 +33,7 @@
 #include <cstring>
 #include <string>
 
+#include "kaon_common.h"
 #include "kaon_device.h"
 #include "kaon_ns.h"
 
@@ -58,104 +59,6 @@ int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(what, e);
   return 0;
-}
-
-// ------------------------------------------------------------ workspace views
-struct Ws {
-  float* base;
-  __device__ KAON_G float* mu(const KaonTensor& T) const { return G(base + T.ws_row); }
-  __device__ KAON_G float* rf(const KaonTensor& T) const { return G(base + T.ws_row + T.R); }
-  __device__ KAON_G float* rs(const KaonTensor& T) const { return G(base + T.ws_row + 2 * T.R); }
-  __device__ KAON_G uint32_t* ramax(const KaonTensor& T) const {
-    return G((uint32_t*)(base + T.ws_row + 3 * T.R));
-  }
-  __device__ KAON_G float* roldsc(const KaonTensor& T) const { return G(base + T.ws_row + 4 * T.R); }
-  __device__ KAON_G float* cf(const KaonTensor& T) const { return G(base + T.ws_col); }
-  __device__ KAON_G float* part(const KaonTensor& T) const { return G(base + T.ws_part); }
-  __device__ KAON_G uint32_t* bamax(const KaonTensor& T) const { return G((uint32_t*)(base + T.ws_blk)); }
-  __device__ KAON_G float* boldsc(const KaonTensor& T, int64_t nb) const { return G(base + T.ws_blk + nb); }
-  __device__ KAON_G float* scal(const KaonTensor& T) const { return G(base + T.ws_scal); }
-  // generic address of the keep-count word (for atomics)
-  __device__ uint32_t* keep_ctr(const KaonTensor& T) const { return (uint32_t*)(base + T.ws_scal) + 1; }
-  // AdaMuon: the bf16 momentum, then the orthogonal factor O, [R, C] (first
-  // buffer of the Newton-Schulz block)
-  __device__ uint16_t* mo(const KaonTensor& T) const { return (uint16_t*)(base + T.ws_aux); }
-  // what the row kernels read as "the gradient": O for AdaMuon's factored passes
-  __device__ const void* src(const KaonTensor& T, int flags) const {
-    return (flags & KAON_F_SRC_O) ? (const void*)mo(T) : T.g;
-  }
-};
-
-// Streaming accesses: the gradient, parameter and momentum streams of a
-// 2.6B-param step are far larger than the caches, so they are loaded and
-// stored as non-temporal accesses (NT); small reused arrays (column
-// factors, per-row values) are not.
-template <bool NT, class V>
-__device__ __forceinline__ V ld_stream(const KAON_G V* p) {
-  return NT ? __builtin_nontemporal_load(p) : *p;
-}
-template <class V>
-__device__ __forceinline__ void st_stream(KAON_G V* p, V v) {
-  __builtin_nontemporal_store(v, p);
-}
-
-template <int DT>
-__device__ __forceinline__ float round_to(float x) {
-  return DT == KAON_BF16 ? rbf(x) : x;
-}
-
-__device__ __forceinline__ int64_t nblocks4(const KaonTensor& T) { return (T.n + T.block4 - 1) / T.block4; }
-
-// Rows [rb, re) of the calling wave inside slice `it` (RW rows per wave).
-struct WaveRows {
-  int64_t rb, re;
-  int w, lane;
-};
-__device__ __forceinline__ WaveRows wave_rows(const KaonItem& it) {
-  WaveRows wr;
-  // the wave index is uniform across the wave; readfirstlane tells the compiler
-  wr.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  wr.lane = threadIdx.x & 63;
-  const int64_t end = (int64_t)it.row0 + it.nrows;
-  wr.rb = min((int64_t)it.row0 + (int64_t)wr.w * it.kind, end);
-  wr.re = min(wr.rb + it.kind, end);
-  return wr;
-}
-
-// Slice sl of a run item (rows [row0 + 4 RW sl, ...), RW = kind) and the
-// number of slices in the run.
-__device__ __forceinline__ KaonItem slice_item(const KaonItem& run, int sl) {
-  KaonItem s = run;
-  const int span = 4 * run.kind;
-  s.row0 = run.row0 + sl * span;
-  s.nrows = min(span, run.nrows - sl * span);
-  return s;
-}
-__device__ __forceinline__ int run_slices(const KaonItem& run) {
-  return (run.nrows + 4 * run.kind - 1) / (4 * run.kind);
-}
-// Column partial of a run: one row of C floats per run.
-__device__ __forceinline__ KAON_G float* run_part(const Ws& ws, const KaonTensor& T, const KaonItem& run) {
-  return ws.part(T) + (int64_t)(run.row0 / (KAON_RUN * 4 * run.kind)) * T.C;
-}
-
-// Chunks of a row: the element range [8c, 8c+8) clipped to the row length.
-__device__ __forceinline__ int chunk_cnt(int64_t c, int64_t C) {
-  const int64_t j0 = c * 8;
-  return j0 >= C ? 0 : (int)min<int64_t>(8, C - j0);
-}
-
-// Zero what phase 5 accumulates with atomics (keep-count; 4-bit block absmax
-// of blocks that straddle rows).  Run by the phase-1 slice.
-__device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const Ws& ws, int codec) {
-  if (it.row0 == 0 && threadIdx.x == 0) ((KAON_G uint32_t*)ws.scal(T))[1] = 0u;
-  if (codec == KAON_MOM_4BIT) {
-    const int64_t e_begin = (int64_t)it.row0 * T.C;
-    const int64_t e_end = (int64_t)(it.row0 + it.nrows) * T.C;
-    if (e_end <= e_begin) return;
-    const int64_t b0 = e_begin / T.block4, b1 = (e_end - 1) / T.block4;
-    for (int64_t b = b0 + threadIdx.x; b <= b1; b += KAON_WG) ws.bamax(T)[b] = 0u;
-  }
 }
 
 // Columns per LDS segment of the streamed rows' column fold (phase 1).
@@ -529,22 +432,6 @@ __global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restric
 // issued before the first use, so each lane keeps up to 24 x 16 bytes in
 // flight; the row reductions and the column fold then run from registers.
 // The arithmetic and its order are those of k_stats / k_ss.
-
-__device__ __forceinline__ void unpack8(const ku4 v, float o[8]) {
-  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
-  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
-  o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xFFFF0000u);
-  o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xFFFF0000u);
-}
-
-// Per-row values of a wave group: lane j (< nrows) loads row rb + j's value,
-// issued with the chunk loads; lane_val(v, j) hands row j's value to the wave.
-__device__ __forceinline__ int64_t lane_row(int64_t rb, int nrows, int lane) {
-  return rb + (lane < nrows ? lane : 0);
-}
-__device__ __forceinline__ float lane_val(float v, int j) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-}
 
 // Chunk k of the lane in each of the wave group's rows.  Every load is
 // issued unconditionally from a valid address (rows past the group and
@@ -964,13 +851,6 @@ __device__ __forceinline__ void st_mom_at(void* mbuf, int64_t n, int64_t e0, int
 template <int CODEC>
 __device__ __forceinline__ void st_mom_raw(const KaonTensor& T, int64_t e0, int cnt, bool vec, const uint32_t q[8]) {
   st_mom_at<CODEC>(T.m, T.n, e0, cnt, vec, q);
-}
-
-// MSAM perturbation value: clamp(nan_to_num(x, 0, +b, -b), -b, b) (msam.py:222-230).
-__device__ __forceinline__ float msam_e(float x, float bound) {
-  if (x != x) return 0.0f;
-  if (isinf(x)) return x > 0.0f ? bound : -bound;
-  return fminf(fmaxf(x, -bound), bound);
 }
 
 // int8 dequant q*sc with q the stored byte: (ub - 128)*sc = fma(ub, sc, -128 sc)
@@ -2550,586 +2430,6 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
   }
 }
 
-// =============================================================== fast path
-// Phases 5 and 6 specialized at compile time for bf16 params and grads,
-// stochastic-rounding writes and 16-byte-aligned rows: every full 8-element
-// chunk runs straight-line code; only a row's partial last chunk takes the
-// generic per-element route.  FLAGS: bit 0 GC, 1 cautious, 2 weight decay,
-// 3 Nekaon removal, 4 Nekaon climb.
-enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16 };
-
-// int8 requant code of mf with r = RN64(1/scale), as a float in [-127, 127]
-__device__ __forceinline__ float q_int8(float mf, double r) {
-  const float x = rintf(div_r64(mf, r));
-  return fminf(fmaxf(x, -127.0f), 127.0f);
-}
-
-// Four int8 codes (floats in [-127, 127]) as the stored little-endian bytes:
-// code + 128 is exact in [1, 255]; v_cvt_pk_u8_f32 inserts each byte and the
-// xor turns offset-binary into two's complement.
-__device__ __forceinline__ uint32_t pack_int8x4(float a, float b, float c, float d) {
-  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(a + 128.0f, 0, 0u);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(b + 128.0f, 1, w);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.0f, 2, w);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(d + 128.0f, 3, w);
-  return w ^ 0x80808080u;
-}
-
-// Per-tensor values of a fast slice, read from its descriptor once per
-// workgroup.  Offsets inside the tensor are 32-bit (the planner keeps tensors
-// of more than 2^31 elements off this kernel), so every access is a uniform
-// base plus a 32-bit byte offset, and nothing is reloaded after a store.
-struct FastCtx {
-  const KAON_G uint8_t* g;       // bf16 grads
-  KAON_G uint8_t* p;             // bf16 params
-  KAON_G uint8_t* m;             // momentum codes or bf16 momentum
-  KAON_G uint8_t* msc;           // momentum scales (per row or per block)
-  const KAON_G uint8_t* cf;      // column factors (Adakaon)
-  KAON_G uint8_t* bamax;         // 4-bit: per-block |m| maximum
-  KAON_G uint8_t* boldsc;        // 4-bit: per-block scale before the step
-  const KAON_G uint16_t* nz[3];  // injected noise streams, or null
-  const KAON_G uint8_t* m2;      // AdaPNM: the negative buffer (read only)
-  const KAON_G uint8_t* m2sc;    // AdaPNM: its scales
-  const KAON_G uint8_t* o;       // AdaMuon: the orthogonal factor O (bf16, row-major like g)
-  uint32_t tid;                  // Philox tensor id
-  int bsh;                       // 4-bit: log2 of the block size
-  int GL;                        // 4-bit: lanes per block
-  bool xrow;                     // 4-bit: blocks cross rows (C % block != 0)
-};
-
-// noise8 of the chunk at element e0 < 2^31 (the counter's high word is 0).
-__device__ __forceinline__ void noise8_u32(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream, uint32_t e0,
-                                           const KAON_G uint16_t* inj, uint32_t w[8]) {
-  if (inj) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      w[i] = inj[e0 + i];
-      settle(w[i]);
-    }
-    return;
-  }
-  uint32_t c[4] = {e0 >> 3, 0u, tid, stream};
-  philox10(c, (uint32_t)seed, step);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[2 * i] = c[i] & 0xFFFFu;
-    w[2 * i + 1] = c[i] >> 16;
-  }
-}
-
-// Global loads of one chunk, issued a chunk ahead of its arithmetic.
-struct FastIn {
-  ku4 g, p, m16;
-  ku2 m8;
-  uint32_t m4;
-  kf4 c0, c1;
-  float bo, ba;  // 4-bit: block scale before the step, block |m| maximum
-  ku4 n16;       // AdaPNM: the negative buffer (bf16, int8, 4-bit) and its 4-bit block scale
-  ku2 n8;
-  uint32_t n4;
-  float bn;
-  ku4 o;         // AdaMuon: O
-};
-
-// AdaMuon's keep count reads no momentum (the update is O's; the momentum of
-// the raw grad was stepped and its absmax taken by the momentum pass)
-template <int OPT, int PHASE>
-constexpr bool fast_reads_m() {
-  return !(OPT == KAON_OPT_ADAMUON && PHASE == 5);
-}
-
-// Which passes of the specialized kernel read the weights: the apply, and for
-// Adakaon's coupled form of weight decay also the keep count (AdaPNM decays p
-// in the apply only).
-template <int OPT, int PHASE, int FLAGS>
-constexpr bool fast_needs_p() {
-  return PHASE == 6 || ((FLAGS & FF_WD) && OPT != KAON_OPT_ADAPNM);
-}
-
-template <int OPT, int PHASE, int CODEC, int FLAGS>
-__device__ __forceinline__ void fast_load(FastIn& in, const FastCtx& X, uint32_t e0, uint32_t j0) {
-  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
-  constexpr bool RM = fast_reads_m<OPT, PHASE>();
-  const ku4 z4 = ku4{0u, 0u, 0u, 0u};
-  in.g = ld_stream<true>((const KAON_G ku4*)(X.g + 2u * e0));
-  in.p = NEEDP ? ld_stream<true>((const KAON_G ku4*)(X.p + 2u * e0)) : z4;
-  in.o = MUON ? *(const KAON_G ku4*)(X.o + 2u * e0) : z4;
-  in.m8 = RM && CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m + e0)) : ku2{0u, 0u};
-  in.m4 = RM && CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m + (e0 >> 1))) : 0u;
-  in.m16 = RM && CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m + 2u * e0)) : z4;
-  in.n8 = PNM && CODEC == KAON_MOM_INT8 ? ld_stream<true>((const KAON_G ku2*)(X.m2 + e0)) : ku2{0u, 0u};
-  in.n4 = PNM && CODEC == KAON_MOM_4BIT ? ld_stream<true>((const KAON_G uint32_t*)(X.m2 + (e0 >> 1))) : 0u;
-  in.n16 = PNM && CODEC == KAON_MOM_BF16 ? ld_stream<true>((const KAON_G ku4*)(X.m2 + 2u * e0)) : z4;
-  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
-    in.c0 = *(const KAON_G kf4*)(X.cf + 4u * j0);
-    in.c1 = *(const KAON_G kf4*)(X.cf + 4u * j0 + 16u);
-  } else {
-    in.c0 = in.c1 = kf4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-  in.bo = in.ba = in.bn = 0.0f;
-  if (CODEC == KAON_MOM_4BIT && RM) {
-    const uint32_t blk4 = (e0 >> X.bsh) * 4u;
-    in.bo = *(const KAON_G float*)((PHASE == 5 ? X.msc : X.boldsc) + blk4);
-    if (PHASE == 6) in.ba = *(const KAON_G float*)(X.bamax + blk4);
-    if (PNM) in.bn = *(const KAON_G float*)(X.m2sc + blk4);
-  }
-}
-
-// Completes the loads of `in` on every path (see settle), so that the
-// branches consuming them leave nothing pending for the next prefetch to wait on.
-template <int OPT, int PHASE, int CODEC, int FLAGS>
-__device__ __forceinline__ void fast_settle(const FastIn& in) {
-  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
-  constexpr bool RM = fast_reads_m<OPT, PHASE>();
-  settle(in.g.x); settle(in.g.y); settle(in.g.z); settle(in.g.w);
-  if (MUON) {
-    settle(in.o.x); settle(in.o.y); settle(in.o.z); settle(in.o.w);
-  }
-  if (NEEDP) {
-    settle(in.p.x); settle(in.p.y); settle(in.p.z); settle(in.p.w);
-  }
-  if (RM && CODEC == KAON_MOM_INT8) {
-    settle(in.m8.x); settle(in.m8.y);
-  }
-  if (RM && CODEC == KAON_MOM_4BIT) {
-    settle(in.m4); settle(in.bo);
-    if (PHASE == 6) settle(in.ba);
-  }
-  if (RM && CODEC == KAON_MOM_BF16) {
-    settle(in.m16.x); settle(in.m16.y); settle(in.m16.z); settle(in.m16.w);
-  }
-  if (PNM) {
-    if (CODEC == KAON_MOM_INT8) {
-      settle(in.n8.x); settle(in.n8.y);
-    }
-    if (CODEC == KAON_MOM_4BIT) {
-      settle(in.n4); settle(in.bn);
-    }
-    if (CODEC == KAON_MOM_BF16) {
-      settle(in.n16.x); settle(in.n16.y); settle(in.n16.z); settle(in.n16.w);
-    }
-  }
-  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
-    settle(in.c0.x); settle(in.c0.y); settle(in.c0.z); settle(in.c0.w);
-    settle(in.c1.x); settle(in.c1.y); settle(in.c1.z); settle(in.c1.w);
-  }
-}
-
-// FAC1: clip divisor 1 (skip the exact division).  DQX: int8 dequant as
-// q*scale for rows whose old scale (AdaPNM: either buffer's) is too large for
-// the fma form.  WLO: the momentum lerp weight is below 0.5 (its branch of
-// torch's lerp).
-template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX, bool WLO>
-__device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, const KaonHyper& hp, uint32_t e0,
-                                           float mu, float rf, float oldsc, float m128, float negsc, float m128n,
-                                           float newsc, double rnew, double rfac, double rden, int lane,
-                                           uint32_t& keep, float& amax) {
-  constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
-  constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
-  constexpr bool MOM = CODEC != KAON_MOM_NONE;
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
-  constexpr bool NEEDP = fast_needs_p<OPT, PHASE, FLAGS>();
-  const ku4 gv4 = in.g, pv4 = in.p, mb16 = in.m16;
-  const ku2 mi8 = in.m8;
-  const uint32_t m4 = in.m4;
-  float f[8];
-  if (OPT == KAON_OPT_ADAKAON || PNM || MUON) {
-    f[0] = in.c0.x; f[1] = in.c0.y; f[2] = in.c0.z; f[3] = in.c0.w;
-    f[4] = in.c1.x; f[5] = in.c1.y; f[6] = in.c1.z; f[7] = in.c1.w;
-  }
-  // 4-bit: one block per chunk
-  float b_old = 1.0f, b_new = 1.0f;
-  double b_r = 1.0;
-  uint32_t blk4 = 0;  // byte offset of the chunk's block in the per-block arrays
-  if (CODEC == KAON_MOM_4BIT) {
-    blk4 = (e0 >> X.bsh) * 4u;
-    b_old = in.bo;
-    if (PHASE == 6) {
-      b_new = fmaxf(in.ba, 1e-12f) / 7.0f;
-      b_r = rcp64(b_new);
-    }
-  }
-  float g[8], p[8];
-  unpack8(gv4, g);
-  if (NEEDP) unpack8(pv4, p);
-  if (GC) {
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float a0 = g[i] - mu, a1 = g[i + 1] - mu;
-      rbf2(a0, a1);
-      g[i] = a0;
-      g[i + 1] = a1;
-    }
-  }
-  uint32_t nz0[8], nz1[8], nz2[8];
-  if (NKR && NEEDP) noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
-  if (PHASE == 6) noise8_u32(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
-  if (PHASE == 6 && NKC) noise8_u32(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
-
-  float mold[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (CODEC == KAON_MOM_INT8) {
-      const uint32_t w = i < 4 ? mi8.x : mi8.y;
-      if (DQX)
-        mold[i] = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * oldsc;
-      else
-        mold[i] = __fmaf_rn((float)(((w ^ 0x80808080u) >> (8 * (i & 3))) & 0xFFu), oldsc, m128);
-    } else if (CODEC == KAON_MOM_4BIT) {
-      mold[i] = ((float)((m4 >> (4 * i)) & 0xFu) - 8.0f) * b_old;
-    } else if (CODEC == KAON_MOM_BF16) {
-      const uint32_t mw[4] = {mb16.x, mb16.y, mb16.z, mb16.w};
-      const uint32_t w = mw[i >> 1];
-      mold[i] = (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
-    } else {
-      mold[i] = 0.0f;
-    }
-  }
-  // AdaPNM: the negative buffer, dequantized as the positive one
-  float mng[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    mng[i] = 0.0f;
-    if (!PNM) continue;
-    if (CODEC == KAON_MOM_INT8) {
-      const uint32_t w = i < 4 ? in.n8.x : in.n8.y;
-      if (DQX)
-        mng[i] = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * negsc;
-      else
-        mng[i] = __fmaf_rn((float)(((w ^ 0x80808080u) >> (8 * (i & 3))) & 0xFFu), negsc, m128n);
-    } else if (CODEC == KAON_MOM_4BIT) {
-      mng[i] = ((float)((in.n4 >> (4 * i)) & 0xFu) - 8.0f) * in.bn;
-    } else if (CODEC == KAON_MOM_BF16) {
-      const uint32_t nw[4] = {in.n16.x, in.n16.y, in.n16.z, in.n16.w};
-      const uint32_t w = nw[i >> 1];
-      mng[i] = (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
-    }
-  }
-  float d[8], mf[8], of[8];
-  uint32_t mbits[8];
-  if (MUON) unpack8(in.o, of);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float pw = p[i];
-    if (NKR && NEEDP) pw = bf2f(sr_bf16(p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old), nz0[i]));
-    p[i] = pw;
-    if (MUON) {
-      // the update is O's (factored, clipped, lr = 0.2 lr); the momentum of the
-      // raw grad is requantized in the apply
-      const float u = (of[i] * rf) * f[i];
-      d[i] = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
-      mf[i] = PHASE == 6 ? klerp_b<WLO>(mold[i], g[i], hp.w1) : 0.0f;
-    } else if (PNM) {
-      // this step's positive buffer (decay beta1^2), the pos-neg mix, the
-      // factored preconditioner with the bias correction, clip and lr
-      const float mfv = __fmaf_rn(hp.a1, g[i], mold[i] * hp.b1);
-      const float pn = __fmaf_rn(hp.pn_neg, mng[i], mfv * hp.pn_pos) * hp.pn_rnorm;
-      const float u = pn * ((rf * f[i]) * hp.bc2);
-      d[i] = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
-      mf[i] = mfv;
-      if (CODEC == KAON_MOM_BF16) mbits[i] = f2bf(mfv);
-    } else if (OPT == KAON_OPT_ADAKAON) {
-      const float u = (g[i] * rf) * f[i];
-      const float ud = (FAC1 ? u : div_r64(u, rfac)) * hp.lr;
-      if (CODEC == KAON_MOM_BF16) {
-        const uint32_t mb = f2bf(klerp_b<WLO>(mold[i], rbf(ud), hp.w1));
-        mbits[i] = mb;
-        mf[i] = bf2f(mb);
-        d[i] = mf[i];
-      } else if (MOM) {
-        mf[i] = klerp_b<WLO>(mold[i], ud, hp.w1);
-        d[i] = mf[i];
-      } else {
-        mf[i] = 0.0f;
-        d[i] = ud;
-      }
-    } else {
-      d[i] = ksign(__fmaf_rn(hp.a1, g[i], mold[i] * hp.b1));
-      mf[i] = __fmaf_rn(hp.a2, g[i], mold[i] * hp.b2);
-      if (CODEC == KAON_MOM_BF16) mbits[i] = f2bf(mf[i]);
-    }
-    if (WD && !PNM) d[i] = __fmaf_rn(hp.wdl, pw, d[i]);
-  }
-  if (PHASE == 5) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (CAUT) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
-      // AdaPNM's absmax of the new positive buffer comes from its clip-sum pass,
-      // AdaMuon's from its momentum pass
-      if ((CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON) amax = fmaxf(amax, fabsf(mf[i]));
-    }
-    return;
-  }
-  // ---- phase 6: requant, cautious, SR write (+ Nekaon climb)
-  float mdq[8];
-  uint32_t codes[8];
-  float xq[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (CODEC == KAON_MOM_INT8) {
-      xq[i] = q_int8(mf[i], rnew);
-      mdq[i] = xq[i] * newsc;
-    } else if (CODEC == KAON_MOM_4BIT) {
-      float x = rintf(div_r64(mf[i], b_r));
-      x = fminf(fmaxf(x, -7.0f), 7.0f);
-      codes[i] = (uint32_t)((int)x + 8);
-      mdq[i] = x * b_new;
-    } else if (CODEC == KAON_MOM_BF16) {
-      mdq[i] = mf[i];
-    } else {
-      mdq[i] = 0.0f;
-    }
-  }
-  uint32_t o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float dd = d[i];
-    if (CAUT) dd = div_r64(d[i] * (d[i] * g[i] > 0.0f ? 1.0f : 0.0f), rden);
-    if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
-    // AdaPNM's decoupled decay p * (1 - lr wd), rounded to the param dtype
-    const float pd = PNM && WD ? rbf(p[i] * hp.wdl) : p[i];
-    o[i] = sr_word(pd - dd, nz1[i]);
-    if (NKC) o[i] = sr_word(__uint_as_float(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
-  }
-  ku4 ov;
-  ov.x = pack_hi16(o[0], o[1]);
-  ov.y = pack_hi16(o[2], o[3]);
-  ov.z = pack_hi16(o[4], o[5]);
-  ov.w = pack_hi16(o[6], o[7]);
-  st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
-  if (CODEC == KAON_MOM_INT8) {
-    ku2 mv;
-    mv.x = pack_int8x4(xq[0], xq[1], xq[2], xq[3]);
-    mv.y = pack_int8x4(xq[4], xq[5], xq[6], xq[7]);
-    st_stream((KAON_G ku2*)(X.m + e0), mv);
-  } else if (CODEC == KAON_MOM_4BIT) {
-    uint32_t v = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
-    *(KAON_G uint32_t*)(X.m + (e0 >> 1)) = v;
-    if ((e0 & ((1u << X.bsh) - 1u)) == 0u) *(KAON_G float*)(X.msc + blk4) = b_new;  // the block's first chunk
-  } else if (CODEC == KAON_MOM_BF16) {
-    ku4 mv;
-    mv.x = mbits[0] | (mbits[1] << 16);
-    mv.y = mbits[2] | (mbits[3] << 16);
-    mv.z = mbits[4] | (mbits[5] << 16);
-    mv.w = mbits[6] | (mbits[7] << 16);
-    st_stream((KAON_G ku4*)(X.m + 2u * e0), mv);
-  }
-}
-
-// Fast slices (the planner's fast_eligible tensors): factored, bf16 params and
-// grads, stochastic rounding, 16-byte aligned rows with C % 8 == 0 and, for
-// 4-bit, blocks of 8*G elements with G | 64 (blocks that cross rows take one
-// atomic maximum per chunk instead of the lane-group reduction).
-template <int OPT, int PHASE, int CODEC, int FLAGS>
-__global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__ D,
-                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  constexpr bool CAUT = FLAGS & FF_CAUT;
-  constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
-  constexpr bool PNM = OPT == KAON_OPT_ADAPNM, MUON = OPT == KAON_OPT_ADAMUON;
-  __shared__ uint32_t keep_s[4];
-  const KaonItem it = items[blockIdx.x];
-  const KaonTensor& T = D[it.tensor];
-  const uint32_t C = (uint32_t)T.C;
-  const int64_t n = T.n;
-  const uint32_t nfull = C >> 3;  // full chunks per row
-  const WaveRows wr = wave_rows(it);
-  FastCtx X;
-  X.g = (const KAON_G uint8_t*)G(T.g);
-  X.p = (KAON_G uint8_t*)G(T.p);
-  // AdaPNM: m is this step's positive buffer (m on odd steps, m2 on even ones)
-  const bool swap = PNM && (hp.step & 1u) == 0u;
-  X.m = (KAON_G uint8_t*)G(swap ? T.m2 : T.m);
-  X.msc = (KAON_G uint8_t*)G(swap ? T.m2_scale : T.m_scale);
-  X.m2 = (const KAON_G uint8_t*)G(swap ? T.m : T.m2);
-  X.m2sc = (const KAON_G uint8_t*)G(swap ? T.m_scale : T.m2_scale);
-  X.o = MUON ? (const KAON_G uint8_t*)G(ws.mo(T)) : nullptr;
-  X.cf = (const KAON_G uint8_t*)ws.cf(T);
-  X.bamax = (KAON_G uint8_t*)ws.bamax(T);
-  X.boldsc = CODEC == KAON_MOM_4BIT ? (KAON_G uint8_t*)ws.boldsc(T, nblocks4(T)) : X.bamax;
-#pragma unroll
-  for (int s = 0; s < 3; ++s) X.nz[s] = G(T.noise[s]);
-  X.tid = (uint32_t)T.tensor_id;
-  // 4-bit blocks are 8*GL elements with GL | 64, a power of two
-  X.bsh = CODEC == KAON_MOM_4BIT ? __builtin_ctz((uint32_t)T.block4) : 3;
-  X.GL = CODEC == KAON_MOM_4BIT ? (int)(T.block4 >> 3) : 1;
-  X.xrow = CODEC == KAON_MOM_4BIT && (T.C % T.block4) != 0;
-
-  // clip divisor of the tensor (phase 4)
-  const float fac = OPT == KAON_OPT_ADAKAON || PNM || MUON ? ws.scal(T)[0] : 1.0f;
-  const double rfac = rcp64(fac);
-  double rden = 1.0;
-  if (PHASE == 6 && CAUT) {
-    const uint32_t cnt = ((const KAON_G uint32_t*)ws.scal(T))[1];
-    rden = rcp64(fmaxf((float)cnt / (float)n, 1e-8f));
-  }
-  uint32_t keep = 0;
-  // Adakaon / Nekaon momentum lerp weight 1 - beta1 (Lion has no lerp, AdaPNM an fma)
-  const bool wlo = fabsf(hp.w1) < 0.5f;
-  // per-row values of the wave's rows, one row per lane
-  const int nrows = (int)(wr.re - wr.rb);
-  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
-  const float mu_l = (FLAGS & FF_GC) && nrows > 0 ? ws.mu(T)[rl] : 0.0f;
-  const float rf_l = (OPT == KAON_OPT_ADAKAON || PNM || MUON) && nrows > 0 ? ws.rf(T)[rl] : 1.0f;
-  const float sc_l = CODEC == KAON_MOM_INT8 && nrows > 0
-                         ? (PHASE == 5 ? *(const KAON_G float*)(X.msc + 4u * (uint32_t)rl) : ws.roldsc(T)[rl])
-                         : 1.0f;
-  const float ng_l = PNM && CODEC == KAON_MOM_INT8 && nrows > 0 ? *(const KAON_G float*)(X.m2sc + 4u * (uint32_t)rl)
-                                                                : 1.0f;
-  const float am_l = CODEC == KAON_MOM_INT8 && PHASE == 6 && nrows > 0 ? __uint_as_float(ws.ramax(T)[rl]) : 0.0f;
-  settle(mu_l);
-  settle(rf_l);
-  settle(sc_l);
-  settle(ng_l);
-  settle(am_l);
-  // Each row is worked on by L = T.fast_lanes consecutive lanes (a power of
-  // two), so a wave covers P = 64 / L rows at a time (a row set); chunk
-  // round k of a row is chunks [L k, L k + L) with lane group member cl
-  // taking chunk cl + L k.  The wave walks (row set, round) positions in
-  // order, issuing the loads of the next position before the arithmetic of
-  // the current one.  Lanes of rows past the slice, and of chunks past the
-  // row end, load a valid chunk of their row again and skip the arithmetic.
-  const int lsh = __builtin_ctz((uint32_t)T.fast_lanes);
-  const uint32_t L = 1u << lsh;
-  const int P = 64 >> lsh;
-  const int rounds = (int)((nfull + L - 1) >> lsh);
-  const int nsets = (nrows + P - 1) / P;
-  const int total = nsets * rounds;
-  const int grp = wr.lane >> lsh;             // the lane's row inside a row set
-  const uint32_t cl = (uint32_t)wr.lane & (L - 1u);
-  FastIn buf0, buf1;
-  if (total > 0) {
-    const uint32_t c = min(cl, nfull - 1u);
-    const uint32_t re = (uint32_t)(wr.rb + min(grp, nrows - 1)) * C;
-    fast_load<OPT, PHASE, CODEC, FLAGS>(buf0, X, re + 8u * c, 8u * c);
-  }
-  int s = 0, k = 0;
-  int rj = 0;        // the lane's row (index into the wave's rows), clamped
-  bool valid = false;
-  uint32_t rowe = 0;
-  float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f, negsc = 1.0f, m128n = 0.0f;
-  double rnew = 1.0;
-  bool dqf = true;
-  // One position: arithmetic on `cur`, loads of the next position into `nxt`.
-  // Called with the two buffers alternating, so no register copies wait on
-  // the loads in flight.
-  auto step = [&](int t, const FastIn& cur, FastIn& nxt) {
-    if (k == 0) {
-      const int ri = s * P + grp;
-      valid = ri < nrows;
-      rj = min(ri, nrows - 1);
-      rowe = (uint32_t)(wr.rb + rj) * C;
-      mu = (FLAGS & FF_GC) ? __shfl(mu_l, rj) : 0.0f;
-      rf = OPT == KAON_OPT_ADAKAON || PNM || MUON ? __shfl(rf_l, rj) : 1.0f;
-      if (CODEC == KAON_MOM_INT8) {
-        oldsc = __shfl(sc_l, rj);
-        if (PNM) negsc = __shfl(ng_l, rj);
-        if (PHASE == 6) {
-          newsc = fmaxf(__shfl(am_l, rj), 1e-12f) / 127.0f;
-          rnew = rcp64(newsc);
-          if (valid && cl == 0) *(KAON_G float*)(X.msc + 4u * (uint32_t)(wr.rb + rj)) = newsc;
-        }
-      }
-      m128 = -128.0f * oldsc;
-      m128n = -128.0f * negsc;
-      // fma(ub, sc, -128 sc) is the exact product q*sc while 128*sc is finite
-      dqf = CODEC != KAON_MOM_INT8 || (fabsf(oldsc) < 0x1p120f && (!PNM || fabsf(negsc) < 0x1p120f));
-      amax = 0.0f;
-    }
-    int sn = s, kn = k + 1;
-    if (kn == rounds) {
-      kn = 0;
-      ++sn;
-    }
-    {
-      const bool last = t + 1 == total;
-      const int rn = last ? rj : min((sn * P) + grp, nrows - 1);
-      const uint32_t cn = min(cl + L * (uint32_t)(last ? k : kn), nfull - 1u);
-      fast_load<OPT, PHASE, CODEC, FLAGS>(nxt, X, (uint32_t)(wr.rb + rn) * C + 8u * cn, 8u * cn);
-    }
-    fast_settle<OPT, PHASE, CODEC, FLAGS>(cur);
-    const uint32_t c = cl + L * (uint32_t)k;
-    const bool full = valid && c < nfull;
-    float camax = 0.0f;
-    if (full) {
-      const uint32_t e0 = rowe + 8u * c;
-      if (wlo) {
-        if (fac == 1.0f && dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-        else if (dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-        else
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-      } else {
-        if (fac == 1.0f && dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-        else if (dqf)
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-        else
-          fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
-      }
-    }
-    if (PHASE == 5 && QUANT && !PNM && !MUON) {
-      if (CODEC == KAON_MOM_INT8) {
-        amax = fmaxf(amax, camax);
-      } else if (X.xrow) {
-        // 4-bit blocks across rows (a block is still whole chunks): one atomic
-        // maximum per chunk into the block's |m| maximum (zeroed by phase 1)
-        if (full) {
-          const uint32_t e0c = rowe + c * 8u;
-          const uint32_t blk4 = (e0c >> X.bsh) * 4u;
-          if (camax > 0.0f) atomicMax((uint32_t*)(X.bamax + blk4), __float_as_uint(camax));
-          if ((e0c & ((1u << X.bsh) - 1u)) == 0u)
-            *(KAON_G float*)(X.boldsc + blk4) = *(const KAON_G float*)(X.msc + blk4);
-        }
-      } else {
-        // 4-bit: a block is GL consecutive chunks, GL | L, so its lanes are
-        // one aligned group of GL lanes
-        float a = camax;
-        for (int o = X.GL / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-        if (full && (wr.lane & (X.GL - 1)) == 0) {
-          const uint32_t blk4 = ((rowe + c * 8u) >> X.bsh) * 4u;
-          *(KAON_G uint32_t*)(X.bamax + blk4) = __float_as_uint(a);
-          *(KAON_G float*)(X.boldsc + blk4) = *(const KAON_G float*)(X.msc + blk4);
-        }
-      }
-    }
-    if (PHASE == 5 && CODEC == KAON_MOM_INT8 && !PNM && !MUON && kn == 0) {
-      // row maxima of the set: reduce over each row's L lanes
-      float a = amax;
-      for (int o = (int)L / 2; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-      if (valid && cl == 0) {
-        ws.ramax(T)[wr.rb + rj] = __float_as_uint(a);
-        ws.roldsc(T)[wr.rb + rj] = oldsc;
-      }
-    }
-    s = sn;
-    k = kn;
-  };
-  for (int t = 0; t < total; t += 2) {
-    step(t, buf0, buf1);
-    if (t + 1 < total) step(t + 1, buf1, buf0);
-  }
-  if (PHASE == 5 && CAUT) {
-    const uint32_t wsum = wave_sum_u32(keep);
-    if (wr.lane == 0) keep_s[wr.w] = wsum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t tot = keep_s[0] + keep_s[1] + keep_s[2] + keep_s[3];
-      if (tot) atomicAdd(ws.keep_ctr(T), tot);
-    }
-  }
-}
-
 // =============================================================== MSAM apply
 template <int PT, int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__ D,
@@ -3300,7 +2600,6 @@ __global__ __launch_bounds__(KAON_WG) void k_copy(const ku4* __restrict__ src_, 
 }
 
 // ------------------------------------------------------------ dispatch tables
-using ElemFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
 
 template <int OPT, int PHASE, int PT, int GT>
 ElemFn elem_by_codec(int codec) {
@@ -3323,68 +2622,6 @@ ElemFn elem_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-// specialized kernels available: (opt, codec, flags) with flags among the
-// defaults of the reference optimizers (GC and cautious on, WD on or off;
-// Nekaon: the climb, plus the removal after the first step, WD on or off;
-// MSAM norm="global": the removal alone)
-template <int OPT, int PHASE, int CODEC>
-ElemFn fast_by_flags(int ff) {
-  if constexpr (OPT == KAON_OPT_ADAMUON) {
-    // int8 / 4-bit momenta (requantized in the apply); GC is off by default
-    if constexpr (CODEC != KAON_MOM_INT8 && CODEC != KAON_MOM_4BIT) return nullptr;
-    switch (ff) {
-      case FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_CAUT>;
-      case FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_CAUT | FF_WD>;
-    }
-  }
-  switch (ff) {
-    case FF_GC | FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT>;
-    case FF_GC | FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD>;
-  }
-  if constexpr (OPT == KAON_OPT_ADAKAON && CODEC != KAON_MOM_NONE) {
-    // phase 5 reads the weights (and so the removal) only under weight decay
-    switch (ff) {
-      case FF_GC | FF_CAUT | FF_WD | FF_NKR:
-        return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKR>;
-    }
-    if constexpr (PHASE == 6) {
-      switch (ff) {
-        case FF_GC | FF_CAUT | FF_NKR: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKR>;
-      }
-      if constexpr (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) {
-        switch (ff) {
-          case FF_GC | FF_CAUT | FF_NKC:
-            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC>;
-          case FF_GC | FF_CAUT | FF_NKC | FF_NKR:
-            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_NKC | FF_NKR>;
-          case FF_GC | FF_CAUT | FF_WD | FF_NKC:
-            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC>;
-          case FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR:
-            return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_NKC | FF_NKR>;
-        }
-      }
-    }
-  }
-  return nullptr;
-}
-
-template <int OPT, int PHASE>
-ElemFn fast_fn(int codec, int ff) {
-  if (PHASE == 5) {
-    // the climb is a phase-6 write; the removal matters to phase 5 only where it reads
-    // the weights (weight decay): drop the flags phase 5 does not look at
-    ff &= ~FF_NKC;
-    if (!(ff & FF_WD)) ff &= ~FF_NKR;
-  }
-  switch (codec) {
-    case KAON_MOM_NONE: return OPT == KAON_OPT_ADAKAON ? fast_by_flags<OPT, PHASE, KAON_MOM_NONE>(ff) : nullptr;
-    case KAON_MOM_BF16: return fast_by_flags<OPT, PHASE, KAON_MOM_BF16>(ff);
-    case KAON_MOM_INT8: return fast_by_flags<OPT, PHASE, KAON_MOM_INT8>(ff);
-    case KAON_MOM_4BIT: return fast_by_flags<OPT, PHASE, KAON_MOM_4BIT>(ff);
-  }
-  return nullptr;
-}
-
 int fast_flags(const KaonHyper& h) {
   int ff = 0;
   if (h.flags & KAON_F_GC) ff |= FF_GC;
@@ -3402,7 +2639,7 @@ int launch_elem(const KaonLaunch& L, Ws ws, const KaonHyper& h, int codec, hipSt
   int32_t n_fast = L.n_fast;
   ElemFn ff = nullptr;
   if (n_fast > 0 && h.bf16_method == KAON_SR && h.p_dtype == KAON_BF16 && h.g_dtype == KAON_BF16)
-    ff = fast_fn<OPT, PHASE>(codec, fast_flags(h));
+    ff = fast_kernel(OPT, PHASE, codec, fast_flags(h));
   if (!ff) n_fast = 0;
   if (n_fast > 0) {
     hipLaunchKernelGGL(ff, dim3(n_fast), dim3(KAON_WG), 0, st, L.descs, L.elem_items, ws, h);
@@ -3742,11 +2979,11 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
     return check_launch(what);
   };
   if ((mask & (1u << 5)) && (h.flags & KAON_F_CAUTIOUS) && L->n_elem_items > 0) {
-    ElemFn ff = fast_cfg ? fast_fn<KAON_OPT_ADAPNM, 5>(h.codec, fast_flags(h)) : nullptr;
+    ElemFn ff = fast_cfg ? fast_kernel(KAON_OPT_ADAPNM, 5, h.codec, fast_flags(h)) : nullptr;
     if ((rc = launch_pnm(ff, f5, "kaon: AdaPNM keep-count launch"))) return rc;
   }
   if ((mask & (1u << 6)) && L->n_elem_items > 0) {
-    ElemFn ff = fast_cfg ? fast_fn<KAON_OPT_ADAPNM, 6>(h.codec, fast_flags(h)) : nullptr;
+    ElemFn ff = fast_cfg ? fast_kernel(KAON_OPT_ADAPNM, 6, h.codec, fast_flags(h)) : nullptr;
     if ((rc = launch_pnm(ff, f6, "kaon: AdaPNM apply launch"))) return rc;
   }
   return 0;

@@ -100,6 +100,46 @@ def test_newton_schulz_matches_oracle(shape):
     assert close.mean() > 0.95, close.mean()
 
 
+def _ns_torch(g: torch.Tensor, steps: int) -> torch.Tensor:
+    """zeropower_via_newtonschulz5 (src/kaon/adamuon.py:97-121) restated with torch bf16
+    matmuls on the GPU: transpose to the smaller inner dimension, divide by the
+    Frobenius norm + 1e-7, then x <- a x + (b A + c A A) x with A = x x^T.  Every
+    right-hand operand is made contiguous first."""
+    a, b, c = 3.4445, -4.7750, 2.0315
+    x = g.bfloat16()
+    tr = x.size(0) > x.size(1)
+    if tr:
+        x = x.t().contiguous()
+    x = x / (x.norm() + 1e-7)
+    for _ in range(steps):
+        aa = torch.matmul(x, x.t().contiguous())
+        bb = b * aa + c * torch.matmul(aa, aa.contiguous())
+        x = a * x + torch.matmul(bb, x.contiguous())
+    if tr:
+        x = x.t().contiguous()
+    return x.float()
+
+
+# BASELINE configs[4]'s own matrices: the 1280-row linears and the conv
+# [1280, 1280, 3, 3] as 1280 x 11520 (the 256-tile GEMM path), [5120, 1280]
+# transposed, and a 640-row conv
+@pytest.mark.parametrize("shape", [(1280, 1280), (1280, 2048), (1280, 5120), (5120, 1280), (1280, 11520),
+                                   (640, 5760)])
+def test_newton_schulz_sdxl_sizes_match_torch(shape):
+    """Newton-Schulz at the SDXL set's sizes (too large for the scalar oracle) against
+    the reference's iteration run with torch's bf16 GEMMs on the same device: within the
+    reference's own tolerance for this iteration (rtol 2e-2, atol 2e-3; its
+    tests/test_adamuon.py:101-118), most elements within one bf16 step."""
+    print(f"[gpu] newton-schulz sdxl {shape}", flush=True)
+    rng = np.random.default_rng(sum(shape) + 1)
+    g = O.bf16_to_f32(O.f32_to_bf16((rng.standard_normal(shape) * 1e-3).astype(np.float32)))
+    got = _ns_on_gpu(g, 2)
+    want = _ns_torch(torch.from_numpy(g).cuda(), 2).cpu().numpy()
+    assert np.allclose(got, want, rtol=2e-2, atol=2e-3), np.abs(got - want).max()
+    close = np.isclose(got, want, rtol=1e-2, atol=1e-4)
+    assert close.mean() > 0.95, close.mean()
+
+
 def test_newton_schulz_orthogonalizes():
     """Five quintic steps leave every singular value in (0.5, 1.3)."""
     rng = np.random.default_rng(7)

@@ -103,6 +103,13 @@ EXTRA = {
     "cfg3_nekaon_4bit_b256": _case("nekaon", _SDXL, dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), weight_decay=0.1,
                                                           momentum_dtype="4bit", momentum_4bit_block=256),
                                    outlier_frac=0.01, eval_train=True),
+    # Nekaon's keep count evaluates the cautious test for both neighbours the removal's
+    # stochastic rounding can pick and draws the noise only where they disagree; a decay
+    # of 50 on weights of 0.02 cancels the update often, so that branch runs too
+    "nekaon_lazy_removal_ambiguous": _case("nekaon", [[320, 1280], [64, 640, 3, 3], [5120, 640]],
+                                           dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), weight_decay=50.0,
+                                                momentum_dtype="4bit", momentum_4bit_block=64),
+                                           steps=4, eval_train=True),
     # Nekaon with a param without a gradient on some steps (its climb is still removed and
     # re-added), all three on step 3
     "nekaon_gradless": _case("nekaon", [[320, 1280], [13, 2880], [640]],

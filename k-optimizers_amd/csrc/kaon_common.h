@@ -126,10 +126,10 @@ __device__ __forceinline__ float lane_val(float v, int j) {
 }
 
 // MSAM perturbation value: clamp(nan_to_num(x, 0, +b, -b), -b, b) (msam.py:222-230).
+// For a bound that is not NaN the clamp already takes +-inf to +-b, so only a
+// NaN x needs a case of its own.
 __device__ __forceinline__ float msam_e(float x, float bound) {
-  if (x != x) return 0.0f;
-  if (isinf(x)) return x > 0.0f ? bound : -bound;
-  return fminf(fmaxf(x, -bound), bound);
+  return x != x ? 0.0f : fminf(fmaxf(x, -bound), bound);
 }
 
 // Flags of the specialized phase-5/6 kernels: bit 0 GC, 1 cautious, 2 weight

@@ -228,11 +228,11 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   }
   // LAZY: the keep count of a step that removes the previous climb and decays
   // the weights (phase 5 with NKR and WD) reads p after the removal's
-  // stochastic rounding, which is one of two bf16 neighbours of p + e (exactly
-  // p + e when its low half is zero).  The cautious test is evaluated for both;
-  // the removal's noise is drawn only for chunks where some element's test
-  // depends on which one it is (or p + e is not finite).  Exact, and rare.
-  constexpr bool LAZY = PHASE == 5 && NKR && NEEDP && !PNM && !MUON;
+  // stochastic rounding, which is one of two bf16 neighbours of p + e.  The
+  // cautious test is evaluated for both; the removal's noise is drawn only for
+  // chunks where some element's keep bit depends on which one it is.  Exact,
+  // and rare.
+  constexpr bool LAZY = PHASE == 5 && CAUT && NKR && NEEDP && !PNM && !MUON;
   uint32_t nz0[8], nz1[8], nz2[8];
   if (NKR && NEEDP && !LAZY) noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
   if (PHASE == 6) noise8_u32(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
@@ -326,37 +326,40 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     if (WD && !PNM && !LAZY) d[i] = __fmaf_rn(hp.wdl, pw, d[i]);
   }
   if (LAZY) {
-    // With lo the truncation of x = p + e, the candidates are lo and lo + one bf16
-    // ulp; for |x| < 2^127 both are finite and at most max(|x| 2^-7, 2^-133) apart,
-    // so the exact decayed values differ by at most |wdl| times that.  Where the
-    // rounded |d_lo| exceeds twice that bound (and 2^-40), |g| >= 2^-100 and d is
-    // not NaN, both candidates give d of one sign, at least 2^-41 in magnitude, and
-    // products d g that do not underflow (fp32 denormals are kept): the same keep
-    // bit.  Anything else is ambiguous.
-    const float wtol = fabsf(hp.wdl) * 0x1p-6f;
-    const float wfloor = fmaxf(0x1p-40f, fabsf(hp.wdl) * 0x1p-132f);
-    bool amb = false;
-    float dl[8];
+    // For finite x = p + e the removal's rounding gives one of two bf16 bit
+    // patterns: lo (x with its low half cleared) or lo + 0x10000 (one bf16 ulp
+    // further from zero, inf past the largest finite value); for x = +-inf it
+    // gives lo, and for NaN a NaN, whose keep bit is 0.  The keep bit d g > 0
+    // is evaluated for both patterns.  Where they agree on every lane the
+    // rounding cannot change it (a NaN x agrees only when both are 0) and lo's
+    // d stands in; otherwise the wave draws the noise and rounds exactly.
+    // The wave's keep bits are counted from the ballots (lane 0 carries them).
+    uint64_t dis = 0;
+    uint32_t cnt = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float dlo = __fmaf_rn(hp.wdl, __uint_as_float(__float_as_uint(xr[i]) & 0xFFFF0000u), d[i]);
-      const float tol = fmaxf(fabsf(xr[i]) * wtol, wfloor);
-      amb = amb || !(fabsf(dlo) > tol) || !(fabsf(g[i]) >= 0x1p-100f) || !(fabsf(xr[i]) < 0x1p127f);
-      dl[i] = dlo;
+      const uint32_t lb = __float_as_uint(xr[i]) & 0xFFFF0000u;
+      const float dlo = __fmaf_rn(hp.wdl, __uint_as_float(lb), d[i]);
+      const float dhi = __fmaf_rn(hp.wdl, __uint_as_float(lb + 0x10000u), d[i]);
+      const uint64_t ml = __builtin_amdgcn_ballot_w64(dlo * g[i] > 0.0f);
+      dis |= ml ^ __builtin_amdgcn_ballot_w64(dhi * g[i] > 0.0f);
+      cnt += (uint32_t)__builtin_popcountll(ml);
     }
-    if (__builtin_amdgcn_ballot_w64(amb) != 0) {
+    if (dis != 0) {
       noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d[i] = __fmaf_rn(hp.wdl, bf2f(sr_bf16(xr[i], nz0[i])), d[i]);
+      for (int i = 0; i < 8; ++i) {
+        const float dx = __fmaf_rn(hp.wdl, bf2f(sr_bf16(xr[i], nz0[i])), d[i]);
+        keep += dx * g[i] > 0.0f ? 1u : 0u;
+      }
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) d[i] = dl[i];
+      keep += lane == 0 ? cnt : 0u;
     }
   }
   if (PHASE == 5) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (CAUT) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
+      if (CAUT && !LAZY) keep += d[i] * g[i] > 0.0f ? 1u : 0u;
       // AdaPNM's absmax of the new positive buffer comes from its clip-sum pass,
       // AdaMuon's from its momentum pass
       if ((CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON) amax = fmaxf(amax, fabsf(mf[i]));

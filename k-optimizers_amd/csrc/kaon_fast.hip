@@ -80,6 +80,58 @@ __device__ __forceinline__ void noise8_u32(uint64_t seed, uint32_t step, uint32_
   }
 }
 
+// noise8_u32 with each 16-bit value in the high half of its word (the random
+// operand of v_cvt_sr_bf16_f32).
+__device__ __forceinline__ void noise8_hi(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream, uint32_t e0,
+                                          const KAON_G uint16_t* inj, uint32_t w[8]) {
+  if (inj) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w[i] = (uint32_t)inj[e0 + i] << 16;
+      settle(w[i]);
+    }
+    return;
+  }
+  uint32_t c[4] = {e0 >> 3, 0u, tid, stream};
+  philox10(c, (uint32_t)seed, step);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[2 * i] = c[i] << 16;
+    w[2 * i + 1] = c[i] & 0xFFFF0000u;
+  }
+}
+
+typedef __bf16 kbf16x2 __attribute__((ext_vector_type(2)));
+
+// The SR bit trick of eight values, as packed bf16 pairs.  v_cvt_sr_bf16_f32
+// adds the high half of its random operand to the fp32 bits and truncates,
+// which is the trick ((bits(x) + noise) with the low half cleared) for every
+// x that is not NaN; it was compared with the trick on the device over every
+// bf16 high half with noise around the carry boundary.  For a NaN the trick
+// gives inf (a NaN whose payload sits in the low half plus a carry-free noise)
+// or 0x7FC0, the instruction some NaN, so a chunk with a NaN anywhere in the
+// wave takes the trick itself.  nzh: noise in the high halves.
+__device__ __forceinline__ ku4 sr_chunk(const float x[8], const uint32_t nzh[8]) {
+  uint64_t nan = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nan |= __builtin_amdgcn_ballot_w64(x[i] != x[i]);
+  uint32_t w[4];
+  if (nan == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kbf16x2 v = {};
+      v = __builtin_amdgcn_cvt_sr_bf16_f32(v, x[2 * i], nzh[2 * i], false);
+      v = __builtin_amdgcn_cvt_sr_bf16_f32(v, x[2 * i + 1], nzh[2 * i + 1], true);
+      w[i] = __builtin_bit_cast(uint32_t, v);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = pack_hi16(sr_word(x[2 * i], nzh[2 * i] >> 16), sr_word(x[2 * i + 1], nzh[2 * i + 1] >> 16));
+  }
+  return ku4{w[0], w[1], w[2], w[3]};
+}
+
 // Global loads of one chunk, issued a chunk ahead of its arithmetic.
 struct FastIn {
   ku4 g, p, m16;
@@ -234,9 +286,16 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   // and rare.
   constexpr bool LAZY = PHASE == 5 && CAUT && NKR && NEEDP && !PNM && !MUON;
   uint32_t nz0[8], nz1[8], nz2[8];
-  if (NKR && NEEDP && !LAZY) noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
-  if (PHASE == 6) noise8_u32(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
-  if (PHASE == 6 && NKC) noise8_u32(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
+  // phase 6 rounds through sr_chunk (noise in the high halves); phase 5 only
+  // uses the removal's noise, through sr_bf16
+  if (NKR && NEEDP && !LAZY) {
+    if (PHASE == 6)
+      noise8_hi(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
+    else
+      noise8_u32(hp.seed, hp.step, X.tid, 0u, e0, X.nz[0], nz0);
+  }
+  if (PHASE == 6) noise8_hi(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
+  if (PHASE == 6 && NKC) noise8_hi(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
 
   float mold[8];
 #pragma unroll
@@ -280,14 +339,19 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   float d[8], mf[8], of[8], xr[8];
   uint32_t mbits[8];
   if (MUON) unpack8(in.o, of);
+  if (NKR && NEEDP) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[i] = p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old);
+    if (PHASE == 6) {
+      unpack8(sr_chunk(xr, nz0), p);
+    } else if (!LAZY) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = bf2f(sr_bf16(xr[i], nz0[i]));
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float pw = p[i];
-    if (NKR && NEEDP) {
-      xr[i] = p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old);
-      if (!LAZY) pw = bf2f(sr_bf16(xr[i], nz0[i]));
-    }
-    p[i] = pw;
+    const float pw = p[i];
     if (MUON) {
       // the update is O's (factored, clipped, lr = 0.2 lr); the momentum of the
       // raw grad is requantized in the apply
@@ -386,7 +450,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
       mdq[i] = 0.0f;
     }
   }
-  uint32_t o[8];
+  float xs[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float dd = d[i];
@@ -394,14 +458,16 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     if (OPT == KAON_OPT_LION) dd = dd * hp.lr;
     // AdaPNM's decoupled decay p * (1 - lr wd), rounded to the param dtype
     const float pd = PNM && WD ? rbf(p[i] * hp.wdl) : p[i];
-    o[i] = sr_word(pd - dd, nz1[i]);
-    if (NKC) o[i] = sr_word(__uint_as_float(o[i]) + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+    xs[i] = pd - dd;
   }
-  ku4 ov;
-  ov.x = pack_hi16(o[0], o[1]);
-  ov.y = pack_hi16(o[2], o[3]);
-  ov.z = pack_hi16(o[4], o[5]);
-  ov.w = pack_hi16(o[6], o[7]);
+  ku4 ov = sr_chunk(xs, nz1);
+  if (NKC) {
+    float y[8];
+    unpack8(ov, y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = y[i] + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new);
+    ov = sr_chunk(y, nz2);
+  }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
   if (CODEC == KAON_MOM_INT8) {
     ku2 mv;

@@ -188,3 +188,65 @@ def test_msam_load_clears_the_climb_and_validates():
         MSAM([p], eps=-1.0)
     with pytest.raises(NotImplementedError):
         MSAM([p], norm="tensor")
+
+
+# ---------------------------------------------------------------- the other direction
+# tests/golden/make_interop.py wrote kaon_amd checkpoints (the state_dict of a
+# kaon_amd optimizer holding the oracle's state after the case's first steps),
+# loaded each into the reference optimizer and let it take the last step.
+INTEROP_BACK = ("ada_int8_sr", "ada_4bit_sr", "ada_bf16_rn", "ada_kahan", "lion_int8_sr", "lion_4bit_rn")
+
+
+def _interop(name):
+    import os
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    return dict(np.load(os.path.join(here, "golden", f"interop_{name}.npz")))
+
+
+@pytest.mark.parametrize("name", INTEROP_BACK)
+def test_reference_resumes_from_a_kaon_amd_checkpoint(name):
+    """The oracle, restarted from the checkpoint the reference loaded, takes the
+    same last step in torch CPU's reduction order: identical weights, codes,
+    scales and fp32 state to what the reference wrote.  For bf16 params the
+    reference's own loader rounds the fp32 state (row, col, v, scales) to bf16
+    on the way in, for its own checkpoints as for these; the restart does the same."""
+    import oracle as O
+    from golden_compare import build_oracle, set_grads
+
+    case = CASES[name]
+    fx = _interop(name)
+    assert int(fx["c_step"]) == case["steps"] - 1
+    oparams, oopt = build_oracle(case)
+    for i, prm in enumerate(oparams):
+        prm.p[...] = fx[f"cp{i}"].reshape(prm.p.shape)
+        for k in list(prm.state):
+            key = f"c{i}_{k}"
+            if k.startswith("_") or key not in fx:
+                continue
+            v = fx[key]
+            if np.ndim(prm.state[k]) == 0 and not isinstance(prm.state[k], np.ndarray):
+                prm.state[k] = type(prm.state[k])(v)
+                continue
+            v = v.reshape(np.shape(prm.state[k])).astype(np.asarray(prm.state[k]).dtype)
+            if case["p_dtype"] == "bf16" and v.dtype == np.float32:
+                # the reference's load: torch's Optimizer.load_state_dict casts floating
+                # state to the param dtype, and load_state_dict_preserving_dtypes
+                # (_momentum_codec.py:417-452) casts the rounded values back to fp32
+                v = O.bf16_to_f32(O.f32_to_bf16(v)).reshape(v.shape)
+            prm.state[k] = v
+    set_grads(case, oparams, case["steps"])
+    oopt.t = case["steps"] - 1  # the SR noise of the last step is keyed on its step number
+    with O.torch_order():
+        oopt.step()
+    for i, prm in enumerate(oparams):
+        assert np.array_equal(prm.p.reshape(-1), fx[f"p{i}"].reshape(-1)), (name, i, "weights")
+        for k, v in prm.state.items():
+            key = f"s{i}_{k}"
+            if k.startswith("_") or key not in fx:
+                continue
+            a = np.asarray(v).reshape(-1)
+            b = fx[key].reshape(-1)
+            if a.dtype != b.dtype and a.itemsize == b.itemsize:
+                b = b.view(a.dtype)
+            assert np.array_equal(a, b.astype(a.dtype)), (name, i, k)

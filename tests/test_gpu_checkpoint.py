@@ -132,3 +132,40 @@ def test_save_load_resume_matches_uninterrupted(name):
                 assert np.array_equal(to_bits(sa[k]).reshape(-1), to_bits(sb[k]).reshape(-1)), (name, i, k)
             else:
                 assert sa[k] == sb[k], (name, i, k)
+
+
+INTEROP_BACK = ("ada_int8_sr", "ada_4bit_sr", "ada_bf16_rn", "ada_kahan", "lion_int8_sr", "lion_4bit_rn")
+
+
+@pytest.mark.parametrize("name", INTEROP_BACK)
+def test_state_dict_is_the_checkpoint_the_reference_resumed_from(name):
+    """tests/golden/make_interop.py loaded a kaon_amd checkpoint into the reference
+    and let it step (tests/test_checkpoint_cpu.py replays that step).  The HIP
+    optimizer's own state_dict after the same first steps is that checkpoint:
+    the same keys, dtypes, shapes and bytes for the weights and every state
+    tensor, and the same step count and SR key."""
+    import os
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    fx = dict(np.load(os.path.join(here, "golden", f"interop_{name}.npz")))
+    case = dict(CASES[name], steps=CASES[name]["steps"] - 1)
+    print(f"[gpu] state_dict vs interop checkpoint {name}", flush=True)
+    params, opt, _ = run_gpu(case)
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    buf.seek(0)
+    sd = torch.load(buf, weights_only=True)
+    assert int(sd["kaon_amd"]["step"]) == int(fx["c_step"])
+    assert int(sd["kaon_amd"]["sr_seed"]) == int(fx["c_sr_seed"])
+    for i, p in enumerate(params):
+        assert np.array_equal(to_bits(p), fx[f"cp{i}"]), (name, i, "weights")
+        want = {k[len(f"c{i}_"):] for k in fx if k.startswith(f"c{i}_")}
+        assert sorted(sd["state"][i]) == sorted(want), (name, i, sorted(sd["state"][i]), sorted(want))
+        for k, v in sd["state"][i].items():
+            ref = fx[f"c{i}_{k}"]
+            if not torch.is_tensor(v):
+                assert int(v) == int(ref), (name, i, k)
+                continue
+            got = to_bits(v)
+            assert got.dtype == ref.dtype and got.shape == ref.shape, (name, i, k, got.dtype, got.shape, ref.shape)
+            assert np.array_equal(got, ref), (name, i, k)

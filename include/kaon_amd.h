@@ -255,8 +255,10 @@ const char* kaon_last_error(void);
  * the generic kernel, and for the specialized kernel slices of 4 * kind rows
  * whose kind (rows per wave) is a multiple of 64 / fast_lanes.
  * Item arrays may be NULL to query sizes; info is
- * always filled.  Returns 0, or non-zero with kaon_last_error() set (e.g. a
- * tensor of 2^31 or more elements, or a momentum codec without its buffer). */
+ * always filled.  Tensors may hold up to 2^32 - 1 elements; from 2^31 on only
+ * 2-D tensors of Adakaon and Lion plans (Nekaon and MSAM plan as Adakaon).
+ * Returns 0, or non-zero with kaon_last_error() set (e.g. a tensor of 2^32 or
+ * more elements, or a momentum codec without its buffer). */
 int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n, KaonItem* row_items,
               KaonItem* elem_items, KaonItem* fin_items, KaonItem* flat_items, KaonItem* ns_sq_items,
               KaonItem* ns_rect_items, KaonPlanInfo* info);

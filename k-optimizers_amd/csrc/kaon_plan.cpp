@@ -140,8 +140,17 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     KaonTensor& t = descs[i];
     if (t.R < 1 || t.C < 0) return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has a bad shape");
     t.n = t.R * t.C;
-    if (t.n >= (int64_t)1 << 31)
-      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has >= 2^31 elements");
+    // Element offsets inside a tensor are 32-bit unsigned in the generic
+    // phase-5/6, MSAM and momentum-norm kernels: up to 2^32 - 1 elements.
+    // From 2^31 on only 2-D tensors of Adakaon / Lion plans (Nekaon and MSAM
+    // step through Adakaon's) are planned; the other optimizers' kernels and
+    // the 1-D row path keep signed 32-bit offsets.
+    if (t.n >= (int64_t)1 << 32)
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) + " has >= 2^32 elements");
+    if (t.n >= (int64_t)1 << 31 && (!t.factored || (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION)))
+      return plan_fail("kaon_plan: tensor " + std::to_string(i) +
+                       " has >= 2^31 elements; tensors that large step only as 2-D params of "
+                       "Adakaon / Lion / Nekaon / MSAM");
     if (!t.factored && t.R != 1) return plan_fail("kaon_plan: a 1-D tensor must have R == 1");
     if (opt == KAON_OPT_ADAMUON && !t.factored)
       return plan_fail("kaon_plan: tensor " + std::to_string(i) +
@@ -255,7 +264,8 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     // the sliced elements (the D statistics)
     const int64_t nflat = opt == KAON_OPT_KPRODIGY ? t.pd_ns : t.n;
     for (int64_t e0 = 0; e0 < nflat; e0 += KAON_FLAT_ITEM)
-      flats.push_back(KaonItem{i, (int32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, nflat - e0), 0});
+      // the element offset as 32 unsigned bits (the kernels read it back as uint32)
+      flats.push_back(KaonItem{i, (int32_t)(uint32_t)e0, (int32_t)std::min<int64_t>(KAON_FLAT_ITEM, nflat - e0), 0});
   }
   // elem order: specialized-kernel slices first, each part largest tensors first
   std::stable_sort(elems.begin(), elems.end(), [](const RowIt& a, const RowIt& b) {

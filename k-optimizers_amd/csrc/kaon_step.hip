@@ -1184,7 +1184,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       float dout[8], mnew[8];
       float chunk_amax = 0.0f;
       // 4-bit blocks that cross chunks or rows: the chunk's first block and offset
-      // (one 32-bit division, n < 2^31), then walked element by element
+      // (one 32-bit division, n < 2^32), then walked element by element
       uint32_t wblk = 0u, woff = 0u;
       if (CODEC == KAON_MOM_4BIT && mom && !blk_fast) {
         wblk = (uint32_t)e0 / (uint32_t)B;
@@ -1828,7 +1828,7 @@ __global__ __launch_bounds__(KAON_WG) void k_msq(const KaonTensor* __restrict__ 
       const int64_t e0 = r * C + c * 8;
       uint32_t mq[8];
       ld_mom_at<CODEC>(T.m, e0, cnt, vec && cnt == 8, mq);
-      // 4-bit: walk the blocks from the chunk's first element (32-bit: n < 2^31)
+      // 4-bit: walk the blocks from the chunk's first element (32-bit: n < 2^32)
       uint32_t blk = 0u, boff = 0u;
       if (CODEC == KAON_MOM_4BIT) {
         blk = (uint32_t)e0 / (uint32_t)T.block4;
@@ -2437,7 +2437,7 @@ __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__
                                                   float factor, float bound, uint32_t sid) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
-  // tensors hold < 2^31 elements: 32-bit element and row arithmetic
+  // tensors hold < 2^32 elements: unsigned 32-bit element and row arithmetic
   const uint32_t e_begin = (uint32_t)it.row0, e_end = (uint32_t)it.row0 + (uint32_t)it.nrows;
   const bool vecT = T.vec_flat != 0;
   // the scale of element e is scale[e / span] (int8: span C per row, or the whole 1-D tensor;

@@ -90,7 +90,7 @@ def _plan(shapes, opt=0, codec=3, block=128, g_dtype=1):
     for k in range(info.n_elem_items):
         it = elems[k]
         d = descs[it.tensor]
-        fast = (g_dtype == 1 and d.factored == 1 and d.vec_rows == 1 and d.C % 8 == 0
+        fast = (g_dtype == 1 and d.factored == 1 and d.vec_rows == 1 and d.C % 8 == 0 and d.R * d.C <= 1 << 31
                 and (codec != 4 or (d.block4 % 8 == 0 and 64 % (d.block4 // 8) == 0)))
         assert (k < info.n_fast) == fast, (k, d.R, d.C)
         covered[it.tensor][it.row0:it.row0 + it.nrows] += 1
@@ -404,3 +404,26 @@ def test_plan_refuses_a_missing_momentum_buffer():
     args = L.KaonPlanArgs(0, 0, 1, 1, 0)
     assert L.lib().kaon_plan(ctypes.byref(args), descs, 1, None, None, None, None, None, None,
                              ctypes.byref(info)) == 0
+
+
+def test_plan_limits_for_tensors_of_2_to_the_31_elements_and_more():
+    """Up to 2^32 - 1 elements: 2-D tensors of Adakaon and Lion plans are planned on
+    the generic phase-5/6 kernel (the specialized one addresses bf16 by 32-bit byte
+    offsets) with flat items whose element offsets pass 2^31; 1-D tensors, other
+    optimizers and 2^32 elements are refused with a message."""
+    L = _lib()
+    big = (131073, 16384)  # 2^31 + 2^14 elements
+    for opt in (0, 1):
+        rc, descs, info, _rows, _fins, flats = _plan([big], opt=opt)
+        assert rc == 0
+        assert info.n_fast == 0
+        offs = sorted((flats[k].row0 & 0xFFFFFFFF) for k in range(info.n_flat_items))
+        assert offs[0] == 0 and offs[-1] == (descs[0].R * descs[0].C - 1) // 16384 * 16384
+        assert all(b - a == 16384 for a, b in zip(offs, offs[1:]))
+    for opt in (2, 3, 4):  # AdaMuon, AdaPNM, KProdigy
+        assert _plan([big], opt=opt)[0] != 0
+        assert b"2^31" in L.lib().kaon_last_error()
+    assert _plan([(1 << 31,)])[0] != 0  # 1-D
+    assert b"2^31" in L.lib().kaon_last_error()
+    assert _plan([(1 << 16, 1 << 16)])[0] != 0  # 2^32
+    assert b"2^32" in L.lib().kaon_last_error()

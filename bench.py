@@ -51,22 +51,28 @@ METRIC = "Gparam/s + % HBM roofline per optimizer step, 2.6B bf16 params, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
-    "adakaon_int8": dict(desc="configs[2]: Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, SR bf16, lr 1e-4",
-                         opt="adakaon", kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8"), bm=1.0),
-    "lion_int8": dict(desc="configs[1]: Lion betas=(0.95,0.98) int8 momentum, cautious, GC, SR bf16, lr 2e-4",
+    "adakaon_int8": dict(desc="configs[2]: Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, SR bf16, lr 1e-4, "
+                              "fused=True",
+                         opt="adakaon", kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8", fused=True),
+                         bm=1.0),
+    "lion_int8": dict(desc="configs[1]: Lion betas=(0.95,0.98) int8 momentum, cautious, GC, SR bf16, lr 2e-4, "
+                           "p.grad left centralized as the reference's Lion leaves it",
                       opt="lion", kw=dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="int8"), bm=1.0),
     "nekaon_4bit": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 128, wd 0.1, cautious, GC, SR bf16, "
-                             "lr 1e-4, 1% Student-t outliers", opt="nekaon",
-                        kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=128),
+                             "lr 1e-4, 1% Student-t outliers, fused=True", opt="nekaon",
+                        kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=128,
+                                fused=True),
                         bm=0.5, outliers=0.01),
     # configs[3] names block sizes 64 and 256 (the default workload above keeps Nekaon's default 128)
     "nekaon_4bit_b64": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 64, wd 0.1, cautious, GC, SR bf16, "
-                                 "lr 1e-4, 1% Student-t outliers", opt="nekaon",
-                            kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=64),
+                                 "lr 1e-4, 1% Student-t outliers, fused=True", opt="nekaon",
+                            kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=64,
+                                    fused=True),
                             bm=0.5, outliers=0.01),
     "nekaon_4bit_b256": dict(desc="configs[3]: Nekaon k=1.5 beta1=0.2 4-bit block 256, wd 0.1, cautious, GC, SR "
-                                  "bf16, lr 1e-4, 1% Student-t outliers", opt="nekaon",
-                             kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=256),
+                                  "bf16, lr 1e-4, 1% Student-t outliers, fused=True", opt="nekaon",
+                             kw=dict(lr=1e-4, betas=(0.2, 0.999), momentum_dtype="4bit", momentum_4bit_block=256,
+                                     fused=True),
                              bm=0.5, outliers=0.01),
     "adamuon_int8": dict(desc="configs[4]: AdaMuon ns_steps=2, betas=(0.95,0.999), int8 momentum, factored 2nd "
                               "moment, cautious, SR bf16, lr 2e-2; Newton-Schulz on every 2-D / conv matrix, 1-D "
@@ -75,11 +81,12 @@ WORKLOADS = {
     # AdaPNM (src/kaon/adapnm.py): two momenta, the positive one read and
     # written, the negative one read (b_neg), on the same SDXL set
     "adapnm_int8": dict(desc="AdaPNM betas=(0.8,0.999) beta0=0.5, two int8 momenta, factored 2nd moment, cautious, "
-                             "GC, SR bf16, lr 1e-4", opt="adapnm",
-                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="int8"), bm=1.0, b_neg=1.0),
+                             "GC, SR bf16, lr 1e-4, fused=True", opt="adapnm",
+                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="int8", fused=True), bm=1.0,
+                        b_neg=1.0),
     "adapnm_bf16": dict(desc="AdaPNM defaults: betas=(0.8,0.999) beta0=0.5, two bf16 momenta, factored 2nd moment, "
-                             "cautious, GC, SR bf16, lr 1e-4", opt="adapnm",
-                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="bfloat16"), bm=2.0,
+                             "cautious, GC, SR bf16, lr 1e-4, fused=True", opt="adapnm",
+                        kw=dict(lr=1e-4, betas=(0.8, 0.999), beta0=0.5, momentum_dtype="bfloat16", fused=True), bm=2.0,
                         b_neg=2.0),
     # KProdigy (src/kaon/kprodigy.py): two passes around a cross-tensor D
     # estimate; b_extra = the fp32 v (read + write) and the sliced s (read + write) and p0 (read)
@@ -95,14 +102,15 @@ WORKLOADS = {
     # MSAM norm="global" over Adakaon (src/kaon/msam.py): the removal rides in
     # Adakaon's apply; b_extra = the norm pass (m read) and the climb pass (m read, p read + write)
     "msam_int8": dict(desc="MSAM rho=0.3 norm='global' over Adakaon betas=(0.9,0.999) int8 momentum, cautious, GC, "
-                           "SR bf16, lr 1e-4", opt="msam",
-                      kw=dict(lr=1e-4, rho=0.3, betas=(0.9, 0.999), momentum_dtype="int8"), bm=1.0,
+                           "SR bf16, lr 1e-4, fused=True", opt="msam",
+                      kw=dict(lr=1e-4, rho=0.3, betas=(0.9, 0.999), momentum_dtype="int8", fused=True), bm=1.0,
                       b_extra=1.0 + 4.0 + 1.0),
     # the launch-bound regime: the reference's LoRA proxy bag (benchmarks/proxy/harness.py:117-127:
     # 512 tensors [8, 16], fp32) stepped by Adakaon with bf16 momentum, the configuration its
     # control ranking lists as "Adakaon-bf16-fused" (benchmarks/control/RANKINGS.md:83)
     "lora_bag": dict(desc="LoRA bag: 512 x [8,16] fp32 params and grads, Adakaon bf16 momentum, cautious, GC, "
-                          "lr 1e-4", opt="adakaon", kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="bfloat16"),
+                          "lr 1e-4, fused=True", opt="adakaon",
+                     kw=dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="bfloat16", fused=True),
                      bm=2.0, shapes=[(8, 16)] * 512, pdtype="f32"),
 }
 LORA_METRIC = "ms per optimizer step, LoRA bag 512 x [8,16] fp32, 1 GPU"

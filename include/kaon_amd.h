@@ -357,6 +357,15 @@ int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, floa
  * an infinite bound. */
 int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
+/* Leaves p.grad centralized, as the reference's native path does
+ * (centralize_grads_, _backend.py:147-177, called at adakaon.py:352-353 and
+ * :399-401): after a step with KAON_F_GC, every 2-D / conv gradient of the plan
+ * is overwritten with round(g - mu) in its dtype, mu the row means the step
+ * used.  The step itself never writes the gradient; callers that mirror the
+ * reference's fused path (which centralizes in-kernel, adakaon.py:387-409) skip
+ * this call. */
+int kaon_gc_writeback(const KaonLaunch* L, const KaonHyper* hp, void* stream);
+
 /* ---------------------------------------------------------- primitives */
 /* _quant_int8 (_momentum_codec.py:72-83): rows x cols fp32 -> int8 codes +
  * per-row scale (rows = 1 for a 1-D tensor). */

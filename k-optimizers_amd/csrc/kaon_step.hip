@@ -2431,6 +2431,44 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
 }
 
 // =============================================================== MSAM apply
+// The centralized gradient written back over p.grad, as the reference's native
+// path leaves it (centralize_grads_, _backend.py:147-177: g -= mean over the
+// fan-in, in the grad dtype, for params of 2 dims or more): g = round(g - mu)
+// with the row means phase 1 stored.  One slice per workgroup, as phase 3.
+template <int GT>
+__global__ __launch_bounds__(KAON_WG) void k_gc_write(const KaonTensor* __restrict__ D,
+                                                      const KaonItem* __restrict__ items, Ws ws) {
+  const KaonItem run = items[blockIdx.x / KAON_RUN];
+  const int sl = (int)(blockIdx.x % KAON_RUN);
+  if (sl >= run_slices(run)) return;
+  const KaonItem it = slice_item(run, sl);
+  const KaonTensor& T = D[it.tensor];
+  if (!T.factored || T.n == 0) return;
+  const int64_t C = T.C, nch = (C + 7) >> 3;
+  const bool vec = T.vec_rows != 0;
+  const WaveRows wr = wave_rows(it);
+  for (int64_t r = wr.rb; r < wr.re; ++r) {
+    const float mu = uniform_f(ws.mu(T)[r]);
+    for (int64_t c = wr.lane; c < nch; c += 64) {
+      const int cnt = chunk_cnt(c, C);
+      const int64_t e0 = r * C + c * 8;
+      const bool vv = vec && cnt == 8;
+      float x[8];
+      ld8<GT>(T.g, e0, cnt, vv, x);
+      if (GT == KAON_BF16) {
+        uint32_t b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b[i] = f2bf(x[i] - mu);
+        st8_bits(const_cast<void*>(T.g), e0, cnt, vv, b);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = x[i] - mu;
+        st8_f32(const_cast<void*>(T.g), e0, cnt, vv, x);
+      }
+    }
+  }
+}
+
 template <int PT, int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, KaonHyper hp,
@@ -3111,6 +3149,17 @@ int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, floa
   hipLaunchKernelGGL(fn, dim3(L->n_flat_items), dim3(KAON_WG), 0, (hipStream_t)stream, L->descs, L->flat_items,
                      *hp, factor, bound, stream_id);
   return check_launch("kaon: msam launch");
+}
+
+int kaon_gc_writeback(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
+  int rc = validate(L, hp, "kaon_gc_writeback: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0 || L->n_row_items <= 0 || !(hp->flags & KAON_F_GC)) return 0;
+  if (hp->flags & KAON_F_SRC_O) return fail("kaon_gc_writeback: the row items read O, not the gradient");
+  auto fn = hp->g_dtype == KAON_BF16 ? k_gc_write<KAON_BF16> : k_gc_write<KAON_F32>;
+  hipLaunchKernelGGL(fn, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, (hipStream_t)stream, L->descs,
+                     L->row_items, Ws{(float*)L->workspace});
+  return check_launch("kaon: gc writeback launch");
 }
 
 // ---------------------------------------------------------------- primitives

@@ -8,6 +8,7 @@ State keys, dtypes and shapes are the reference's (K-Optimizers "kaon"
 """
 from __future__ import annotations
 
+import ctypes
 import operator
 from typing import Any, Iterable
 
@@ -118,8 +119,18 @@ class KaonOptimizer(torch.optim.Optimizer):
         self._launch_cache: dict[int, tuple[tuple, list]] = {}  # param group -> (key, launches)
         self._state_version = 0
         self._inject_noise: dict[torch.Tensor, list] = {}  # tests: param -> [uint16 noise per stream]
+        # After a step with gradient centralization, leave p.grad centralized as the
+        # reference's path does (centralize_grads_, src/kaon/_backend.py:147-177): its
+        # native paths centralize in place, its fused Adakaon / AdaPNM kernels do not.
+        # One extra read and write of the 2-D gradients; set False to skip it.
+        self.centralize_grads_in_place = True
 
     # ------------------------------------------------------------ helpers
+    def _gc_writeback(self, group: dict[str, Any], plan: Any, hp: Any, dev: torch.device) -> None:
+        if self.centralize_grads_in_place and group.get("gradient_centralization"):
+            L.check(L.lib().kaon_gc_writeback(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
+                    "kaon_gc_writeback")
+
     def _tensor_ids(self) -> dict[int, int]:
         return {id(p): i for i, p in enumerate(p for g in self.param_groups for p in g["params"])}
 

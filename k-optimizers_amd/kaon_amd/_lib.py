@@ -111,6 +111,7 @@ SIGNATURES = {
     "kaon_plan": ([ctypes.POINTER(KaonPlanArgs), _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP,
                    ctypes.POINTER(KaonPlanInfo)], ctypes.c_int),
     "kaon_adakaon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
+    "kaon_gc_writeback": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adakaon_step_noalloc": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _I64, _VP],
                                   ctypes.c_int),
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),

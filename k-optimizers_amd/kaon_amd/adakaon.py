@@ -75,6 +75,9 @@ class Adakaon(KaonOptimizer):
         self._foreach_batch_cutoff = foreach_batch_cutoff
         self._foreach_stack_budget = foreach_stack_budget
         self._fused = bool(fused)
+        # the fused path centralizes inside its kernels and leaves p.grad as it was
+        # (adakaon.py:387-409); the native path centralizes p.grad in place
+        self.centralize_grads_in_place = not self._fused
 
     @torch.no_grad()
     def _init_state(self, p: torch.Tensor, state: dict[str, Any], group: dict[str, Any]) -> None:
@@ -149,6 +152,7 @@ class Adakaon(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt, nk, gid)
                 L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_adakaon_step")
+                self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

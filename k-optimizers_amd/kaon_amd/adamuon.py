@@ -144,6 +144,7 @@ class AdaMuon(KaonOptimizer):
             for fn, plan, pdt, gdt, dev in self._launches(gid, group, params):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(getattr(lib, fn)(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)), fn)
+                self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

@@ -103,6 +103,9 @@ class AdaPNM(KaonOptimizer):
         self._foreach_batch_cutoff = foreach_batch_cutoff
         self._foreach_stack_budget = foreach_stack_budget
         self._fused = bool(fused)
+        # as Adakaon: native centralize_grads_ (adapnm.py:614-615); the fused kernels
+        # centralize in-kernel (adapnm.py:660-665 only for the native subset)
+        self.centralize_grads_in_place = not self._fused
 
     @torch.no_grad()
     def _init_state(self, p: torch.Tensor, state: dict[str, Any], group: dict[str, Any]) -> None:
@@ -193,6 +196,7 @@ class AdaPNM(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(lib.kaon_adapnm_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_adapnm_step")
+                self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

@@ -281,4 +281,5 @@ class KProdigy(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt, c)
                 L.check(lib.kaon_kprodigy_pass2(ctypes.byref(plan.launch), ctypes.byref(hp),
                                                 E.stream_handle(dev)), "kaon_kprodigy_pass2")
+                self._gc_writeback(group, plan, hp, dev)
             group["k"] = group["k"] + 1

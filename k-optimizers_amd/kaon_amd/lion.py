@@ -106,6 +106,7 @@ class Lion(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(lib.kaon_lion_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_lion_step")
+                self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

@@ -55,8 +55,9 @@ def test_lion_big_tensor_equals_its_rows_as_two_tensors(momentum_dtype, block, s
     opt_parts._inject_noise[parts[0]] = [None, noise[: split * C], None]
     opt_parts._inject_noise[parts[1]] = [None, noise[split * C:], None]
     for g in grads:
+        # copies: each step leaves its p.grad centralized in place
+        parts[0].grad, parts[1].grad = g[:split].clone(), g[split:].clone()
         big.grad = g
-        parts[0].grad, parts[1].grad = g[:split].contiguous(), g[split:].contiguous()
         opt_big.step()
         opt_parts.step()
     torch.cuda.synchronize()
@@ -85,7 +86,8 @@ def test_adakaon_big_tensor_factored_state():
     g = grads[0]
     del grads
     p = torch.nn.Parameter(p0.clone())
-    opt = Adakaon([p], lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0, momentum_dtype="int8")
+    # fused=True leaves p.grad as given, so the restatement below reads the raw grads
+    opt = Adakaon([p], lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0, momentum_dtype="int8", fused=True)
     p.grad = g
     opt.step()
     torch.cuda.synchronize()

@@ -38,8 +38,9 @@ extern "C" {
 
 #define KAON_ABI_VERSION 7
 
-/* element types of params / grads (p.dtype, p.grad.dtype) */
-enum { KAON_F32 = 0, KAON_BF16 = 1 };
+/* element types of params / grads (p.dtype, p.grad.dtype); fp16 params and
+ * grads (both fp16) step in Adakaon and Lion plans only, written by RN or kahan */
+enum { KAON_F32 = 0, KAON_BF16 = 1, KAON_F16 = 2 };
 
 /* momentum storage ("momentum_dtype"), _momentum_codec.py:253-406 */
 enum { KAON_MOM_NONE = 0, KAON_MOM_F32 = 1, KAON_MOM_BF16 = 2, KAON_MOM_INT8 = 3, KAON_MOM_4BIT = 4 };

@@ -52,7 +52,26 @@ __device__ __forceinline__ void st_stream(KAON_G V* p, V v) {
 
 template <int DT>
 __device__ __forceinline__ float round_to(float x) {
-  return DT == KAON_BF16 ? rbf(x) : x;
+  return DT == KAON_BF16 ? rbf(x) : DT == KAON_F16 ? rhf(x) : x;
+}
+// A 16-bit param / grad of type DT: bits -> fp32, fp32 -> bits (RNE).
+template <int DT>
+__device__ __forceinline__ float lp2f(uint32_t b) {
+  return DT == KAON_F16 ? h2f(b) : bf2f(b);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t f2lp(float f) {
+  return DT == KAON_F16 ? f2h(f) : f2bf(f);
+}
+// Grad-dtype rounding of a GC'd pair (gfx950 conversion for bf16).
+template <int GT>
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  if (GT == KAON_BF16) {
+    rbf2(a, b);
+  } else if (GT == KAON_F16) {
+    a = rhf(a);
+    b = rhf(b);
+  }
 }
 
 __device__ __forceinline__ int64_t nblocks4(const KaonTensor& T) { return (T.n + T.block4 - 1) / T.block4; }

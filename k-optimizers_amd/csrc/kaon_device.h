@@ -43,6 +43,18 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// ------------------------------------------------------------------ fp16
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+// fp32 -> fp16 round-to-nearest-even (v_cvt_f16_f32 in the default rounding
+// mode: overflow to inf, fp16 subnormals kept), NaN -> 0x7E00 with the sign
+// (c10::Half semantics).
+__device__ __forceinline__ uint32_t f2h(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7E00u;
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float rhf(float f) { return h2f(f2h(f)); }
+
 // torch.lerp on CPU: self + w*(end-self) if |w| < 0.5 else end - (end-self)*(1-w),
 // each as one fused multiply-add (ATen/native/Lerp.h:22-35).
 __device__ __forceinline__ float klerp(float a, float b, float w) {
@@ -172,6 +184,20 @@ __device__ __forceinline__ void ld8(const void* base, int64_t off, int cnt, bool
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = i < cnt ? bf2f(b[i]) : 0.0f;
+    }
+  } else if (DT == KAON_F16) {
+    const KAON_G uint16_t* b = G((const uint16_t*)base + off);
+    if (vec) {
+      const ku4 v = *(const KAON_G ku4*)b;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = h2f(w[i] & 0xFFFFu);
+        o[2 * i + 1] = h2f(w[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = i < cnt ? h2f(b[i]) : 0.0f;
     }
   } else {
     const KAON_G float* b = G((const float*)base + off);

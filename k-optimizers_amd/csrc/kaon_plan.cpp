@@ -121,7 +121,17 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       opt != KAON_OPT_KPRODIGY)
     return plan_fail("kaon_plan: unknown optimizer");
   if (codec < KAON_MOM_NONE || codec > KAON_MOM_4BIT) return plan_fail("kaon_plan: unknown codec");
-  if (g_dtype != KAON_F32 && g_dtype != KAON_BF16) return plan_fail("kaon_plan: unknown grad dtype");
+  if (g_dtype != KAON_F32 && g_dtype != KAON_BF16 && g_dtype != KAON_F16)
+    return plan_fail("kaon_plan: unknown grad dtype");
+  if (args->p_dtype != KAON_F32 && args->p_dtype != KAON_BF16 && args->p_dtype != KAON_F16)
+    return plan_fail("kaon_plan: unknown param dtype");
+  if (g_dtype == KAON_F16 || args->p_dtype == KAON_F16) {
+    // fp16 params (RN or kahan writes, _backend.py:82-98) with fp16 grads, on the
+    // generic kernels of Adakaon and Lion
+    if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION)
+      return plan_fail("kaon_plan: fp16 params step in Adakaon and Lion plans only");
+    if (g_dtype != KAON_F16 || args->p_dtype != KAON_F16) return plan_fail("kaon_plan: fp16 params take fp16 grads");
+  }
   std::memset(info, 0, sizeof(*info));
   info->n_tensors = n;
 

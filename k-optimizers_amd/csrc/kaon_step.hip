@@ -170,7 +170,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
             float a0 = xb[k][i] - mu, a1 = xb[k][i + 1] - mu;
-            if (GT == KAON_BF16) rbf2(a0, a1);
+            round_pair<GT>(a0, a1);
             xb[k][i] = a0;
             xb[k][i + 1] = a1;
           }
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           float a0 = x[i] - mu, a1 = x[i + 1] - mu;
-          if (GT == KAON_BF16) rbf2(a0, a1);
+          round_pair<GT>(a0, a1);
           x[i] = a0;
           x[i + 1] = a1;
         }
@@ -1108,10 +1108,10 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       }
       const bool need_p = PHASE == 6 || wd;
       if (need_p && cnt > 0) {
-        if (PT == KAON_BF16) {
+        if (PT != KAON_F32) {
           ld8_bits(T.p, e0, cnt, vec, pb);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+          for (int i = 0; i < 8; ++i) p[i] = lp2f<PT>(pb[i]);
         } else {
           ld8<KAON_F32>(T.p, e0, cnt, vec, p);
         }
@@ -1174,7 +1174,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           float a0 = g[i] - rc.mu, a1 = g[i + 1] - rc.mu;
-          if (GT == KAON_BF16) rbf2(a0, a1);
+          round_pair<GT>(a0, a1);
           g[i] = a0;
           g[i + 1] = a1;
         }
@@ -1340,17 +1340,20 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
           ld8_bits(T.shift, e0, cnt, vec, sh);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            // shift -= bf16(delta); p0 = p; p += shift; shift += p0 - p  (_backend.py:90-94)
-            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            // shift -= lp(delta); p0 = p; p += shift; shift += p0 - p, in the
+            // param dtype (_backend.py:90-94)
+            const float s = round_to<PT>(lp2f<PT>(sh[i]) - round_to<PT>(dout[i]));
             const float p0 = p[i];
-            const float p1 = rbf(p0 + s);
-            o[i] = f2bf(p1);
-            sh[i] = f2bf(s + rbf(p0 - p1));
+            const float p1 = round_to<PT>(p0 + s);
+            o[i] = f2lp<PT>(p1);
+            sh[i] = f2lp<PT>(s + round_to<PT>(p0 - p1));
           }
           st8_bits(T.shift, e0, cnt, vec, sh);
-        } else if (hp.bf16_method == KAON_RN) {
+        } else if (hp.bf16_method == KAON_RN || PT == KAON_F16) {
+          // fp16 params are written by RN under "stochastic_rounding" too: the
+          // reference's SR write is bf16-only (_backend.py:95-98)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+          for (int i = 0; i < 8; ++i) o[i] = f2lp<PT>(p[i] - round_to<PT>(dout[i]));
         } else {
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz1[i]);
@@ -1503,7 +1506,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           float a0 = g[i] - mu, a1 = g[i + 1] - mu;
-          if (GT == KAON_BF16) rbf2(a0, a1);
+          round_pair<GT>(a0, a1);
           g[i] = a0;
           g[i + 1] = a1;
         }
@@ -2016,7 +2019,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           float a0 = g[i] - mu, a1 = g[i + 1] - mu;
-          if (GT == KAON_BF16) rbf2(a0, a1);
+          round_pair<GT>(a0, a1);
           g[i] = a0;
           g[i + 1] = a1;
         }
@@ -2322,7 +2325,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
           float a0 = g[i] - mu, a1 = g[i + 1] - mu;
-          if (GT == KAON_BF16) rbf2(a0, a1);
+          round_pair<GT>(a0, a1);
           g[i] = a0;
           g[i + 1] = a1;
         }
@@ -2455,10 +2458,10 @@ __global__ __launch_bounds__(KAON_WG) void k_gc_write(const KaonTensor* __restri
       const bool vv = vec && cnt == 8;
       float x[8];
       ld8<GT>(T.g, e0, cnt, vv, x);
-      if (GT == KAON_BF16) {
+      if (GT != KAON_F32) {
         uint32_t b[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) b[i] = f2bf(x[i] - mu);
+        for (int i = 0; i < 8; ++i) b[i] = f2lp<GT>(x[i] - mu);
         st8_bits(const_cast<void*>(T.g), e0, cnt, vv, b);
       } else {
 #pragma unroll
@@ -2657,6 +2660,8 @@ ElemFn elem_fn(int pt, int gt, int codec) {
   if (pt == KAON_BF16 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_BF16, KAON_F32>(codec);
   if (pt == KAON_F32 && gt == KAON_BF16) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_BF16>(codec);
   if (pt == KAON_F32 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_F32>(codec);
+  if constexpr (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)
+    if (pt == KAON_F16 && gt == KAON_F16) return elem_by_codec<OPT, PHASE, KAON_F16, KAON_F16>(codec);
   return nullptr;
 }
 
@@ -2710,11 +2715,14 @@ StatsFn stats_fn_gt(int cls, bool eps) {
   return nullptr;
 }
 StatsFn stats_fn(int gt, int cls, bool eps) {
+  if (gt == KAON_F16) return cls >= 3 && cls != 5 ? stats_fn_gt<KAON_F16>(cls, eps) : nullptr;
   return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls, eps) : stats_fn_gt<KAON_F32>(cls, eps);
 }
 
 using SsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
-SsFn ss_fn(int gt) { return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : (SsFn)k_ss<KAON_F32>; }
+SsFn ss_fn(int gt) {
+  return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : gt == KAON_F16 ? (SsFn)k_ss<KAON_F16> : (SsFn)k_ss<KAON_F32>;
+}
 
 using MsamFn = void (*)(const KaonTensor*, const KaonItem*, KaonHyper, float, float, uint32_t);
 MsamFn msam_fn(int pt, int codec) {
@@ -2739,6 +2747,7 @@ int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipS
     if (cnt <= 0) continue;
     if (cls < 3 && hp.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
     StatsFn fn = stats_fn(hp.g_dtype, cls, (hp.flags & KAON_F_EPS) != 0);
+    if (!fn) return fail("kaon: no row-statistics kernel for this grad dtype and row class");
     const size_t lds = (mode == 0 && cls >= 3) ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
     hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);
     off += cnt;
@@ -2844,10 +2853,22 @@ PdFn pd2_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who) {
+// half_ok: the entry point steps fp16 params (Adakaon, Lion and the gradient
+// write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
+// rides along (the reference's add_stochastic_ has no fp16 path,
+// _stochastic_rounding.py:55-68).
+int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool half_ok = false) {
   if (!L || !hp) return fail(who);
-  if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16) return fail("kaon: bad p_dtype");
-  if (hp->g_dtype != KAON_F32 && hp->g_dtype != KAON_BF16) return fail("kaon: bad g_dtype");
+  if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16 && hp->p_dtype != KAON_F16)
+    return fail("kaon: bad p_dtype");
+  if (hp->g_dtype != KAON_F32 && hp->g_dtype != KAON_BF16 && hp->g_dtype != KAON_F16)
+    return fail("kaon: bad g_dtype");
+  if (hp->p_dtype == KAON_F16 || hp->g_dtype == KAON_F16) {
+    if (!half_ok) return fail((std::string(who) + ": fp16 params step in Adakaon and Lion plans only").c_str());
+    if (hp->p_dtype != KAON_F16 || hp->g_dtype != KAON_F16) return fail("kaon: fp16 params take fp16 grads");
+    if (hp->flags & (KAON_F_NK_REMOVE | KAON_F_NK_CLIMB))
+      return fail("kaon: the Nekaon / MSAM perturbation has no fp16 write (add_stochastic_ is bf16 / fp32 only)");
+  }
   if (hp->codec < KAON_MOM_NONE || hp->codec > KAON_MOM_4BIT) return fail("kaon: bad codec");
   if (hp->bf16_method < KAON_SR || hp->bf16_method > KAON_KAHAN) return fail("kaon: bad bf16_method");
   if (L->n_tensors > 0 && (!L->descs || !L->workspace)) return fail("kaon: null descriptor table or workspace");
@@ -2864,7 +2885,7 @@ int kaon_abi_version(void) { return KAON_ABI_VERSION; }
 const char* kaon_last_error(void) { return g_err.c_str(); }
 
 int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
-  int rc = validate(L, hp, "kaon_adakaon_phases: null argument");
+  int rc = validate(L, hp, "kaon_adakaon_phases: null argument", true);
   if (rc) return rc;
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   hipStream_t st = (hipStream_t)stream;
@@ -3112,7 +3133,7 @@ int kaon_kprodigy_pass2(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
 }
 
 int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
-  int rc = validate(L, hp, "kaon_lion_phases: null argument");
+  int rc = validate(L, hp, "kaon_lion_phases: null argument", true);
   if (rc) return rc;
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (hp->codec == KAON_MOM_NONE) return fail("kaon_lion_step: Lion always keeps a momentum buffer");
@@ -3152,11 +3173,12 @@ int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, floa
 }
 
 int kaon_gc_writeback(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
-  int rc = validate(L, hp, "kaon_gc_writeback: null argument");
+  int rc = validate(L, hp, "kaon_gc_writeback: null argument", true);
   if (rc) return rc;
   if (L->n_tensors <= 0 || L->n_row_items <= 0 || !(hp->flags & KAON_F_GC)) return 0;
   if (hp->flags & KAON_F_SRC_O) return fail("kaon_gc_writeback: the row items read O, not the gradient");
-  auto fn = hp->g_dtype == KAON_BF16 ? k_gc_write<KAON_BF16> : k_gc_write<KAON_F32>;
+  auto fn = hp->g_dtype == KAON_BF16 ? k_gc_write<KAON_BF16>
+            : hp->g_dtype == KAON_F16 ? k_gc_write<KAON_F16> : k_gc_write<KAON_F32>;
   hipLaunchKernelGGL(fn, dim3(L->n_row_items * KAON_RUN), dim3(KAON_WG), 0, (hipStream_t)stream, L->descs,
                      L->row_items, Ws{(float*)L->workspace});
   return check_launch("kaon: gc writeback launch");

@@ -110,6 +110,7 @@ class KaonOptimizer(torch.optim.Optimizer):
 
     _OPT = L.OPT_ADAKAON
     _NAME = "kaon"
+    _HALF = False  # float16 params (RN / kahan writes, src/kaon/_backend.py:82-98)
 
     def __init__(self, params: Iterable[Any], defaults: dict[str, Any]) -> None:
         super().__init__(params, defaults)
@@ -185,6 +186,12 @@ class KaonOptimizer(torch.optim.Optimizer):
                 raise RuntimeError(f"kaon_amd: {self._NAME} steps run on a ROCm GPU; got a param on {p.device}")
             if not p.is_contiguous():
                 raise ValueError("kaon_amd: params must be contiguous")
+            if p.dtype == torch.float16 or p.grad.dtype == torch.float16:
+                if not self._HALF:
+                    raise NotImplementedError(
+                        f"kaon_amd: {self._NAME} does not step float16 params in this build (Adakaon and Lion do)")
+                if p.dtype != p.grad.dtype:
+                    raise NotImplementedError("kaon_amd: float16 params take float16 grads")
             if p.grad.dtype != p.dtype and p.grad.dtype not in (torch.float32, torch.bfloat16):
                 raise NotImplementedError(f"kaon_amd: grad dtype {p.grad.dtype} is not supported")
 

@@ -23,8 +23,10 @@ def dtype_code(dt: torch.dtype) -> int:
         return L.BF16
     if dt == torch.float32:
         return L.F32
+    if dt == torch.float16:
+        return L.F16
     raise NotImplementedError(
-        f"kaon_amd: params/grads of dtype {dt} are not supported (bfloat16 and float32 are)")
+        f"kaon_amd: params/grads of dtype {dt} are not supported (bfloat16, float16 and float32 are)")
 
 
 def stream_handle(device: torch.device) -> int:

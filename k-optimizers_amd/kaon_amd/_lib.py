@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
 ABI_VERSION = 7
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
 MOM_CODE = {"none": MOM_NONE, "float32": MOM_F32, "bfloat16": MOM_BF16, "int8": MOM_INT8, "4bit": MOM_4BIT}
 SR, RN, KAHAN = 0, 1, 2

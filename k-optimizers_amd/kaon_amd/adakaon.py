@@ -30,6 +30,7 @@ from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_mom
 class Adakaon(KaonOptimizer):
     _OPT = L.OPT_ADAKAON
     _NAME = "Adakaon"
+    _HALF = True
 
     def __init__(
         self,

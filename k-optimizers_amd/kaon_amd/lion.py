@@ -21,6 +21,7 @@ from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_mom
 class Lion(KaonOptimizer):
     _OPT = L.OPT_LION
     _NAME = "Lion"
+    _HALF = True
 
     def __init__(
         self,

@@ -176,6 +176,12 @@ class MSAM(torch.optim.Optimizer):
             raise RuntimeError(
                 "MSAM.step() called outside train mode. Call optimizer.train() before the "
                 "training step (and optimizer.eval() before sampling / checkpointing).")
+        if self.rho != 0.0 and any(p.dtype == torch.float16 for g in self.param_groups for p in g["params"]):
+            # the perturbation is an add_stochastic_ write, which the reference has for
+            # bf16 and fp32 targets only (_stochastic_rounding.py:55-68)
+            raise NotImplementedError(
+                "add_stochastic_ for target dtype torch.float16 is not implemented; currently only "
+                "torch.bfloat16 and torch.float32 are supported")
         if self._fused:
             # The removal and the climb are folded into the Adakaon apply of the params
             # that step.  A param with a momentum but no gradient this step is not

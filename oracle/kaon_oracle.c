@@ -67,7 +67,7 @@
 #define KAON_RUN 4           /* slices per run (one column partial per run) */
 
 /* dtype codes shared with the HIP library and oracle.py */
-enum { KO_F32 = 0, KO_BF16 = 1 };
+enum { KO_F32 = 0, KO_BF16 = 1, KO_F16 = 2 };
 enum { KO_MOM_NONE = 0, KO_MOM_F32 = 1, KO_MOM_BF16 = 2, KO_MOM_INT8 = 3, KO_MOM_4BIT = 4 };
 enum { KO_SR = 0, KO_RN = 1, KO_KAHAN = 2 };
 
@@ -85,6 +85,43 @@ static inline uint16_t f_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 static inline float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
+
+/* IEEE binary16 from its bits (subnormals included). */
+static inline float f16_to_f(uint16_t h) {
+    const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0) {
+        const float f = (float)m * 0x1p-24f; /* exact: m < 2^10 */
+        return s ? -f : f;
+    }
+    if (e == 31) return u2f(s | 0x7F800000u | (m << 13));
+    return u2f(s | ((e + 112u) << 23) | (m << 13));
+}
+
+/* fp32 -> binary16 round-to-nearest-even: overflow to inf (from 65520 on),
+ * subnormals in units of 2^-24, NaN -> 0x7E00 with the sign (c10::Half's
+ * fp16_ieee_from_fp32_value). */
+static inline uint16_t f_to_f16(float f) {
+    const uint32_t u = f2u(f), s = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(s | 0x7E00u);
+    if (a >= 0x477FF000u) return (uint16_t)(s | 0x7C00u);
+    if (a < 0x38800000u) /* below 2^-14: |f| * 2^24 is exact, rint rounds half to even */
+        return (uint16_t)(s | (uint32_t)rintf(u2f(a) * 0x1p24f));
+    const uint32_t r = a + 0xFFFu + ((a >> 13) & 1u);
+    return (uint16_t)(s | ((r >> 13) - (112u << 10)));
+}
+static inline float round_f16(float f) { return f16_to_f(f_to_f16(f)); }
+
+/* 16-bit element types by code (KO_BF16 / KO_F16). */
+static inline float lp_to_f(int dt, uint16_t h) { return dt == KO_F16 ? f16_to_f(h) : bf16_to_f(h); }
+static inline uint16_t f_to_lp(int dt, float f) { return dt == KO_F16 ? f_to_f16(f) : f_to_bf16(f); }
+static inline float round_lp(int dt, float f) { return dt == KO_F16 ? round_f16(f) : round_bf16(f); }
+
+void ko_f32_to_f16(const float* x, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f_to_f16(x[i]);
+}
+void ko_f16_to_f32(const uint16_t* h, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f(h[i]);
+}
 
 /* torch.lerp on CPU (fused multiply-add form, branch at |w| = 0.5). */
 static inline float ko_lerp(float a, float b, float w) {
@@ -252,13 +289,13 @@ typedef struct {
 } KoHyper;
 
 static inline float load_g(const KoTensor* t, int64_t i) {
-    return t->g_dtype == KO_BF16 ? bf16_to_f(((const uint16_t*)t->g)[i]) : ((const float*)t->g)[i];
+    return t->g_dtype == KO_F32 ? ((const float*)t->g)[i] : lp_to_f(t->g_dtype, ((const uint16_t*)t->g)[i]);
 }
 static inline float load_p(const KoTensor* t, int64_t i) {
-    return t->p_dtype == KO_BF16 ? bf16_to_f(((const uint16_t*)t->p)[i]) : ((const float*)t->p)[i];
+    return t->p_dtype == KO_F32 ? ((const float*)t->p)[i] : lp_to_f(t->p_dtype, ((const uint16_t*)t->p)[i]);
 }
 static inline float round_g(const KoTensor* t, float x) {
-    return t->g_dtype == KO_BF16 ? round_bf16(x) : x;
+    return t->g_dtype == KO_F32 ? x : round_lp(t->g_dtype, x);
 }
 
 /* torch CPU's fp32 sum order (aten/src/ATen/native/cpu/SumKernel.cpp as
@@ -490,22 +527,25 @@ static void write_sub(const KoTensor* t, const float* delta, const KoHyper* h, u
         return;
     }
     uint16_t* p = (uint16_t*)t->p;
-    if (h->bf16_method == KO_SR) {
+    const int dt = t->p_dtype;
+    if (h->bf16_method == KO_SR && dt == KO_BF16) {
         for (int64_t i = 0; i < n; ++i) {
             float x = bf16_to_f(p[i]) - delta[i];
             p[i] = sr_bf16(x, sr_noise(h->seed, h->step, t->tensor_id, stream, i, t->noise[stream]));
         }
-    } else if (h->bf16_method == KO_RN) {
+    } else if (h->bf16_method != KO_KAHAN) {
+        /* RN: p.sub_(delta.to(p.dtype)); fp16 params take it under "stochastic_rounding"
+         * too, the SR write being bf16-only (_backend.py:95-98) */
         for (int64_t i = 0; i < n; ++i)
-            p[i] = f_to_bf16(bf16_to_f(p[i]) - bf16_to_f(f_to_bf16(delta[i])));
-    } else { /* kahan: shift -= bf16(delta); p0 = p; p += shift; shift += p0 - p */
+            p[i] = f_to_lp(dt, lp_to_f(dt, p[i]) - round_lp(dt, delta[i]));
+    } else { /* kahan in the param dtype: shift -= lp(delta); p0 = p; p += shift; shift += p0 - p */
         uint16_t* sh = t->shift;
         for (int64_t i = 0; i < n; ++i) {
-            float s = round_bf16(bf16_to_f(sh[i]) - round_bf16(delta[i]));
-            float p0 = bf16_to_f(p[i]);
-            float p1 = round_bf16(p0 + s);
-            p[i] = f_to_bf16(p1);
-            sh[i] = f_to_bf16(s + round_bf16(p0 - p1));
+            float s = round_lp(dt, lp_to_f(dt, sh[i]) - round_lp(dt, delta[i]));
+            float p0 = lp_to_f(dt, p[i]);
+            float p1 = round_lp(dt, p0 + s);
+            p[i] = f_to_lp(dt, p1);
+            sh[i] = f_to_lp(dt, s + round_lp(dt, p0 - p1));
         }
     }
 }

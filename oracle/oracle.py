@@ -49,7 +49,7 @@ from typing import Any
 
 import numpy as np
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 MOM_CODE = {"none": 0, "float32": 1, "bfloat16": 2, "int8": 3, "4bit": 4}
 BF16_METHOD = {"stochastic_rounding": 0, "none": 1, "kahan": 2}
 
@@ -116,6 +116,9 @@ def lib() -> ctypes.CDLL:
         L.ko_fsum.restype = ctypes.c_float
         L.ko_msam_apply.argtypes = [ctypes.POINTER(KoTensor), ctypes.POINTER(KoHyper),
                                     ctypes.c_double, ctypes.c_double, ctypes.c_uint32]
+        for name in ("ko_f32_to_f16", "ko_f16_to_f32"):
+            getattr(L, name).argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+            getattr(L, name).restype = None
         L.ko_csum.argtypes = [ctypes.c_void_p, ctypes.c_int64]
         L.ko_csum.restype = ctypes.c_float
         for name in ("ko_torch_inner_sum", "ko_torch_sumsq"):
@@ -170,6 +173,22 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> binary16 bits, round to nearest even, overflow to inf, NaN -> 0x7E00
+    with the sign (kaon_oracle.c f_to_f16)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ko_f32_to_f16(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().ko_f16_to_f32(_ptr(h), h.size, _ptr(out))
+    return out
 
 
 # ------------------------------------------------------------------ primitives
@@ -366,7 +385,7 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
             st["col"] = np.zeros(C, dtype=np.float32)
         else:
             st["v"] = np.zeros(prm.shape, dtype=np.float32)
-        if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+        if prm.p_dtype in (BF16, F16) and group.get("bf16_method") == "kahan":
             st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
         return
     if opt == "adapnm":
@@ -379,7 +398,7 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
                 st["max_v"] = np.zeros(n, dtype=np.float32)
         _alloc_momentum(st, "m_pos", prm, group)
         _alloc_momentum(st, "m_neg", prm, group)
-        if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+        if prm.p_dtype in (BF16, F16) and group.get("bf16_method") == "kahan":
             st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
         return
     if opt in ("adakaon", "adamuon"):
@@ -403,7 +422,7 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
             st["m_scale"] = np.ones((n + bs - 1) // bs, dtype=np.float32)
             st["m_numel"] = n
             st["m_block"] = bs
-    if prm.p_dtype == BF16 and group.get("bf16_method") == "kahan":
+    if prm.p_dtype in (BF16, F16) and group.get("bf16_method") == "kahan":
         st["shift"] = np.zeros(prm.shape, dtype=np.uint16)
 
 
@@ -671,7 +690,9 @@ def make_param(shape, p_dtype=BF16, g_dtype=BF16, tensor_id=0, *, p_values=None,
     shape = tuple(int(s) for s in shape)
     def conv(v, dt):
         v = np.ascontiguousarray(v, dtype=np.float32).reshape(shape)
-        return f32_to_bf16(v).reshape(shape) if dt == BF16 else v.copy()
+        if dt == BF16:
+            return f32_to_bf16(v).reshape(shape)
+        return f32_to_f16(v).reshape(shape) if dt == F16 else v.copy()
     prm = OParam(p=conv(p_values, p_dtype), p_dtype=p_dtype, shape=shape, tensor_id=tensor_id,
                  g_dtype=g_dtype)
     if g_values is not None:
@@ -680,12 +701,14 @@ def make_param(shape, p_dtype=BF16, g_dtype=BF16, tensor_id=0, *, p_values=None,
 
 
 def values(a: np.ndarray, dtype: int) -> np.ndarray:
-    return bf16_to_f32(a) if dtype == BF16 else a.astype(np.float32)
+    if dtype == BF16:
+        return bf16_to_f32(a)
+    return f16_to_f32(a) if dtype == F16 else a.astype(np.float32)
 
 
 __all__ = [
-    "BF16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "TORCH_ORDER", "bf16_to_f32", "csum",
-    "dequant", "f32_to_bf16", "fourbit_block_size", "gc_bf16", "init_state", "lerp", "lib", "make_param",
+    "BF16", "F16", "F32", "KoHyper", "KoTensor", "OParam", "OracleOptimizer", "TORCH_ORDER", "bf16_to_f32", "csum",
+    "dequant", "f16_to_f32", "f32_to_bf16", "f32_to_f16", "fourbit_block_size", "gc_bf16", "init_state", "lerp", "lib", "make_param",
     "newton_schulz", "philox4x32_10", "quant_4bit", "quant_int8", "rows_per_wave", "sr_noise", "sr_round",
     "torch_inner_sum", "torch_order", "torch_outer_sum", "torch_sumsq", "values",
 ]

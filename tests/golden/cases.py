@@ -40,6 +40,23 @@ CASES = {
                                                           bf16_method="none", foreach=True)),
     "ada_kahan": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="bfloat16",
                                                bf16_method="kahan", foreach=False)),
+    # fp16 params and grads (the reference's RN / kahan writes, src/kaon/_backend.py:82-98;
+    # "stochastic_rounding" writes fp16 by RN too)
+    "ada_f16_rn": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01,
+                                                momentum_dtype="int8", bf16_method="none", foreach=False),
+                        p_dtype="f16", g_dtype="f16"),
+    "ada_f16_sr": _case("adakaon", _ODD, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="4bit",
+                                              momentum_4bit_block=16, foreach=False),
+                        p_dtype="f16", g_dtype="f16"),
+    "ada_f16_kahan": _case("adakaon", _SMALL, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="bfloat16",
+                                                   bf16_method="kahan", foreach=False),
+                           p_dtype="f16", g_dtype="f16"),
+    "lion_f16_rn": _case("lion", _SMALL, dict(lr=2e-4, betas=(0.95, 0.98), weight_decay=0.1,
+                                              momentum_dtype="int8", bf16_method="none", foreach=False),
+                         p_dtype="f16", g_dtype="f16"),
+    "lion_f16_kahan": _case("lion", _ODD, dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="4bit",
+                                               momentum_4bit_block=16, bf16_method="kahan", foreach=False),
+                            p_dtype="f16", g_dtype="f16"),
     # Lion (src/kaon/lion.py)
     "lion_int8_sr": _case("lion", _SMALL, dict(lr=2e-4, betas=(0.95, 0.98), weight_decay=0.1,
                                                momentum_dtype="int8", foreach=False)),

@@ -91,7 +91,7 @@ def _install_noise_hooks(kaon_mod) -> None:
 
 def _bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().contiguous()
-    if t.dtype == torch.bfloat16:
+    if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16).copy()
     return t.numpy().copy()
 
@@ -100,7 +100,7 @@ def build_params(case):
     params = []
     for i, shape in enumerate(case["shapes"]):
         v = param_values(case, i)
-        dt = torch.bfloat16 if case["p_dtype"] == "bf16" else torch.float32
+        dt = {"bf16": torch.bfloat16, "f16": torch.float16}.get(case["p_dtype"], torch.float32)
         params.append(torch.nn.Parameter(torch.from_numpy(v).to(dt)))
     return params
 
@@ -141,7 +141,7 @@ def run_case(kaon, case):
     for step in range(1, case["steps"] + 1):
         for i, p in enumerate(params):
             g = grad_values(case, i, step)
-            gdt = torch.bfloat16 if case["g_dtype"] == "bf16" else torch.float32
+            gdt = {"bf16": torch.bfloat16, "f16": torch.float16}.get(case["g_dtype"], torch.float32)
             p.grad = torch.from_numpy(g).to(gdt)
         _CTX["step"] = step
         opt.step()

@@ -63,7 +63,7 @@ def group_for(case) -> dict:
 
 
 def dt(name: str) -> int:
-    return O.BF16 if name == "bf16" else O.F32
+    return {"bf16": O.BF16, "f16": O.F16}.get(name, O.F32)
 
 
 def build_oracle(case):
@@ -78,7 +78,12 @@ def build_oracle(case):
 def set_grads(case, params, step):
     for i, prm in enumerate(params):
         g = grad_values(case, i, step)
-        prm.g = O.f32_to_bf16(g).reshape(prm.shape) if prm.g_dtype == O.BF16 else g.copy()
+        if prm.g_dtype == O.BF16:
+            prm.g = O.f32_to_bf16(g).reshape(prm.shape)
+        elif prm.g_dtype == O.F16:
+            prm.g = O.f32_to_f16(g).reshape(prm.shape)
+        else:
+            prm.g = g.copy()
 
 
 def run_oracle(case):

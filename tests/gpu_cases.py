@@ -18,7 +18,7 @@ DEV = torch.device("cuda:0")
 
 
 def tdtype(name: str) -> torch.dtype:
-    return torch.bfloat16 if name == "bf16" else torch.float32
+    return {"bf16": torch.bfloat16, "f16": torch.float16}.get(name, torch.float32)
 
 
 def make_opt(case, params, group=None):
@@ -69,7 +69,7 @@ def make_opt(case, params, group=None):
 
 def to_bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().contiguous().cpu()
-    if t.dtype == torch.bfloat16:
+    if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16).copy()
     return t.numpy().copy()
 
@@ -149,7 +149,12 @@ def oracle_case_run(case, group=None, values=None):
                 prm.g = None
                 continue
             gv = grad_values(case, i, step)
-            prm.g = O.f32_to_bf16(gv).reshape(prm.shape) if prm.g_dtype == O.BF16 else gv.copy()
+            if prm.g_dtype == O.BF16:
+                prm.g = O.f32_to_bf16(gv).reshape(prm.shape)
+            elif prm.g_dtype == O.F16:
+                prm.g = O.f32_to_f16(gv).reshape(prm.shape)
+            else:
+                prm.g = gv.copy()
         opt.step()
     evalp = None
     if case.get("eval_train"):

@@ -30,7 +30,7 @@ INTEROP = [k for k, c in CASES.items() if c["opt"] in ("adakaon", "lion", "adapn
 
 
 def _tdt(name):
-    return torch.bfloat16 if name == "bf16" else torch.float32
+    return {"bf16": torch.bfloat16, "f16": torch.float16}.get(name, torch.float32)
 
 
 def _cpu_opt(case):
@@ -47,7 +47,9 @@ def _cpu_opt(case):
     return opt, params
 
 
-def _golden_state(gold, i):
+def _golden_state(gold, i, p_dtype="bf16"):
+    """The fixture's state of param i as torch tensors; 16-bit arrays are bf16
+    momenta, or the kahan shift in the param dtype."""
     out = {}
     pre = f"s{i}_"
     for k, a in gold.items():
@@ -56,8 +58,9 @@ def _golden_state(gold, i):
         key = k[len(pre):]
         if key.endswith("_numel") or key.endswith("_block") or key == "step":  # ints
             out[key] = int(a)
-        elif a.dtype == np.uint16:  # bf16 bits
-            out[key] = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        elif a.dtype == np.uint16:  # 16-bit float bits
+            dt = _tdt(p_dtype) if key == "shift" else torch.bfloat16
+            out[key] = torch.from_numpy(a.view(np.int16).copy()).view(dt)
         else:
             out[key] = torch.from_numpy(a.copy())
     return out
@@ -70,7 +73,7 @@ def _bytes(t):
 def _reference_sd(name, opt):
     gold = load_golden(name)
     sd = opt.state_dict()
-    sd["state"] = {i: _golden_state(gold, i) for i in range(len(CASES[name]["shapes"]))}
+    sd["state"] = {i: _golden_state(gold, i, CASES[name]["p_dtype"]) for i in range(len(CASES[name]["shapes"]))}
     sd.pop("kaon_amd", None)
     return sd, gold
 
@@ -81,7 +84,7 @@ def test_fresh_state_has_the_reference_layout(name):
     opt, params = _cpu_opt(case)
     gold = load_golden(name)
     for i, p in enumerate(params):
-        ref = _golden_state(gold, i)
+        ref = _golden_state(gold, i, case["p_dtype"])
         st = opt.state[p]
         assert sorted(st) == sorted(ref), (name, i, sorted(st), sorted(ref))
         for k, v in ref.items():
@@ -106,7 +109,7 @@ def test_reference_checkpoint_loads_byte_identical(name):
     sd, gold = _reference_sd(name, opt)
     opt.load_state_dict(sd)
     for i, p in enumerate(params):
-        ref = _golden_state(gold, i)
+        ref = _golden_state(gold, i, case["p_dtype"])
         st = opt.state[p]
         for k, v in ref.items():
             if not torch.is_tensor(v):

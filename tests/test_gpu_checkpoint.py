@@ -42,21 +42,22 @@ def _golden_state(gold, i):
     return out
 
 
-def _torch_state(st):
+def _torch_state(st, pdt=torch.bfloat16):
+    """16-bit arrays are bf16 momenta, or the kahan shift in the param dtype."""
     out = {}
     for k, a in st.items():
         if k in ("m_numel", "m_block"):
             out[k] = int(a)
         elif a.dtype == np.uint16:
-            out[k] = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+            out[k] = torch.from_numpy(a.view(np.int16).copy()).view(pdt if k == "shift" else torch.bfloat16)
         else:
             out[k] = torch.from_numpy(a.copy())
     return out
 
 
 def _param_tensor(a, pdt):
-    if pdt == torch.bfloat16:
-        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    if pdt in (torch.bfloat16, torch.float16):
+        return torch.from_numpy(a.view(np.int16).copy()).view(pdt).to(DEV)
     return torch.from_numpy(a.astype(np.float32)).to(DEV)
 
 
@@ -72,15 +73,15 @@ def test_resume_from_reference_checkpoint(name):
     opt = make_opt(case, params)
     sd = opt.state_dict()
     sd.pop("kaon_amd", None)
-    sd["state"] = {i: _torch_state(_golden_state(gold, i)) for i in range(len(params))}
+    sd["state"] = {i: _torch_state(_golden_state(gold, i), pdt) for i in range(len(params))}
     opt.load_state_dict(sd)
     for i, p in enumerate(params):
         p.grad = torch.from_numpy(grad_values(case, i, nxt)).to(DEV, gdt)
     opt.step()
     torch.cuda.synchronize()
     # oracle from the same params and state
-    dt = O.BF16 if case["p_dtype"] == "bf16" else O.F32
-    gt = O.BF16 if case["g_dtype"] == "bf16" else O.F32
+    dt = {"bf16": O.BF16, "f16": O.F16}.get(case["p_dtype"], O.F32)
+    gt = {"bf16": O.BF16, "f16": O.F16}.get(case["g_dtype"], O.F32)
     oparams = []
     for i, shape in enumerate(case["shapes"]):
         pv = O.values(gold[f"p{i}"], dt)
@@ -93,7 +94,12 @@ def test_resume_from_reference_checkpoint(name):
             else:
                 prm.state[k] = np.ascontiguousarray(a).reshape(np.shape(prm.state[k])).copy()
         g = grad_values(case, i, nxt)
-        prm.g = O.f32_to_bf16(g).reshape(prm.shape) if gt == O.BF16 else g.copy()
+        if gt == O.BF16:
+            prm.g = O.f32_to_bf16(g).reshape(prm.shape)
+        elif gt == O.F16:
+            prm.g = O.f32_to_f16(g).reshape(prm.shape)
+        else:
+            prm.g = g.copy()
     oopt.step()
     assert_same_as_oracle(case, oparams, params, opt, label=f"resume {name}")
     # the loaded 1-D int8 scale keeps the checkpoint's shape through the step

@@ -55,7 +55,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 MSAM_GLOBAL = [k for k, c in CASES.items() if c["opt"] == "msam" and c["kwargs"].get("norm", "global") == "global"]
 BIT_CASES = [k for k, c in CASES.items()
-             if c["g_dtype"] == "bf16" and c["opt"] not in ("adamuon", "kprodigy") and k not in MSAM_GLOBAL]
+             if c["g_dtype"] in ("bf16", "f16") and c["opt"] not in ("adamuon", "kprodigy") and k not in MSAM_GLOBAL]
 F32_CASES = [k for k, c in CASES.items() if c["g_dtype"] == "f32" and c["opt"] != "kprodigy" and k not in MSAM_GLOBAL]
 PD_CASES = [k for k, c in CASES.items() if c["opt"] == "kprodigy"]
 MUON_CASES = [k for k, c in CASES.items() if c["opt"] == "adamuon"]

@@ -349,6 +349,14 @@ int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, 
 int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, float bound,
                     uint32_t stream_id, void* stream);
 
+/* MSAM norm="tensor" perturbation (msam.py:219-222, 231-235): each tensor's
+ * p += m * s with its own s = reciprocal(||m|| + eps) * signed_rho (torch's
+ * python-scalar-over-tensor division), ||m|| the fp32 square root of the sum
+ * kaon_momentum_sumsq stored for the tensor, which must run first on the same
+ * launch.  stream_id as for kaon_msam_apply. */
+int kaon_msam_apply_tensor(const KaonLaunch* L, const KaonHyper* hp, float signed_rho, float eps,
+                           uint32_t stream_id, void* stream);
+
 /* Each tensor's sum of squares of its dequantized momentum into its scalar word
  * 2 of the workspace (rows in the 64-lane order, then the rows in that order),
  * for MSAM norm="global", whose climb is rho * m / (||m|| + eps) with ||m|| over

@@ -2475,9 +2475,18 @@ __global__ __launch_bounds__(KAON_WG) void k_gc_write(const KaonTensor* __restri
 template <int PT, int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, KaonHyper hp,
-                                                  float factor, float bound, uint32_t sid) {
+                                                  float factor, float bound, uint32_t sid, const float* wsb) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
+  if (wsb) {
+    // norm="tensor" (msam.py:219-222): factor is sign * rho and bound is eps;
+    // the tensor's own scale (sign * rho) / (||m|| + eps), evaluated as torch does
+    // a python scalar over a tensor, reciprocal(||m|| + eps) * (sign * rho), with
+    // ||m|| the square root of the sum kaon_momentum_sumsq left in scalar word 2
+    const float nrm = sqrtf(G(wsb + T.ws_scal)[2]);
+    factor = (1.0f / (nrm + bound)) * factor;
+    bound = __builtin_inff();
+  }
   // tensors hold < 2^32 elements: unsigned 32-bit element and row arithmetic
   const uint32_t e_begin = (uint32_t)it.row0, e_end = (uint32_t)it.row0 + (uint32_t)it.nrows;
   const bool vecT = T.vec_flat != 0;
@@ -2724,7 +2733,7 @@ SsFn ss_fn(int gt) {
   return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : gt == KAON_F16 ? (SsFn)k_ss<KAON_F16> : (SsFn)k_ss<KAON_F32>;
 }
 
-using MsamFn = void (*)(const KaonTensor*, const KaonItem*, KaonHyper, float, float, uint32_t);
+using MsamFn = void (*)(const KaonTensor*, const KaonItem*, KaonHyper, float, float, uint32_t, const float*);
 MsamFn msam_fn(int pt, int codec) {
 #define KAON_MSAM_CASE(PTV)                                            \
   switch (codec) {                                                     \
@@ -3168,8 +3177,21 @@ int kaon_msam_apply(const KaonLaunch* L, const KaonHyper* hp, float factor, floa
   MsamFn fn = msam_fn(hp->p_dtype, hp->codec);
   if (!fn) return fail("kaon_msam_apply: needs a momentum codec");
   hipLaunchKernelGGL(fn, dim3(L->n_flat_items), dim3(KAON_WG), 0, (hipStream_t)stream, L->descs, L->flat_items,
-                     *hp, factor, bound, stream_id);
+                     *hp, factor, bound, stream_id, (const float*)nullptr);
   return check_launch("kaon: msam launch");
+}
+
+int kaon_msam_apply_tensor(const KaonLaunch* L, const KaonHyper* hp, float signed_rho, float eps,
+                           uint32_t stream_id, void* stream) {
+  int rc = validate(L, hp, "kaon_msam_apply_tensor: null argument");
+  if (rc) return rc;
+  if (L->n_tensors <= 0) return 0;
+  if (stream_id > 2) return fail("kaon_msam_apply_tensor: stream_id must be 0, 1 or 2");
+  MsamFn fn = msam_fn(hp->p_dtype, hp->codec);
+  if (!fn) return fail("kaon_msam_apply_tensor: needs a momentum codec");
+  hipLaunchKernelGGL(fn, dim3(L->n_flat_items), dim3(KAON_WG), 0, (hipStream_t)stream, L->descs, L->flat_items,
+                     *hp, signed_rho, eps, stream_id, (const float*)L->workspace);
+  return check_launch("kaon: msam tensor-norm launch");
 }
 
 int kaon_gc_writeback(const KaonLaunch* L, const KaonHyper* hp, void* stream) {

@@ -124,6 +124,8 @@ SIGNATURES = {
     "kaon_adamuon_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_adapnm_phases": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _U32, _VP], ctypes.c_int),
     "kaon_msam_apply": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _F, _F, _U32, _VP], ctypes.c_int),
+    "kaon_msam_apply_tensor": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _F, _F, _U32, _VP],
+                               ctypes.c_int),
     "kaon_momentum_sumsq": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_quant_int8": ([_VP, _I64, _I64, _VP, _VP, _VP], ctypes.c_int),
     "kaon_quant_4bit": ([_VP, _I64, _I32, _VP, _VP, _VP], ctypes.c_int),

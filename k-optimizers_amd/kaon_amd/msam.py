@@ -8,6 +8,9 @@ momentum for the next forward/backward:
   over every momentum of the net (``_global_mnorm``, :191-199) -- a
   cross-tensor reduction between the inner step and the climb
   (``kaon_momentum_sumsq``, the tensors added in param order in fp32);
+* ``norm="tensor"``: ``e = rho * m / (||m|| + eps)`` with each tensor's own norm
+  (:219-222), recomputed at every climb and removal (``kaon_momentum_sumsq`` then
+  ``kaon_msam_apply_tensor``, which forms each tensor's scale on the device);
 * ``norm="none"``: ``e = clamp(nan_to_num(rho * m), +-|rho| * clip * lr)`` with the
   bound frozen at climb time (:169-188, Nekaon's form).
 
@@ -15,8 +18,8 @@ Over a plain :class:`Adakaon` the removal (and for ``norm="none"`` the climb)
 is folded into the Adakaon apply pass, as three stochastic roundings of one
 register value (SR noise streams 0, 1, 2); over any other kaon_amd optimizer
 with a momentum buffer they are separate ``kaon_msam_apply`` passes, as in the
-reference.  ``norm="tensor"`` is not part of this build (it raises).  In the
-global norm a NaN momentum coordinate contributes no climb (the reference
+reference; ``norm="tensor"`` always takes those separate passes.  In the global
+and tensor norms a NaN momentum coordinate contributes no climb (the reference
 would carry the NaN into the weights).
 """
 from __future__ import annotations
@@ -52,8 +55,6 @@ class MSAM(torch.optim.Optimizer):
             raise ValueError(f"eps must be >= 0, got {eps}")
         if norm not in ("global", "tensor", "none"):
             raise ValueError(f"norm must be 'global', 'tensor' or 'none', got {norm!r}")
-        if norm == "tensor":
-            raise NotImplementedError("kaon_amd: MSAM norm='tensor' is not part of this build")
         base = Adakaon if base_optimizer is None else base_optimizer
         self._bind(base(params, **kwargs), rho, norm, eps)
 
@@ -159,6 +160,16 @@ class MSAM(torch.optim.Optimizer):
         sid = 0 if sign < 0 else 2
         for gid, pdt, plan, _tids, _idx in (self._momentum_plans() if plans is None else plans):
             group = self.param_groups[gid]
+            if self.norm == "tensor":
+                # each tensor's radius from its current momentum (msam.py:219-222); m is
+                # unchanged between a climb and its removal, so the round trip is exact
+                h = self._hyper(gid, pdt, step)
+                dev = plan.workspace.device
+                L.check(lib.kaon_momentum_sumsq(ctypes.byref(plan.launch), ctypes.byref(h), E.stream_handle(dev)),
+                        "kaon_momentum_sumsq")
+                L.check(lib.kaon_msam_apply_tensor(ctypes.byref(plan.launch), ctypes.byref(h), sign * self.rho,
+                                                   self.eps, sid, E.stream_handle(dev)), "kaon_msam_apply_tensor")
+                continue
             if self.norm == "global":
                 factor, bound = sign * self.rho / (self._mnorm + self.eps), math.inf
             else:
@@ -182,7 +193,7 @@ class MSAM(torch.optim.Optimizer):
             raise NotImplementedError(
                 "add_stochastic_ for target dtype torch.float16 is not implemented; currently only "
                 "torch.bfloat16 and torch.float32 are supported")
-        if self._fused:
+        if self._fused and self.norm != "tensor":
             # The removal and the climb are folded into the Adakaon apply of the params
             # that step.  A param with a momentum but no gradient this step is not
             # stepped; MSAM still removes its climb and climbs again along its
@@ -214,7 +225,7 @@ class MSAM(torch.optim.Optimizer):
                 self._has_e = False
             self._eclamp = {}
             loss = self.inner.step(closure)
-            if self.norm == "none":
+            if self.norm in ("none", "tensor"):
                 if self.rho != 0.0 and self._has_momentum():
                     self._apply(+1.0)
                     self._has_e = True

@@ -592,8 +592,15 @@ float ko_momentum_sumsq(const KoTensor* t) {
     float* rs = (float*)malloc(sizeof(float) * (size_t)R);
     mom_dequant(t, m);
     for (int64_t i = 0; i < n; ++i) m[i] = m[i] * m[i];
-    for (int64_t r = 0; r < R; ++r) rs[r] = ko_csum(m + r * C, C);
-    float s = ko_csum(rs, R);
+    float s;
+    if (t->torch_order) {
+        /* MSAM norm="tensor": (m * m).reshape(n, -1).sum(dim=1), one contiguous row
+         * per tensor (msam.py:219-221) */
+        s = ko_torch_inner_sum(m, n);
+    } else {
+        for (int64_t r = 0; r < R; ++r) rs[r] = ko_csum(m + r * C, C);
+        s = ko_csum(rs, R);
+    }
     free(m); free(rs);
     return s;
 }

@@ -596,6 +596,42 @@ class OracleOptimizer:
             sq = np.float32(sq + np.float32(lib().ko_momentum_sumsq(ctypes.byref(t))))
         return float(np.sqrt(sq, dtype=np.float32))
 
+    def tensor_factor(self, prm: OParam, sign: float) -> float:
+        """MSAM norm="tensor" (msam.py:219-222): scale = (sign * rho) / (||m|| + eps)
+        in fp32 as torch evaluates a python scalar over a tensor, reciprocal(norm + eps)
+        * (sign * rho); ||m|| the fp32 square root of the tensor's sum of squares."""
+        t = _tensor(prm, self.group["momentum_dtype"])
+        s = np.float32(lib().ko_momentum_sumsq(ctypes.byref(t)))
+        nrm = np.sqrt(s, dtype=np.float32)
+        rec = np.float32(1.0) / np.float32(nrm + np.float32(self.meps))
+        return float(np.float32(rec * np.float32(sign * self.rho)))
+
+    def _msam_tensor_apply(self, sign: float, noise: dict[int, list] | None, step: int | None = None) -> None:
+        h = _hyper(self.group, self.seed, self.t if step is None else step)
+        stream = 0 if sign < 0 else 2
+        for prm in self.params:
+            if "m" not in prm.state:
+                continue
+            f = self.tensor_factor(prm, sign)
+            t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
+            lib().ko_msam_apply(ctypes.byref(t), ctypes.byref(h), f, math.inf, stream)
+
+    def _msam_tensor_step(self, noise: dict[int, list] | None) -> None:
+        """MSAM.step with norm="tensor" (msam.py:375-406): remove the previous climb
+        with each tensor's own radius, the inner step, climb along the new momentum."""
+        if self.has_e:
+            self._msam_tensor_apply(-1.0, noise)
+            self.has_e = False
+        h = _hyper(self.group, self.seed, self.t)
+        for prm in self.params:
+            if prm.g is None:
+                continue
+            t = _tensor(prm, self.group["momentum_dtype"], None if noise is None else noise.get(prm.tensor_id))
+            _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
+        if self.rho != 0.0 and any("m" in prm.state for prm in self.params):
+            self._msam_tensor_apply(+1.0, noise)
+            self.has_e = True
+
     def _msam_global_step(self, noise: dict[int, list] | None) -> None:
         """MSAM.step with norm="global" (msam.py:375-406): remove the previous climb
         (folded into the Adakaon step, factor -rho/(||m||+eps) with the cached norm,
@@ -630,6 +666,9 @@ class OracleOptimizer:
             return
         if self.opt == "msam" and self.norm == "global":
             self._msam_global_step(noise)
+            return
+        if self.opt == "msam" and self.norm == "tensor":
+            self._msam_tensor_step(noise)
             return
         h = _hyper(self.group, self.seed, self.t)
         md = self.group["momentum_dtype"]
@@ -675,6 +714,9 @@ class OracleOptimizer:
         ``step`` keys the SR noise (default: the current step count).  A caller
         that drives MSAM over another optimizer by hand sets ``rho``, ``norm``,
         ``meps`` (and ``mnorm`` from :meth:`global_mnorm`) on this object."""
+        if self.norm == "tensor":
+            self._msam_tensor_apply(sign, noise, step)
+            return
         h = _hyper(self.group, self.seed, self.t if step is None else step)
         factor = sign * (-self.k)
         bound = self.bound

@@ -92,6 +92,16 @@ CASES = {
                                   p_dtype="f32", g_dtype="f32", eval_train=True),
     "msam_none_int8": _case("msam", _SMALL, dict(lr=1e-3, rho=0.5, norm="none", betas=(0.5, 0.999),
                                                  momentum_dtype="int8", foreach=False), eval_train=True),
+    # norm="tensor": each tensor's climb on its own momentum norm (msam.py:219-222)
+    "msam_tensor_int8": _case("msam", _SMALL, dict(lr=1e-3, rho=0.3, norm="tensor", betas=(0.9, 0.999),
+                                                   weight_decay=0.01, momentum_dtype="int8", foreach=False),
+                              eval_train=True),
+    "msam_tensor_4bit_rn": _case("msam", _ODD, dict(lr=1e-3, rho=-0.2, norm="tensor", betas=(0.8, 0.999),
+                                                    momentum_dtype="4bit", momentum_4bit_block=16,
+                                                    bf16_method="none", foreach=False), eval_train=True),
+    "msam_tensor_bf16_f32": _case("msam", _SMALL, dict(lr=1e-3, rho=0.05, norm="tensor", momentum_dtype="bfloat16",
+                                                       foreach=False), p_dtype="f32", g_dtype="f32",
+                                  eval_train=True),
     # AdaPNM (src/kaon/adapnm.py) -- two momenta alternating by step parity
     "pnm_bf16_sr": _case("adapnm", _SMALL, dict(lr=1e-3, betas=(0.8, 0.999), beta0=0.5,
                                                 momentum_dtype="bfloat16", foreach=False)),

@@ -175,7 +175,7 @@ def test_nekaon_load_clears_the_climb():
 
 def test_msam_load_clears_the_climb_and_validates():
     """MSAM.load_state_dict (msam.py:409-421) clears the climb and the cached norm;
-    the constructor checks follow msam.py:101-108 (norm="tensor" is not built here)."""
+    the constructor checks follow msam.py:101-108."""
     from kaon_amd import MSAM
 
     p = torch.nn.Parameter(torch.zeros(8, 16, dtype=torch.bfloat16))
@@ -189,8 +189,7 @@ def test_msam_load_clears_the_climb_and_validates():
         MSAM([p], norm="layer")
     with pytest.raises(ValueError):
         MSAM([p], eps=-1.0)
-    with pytest.raises(NotImplementedError):
-        MSAM([p], norm="tensor")
+    assert MSAM([p], norm="tensor").norm == "tensor"
 
 
 # ---------------------------------------------------------------- the other direction

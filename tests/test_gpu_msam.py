@@ -198,8 +198,6 @@ def test_api_errors():
     from kaon_amd import MSAM
 
     p = torch.nn.Parameter(torch.zeros(8, 16, device=DEV, dtype=torch.bfloat16))
-    with pytest.raises(NotImplementedError):
-        MSAM([p], norm="tensor")
     with pytest.raises(ValueError):
         MSAM([p], norm="layer")
     with pytest.raises(ValueError):

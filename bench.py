@@ -515,7 +515,11 @@ def main() -> int:
     gps = nparam / (ms * 1e-3) / 1e9
     bm = w["bm"]
     eb = 4.0 if pdt == torch.float32 else 2.0   # param and grad element bytes
-    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0) + w.get("b_extra", 0.0)
+    # a step that leaves p.grad centralized (Lion; Adakaon / AdaPNM off their fused path)
+    # also writes the gradient once: eb more bytes per param
+    gc_write = bool(getattr(opt, "centralize_grads_in_place", False)) and \
+        w["kw"].get("gradient_centralization", True) and w["opt"] in ("lion", "adakaon")
+    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0) + w.get("b_extra", 0.0) + (eb if gc_write else 0.0)
     step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
     print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
           file=sys.stderr, flush=True)
@@ -562,7 +566,7 @@ def main() -> int:
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
                                "avg_ms": round(br[dom], 4)}
         else:
-            bpp = phase_bytes(dom, bm, wd, w["opt"], w)
+            bpp = phase_bytes(dom, bm, wd, w["opt"], w) + (2.0 if gc_write and dom == 6 else 0.0)
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
             out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),

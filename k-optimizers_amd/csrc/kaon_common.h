@@ -152,8 +152,9 @@ __device__ __forceinline__ float msam_e(float x, float bound) {
 }
 
 // Flags of the specialized phase-5/6 kernels: bit 0 GC, 1 cautious, 2 weight
-// decay, 3 Nekaon removal, 4 Nekaon climb.
-enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16 };
+// decay, 3 Nekaon removal, 4 Nekaon climb, 5 the centralized gradient written
+// back over p.grad by the apply.
+enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16, FF_GCW = 32 };
 
 // A phase-5/6 kernel over work items: (descriptors, items, workspace, hyper-parameters).
 using ElemFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);

@@ -44,6 +44,7 @@ __device__ __forceinline__ uint32_t pack_int8x4(float a, float b, float c, float
 // base plus a 32-bit byte offset, and nothing is reloaded after a store.
 struct FastCtx {
   const KAON_G uint8_t* g;       // bf16 grads
+  KAON_G uint8_t* gw;            // the same, written by the apply under FF_GCW
   KAON_G uint8_t* p;             // bf16 params
   KAON_G uint8_t* m;             // momentum codes or bf16 momentum
   KAON_G uint8_t* msc;           // momentum scales (per row or per block)
@@ -469,6 +470,15 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     ov = sr_chunk(y, nz2);
   }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
+  if (PHASE == 6 && (FLAGS & FF_GCW) && GC) {
+    // the centralized gradient, already rounded to bf16 (its low halves are zero)
+    ku4 gv;
+    gv.x = pack_hi16(__float_as_uint(g[0]), __float_as_uint(g[1]));
+    gv.y = pack_hi16(__float_as_uint(g[2]), __float_as_uint(g[3]));
+    gv.z = pack_hi16(__float_as_uint(g[4]), __float_as_uint(g[5]));
+    gv.w = pack_hi16(__float_as_uint(g[6]), __float_as_uint(g[7]));
+    st_stream((KAON_G ku4*)(X.gw + 2u * e0), gv);
+  }
   if (CODEC == KAON_MOM_INT8) {
     ku2 mv;
     mv.x = pack_int8x4(xq[0], xq[1], xq[2], xq[3]);
@@ -509,6 +519,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   const WaveRows wr = wave_rows(it);
   FastCtx X;
   X.g = (const KAON_G uint8_t*)G(T.g);
+  X.gw = (KAON_G uint8_t*)G(const_cast<void*>(T.g));
   X.p = (KAON_G uint8_t*)G(T.p);
   // AdaPNM: m is this step's positive buffer (m on odd steps, m2 on even ones)
   const bool swap = PNM && (hp.step & 1u) == 0u;
@@ -720,6 +731,14 @@ ElemFn fast_by_flags(int ff) {
     case FF_GC | FF_CAUT: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT>;
     case FF_GC | FF_CAUT | FF_WD: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD>;
   }
+  if constexpr (PHASE == 6 && (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)) {
+    // Lion, and Adakaon off its fused path, leave p.grad centralized (the
+    // reference's native path)
+    switch (ff) {
+      case FF_GC | FF_CAUT | FF_GCW: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_GCW>;
+      case FF_GC | FF_CAUT | FF_WD | FF_GCW: return k_fast<OPT, PHASE, CODEC, FF_GC | FF_CAUT | FF_WD | FF_GCW>;
+    }
+  }
   if constexpr (OPT == KAON_OPT_ADAKAON && CODEC != KAON_MOM_NONE) {
     // phase 5 reads the weights (and so the removal) only under weight decay
     switch (ff) {
@@ -750,9 +769,10 @@ ElemFn fast_by_flags(int ff) {
 template <int OPT, int PHASE>
 ElemFn fast_fn(int codec, int ff) {
   if (PHASE == 5) {
-    // the climb is a phase-6 write; the removal matters to phase 5 only where it reads
-    // the weights (weight decay): drop the flags phase 5 does not look at
-    ff &= ~FF_NKC;
+    // the climb and the gradient write-back are phase-6 writes; the removal matters to
+    // phase 5 only where it reads the weights (weight decay): drop the flags phase 5
+    // does not look at
+    ff &= ~(FF_NKC | FF_GCW);
     if (!(ff & FF_WD)) ff &= ~FF_NKR;
   }
   switch (codec) {

@@ -1322,6 +1322,17 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       }
       if (cnt <= 0) continue;
       // ---------------- phase 6 writes
+      if (gc && (hp.flags & KAON_F_GC_WRITE) && (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)) {
+        // the centralized gradient over p.grad (already rounded to the grad dtype)
+        if (GT == KAON_F32) {
+          st8_f32(const_cast<void*>(T.g), e0, cnt, vec, g);
+        } else {
+          uint32_t gb[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) gb[i] = f2lp<GT>(g[i]);
+          st8_bits(const_cast<void*>(T.g), e0, cnt, vec, gb);
+        }
+      }
       if (CODEC == KAON_MOM_4BIT && mom && blk_fast && (wr.lane % GL) == 0) G(T.m_scale)[blk] = b_new;
       if (mom) st_mom_raw<CODEC>(T, e0, cnt, vec, qout);
       if (PT == KAON_F32) {
@@ -2681,6 +2692,7 @@ int fast_flags(const KaonHyper& h) {
   if (h.flags & KAON_F_WD) ff |= FF_WD;
   if (h.flags & KAON_F_NK_REMOVE) ff |= FF_NKR;
   if (h.flags & KAON_F_NK_CLIMB) ff |= FF_NKC;
+  if ((h.flags & KAON_F_GC_WRITE) && (h.flags & KAON_F_GC)) ff |= FF_GCW;
   return ff;
 }
 

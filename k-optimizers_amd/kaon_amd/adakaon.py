@@ -110,6 +110,8 @@ class Adakaon(KaonOptimizer):
         flags = 0
         if group["gradient_centralization"]:
             flags |= L.F_GC
+            if self.centralize_grads_in_place and nk is None:
+                flags |= L.F_GC_WRITE  # the apply stores the centralized gradient
         if group["cautious"]:
             flags |= L.F_CAUTIOUS
         if wd != 0:
@@ -153,7 +155,8 @@ class Adakaon(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt, nk, gid)
                 L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_adakaon_step")
-                self._gc_writeback(group, plan, hp, dev)
+                if nk is not None:  # under MSAM / Nekaon the apply carries the perturbation instead
+                    self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

@@ -79,6 +79,8 @@ class Lion(KaonOptimizer):
         flags = L.F_MOMENTUM
         if group["gradient_centralization"]:
             flags |= L.F_GC
+            if self.centralize_grads_in_place:
+                flags |= L.F_GC_WRITE  # the apply stores the centralized gradient
         if group["cautious"]:
             flags |= L.F_CAUTIOUS
         if wd != 0:
@@ -107,7 +109,6 @@ class Lion(KaonOptimizer):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(lib.kaon_lion_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_lion_step")
-                self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

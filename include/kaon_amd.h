@@ -133,7 +133,9 @@ typedef struct KaonTensor {
  * kind 1 = row statistics.  Flat items: elements [row0, row0 + nrows).
  * Newton-Schulz tiles: row0 = tile row, nrows = tile column of the padded
  * matrices, kind = 0 for KAON_NS_TILE tiles, 1 for 2 * KAON_NS_TILE tiles (the
- * symmetric products list only row <= column for those). */
+ * symmetric products list only row <= column for those).  The big tiles are
+ * interleaved per XCD (item KAON_NS_XCDS * i + x is XCD x's i-th) and include
+ * idle items, tensor = -1, where one XCD's list is shorter than another's. */
 typedef struct KaonItem {
   int32_t tensor;
   int32_t row0;
@@ -157,6 +159,10 @@ typedef struct KaonItem {
 #define KAON_ROW_CLASSES 7
 /* Tile edge of the Newton-Schulz GEMMs; the iterate is zero-padded to it. */
 #define KAON_NS_TILE 128
+/* XCDs of the target GPU (MI355X: 8 of 32 CUs, each with its own L2): the
+ * big Newton-Schulz tiles are laid out for a launch's workgroup b running on
+ * XCD b % KAON_NS_XCDS. */
+#define KAON_NS_XCDS 8
 
 /*
  * Host-side plan: kaon_plan() fills the workspace offsets of every

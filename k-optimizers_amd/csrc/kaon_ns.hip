@@ -72,8 +72,24 @@ __device__ __forceinline__ uint32_t half_of(const ku4 v, int e) {
   return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
+// 8 bf16 into row r, columns c .. c + 7 of a row-major matrix, the ones inside
+// rows x cols only.  ALN: the row stride is a multiple of 8.
+__device__ __forceinline__ void ns_st8(uint16_t* p, int64_t ld, int r, int c, int rows, int cols, bool aln, ku4 v) {
+  if (r >= rows) return;
+  KAON_G uint16_t* q = G(p) + (int64_t)r * ld + c;
+  if (aln && c + 8 <= cols) {
+    *(KAON_G ku4*)q = v;
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (c + e < cols) q[e] = (uint16_t)half_of(v, e);
+}
+
 // MODE 0: A = x x^T.  MODE 1: B = b*A + c*(A A).  MODE 2: x' = a*x + B x.
-template <int MODE>
+// FIN (MODE 2, the last iteration): x' goes straight to O [R, C] over M,
+// transposed back when R > C, and the padding is dropped.
+template <int MODE, bool FIN = false>
 __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, float* ws, int parity,
                                                  float ca, float cb, float cc) {
@@ -167,34 +183,45 @@ __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ 
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         bfr[j] = *(const bf16x8*)&Bs[(wn * 64 + j * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 8];
+      // the transposed product of each 32 x 32 block (see the epilogue)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     }
   }
 
-  // epilogue: lane l of a 32x32 tile holds column l%32, rows (r/4)*8 + (l/32)*4 + r%4
+  // epilogue: acc[i][j] holds block (i, j) transposed, so lane l has row l % 32
+  // of the block, columns 8 (r / 4) + 4 (l / 32) + r % 4: 8-byte accesses
+  const uint16_t* eop = MODE == 1 ? nb.a : xc;
+  const int lde = MODE == 1 ? mp : kp;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = row0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        const int col = col0 + wn * 64 + j * 32 + (lane & 31);
-        const float v = acc[i][j][r];
-        uint32_t o;
-        if (MODE == 0) {
-          o = f2bf(v);
-        } else if (MODE == 1) {
-          const float e = bf2f(G(nb.a)[(int64_t)row * mp + col]);
-          o = f2bf(rbf(cb * e) + rbf(cc * rbf(v)));
-        } else {
-          const float e = bf2f(G(xc)[(int64_t)row * kp + col]);
-          o = f2bf(rbf(ca * e) + rbf(v));
+      for (int g = 0; g < 4; ++g) {
+        const int row = row0 + wm * 64 + i * 32 + (lane & 31);
+        const int col = col0 + wn * 64 + j * 32 + 8 * g + 4 * (lane >> 5);
+        uint64_t ev = 0;
+        if (MODE != 0) ev = *(const KAON_G uint64_t*)G(eop + (int64_t)row * lde + col);
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = acc[i][j][4 * g + e];
+          const float ef = __uint_as_float((uint32_t)(ev >> (16 * e)) << 16);
+          o[e] = MODE == 0 ? f2bf(v) : MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * rbf(v))) : f2bf(rbf(ca * ef) + rbf(v));
         }
-        G(out)[(int64_t)row * ldc + col] = (uint16_t)o;
+        if (FIN) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int orow = T.ns_tr ? col + e : row, ocol = T.ns_tr ? row : col + e;
+            if (orow < T.R && ocol < T.C) G(nb.mo)[(int64_t)orow * T.C + ocol] = (uint16_t)o[e];
+          }
+        } else {
+          *(KAON_G uint64_t*)G(out + (int64_t)row * ldc + col) =
+              (uint64_t)(o[0] | (o[1] << 16)) | ((uint64_t)(o[2] | (o[3] << 16)) << 32);
+        }
       }
 }
 
@@ -219,13 +246,14 @@ constexpr int XLD = BT + 16;
 static_assert(BK * XLD <= BT * BLD, "the x tile fits the B stage");
 constexpr int NS_LDS = (2 * 2 * BT * BLD > 4 * 128 * WLD) ? 2 * 2 * BT * BLD : 4 * 128 * WLD;
 
-template <int MODE>
+template <int MODE, bool FIN = false>
 __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, float* ws, int parity,
                                                   float ca, float cb, float cc) {
   // K loop: [stage][A, B][BT][BLD]; epilogue: [wave][128][WLD]
   __shared__ __attribute__((aligned(16))) uint16_t lds[NS_LDS];
   const KaonItem it = items[blockIdx.x];
+  if (it.tensor < 0) return;  // an idle item of a shorter XCD list
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
   const int mp = T.m_pad, kp = T.k_pad;
@@ -333,12 +361,14 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       }
     }
   };
+  // the transposed product of each 32 x 32 block, so that a lane ends up with
+  // 4-column runs of one output row (see the epilogue)
   auto mma = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
   };
   constexpr int SG_MFMA = 0x008, SG_VMEM_RD = 0x020, SG_DS_RD = 0x100, SG_DS_WR = 0x200;
   constexpr int NWR = 2 * NS;  // LDS store instructions per step
@@ -412,15 +442,20 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       ev[u] = *(const KAON_G ku4*)(eop + (int64_t)(wr0 + i * 32 + (q >> 2)) * lde + wc0 + j * 32 + (q & 3) * 8);
     }
   }
+  // acc[i][j] holds block (i, j) transposed: lane l has output row l % 32 of
+  // the block, columns 8 (r / 4) + 4 (l / 32) + r % 4 -- one 8-byte LDS write
+  // per 4 registers
   uint16_t* stg = lds + w * (128 * WLD);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        stg[(i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * WLD + j * 32 + (lane & 31)] =
-            (uint16_t)f2bf(acc[i][j][r]);
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t lo = f2bf(acc[i][j][4 * g]) | (f2bf(acc[i][j][4 * g + 1]) << 16);
+        const uint32_t hi = f2bf(acc[i][j][4 * g + 2]) | (f2bf(acc[i][j][4 * g + 3]) << 16);
+        *(uint64_t*)&stg[(i * 32 + (lane & 31)) * WLD + j * 32 + 8 * g + 4 * (lane >> 5)] = (uint64_t)lo | ((uint64_t)hi << 32);
+      }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
   // u = (32 x 32 sub-tile i, j) x half h: rows rr = q / 4, 8 columns from c8
@@ -438,7 +473,26 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       }
       ov = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
     }
-    *(KAON_G ku4*)G(out + (int64_t)(wr0 + i * 32 + rr) * ldc + wc0 + j * 32 + c8) = ov;
+    if (!FIN)
+      *(KAON_G ku4*)G(out + (int64_t)(wr0 + i * 32 + rr) * ldc + wc0 + j * 32 + c8) = ov;
+    else if (!T.ns_tr)
+      ns_st8(nb.mo, T.C, wr0 + i * 32 + rr, wc0 + j * 32 + c8, (int)T.R, (int)T.C, (T.C & 7) == 0, ov);
+    else  // each lane rewrites the chunk it read: no other lane touches it
+      *(ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8] = ov;
+  }
+  if (FIN && T.ns_tr) {
+    // O[c][r] = x'[r][c]: 8-row column chunks of the staged x' tile
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), cr = q >> 2, r8 = (q & 3) * 8;
+      uint32_t xs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[e] = stg[(i * 32 + r8 + e) * WLD + j * 32 + cr];
+      const ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
+      ns_st8(nb.mo, T.C, wc0 + j * 32 + cr, wr0 + i * 32 + r8, (int)T.R, (int)T.C, (T.C & 7) == 0, mv);
+    }
   }
   if (!mirror) return;
   // out[c][r] for this tile's (r, c): 8-row column chunks; for B, the b A term
@@ -483,18 +537,6 @@ __device__ __forceinline__ ku4 ns_ld8(const uint16_t* p, int64_t ld, int r, int 
   return ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
 }
 
-__device__ __forceinline__ void ns_st8(uint16_t* p, int64_t ld, int r, int c, int rows, int cols, bool aln, ku4 v) {
-  if (r >= rows) return;
-  KAON_G uint16_t* q = G(p) + (int64_t)r * ld + c;
-  if (aln && c + 8 <= cols) {
-    *(KAON_G ku4*)q = v;
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (c + e < cols) q[e] = (uint16_t)half_of(v, e);
-}
-
 // x = bf16(v / den) on 8 packed bf16 (torch's bf16 division: fp32 quotient,
 // rounded to bf16), or v itself
 template <bool SCALE>
@@ -506,46 +548,50 @@ __device__ __forceinline__ ku4 ns_map8(ku4 v, double rden) {
   return ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
 }
 
-// One 128 x 128 tile from src to dst, dst(r0 + i, c0 + j) = f(src(r0 + i, c0 + j))
-// or, transposed, f(src(c0 + j, r0 + i)); source elements outside its
-// srows x scols read as 0 (the iterate's zero padding), destination writes stay
-// inside drows x dcols.  16-byte global accesses wherever rows are aligned.
-// The transpose goes through an LDS tile of 256-byte rows whose 16-byte chunks
-// are XOR-swizzled by row / 8: row chunk writes and 8-row column reads both
-// touch 16 distinct chunks per 16 lanes.
-template <bool TR, bool SCALE>
-__device__ __forceinline__ void ns_move_tile(const uint16_t* src, int64_t lds_, int srows, int scols, uint16_t* dst,
-                                             int64_t ldd, int drows, int dcols, int r0, int c0, double rden,
-                                             uint16_t* tile) {
-  const bool sa = (lds_ & 7) == 0, da = (ldd & 7) == 0;
+// One 128 x 128 tile of the iterate, x(r0 + i, c0 + j) = bf16(M(r0 + i, c0 + j) / den)
+// or, transposed, bf16(M(c0 + j, r0 + i) / den); elements outside M's rows x
+// cols read as 0 (the iterate's zero padding).  The iterate's rows are a
+// multiple of 128 long, so its writes are 16-byte and in range.  A thread
+// issues all eight of its 16-byte loads before it uses the first.  The
+// transpose goes through an LDS tile of 256-byte rows whose 16-byte chunks are
+// XOR-swizzled by row / 8: row chunk writes and 8-row column reads both touch
+// 16 distinct chunks per 16 lanes.
+template <bool TR>
+__device__ __forceinline__ void ns_prep_tile(const uint16_t* m, int64_t ldm, int rows, int cols, uint16_t* x,
+                                             int64_t ldx, int r0, int c0, double rden, uint16_t* tile) {
+  const bool ma = (ldm & 7) == 0;
   const int tid = threadIdx.x;
+  constexpr int NQ = TILE * TILE / 8 / 256;  // 16-byte chunks per thread
+  ku4 v[NQ];
+  // TR: source rows c0 .. c0 + 127 (tile rows), columns r0 .. r0 + 127
+#pragma unroll
+  for (int s = 0; s < NQ; ++s) {
+    const int q = tid + 256 * s, tt = q >> 4, ch = q & 15;
+    v[s] = TR ? ns_ld8(m, ldm, c0 + tt, r0 + ch * 8, rows, cols, ma) : ns_ld8(m, ldm, r0 + tt, c0 + ch * 8, rows, cols, ma);
+  }
   if (!TR) {
-#pragma unroll 2
-    for (int q = tid; q < TILE * TILE / 8; q += 256) {
-      const int i = r0 + (q >> 4), j = c0 + (q & 15) * 8;
-      if (i >= drows || j >= dcols) continue;
-      ns_st8(dst, ldd, i, j, drows, dcols, da, ns_map8<SCALE>(ns_ld8(src, lds_, i, j, srows, scols, sa), rden));
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      const int q = tid + 256 * s;
+      *(KAON_G ku4*)G(x + (int64_t)(r0 + (q >> 4)) * ldx + c0 + (q & 15) * 8) = ns_map8<true>(v[s], rden);
     }
     return;
   }
-  // source rows c0 .. c0 + 127 (tile rows tt), columns r0 .. r0 + 127
-#pragma unroll 2
-  for (int q = tid; q < TILE * TILE / 8; q += 256) {
-    const int tt = q >> 4, ch = q & 15;
-    const ku4 v = ns_ld8(src, lds_, c0 + tt, r0 + ch * 8, srows, scols, sa);
-    *(ku4*)&tile[tt * TILE + ((ch ^ ((tt >> 3) & 15)) << 3)] = v;
+#pragma unroll
+  for (int s = 0; s < NQ; ++s) {
+    const int q = tid + 256 * s, tt = q >> 4, ch = q & 15;
+    *(ku4*)&tile[tt * TILE + ((ch ^ ((tt >> 3) & 15)) << 3)] = v[s];
   }
   __syncthreads();
-#pragma unroll 2
-  for (int q = tid; q < TILE * TILE / 8; q += 256) {
-    const int ii = q >> 4, g = q & 15;  // destination row r0 + ii, columns c0 + 8 g ..
-    if (r0 + ii >= drows || c0 + g * 8 >= dcols) continue;
+#pragma unroll
+  for (int s = 0; s < NQ; ++s) {
+    const int q = tid + 256 * s, ii = q >> 4, g = q & 15;  // x row r0 + ii, columns c0 + 8 g ..
     const int off = (((ii >> 3) ^ g) << 3) + (ii & 7);
     uint32_t h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[e] = tile[(g * 8 + e) * TILE + off];
-    const ku4 v = ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    ns_st8(dst, ldd, r0 + ii, c0 + g * 8, drows, dcols, da, ns_map8<SCALE>(v, rden));
+    const ku4 t = ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    *(KAON_G ku4*)G(x + (int64_t)(r0 + ii) * ldx + c0 + g * 8) = ns_map8<true>(t, rden);
   }
 }
 
@@ -556,6 +602,7 @@ __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ 
                                                  const KaonItem* __restrict__ items, float* ws) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[TILE * TILE];
   const KaonItem it = items[blockIdx.x];
+  if (it.tensor < 0) return;  // an idle big-tile item
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
   const double rden = rcp64(G(ws)[T.ws_scal + 2]);
@@ -564,28 +611,9 @@ __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ 
     if (s) __syncthreads();  // the transpose tile is reused
     const int i0 = (it.row0 * sub + s / sub) * TILE, t0 = (it.nrows * sub + s % sub) * TILE;
     if (T.ns_tr)
-      ns_move_tile<true, true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, T.m_pad, T.k_pad, i0, t0, rden, tile);
+      ns_prep_tile<true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, i0, t0, rden, tile);
     else
-      ns_move_tile<false, true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, T.m_pad, T.k_pad, i0, t0, rden, tile);
-  }
-}
-
-// O [R, C] from the final iterate (transposed back when R > C), over M.
-__global__ __launch_bounds__(256) void k_ns_post(const KaonTensor* __restrict__ D,
-                                                 const KaonItem* __restrict__ items, float* ws, int parity) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[TILE * TILE];
-  const KaonItem it = items[blockIdx.x];
-  const KaonTensor& T = D[it.tensor];
-  const NsBufs nb = ns_bufs(ws, T);
-  const uint16_t* x = parity ? nb.x1 : nb.x0;
-  const int sub = it.kind ? 2 : 1;
-  for (int s = 0; s < sub * sub; ++s) {
-    if (s) __syncthreads();
-    const int i0 = (it.row0 * sub + s / sub) * TILE, t0 = (it.nrows * sub + s % sub) * TILE;
-    if (T.ns_tr)  // O(t, i) = x(i, t)
-      ns_move_tile<true, false>(x, T.k_pad, T.m_pad, T.k_pad, nb.mo, T.C, (int)T.R, (int)T.C, t0, i0, 0.0, tile);
-    else
-      ns_move_tile<false, false>(x, T.k_pad, T.m_pad, T.k_pad, nb.mo, T.C, (int)T.R, (int)T.C, i0, t0, 0.0, tile);
+      ns_prep_tile<false>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, i0, t0, rden, tile);
   }
 }
 
@@ -623,12 +651,18 @@ int kaon_ns_run(const KaonLaunch& L, int steps, hipStream_t st) {
     if (nsq_s) hipLaunchKernelGGL(k_ns_gemm<0>, dim3(nsq_s), dim3(256), 0, st, L.descs, sq_s, ws, par, a, b, c);
     if (nsq_b) hipLaunchKernelGGL(k_ns_gemm2<1>, dim3(nsq_b), dim3(256), 0, st, L.descs, L.ns_sq_items, ws, par, a, b, c);
     if (nsq_s) hipLaunchKernelGGL(k_ns_gemm<1>, dim3(nsq_s), dim3(256), 0, st, L.descs, sq_s, ws, par, a, b, c);
-    if (nrect_b)
+    // the last iteration writes O over M
+    const bool fin = s == steps - 1;
+    if (nrect_b && fin)
+      hipLaunchKernelGGL((k_ns_gemm2<2, true>), dim3(nrect_b), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, par,
+                         a, b, c);
+    else if (nrect_b)
       hipLaunchKernelGGL(k_ns_gemm2<2>, dim3(nrect_b), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, par, a, b, c);
-    if (nrect_s) hipLaunchKernelGGL(k_ns_gemm<2>, dim3(nrect_s), dim3(256), 0, st, L.descs, rect_s, ws, par, a, b, c);
+    if (nrect_s && fin)
+      hipLaunchKernelGGL((k_ns_gemm<2, true>), dim3(nrect_s), dim3(256), 0, st, L.descs, rect_s, ws, par, a, b, c);
+    else if (nrect_s)
+      hipLaunchKernelGGL(k_ns_gemm<2>, dim3(nrect_s), dim3(256), 0, st, L.descs, rect_s, ws, par, a, b, c);
     rc = ns_check("kaon: Newton-Schulz GEMM launch");
   }
-  if (rc) return rc;
-  hipLaunchKernelGGL(k_ns_post, dim3(L.n_ns_rect), dim3(256), 0, st, L.descs, L.ns_rect_items, ws, steps & 1);
-  return ns_check("kaon: Newton-Schulz output launch");
+  return rc;
 }

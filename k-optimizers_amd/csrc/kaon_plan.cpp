@@ -101,6 +101,59 @@ bool fast_eligible(const KaonPlanArgs& a, const KaonTensor& t) {
   return true;
 }
 
+// The big Newton-Schulz tiles in the order the GPU runs them.  Workgroup b of a
+// launch runs on XCD b % KAON_NS_XCDS, and each XCD starts its own workgroups in
+// order, so item KAON_NS_XCDS * i + x is XCD x's i-th tile.  A matrix's tiles go
+// to one XCD and share its L2 (a matrix with more than 1/64 of the launch's work
+// is cut into pieces of at most that much).  Pieces are dealt with the longest
+// tiles first, each to the XCD with the least work so far; an XCD's list that
+// comes out shorter than the longest ends in idle items (tensor -1).  A tile
+// costs its K length: k_pad + m_pad for the products (x x^T, then A A), m_pad
+// for the iterate (B x).
+static void ns_xcd_order(std::vector<KaonItem>& v, const KaonTensor* descs, bool sq) {
+  constexpr int X = KAON_NS_XCDS;
+  if (v.empty()) return;
+  auto cost = [&](const KaonItem& it) {
+    const KaonTensor& t = descs[it.tensor];
+    return sq ? (int64_t)t.k_pad + t.m_pad : (int64_t)t.m_pad;
+  };
+  int64_t total = 0;
+  for (const KaonItem& it : v) total += cost(it);
+  const int64_t cap = std::max<int64_t>(1, total / (8 * X));
+  struct Piece {
+    size_t b, e;
+    int64_t c, per;
+  };
+  std::vector<Piece> pieces;
+  for (size_t i = 0; i < v.size();) {
+    const int64_t per = cost(v[i]);
+    size_t j = i;
+    int64_t c = 0;
+    while (j < v.size() && v[j].tensor == v[i].tensor && (j == i || c + per <= cap)) {
+      c += per;
+      ++j;
+    }
+    pieces.push_back(Piece{i, j, c, per});
+    i = j;
+  }
+  std::stable_sort(pieces.begin(), pieces.end(), [](const Piece& a, const Piece& b) {
+    return a.per != b.per ? a.per > b.per : a.c > b.c;
+  });
+  std::vector<std::vector<KaonItem>> lists(X);
+  int64_t load[X] = {};
+  for (const Piece& pc : pieces) {
+    const int x = (int)(std::min_element(load, load + X) - load);
+    load[x] += pc.c;
+    lists[x].insert(lists[x].end(), v.begin() + pc.b, v.begin() + pc.e);
+  }
+  size_t len = 0;
+  for (const auto& l : lists) len = std::max(len, l.size());
+  std::vector<KaonItem> out(len * X, KaonItem{-1, 0, 0, 1});
+  for (int x = 0; x < X; ++x)
+    for (size_t i = 0; i < lists[x].size(); ++i) out[i * X + x] = lists[x][i];
+  v.swap(out);
+}
+
 // Words of AdaMuon's Newton-Schulz block (bf16 buffers, each 16-byte aligned):
 // M / O [R*C], the iterate and its successor [m_pad*k_pad], A and B [m_pad^2].
 int64_t ns_words(const KaonTensor& t) {
@@ -230,8 +283,15 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
         // only, their mirror is written with them
         for (int32_t a = 0; a < tm; ++a)
           for (int32_t b = big ? a : 0; b < tm; ++b) (big ? ns_sq_big : ns_sq).push_back(KaonItem{i, a, b, big});
-        for (int32_t a = 0; a < tm; ++a)
-          for (int32_t b = 0; b < tk; ++b) (big ? ns_rect_big : ns_rect).push_back(KaonItem{i, a, b, big});
+        // big tiles of the iterate column by column: the tiles of one column
+        // read the same columns of x
+        if (big) {
+          for (int32_t b = 0; b < tk; ++b)
+            for (int32_t a = 0; a < tm; ++a) ns_rect_big.push_back(KaonItem{i, a, b, 1});
+        } else {
+          for (int32_t a = 0; a < tm; ++a)
+            for (int32_t b = 0; b < tk; ++b) ns_rect.push_back(KaonItem{i, a, b, 0});
+        }
       }
     }
     if (opt == KAON_OPT_KPRODIGY) {
@@ -303,6 +363,8 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
   if (fin_items && !fins.empty()) std::memcpy(fin_items, fins.data(), fins.size() * sizeof(KaonItem));
   if (flat_items && !flats.empty()) std::memcpy(flat_items, flats.data(), flats.size() * sizeof(KaonItem));
   // Newton-Schulz tiles: the big-tile items first
+  ns_xcd_order(ns_sq_big, descs, true);
+  ns_xcd_order(ns_rect_big, descs, false);
   info->n_ns_sq_big = (int32_t)ns_sq_big.size();
   info->n_ns_rect_big = (int32_t)ns_rect_big.size();
   ns_sq.insert(ns_sq.begin(), ns_sq_big.begin(), ns_sq_big.end());

@@ -30,6 +30,7 @@ ROW_CLASSES = 7
 COLITEM = 2048
 FLAT_ITEM = 16384
 NS_TILE = 128
+NS_XCDS = 8  # KAON_NS_XCDS: big Newton-Schulz tiles are laid out per XCD
 
 
 class KaonTensor(ctypes.Structure):

@@ -317,10 +317,24 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
     assert info.n_fast > 0
     for j in range(info.n_elem_items):
         assert (j < info.n_fast) == (descs[elems[j].tensor].C % 8 == 0), (j, descs[elems[j].tensor].C)
-    # big-tile items lead both lists
-    assert (info.n_ns_sq_big, info.n_ns_rect_big) == (nbig_sq, nbig_rect)
-    assert all(sq[j].kind == (j < nbig_sq) for j in range(info.n_ns_sq))
-    assert all(rect[j].kind == (j < nbig_rect) for j in range(info.n_ns_rect))
+    # big-tile items lead both lists, laid out per XCD: item 8 i + x is XCD x's
+    # i-th tile, and a shorter XCD list ends in idle items (tensor -1)
+    for items, nbig, nreal, sqk in ((sq, info.n_ns_sq_big, nbig_sq, True),
+                                    (rect, info.n_ns_rect_big, nbig_rect, False)):
+        X = L.NS_XCDS
+        assert nbig % X == 0 and nbig >= nreal
+        assert sum(items[j].tensor >= 0 for j in range(nbig)) == nreal
+        assert all(items[j].kind == (j < nbig) for j in range(len(items)))
+        assert all(items[j].tensor >= 0 for j in range(nbig, len(items)))
+        loads = []
+        for x in range(X):
+            lst = [items[j] for j in range(x, nbig, X)]
+            real = [it.tensor >= 0 for it in lst]
+            assert real == sorted(real, reverse=True)  # idle items only at the end
+            loads.append(sum((descs[it.tensor].k_pad + descs[it.tensor].m_pad) if sqk else descs[it.tensor].m_pad
+                             for it in lst if it.tensor >= 0))
+        # pieces are at most 1/64 of the work: no XCD gets much more than its share
+        assert max(loads) <= sum(loads) / X * 1.2 + 1, loads
 
 
 def test_adamuon_plan_rejects_1d():

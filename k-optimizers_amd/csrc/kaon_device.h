@@ -336,5 +336,11 @@ __device__ __forceinline__ void rbf2(float& a, float& b) {
   a = __uint_as_float(w << 16);
   b = __uint_as_float(w & 0xFFFF0000u);
 }
+// The same instruction as a packed pair: f2bf(a) | f2bf(b) << 16 for non-NaN
+// inputs.  For intermediates whose NaN payload is never observed.
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  kaon_f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, kaon_bf16x2));
+}
 
 }  // namespace kaon

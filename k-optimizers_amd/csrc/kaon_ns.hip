@@ -86,6 +86,42 @@ __device__ __forceinline__ void ns_st8(uint16_t* p, int64_t ld, int r, int c, in
     if (c + e < cols) q[e] = (uint16_t)half_of(v, e);
 }
 
+// The epilogue term on a packed pair of bf16-valued products x0, x1 and the
+// packed A / x pair ew, with torch's roundings of each bf16 operation:
+// MODE 1: bf16(bf16(b A) + bf16(c x)), MODE 2: bf16(bf16(a x) + x).
+template <int MODE>
+__device__ __forceinline__ uint32_t ns_comb2(float x0, float x1, uint32_t ew, float ca, float cb, float cc) {
+  float t0 = __uint_as_float(ew << 16), t1 = __uint_as_float(ew & 0xFFFF0000u);
+  if (MODE == 1) {
+    t0 *= cb;
+    t1 *= cb;
+    rbf2(t0, t1);
+    float u0 = cc * x0, u1 = cc * x1;
+    rbf2(u0, u1);
+    return f2bf2(t0 + u0, t1 + u1);
+  }
+  t0 *= ca;
+  t1 *= ca;
+  rbf2(t0, t1);
+  return f2bf2(t0 + x0, t1 + x1);
+}
+
+template <int MODE>
+__device__ __forceinline__ ku4 ns_comb8(ku4 xv, ku4 ev, float ca, float cb, float cc) {
+  auto one = [&](uint32_t xw, uint32_t ew) {
+    return ns_comb2<MODE>(__uint_as_float(xw << 16), __uint_as_float(xw & 0xFFFF0000u), ew, ca, cb, cc);
+  };
+  return ku4{one(xv.x, ev.x), one(xv.y, ev.y), one(xv.z, ev.z), one(xv.w, ev.w)};
+}
+
+// A packed bf16 pair with every NaN made torch's 0x7FC0: the packed conversion
+// leaves NaN payloads unspecified, and O is the factor the step goes on with.
+__device__ __forceinline__ uint32_t ns_canon2(uint32_t w) {
+  const uint32_t lo = (w & 0x7FFFu) > 0x7F80u ? 0x7FC0u : (w & 0xFFFFu);
+  const uint32_t hi = ((w >> 16) & 0x7FFFu) > 0x7F80u ? 0x7FC0u : (w >> 16);
+  return lo | (hi << 16);
+}
+
 // MODE 0: A = x x^T.  MODE 1: B = b*A + c*(A A).  MODE 2: x' = a*x + B x.
 // FIN (MODE 2, the last iteration): x' goes straight to O [R, C] over M,
 // transposed back when R > C, and the padding is dropped.
@@ -205,22 +241,26 @@ __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ 
         const int col = col0 + wn * 64 + j * 32 + 8 * g + 4 * (lane >> 5);
         uint64_t ev = 0;
         if (MODE != 0) ev = *(const KAON_G uint64_t*)G(eop + (int64_t)row * lde + col);
-        uint32_t o[4];
+        uint32_t w[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float v = acc[i][j][4 * g + e];
-          const float ef = __uint_as_float((uint32_t)(ev >> (16 * e)) << 16);
-          o[e] = MODE == 0 ? f2bf(v) : MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * rbf(v))) : f2bf(rbf(ca * ef) + rbf(v));
+        for (int h = 0; h < 2; ++h) {
+          float x0 = acc[i][j][4 * g + 2 * h], x1 = acc[i][j][4 * g + 2 * h + 1];
+          if (MODE == 0) {
+            w[h] = f2bf2(x0, x1);
+          } else {
+            rbf2(x0, x1);
+            w[h] = ns_comb2<MODE>(x0, x1, (uint32_t)(ev >> (32 * h)), ca, cb, cc);
+          }
+          if (FIN) w[h] = ns_canon2(w[h]);
         }
         if (FIN) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int orow = T.ns_tr ? col + e : row, ocol = T.ns_tr ? row : col + e;
-            if (orow < T.R && ocol < T.C) G(nb.mo)[(int64_t)orow * T.C + ocol] = (uint16_t)o[e];
+            if (orow < T.R && ocol < T.C) G(nb.mo)[(int64_t)orow * T.C + ocol] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
           }
         } else {
-          *(KAON_G uint64_t*)G(out + (int64_t)row * ldc + col) =
-              (uint64_t)(o[0] | (o[1] << 16)) | ((uint64_t)(o[2] | (o[3] << 16)) << 32);
+          *(KAON_G uint64_t*)G(out + (int64_t)row * ldc + col) = (uint64_t)w[0] | ((uint64_t)w[1] << 32);
         }
       }
 }
@@ -425,15 +465,19 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   }
 
   // Epilogue.  bf16(v) of the wave's whole 128 x 128 tile goes to its own LDS
-  // region (the stages are free after the last barrier); it is read back as
-  // 16-byte row chunks (normal store) or 8-row column chunks (mirror).  The
-  // a x / b A term of a pass is loaded whole (32 x 16 B per lane) before the
-  // pass starts, the normal pass's before the staging, so each pass waits for
-  // global memory once rather than once per 32 x 32 sub-tile.
+  // region (the stages are free after the last barrier) and is read back as
+  // 16-byte row chunks for the normal store.  The a x / b A term is loaded
+  // whole (32 x 16 B per lane) before the staging, so the wave waits for global
+  // memory once.  The symmetric products' mirror and the transposed O of R > C
+  // write the final values back to the staging tile and read them as 8-row
+  // column chunks with the LDS transpose read.  (The mirror of B = b A + c A A
+  // is the normal tile transposed: A is exactly symmetric, so is A A.)
   const bool mirror = MODE != 2 && it.row0 != it.nrows;
+  const bool trout = FIN && T.ns_tr;
   const KAON_G uint16_t* eop = G((const uint16_t*)(MODE == 1 ? nb.a : xc));
   const int lde = MODE == 1 ? mp : kp;
   const int wr0 = row0 + wm * 128, wc0 = col0 + wn * 128;
+  const bool oaln = (T.C & 7) == 0;
   ku4 ev[32];
   if (MODE != 0) {
 #pragma unroll
@@ -452,8 +496,8 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const uint32_t lo = f2bf(acc[i][j][4 * g]) | (f2bf(acc[i][j][4 * g + 1]) << 16);
-        const uint32_t hi = f2bf(acc[i][j][4 * g + 2]) | (f2bf(acc[i][j][4 * g + 3]) << 16);
+        const uint32_t lo = f2bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+        const uint32_t hi = f2bf2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
         *(uint64_t*)&stg[(i * 32 + (lane & 31)) * WLD + j * 32 + 8 * g + 4 * (lane >> 5)] = (uint64_t)lo | ((uint64_t)hi << 32);
       }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
@@ -463,64 +507,36 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   for (int u = 0; u < 32; ++u) {
     const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), rr = q >> 2, c8 = (q & 3) * 8;
     const ku4 xv = *(const ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8];
-    ku4 ov = xv;
-    if (MODE != 0) {
-      uint32_t o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = __uint_as_float(half_of(xv, e) << 16), ef = __uint_as_float(half_of(ev[u], e) << 16);
-        o[e] = MODE == 1 ? f2bf(rbf(cb * ef) + rbf(cc * x)) : f2bf(rbf(ca * ef) + x);
-      }
-      ov = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
-    }
+    ku4 ov = MODE == 0 ? xv : ns_comb8<MODE>(xv, ev[u], ca, cb, cc);
+    if (FIN) ov = ku4{ns_canon2(ov.x), ns_canon2(ov.y), ns_canon2(ov.z), ns_canon2(ov.w)};
     if (!FIN)
       *(KAON_G ku4*)G(out + (int64_t)(wr0 + i * 32 + rr) * ldc + wc0 + j * 32 + c8) = ov;
-    else if (!T.ns_tr)
-      ns_st8(nb.mo, T.C, wr0 + i * 32 + rr, wc0 + j * 32 + c8, (int)T.R, (int)T.C, (T.C & 7) == 0, ov);
-    else  // each lane rewrites the chunk it read: no other lane touches it
-      *(ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8] = ov;
+    else if (!trout)
+      ns_st8(nb.mo, T.C, wr0 + i * 32 + rr, wc0 + j * 32 + c8, (int)T.R, (int)T.C, oaln, ov);
+    // each lane rewrites the chunk it read: no other lane touches it
+    if (MODE != 0 && (mirror || trout)) *(ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8] = ov;
   }
-  if (FIN && T.ns_tr) {
-    // O[c][r] = x'[r][c]: 8-row column chunks of the staged x' tile
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), cr = q >> 2, r8 = (q & 3) * 8;
-      uint32_t xs[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xs[e] = stg[(i * 32 + r8 + e) * WLD + j * 32 + cr];
-      const ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
-      ns_st8(nb.mo, T.C, wc0 + j * 32 + cr, wr0 + i * 32 + r8, (int)T.R, (int)T.C, (T.C & 7) == 0, mv);
-    }
-  }
-  if (!mirror) return;
-  // out[c][r] for this tile's (r, c): 8-row column chunks; for B, the b A term
-  // is read at the transposed position (A is symmetric, A[r][c] = A[c][r])
-  if (MODE == 1) {
-#pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
-      ev[u] = *(const KAON_G ku4*)(eop + (int64_t)(wc0 + j * 32 + (q >> 2)) * lde + wr0 + i * 32 + (q & 3) * 8);
-    }
-  }
+  if (!mirror && !trout) return;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  // Transposed pass: 16-lane group gq of u takes columns c0 .. c0 + 15 and
+  // rows r0 .. r0 + 7 of sub-tile (i, j); lane s of the group points the
+  // transpose read at row r0 + s / 4 (+ 4), columns c0 + 4 (s % 4) .. + 3, and
+  // lane s receives column c0 + s, rows r0 .. r0 + 3 (r0 + 4 .. + 7): the
+  // 16 bytes of row c0 + s of the transposed tile from column r0.
+  const int gq = lane >> 4, sl = lane & 15;
 #pragma unroll
   for (int u = 0; u < 32; ++u) {
-    const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), cr = q >> 2, r8 = (q & 3) * 8;
-    uint32_t xs[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xs[e] = stg[(i * 32 + r8 + e) * WLD + j * 32 + cr];
-    ku4 mv = ku4{xs[0] | (xs[1] << 16), xs[2] | (xs[3] << 16), xs[4] | (xs[5] << 16), xs[6] | (xs[7] << 16)};
-    if (MODE == 1) {
-      uint32_t o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = __uint_as_float(xs[e] << 16), ef = __uint_as_float(half_of(ev[u], e) << 16);
-        o[e] = f2bf(rbf(cb * ef) + rbf(cc * x));
-      }
-      mv = ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
-    }
-    *(KAON_G ku4*)G(out + (int64_t)(wc0 + j * 32 + cr) * ldc + wr0 + i * 32 + r8) = mv;
+    const int i = u >> 3, j = (u >> 1) & 3, h = u & 1;
+    const int c0 = j * 32 + 16 * (gq & 1), r0 = i * 32 + 8 * ((gq >> 1) + 2 * h);
+    const uint16_t* p = stg + (r0 + (sl >> 2)) * WLD + c0 + 4 * (sl & 3);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p + 4 * WLD));
+    const ku4 mv = __builtin_bit_cast(ku4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    if (mirror)
+      *(KAON_G ku4*)G(out + (int64_t)(wc0 + c0 + sl) * ldc + wr0 + r0) = mv;
+    else
+      ns_st8(nb.mo, T.C, wc0 + c0 + sl, wr0 + r0, (int)T.R, (int)T.C, oaln, mv);
   }
 }
 

@@ -554,14 +554,12 @@ __device__ __forceinline__ ku4 ns_ld8(const uint16_t* p, int64_t ld, int r, int 
 }
 
 // x = bf16(v / den) on 8 packed bf16 (torch's bf16 division: fp32 quotient,
-// rounded to bf16), or v itself
-template <bool SCALE>
-__device__ __forceinline__ ku4 ns_map8(ku4 v, double rden) {
-  if (!SCALE) return v;
-  uint32_t o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = f2bf(div_r64(__uint_as_float(half_of(v, e) << 16), rden));
-  return ku4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+// rounded to bf16; a NaN stays some NaN, made 0x7FC0 when O is written)
+__device__ __forceinline__ ku4 ns_scale8(ku4 v, double rden) {
+  auto two = [&](uint32_t w) {
+    return f2bf2(div_r64(__uint_as_float(w << 16), rden), div_r64(__uint_as_float(w & 0xFFFF0000u), rden));
+  };
+  return ku4{two(v.x), two(v.y), two(v.z), two(v.w)};
 }
 
 // One 128 x 128 tile of the iterate, x(r0 + i, c0 + j) = bf16(M(r0 + i, c0 + j) / den)
@@ -569,9 +567,13 @@ __device__ __forceinline__ ku4 ns_map8(ku4 v, double rden) {
 // cols read as 0 (the iterate's zero padding).  The iterate's rows are a
 // multiple of 128 long, so its writes are 16-byte and in range.  A thread
 // issues all eight of its 16-byte loads before it uses the first.  The
-// transpose goes through an LDS tile of 256-byte rows whose 16-byte chunks are
-// XOR-swizzled by row / 8: row chunk writes and 8-row column reads both touch
-// 16 distinct chunks per 16 lanes.
+// transpose goes through an LDS tile of M's rows (256 bytes each) whose 16-byte
+// chunks are XOR-swizzled by 2 (row % 4), and comes back as 8-row column
+// chunks by the LDS transpose read: lane s of a 16-lane group points at tile
+// row 8 g + s / 4 (+ 4), columns 16 ci + 4 (s % 4) .. + 3, and receives column
+// 16 ci + s, rows 8 g .. 8 g + 7 -- the 16 bytes of x row r0 + 16 ci + s from
+// column c0 + 8 g.  The four rows of a read sit in four different 32-byte bank
+// groups.
 template <bool TR>
 __device__ __forceinline__ void ns_prep_tile(const uint16_t* m, int64_t ldm, int rows, int cols, uint16_t* x,
                                              int64_t ldx, int r0, int c0, double rden, uint16_t* tile) {
@@ -589,25 +591,27 @@ __device__ __forceinline__ void ns_prep_tile(const uint16_t* m, int64_t ldm, int
 #pragma unroll
     for (int s = 0; s < NQ; ++s) {
       const int q = tid + 256 * s;
-      *(KAON_G ku4*)G(x + (int64_t)(r0 + (q >> 4)) * ldx + c0 + (q & 15) * 8) = ns_map8<true>(v[s], rden);
+      *(KAON_G ku4*)G(x + (int64_t)(r0 + (q >> 4)) * ldx + c0 + (q & 15) * 8) = ns_scale8(v[s], rden);
     }
     return;
   }
 #pragma unroll
   for (int s = 0; s < NQ; ++s) {
     const int q = tid + 256 * s, tt = q >> 4, ch = q & 15;
-    *(ku4*)&tile[tt * TILE + ((ch ^ ((tt >> 3) & 15)) << 3)] = v[s];
+    *(ku4*)&tile[tt * TILE + ((ch ^ (2 * (tt & 3))) << 3)] = v[s];
   }
   __syncthreads();
+  // wave w, step k: column block ci of 16 x rows, 8-column groups g = 4 gh + (lane / 16)
+  const int w = tid >> 6, gq = (tid >> 4) & 3, sl = tid & 15;
 #pragma unroll
-  for (int s = 0; s < NQ; ++s) {
-    const int q = tid + 256 * s, ii = q >> 4, g = q & 15;  // x row r0 + ii, columns c0 + 8 g ..
-    const int off = (((ii >> 3) ^ g) << 3) + (ii & 7);
-    uint32_t h[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = tile[(g * 8 + e) * TILE + off];
-    const ku4 t = ku4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    *(KAON_G ku4*)G(x + (int64_t)(r0 + ii) * ldx + c0 + g * 8) = ns_map8<true>(t, rden);
+  for (int k = 0; k < NQ; ++k) {
+    const int P = k * 4 + w, ci = P & 7, g = 4 * (P >> 3) + gq;
+    const int row = 8 * g + (sl >> 2), ch = (2 * ci + ((sl & 3) >> 1)) ^ (2 * (row & 3));
+    const uint16_t* p = tile + row * TILE + (ch << 3) + 4 * (sl & 1);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p + 4 * TILE));
+    const ku4 t = __builtin_bit_cast(ku4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    *(KAON_G ku4*)G(x + (int64_t)(r0 + 16 * ci + sl) * ldx + c0 + 8 * g) = ns_scale8(t, rden);
   }
 }
 

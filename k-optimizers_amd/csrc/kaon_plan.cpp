@@ -270,9 +270,13 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     if (opt == KAON_OPT_ADAMUON) {
       const int64_t m = std::min(t.R, t.C), k = std::max(t.R, t.C);
       t.ns_tr = t.R > t.C ? 1 : 0;
-      // big matrices take 2*KAON_NS_TILE tiles when that adds no row padding
+      // Matrices of at least 4 * KAON_NS_TILE rows take 2 * KAON_NS_TILE tiles
+      // when the padding that adds grows the m^2 terms by at most 1.5x: the
+      // big-tile kernel runs at more than twice the small one's rate (m = 640
+      // pads to 768, m = 320 stays on small tiles).
       const int64_t m128 = (m + KAON_NS_TILE - 1) / KAON_NS_TILE * KAON_NS_TILE;
-      const bool big = m128 >= 4 * KAON_NS_TILE && m128 % (2 * KAON_NS_TILE) == 0;
+      const int64_t m256 = (m + 2 * KAON_NS_TILE - 1) / (2 * KAON_NS_TILE) * (2 * KAON_NS_TILE);
+      const bool big = m128 >= 4 * KAON_NS_TILE && 2 * m256 * m256 <= 3 * m128 * m128;
       const int64_t tile = big ? 2 * KAON_NS_TILE : KAON_NS_TILE;
       t.m_pad = (int32_t)((m + tile - 1) / tile * tile);
       t.k_pad = (int32_t)((k + tile - 1) / tile * tile);

@@ -84,10 +84,11 @@ def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     return O.bf16_to_f32(o).reshape(g.shape)
 
 
-# the last four take the 256-tile GEMMs (m = min(R, C) a multiple of 256, >= 512):
+# the last six take the 256-tile GEMMs (m = min(R, C) >= 512, padded to a multiple
+# of 256 where that grows m^2 by at most 1.5x: 640 -> 768 in the last two):
 # symmetric products on row <= column tiles with mirrored stores
 @pytest.mark.parametrize("shape", [(64, 96), (96, 64), (77, 33), (130, 300), (256, 640), (640, 256), (320, 2880),
-                                   (512, 1024), (1024, 512), (512, 2000), (768, 1280)])
+                                   (512, 1024), (1024, 512), (512, 2000), (768, 1280), (640, 700), (1000, 640)])
 def test_newton_schulz_matches_oracle(shape):
     print(f"[gpu] newton-schulz {shape}", flush=True)
     rng = np.random.default_rng(sum(shape))
@@ -122,7 +123,7 @@ def _ns_torch(g: torch.Tensor, steps: int) -> torch.Tensor:
 
 # BASELINE configs[4]'s own matrices: the 1280-row linears and the conv
 # [1280, 1280, 3, 3] as 1280 x 11520 (the 256-tile GEMM path), [5120, 1280]
-# transposed, and a 640-row conv
+# transposed, and a 640-row conv (256 tiles over rows padded to 768)
 @pytest.mark.parametrize("shape", [(1280, 1280), (1280, 2048), (1280, 5120), (5120, 1280), (1280, 11520),
                                    (640, 5760)])
 def test_newton_schulz_sdxl_sizes_match_torch(shape):

@@ -263,8 +263,8 @@ def test_state_layout_matches_reference_at_init():
 
 def test_adamuon_plan_pads_and_tiles_newton_schulz():
     """AdaMuon plans: m_pad/k_pad round min/max(R, C) up to the GEMM tile (twice
-    KAON_NS_TILE when m rounds to a multiple of it with no extra padding and is at
-    least 4 tiles), the transposed flag marks R > C, every tile of the padded
+    KAON_NS_TILE when m is at least 4 tiles and the padding to the big tile grows
+    m^2 by at most 1.5x), the transposed flag marks R > C, every tile of the padded
     products is listed once (big symmetric products: row <= column only, big
     items first), and the Newton-Schulz blocks do not overlap other workspace."""
     L = _lib()
@@ -289,8 +289,9 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
         d = descs[i]
         m, k = min(d.R, d.C), max(d.R, d.C)
         m128 = -(-m // L.NS_TILE) * L.NS_TILE
-        big = m128 >= 4 * L.NS_TILE and m128 % (2 * L.NS_TILE) == 0
-        assert big == (m in (1280, 512, 1024)), (s, big)
+        m256 = -(-m // (2 * L.NS_TILE)) * 2 * L.NS_TILE
+        big = m128 >= 4 * L.NS_TILE and 2 * m256 * m256 <= 3 * m128 * m128
+        assert big == (m in (1280, 512, 1024, 640)), (s, big)
         t = 2 * L.NS_TILE if big else L.NS_TILE
         assert d.ns_tr == (1 if d.R > d.C else 0)
         assert d.m_pad == -(-m // t) * t and d.k_pad == -(-k // t) * t

@@ -147,7 +147,8 @@ def phase_bytes(phase: int, bm: float, wd: bool, opt: str = "adakaon", w: dict |
 
 
 KERNEL_SOURCES = ("k-optimizers_amd/csrc/kaon_step.hip", "k-optimizers_amd/csrc/kaon_fast.hip",
-                  "k-optimizers_amd/csrc/kaon_common.h", "k-optimizers_amd/csrc/kaon_device.h")
+                  "k-optimizers_amd/csrc/kaon_common.h", "k-optimizers_amd/csrc/kaon_device.h",
+                  "k-optimizers_amd/csrc/kaon_ns.hip", "k-optimizers_amd/csrc/kaon_plan.cpp")
 
 
 def kernel_source_hash() -> str:
@@ -564,7 +565,7 @@ def main() -> int:
                                "unit": "TFLOP/s", "frac": round(ach / BF16_MFMA_PEAK_TFLOPS, 4),
                                "traffic": measured_traffic(args.workload, dom),
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
-                               "avg_ms": round(br[dom], 4)}
+                               "avg_ms": round(br[dom], 4), "source": kernel_source_hash()}
         else:
             bpp = phase_bytes(dom, bm, wd, w["opt"], w) + (2.0 if gc_write and dom == 6 else 0.0)
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0

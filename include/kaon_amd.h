@@ -69,9 +69,9 @@ enum {
   KAON_F_PD_COUPLED = 1024, /* KProdigy pass 1: weight decay folded into the gradient
                                (decouple=False, kprodigy.py:342-349) */
   KAON_F_PD_STATS = 2048,   /* KProdigy pass 1: update s and the D statistics this step */
-  KAON_F_GC_WRITE = 4096    /* Adakaon / Lion apply: also store the centralized gradient over
-                               p.grad, as the reference's native path leaves it
-                               (centralize_grads_, _backend.py:147-177) */
+  KAON_F_GC_WRITE = 4096    /* Adakaon / Lion apply and KProdigy pass 2: also store the
+                               centralized gradient over p.grad, as the reference's native
+                               path leaves it (centralize_grads_, _backend.py:147-177) */
 };
 
 /*

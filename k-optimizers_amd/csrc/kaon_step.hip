@@ -2258,7 +2258,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_sfin(const KaonTensor* __restric
 // or 6 (apply): numerator = the momentum (float codecs as pass 1 stored it; int8 /
 // 4-bit requantized here from the old codes with pass 1's absmax) or g; over
 // max(sqrt(v), dn*eps), or times min(r c / dn, 1/(dn*eps)); times dlr; decoupled
-// WD; cautious; write.
+// WD; cautious; write.  With KAON_F_GC_WRITE the apply also stores the
+// centralized gradient over p.grad.
 template <int PHASE, int PT, int GT, int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
@@ -2401,6 +2402,17 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
         dout[i] = cautious ? div_r64(d * (kp ? 1.0f : 0.0f), rden) : d;
       }
       if (PHASE != 6) continue;
+      if (gc && (hp.flags & KAON_F_GC_WRITE)) {
+        // the centralized gradient over p.grad (already rounded to the grad dtype)
+        if (GT == KAON_F32) {
+          st8_f32(const_cast<void*>(T.g), e0, cnt, vec, g);
+        } else {
+          uint32_t gb[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) gb[i] = f2lp<GT>(g[i]);
+          st8_bits(const_cast<void*>(T.g), e0, cnt, vec, gb);
+        }
+      }
       if (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) st_mom_at<CODEC>(T.m, n, e0, cnt, vec, qout);
       if (PT == KAON_F32) {
         float o[8];

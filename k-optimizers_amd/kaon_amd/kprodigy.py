@@ -279,7 +279,8 @@ class KProdigy(KaonOptimizer):
                 self.state[p]["step"] += 1
             for plan, pdt, gdt, dev, _positions, _idx in launches:
                 hp = self._hyper(group, pdt, gdt, c)
+                if self.centralize_grads_in_place:
+                    hp.flags |= L.F_GC_WRITE  # the apply stores the centralized gradient
                 L.check(lib.kaon_kprodigy_pass2(ctypes.byref(plan.launch), ctypes.byref(hp),
                                                 E.stream_handle(dev)), "kaon_kprodigy_pass2")
-                self._gc_writeback(group, plan, hp, dev)
             group["k"] = group["k"] + 1

@@ -6,8 +6,9 @@ before stepping (centralize_grads_, src/kaon/_backend.py:147-177), so a
 caller reading p.grad after step() sees g - mean over the fan-in, in the
 grad dtype, for params of 2 dims or more.  The fused Adakaon / AdaPNM kernels
 centralize in-kernel and leave p.grad as it was (src/kaon/adakaon.py:387-409).
-kaon_amd's step never writes the gradient; kaon_gc_writeback writes the
-centralized one back after it.  Checked against the oracle's bf16 GC.
+The Adakaon / Lion apply and KProdigy's pass 2 store the centralized gradient
+as they read it (KAON_F_GC_WRITE); AdaPNM and AdaMuon write it back after the
+step with kaon_gc_writeback.  Checked against the oracle's bf16 GC.
 """
 import numpy as np
 import pytest

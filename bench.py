@@ -152,14 +152,20 @@ KERNEL_SOURCES = ("k-optimizers_amd/csrc/kaon_step.hip", "k-optimizers_amd/csrc/
 
 
 def kernel_source_hash() -> str:
-    """sha256 (first 16 hex digits) of the step kernels' source files, the key a
-    committed PMC summary records for the build it measured."""
+    """sha256 (first 16 hex digits) of the step kernels' source files with their
+    comments and blank lines removed, the key a committed PMC summary records for
+    the build it measured (an edit to a comment does not invalidate it)."""
     import hashlib
+    import re
 
     h = hashlib.sha256()
     for rel in KERNEL_SOURCES:
-        with open(os.path.join(ROOT, rel), "rb") as fh:
-            h.update(fh.read())
+        with open(os.path.join(ROOT, rel), encoding="utf-8") as fh:
+            text = fh.read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        lines = [ln.rstrip() for ln in text.splitlines() if ln.strip()]
+        h.update("\n".join(lines).encode())
     return h.hexdigest()[:16]
 
 

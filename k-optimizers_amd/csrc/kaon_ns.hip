@@ -12,13 +12,16 @@
 // through all three products, so the GEMMs run on whole tiles with no edge
 // masks and the padding never reaches the result.
 //
-// GEMM: one 128 x 128 output tile per workgroup (4 wave64, each 64 x 64 = 2 x 2
-// v_mfma_f32_32x32x16_bf16 tiles), K in steps of 64 staged through LDS; the
-// next K step's global loads are in flight while the MFMAs run.  Work items
-// list (tensor, tile row, tile column) for every tensor of the plan, so one
-// launch per product covers the whole parameter list.  A = x x^T and A A are
-// "NT" products (both operands row-major along K; A is symmetric); B x reads
-// x along its rows and is transposed into LDS on the way in.
+// GEMMs: matrices of at least 512 rows take 256 x 256 output tiles (k_ns_gemm2,
+// 4 wave64 of 128 x 128, two LDS stages of K = 64), the rest 128 x 128 tiles
+// (k_ns_gemm, 4 wave64 of 64 x 64); both on v_mfma_f32_32x32x16_bf16 with the
+// next K step's global loads in flight while the MFMAs run.  Work items list
+// (tensor, tile row, tile column) for every tensor of the plan, so one launch
+// per product and tile size covers the whole parameter list; the planner lays
+// the big tiles out per XCD.  A = x x^T and A A are "NT" products (both
+// operands row-major along K; A is symmetric, so big tiles cover row <= column
+// and mirror); B x reads x along its rows with the LDS transpose read.  The
+// last iteration's B x writes the orthogonal factor O over M.
 #include "kaon_ns.h"
 
 #include <string>

@@ -25,6 +25,7 @@
 #include "kaon_ns.h"
 
 #include <string>
+#include <type_traits>
 
 #include "kaon_device.h"
 
@@ -326,13 +327,17 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   constexpr int KC = BK / 8;     // 16-byte chunks per row per step
   constexpr int NS = BT * KC / 256;
   ku4 ra[NS], rb[NS];
-  auto gload = [&](int k0) {
+  // DG: a diagonal tile of a symmetric product, whose two operands are the same
+  // row panel -- it is loaded and stored once and both fragments read it
+  auto gload = [&](int k0, auto dg) {
+    constexpr bool DG = decltype(dg)::value;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int q = tid + 256 * s, r = q / KC, kc = q % KC;
       ra[s] = *(const KAON_G ku4*)G(Aop + (int64_t)(row0 + r) * lda + k0 + kc * 8);
     }
     if (MODE != 2) {
+      if (DG) return;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int q = tid + 256 * s, r = q / KC, kc = q % KC;
@@ -347,7 +352,8 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       }
     }
   };
-  auto lstore = [&](int st) {
+  auto lstore = [&](int st, auto dg) {
+    constexpr bool DG = decltype(dg)::value;
     uint16_t* as = As(st);
     uint16_t* bs = Bs(st);
 #pragma unroll
@@ -356,6 +362,7 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       *(ku4*)&as[r * BLD + kc * 8] = ra[s];
     }
     if (MODE != 2) {
+      if (DG) return;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int q = tid + 256 * s, r = q / KC, kc = q % KC;
@@ -417,25 +424,29 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   constexpr int NWR = 2 * NS;  // LDS store instructions per step
   constexpr int RD2 = MODE == 2 ? 2 : 1;  // MODE 2: 12 fragment reads per sub-step, else 8
 
+  auto kloop = [&](auto dg) {
+  constexpr bool DG = decltype(dg)::value;
+  constexpr int VMS = DG ? NS / 8 : 2 * NS / 8;  // global loads per scheduling slot of sub-step 0
+  constexpr int WRS = DG ? NWR / 16 : NWR / 8;   // LDS stores per slot of sub-step 3
   const int nk = K / BK;
-  gload(0);
-  lstore(0);
+  gload(0, dg);
+  lstore(0, dg);
   __syncthreads();
   for (int ks = 0; ks < nk; ++ks) {
     const int cur = ks & 1;
     const uint16_t* as = As(cur);
-    const uint16_t* bs = Bs(cur);
+    const uint16_t* bs = DG ? As(cur) : Bs(cur);
     lfrag(0, as, bs, 0);
-    gload(min(ks + 1, nk - 1) * BK);
+    gload(min(ks + 1, nk - 1) * BK, dg);
     lfrag(1, as, bs, 16);
     mma(0);
     __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 4 + 4 * RD2, 0);  // sub-step 0's fragments
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, 2 * NS / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, 2 * NS / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
@@ -457,15 +468,20 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
       __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
-    lstore(cur ^ 1);  // that stage was last read before the previous barrier
+    lstore(cur ^ 1, dg);  // that stage was last read before the previous barrier
     mma(1);
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_WR, NWR / 8, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_WR, WRS, 0);
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
     }
     __syncthreads();
   }
+  };
+  if (MODE != 2 && it.row0 == it.nrows)
+    kloop(std::true_type{});
+  else
+    kloop(std::false_type{});
 
   // Epilogue.  bf16(v) of the wave's whole 128 x 128 tile goes to its own LDS
   // region (the stages are free after the last barrier) and is read back as

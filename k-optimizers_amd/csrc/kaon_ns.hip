@@ -581,62 +581,95 @@ __device__ __forceinline__ ku4 ns_scale8(ku4 v, double rden) {
   return ku4{two(v.x), two(v.y), two(v.z), two(v.w)};
 }
 
-// One 128 x 128 tile of the iterate, x(r0 + i, c0 + j) = bf16(M(r0 + i, c0 + j) / den)
-// or, transposed, bf16(M(c0 + j, r0 + i) / den); elements outside M's rows x
-// cols read as 0 (the iterate's zero padding).  The iterate's rows are a
-// multiple of 128 long, so its writes are 16-byte and in range.  A thread
-// issues all eight of its 16-byte loads before it uses the first.  The
-// transpose goes through an LDS tile of M's rows (256 bytes each) whose 16-byte
-// chunks are XOR-swizzled by 2 (row % 4), and comes back as 8-row column
-// chunks by the LDS transpose read: lane s of a 16-lane group points at tile
-// row 8 g + s / 4 (+ 4), columns 16 ci + 4 (s % 4) .. + 3, and receives column
-// 16 ci + s, rows 8 g .. 8 g + 7 -- the 16 bytes of x row r0 + 16 ci + s from
-// column c0 + 8 g.  The four rows of a read sit in four different 32-byte bank
-// groups.
-template <bool TR>
-__device__ __forceinline__ void ns_prep_tile(const uint16_t* m, int64_t ldm, int rows, int cols, uint16_t* x,
-                                             int64_t ldx, int r0, int c0, double rden, uint16_t* tile) {
-  const bool ma = (ldm & 7) == 0;
-  const int tid = threadIdx.x;
-  constexpr int NQ = TILE * TILE / 8 / 256;  // 16-byte chunks per thread
-  ku4 v[NQ];
-  // TR: source rows c0 .. c0 + 127 (tile rows), columns r0 .. r0 + 127
+// The transposed iterate of an R > C matrix, x(r0 + i, c0 + j) = bf16(M(c0 + j,
+// r0 + i) / den), in 128 x 128 tiles; elements outside M's rows x cols read as
+// 0 (the iterate's zero padding).  The iterate's rows are a multiple of 128
+// long, so its writes are 16-byte and in range.  A tile goes through an LDS
+// tile of M's rows (256 bytes each) whose 16-byte chunks are XOR-swizzled by
+// 2 (row % 4), and comes back as 8-row column chunks by the LDS transpose read:
+// lane s of a 16-lane group points at tile row 8 g + s / 4 (+ 4), columns
+// 16 ci + 4 (s % 4) .. + 3, and receives column 16 ci + s, rows 8 g .. 8 g + 7
+// -- the 16 bytes of x row r0 + 16 ci + s from column c0 + 8 g.  The four rows
+// of a read sit in four different 32-byte bank groups.
+struct NsTrTile {
+  const uint16_t* m;
+  int64_t ldm;
+  int rows, cols;
+  uint16_t* x;
+  int64_t ldx;
+  double rden;
+};
+constexpr int NS_NQ = TILE * TILE / 8 / 256;  // 16-byte chunks per thread per tile
+
+// source rows c0 .. c0 + 127 (tile rows), columns r0 .. r0 + 127
+__device__ __forceinline__ void ns_tr_load(const NsTrTile& a, int r0, int c0, ku4 (&v)[NS_NQ]) {
+  const bool ma = (a.ldm & 7) == 0;
 #pragma unroll
-  for (int s = 0; s < NQ; ++s) {
-    const int q = tid + 256 * s, tt = q >> 4, ch = q & 15;
-    v[s] = TR ? ns_ld8(m, ldm, c0 + tt, r0 + ch * 8, rows, cols, ma) : ns_ld8(m, ldm, r0 + tt, c0 + ch * 8, rows, cols, ma);
+  for (int s = 0; s < NS_NQ; ++s) {
+    const int q = threadIdx.x + 256 * s, tt = q >> 4, ch = q & 15;
+    v[s] = ns_ld8(a.m, a.ldm, c0 + tt, r0 + ch * 8, a.rows, a.cols, ma);
   }
-  if (!TR) {
+}
+
+__device__ __forceinline__ void ns_tr_stage(const ku4 (&v)[NS_NQ], uint16_t* tile) {
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) {
-      const int q = tid + 256 * s;
-      *(KAON_G ku4*)G(x + (int64_t)(r0 + (q >> 4)) * ldx + c0 + (q & 15) * 8) = ns_scale8(v[s], rden);
-    }
-    return;
-  }
-#pragma unroll
-  for (int s = 0; s < NQ; ++s) {
-    const int q = tid + 256 * s, tt = q >> 4, ch = q & 15;
+  for (int s = 0; s < NS_NQ; ++s) {
+    const int q = threadIdx.x + 256 * s, tt = q >> 4, ch = q & 15;
     *(ku4*)&tile[tt * TILE + ((ch ^ (2 * (tt & 3))) << 3)] = v[s];
   }
-  __syncthreads();
+}
+
+__device__ __forceinline__ void ns_tr_store(const NsTrTile& a, int r0, int c0, const uint16_t* tile) {
   // wave w, step k: column block ci of 16 x rows, 8-column groups g = 4 gh + (lane / 16)
-  const int w = tid >> 6, gq = (tid >> 4) & 3, sl = tid & 15;
+  const int tid = threadIdx.x, w = tid >> 6, gq = (tid >> 4) & 3, sl = tid & 15;
 #pragma unroll
-  for (int k = 0; k < NQ; ++k) {
+  for (int k = 0; k < NS_NQ; ++k) {
     const int P = k * 4 + w, ci = P & 7, g = 4 * (P >> 3) + gq;
     const int row = 8 * g + (sl >> 2), ch = (2 * ci + ((sl & 3) >> 1)) ^ (2 * (row & 3));
     const uint16_t* p = tile + row * TILE + (ch << 3) + 4 * (sl & 1);
     const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
     const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p + 4 * TILE));
     const ku4 t = __builtin_bit_cast(ku4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    *(KAON_G ku4*)G(x + (int64_t)(r0 + 16 * ci + sl) * ldx + c0 + 8 * g) = ns_scale8(t, rden);
+    *(KAON_G ku4*)G(a.x + (int64_t)(r0 + 16 * ci + sl) * a.ldx + c0 + 8 * g) = ns_scale8(t, a.rden);
+  }
+}
+
+// Rows [r0, r1) of the iterate over its whole width, x = bf16(M / den) with
+// zeros past M's rows x cols: whole rows of M and of x are long contiguous
+// runs.  A thread takes every 256th 16-byte chunk of the rows, four at a time
+// with their loads issued first.
+__device__ __forceinline__ void ns_prep_rows(const uint16_t* m, int64_t ldm, int rows, int cols, uint16_t* x,
+                                             int64_t ldx, int r0, int r1, double rden) {
+  const bool ma = (ldm & 7) == 0;
+  const int nch = (int)(ldx >> 3);  // 16-byte chunks per row of x
+  const int dr = 256 / nch, dc = 256 % nch;
+  int r = r0 + (int)threadIdx.x / nch, c = (int)threadIdx.x % nch;
+  while (r < r1) {
+    ku4 v[4];
+    int rs[4], cs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      rs[u] = r;
+      cs[u] = c;
+      v[u] = r < r1 ? ns_ld8(m, ldm, r, c * 8, rows, cols, ma) : ku4{0u, 0u, 0u, 0u};
+      r += dr;
+      c += dc;
+      if (c >= nch) {
+        c -= nch;
+        ++r;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (rs[u] < r1) *(KAON_G ku4*)G(x + (int64_t)rs[u] * ldx + cs[u] * 8) = ns_scale8(v[u], rden);
   }
 }
 
 // x = bf16(M / den) into the padded iterate (transposed when R > C), zeros in
 // the padding; den = bf16(bf16(||M||) + 1e-7) from the workspace (phase 8).
-// One item = one tile (kind 0) or 2 x 2 tiles (kind 1, a big-tile item).
+// Transposed: one item = one tile (kind 0) or 2 x 2 tiles (kind 1, a big-tile
+// item).  Otherwise the tk items of a row tile split its rows: item (a, b)
+// takes rows [a T + b T / tk, a T + (b + 1) T / tk) over the whole width.
 __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, float* ws) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[TILE * TILE];
@@ -645,14 +678,28 @@ __global__ __launch_bounds__(256) void k_ns_prep(const KaonTensor* __restrict__ 
   const KaonTensor& T = D[it.tensor];
   const NsBufs nb = ns_bufs(ws, T);
   const double rden = rcp64(G(ws)[T.ws_scal + 2]);
-  const int sub = it.kind ? 2 : 1;
-  for (int s = 0; s < sub * sub; ++s) {
-    if (s) __syncthreads();  // the transpose tile is reused
+  if (!T.ns_tr) {
+    const int tt = it.kind ? 2 * TILE : TILE, tk = T.k_pad / tt;
+    const int r0 = it.row0 * tt + it.nrows * tt / tk, r1 = it.row0 * tt + (it.nrows + 1) * tt / tk;
+    ns_prep_rows(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, r0, r1, rden);
+    return;
+  }
+  // the sub * sub tiles of the item, the next tile's loads issued before the
+  // current one is staged
+  const NsTrTile a{nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, rden};
+  const int sub = it.kind ? 2 : 1, ntile = sub * sub;
+  ku4 v[NS_NQ], vn[NS_NQ];
+  ns_tr_load(a, it.row0 * sub * TILE, it.nrows * sub * TILE, v);
+  for (int s = 0; s < ntile; ++s) {
     const int i0 = (it.row0 * sub + s / sub) * TILE, t0 = (it.nrows * sub + s % sub) * TILE;
-    if (T.ns_tr)
-      ns_prep_tile<true>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, i0, t0, rden, tile);
-    else
-      ns_prep_tile<false>(nb.mo, T.C, (int)T.R, (int)T.C, nb.x0, T.k_pad, i0, t0, rden, tile);
+    if (s) __syncthreads();  // the previous tile's transpose reads are done
+    ns_tr_stage(v, tile);
+    if (s + 1 < ntile)
+      ns_tr_load(a, (it.row0 * sub + (s + 1) / sub) * TILE, (it.nrows * sub + (s + 1) % sub) * TILE, vn);
+    __syncthreads();
+    ns_tr_store(a, i0, t0, tile);
+#pragma unroll
+    for (int q = 0; q < NS_NQ; ++q) v[q] = vn[q];
   }
 }
 

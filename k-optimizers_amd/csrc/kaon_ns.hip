@@ -92,28 +92,36 @@ __device__ __forceinline__ void ns_st8(uint16_t* p, int64_t ld, int r, int c, in
 
 // The epilogue term on a packed pair of bf16-valued products x0, x1 and the
 // packed A / x pair ew, with torch's roundings of each bf16 operation:
-// MODE 1: bf16(bf16(b A) + bf16(c x)), MODE 2: bf16(bf16(a x) + x).
+// MODE 1: bf16(bf16(b A) + bf16(c x)), MODE 2: bf16(bf16(a x) + x).  nan is
+// set where a result is NaN (the packed conversion keeps NaN as NaN).
 template <int MODE>
-__device__ __forceinline__ uint32_t ns_comb2(float x0, float x1, uint32_t ew, float ca, float cb, float cc) {
+__device__ __forceinline__ uint32_t ns_comb2(float x0, float x1, uint32_t ew, float ca, float cb, float cc,
+                                             bool& nan) {
   float t0 = __uint_as_float(ew << 16), t1 = __uint_as_float(ew & 0xFFFF0000u);
+  float s0, s1;
   if (MODE == 1) {
     t0 *= cb;
     t1 *= cb;
     rbf2(t0, t1);
     float u0 = cc * x0, u1 = cc * x1;
     rbf2(u0, u1);
-    return f2bf2(t0 + u0, t1 + u1);
+    s0 = t0 + u0;
+    s1 = t1 + u1;
+  } else {
+    t0 *= ca;
+    t1 *= ca;
+    rbf2(t0, t1);
+    s0 = t0 + x0;
+    s1 = t1 + x1;
   }
-  t0 *= ca;
-  t1 *= ca;
-  rbf2(t0, t1);
-  return f2bf2(t0 + x0, t1 + x1);
+  nan |= __builtin_isunordered(s0, s1);
+  return f2bf2(s0, s1);
 }
 
 template <int MODE>
-__device__ __forceinline__ ku4 ns_comb8(ku4 xv, ku4 ev, float ca, float cb, float cc) {
+__device__ __forceinline__ ku4 ns_comb8(ku4 xv, ku4 ev, float ca, float cb, float cc, bool& nan) {
   auto one = [&](uint32_t xw, uint32_t ew) {
-    return ns_comb2<MODE>(__uint_as_float(xw << 16), __uint_as_float(xw & 0xFFFF0000u), ew, ca, cb, cc);
+    return ns_comb2<MODE>(__uint_as_float(xw << 16), __uint_as_float(xw & 0xFFFF0000u), ew, ca, cb, cc, nan);
   };
   return ku4{one(xv.x, ev.x), one(xv.y, ev.y), one(xv.z, ev.z), one(xv.w, ev.w)};
 }
@@ -253,7 +261,8 @@ __global__ __launch_bounds__(256) void k_ns_gemm(const KaonTensor* __restrict__ 
             w[h] = f2bf2(x0, x1);
           } else {
             rbf2(x0, x1);
-            w[h] = ns_comb2<MODE>(x0, x1, (uint32_t)(ev >> (32 * h)), ca, cb, cc);
+            bool nan = false;  // the final store below makes every NaN 0x7FC0 itself
+            w[h] = ns_comb2<MODE>(x0, x1, (uint32_t)(ev >> (32 * h)), ca, cb, cc, nan);
           }
           if (FIN) w[h] = ns_canon2(w[h]);
         }
@@ -522,18 +531,37 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
   // u = (32 x 32 sub-tile i, j) x half h: rows rr = q / 4, 8 columns from c8
+  bool nan = false;  // some result of this lane is NaN
 #pragma unroll
   for (int u = 0; u < 32; ++u) {
     const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), rr = q >> 2, c8 = (q & 3) * 8;
     const ku4 xv = *(const ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8];
-    ku4 ov = MODE == 0 ? xv : ns_comb8<MODE>(xv, ev[u], ca, cb, cc);
-    if (FIN) ov = ku4{ns_canon2(ov.x), ns_canon2(ov.y), ns_canon2(ov.z), ns_canon2(ov.w)};
+    const ku4 ov = MODE == 0 ? xv : ns_comb8<MODE>(xv, ev[u], ca, cb, cc, nan);
     if (!FIN)
       *(KAON_G ku4*)G(out + (int64_t)(wr0 + i * 32 + rr) * ldc + wc0 + j * 32 + c8) = ov;
     else if (!trout)
       ns_st8(nb.mo, T.C, wr0 + i * 32 + rr, wc0 + j * 32 + c8, (int)T.R, (int)T.C, oaln, ov);
     // each lane rewrites the chunk it read: no other lane touches it
     if (MODE != 0 && (mirror || trout)) *(ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8] = ov;
+  }
+  if (FIN && __builtin_amdgcn_ballot_w64(nan) != 0) {
+    // O holds torch's 0x7FC0 for every NaN: a wave that made one goes over its
+    // tile again -- O's chunks recomputed (the a x term read again) and
+    // rewritten, or (transposed O) the staged chunks rewritten before the
+    // transposed pass reads them
+    for (int u = 0; u < 32; ++u) {
+      const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1), rr = q >> 2, c8 = (q & 3) * 8;
+      ku4 ov = *(const ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8];
+      if (!trout) {
+        const ku4 e = *(const KAON_G ku4*)(eop + (int64_t)(wr0 + i * 32 + rr) * lde + wc0 + j * 32 + c8);
+        ov = ns_comb8<MODE>(ov, e, ca, cb, cc, nan);
+      }
+      ov = ku4{ns_canon2(ov.x), ns_canon2(ov.y), ns_canon2(ov.z), ns_canon2(ov.w)};
+      if (trout)
+        *(ku4*)&stg[(i * 32 + rr) * WLD + j * 32 + c8] = ov;
+      else
+        ns_st8(nb.mo, T.C, wr0 + i * 32 + rr, wc0 + j * 32 + c8, (int)T.R, (int)T.C, oaln, ov);
+    }
   }
   if (!mirror && !trout) return;
   __builtin_amdgcn_s_waitcnt(0xc07f);

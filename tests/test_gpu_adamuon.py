@@ -64,6 +64,11 @@ def test_adamuon_golden_case(name):
 def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     """O of one matrix through the phases API (momentum pass with beta1 = 0, so
     M = g; then Newton-Schulz); read back from the plan's workspace."""
+    return O.bf16_to_f32(_ns_bits_on_gpu(g, steps)).reshape(g.shape)
+
+
+def _ns_bits_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
+    """The bf16 bits of O [R, C] (see _ns_on_gpu)."""
     from kaon_amd import AdaMuon
     from kaon_amd import _lib as L
 
@@ -80,8 +85,20 @@ def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     torch.cuda.synchronize()
     d = plan.descs[0]
     ws16 = plan.workspace.view(torch.int16)
-    o = ws16[2 * d.ws_aux: 2 * d.ws_aux + g.size].cpu().numpy().view(np.uint16)
-    return O.bf16_to_f32(o).reshape(g.shape)
+    return ws16[2 * d.ws_aux: 2 * d.ws_aux + g.size].cpu().numpy().view(np.uint16).copy()
+
+
+@pytest.mark.parametrize("shape", [(77, 33), (96, 64), (512, 1024), (1024, 512), (640, 700)])
+def test_newton_schulz_nan_gives_torch_nan(shape):
+    """A NaN in the gradient makes every element of O NaN, and O holds torch's bf16 NaN
+    0x7FC0 (the GEMM epilogues' packed conversion leaves NaN payloads unspecified; the
+    last product makes them canonical, in the big-tile kernel only in waves that made one)."""
+    print(f"[gpu] newton-schulz NaN {shape}", flush=True)
+    rng = np.random.default_rng(7)
+    g = O.bf16_to_f32(O.f32_to_bf16((rng.standard_normal(shape) * 1e-3).astype(np.float32)))
+    g[shape[0] // 3, shape[1] // 2] = np.nan
+    o = _ns_bits_on_gpu(g, 2)
+    assert np.all(o == 0x7FC0), np.unique(o)[:8]
 
 
 # the last six take the 256-tile GEMMs (m = min(R, C) >= 512, padded to a multiple

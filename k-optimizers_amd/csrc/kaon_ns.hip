@@ -433,6 +433,13 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   constexpr int NWR = 2 * NS;  // LDS store instructions per step
   constexpr int RD2 = MODE == 2 ? 2 : 1;  // MODE 2: 12 fragment reads per sub-step, else 8
 
+  // B x's epilogue adds a x at the output position: rows [wr0, wr0 + 128) of x,
+  // the K rows this wave's tile streams at K offsets wr0 and wr0 + 64.  The
+  // first 64 of them (ev[0..15]) are copied out of the LDS stage at K offset
+  // wr0; the rest are read from memory after the loop (keeping all 128 rows
+  // would take 128 more VGPRs than the wave has).
+  const int wr0 = row0 + wm * 128, wc0 = col0 + wn * 128;
+  ku4 ev[32];
   auto kloop = [&](auto dg) {
   constexpr bool DG = decltype(dg)::value;
   constexpr int VMS = DG ? NS / 8 : 2 * NS / 8;  // global loads per scheduling slot of sub-step 0
@@ -445,6 +452,13 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
     const int cur = ks & 1;
     const uint16_t* as = As(cur);
     const uint16_t* bs = DG ? As(cur) : Bs(cur);
+    if (MODE == 2 && ks * BK == wr0) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
+        ev[u] = *(const ku4*)&bs[(i * 32 + (q >> 2)) * XLD + wn * 128 + j * 32 + (q & 3) * 8];
+      }
+    }
     lfrag(0, as, bs, 0);
     gload(min(ks + 1, nk - 1) * BK, dg);
     lfrag(1, as, bs, 16);
@@ -504,12 +518,10 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   const bool trout = FIN && T.ns_tr;
   const KAON_G uint16_t* eop = G((const uint16_t*)(MODE == 1 ? nb.a : xc));
   const int lde = MODE == 1 ? mp : kp;
-  const int wr0 = row0 + wm * 128, wc0 = col0 + wn * 128;
   const bool oaln = (T.C & 7) == 0;
-  ku4 ev[32];
   if (MODE != 0) {
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
+    for (int u = MODE == 2 ? 16 : 0; u < 32; ++u) {
       const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
       ev[u] = *(const KAON_G ku4*)(eop + (int64_t)(wr0 + i * 32 + (q >> 2)) * lde + wc0 + j * 32 + (q & 3) * 8);
     }

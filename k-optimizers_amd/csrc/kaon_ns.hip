@@ -441,65 +441,65 @@ __global__ __launch_bounds__(256) void k_ns_gemm2(const KaonTensor* __restrict__
   const int wr0 = row0 + wm * 128, wc0 = col0 + wn * 128;
   ku4 ev[32];
   auto kloop = [&](auto dg) {
-  constexpr bool DG = decltype(dg)::value;
-  constexpr int VMS = DG ? NS / 8 : 2 * NS / 8;  // global loads per scheduling slot of sub-step 0
-  constexpr int WRS = DG ? NWR / 16 : NWR / 8;   // LDS stores per slot of sub-step 3
-  const int nk = K / BK;
-  gload(0, dg);
-  lstore(0, dg);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ++ks) {
-    const int cur = ks & 1;
-    const uint16_t* as = As(cur);
-    const uint16_t* bs = DG ? As(cur) : Bs(cur);
-    if (MODE == 2 && ks * BK == wr0) {
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
-        ev[u] = *(const ku4*)&bs[(i * 32 + (q >> 2)) * XLD + wn * 128 + j * 32 + (q & 3) * 8];
-      }
-    }
-    lfrag(0, as, bs, 0);
-    gload(min(ks + 1, nk - 1) * BK, dg);
-    lfrag(1, as, bs, 16);
-    mma(0);
-    __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 4 + 4 * RD2, 0);  // sub-step 0's fragments
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    lfrag(0, as, bs, 32);
-    mma(1);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    lfrag(1, as, bs, 48);
-    mma(0);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
-    lstore(cur ^ 1, dg);  // that stage was last read before the previous barrier
-    mma(1);
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      __builtin_amdgcn_sched_group_barrier(SG_DS_WR, WRS, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
-    }
+    constexpr bool DG = decltype(dg)::value;
+    constexpr int VMS = DG ? NS / 8 : 2 * NS / 8;  // global loads per scheduling slot of sub-step 0
+    constexpr int WRS = DG ? NWR / 16 : NWR / 8;   // LDS stores per slot of sub-step 3
+    const int nk = K / BK;
+    gload(0, dg);
+    lstore(0, dg);
     __syncthreads();
-  }
+    for (int ks = 0; ks < nk; ++ks) {
+      const int cur = ks & 1;
+      const uint16_t* as = As(cur);
+      const uint16_t* bs = DG ? As(cur) : Bs(cur);
+      if (MODE == 2 && ks * BK == wr0) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int i = u >> 3, j = (u >> 1) & 3, q = lane + 64 * (u & 1);
+          ev[u] = *(const ku4*)&bs[(i * 32 + (q >> 2)) * XLD + wn * 128 + j * 32 + (q & 3) * 8];
+        }
+      }
+      lfrag(0, as, bs, 0);
+      gload(min(ks + 1, nk - 1) * BK, dg);
+      lfrag(1, as, bs, 16);
+      mma(0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 4 + 4 * RD2, 0);  // sub-step 0's fragments
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VMEM_RD, VMS, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      }
+      lfrag(0, as, bs, 32);
+      mma(1);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      }
+      lfrag(1, as, bs, 48);
+      mma(0);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_RD, RD2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      }
+      lstore(cur ^ 1, dg);  // that stage was last read before the previous barrier
+      mma(1);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_WR, WRS, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+      }
+      __syncthreads();
+    }
   };
   if (MODE != 2 && it.row0 == it.nrows)
     kloop(std::true_type{});

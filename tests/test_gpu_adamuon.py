@@ -69,23 +69,52 @@ def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
 
 def _ns_bits_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     """The bf16 bits of O [R, C] (see _ns_on_gpu)."""
+    return _ns_bits_many_on_gpu([g], steps)[0]
+
+
+def _ns_bits_many_on_gpu(gs: list, steps: int) -> list:
+    """The bf16 bits of O for several matrices stepped through one plan."""
     from kaon_amd import AdaMuon
     from kaon_amd import _lib as L
 
-    p = torch.nn.Parameter(torch.zeros(g.shape, dtype=torch.bfloat16, device="cuda"))
-    p.grad = torch.from_numpy(g).to("cuda", torch.bfloat16)
-    opt = AdaMuon([p], betas=(0.0, 0.999), ns_steps=steps)
+    params = []
+    for g in gs:
+        p = torch.nn.Parameter(torch.zeros(g.shape, dtype=torch.bfloat16, device="cuda"))
+        p.grad = torch.from_numpy(g).to("cuda", torch.bfloat16)
+        params.append(p)
+    opt = AdaMuon(params, betas=(0.0, 0.999), ns_steps=steps)
     group = opt.param_groups[0]
-    opt._init_state(p, opt.state[p], group)
-    plan = opt._plan((0, 1, 1, 2), group, [p], L.MOM_NONE, {id(p): 0}, L.OPT_ADAMUON)
+    for p in params:
+        opt._init_state(p, opt.state[p], group)
+    plan = opt._plan((0, 1, 1, 2), group, params, L.MOM_NONE, {id(p): i for i, p in enumerate(params)},
+                     L.OPT_ADAMUON)
     hp = opt._hyper(group, L.BF16, L.BF16)
     s = torch.cuda.current_stream().cuda_stream
     L.check(L.lib().kaon_adamuon_phases(ctypes.byref(plan.launch), ctypes.byref(hp), (1 << 8) | (1 << 9), s),
             "kaon_adamuon_phases")
     torch.cuda.synchronize()
-    d = plan.descs[0]
     ws16 = plan.workspace.view(torch.int16)
-    return ws16[2 * d.ws_aux: 2 * d.ws_aux + g.size].cpu().numpy().view(np.uint16).copy()
+    out = []
+    for i, g in enumerate(gs):
+        d = plan.descs[i]
+        out.append(ws16[2 * d.ws_aux: 2 * d.ws_aux + g.size].cpu().numpy().view(np.uint16).copy())
+    return out
+
+
+def test_newton_schulz_of_a_mixed_plan_equals_each_matrix_alone():
+    """Matrices of every tile path in one plan (big and small tiles, transposed, padded 640 -> 768,
+    a diagonal-heavy square, enough tiles for the per-XCD lists to interleave tensors and pad with
+    idle items): each O is bit for bit the O of that matrix planned alone.  A tile's products do
+    not depend on where the planner puts it, so any mix-up of tensors, tiles or idle items shows."""
+    print("[gpu] newton-schulz mixed plan", flush=True)
+    shapes = [(512, 1024), (1024, 512), (640, 700), (77, 33), (1280, 1280), (130, 300), (768, 1280),
+              (5120, 640), (96, 64)]
+    rng = np.random.default_rng(11)
+    gs = [O.bf16_to_f32(O.f32_to_bf16((rng.standard_normal(s) * 1e-3).astype(np.float32))) for s in shapes]
+    together = _ns_bits_many_on_gpu(gs, 2)
+    for s, g, o in zip(shapes, gs, together):
+        alone = _ns_bits_on_gpu(g, 2)
+        assert np.array_equal(o, alone), (s, int((o != alone).sum()))
 
 
 @pytest.mark.parametrize("shape", [(77, 33), (96, 64), (512, 1024), (1024, 512), (640, 700)])

@@ -9,20 +9,15 @@ State keys, dtypes and shapes are the reference's (K-Optimizers "kaon"
 from __future__ import annotations
 
 import ctypes
-import operator
 from typing import Any, Iterable
 
 import torch
 
 from . import _engine as E
+from . import _keys as K
 from . import _lib as L
 
 _FOURBIT_BLOCK = 128          # src/kaon/_momentum_codec.py:59
-# per-tensor accessors mapped over a param group each step (C-level map, no Python loop)
-_DP = torch.Tensor.data_ptr
-_CONTIG = torch.Tensor.is_contiguous
-_GRAD = operator.attrgetter("grad")
-_DTYPE = operator.attrgetter("dtype")
 FOREACH_BATCH_CUTOFF = 2_000_000  # src/kaon/_backend.py:53 (accepted for API compatibility)
 
 
@@ -145,24 +140,23 @@ class KaonOptimizer(torch.optim.Optimizer):
         if hasattr(self, "_plans"):  # tensor ids (the SR counter field) shift
             self._invalidate()
 
-    def _group_key(self, group: dict[str, Any], params: list[torch.Tensor]) -> tuple:
-        """What a group's launches depend on: state version, codec settings, and the
-        param and grad pointers (grad dtype and contiguity included)."""
-        grads = list(map(_GRAD, params))
-        return (self._state_version, group["momentum_dtype"], group["bf16_method"], group["betas"][0] > 0,
-                tuple(map(_DP, params)), tuple(map(_DP, grads)), tuple(map(_DTYPE, grads)),
-                tuple(map(_CONTIG, grads)))
+    @staticmethod
+    def _stepped(group: dict[str, Any]) -> tuple[list[torch.Tensor], bytes]:
+        """The group's params that have a gradient, and the pointer key of them and
+        their grads (param and grad storage, grad dtype, contiguity and layout)."""
+        return K.group_key(group["params"])
 
-    def _launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor]) -> list:
+    def _group_key(self, group: dict[str, Any], pkey: bytes) -> tuple:
+        """What a group's launches depend on: state version, codec settings, and the
+        pointer key of ``_stepped``."""
+        return (self._state_version, group["momentum_dtype"], group["bf16_method"], group["betas"][0] > 0, pkey)
+
+    def _launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor], pkey: bytes) -> list:
         """The group's launches (plan, p dtype, g dtype, device, ...), reused while
         ``_group_key`` is unchanged; otherwise checks the params, creates missing state
         and plans again (``_build_launches``).  The stream is looked up per step."""
-        try:
-            key = self._group_key(group, params)
-        except RuntimeError:  # e.g. a sparse grad: the checks below raise the proper error
-            key = None
         hit = self._launch_cache.get(gid)
-        if key is not None and hit is not None and hit[0] == key:
+        if hit is not None and hit[0] == self._group_key(group, pkey):
             return hit[1]
         self._check_params(params)
         for p in params:
@@ -171,7 +165,7 @@ class KaonOptimizer(torch.optim.Optimizer):
                 self._init_state(p, state, group)
                 self._state_version += 1
         out = self._build_launches(gid, group, params, self._tensor_ids())
-        self._launch_cache[gid] = (self._group_key(group, params), out)
+        self._launch_cache[gid] = (self._group_key(group, pkey), out)
         return out
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

@@ -138,10 +138,10 @@ class AdaMuon(KaonOptimizer):
         self._t += 1
         lib = L.lib()
         for gid, group in enumerate(self.param_groups):
-            params = [p for p in group["params"] if p.grad is not None]
+            params, pkey = self._stepped(group)
             if not params:
                 continue
-            for fn, plan, pdt, gdt, dev in self._launches(gid, group, params):
+            for fn, plan, pdt, gdt, dev in self._launches(gid, group, params, pkey):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(getattr(lib, fn)(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)), fn)
                 self._gc_writeback(group, plan, hp, dev)

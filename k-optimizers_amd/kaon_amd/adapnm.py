@@ -189,8 +189,8 @@ class AdaPNM(KaonOptimizer):
                 loss = closure()
         lib = L.lib()
         for gid, group in enumerate(self.param_groups):
-            params = [p for p in group["params"] if p.grad is not None]
-            launches = self._launches(gid, group, params) if params else []
+            params, pkey = self._stepped(group)
+            launches = self._launches(gid, group, params, pkey) if params else []
             group["step"] += 1
             for plan, pdt, gdt, dev in launches:
                 hp = self._hyper(group, pdt, gdt)

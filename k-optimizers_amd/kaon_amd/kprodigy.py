@@ -240,8 +240,8 @@ class KProdigy(KaonOptimizer):
             if group["lr"] not in (lr, 0.0):
                 raise RuntimeError("KProdigy: groups sharing one D estimate must use the same lr "
                                    "(or 0 for a frozen group). Use independent_d=True for per-group lr.")
-            params = [p for p in group["params"] if p.grad is not None]
-            launches = self._launches(gid, group, params) if params else []
+            params, pkey = self._stepped(group)
+            launches = self._launches(gid, group, params, pkey) if params else []
             per_group.append((group, params, launches))
             for plan, pdt, gdt, dev, positions, stat_idx in launches:
                 hp = self._hyper(group, pdt, gdt, c)

@@ -102,10 +102,10 @@ class Lion(KaonOptimizer):
         self._t += 1
         lib = L.lib()
         for gid, group in enumerate(self.param_groups):
-            params = [p for p in group["params"] if p.grad is not None]
+            params, pkey = self._stepped(group)
             if not params:
                 continue
-            for plan, pdt, gdt, dev in self._launches(gid, group, params):
+            for plan, pdt, gdt, dev in self._launches(gid, group, params, pkey):
                 hp = self._hyper(group, pdt, gdt)
                 L.check(lib.kaon_lion_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_lion_step")

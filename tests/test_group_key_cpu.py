@@ -1,0 +1,65 @@
+"""The launch-cache key of a parameter group (kaon_amd._keys, native helper
+_kaon_key): which params a step takes, and a key that changes whenever a cached
+plan would no longer describe them.  CPU tensors: the helper reads only host
+metadata (storage pointers, dtype, layout)."""
+import torch
+
+from kaon_amd import _keys as K
+
+
+def _params(n=12, shape=(8, 16)):
+    ps = [torch.nn.Parameter(torch.zeros(shape)) for _ in range(n)]
+    for i, p in enumerate(ps):
+        if i % 5 != 3:
+            p.grad = torch.randn(shape)
+    return ps
+
+
+def test_kept_params_are_those_with_a_grad_in_order():
+    ps = _params()
+    kept, key = K.group_key(ps)
+    assert kept == [p for p in ps if p.grad is not None]
+    assert all(a is b for a, b in zip(kept, [p for p in ps if p.grad is not None]))
+    assert len(key) == 19 * len(kept)
+    assert K.group_key([]) == ([], b"")
+
+
+def test_key_is_stable_while_nothing_changes():
+    ps = _params()
+    _, k0 = K.group_key(ps)
+    for p in ps:
+        if p.grad is not None:
+            p.grad.mul_(2.0)  # values change, storage does not
+    assert K.group_key(ps)[1] == k0
+
+
+def test_key_changes_with_everything_a_plan_depends_on():
+    ps = _params()
+    base = K.group_key(ps)[1]
+    i = 0
+
+    def changed(mutate):
+        q = _params()
+        for a, b in zip(q, ps):
+            a.data = b.data
+            a.grad = b.grad
+        mutate(q)
+        return K.group_key(q)[1] != base
+
+    assert changed(lambda q: setattr(q[i], "grad", q[i].grad.clone()))                  # new grad storage
+    assert changed(lambda q: (setattr(q[i], "grad_dtype", None),                         # grad dtype
+                              setattr(q[i], "grad", q[i].grad.to(torch.bfloat16))))
+    assert changed(lambda q: setattr(q[i], "grad", torch.randn(16, 8).t()))             # grad not contiguous
+    assert changed(lambda q: setattr(q[i], "data", q[i].data.clone()))                  # param storage
+    assert changed(lambda q: setattr(q[3], "grad", torch.randn(8, 16)))                 # a param gains a grad
+    assert changed(lambda q: setattr(q[i], "grad", None))                               # a param loses it
+    sp = torch.randn(8, 16).to_sparse()
+    assert changed(lambda q: setattr(q[i], "grad", sp))                                 # a sparse grad
+
+
+def test_non_tensors_are_refused():
+    try:
+        K.group_key([object()])
+    except TypeError:
+        return
+    raise AssertionError("expected a TypeError")

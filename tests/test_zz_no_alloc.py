@@ -49,8 +49,8 @@ def _step_noalloc(opt):
     fn = _noalloc_fn()
     opt._t += 1
     for gid, group in enumerate(opt.param_groups):
-        params = [p for p in group["params"] if p.grad is not None]
-        for plan, pdt, gdt, dev in opt._launches(gid, group, params):
+        params, pkey = opt._stepped(group)
+        for plan, pdt, gdt, dev in opt._launches(gid, group, params, pkey):
             hp = opt._hyper(group, pdt, gdt, None, gid)
             rc = fn(ctypes.byref(plan.launch), ctypes.byref(hp), int(plan.info.ws_words), E.stream_handle(dev))
             L.check(rc, "kaon_adakaon_step_noalloc")

@@ -453,9 +453,12 @@ __device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64
   }
 }
 
-// q = (G - mu)^2 (+ eps1 with EPS) of one chunk, G - mu rounded to bf16 (GC
-// in the grad dtype)
-template <bool EPS>
+// q = (G - mu)^2 (+ eps1) of one chunk, G - mu rounded to bf16 (GC in the
+// grad dtype).  EPS 0: no eps1; 2: x*x + eps1 rounded twice; 1: the same as
+// one fused multiply-add, which gives the same bits for every bf16-valued x
+// when eps1 is 0 or at least 2^-100: x*x is exact unless |x| < 2^-67, and
+// then x*x < 2^-134 lies below half an ulp of eps1, so both forms give eps1.
+template <int EPS>
 __device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e1, float q[8]) {
   float x[8];
   unpack8(v, x);
@@ -469,7 +472,7 @@ __device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = EPS ? x[i] * x[i] + e1 : x[i] * x[i];
+  for (int i = 0; i < 8; ++i) q[i] = EPS == 1 ? __fmaf_rn(x[i], x[i], e1) : EPS == 2 ? x[i] * x[i] + e1 : x[i] * x[i];
 }
 
 // Column partial of a slice, segment by segment: segment k is chunk k of
@@ -515,7 +518,7 @@ __device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0
   *dst = ku2{__float_as_uint(a0), __float_as_uint(a1)};
 }
 
-template <int CPL, int RW, bool EPS>
+template <int CPL, int RW, int EPS>
 __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
                                               const KaonHyper& hp, int mode, float (*seg)[4][512],
                                               KAON_G float* part, bool acc, bool last, float* racc) {
@@ -536,7 +539,9 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
   const void* gsrc = ws.src(T, hp.flags);
   ku4 raw[RW][CPL];
   load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, it.row0, C, nch, wr.lane, raw);
-  // GC means of the wave's rows
+  // GC means of the wave's rows; both per-row divisions by C are exact
+  // through the fp64 reciprocal (div_r64)
+  const double rc = rcp64((float)C);
   float mu[RW];
   KAON_G float* mu_arr = ws.mu(T);
 #pragma unroll
@@ -553,7 +558,7 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
         for (int i = 0; i < 8; ++i) a = a + x[i];
       }
     }
-    mu[j] = rbf(wave_csum(a) / (float)C);
+    mu[j] = rbf(div_r64(wave_csum(a), rc));
     if (wr.lane == 0) mu_arr[wr.rb + j] = mu[j];
   }
   if (mode == 1) return;
@@ -590,7 +595,7 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
     if (j >= nrows) continue;
     const float s2 = wave_csum(a2[j]);
     const float rv = lane_val(row_old, j);
-    if (wr.lane == 0) G(T.row)[wr.rb + j] = klerp(rv, s2 / (float)C, hp.w2);
+    if (wr.lane == 0) G(T.row)[wr.rb + j] = klerp(rv, div_r64(s2, rc), hp.w2);
   }
 }
 
@@ -700,7 +705,7 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
     case 24: if (CLS == 2) BODY<24, 1 X>(__VA_ARGS__); break;                                  \
   }
 
-template <int CLS, bool EPS>
+template <int CLS, int EPS>
 __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, const KaonItem* __restrict__ items,
                                              const Ws& ws, const KaonHyper& hp, int mode, float (*seg)[4][512],
                                              float* racc) {
@@ -721,10 +726,10 @@ __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, c
 }
 
 // Classes 0 and 1 are held to 4 waves per SIMD (128 VGPRs), which their
-// bodies fit without spilling, and keep the run partial in LDS (rows of at
-// most 2048 and 5120 elements); class 2 rows take more registers and
-// accumulate the run partial in the workspace.
-template <int CLS, bool EPS>
+// bodies fit without spilling; class 2 rows take more registers.  Every
+// class keeps its run partial in LDS (rows of at most 2048, 5120 and 12288
+// elements) and stores it once per run.
+template <int CLS, int EPS>
 __global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __restrict__ D,
                                                          const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                          int mode) {
@@ -732,12 +737,13 @@ __global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __res
   __shared__ __attribute__((aligned(16))) float racc[CLS == 0 ? 4 * 512 : 10 * 512];
   pf_stats_run<CLS, EPS>(D, items, ws, hp, mode, seg, racc);
 }
-template <bool EPS>
+template <int EPS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __restrict__ D,
                                                            const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                            int mode) {
   __shared__ __attribute__((aligned(16))) float seg[2][4][512];
-  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, nullptr);
+  __shared__ __attribute__((aligned(16))) float racc[24 * 512];
+  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, racc);
 }
 
 // One slice per workgroup: workgroup b takes slice b % KAON_RUN of run b / KAON_RUN.
@@ -2734,12 +2740,13 @@ using StatsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int)
 // holds one slice column partial
 constexpr int kClassMaxC[KAON_ROW_CLASSES] = {4 * 512, 10 * 512, 24 * 512, 4 * 512, 10 * 512, 24 * 512, kSeg};
 
+// eps: 0 none, 1 fused square (eps1 == 0 or >= 2^-100), 2 unfused (sq_chunk)
 template <int GT>
-StatsFn stats_fn_gt(int cls, bool eps) {
+StatsFn stats_fn_gt(int cls, int eps) {
   switch (cls) {
-    case 0: return eps ? k_pf_stats<0, true> : k_pf_stats<0, false>;
-    case 1: return eps ? k_pf_stats<1, true> : k_pf_stats<1, false>;
-    case 2: return eps ? k_pf_stats_wide<true> : k_pf_stats_wide<false>;
+    case 0: return eps == 1 ? k_pf_stats<0, 1> : eps == 2 ? k_pf_stats<0, 2> : k_pf_stats<0, 0>;
+    case 1: return eps == 1 ? k_pf_stats<1, 1> : eps == 2 ? k_pf_stats<1, 2> : k_pf_stats<1, 0>;
+    case 2: return eps == 1 ? k_pf_stats_wide<1> : eps == 2 ? k_pf_stats_wide<2> : k_pf_stats_wide<0>;
     case 3: return k_stats<GT, 4>;
     case 4: return k_stats<GT, 10>;
     case 5: return k_stats<GT, 24>;
@@ -2747,7 +2754,7 @@ StatsFn stats_fn_gt(int cls, bool eps) {
   }
   return nullptr;
 }
-StatsFn stats_fn(int gt, int cls, bool eps) {
+StatsFn stats_fn(int gt, int cls, int eps) {
   if (gt == KAON_F16) return cls >= 3 && cls != 5 ? stats_fn_gt<KAON_F16>(cls, eps) : nullptr;
   return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls, eps) : stats_fn_gt<KAON_F32>(cls, eps);
 }
@@ -2779,7 +2786,8 @@ int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipS
     const int32_t cnt = L.row_runs[cls];
     if (cnt <= 0) continue;
     if (cls < 3 && hp.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
-    StatsFn fn = stats_fn(hp.g_dtype, cls, (hp.flags & KAON_F_EPS) != 0);
+    const int eps = !(hp.flags & KAON_F_EPS) ? 0 : (hp.eps1 == 0.0f || hp.eps1 >= 0x1p-100f) ? 1 : 2;
+    StatsFn fn = stats_fn(hp.g_dtype, cls, eps);
     if (!fn) return fail("kaon: no row-statistics kernel for this grad dtype and row class");
     const size_t lds = (mode == 0 && cls >= 3) ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
     hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);

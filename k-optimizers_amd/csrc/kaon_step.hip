@@ -2698,7 +2698,7 @@ ElemFn elem_fn(int pt, int gt, int codec) {
   if (pt == KAON_BF16 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_BF16, KAON_F32>(codec);
   if (pt == KAON_F32 && gt == KAON_BF16) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_BF16>(codec);
   if (pt == KAON_F32 && gt == KAON_F32) return elem_by_codec<OPT, PHASE, KAON_F32, KAON_F32>(codec);
-  if constexpr (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)
+  if constexpr (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION || OPT == KAON_OPT_ADAMUON)
     if (pt == KAON_F16 && gt == KAON_F16) return elem_by_codec<OPT, PHASE, KAON_F16, KAON_F16>(codec);
   return nullptr;
 }
@@ -2894,8 +2894,8 @@ PdFn pd2_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-// half_ok: the entry point steps fp16 params (Adakaon, Lion and the gradient
-// write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
+// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon and the
+// gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
 // rides along (the reference's add_stochastic_ has no fp16 path,
 // _stochastic_rounding.py:55-68).
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool half_ok = false) {
@@ -2905,7 +2905,7 @@ int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool hal
   if (hp->g_dtype != KAON_F32 && hp->g_dtype != KAON_BF16 && hp->g_dtype != KAON_F16)
     return fail("kaon: bad g_dtype");
   if (hp->p_dtype == KAON_F16 || hp->g_dtype == KAON_F16) {
-    if (!half_ok) return fail((std::string(who) + ": fp16 params step in Adakaon and Lion plans only").c_str());
+    if (!half_ok) return fail((std::string(who) + ": fp16 params step in Adakaon, Lion and AdaMuon plans only").c_str());
     if (hp->p_dtype != KAON_F16 || hp->g_dtype != KAON_F16) return fail("kaon: fp16 params take fp16 grads");
     if (hp->flags & (KAON_F_NK_REMOVE | KAON_F_NK_CLIMB))
       return fail("kaon: the Nekaon / MSAM perturbation has no fp16 write (add_stochastic_ is bf16 / fp32 only)");
@@ -2965,7 +2965,7 @@ int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
 }
 
 int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
-  int rc = validate(L, hp, "kaon_adamuon_phases: null argument");
+  int rc = validate(L, hp, "kaon_adamuon_phases: null argument", true);
   if (rc) return rc;
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (L->n_ns_rect <= 0) return fail("kaon_adamuon: the launch was not planned for AdaMuon (no Newton-Schulz tiles)");
@@ -2983,7 +2983,9 @@ int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
       hipLaunchKernelGGL(k_muon_zero, dim3(L->n_tensors), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
       if ((rc = check_launch("kaon: AdaMuon zero launch"))) return rc;
     }
-    MuonMomFn fm = h.g_dtype == KAON_BF16 ? muon_mom_gt<KAON_BF16>(codec) : muon_mom_gt<KAON_F32>(codec);
+    MuonMomFn fm = h.g_dtype == KAON_BF16  ? muon_mom_gt<KAON_BF16>(codec)
+                   : h.g_dtype == KAON_F16 ? muon_mom_gt<KAON_F16>(codec)
+                                           : muon_mom_gt<KAON_F32>(codec);
     hipLaunchKernelGGL(fm, dim3(L->n_row_items), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
     hipLaunchKernelGGL(k_muon_norm, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws);
     if ((rc = check_launch("kaon: AdaMuon momentum launch"))) return rc;

@@ -33,6 +33,7 @@ _UPDATE_RMS = 0.2  # adamuon.py:88
 class AdaMuon(KaonOptimizer):
     _OPT = L.OPT_ADAMUON
     _NAME = "AdaMuon"
+    _HALF = True  # fp16 params with fp16 grads: RN / kahan writes (subtract_one_, _backend.py:82-98)
 
     def __init__(
         self,

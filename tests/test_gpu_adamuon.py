@@ -62,6 +62,47 @@ def test_adamuon_golden_case(name):
                 assert np.abs(x - y).max() <= 2e-2 * np.abs(y).max() + 1e-30, (name, i, k)
 
 
+# fp16 params and grads (the reference's per-param path: the momentum of
+# grad.float(), subtract_one_ in the param dtype, RN under "stochastic_rounding"
+# since the SR write is bf16-only, src/kaon/adamuon.py:565-615,
+# src/kaon/_backend.py:82-98).  No reference fixture holds fp16 AdaMuon; the
+# oracle's fp16 reads and writes are the ones its fp16 Adakaon goldens pin.
+F16_CASES = {
+    "adamuon_f16_int8_rn": dict(CASES["adamuon_int8_sr"], p_dtype="f16", g_dtype="f16"),
+    "adamuon_f16_bf16_kahan": dict(CASES["adamuon_bf16_rn"], p_dtype="f16", g_dtype="f16",
+                                   kwargs=dict(CASES["adamuon_bf16_rn"]["kwargs"], bf16_method="kahan")),
+    "adamuon_f16_4bit_none": dict(CASES["adamuon_int8_sr"], p_dtype="f16", g_dtype="f16",
+                                  kwargs=dict(CASES["adamuon_int8_sr"]["kwargs"], momentum_dtype="4bit",
+                                              bf16_method="none", weight_decay=0.01)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(F16_CASES))
+def test_adamuon_fp16_params_match_oracle(name):
+    case = F16_CASES[name]
+    print(f"[gpu] adamuon fp16 case {name}", flush=True)
+    oparams, _, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case)
+    for i, (op, p) in enumerate(zip(oparams, params)):
+        assert p.dtype == torch.float16
+        st = _state(opt, p)
+        for k in ("m", "m_scale"):
+            if k in op.state:
+                gv = to_bits(st[k]).reshape(-1)
+                ov = np.asarray(op.state[k]).reshape(-1)
+                if gv.dtype != ov.dtype:
+                    gv = gv.view(ov.dtype) if gv.itemsize == ov.itemsize else gv.astype(ov.dtype)
+                assert int((gv != ov).sum()) == 0, (name, i, k)
+        if p.ndim < 2:
+            assert np.array_equal(to_bits(p).reshape(-1), op.p.reshape(-1)), (name, i, "1-D weights")
+            if "shift" in op.state:
+                assert np.array_equal(to_bits(st["shift"]).reshape(-1), np.asarray(op.state["shift"]).reshape(-1))
+        else:
+            a = O.values(to_bits(p).reshape(op.p.shape), op.p_dtype)
+            b = O.values(op.p, op.p_dtype)
+            assert np.allclose(a, b, rtol=2e-2, atol=2e-3), (name, i, np.abs(a - b).max())
+
+
 def _ns_on_gpu(g: np.ndarray, steps: int) -> np.ndarray:
     """O of one matrix through the phases API (momentum pass with beta1 = 0, so
     M = g; then Newton-Schulz); read back from the plan's workspace."""

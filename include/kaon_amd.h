@@ -39,8 +39,8 @@ extern "C" {
 #define KAON_ABI_VERSION 7
 
 /* element types of params / grads (p.dtype, p.grad.dtype); fp16 params and
- * grads (both fp16) step in Adakaon, Lion and AdaMuon plans only, written by RN
- * or kahan */
+ * grads (both fp16) step in Adakaon, Lion, AdaMuon and AdaPNM plans only,
+ * written by RN or kahan */
 enum { KAON_F32 = 0, KAON_BF16 = 1, KAON_F16 = 2 };
 
 /* momentum storage ("momentum_dtype"), _momentum_codec.py:253-406 */

@@ -180,9 +180,9 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     return plan_fail("kaon_plan: unknown param dtype");
   if (g_dtype == KAON_F16 || args->p_dtype == KAON_F16) {
     // fp16 params (RN or kahan writes, _backend.py:82-98) with fp16 grads, on the
-    // generic kernels of Adakaon, Lion and AdaMuon
-    if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON)
-      return plan_fail("kaon_plan: fp16 params step in Adakaon, Lion and AdaMuon plans only");
+    // generic kernels of Adakaon, Lion, AdaMuon and AdaPNM
+    if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM)
+      return plan_fail("kaon_plan: fp16 params step in Adakaon, Lion, AdaMuon and AdaPNM plans only");
     if (g_dtype != KAON_F16 || args->p_dtype != KAON_F16) return plan_fail("kaon_plan: fp16 params take fp16 grads");
   }
   std::memset(info, 0, sizeof(*info));

@@ -1504,10 +1504,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
       ld_mom_at<CODEC>(mneg, e0, cnt, vec, nq);
       ld8<KAON_F32>(fsrc, j0, cnt, vec, f);
       if (PHASE == 6) {
-        if (PT == KAON_BF16) {
+        if (PT != KAON_F32) {
           ld8_bits(T.p, e0, cnt, vec, pb);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+          for (int i = 0; i < 8; ++i) p[i] = lp2f<PT>(pb[i]);
         } else {
           ld8<KAON_F32>(T.p, e0, cnt, vec, p);
         }
@@ -1620,7 +1620,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
           qout[i] = __float_as_uint(mfv);
         }
         dout[i] = cautious ? div_r64(d * (kp ? 1.0f : 0.0f), rden) : d;
-        if (wd) p[i] = lowp ? rbf(p[i] * hp.wdl) : p[i] * hp.wdl;
+        // p.data.mul_(1 - lr*wd) in the param dtype (adapnm.py:1227-1228)
+        if (wd) p[i] = round_to<PT>(p[i] * hp.wdl);
       }
       if (PHASE != 6) continue;
       // ---------------- phase 6 writes
@@ -1637,16 +1638,18 @@ __global__ __launch_bounds__(KAON_WG) void k_pnm(const KaonTensor* __restrict__ 
           ld8_bits(T.shift, e0, cnt, vec, sh);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            // kahan in the param dtype (_backend.py:90-94)
+            const float s = round_to<PT>(lp2f<PT>(sh[i]) - round_to<PT>(dout[i]));
             const float p0 = p[i];
-            const float p1 = rbf(p0 + s);
-            o[i] = f2bf(p1);
-            sh[i] = f2bf(s + rbf(p0 - p1));
+            const float p1 = round_to<PT>(p0 + s);
+            o[i] = f2lp<PT>(p1);
+            sh[i] = f2lp<PT>(s + round_to<PT>(p0 - p1));
           }
           st8_bits(T.shift, e0, cnt, vec, sh);
-        } else if (hp.bf16_method == KAON_RN) {
+        } else if (hp.bf16_method == KAON_RN || PT == KAON_F16) {
+          // fp16 params take RN under "stochastic_rounding" too (_backend.py:95-98)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+          for (int i = 0; i < 8; ++i) o[i] = f2lp<PT>(p[i] - round_to<PT>(dout[i]));
         } else {
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz[i]);
@@ -2844,6 +2847,7 @@ PnmFn pnm_fn(int pt, int gt, int codec) {
   if (pt == KAON_BF16 && gt == KAON_F32) return pnm_by_codec<PHASE, KAON_BF16, KAON_F32>(codec);
   if (pt == KAON_F32 && gt == KAON_BF16) return pnm_by_codec<PHASE, KAON_F32, KAON_BF16>(codec);
   if (pt == KAON_F32 && gt == KAON_F32) return pnm_by_codec<PHASE, KAON_F32, KAON_F32>(codec);
+  if (pt == KAON_F16 && gt == KAON_F16) return pnm_by_codec<PHASE, KAON_F16, KAON_F16>(codec);
   return nullptr;
 }
 
@@ -2894,8 +2898,8 @@ PdFn pd2_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon and the
-// gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
+// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon, AdaPNM
+// and the gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
 // rides along (the reference's add_stochastic_ has no fp16 path,
 // _stochastic_rounding.py:55-68).
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool half_ok = false) {
@@ -2905,7 +2909,8 @@ int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool hal
   if (hp->g_dtype != KAON_F32 && hp->g_dtype != KAON_BF16 && hp->g_dtype != KAON_F16)
     return fail("kaon: bad g_dtype");
   if (hp->p_dtype == KAON_F16 || hp->g_dtype == KAON_F16) {
-    if (!half_ok) return fail((std::string(who) + ": fp16 params step in Adakaon, Lion and AdaMuon plans only").c_str());
+    if (!half_ok)
+      return fail((std::string(who) + ": fp16 params step in Adakaon, Lion, AdaMuon and AdaPNM plans only").c_str());
     if (hp->p_dtype != KAON_F16 || hp->g_dtype != KAON_F16) return fail("kaon: fp16 params take fp16 grads");
     if (hp->flags & (KAON_F_NK_REMOVE | KAON_F_NK_CLIMB))
       return fail("kaon: the Nekaon / MSAM perturbation has no fp16 write (add_stochastic_ is bf16 / fp32 only)");
@@ -3029,7 +3034,7 @@ int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
 }
 
 int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
-  int rc = validate(L, hp, "kaon_adapnm_phases: null argument");
+  int rc = validate(L, hp, "kaon_adapnm_phases: null argument", true);
   if (rc) return rc;
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (hp->codec == KAON_MOM_NONE) return fail("kaon_adapnm_step: AdaPNM keeps two momentum buffers; pass their codec");

@@ -183,7 +183,7 @@ class KaonOptimizer(torch.optim.Optimizer):
             if p.dtype == torch.float16 or p.grad.dtype == torch.float16:
                 if not self._HALF:
                     raise NotImplementedError(
-                        f"kaon_amd: {self._NAME} does not step float16 params in this build (Adakaon, Lion and AdaMuon do)")
+                        f"kaon_amd: {self._NAME} does not step float16 params in this build (Adakaon, Lion, AdaMuon and AdaPNM do)")
                 if p.dtype != p.grad.dtype:
                     raise NotImplementedError("kaon_amd: float16 params take float16 grads")
             if p.grad.dtype != p.dtype and p.grad.dtype not in (torch.float32, torch.bfloat16):

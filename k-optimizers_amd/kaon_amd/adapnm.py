@@ -32,6 +32,7 @@ from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_mom
 class AdaPNM(KaonOptimizer):
     _OPT = L.OPT_ADAPNM
     _NAME = "AdaPNM"
+    _HALF = True  # fp16 params with fp16 grads: RN / kahan writes (subtract_one_, _backend.py:82-98)
 
     def __init__(
         self,

@@ -817,9 +817,10 @@ int ko_adapnm_tensor(const KoTensor* t, const KoHyper* h) {
     /* decoupled weight decay first, in the param dtype: p *= (1 - lr*wd) */
     if (h->wd != 0) {
         const float f = (float)(1.0 - h->lr * h->wd);
-        if (t->p_dtype == KO_BF16) {
+        if (t->p_dtype != KO_F32) { /* bf16 / fp16: the product rounded to the param dtype */
             uint16_t* p = (uint16_t*)t->p;
-            for (int64_t i = 0; i < n; ++i) p[i] = f_to_bf16(bf16_to_f(p[i]) * f);
+            const int dt = t->p_dtype;
+            for (int64_t i = 0; i < n; ++i) p[i] = f_to_lp(dt, lp_to_f(dt, p[i]) * f);
         } else {
             float* p = (float*)t->p;
             for (int64_t i = 0; i < n; ++i) p[i] = p[i] * f;

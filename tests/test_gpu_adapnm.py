@@ -76,6 +76,14 @@ EXTRA = {
     # rows of 5 to 10 chunks per lane (the prefetching clip-sum kernel's second row class)
     "class1_int8": _case([[96, 5120], [64, 320, 3, 3], [40, 2056]], dict(lr=1e-3, momentum_dtype="int8")),
     "class1_bf16": _case([[48, 4096], [32, 2880]], dict(lr=1e-3, momentum_dtype="bfloat16", weight_decay=0.01)),
+    # fp16 params and grads (the reference's native path: p.mul_(1 - lr*wd) and subtract_one_ in
+    # fp16, RN under "stochastic_rounding", src/kaon/adapnm.py:1222-1258, src/kaon/_backend.py:82-98)
+    "f16_int8_sr": _case([[40, 24], [16, 8, 3, 3], [56]], dict(lr=1e-3, momentum_dtype="int8", weight_decay=0.05),
+                         p="f16", g="f16"),
+    "f16_4bit_kahan": _case([[37, 45], [101]], dict(lr=1e-3, momentum_dtype="4bit", momentum_4bit_block=16,
+                                                    bf16_method="kahan", weight_decay=0.1), p="f16", g="f16"),
+    "f16_bf16_rn_ams": _case([[48, 40], [80]], dict(lr=2e-3, momentum_dtype="bfloat16", bf16_method="none",
+                                                    ams_bound=True), p="f16", g="f16"),
 }
 
 

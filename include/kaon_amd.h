@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 7
+#define KAON_ABI_VERSION 8
 
 /* element types of params / grads (p.dtype, p.grad.dtype); fp16 params and
  * grads (both fp16) step in Adakaon, Lion, AdaMuon and AdaPNM plans only,
@@ -217,6 +217,8 @@ typedef struct KaonLaunch {
   int32_t n_ns_sq, n_ns_rect;
   int32_t n_ns_sq_big, n_ns_rect_big;
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
+  int64_t ws_words;           /* KaonPlanInfo.ws_words of the plan that filled descs: the
+                                 workspace the descriptors' offsets address, in 4-byte words */
 } KaonLaunch;
 
 /* Per-launch hyper-parameters of one param group, rounded to fp32 on the
@@ -289,12 +291,14 @@ int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);
  * until the process ends (L->workspace is ignored).  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * ws_words is the plan's KaonPlanInfo.ws_words; a plan that needs more than
- * KAON_NOALLOC_WS_BYTES / 4 words is rejected with an error.  Allocates
- * nothing.  Every call on a device shares that device's array, so calls that
- * overlap on one device (two streams or two host threads) race; the device
- * the stream belongs to must be current. */
-int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* hp, int64_t ws_words, void* stream);
+ * The size checked is the launch's own L->ws_words (the plan's
+ * KaonPlanInfo.ws_words): a launch that needs more than
+ * KAON_NOALLOC_WS_BYTES / 4 words, or that carries no size, is rejected with
+ * an error before anything is enqueued.  Allocates nothing.  Every call on a
+ * device shares that device's array, so calls that overlap on one device (two
+ * streams or two host threads) race; the device the stream belongs to must be
+ * current. */
+int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* hp, void* stream);
 
 /* Lion step over one planned param group (lion.py:322-352, 416-485). */
 int kaon_lion_step(const KaonLaunch* L, const KaonHyper* hp, void* stream);

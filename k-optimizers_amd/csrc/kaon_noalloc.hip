@@ -69,12 +69,15 @@ int scratch_here(void** out) {
 
 }  // namespace
 
-extern "C" int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* hp, int64_t ws_words,
-                                         void* stream) {
+extern "C" int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   if (!L || !hp) return noalloc_fail("kaon_adakaon_step_noalloc: null argument");
   const int64_t cap = (int64_t)(KAON_NOALLOC_WS_BYTES / sizeof(float));
-  if (ws_words < 0 || ws_words > cap)
-    return noalloc_fail("kaon_adakaon_step_noalloc: the plan needs a workspace of " + std::to_string(ws_words) +
+  const int64_t need = L->ws_words;
+  if (L->n_tensors > 0 && need <= 0)
+    return noalloc_fail("kaon_adakaon_step_noalloc: the launch carries no workspace size (KaonLaunch.ws_words, "
+                        "the plan's KaonPlanInfo.ws_words)");
+  if (need > cap)
+    return noalloc_fail("kaon_adakaon_step_noalloc: the plan needs a workspace of " + std::to_string(need) +
                         " words; the static workspace holds " + std::to_string(cap) +
                         " (KAON_NOALLOC_WS_BYTES); step this group with kaon_adakaon_step");
   void* ws = nullptr;

@@ -162,6 +162,7 @@ class Plan:
         la.n_ns_sq, la.n_ns_rect = info.n_ns_sq, info.n_ns_rect
         la.n_ns_sq_big, la.n_ns_rect_big = info.n_ns_sq_big, info.n_ns_rect_big
         la.workspace = self.workspace.data_ptr()
+        la.ws_words = int(info.ws_words)
         self.launch = la
 
 

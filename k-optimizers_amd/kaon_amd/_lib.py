@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, BF16, F16 = 0, 1, 2
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -79,7 +79,8 @@ class KaonLaunch(ctypes.Structure):
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
-                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("workspace", ctypes.c_void_p)]
+                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("workspace", ctypes.c_void_p),
+                ("ws_words", ctypes.c_int64)]
 
 
 class KaonHyper(ctypes.Structure):
@@ -114,8 +115,7 @@ SIGNATURES = {
                    ctypes.POINTER(KaonPlanInfo)], ctypes.c_int),
     "kaon_adakaon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_gc_writeback": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
-    "kaon_adakaon_step_noalloc": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _I64, _VP],
-                                  ctypes.c_int),
+    "kaon_adakaon_step_noalloc": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_lion_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adamuon_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),
     "kaon_adapnm_step": ([ctypes.POINTER(KaonLaunch), ctypes.POINTER(KaonHyper), _VP], ctypes.c_int),

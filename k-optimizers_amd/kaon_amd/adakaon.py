@@ -5,13 +5,18 @@ Constructor, knobs, param-group keys and state layout follow the reference
 update (GC, factored second moment, RMS clip, momentum codec, decoupled WD,
 cautious masking, SR / RN / kahan / fp32 write) as one multi-tensor launch
 sequence per param group and dtype pair (``kaon_adakaon_step``).  The
-reference's ``foreach`` / ``fused`` / stacking knobs are accepted and have no
-effect: there is one path.
+reference's ``foreach`` / ``fused`` / stacking knobs are accepted; the weights
+and state come out of one path whatever they say (``fused`` decides only what
+``p.grad`` holds afterwards, below).
 
-Differences from the reference, by design:
-* gradients are read, never written: the reference's native path leaves
-  ``p.grad`` centralized (src/kaon/_backend.py:147-177); here GC happens in
-  registers;
+``p.grad`` after the step follows the reference's path: with GC on, the
+default (``fused=False``, the reference's native path, which centralizes
+``p.grad`` in place, src/kaon/_backend.py:147-177) stores the centralized
+gradient over ``p.grad`` from the apply kernel (``KAON_F_GC_WRITE``);
+``fused=True`` (the reference's fused path centralizes inside its kernels,
+adakaon.py:387-409) leaves ``p.grad`` as given.
+
+Difference from the reference, by design:
 * stochastic rounding draws Philox4x32-10 noise keyed by (``sr_seed``, step,
   param index, element) instead of ``torch.randint`` from the global RNG.
 """

@@ -442,3 +442,33 @@ def test_plan_limits_for_tensors_of_2_to_the_31_elements_and_more():
     assert b"2^31" in L.lib().kaon_last_error()
     assert _plan([(1 << 16, 1 << 16)])[0] != 0  # 2^32
     assert b"2^32" in L.lib().kaon_last_error()
+
+
+def check_noalloc_refuses_oversized_plans():
+    """kaon_adakaon_step_noalloc checks the launch's own workspace size (KaonLaunch.ws_words,
+    copied from the plan): a real plan larger than the static device array, or a launch
+    that carries no size, is refused before anything touches a device."""
+    L = _lib()
+    descs = (L.KaonTensor * 2)()
+    for i, (R, C) in enumerate(((262144, 2880), (640, 2880))):
+        d = descs[i]
+        d.R, d.C, d.factored, d.block4, d.tensor_id = R, C, 1, 128, i
+        d.g = d.p = d.m = d.m_scale = 0x1000 * (i + 1)
+    info = L.KaonPlanInfo()
+    args = L.KaonPlanArgs(L.OPT_ADAKAON, L.MOM_INT8, L.BF16, L.BF16, L.SR)
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, 2, None, None, None, None, None, None,
+                             ctypes.byref(info)) == 0
+    cap = (32 * 1024 * 1024) // 4
+    assert info.ws_words > cap
+    fn = L.lib().kaon_adakaon_step_noalloc
+    la, hp = L.KaonLaunch(), L.KaonHyper()
+    la.n_tensors, la.n_row_items, la.ws_words = 2, info.n_row_items, info.ws_words
+    assert fn(ctypes.byref(la), ctypes.byref(hp), None) != 0
+    assert b"static workspace" in L.lib().kaon_last_error()
+    la.ws_words = 0
+    assert fn(ctypes.byref(la), ctypes.byref(hp), None) != 0
+    assert b"no workspace size" in L.lib().kaon_last_error()
+
+
+def test_noalloc_refuses_oversized_plans_before_any_launch():
+    check_noalloc_refuses_oversized_plans()

@@ -28,10 +28,7 @@ def _need_gpu():
 def _noalloc_fn():
     from kaon_amd import _lib as L
 
-    fn = L.lib().kaon_adakaon_step_noalloc
-    fn.argtypes = [ctypes.POINTER(L.KaonLaunch), ctypes.POINTER(L.KaonHyper), ctypes.c_int64, ctypes.c_void_p]
-    fn.restype = ctypes.c_int
-    return fn
+    return L.lib().kaon_adakaon_step_noalloc
 
 
 def _bits(t):
@@ -52,7 +49,8 @@ def _step_noalloc(opt):
         params, pkey = opt._stepped(group)
         for plan, pdt, gdt, dev in opt._launches(gid, group, params, pkey):
             hp = opt._hyper(group, pdt, gdt, None, gid)
-            rc = fn(ctypes.byref(plan.launch), ctypes.byref(hp), int(plan.info.ws_words), E.stream_handle(dev))
+            assert plan.launch.ws_words == plan.info.ws_words
+            rc = fn(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev))
             L.check(rc, "kaon_adakaon_step_noalloc")
 
 
@@ -106,11 +104,8 @@ def test_noalloc_matches_step_two_calls_second_smaller():
 
 
 def test_noalloc_rejects_a_plan_beyond_the_static_workspace():
-    from kaon_amd import _lib as L
+    """The size checked is the launch's own: a real plan whose workspace exceeds the
+    static array is refused before any launch, and so is a launch with no size."""
+    import test_lib_cpu as C
 
-    fn = _noalloc_fn()
-    la, hp = L.KaonLaunch(), L.KaonHyper()
-    too_big = (32 * 1024 * 1024) // 4 + 1
-    rc = fn(ctypes.byref(la), ctypes.byref(hp), too_big, None)
-    assert rc != 0
-    assert b"static workspace" in L.lib().kaon_last_error()
+    C.check_noalloc_refuses_oversized_plans()

@@ -144,11 +144,18 @@ __device__ __forceinline__ float lane_val(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-// MSAM perturbation value: clamp(nan_to_num(x, 0, +b, -b), -b, b) (msam.py:222-230).
-// For a bound that is not NaN the clamp already takes +-inf to +-b, so only a
-// NaN x needs a case of its own.
-__device__ __forceinline__ float msam_e(float x, float bound) {
-  return x != x ? 0.0f : fminf(fmaxf(x, -bound), bound);
+// MSAM perturbation value (msam.py:216-230).  norm="none" (a finite bound b):
+// clamp(nan_to_num(x, 0, +b, -b), -b, b); for a bound that is not NaN the clamp
+// already takes +-inf to +-b, so only a NaN x needs a case of its own, and it
+// becomes 0.  norm="global" / "tensor" (bound +inf): the reference multiplies
+// the momentum by its scale with no sanitizing, so x passes as it is and a NaN
+// reaches the weights.  `nanfill` is msam_nanfill(bound), formed once per
+// launch: 0 for a finite bound, NaN for +inf.
+__device__ __forceinline__ float msam_nanfill(float bound) {
+  return bound == __builtin_inff() ? __builtin_nanf("") : 0.0f;
+}
+__device__ __forceinline__ float msam_e(float x, float bound, float nanfill) {
+  return x != x ? nanfill : fminf(fmaxf(x, -bound), bound);
 }
 
 // Flags of the specialized phase-5/6 kernels: bit 0 GC, 1 cautious, 2 weight

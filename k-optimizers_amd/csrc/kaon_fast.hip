@@ -341,8 +341,9 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   uint32_t mbits[8];
   if (MUON) unpack8(in.o, of);
   if (NKR && NEEDP) {
+    const float nf_old = msam_nanfill(hp.nk_bound_old);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xr[i] = p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old);
+    for (int i = 0; i < 8; ++i) xr[i] = p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old, nf_old);
     if (PHASE == 6) {
       unpack8(sr_chunk(xr, nz0), p);
     } else if (!LAZY) {
@@ -465,8 +466,9 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   if (NKC) {
     float y[8];
     unpack8(ov, y);
+    const float nf_new = msam_nanfill(hp.nk_bound_new);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = y[i] + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new);
+    for (int i = 0; i < 8; ++i) y[i] = y[i] + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new, nf_new);
     ov = sr_chunk(y, nz2);
   }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);

@@ -1052,6 +1052,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const bool mom = (hp.flags & KAON_F_MOMENTUM) != 0 && CODEC != KAON_MOM_NONE && (!MUON || (PHASE == 6 && QUANT_C));
   const bool nk_remove = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_REMOVE);
   const bool nk_climb = OPT == KAON_OPT_ADAKAON && mom && (hp.flags & KAON_F_NK_CLIMB);
+  const float nf_old = msam_nanfill(hp.nk_bound_old), nf_new = msam_nanfill(hp.nk_bound_new);
   constexpr bool QUANT = CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT;
   const bool quant = mom && QUANT;
   const bool lowp = PT == KAON_BF16;
@@ -1234,7 +1235,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
         }
         float pw = p[i];  // weight the inner step sees (after the Nekaon removal)
         if (nk_remove && need_p) {
-          const float ev = msam_e(mold * hp.nk_k, hp.nk_bound_old);
+          const float ev = msam_e(mold * hp.nk_k, hp.nk_bound_old, nf_old);
           pw = lowp ? bf2f(sr_bf16(p[i] + ev, nz0[i])) : p[i] + ev;
         }
         float d, mfv = 0.0f;
@@ -1346,7 +1347,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float x = p[i] - dout[i];
-          if (nk_climb) x = x + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new);
+          if (nk_climb) x = x + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new, nf_new);
           o[i] = x;
         }
         st8_f32(T.p, e0, cnt, vec, o);
@@ -1378,7 +1379,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
         if (nk_climb) {
 #pragma unroll
           for (int i = 0; i < 8; ++i)
-            o[i] = sr_bf16(bf2f(o[i]) + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new), nz2[i]);
+            o[i] = sr_bf16(bf2f(o[i]) + msam_e(mnew[i] * (-hp.nk_k), hp.nk_bound_new, nf_new), nz2[i]);
         }
         st8_bits(T.p, e0, cnt, vec, o);
       }
@@ -2519,6 +2520,7 @@ __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__
     factor = (1.0f / (nrm + bound)) * factor;
     bound = __builtin_inff();
   }
+  const float nanfill = msam_nanfill(bound);
   // tensors hold < 2^32 elements: unsigned 32-bit element and row arithmetic
   const uint32_t e_begin = (uint32_t)it.row0, e_end = (uint32_t)it.row0 + (uint32_t)it.nrows;
   const bool vecT = T.vec_flat != 0;
@@ -2566,7 +2568,7 @@ __global__ __launch_bounds__(KAON_WG) void k_msam(const KaonTensor* __restrict__
         else if (CODEC == KAON_MOM_BF16) mold = bf2f(mq[i]);
         else mold = __uint_as_float(mq[i]);
       }
-      ev[i] = msam_e(mold * factor, bound);
+      ev[i] = msam_e(mold * factor, bound, nanfill);
     }
     if (PT == KAON_F32) {
       float p[8];

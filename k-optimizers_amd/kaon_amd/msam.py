@@ -18,9 +18,10 @@ Over a plain :class:`Adakaon` the removal (and for ``norm="none"`` the climb)
 is folded into the Adakaon apply pass, as three stochastic roundings of one
 register value (SR noise streams 0, 1, 2); over any other kaon_amd optimizer
 with a momentum buffer they are separate ``kaon_msam_apply`` passes, as in the
-reference; ``norm="tensor"`` always takes those separate passes.  In the global
-and tensor norms a NaN momentum coordinate contributes no climb (the reference
-would carry the NaN into the weights).
+reference; ``norm="tensor"`` always takes those separate passes.  As in the
+reference, the global and tensor norms scale the momentum with no sanitizing
+(a NaN or inf coordinate reaches the weights; a tensor whose norm is NaN goes
+NaN whole), while ``norm="none"`` maps NaN to a zero climb and clamps +-inf.
 """
 from __future__ import annotations
 

@@ -565,17 +565,22 @@ static void write_add(const KoTensor* t, const float* e, const KoHyper* h, uint3
     }
 }
 
-/* MSAM norm="none" perturbation (msam.py:223-235):
- * e = clamp(nan_to_num(m * factor, 0, +b, -b), -b, b); p += e. */
+/* MSAM perturbation p += e (msam.py:216-235).  norm="none" (finite bound):
+ * e = clamp(nan_to_num(m * factor, 0, +b, -b), -b, b).  norm="global" /
+ * "tensor" (bound +inf): e = m * factor with no sanitizing (msam.py:216-222),
+ * so a NaN or inf coordinate reaches the weights. */
 static void msam_apply(const KoTensor* t, const KoHyper* h, float factor, float bound, uint32_t stream) {
     int64_t n = t->R * t->C;
     float* e = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
     mom_dequant(t, e);
+    const int raw = isinf(bound) && bound > 0;
     for (int64_t i = 0; i < n; ++i) {
         float x = e[i] * factor;
-        if (isnan(x)) x = 0.0f;
-        else if (isinf(x)) x = x > 0 ? bound : -bound;
-        x = fminf(fmaxf(x, -bound), bound);
+        if (!raw) {
+            if (isnan(x)) x = 0.0f;
+            else if (isinf(x)) x = x > 0 ? bound : -bound;
+            x = fminf(fmaxf(x, -bound), bound);
+        }
         e[i] = x;
     }
     write_add(t, e, h, stream);

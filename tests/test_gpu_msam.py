@@ -215,3 +215,45 @@ def test_dtype_matrix_matches_oracle():
         case = _case([[48, 40], [64]], dict(lr=1e-3, rho=0.3, momentum_dtype="int8"), p=p, g=g)
         print(f"[gpu] msam dtypes p={p} g={g}", flush=True)
         _check(case, f"p={p} g={g}")
+
+
+@pytest.mark.parametrize("norm", ["global", "tensor", "none"])
+@pytest.mark.parametrize("mom", ["bfloat16", "int8"])
+def test_nan_momentum_follows_the_reference(norm, mom):
+    """A NaN momentum coordinate (bf16) or row scale (int8) planted after two steps, then
+    eval() / train().  norm="global" and "tensor" multiply the momentum by their scale with
+    no sanitizing (msam.py:216-222): the global form carries the NaN coordinates into the
+    weights, the tensor form makes its own norm NaN and so the whole tensor; norm="none"
+    maps NaN to a zero climb (msam.py:223-230).  Weights must equal the oracle's bit for
+    bit after each swap (a NaN bf16 weight is torch's 0x7FC0 on both sides)."""
+    print(f"[gpu] msam NaN momentum norm={norm} mom={mom}", flush=True)
+    case = _case([[24, 32], [40]], dict(lr=1e-3, rho=0.3, norm=norm, momentum_dtype=mom), steps=2, seed=11)
+    case["eval_train"] = False
+    oparams, oopt, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case)
+    assert_same_as_oracle(case, oparams, params, opt, label=f"nan {norm} {mom} before")
+    st = opt.inner.state[params[0]]
+    if mom == "bfloat16":
+        st["m"].view(torch.int16).view(-1)[5] = 0x7FC0
+        oparams[0].state["m"].reshape(-1)[5] = 0x7FC0
+    else:
+        st["m_scale"].view(-1)[3] = float("nan")
+        oparams[0].state["m_scale"].reshape(-1)[3] = np.float32("nan")
+    for label, sign in (("eval", -1.0), ("train", +1.0)):
+        if sign < 0:
+            opt.eval()
+        else:
+            opt.train()
+        oopt.msam_apply(sign)
+        torch.cuda.synchronize()
+        for i, (op, p) in enumerate(zip(oparams, params)):
+            got, want = to_bits(p).reshape(-1), op.p.reshape(-1)
+            assert np.array_equal(got, want), (norm, mom, label, i, int((got != want).sum()))
+        w = O.bf16_to_f32(oparams[0].p.reshape(-1))
+        nan_w = int(np.isnan(w).sum())
+        if norm == "none":
+            assert nan_w == 0
+        elif norm == "tensor":
+            assert nan_w == w.size
+        else:
+            assert nan_w == (1 if mom == "bfloat16" else 32)

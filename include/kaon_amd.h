@@ -70,9 +70,15 @@ enum {
   KAON_F_PD_COUPLED = 1024, /* KProdigy pass 1: weight decay folded into the gradient
                                (decouple=False, kprodigy.py:342-349) */
   KAON_F_PD_STATS = 2048,   /* KProdigy pass 1: update s and the D statistics this step */
-  KAON_F_GC_WRITE = 4096    /* Adakaon / Lion apply and KProdigy pass 2: also store the
+  KAON_F_GC_WRITE = 4096,   /* Adakaon / Lion apply and KProdigy pass 2: also store the
                                centralized gradient over p.grad, as the reference's native
                                path leaves it (centralize_grads_, _backend.py:147-177) */
+  KAON_F_TORCH_ORDER = 8192 /* Adakaon / Lion steps and kaon_momentum_sumsq: the step's fp32
+                               sums in torch CPU's order instead of the canonical 64-lane one
+                               (below): the GC row means (_backend.py:147-177), the factored
+                               row / column means and the row factors' mean (_factored.py:48-52,
+                               76-82), the RMS clip norm (_backend.py:45-47), MSAM's per-tensor
+                               momentum norm (msam.py:219-221) */
 };
 
 /*
@@ -144,7 +150,18 @@ typedef struct KaonItem {
   int32_t kind;
 } KaonItem;
 
-/* Work decomposition and canonical reduction order shared with the CPU
+/* torch CPU's order (KAON_F_TORCH_ORDER), as torch 2.10 on x86-64 computes the
+ * reference's sums (aten/src/ATen/native/cpu/SumKernel.cpp, the norm kernel):
+ * a row's sum takes 8-float vectors, four side by side, in a cascade of four
+ * levels whose first takes 2^max(4, ceil(log2(rows))/4) rows of 32 floats, then
+ * the leftover vectors, the four slots, the scalar tail and the 8 lanes in
+ * order; a column's sum is the same cascade down the rows (blocks of 32
+ * columns; the rest of the columns four row slots apiece); ||U|| keeps 8 lanes,
+ * lane k a sequential fused multiply-add chain over elements k, k+8, ..., the
+ * lanes added in order, then the tail.  The chain has no parallel form, so the
+ * clip costs n/8 dependent fma per tensor in this mode.
+ *
+ * Work decomposition and canonical reduction order shared with the CPU
  * oracle.  Row sums: 64 lanes, lane l adds the 8-element chunks l, l+64, ...
  * in order, then an xor butterfly.  Column sums: wave groups of
  * RW = max(1, KAON_ROW_BUDGET / chunks-per-lane) consecutive rows (summed in

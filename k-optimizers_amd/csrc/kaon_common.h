@@ -128,6 +128,46 @@ __device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const
   }
 }
 
+// Phase 1 of a 1-D tensor (the whole tensor is one row), by the workgroup:
+// v = lerp(v, g*g (+eps1), 1-beta2) (adakaon.py:990-995); AdaPNM:
+// v = v*beta2 + (1-beta2)*g*g, mul_ then addcmul_ (one fma in torch), and the
+// running max under ams_bound (adapnm.py:1243-1248).  Elementwise: no sum.
+template <int GT>
+__device__ void stats_1d(const KaonTensor& T, const void* gsrc, const KaonHyper& hp) {
+  const int64_t C = T.C;
+  const int64_t nch = (C + 7) >> 3;
+  const bool vec = T.vec_rows != 0;
+  const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  const bool pnm = (hp.flags & KAON_F_PNM) != 0;
+  const bool ams = pnm && (hp.flags & KAON_F_AMS) != 0 && T.max_v;
+  for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
+    const int cnt = chunk_cnt(c, C);
+    const bool vv = vec && cnt == 8;
+    float x[8], v[8];
+    ld8<GT>(gsrc, c * 8, cnt, vv, x);
+    ld8<KAON_F32>(T.v, c * 8, cnt, vv, v);
+    if (pnm) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = __fmaf_rn(hp.a2 * x[i], x[i], v[i] * hp.b2);
+      if (ams) {
+        float mx[8];
+        ld8<KAON_F32>(T.max_v, c * 8, cnt, vv, mx);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], v[i]);
+        st8_f32(T.max_v, c * 8, cnt, vv, mx);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float q = x[i] * x[i];
+        if (eps) q = q + hp.eps1;
+        v[i] = klerp(v[i], q, hp.w2);
+      }
+    }
+    st8_f32(T.v, c * 8, cnt, vv, v);
+  }
+}
+
 __device__ __forceinline__ void unpack8(const ku4 v, float o[8]) {
   o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
   o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
@@ -162,6 +202,13 @@ __device__ __forceinline__ float msam_e(float x, float bound, float nanfill) {
 // decay, 3 Nekaon removal, 4 Nekaon climb, 5 the centralized gradient written
 // back over p.grad by the apply.
 enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16, FF_GCW = 32 };
+
+// Phases 1-4 of an Adakaon step (mode 0) or phase 1 of a Lion step (mode 1)
+// with the sums in torch CPU's order (KAON_F_TORCH_ORDER; kaon_torch.hip), for
+// the phase bits of `mask`; and kaon_momentum_sumsq's per-tensor sums in that
+// order.  Both return a HIP status.
+int torch_phases(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mask, int mode, hipStream_t st);
+int torch_momentum_sumsq(const KaonLaunch& L, Ws ws, int codec, hipStream_t st);
 
 // A phase-5/6 kernel over work items: (descriptors, items, workspace, hyper-parameters).
 using ElemFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);

@@ -87,38 +87,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
 
   if (!T.factored) {
-    // v = lerp(v, g*g (+eps1), 1-beta2) over the single row (adakaon.py:990-995);
-    // AdaPNM: v = v*beta2 + (1-beta2)*g*g, mul_ then addcmul_ (one fma in torch),
-    // and the running max under ams_bound (adapnm.py:1243-1248)
-    if (mode != 0) return;
-    const bool pnm = (hp.flags & KAON_F_PNM) != 0;
-    const bool ams = pnm && (hp.flags & KAON_F_AMS) != 0 && T.max_v;
-    for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
-      const int cnt = chunk_cnt(c, C);
-      const bool vv = vec && cnt == 8;
-      float x[8], v[8];
-      ld8<GT>(gsrc, c * 8, cnt, vv, x);
-      ld8<KAON_F32>(T.v, c * 8, cnt, vv, v);
-      if (pnm) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __fmaf_rn(hp.a2 * x[i], x[i], v[i] * hp.b2);
-        if (ams) {
-          float mx[8];
-          ld8<KAON_F32>(T.max_v, c * 8, cnt, vv, mx);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], v[i]);
-          st8_f32(T.max_v, c * 8, cnt, vv, mx);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float q = x[i] * x[i];
-          if (eps) q = q + hp.eps1;
-          v[i] = klerp(v[i], q, hp.w2);
-        }
-      }
-      st8_f32(T.v, c * 8, cnt, vv, v);
-    }
+    if (mode == 0) stats_1d<GT>(T, gsrc, hp);
     return;
   }
 
@@ -2943,19 +2912,26 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
   const int codec = mom ? h.codec : KAON_MOM_NONE;
   if (!mom) h.flags &= ~(KAON_F_MOMENTUM | KAON_F_NK_REMOVE | KAON_F_NK_CLIMB);
   h.codec = codec;
-  if (mask & (1u << 1)) {
-    if ((rc = launch_stats(*L, ws, h, 0, st))) return rc;
-  }
-  if ((mask & (1u << 2)) && L->n_fin_items > 0) {
-    hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
-    if ((rc = check_launch("kaon: k_fin launch"))) return rc;
-  }
-  if (mask & (1u << 3)) {
-    if ((rc = launch_ss(*L, ws, h, st))) return rc;
-  }
-  if (mask & (1u << 4)) {
-    hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, h);
-    if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
+  if (h.flags & KAON_F_TORCH_ORDER) {
+    // the GC / row / column / row-factor means and the clip norm in torch CPU's order
+    const int e = torch_phases(*L, ws, h, mask & 0x1Eu, 0, st);
+    if (e) return fail("kaon: torch-order sum launch", (hipError_t)e);
+  } else {
+    if (mask & (1u << 1)) {
+      if ((rc = launch_stats(*L, ws, h, 0, st))) return rc;
+    }
+    if ((mask & (1u << 2)) && L->n_fin_items > 0) {
+      hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
+      if ((rc = check_launch("kaon: k_fin launch"))) return rc;
+    }
+    if (mask & (1u << 3)) {
+      if ((rc = launch_ss(*L, ws, h, st))) return rc;
+    }
+    if (mask & (1u << 4)) {
+      hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws,
+                         h);
+      if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
+    }
   }
   const bool quant = codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT;
   if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {
@@ -2974,6 +2950,8 @@ int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
 int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
   int rc = validate(L, hp, "kaon_adamuon_phases: null argument", true);
   if (rc) return rc;
+  if (hp->flags & KAON_F_TORCH_ORDER)
+    return fail("kaon_adamuon_step: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (L->n_ns_rect <= 0) return fail("kaon_adamuon: the launch was not planned for AdaMuon (no Newton-Schulz tiles)");
   hipStream_t st = (hipStream_t)stream;
@@ -3038,6 +3016,8 @@ int kaon_adamuon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
 int kaon_adapnm_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, void* stream) {
   int rc = validate(L, hp, "kaon_adapnm_phases: null argument", true);
   if (rc) return rc;
+  if (hp->flags & KAON_F_TORCH_ORDER)
+    return fail("kaon_adapnm_step: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   if (hp->codec == KAON_MOM_NONE) return fail("kaon_adapnm_step: AdaPNM keeps two momentum buffers; pass their codec");
   hipStream_t st = (hipStream_t)stream;
@@ -3108,6 +3088,12 @@ int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
   if (L->n_tensors <= 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   Ws ws{(float*)L->workspace};
+  if (hp->flags & KAON_F_TORCH_ORDER) {
+    if (hp->codec == KAON_MOM_NONE) return fail("kaon_momentum_sumsq: needs a momentum codec");
+    const int e = torch_momentum_sumsq(*L, ws, hp->codec, st);
+    if (e) return fail("kaon: torch-order momentum sum launch", (hipError_t)e);
+    return 0;
+  }
   using MsqFn = void (*)(const KaonTensor*, const KaonItem*, Ws);
   MsqFn f = nullptr;
   switch (hp->codec) {
@@ -3132,6 +3118,8 @@ int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
 int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   int rc = validate(L, hp, "kaon_kprodigy_pass1: null argument");
   if (rc) return rc;
+  if (hp->flags & KAON_F_TORCH_ORDER)
+    return fail("kaon_kprodigy_pass1: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");
   if (L->n_tensors <= 0 || L->n_row_items <= 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   Ws ws{(float*)L->workspace};
@@ -3165,6 +3153,8 @@ int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
 int kaon_kprodigy_pass2(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
   int rc = validate(L, hp, "kaon_kprodigy_pass2: null argument");
   if (rc) return rc;
+  if (hp->flags & KAON_F_TORCH_ORDER)
+    return fail("kaon_kprodigy_pass2: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");
   if (L->n_tensors <= 0 || L->n_elem_items <= 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   Ws ws{(float*)L->workspace};
@@ -3193,7 +3183,10 @@ int kaon_lion_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask, vo
   h.flags |= KAON_F_MOMENTUM;
   h.flags &= ~(KAON_F_NK_REMOVE | KAON_F_NK_CLIMB);
   const bool quant = h.codec == KAON_MOM_INT8 || h.codec == KAON_MOM_4BIT;
-  if (mask & (1u << 1)) {
+  if ((mask & (1u << 1)) && (h.flags & KAON_F_TORCH_ORDER)) {
+    const int e = torch_phases(*L, ws, h, 1u << 1, 1, st);
+    if (e) return fail("kaon: torch-order GC mean launch", (hipError_t)e);
+  } else if (mask & (1u << 1)) {
     if ((rc = launch_stats(*L, ws, h, 1, st))) return rc;
   }
   if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {

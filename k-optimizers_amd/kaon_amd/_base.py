@@ -73,6 +73,19 @@ def load_state_dict_preserving_dtypes(optimizer: torch.optim.Optimizer, state_di
                 st[key] = v.detach().to(device=p.device, copy=True)
 
 
+REDUCTION_ORDERS = ("canonical", "torch")
+
+
+def validate_reduction_order(order: str) -> str:
+    """``reduction_order`` (no counterpart in the reference): "canonical" sums the step's
+    fp32 reductions in the library's fixed 64-lane order (the default; the faster form);
+    "torch" sums them in torch CPU's order (KAON_F_TORCH_ORDER), which reproduces the
+    reference's results bit for bit and costs the clip norm's n/8 sequential fma chains."""
+    if order not in REDUCTION_ORDERS:
+        raise ValueError(f"reduction_order must be 'canonical' or 'torch', got {order!r}")
+    return order
+
+
 def validate_common(lr: float, betas: tuple[float, float], momentum_dtype: str, bf16_method: str,
                     foreach_batch_cutoff: int, auto_lr: bool) -> tuple[float, float]:
     beta1, beta2 = float(betas[0]), float(betas[1])

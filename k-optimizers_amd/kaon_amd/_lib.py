@@ -23,6 +23,7 @@ OPT_ADAKAON, OPT_LION, OPT_ADAMUON, OPT_ADAPNM, OPT_KPRODIGY = 0, 1, 2, 3, 4
 
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB, F_SRC_O = 1, 2, 4, 8, 16, 32, 64, 128
 F_GC_WRITE = 4096
+F_TORCH_ORDER = 8192
 F_PNM, F_AMS, F_PD_COUPLED, F_PD_STATS = 256, 512, 1024, 2048
 
 ROW_BUDGET = 20

@@ -29,7 +29,8 @@ import torch
 
 from . import _engine as E
 from . import _lib as L
-from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common
+from ._base import (FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common,
+                    validate_reduction_order)
 
 
 class Adakaon(KaonOptimizer):
@@ -60,8 +61,10 @@ class Adakaon(KaonOptimizer):
         auto_lr_scale: float = 1.0,
         auto_lr_fuse_rel: float = 0.0,
         auto_lr_d0: float | None = None,
+        reduction_order: str = "canonical",
     ) -> None:
         beta1, beta2 = validate_common(lr, betas, momentum_dtype, bf16_method, foreach_batch_cutoff, auto_lr)
+        self.reduction_order = validate_reduction_order(reduction_order)
         if clip_threshold <= 0.0:
             raise ValueError(f"clip_threshold must be > 0, got {clip_threshold}")
         defaults = {
@@ -126,6 +129,8 @@ class Adakaon(KaonOptimizer):
         mom = beta1 > 0
         if mom:
             flags |= L.F_MOMENTUM
+        if self.reduction_order == "torch":
+            flags |= L.F_TORCH_ORDER
         if nk is not None and mom:
             if nk["remove"] and gid in nk["bound_old"]:
                 flags |= L.F_NK_REMOVE

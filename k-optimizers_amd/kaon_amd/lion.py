@@ -15,7 +15,8 @@ import torch
 
 from . import _engine as E
 from . import _lib as L
-from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common
+from ._base import (FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common,
+                    validate_reduction_order)
 
 
 class Lion(KaonOptimizer):
@@ -42,8 +43,10 @@ class Lion(KaonOptimizer):
         auto_lr_scale: float = 1.0,
         auto_lr_fuse_rel: float = 0.0,
         auto_lr_d0: float | None = None,
+        reduction_order: str = "canonical",
     ) -> None:
         beta1, beta2 = validate_common(lr, betas, momentum_dtype, bf16_method, foreach_batch_cutoff, auto_lr)
+        self.reduction_order = validate_reduction_order(reduction_order)
         if weight_decay < 0.0:
             raise ValueError(f"weight_decay must be >= 0, got {weight_decay}")
         defaults = {
@@ -85,6 +88,8 @@ class Lion(KaonOptimizer):
             flags |= L.F_CAUTIOUS
         if wd != 0:
             flags |= L.F_WD
+        if self.reduction_order == "torch":
+            flags |= L.F_TORCH_ORDER
         h.flags = flags
         h.p_dtype, h.g_dtype = pdt, gdt
         h.codec = L.MOM_CODE[group["momentum_dtype"]]

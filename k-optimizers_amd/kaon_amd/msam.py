@@ -130,6 +130,8 @@ class MSAM(torch.optim.Optimizer):
         h.codec = L.MOM_CODE[self.param_groups[gid]["momentum_dtype"]]
         h.step = (self.inner._t if step is None else step) & 0xFFFFFFFF
         h.seed = self.inner.sr_seed
+        if getattr(self.inner, "reduction_order", "canonical") == "torch":
+            h.flags |= L.F_TORCH_ORDER  # the momentum norms' sums in torch CPU's order
         return h
 
     # ---------------------------------------------------------- perturbation

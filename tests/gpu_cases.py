@@ -21,7 +21,9 @@ def tdtype(name: str) -> torch.dtype:
     return {"bf16": torch.bfloat16, "f16": torch.float16}.get(name, torch.float32)
 
 
-def make_opt(case, params, group=None):
+def make_opt(case, params, group=None, extra=None):
+    """The kaon_amd optimizer of a case; ``extra`` adds constructor keywords (e.g.
+    reduction_order="torch")."""
     from kaon_amd import MSAM, AdaMuon, AdaPNM, Adakaon, KProdigy, Lion, Nekaon
 
     g = dict(group or group_for(case))
@@ -29,6 +31,7 @@ def make_opt(case, params, group=None):
     common = dict(momentum_dtype=g["momentum_dtype"], momentum_4bit_block=g["momentum_4bit_block"],
                   cautious=g["cautious"], gradient_centralization=g["gradient_centralization"],
                   bf16_method=g["bf16_method"])
+    common.update(extra or {})
     if name == "adakaon":
         opt = Adakaon(params, lr=g["lr"], betas=g["betas"], eps=g["eps"], weight_decay=g["weight_decay"],
                       clip_threshold=g["clip_threshold"], **common)
@@ -74,7 +77,7 @@ def to_bits(t: torch.Tensor) -> np.ndarray:
     return t.numpy().copy()
 
 
-def run_gpu(case, group=None, values=None):
+def run_gpu(case, group=None, values=None, extra=None):
     """Step the HIP optimizer on the case; returns (params, opt, eval-mode weights or None)."""
     pdt, gdt = tdtype(case["p_dtype"]), tdtype(case["g_dtype"])
     params = []
@@ -84,7 +87,7 @@ def run_gpu(case, group=None, values=None):
         if gdt != pdt:
             prm.grad_dtype = gdt   # torch >= 2.9 checks grad dtype against this attribute
         params.append(prm)
-    opt = make_opt(case, params, group)
+    opt = make_opt(case, params, group, extra)
     for step in range(1, case["steps"] + 1):
         idle = case.get("no_grad", {}).get(step, ())
         for i, p in enumerate(params):

@@ -472,3 +472,30 @@ def check_noalloc_refuses_oversized_plans():
 
 def test_noalloc_refuses_oversized_plans_before_any_launch():
     check_noalloc_refuses_oversized_plans()
+
+
+def test_other_optimizers_refuse_torch_order():
+    """The torch-order sums (KAON_F_TORCH_ORDER) are built for the Adakaon (Nekaon, MSAM)
+    and Lion steps; the entry points of the other optimizers refuse the flag on the host,
+    before any launch, rather than ignore it."""
+    L = _lib()
+    la, hp = L.KaonLaunch(), L.KaonHyper()
+    la.n_tensors, la.n_row_items = 1, 1
+    la.descs = la.workspace = 0x1000  # never dereferenced: the flag is refused first
+    hp.flags = L.F_TORCH_ORDER
+    hp.p_dtype = hp.g_dtype = L.BF16
+    hp.codec = L.MOM_INT8
+    for fn in ("kaon_adamuon_step", "kaon_adapnm_step", "kaon_kprodigy_pass1", "kaon_kprodigy_pass2"):
+        assert getattr(L.lib(), fn)(ctypes.byref(la), ctypes.byref(hp), None) != 0, fn
+        assert b"torch-order" in L.lib().kaon_last_error(), fn
+
+
+def test_reduction_order_knob():
+    from kaon_amd import Adakaon, Lion, Nekaon
+
+    p = torch.nn.Parameter(torch.zeros(4, 4))
+    assert Adakaon([p]).reduction_order == "canonical"
+    assert Lion([p], reduction_order="torch").reduction_order == "torch"
+    assert Nekaon([p], reduction_order="torch").inner.reduction_order == "torch"
+    with pytest.raises(ValueError):
+        Adakaon([p], reduction_order="cuda")

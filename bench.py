@@ -30,10 +30,17 @@ Besides the JSON line's ``value`` (Gparam/s) the line carries
   int8 m read, p and m written, 5:3);
 * ``lora_bag`` (default workload): ms per step of the launch-bound regime, the
   reference's LoRA proxy bag of 512 fp32 [8, 16] tensors;
-* ``cpu_baseline``: the CPU oracle (oracle/kaon_oracle.c) stepping the same
-  tensors on the host's cores (at most 16 threads), the median of three steps
-  after a warmup, the whole set when a step fits the time budget -- a reported
-  baseline, not the target.
+* ``torch_order`` (Adakaon / Lion workloads): the same step with
+  ``reduction_order="torch"``, whose fp32 sums follow torch CPU's order and so
+  give the reference's bits; ms per step and its phases;
+* ``cpu_baseline``: the reference's CPU path, its native foreach step restated
+  in torch (oracle/torch_foreach.py, pinned bit for bit against the reference's
+  fixtures), on the job's host cores over a fixed sample of the set (every 8th
+  tensor by default, ``--cpu-stride 1`` for the whole set), the median of three
+  steps after a warmup; ``cpu_oracle_baseline`` beside it is the C oracle
+  (oracle/kaon_oracle.c) on the same host (at most 16 threads).  4-bit
+  workloads and the other optimizers report the C oracle as ``cpu_baseline``.
+  A reported baseline, not the target.
 """
 from __future__ import annotations
 
@@ -422,7 +429,7 @@ def cpu_baseline(params, name, budget_s: float) -> dict:
         # matrices with min(R, C) <= 640 (and the 1-D params)
         order = [i for i in order if params[i].ndim < 2 or min(params[i].shape[0],
                                                                params[i].numel() // params[i].shape[0]) <= 640]
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = min(_cpu_threads(), 16)
     oopt_name = "adakaon" if w["opt"] == "nekaon" else ("adakaon" if w["opt"] == "msam" else w["opt"])
 
     def build(i):
@@ -475,6 +482,94 @@ def cpu_baseline(params, name, budget_s: float) -> dict:
             "steps_s": [round(x, 3) for x in walls]}
 
 
+def torch_order_leg(params, name, steps: int = 5, warmup: int = 2) -> dict:
+    """The workload's step with reduction_order="torch" (the fp32 sums in torch CPU's order,
+    the reference's bits) on the same params and grads, a fresh optimizer: ms per step
+    (HIP events) and the phase kernels' times."""
+    import torch
+    from kaon_amd import Adakaon, Lion
+
+    w = WORKLOADS[name]
+    cls = Adakaon if w["opt"] == "adakaon" else Lion
+    opt = cls(params, reduction_order="torch", **w["kw"])
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        opt.step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    nparam = sum(p.numel() for p in params)
+    br = phase_breakdown(opt, name)
+    del opt
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "gparam_s": round(nparam / (ms * 1e-3) / 1e9, 2), "steps": steps,
+            "phases_ms": {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())},
+            "note": "reduction_order='torch': GC / row / column / row-factor means as torch CPU's cascades and "
+                    "the clip norm as its 8 sequential fma chains per tensor (phase 3 writes the divisor)"}
+
+
+def _cpu_threads() -> int:
+    """The host's cores for the CPU baselines: the process's affinity set, capped by the
+    OMP_NUM_THREADS share the host gives the job when it sets one."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap))) if cap and cap.isdigit() else max(1, n)
+
+
+def cpu_torch_foreach(params, name, stride: int) -> dict:
+    """The reference's CPU path: oracle/torch_foreach.py, a torch-CPU restatement of its
+    native foreach step (GC batched by shape, the CPU stack budget min(64M, 4 * 2M),
+    shape buckets, per-param steps above 2M elements, torch.randint SR draws), pinned
+    bit for bit against the reference's fixtures by tests/test_torch_foreach_cpu.py.
+    Every ``stride``-th tensor of a fixed random order of the set (1 = the whole
+    set), its weights and grads copied to the host; one warmup step, then the median
+    of three timed steps on all the job's host cores."""
+    import statistics
+
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_foreach as TF
+
+    w = WORKLOADS[name]
+    kw = w["kw"]
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    order = [int(i) for i in np.random.default_rng(0).permutation(len(params))][::stride]
+    ps = [params[i].detach().cpu() for i in order]
+    gs = [params[i].grad.detach().cpu() for i in order]
+    nparam = sum(p.numel() for p in ps)
+    group = dict(lr=kw["lr"], betas=kw["betas"], eps=(1e-30, 1e-3), weight_decay=0.0, clip_threshold=1.0,
+                 momentum_dtype=kw["momentum_dtype"], cautious=True, gradient_centralization=True,
+                 bf16_method="stochastic_rounding")
+    cls = TF.ForeachAdakaon if w["opt"] == "adakaon" else TF.ForeachLion
+    opt = cls(ps, [g.clone() for g in gs], group)
+    t0 = time.perf_counter()
+    opt.step()
+    warm = time.perf_counter() - t0
+    walls = []
+    for _ in range(3):
+        opt.gs[:] = [g.clone() for g in gs]  # each step centralizes its grads in place, as the reference does
+        t0 = time.perf_counter()
+        opt.step()
+        walls.append(time.perf_counter() - t0)
+    med = statistics.median(walls)
+    what = "the whole set" if stride == 1 else f"every {stride}th tensor of a fixed random order of the set"
+    return {"value": round(nparam / med / 1e9, 4), "unit": "Gparam/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "ms_per_step": round(med * 1e3, 1),
+            "full_set_s_per_step_est": round(med * sum(p.numel() for p in params) / nparam, 2),
+            "sample": f"one {w['opt']} step (torch CPU, the reference's native foreach path restated in "
+                      f"oracle/torch_foreach.py) over {what}: {len(ps)} tensors, {nparam / 1e6:.1f}M params; "
+                      f"torch.set_num_threads({threads}); median of 3 steps after 1 warmup: {med:.2f} s/step "
+                      f"(warmup {warm:.1f} s)",
+            "steps_s": [round(x, 3) for x in walls]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -484,7 +579,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of one CPU-baseline step (the whole set is timed when it fits)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-stride", type=int, default=8,
+                    help="the torch-CPU baseline (Adakaon / Lion workloads) times every N-th tensor of a fixed "
+                         "order of the set; 1 = the whole set")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--no-torch-order", action="store_true",
+                    help="skip the reduction_order='torch' timing of Adakaon / Lion workloads")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -581,6 +681,8 @@ def main() -> int:
                                "avg_ms": round(br[dom], 4), "frac_of_apply_mix": round(ach / mix, 4),
                                "source": kernel_source_hash()}
         out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(br.items())}
+    if w["opt"] in ("adakaon", "lion") and not args.no_torch_order:
+        out["torch_order"] = torch_order_leg(params, args.workload)
     if args.workload == "adakaon_int8" and not args.no_breakdown:
         # the launch-bound regime beside the headline (reference: 0.24 ms for its fused Adakaon
         # on this bag, benchmarks/control/RANKINGS.md:83, on its own hardware)
@@ -588,7 +690,12 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         del opt
-        out["cpu_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)
+        if w["opt"] in ("adakaon", "lion") and w["kw"]["momentum_dtype"] != "4bit":
+            # the reference's own CPU path (torch foreach), and the C oracle beside it
+            out["cpu_baseline"] = cpu_torch_foreach(params, args.workload, args.cpu_stride)
+            out["cpu_oracle_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)
+        else:
+            out["cpu_baseline"] = cpu_baseline(params, args.workload, args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
 

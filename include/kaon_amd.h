@@ -108,7 +108,8 @@ typedef struct KaonTensor {
   int32_t pd_p0_scalar;   /* KProdigy: "p0" is the 0-dim zero (the initial slice had norm 0) */
   int32_t full_v;         /* KProdigy: per-element second moment "v" on a matrix (second_moment
                              "full"); 1-D KProdigy tensors always set it */
-  int32_t pd_pad;
+  int32_t by_size;        /* set by kaon_plan: descs[k].by_size is the tensor that per-tensor
+                             workgroup k takes, the tensors by decreasing numel (longest first) */
   const uint16_t* noise[3]; /* optional injected SR noise per stream (tests) */
   int64_t R, C;           /* matrixized shape */
   int64_t n;              /* R * C */

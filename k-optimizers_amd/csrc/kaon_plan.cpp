@@ -362,6 +362,13 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
   info->n_flat_items = (int32_t)flats.size();
   for (const RowIt& r : rows) info->row_runs[r.cls]++;
   info->ws_words = off > 0 ? off : 4;
+  // per-tensor launches (the torch-order clip norm) take the longest tensors first
+  {
+    std::vector<int32_t> ord(n);
+    for (int32_t i = 0; i < n; ++i) ord[i] = i;
+    std::stable_sort(ord.begin(), ord.end(), [&](int32_t a, int32_t b) { return descs[a].n > descs[b].n; });
+    for (int32_t k = 0; k < n; ++k) descs[k].by_size = ord[k];
+  }
   if (row_items)
     for (size_t k = 0; k < rows.size(); ++k) row_items[k] = rows[k].it;
   if (fin_items && !fins.empty()) std::memcpy(fin_items, fins.data(), fins.size() * sizeof(KaonItem));

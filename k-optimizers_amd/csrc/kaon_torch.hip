@@ -116,8 +116,10 @@ __device__ __forceinline__ float ldx(const void* base, int64_t j) {
 // =============================================================== phase 1
 // Runs (row items): the GC mean and the row EMA of every row in torch's order;
 // 1-D tensors: the elementwise v EMA.  The two halves of each wave take two
-// rows.  mode 1 (Lion): GC means only.
-template <int GT>
+// rows.  mode 1 (Lion): GC means only.  GC is a template parameter and eps1 is
+// added as eps1 or 0 (x*x >= +0, so adding +0 changes nothing): a term has no
+// branch, so a leaf's loads all issue before its adds.
+template <int GT, bool GC>
 __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                   int mode) {
@@ -129,9 +131,8 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
     if (mode == 0) stats_1d<GT>(T, gsrc, hp);
     return;
   }
-  const bool gc = (hp.flags & KAON_F_GC) != 0;
-  if (mode == 1 && !gc) return;
-  const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  if (mode == 1 && !GC) return;
+  const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = (int)(threadIdx.x & 63), half = lane >> 5, pos = lane & 31;
   const int64_t C = T.C, end = (int64_t)it.row0 + it.nrows;
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
     const int64_t r = own ? rb + half : end - 1;
     const int64_t off = r * C;
     float mu = 0.0f;
-    if (gc) {
+    if (GC) {
       const float s = tinner32(C, pos, [&](int64_t j) { return ldx<GT>(gsrc, off + j); });
       mu = round_to<GT>(s / (float)C);
       if (own && pos == 0) ws.mu(T)[r] = mu;
@@ -149,10 +150,8 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
     if (mode == 1) continue;
     const float s2 = tinner32(C, pos, [&](int64_t j) {
       float x = ldx<GT>(gsrc, off + j);
-      if (gc) x = round_to<GT>(x - mu);
-      float q = x * x;
-      if (eps) q = q + hp.eps1;
-      return q;
+      if (GC) x = round_to<GT>(x - mu);
+      return x * x + eadd;
     });
     if (own && pos == 0) G(T.row)[r] = klerp(G(T.row)[r], s2 / (float)C, hp.w2);
   }
@@ -167,7 +166,7 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
 // mean in torch's row order, rf = 1/sqrt(row / mean).
 constexpr int kTfinSub = 8;
 
-template <int GT>
+template <int GT, bool GC>
 __global__ __launch_bounds__(KAON_WG) void k_tfin(const KaonTensor* __restrict__ D,
                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   __shared__ float rm_s;
@@ -179,15 +178,12 @@ __global__ __launch_bounds__(KAON_WG) void k_tfin(const KaonTensor* __restrict__
     const int64_t j = (int64_t)it.row0 + (int64_t)sb * KAON_WG + threadIdx.x;
     if (j >= (int64_t)it.row0 + it.nrows) return;
     const void* gsrc = T.g;
-    const bool gc = (hp.flags & KAON_F_GC) != 0;
-    const bool eps = (hp.flags & KAON_F_EPS) != 0;
+    const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
     const KAON_G float* mu = ws.mu(T);
     auto q = [&](int64_t i) {
       float x = ldx<GT>(gsrc, i * C + j);
-      if (gc) x = round_to<GT>(x - mu[i]);
-      float v = x * x;
-      if (eps) v = v + hp.eps1;
-      return v;
+      if (GC) x = round_to<GT>(x - mu[i]);
+      return x * x + eadd;
     };
     const int64_t jd = C >= 8 ? (C / 32) * 32 : (C / 4) * 4;
     float cs;
@@ -223,126 +219,279 @@ __global__ __launch_bounds__(KAON_WG) void k_tfin(const KaonTensor* __restrict__
 // per tensor), ||U||^2 as torch's norm kernel forms it: lane k of 8 a sequential
 // fma chain over elements k, k+8, ... of the first n - n % 8, the 8 lanes added
 // in order, the tail fma'd after.  U = (G' r) c (factored) or g / sqrt(v) (1-D),
-// G' the GC'd gradient.  Blocks of kTcS chunks of 8 elements: waves 1-3 compute
+// G' the GC'd gradient.  Blocks of kTcS chunks of 8 elements: waves 1-7 compute
 // U of block b + 1 into one LDS buffer (chunk s of the block -> column s, element
 // k -> row k) while lanes 0-7 of wave 0 run the chains over block b in the other.
-constexpr int kTcS = 896;                  // chunks (chain steps) per block
+// A wave64 fma issues every ~4.7 cycles on its SIMD (two independent chains in
+// one wave measure the same 4.7 cycles per fma), so the chain is bound by its
+// SIMD's VALU issue, and any other wave's VALU work on that SIMD slows it.  So:
+// one workgroup per CU (LDS above half the CU's), and the waves that share the
+// chain wave's SIMD (HW_ID) produce nothing.  The producers issue each block's
+// loads two blocks ahead (two register sets), so an HBM round trip under load
+// overlaps two blocks of chain steps, and the chain lanes read LDS a round
+// ahead of their fma.
+// s_getreg operand of HW_ID's SIMD_ID field (hwreg 4, offset 4, 2 bits)
+constexpr int kHwIdSimd = ((2 - 1) << 11) | (4 << 6) | 4;
+constexpr int kTcWG = 512;                 // threads of the clip workgroup (8 waves)
+constexpr int kTcS = 1296;                 // chunks (chain steps) per block
 constexpr int kTcLd = kTcS + 4;            // LDS row stride: the 8 chain rows fall in distinct banks
-constexpr int kTcProd = KAON_WG - 64;      // producer threads
-constexpr int kTcSlots = (kTcS + kTcProd - 1) / kTcProd;
+constexpr int kTcLook = 2;                 // rounds of 16 chain steps the LDS reads run ahead
+constexpr int kTcProdMin = 6 * 64;         // producer threads when the chain wave's SIMD holds two waves
+constexpr int kTcSlots = (kTcS + kTcProdMin - 1) / kTcProdMin;
 
-// U of element e (the tail and ragged rows).
-template <int GT>
-__device__ __forceinline__ float tclip_u(const KaonTensor& T, const Ws& ws, bool gc, int64_t e) {
+// U of element e (the tail and chunks across rows).
+template <int GT, bool GC>
+__device__ __forceinline__ float tclip_u(const KaonTensor& T, const Ws& ws, int64_t e) {
   const float x = ldx<GT>(T.g, e);
   if (!T.factored) return x * (1.0f / sqrtf(G(T.v)[e]));
   const uint32_t r = (uint32_t)e / (uint32_t)T.C, j = (uint32_t)e - r * (uint32_t)T.C;
-  const float xg = gc ? round_to<GT>(x - ws.mu(T)[r]) : x;
+  const float xg = GC ? round_to<GT>(x - ws.mu(T)[r]) : x;
   return (xg * ws.rf(T)[r]) * ws.cf(T)[j];
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences global
+// memory, which waits for every load in flight -- the producers' loads issued
+// blocks ahead included; the block handoff needs only the LDS writes done.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A producer slot's raw loads for one chunk: the grad chunk (16-bit grads kept
+// packed, two to a word), the column factors (or v), the row's GC mean and factor.
 template <int GT>
-__global__ __launch_bounds__(KAON_WG) void k_tclip(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
-                                                   KaonHyper hp) {
-  __shared__ __align__(16) float lds[2 * 8 * kTcLd];
-  const int t = (int)blockIdx.x;
-  if (t >= n_tensors) return;
-  const KaonTensor& T = D[t];
+struct TcRaw {
+  uint32_t x[GT == KAON_F32 ? 8 : 4];
+  float f[8];
+  float mu, rf;
+};
+
+template <int GT>
+__device__ __forceinline__ void tc_ldg(const void* g, int64_t c, bool vec, TcRaw<GT>& w) {
+  if (GT == KAON_F32) {
+    float x[8];
+    ld8<KAON_F32>(g, c * 8, 8, vec, x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w.x[i] = __float_as_uint(x[i]);
+  } else if (vec) {
+    const ku4 v = *(const KAON_G ku4*)G((const uint16_t*)g + c * 8);
+    w.x[0] = v.x; w.x[1] = v.y; w.x[2] = v.z; w.x[3] = v.w;
+  } else {
+    const KAON_G uint16_t* b = G((const uint16_t*)g + c * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.x[i] = (uint32_t)b[2 * i] | ((uint32_t)b[2 * i + 1] << 16);
+  }
+}
+template <int GT>
+__device__ __forceinline__ float tc_x(const TcRaw<GT>& w, int i) {
+  if (GT == KAON_F32) return __uint_as_float(w.x[i]);
+  const uint32_t h = (i & 1) ? (w.x[i >> 1] >> 16) : (w.x[i >> 1] & 0xFFFFu);
+  return lp2f<GT>(h);
+}
+
+// KIND 0: 1-D (u = g / sqrt(v)); 1: factored rows of whole chunks (C % 8 == 0);
+// 2: chunks across rows (element by element).
+template <int GT, bool GC, int KIND>
+__device__ __forceinline__ void tc_load(const KaonTensor& T, const Ws& ws, int64_t c, uint32_t cpr, bool vec,
+                                        TcRaw<GT>& w) {
+  if (KIND == 0) {
+    tc_ldg<GT>(T.g, c, vec, w);
+    ld8<KAON_F32>(T.v, c * 8, 8, vec, w.f);
+  } else if (KIND == 1) {
+    const uint32_t r = (uint32_t)c / cpr, j0 = ((uint32_t)c - r * cpr) * 8u;
+    tc_ldg<GT>(T.g, c, vec, w);
+    ld8<KAON_F32>((const float*)ws.cf(T), j0, 8, vec, w.f);
+    w.mu = GC ? ws.mu(T)[r] : 0.0f;
+    w.rf = ws.rf(T)[r];
+  }
+}
+template <int GT, bool GC, int KIND>
+__device__ __forceinline__ void tc_u(const KaonTensor& T, const Ws& ws, int64_t c, const TcRaw<GT>& w, float u[8]) {
+  if (KIND == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = tc_x<GT>(w, i) * (1.0f / sqrtf(w.f[i]));
+  } else if (KIND == 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = tc_x<GT>(w, i);
+      const float xg = GC ? round_to<GT>(x - w.mu) : x;
+      u[i] = (xg * w.rf) * w.f[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = tclip_u<GT, GC>(T, ws, c * 8 + i);
+  }
+}
+
+// The chain lanes' pass over `cnt` steps of one LDS row.  A full block is
+// straight-line code, 16 steps per round with the four 16-byte reads of the
+// round kTcLook ahead issued before this round's fma, pinned by a scheduling
+// barrier, and one LDS wait per round (the chain wave issues an instruction per
+// ~4 cycles, so a wait per read costs a fifth of the rate)
+// (in a loop the reads of the round ahead made the waits of the round at hand
+// wait for them too); the last block of a tensor, shorter, reads as it goes.
+__device__ __forceinline__ void tc_round(float& acc, const kf4 (&v)[4]) {
+  // one asm statement over the round's sixteen operands, so the compiler's LDS
+  // wait before it is a single s_waitcnt for all four reads; v_fmac_f32 is the
+  // fused multiply-add __fmaf_rn compiles to (one rounding)
+  asm volatile(
+      "v_fmac_f32 %0, %1, %1\n\tv_fmac_f32 %0, %2, %2\n\tv_fmac_f32 %0, %3, %3\n\tv_fmac_f32 %0, %4, %4\n\t"
+      "v_fmac_f32 %0, %5, %5\n\tv_fmac_f32 %0, %6, %6\n\tv_fmac_f32 %0, %7, %7\n\tv_fmac_f32 %0, %8, %8\n\t"
+      "v_fmac_f32 %0, %9, %9\n\tv_fmac_f32 %0, %10, %10\n\tv_fmac_f32 %0, %11, %11\n\t"
+      "v_fmac_f32 %0, %12, %12\n\tv_fmac_f32 %0, %13, %13\n\tv_fmac_f32 %0, %14, %14\n\t"
+      "v_fmac_f32 %0, %15, %15\n\tv_fmac_f32 %0, %16, %16"
+      : "+v"(acc)
+      : "v"(v[0].x), "v"(v[0].y), "v"(v[0].z), "v"(v[0].w), "v"(v[1].x), "v"(v[1].y), "v"(v[1].z), "v"(v[1].w),
+        "v"(v[2].x), "v"(v[2].y), "v"(v[2].z), "v"(v[2].w), "v"(v[3].x), "v"(v[3].y), "v"(v[3].z), "v"(v[3].w));
+}
+__device__ __forceinline__ float tc_chain(const float* row, int cnt, float acc) {
+  const kf4* r4 = (const kf4*)row;
+  if (cnt == kTcS) {
+    constexpr int NR = kTcS / 16, LA = kTcLook;
+    kf4 v[LA + 1][4];
+#pragma unroll
+    for (int t = 0; t < LA; ++t)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[t][k] = r4[t * 4 + k];
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      if (t + LA < NR) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[(t + LA) % (LA + 1)][k] = r4[(t + LA) * 4 + k];
+      }
+      // keep the reads above the round's fma (the scheduler would sink them to their use)
+      __builtin_amdgcn_sched_barrier(0);
+      tc_round(acc, v[t % (LA + 1)]);
+    }
+    return acc;
+  }
+  int s = 0;
+  for (; s + 4 <= cnt; s += 4) {
+    const kf4 x = r4[s / 4];
+    acc = __fmaf_rn(x.x, x.x, acc);
+    acc = __fmaf_rn(x.y, x.y, acc);
+    acc = __fmaf_rn(x.z, x.z, acc);
+    acc = __fmaf_rn(x.w, x.w, acc);
+  }
+  for (; s < cnt; ++s) acc = __fmaf_rn(row[s], row[s], acc);
+  return acc;
+}
+
+template <int GT, bool GC, int KIND>
+__device__ __forceinline__ void tclip_body(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, float* lds,
+                                           const int* simd, int mates) {
   const int64_t n = T.n;
-  if (n == 0) return;
-  const bool gc = (hp.flags & KAON_F_GC) != 0 && T.factored;
   const int64_t body = n - n % 8, nchunks = body / 8;
   const int64_t nblk = (nchunks + kTcS - 1) / kTcS;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = (int)(threadIdx.x & 63);
-  // chunk kinds: 0 = 1-D, 1 = factored rows of whole chunks, 2 = chunks across rows
-  const int kind = !T.factored ? 0 : (T.C % 8 == 0 ? 1 : 2);
   const bool vec = T.vec_rows != 0;
   const uint32_t cpr = (uint32_t)(T.C / 8);
+  // producer rank: the waves other than the chain wave's SIMD mates, in wave order,
+  // when those cover a block in kTcSlots rounds; otherwise waves 1-7
+  static_assert((kTcWG / 64 - 1) * 64 * kTcSlots >= kTcS, "seven producer waves cover a block");
+  const bool skip_mates = (kTcWG / 64 - 1 - mates) * 64 * kTcSlots >= kTcS;
+  int prank = -1, nprod = 0;
+  for (int w = 1; w < kTcWG / 64; ++w) {
+    if (skip_mates && simd[w] == simd[0]) continue;
+    if (w == wave) prank = nprod;
+    ++nprod;
+  }
+  const int q0 = prank * 64 + lane;
+  const int nq = nprod * 64;
+  // two register sets: block b's loads go into set b & 1 (indices fixed at compile time)
+  TcRaw<GT> raw0[kTcSlots], raw1[kTcSlots];
 
-  auto produce = [&](int64_t b, int buf) {
-    const int q0 = (int)threadIdx.x - 64;
-    float x[kTcSlots][8], f[kTcSlots][8], mu[kTcSlots], rf[kTcSlots];
-    // every load of the block's slots first, then the arithmetic
+  auto load_block = [&](int64_t b, TcRaw<GT>(&raw)[kTcSlots]) {
 #pragma unroll
     for (int k = 0; k < kTcSlots; ++k) {
-      const int s = q0 + kTcProd * k;
+      const int s = q0 + nq * k;
       const int64_t c = b * kTcS + s;
-      mu[k] = 0.0f;
-      rf[k] = 1.0f;
-      if (s >= kTcS || c >= nchunks) continue;
-      if (kind == 0) {
-        ld8<GT>(T.g, c * 8, 8, vec, x[k]);
-        ld8<KAON_F32>(T.v, c * 8, 8, vec, f[k]);
-      } else if (kind == 1) {
-        const uint32_t r = (uint32_t)c / cpr, j0 = ((uint32_t)c - r * cpr) * 8u;
-        ld8<GT>(T.g, c * 8, 8, vec, x[k]);
-        ld8<KAON_F32>((const float*)ws.cf(T), j0, 8, vec, f[k]);
-        if (gc) mu[k] = ws.mu(T)[r];
-        rf[k] = ws.rf(T)[r];
-      }
+      if (prank >= 0 && s < kTcS && c < nchunks) tc_load<GT, GC, KIND>(T, ws, c, cpr, vec, raw[k]);
     }
+  };
+  auto store_block = [&](int64_t b, const TcRaw<GT>(&raw)[kTcSlots]) {
+    const int buf = (int)(b & 1);
 #pragma unroll
     for (int k = 0; k < kTcSlots; ++k) {
-      const int s = q0 + kTcProd * k;
-      if (s >= kTcS) continue;
+      const int s = q0 + nq * k;
+      if (prank < 0 || s >= kTcS) continue;
       const int64_t c = b * kTcS + s;
       float u[8];
-      if (c >= nchunks) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = 0.0f;
-      } else if (kind == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = x[k][i] * (1.0f / sqrtf(f[k][i]));
-      } else if (kind == 1) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float xg = gc ? round_to<GT>(x[k][i] - mu[k]) : x[k][i];
-          u[i] = (xg * rf[k]) * f[k][i];
-        }
+      if (c < nchunks) {
+        tc_u<GT, GC, KIND>(T, ws, c, raw[k], u);
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) u[i] = tclip_u<GT>(T, ws, gc, c * 8 + i);
+        for (int i = 0; i < 8; ++i) u[i] = 0.0f;
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) lds[(buf * 8 + i) * kTcLd + s] = u[i];
     }
   };
-
-  if (wave != 0 && nblk > 0) produce(0, 0);
-  __syncthreads();
-  float acc = 0.0f;  // lane k < 8: chain k
-  for (int64_t b = 0; b < nblk; ++b) {
-    if (wave == 0) {
-      if (lane < 8) {
-        const int cnt = (int)min<int64_t>(kTcS, nchunks - b * kTcS);
-        const float* row = lds + ((int)(b & 1) * 8 + lane) * kTcLd;
-        int s = 0;
-#pragma unroll 4
-        for (; s + 4 <= cnt; s += 4) {
-          const kf4 v = *(const kf4*)(row + s);
-          acc = __fmaf_rn(v.x, v.x, acc);
-          acc = __fmaf_rn(v.y, v.y, acc);
-          acc = __fmaf_rn(v.z, v.z, acc);
-          acc = __fmaf_rn(v.w, v.w, acc);
-        }
-        for (; s < cnt; ++s) acc = __fmaf_rn(row[s], row[s], acc);
-      }
-    } else if (b + 1 < nblk) {
-      produce(b + 1, (int)((b + 1) & 1));
+  // The chain wave and the producers run loops of their own with the same
+  // barriers (one after the prologue, one per block), so no register holds a
+  // chain value on one path and a load in flight on the other.
+  if (wave != 0) {
+    // iteration b: store block b + 1 (its loads, issued at iteration b - 2, are
+    // in set (b + 1) & 1), then issue block b + 3's into the same set
+    if (nblk > 0) {
+      load_block(0, raw0);
+      if (nblk > 1) load_block(1, raw1);
+      store_block(0, raw0);
+      if (nblk > 2) load_block(2, raw0);
     }
-    __syncthreads();
+    lds_barrier();
+    for (int64_t b = 0; b < nblk; b += 2) {
+      if (b + 1 < nblk) store_block(b + 1, raw1);
+      if (b + 3 < nblk) load_block(b + 3, raw1);
+      lds_barrier();
+      if (b + 1 >= nblk) break;
+      if (b + 2 < nblk) store_block(b + 2, raw0);
+      if (b + 4 < nblk) load_block(b + 4, raw0);
+      lds_barrier();
+    }
+    return;
   }
-  if (wave != 0) return;
+  float acc = 0.0f;  // lane k < 8: chain k
+  lds_barrier();
+  for (int64_t b = 0; b < nblk; ++b) {
+    if (lane < 8) {
+      const int cnt = (int)min<int64_t>(kTcS, nchunks - b * kTcS);
+      acc = tc_chain(lds + ((int)(b & 1) * 8 + lane) * kTcLd, cnt, acc);
+    }
+    lds_barrier();
+  }
   float ss = __shfl(acc, 0);
 #pragma unroll
   for (int k = 1; k < 8; ++k) ss = ss + __shfl(acc, k);
   for (int64_t e = body; e < n; ++e) {
-    const float u = tclip_u<GT>(T, ws, gc, e);
+    const float u = tclip_u<GT, GC>(T, ws, e);
     ss = __fmaf_rn(u, u, ss);
   }
   // clip_threshold 0 leaves the update unclipped
   if (lane == 0) ws.scal(T)[0] = hp.clip > 0.0f ? fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f) : 1.0f;
+}
+
+template <int GT, bool GC>
+__global__ __launch_bounds__(kTcWG) void k_tclip(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
+                                                 KaonHyper hp) {
+  __shared__ __align__(16) float lds[2 * 8 * kTcLd];
+  __shared__ int simd[kTcWG / 64];
+  if ((int)blockIdx.x >= n_tensors) return;
+  // the longest tensors first: their chains are the phase's critical path
+  const KaonTensor& T = D[D[blockIdx.x].by_size];
+  if (T.n == 0) return;
+  // each wave's SIMD (HW_ID bits 5:4); the chain wave's SIMD mates stay idle
+  // unless more than two of the eight waves share that SIMD
+  if ((threadIdx.x & 63) == 0) simd[threadIdx.x >> 6] = (int)((__builtin_amdgcn_s_getreg(kHwIdSimd) >> 4) & 3u);
+  __syncthreads();
+  int mates = 0;
+  for (int w = 1; w < kTcWG / 64; ++w) mates += simd[w] == simd[0];
+  // the tensor's chunk kind, uniform over the workgroup (GC only touches 2-D tensors)
+  if (!T.factored) tclip_body<GT, false, 0>(T, ws, hp, lds, simd, mates);
+  else if (T.C % 8 == 0) tclip_body<GT, GC, 1>(T, ws, hp, lds, simd, mates);
+  else tclip_body<GT, GC, 2>(T, ws, hp, lds, simd, mates);
 }
 
 // =============================================================== MSAM norm="tensor"
@@ -378,6 +527,25 @@ using TrowFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int);
 using TfinFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
 using TclipFn = void (*)(const KaonTensor*, int32_t, Ws, KaonHyper);
 
+
+template <int GT>
+int torch_phases_gt(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mask, int mode, hipStream_t st) {
+  const bool gc = (h.flags & KAON_F_GC) != 0;
+  if (mask & (1u << 1)) {
+    TrowFn f = gc ? k_trow<GT, true> : k_trow<GT, false>;
+    hipLaunchKernelGGL(f, dim3(L.n_row_items), dim3(KAON_WG), 0, st, L.descs, L.row_items, ws, h, mode);
+  }
+  if (mode == 0 && (mask & (1u << 2)) && L.n_fin_items > 0) {
+    TfinFn f = gc ? k_tfin<GT, true> : k_tfin<GT, false>;
+    hipLaunchKernelGGL(f, dim3(L.n_fin_items * kTfinSub), dim3(KAON_WG), 0, st, L.descs, L.fin_items, ws, h);
+  }
+  if (mode == 0 && (mask & (1u << 3))) {
+    TclipFn f = gc ? k_tclip<GT, true> : k_tclip<GT, false>;
+    hipLaunchKernelGGL(f, dim3(L.n_tensors), dim3(kTcWG), 0, st, L.descs, L.n_tensors, ws, h);
+  }
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 // Phases 1-4 of an Adakaon step (mode 0) or phase 1 of a Lion step (mode 1) in
@@ -385,19 +553,9 @@ using TclipFn = void (*)(const KaonTensor*, int32_t, Ws, KaonHyper);
 // clip divisor, so bit 4 has nothing left to do).  Returns a HIP status.
 int torch_phases(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mask, int mode, hipStream_t st) {
   const int gt = h.g_dtype;
-  if (mask & (1u << 1)) {
-    TrowFn f = gt == KAON_BF16 ? k_trow<KAON_BF16> : gt == KAON_F16 ? k_trow<KAON_F16> : k_trow<KAON_F32>;
-    hipLaunchKernelGGL(f, dim3(L.n_row_items), dim3(KAON_WG), 0, st, L.descs, L.row_items, ws, h, mode);
-  }
-  if (mode == 0 && (mask & (1u << 2)) && L.n_fin_items > 0) {
-    TfinFn f = gt == KAON_BF16 ? k_tfin<KAON_BF16> : gt == KAON_F16 ? k_tfin<KAON_F16> : k_tfin<KAON_F32>;
-    hipLaunchKernelGGL(f, dim3(L.n_fin_items * kTfinSub), dim3(KAON_WG), 0, st, L.descs, L.fin_items, ws, h);
-  }
-  if (mode == 0 && (mask & (1u << 3))) {
-    TclipFn f = gt == KAON_BF16 ? k_tclip<KAON_BF16> : gt == KAON_F16 ? k_tclip<KAON_F16> : k_tclip<KAON_F32>;
-    hipLaunchKernelGGL(f, dim3(L.n_tensors), dim3(KAON_WG), 0, st, L.descs, L.n_tensors, ws, h);
-  }
-  return (int)hipGetLastError();
+  return gt == KAON_BF16  ? torch_phases_gt<KAON_BF16>(L, ws, h, mask, mode, st)
+         : gt == KAON_F16 ? torch_phases_gt<KAON_F16>(L, ws, h, mask, mode, st)
+                          : torch_phases_gt<KAON_F32>(L, ws, h, mask, mode, st);
 }
 
 // kaon_momentum_sumsq in torch's order (MSAM norm="tensor").

@@ -42,7 +42,7 @@ class KaonTensor(ctypes.Structure):
         ("m2", ctypes.c_void_p), ("m2_scale", ctypes.c_void_p), ("max_v", ctypes.c_void_p),
         ("pd_s", ctypes.c_void_p), ("pd_p0", ctypes.c_void_p), ("pd_ns", ctypes.c_int64),
         ("pd_slice", ctypes.c_int32), ("pd_p0_scalar", ctypes.c_int32), ("full_v", ctypes.c_int32),
-        ("pd_pad", ctypes.c_int32),
+        ("by_size", ctypes.c_int32),
         ("noise", ctypes.c_void_p * 3),
         ("R", ctypes.c_int64), ("C", ctypes.c_int64), ("n", ctypes.c_int64),
         ("ws_row", ctypes.c_int64), ("ws_col", ctypes.c_int64), ("ws_part", ctypes.c_int64),

@@ -499,3 +499,15 @@ def test_reduction_order_knob():
     assert Nekaon([p], reduction_order="torch").inner.reduction_order == "torch"
     with pytest.raises(ValueError):
         Adakaon([p], reduction_order="cuda")
+
+
+def test_plan_orders_tensors_longest_first():
+    """kaon_plan's by_size: a permutation of the tensors by decreasing numel (stable), the
+    order the per-tensor clip-norm workgroups take them in."""
+    rc, descs, info, _rows, _fins, _flats = _plan([[64, 40], [1280], [640, 320, 3, 3], [64, 40], [7, 9], [40000]])
+    assert rc == 0
+    order = [descs[k].by_size for k in range(6)]
+    assert sorted(order) == list(range(6))
+    sizes = [descs[i].n for i in order]
+    assert sizes == sorted(sizes, reverse=True)
+    assert order.index(0) < order.index(3)  # equal sizes keep param order

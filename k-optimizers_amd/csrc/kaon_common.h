@@ -23,6 +23,10 @@ struct Ws {
   __device__ KAON_G float* roldsc(const KaonTensor& T) const { return G(base + T.ws_row + 4 * T.R); }
   __device__ KAON_G float* cf(const KaonTensor& T) const { return G(base + T.ws_col); }
   __device__ KAON_G float* part(const KaonTensor& T) const { return G(base + T.ws_part); }
+  // the clip's second column partial (t = G^2 / row), laid out as part
+  __device__ KAON_G float* part2(const KaonTensor& T) const {
+    return G(base + T.ws_part + (int64_t)T.ngroups * T.C);
+  }
   __device__ KAON_G uint32_t* bamax(const KaonTensor& T) const { return G((uint32_t*)(base + T.ws_blk)); }
   __device__ KAON_G float* boldsc(const KaonTensor& T, int64_t nb) const { return G(base + T.ws_blk + nb); }
   __device__ KAON_G float* scal(const KaonTensor& T) const { return G(base + T.ws_scal); }
@@ -128,18 +132,43 @@ __device__ void zero_accumulators(const KaonTensor& T, const KaonItem& it, const
   }
 }
 
+// The clip's algebraic sum of squares (Adakaon, AdaMuon): the scalar words of
+// a tensor hold rm at 4 and the partial sums S_k at 5 + k (one per finalize
+// item of KAON_COLITEM columns, or one for a 1-D tensor); phase 4 forms
+// ss = rm * (S_0 + S_1 + ...) in item order.
+__device__ __forceinline__ int clip_parts(const KaonTensor& T) {
+  return T.factored ? (int)((T.C + KAON_COLITEM - 1) / KAON_COLITEM) : 1;
+}
+__device__ __forceinline__ bool clip_alg(const KaonHyper& hp, int mode) {
+  return mode == 0 && hp.clip > 0.0f && !(hp.flags & KAON_F_PNM);
+}
+// Workgroup sum of one value per thread: the 64-lane xor butterfly per wave,
+// then the four wave sums in order (valid in thread 0).  Every thread calls it.
+__device__ __forceinline__ float wg_sum4(float a, float* red) {
+  const float w = wave_csum(a);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = w;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 // Phase 1 of a 1-D tensor (the whole tensor is one row), by the workgroup:
 // v = lerp(v, g*g (+eps1), 1-beta2) (adakaon.py:990-995); AdaPNM:
 // v = v*beta2 + (1-beta2)*g*g, mul_ then addcmul_ (one fma in torch), and the
-// running max under ams_bound (adapnm.py:1243-1248).  Elementwise: no sum.
+// running max under ams_bound (adapnm.py:1243-1248).  With `scal` (the
+// tensor's scalar words) also the clip's sum of (g * g) / v (the new v; no
+// eps1) in the algebraic form: thread t adds the elements of chunks t, t+256,
+// ... in order, then wg_sum4, into word 5; rm = 1 into word 4.
 template <int GT>
-__device__ void stats_1d(const KaonTensor& T, const void* gsrc, const KaonHyper& hp) {
+__device__ void stats_1d(const KaonTensor& T, const void* gsrc, const KaonHyper& hp, KAON_G float* scal,
+                         float* red) {
+  const bool clip = scal != nullptr;
   const int64_t C = T.C;
   const int64_t nch = (C + 7) >> 3;
   const bool vec = T.vec_rows != 0;
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
   const bool pnm = (hp.flags & KAON_F_PNM) != 0;
   const bool ams = pnm && (hp.flags & KAON_F_AMS) != 0 && T.max_v;
+  float cs = 0.0f;
   for (int64_t c = threadIdx.x; c < nch; c += KAON_WG) {
     const int cnt = chunk_cnt(c, C);
     const bool vv = vec && cnt == 8;
@@ -162,9 +191,17 @@ __device__ void stats_1d(const KaonTensor& T, const void* gsrc, const KaonHyper&
         float q = x[i] * x[i];
         if (eps) q = q + hp.eps1;
         v[i] = klerp(v[i], q, hp.w2);
+        if (clip && i < cnt) cs = cs + (x[i] * x[i]) / v[i];
       }
     }
     st8_f32(T.v, c * 8, cnt, vv, v);
+  }
+  if (clip) {
+    const float S = wg_sum4(cs, red);
+    if (threadIdx.x == 0) {
+      scal[4] = 1.0f;
+      scal[5] = S;
+    }
   }
 }
 

@@ -255,15 +255,18 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     if (t.factored && !t.full_v) {
       off = round4(off + t.C);
       t.ws_part = off;
-      off = round4(off + (int64_t)t.ngroups * t.C);
+      // the column partials of G^2 and, after them, of the clip's G^2 / row
+      off = round4(off + 2 * (int64_t)t.ngroups * t.C);
     }
     t.ws_blk = off;
     if (codec == KAON_MOM_4BIT) {
       const int64_t nb = (t.n + t.block4 - 1) / t.block4;
       off = round4(off + 2 * nb);
     }
+    // scalar words: the clip divisor, the keep count, two of KProdigy's / MSAM's,
+    // and the clip's algebraic sum: rm, then one partial per finalize item (or one)
     t.ws_scal = off;
-    off = round4(off + 4);
+    off = round4(off + 5 + (t.factored ? (t.C + KAON_COLITEM - 1) / KAON_COLITEM : 1));
     t.ws_aux = off;
     t.ns_tr = 0;
     t.m_pad = t.k_pad = 0;

@@ -75,6 +75,8 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
                                                    const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                    int mode) {
   extern __shared__ float lds_col[];
+  __shared__ float winv_s[4][KAON_ROW_BUDGET];  // 1 / row (the new row) of each wave's rows
+  __shared__ float red4[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
@@ -85,9 +87,10 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const int cpl = (int)((nch + 63) >> 6);
   const bool vec = T.vec_rows != 0;
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  const bool alg = clip_alg(hp, mode);
 
   if (!T.factored) {
-    if (mode == 0) stats_1d<GT>(T, gsrc, hp);
+    if (mode == 0) stats_1d<GT>(T, gsrc, hp, alg ? ws.scal(T) : nullptr, red4);
     return;
   }
 
@@ -160,7 +163,11 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
           }
       }
       const float s2 = wave_csum(a2);
-      if (wr.lane == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
+      const float nr = klerp(T.row[r], s2 / (float)C, hp.w2);
+      if (wr.lane == 0) {
+        T.row[r] = nr;
+        if (alg) winv_s[wr.w][r - wr.rb] = 1.0f / nr;
+      }
     } else {
       // streaming: sweep A (GC sum), sweep B (q and the row sum)
       if (gc) {
@@ -196,7 +203,11 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
           }
       }
       const float s2 = wave_csum(a2);
-      if (wr.lane == 0) T.row[r] = klerp(T.row[r], s2 / (float)C, hp.w2);
+      const float nr = klerp(T.row[r], s2 / (float)C, hp.w2);
+      if (wr.lane == 0) {
+        T.row[r] = nr;
+        if (alg) winv_s[wr.w][r - wr.rb] = 1.0f / nr;
+      }
     }
   }
   if (mode == 1) continue;
@@ -234,8 +245,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
         part[j] = sl == 0 ? lds_col[j - c0] : part[j] + lds_col[j - c0];
       __syncthreads();  // lds_col is reused by the next segment
     }
-    continue;
-  }
+  } else {
   for (int wf = 0; wf < 4; ++wf) {
     if (wr.w == wf && has_rows) {
       if (CPL > 0) {
@@ -265,36 +275,92 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = sl == 0 ? lds_col[j] : part[j] + lds_col[j];
   __syncthreads();  // lds_col is reused by the next slice
   }
+  if (!alg) continue;
+  // The clip's second column partial, t = (G * G) / row (the new row; no
+  // eps1), in the same wave-group / slice / run order, the rows read again
+  // (this kernel serves the grad layouts outside the prefetching kernels'
+  // register budget).
+  KAON_G float* part2 = part + (int64_t)T.ngroups * C;
+  const int64_t segC = CPL > 0 ? C : (int64_t)kSeg;
+  for (int64_t c0 = 0; c0 < C; c0 += segC) {
+    const int64_t c1 = min(C, c0 + segC);
+    for (int wf = 0; wf < 4; ++wf) {
+      if (wr.w == wf && has_rows) {
+        for (int64_t c = (c0 >> 3) + wr.lane; c * 8 < c1; c += 64) {
+          const int cnt = chunk_cnt(c, C);
+          float acc[8];
+          for (int64_t r = wr.rb; r < wr.re; ++r) {
+            const float mu = gc ? mu_arr[r] : 0.0f;
+            const float w = winv_s[wf][r - wr.rb];
+            float x[8];
+            ld8<GT>(gsrc, r * C + c * 8, cnt, vec && cnt == 8, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
+              const float t = (gv * gv) * w;
+              acc[i] = r == wr.rb ? t : acc[i] + t;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < cnt) {
+              const int64_t j = c * 8 + i - c0;
+              lds_col[j] = wf == 0 ? acc[i] : lds_col[j] + acc[i];
+            }
+        }
+      }
+      __syncthreads();
+    }
+    for (int64_t j = c0 + threadIdx.x; j < c1; j += KAON_WG)
+      part2[j] = sl == 0 ? lds_col[j - c0] : part2[j] + lds_col[j - c0];
+    __syncthreads();  // lds_col is reused by the next segment or slice
+  }
+  }
 }
 
 // =============================================================== phase 2
 // Finalize items.  kind 0: col = lerp(col, colsum/R, 1-beta2), cf = 1/sqrt(col)
-// for columns [row0, row0+nrows), colsum = the slice partials added in slice
-// order.  kind 1: rm = mean(row) (canonical sum), rf = 1/sqrt(row/rm)
-// (_factored.py:48-52, 76-82).
+// for columns [row0, row0+nrows), colsum = the run partials added in run
+// order; with the algebraic clip sum also the item's partial S_k = sum of
+// colsum2_j / col_j (thread t adds columns t, t+256, ... in order, then
+// wg_sum4).  kind 1: rm = mean(row) (canonical sum), rf = 1/sqrt(row/rm)
+// (_factored.py:48-52, 76-82); rm is kept in the tensor's scalar word 4.
+__device__ __forceinline__ float run_sum(const KAON_G float* part, int ngroups, int64_t C, int64_t j) {
+  float cs = 0.0f;
+  int g = 0;
+  for (; g + 8 <= ngroups; g += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(g + u) * C + j];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cs = cs + v[u];
+  }
+  for (; g < ngroups; ++g) cs = cs + part[(int64_t)g * C + j];
+  return cs;
+}
 __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ D,
                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
   __shared__ float rm_s;
+  __shared__ float red4[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   const int64_t R = T.R, C = T.C;
   if (it.kind == 0) {
+    const bool alg = clip_alg(hp, 0);
     const KAON_G float* part = ws.part(T);
+    const KAON_G float* part2 = ws.part2(T);
     KAON_G float* cf = ws.cf(T);
+    float a = 0.0f;
     for (int64_t j = it.row0 + threadIdx.x; j < (int64_t)it.row0 + it.nrows; j += KAON_WG) {
-      float cs = 0.0f;
-      int g = 0;
-      for (; g + 8 <= T.ngroups; g += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(g + u) * C + j];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) cs = cs + v[u];
-      }
-      for (; g < T.ngroups; ++g) cs = cs + part[(int64_t)g * C + j];
+      const float cs = run_sum(part, T.ngroups, C, j);
       const float nc = klerp(T.col[j], cs / (float)R, hp.w2);
       T.col[j] = nc;
       cf[j] = 1.0f / sqrtf(nc);
+      if (alg) a = a + run_sum(part2, T.ngroups, C, j) / nc;
+    }
+    if (alg) {
+      const float S = wg_sum4(a, red4);
+      if (threadIdx.x == 0) ws.scal(T)[5 + it.row0 / KAON_COLITEM] = S;
     }
   } else {
     if (threadIdx.x < 64) {
@@ -306,7 +372,10 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
           if (j < R) a = a + T.row[j];
         }
       const float s = wave_csum(a);
-      if (threadIdx.x == 0) rm_s = s / (float)R;
+      if (threadIdx.x == 0) {
+        rm_s = s / (float)R;
+        ws.scal(T)[4] = s / (float)R;
+      }
     }
     __syncthreads();
     const float rm = rm_s;
@@ -315,62 +384,12 @@ __global__ __launch_bounds__(KAON_WG) void k_fin(const KaonTensor* __restrict__ 
   }
 }
 
-// =============================================================== phase 3
-// Slices: rs[r] = canonical sum over the row of U^2, U = (G*rf)*cf (factored)
-// or G*(1/sqrt(v)) (1-D: the whole tensor is one row).
-template <int GT>
-__global__ __launch_bounds__(KAON_WG) void k_ss(const KaonTensor* __restrict__ D,
-                                                const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  const KaonItem run = items[blockIdx.x / KAON_RUN];
-  const int sl = (int)(blockIdx.x % KAON_RUN);
-  if (sl >= run_slices(run)) return;
-  const KaonItem it = slice_item(run, sl);
-  const KaonTensor& T = D[it.tensor];
-  const void* gsrc = ws.src(T, hp.flags);
-  const int64_t C = T.C;
-  const int64_t nch = (C + 7) >> 3;
-  const int cpl = (int)((nch + 63) >> 6);
-  const bool vec = T.vec_rows != 0;
-  const bool gc = (hp.flags & KAON_F_GC) && T.factored;
-  const float* cfa = T.factored ? (const float*)ws.cf(T) : T.v;
-  const WaveRows wr = wave_rows(it);
-  for (int64_t r = wr.rb; r < wr.re; ++r) {
-    const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    const float rf = T.factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
-    float a = 0.0f;
-    for (int k = 0; k < cpl; ++k) {
-      const int64_t c = wr.lane + 64 * k;
-      const int cnt = chunk_cnt(c, C);
-      if (cnt <= 0) continue;
-      const bool vv = vec && cnt == 8;
-      float x[8], f[8];
-      ld8<GT>(gsrc, r * C + c * 8, cnt, vv, x);
-      ld8<KAON_F32>(cfa, c * 8, cnt, vv, f);
-      if (gc) {
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-          float a0 = x[i] - mu, a1 = x[i + 1] - mu;
-          round_pair<GT>(a0, a1);
-          x[i] = a0;
-          x[i + 1] = a1;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (i < cnt) {
-          const float u = T.factored ? (x[i] * rf) * f[i] : x[i] * (1.0f / sqrtf(f[i]));
-          a = a + u * u;
-        }
-    }
-    const float s = wave_csum(a);
-    if (wr.lane == 0) ws.rs(T)[r] = s;
-  }
-}
-
 // =============================================================== phase 4
-// Clip divisor of every tensor: max(RMS(U) / clip, 1), RMS(U) = sqrt(sum of
-// the row sums rs) / sqrt(n), the rows summed in the canonical 64-lane order
-// (_factored.py:84-89 via adakaon.py:1001-1003).  One wave per tensor.
+// Clip divisor of every tensor: max(RMS(U) / clip, 1), RMS(U) = sqrt(ss) /
+// sqrt(n) (_factored.py:84-89 via adakaon.py:1001-1003).  Adakaon and AdaMuon
+// take ss in the algebraic form rm * (S_0 + S_1 + ...) (the item partials in
+// item order, from phases 1-2); AdaPNM as the canonical sum over the row sums
+// rs of U^2 of its phase 3.  One wave per tensor.
 __global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
                                                      KaonHyper hp) {
   const int t = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -379,28 +398,37 @@ __global__ __launch_bounds__(KAON_WG) void k_clipdiv(const KaonTensor* __restric
   if (T.n == 0) return;
   const int lane = threadIdx.x & 63;
   const int64_t R = T.R;
-  const KAON_G float* rs = ws.rs(T);
-  float a = 0.0f;
-  for (int64_t c = lane; c * 8 < R; c += 64) {
-    float v[8];
+  float ss;
+  if (clip_alg(hp, 0)) {
+    const KAON_G float* sc = ws.scal(T);
+    const int np = clip_parts(T);
+    float S = 0.0f;
+    for (int k = 0; k < np; ++k) S = S + sc[5 + k];
+    ss = sc[4] * S;
+  } else {
+    const KAON_G float* rs = ws.rs(T);
+    float a = 0.0f;
+    for (int64_t c = lane; c * 8 < R; c += 64) {
+      float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = rs[min(c * 8 + i, R - 1)];
+      for (int i = 0; i < 8; ++i) v[i] = rs[min(c * 8 + i, R - 1)];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (c * 8 + i < R) a = a + v[i];
+      for (int i = 0; i < 8; ++i)
+        if (c * 8 + i < R) a = a + v[i];
+    }
+    ss = wave_csum(a);
   }
-  const float ss = wave_csum(a);
   // clip_threshold 0 (AdaPNM) leaves the update unclipped (adapnm.py:157-161)
   if (lane == 0) ws.scal(T)[0] = hp.clip > 0.0f ? fmaxf((sqrtf(ss) / T.sqrt_n) / hp.clip, 1.0f) : 1.0f;
 }
 
 // =============================================================== prefetching row kernels
-// Phases 1 and 3 for slices of bf16 grads with 16-byte rows (C % 8 == 0) of at
+// Phase 1 for slices of bf16 grads with 16-byte rows (C % 8 == 0) of at
 // most 24 chunks per lane.  A wave loads its whole wave group (RW rows, RW *
 // CPL <= 24 chunks per lane) into registers as packed bf16 with every load
 // issued before the first use, so each lane keeps up to 24 x 16 bytes in
 // flight; the row reductions and the column fold then run from registers.
-// The arithmetic and its order are those of k_stats / k_ss.
+// The arithmetic and its order are those of k_stats.
 
 // Chunk k of the lane in each of the wave group's rows.  Every load is
 // issued unconditionally from a valid address (rows past the group and
@@ -427,19 +455,32 @@ __device__ __forceinline__ void load_group(const uint16_t* __restrict__ g, int64
 // one fused multiply-add, which gives the same bits for every bf16-valued x
 // when eps1 is 0 or at least 2^-100: x*x is exact unless |x| < 2^-67, and
 // then x*x < 2^-134 lies below half an ulp of eps1, so both forms give eps1.
+// With gc the chunk's GC'd values replace it in `v` (bf16 pairs packed as
+// loaded), for the clip partial's second pass over the row registers.
 template <int EPS>
-__device__ __forceinline__ void sq_chunk(const ku4 v, float mu, bool gc, float e1, float q[8]) {
+__device__ __forceinline__ void sq_chunk(ku4& v, float mu, bool gc, float e1, float q[8]) {
+  float x[8];
+  if (gc) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = __uint_as_float(w[i] << 16) - mu, a1 = __uint_as_float(w[i] & 0xFFFF0000u) - mu;
+      w[i] = f2bf2(a0, a1);
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+    v = ku4{w[0], w[1], w[2], w[3]};
+  } else {
+    unpack8(v, x);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = EPS == 1 ? __fmaf_rn(x[i], x[i], e1) : EPS == 2 ? x[i] * x[i] + e1 : x[i] * x[i];
+}
+// q of a chunk whose values are final (GC'd in place by sq_chunk).
+template <int EPS>
+__device__ __forceinline__ void sq_plain(const ku4 v, float e1, float q[8]) {
   float x[8];
   unpack8(v, x);
-  if (gc) {
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float a0 = x[i] - mu, a1 = x[i + 1] - mu;
-      rbf2(a0, a1);
-      x[i] = a0;
-      x[i + 1] = a1;
-    }
-  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) q[i] = EPS == 1 ? __fmaf_rn(x[i], x[i], e1) : EPS == 2 ? x[i] * x[i] + e1 : x[i] * x[i];
 }
@@ -490,7 +531,8 @@ __device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0
 template <int CPL, int RW, int EPS>
 __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
                                               const KaonHyper& hp, int mode, float (*seg)[4][512],
-                                              KAON_G float* part, bool acc, bool last, float* racc) {
+                                              KAON_G float* part, bool acc, bool last, float* racc,
+                                              KAON_G float* part2, float* racc2) {
   const int64_t C = T.C;
   const int nch = (int)(C >> 3);
   WaveRows wr = wave_rows(it);
@@ -559,88 +601,44 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
     __syncthreads();
     seg_fold(seg[k & 1], nw, (int64_t)k * 512, C, part, acc, last, tid, racc);
   }
+  float wr_inv[RW];  // 1 / row_j (the new row) for the clip partial
 #pragma unroll
   for (int j = 0; j < RW; ++j) {
+    wr_inv[j] = 0.0f;
     if (j >= nrows) continue;
     const float s2 = wave_csum(a2[j]);
     const float rv = lane_val(row_old, j);
-    if (wr.lane == 0) G(T.row)[wr.rb + j] = klerp(rv, div_r64(s2, rc), hp.w2);
+    const float nr = klerp(rv, div_r64(s2, rc), hp.w2);
+    if (wr.lane == 0) G(T.row)[wr.rb + j] = nr;
+    wr_inv[j] = 1.0f / nr;
   }
-}
-
-template <int CPL, int RW>
-__device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
-                                           const KaonHyper& hp) {
-  const int64_t C = T.C;
-  const int nch = (int)(C >> 3);
-  const WaveRows wr = wave_rows(it);
-  const int nrows = (int)(wr.re - wr.rb);
-  if (nrows <= 0) return;
-  const bool gc = (hp.flags & KAON_F_GC) != 0;
-  const int64_t rl = lane_row(wr.rb, nrows, wr.lane);
-  const float mu_l = gc ? ws.mu(T)[rl] : 0.0f;
-  const float rf_l = ws.rf(T)[rl];
-  const void* gsrc = ws.src(T, hp.flags);
-  // chunk-outer: each chunk's column factors are loaded once for the wave's
-  // rows (all up front for short rows, else one chunk ahead); every row
-  // still sums its chunks in lane order
-  const KAON_G uint8_t* cfb = (const KAON_G uint8_t*)ws.cf(T);
-  constexpr int CFD = CPL <= 4 ? CPL : 1;
-  kf4 cfv[CPL][2];
-  auto load_cf = [&](int k) {
-    const uint32_t cb = 32u * (uint32_t)min(wr.lane + 64 * k, nch - 1);
-    cfv[k][0] = *(const KAON_G kf4*)(cfb + cb);
-    cfv[k][1] = *(const KAON_G kf4*)(cfb + cb + 16u);
-  };
-#pragma unroll
-  for (int k = 0; k < CFD; ++k) load_cf(k);
-  ku4 raw[RW][CPL];
-  load_group<CPL, RW>((const uint16_t*)gsrc, wr.rb, nrows, it.row0, C, nch, wr.lane, raw);
-  float muj[RW], rfj[RW], a[RW];
-#pragma unroll
-  for (int j = 0; j < RW; ++j) {
-    const int jj = min(j, nrows - 1);
-    muj[j] = lane_val(mu_l, jj);
-    rfj[j] = lane_val(rf_l, jj);
-    a[j] = 0.0f;
-  }
+  if (!clip_alg(hp, mode)) return;
+  // The clip's second column partial, t = (G * G) / row (no eps1: rows of
+  // zeros add nothing), from the registers (GC'd in place by the first pass),
+  // in the same wave-group / slice / run order.  The LDS segment buffers keep
+  // alternating from the first pass's.
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = wr.lane + 64 * k;
-    if (k + CFD < CPL) load_cf(k + CFD);
-    const kf4 c0 = cfv[k][0], c1 = cfv[k][1];
-    const float f[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    if (c < nch) {
+    if (nrows > 0) {
+      float v[8];
 #pragma unroll
       for (int j = 0; j < RW; ++j) {
-        if (j >= nrows) continue;
-        float x[8];
-        unpack8(raw[j][k], x);
-        if (gc) {
+        if (j < nrows) {
+          float q[8];
+          sq_plain<0>(raw[j][k], e1, q);
 #pragma unroll
-          for (int i = 0; i < 8; i += 2) {
-            float a0 = x[i] - muj[j], a1 = x[i + 1] - muj[j];
-            rbf2(a0, a1);
-            x[i] = a0;
-            x[i + 1] = a1;
+          for (int i = 0; i < 8; ++i) {
+            const float t = q[i] * wr_inv[j];
+            v[i] = j == 0 ? t : v[i] + t;
           }
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float u = (x[i] * rfj[j]) * f[i];
-          a[j] = a[j] + u * u;
-        }
       }
+      seg_put(seg[(CPL + k) & 1], wr.w, wr.lane, v);
     }
-  }
-#pragma unroll
-  for (int j = 0; j < RW; ++j) {
-    if (j >= nrows) continue;
-    const float s = wave_csum(a[j]);
-    if (wr.lane == 0) ws.rs(T)[wr.rb + j] = s;
+    __syncthreads();
+    seg_fold(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, racc2);
   }
 }
-
 
 // Row class 0: 1-4 chunks per lane, 1 class 1: 5-10, class 2: 11-24; the
 // body is specialized on the exact chunks per lane and its rows per wave
@@ -677,34 +675,38 @@ __device__ __forceinline__ void pf_ss_body(const KaonTensor& T, const KaonItem& 
 template <int CLS, int EPS>
 __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, const KaonItem* __restrict__ items,
                                              const Ws& ws, const KaonHyper& hp, int mode, float (*seg)[4][512],
-                                             float* racc) {
+                                             float* racc, float* racc2) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
   if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
   zero_accumulators(T, it, ws, hp.codec);
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
   KAON_G float* part = run_part(ws, T, it);
+  KAON_G float* part2 = part + (int64_t)T.ngroups * T.C;
   const int nsl = run_slices(it);
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nsl; ++sl) {
     if (sl > 0) __syncthreads();  // the LDS fold buffers are reused
     const KaonItem si = slice_item(it, sl);
     KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS, T, si, ws, hp, mode, seg, part, sl > 0, sl + 1 == nsl,
-                   racc)
+                   racc, part2, racc2)
   }
 }
 
 // Classes 0 and 1 are held to 4 waves per SIMD (128 VGPRs), which their
 // bodies fit without spilling; class 2 rows take more registers.  Every
 // class keeps its run partial in LDS (rows of at most 2048, 5120 and 12288
-// elements) and stores it once per run.
+// elements) and stores it once per run; the clip's second partial is kept in
+// LDS too in class 0 and accumulated in the workspace in classes 1 and 2 (two
+// run partials in LDS would halve their workgroups per CU).
 template <int CLS, int EPS>
 __global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __restrict__ D,
                                                          const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                          int mode) {
   __shared__ __attribute__((aligned(16))) float seg[2][4][512];
   __shared__ __attribute__((aligned(16))) float racc[CLS == 0 ? 4 * 512 : 10 * 512];
-  pf_stats_run<CLS, EPS>(D, items, ws, hp, mode, seg, racc);
+  __shared__ __attribute__((aligned(16))) float racc2[CLS == 0 ? 4 * 512 : 1];
+  pf_stats_run<CLS, EPS>(D, items, ws, hp, mode, seg, racc, CLS == 0 ? racc2 : nullptr);
 }
 template <int EPS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __restrict__ D,
@@ -712,21 +714,9 @@ __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __r
                                                            int mode) {
   __shared__ __attribute__((aligned(16))) float seg[2][4][512];
   __shared__ __attribute__((aligned(16))) float racc[24 * 512];
-  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, racc);
+  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, racc, nullptr);
 }
 
-// One slice per workgroup: workgroup b takes slice b % KAON_RUN of run b / KAON_RUN.
-template <int CLS>
-__global__ __launch_bounds__(KAON_WG) void k_pf_ss(const KaonTensor* __restrict__ D,
-                                                   const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  const KaonItem run = items[blockIdx.x / KAON_RUN];
-  const int sl = (int)(blockIdx.x % KAON_RUN);
-  if (sl >= run_slices(run)) return;
-  const KaonItem it = slice_item(run, sl);
-  const KaonTensor& T = D[it.tensor];
-  const int cpl = (int)(((T.C >> 3) + 63) >> 6);
-  KAON_PF_SWITCH(CLS, pf_ss_body, , T, it, ws, hp)
-}
 #undef KAON_PF_SWITCH
 #undef KAON_COMMA
 
@@ -1771,7 +1761,7 @@ __device__ __forceinline__ void pnm_ss_body(const KaonTensor& T, const KaonItem&
   }
 }
 
-// One slice per workgroup, as k_pf_ss.
+// One slice per workgroup: workgroup b takes slice b % KAON_RUN of run b / KAON_RUN.
 template <int CODEC>
 __global__ __launch_bounds__(KAON_WG) void k_pnm_ss(const KaonTensor* __restrict__ D,
                                                     const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
@@ -2733,11 +2723,6 @@ StatsFn stats_fn(int gt, int cls, int eps) {
   return gt == KAON_BF16 ? stats_fn_gt<KAON_BF16>(cls, eps) : stats_fn_gt<KAON_F32>(cls, eps);
 }
 
-using SsFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
-SsFn ss_fn(int gt) {
-  return gt == KAON_BF16 ? (SsFn)k_ss<KAON_BF16> : gt == KAON_F16 ? (SsFn)k_ss<KAON_F16> : (SsFn)k_ss<KAON_F32>;
-}
-
 using MsamFn = void (*)(const KaonTensor*, const KaonItem*, KaonHyper, float, float, uint32_t, const float*);
 MsamFn msam_fn(int pt, int codec) {
 #define KAON_MSAM_CASE(PTV)                                            \
@@ -2769,23 +2754,6 @@ int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipS
   }
   if (off != L.n_row_items) return fail("kaon: slice class runs do not add up to n_row_items");
   return check_launch("kaon: k_stats launch");
-}
-
-// Phase 3: prefetching kernels over row classes 0-2, k_ss over the rest.
-int launch_ss(const KaonLaunch& L, Ws ws, const KaonHyper& h, hipStream_t st) {
-  int32_t off = 0;
-  for (int cls = 0; cls < 3; ++cls) {
-    const int32_t cnt = L.row_runs[cls];
-    if (cnt <= 0) continue;
-    if (h.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
-    SsFn fn = cls == 0 ? (SsFn)k_pf_ss<0> : cls == 1 ? (SsFn)k_pf_ss<1> : (SsFn)k_pf_ss<2>;
-    hipLaunchKernelGGL(fn, dim3(cnt * KAON_RUN), dim3(KAON_WG), 0, st, L.descs, L.row_items + off, ws, h);
-    off += cnt;
-  }
-  if (L.n_row_items > off)
-    hipLaunchKernelGGL(ss_fn(h.g_dtype), dim3((L.n_row_items - off) * KAON_RUN), dim3(KAON_WG), 0, st, L.descs,
-                       L.row_items + off, ws, h);
-  return check_launch("kaon: k_ss launch");
 }
 
 using MuonMomFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
@@ -2924,9 +2892,7 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
       hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, h);
       if ((rc = check_launch("kaon: k_fin launch"))) return rc;
     }
-    if (mask & (1u << 3)) {
-      if ((rc = launch_ss(*L, ws, h, st))) return rc;
-    }
+    // phase 3 (the clip's sum of squares) is folded into phases 1 and 2
     if (mask & (1u << 4)) {
       hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws,
                          h);
@@ -2992,9 +2958,7 @@ int kaon_adamuon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
     hipLaunchKernelGGL(k_fin, dim3(L->n_fin_items), dim3(KAON_WG), 0, st, L->descs, L->fin_items, ws, ho);
     if ((rc = check_launch("kaon: k_fin launch"))) return rc;
   }
-  if (mask & (1u << 3)) {
-    if ((rc = launch_ss(*L, ws, ho, st))) return rc;
-  }
+  // phase 3 (the clip's sum of squares) is folded into phases 1 and 2
   if (mask & (1u << 4)) {
     hipLaunchKernelGGL(k_clipdiv, dim3((L->n_tensors + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->n_tensors, ws, ho);
     if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;

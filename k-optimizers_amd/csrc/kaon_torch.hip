@@ -128,7 +128,7 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
   zero_accumulators(T, it, ws, hp.codec);
   const void* gsrc = T.g;
   if (!T.factored) {
-    if (mode == 0) stats_1d<GT>(T, gsrc, hp);
+    if (mode == 0) stats_1d<GT>(T, gsrc, hp, nullptr, nullptr);
     return;
   }
   if (mode == 1 && !GC) return;

@@ -46,8 +46,20 @@
  *     groups whose sums are folded in group order; a run is 4 consecutive
  *     slices whose sums are added in slice order; the run sums are added in
  *     run order (every partial starts from +0.0f).
- *   Sum of squares for the RMS clip: CSUM over each row (C elements), then
- *     CSUM over the R row results.
+ *   Sum of squares for the RMS clip, sum U^2 with U = (G r) c, in algebraic
+ *     form (r_i^2 = mean(row) / row_i, c_j^2 = 1 / col_j, up to roundings):
+ *     ss = rm * S, rm = CSUM(row) / R.  Phase 1 adds t_ij = (G_ij * G_ij) *
+ *     w_i, w_i = 1 / row_i (the new row; G as in the row EMA, without its
+ *     eps1, so rows of zeros add nothing) into a second column partial T2_j
+ *     in the COLSUM order; phase 2 forms
+ *     T2_j / col_j (the new col) and sums them per item of 2048 columns --
+ *     thread t of 256 adds columns t, t+256, ... of the item in order, the
+ *     threads of each wave of 64 are reduced by the xor butterfly, the four
+ *     wave sums added in order -- and S adds the items in order.  1-D
+ *     tensors: t_j = (g_j * g_j) / v_j (the new v), thread t of 256 adds the elements
+ *     of chunks t, t+256, ... in order, then the waves as above; rm = 1.
+ *     AdaPNM's clip keeps the per-element form: CSUM of U^2 over each row,
+ *     then CSUM over the R row results.
  *   FSUM(x[0..n)) (KProdigy's per-tensor D statistics over the sliced
  *     elements): blocks of 16384 consecutive elements, each summed in CSUM
  *     order, then CSUM over the block sums.
@@ -210,6 +222,21 @@ float ko_csum(const float* x, int64_t n) {
     return a[0];
 }
 
+/* The xor butterfly over 64 lane values (the canonical wave reduction). */
+static float lane_tree(float* a) {
+    for (int o = KAON_LANES / 2; o >= 1; o >>= 1)
+        for (int l = 0; l < o; ++l) a[l] = a[l] + a[l + o];
+    return a[0];
+}
+/* A workgroup sum: 256 per-thread values, the xor butterfly per wave of 64,
+ * the four wave sums added in order. */
+static float wg_sum(float* th) {
+    float w0 = lane_tree(th), w1 = lane_tree(th + 64), w2 = lane_tree(th + 128), w3 = lane_tree(th + 192);
+    return ((w0 + w1) + w2) + w3;
+}
+#define KAON_WG_THREADS 256
+#define KAON_COLITEM_ORACLE 2048
+
 /* Rows per wave group of the column-sum order (see the header). */
 #define KAON_FLAT 16384
 float ko_fsum(const float* x, int64_t n) {
@@ -264,9 +291,9 @@ typedef struct {
     /* 1: the GC mean, the row / column means of the factored second moment,
      * the row factors' mean and the RMS clip's norm are summed in torch CPU's
      * order (ko_torch_inner_sum, ko_torch_outer_sum, ko_torch_sumsq) instead of
-     * the canonical one.  For pinning the oracle against the reference's own
-     * output only; the GPU follows the canonical order. */
+     * the canonical one (the GPU's reduction_order="torch" mode). */
     int32_t torch_order;
+    float* ss_out;       /* optional: the clip's sum of squares as used (diagnostics) */
 } KoTensor;
 
 typedef struct {
@@ -618,16 +645,19 @@ int ko_msam_apply(const KoTensor* t, const KoHyper* h, double factor, double bou
 /* ------------------------------------------------ factored second moment */
 /* factored_inv_sqrt_factors (src/kaon/_factored.py:62-83): r = rsqrt(row /
  * mean(row)) into rf [R], c = rsqrt(col) into cf [C]. */
-static void factored_factors(const KoTensor* t, float* rf, float* cf) {
+static float factored_factors(const KoTensor* t, float* rf, float* cf) {
     for (int64_t j = 0; j < t->C; ++j) cf[j] = ko_rsqrt(t->col[j]);
     float rm = (t->torch_order ? ko_torch_inner_sum(t->row, t->R) : ko_csum(t->row, t->R)) / (float)t->R;
     for (int64_t r = 0; r < t->R; ++r) rf[r] = ko_rsqrt(t->row[r] / rm);
+    return rm;
 }
 
 /* update_factored_state + factored_inv_sqrt_factors (src/kaon/_factored.py)
- * on x [R, C]: the row/col EMAs, then the factors into rf / cf when given. */
+ * on x [R, C]: the row/col EMAs, then the factors into rf / cf when given.
+ * With clip_ss (canonical order only) also the clip's sum of squares in the
+ * algebraic form of the header: rm * S. */
 static void factored_state(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* rf,
-                           float* cf) {
+                           float* cf, float* clip_ss) {
     int64_t R = t->R, C = t->C;
     int64_t RW = ko_rows_per_wave(C);
     float* q = (float*)malloc(sizeof(float) * (size_t)C);
@@ -636,6 +666,12 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
     float* pr = (float*)calloc((size_t)C, sizeof(float));  /* run partial */
     float* colsum = (float*)calloc((size_t)C, sizeof(float));
     float* rowold = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
+    /* the clip's second column partial (t = x^2 / row), same partial structure */
+    const int alg = clip_ss && !t->torch_order;
+    float* pw2 = (float*)calloc((size_t)C, sizeof(float));
+    float* ps2 = (float*)calloc((size_t)C, sizeof(float));
+    float* pr2 = (float*)calloc((size_t)C, sizeof(float));
+    float* colsum2 = (float*)calloc((size_t)C, sizeof(float));
     for (int64_t r = 0; r < R; ++r) rowold[r] = t->row[r];
     for (int64_t r = 0; r < R; ++r) {
         for (int64_t j = 0; j < C; ++j) {
@@ -646,15 +682,31 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
         }
         float rmean = ko_csum(q, C) / (float)C;
         t->row[r] = ko_lerp(t->row[r], rmean, w2);
+        if (alg) {
+            const float w = 1.0f / t->row[r];
+            for (int64_t j = 0; j < C; ++j) {
+                const float xx = x[r * C + j] * x[r * C + j];
+                pw2[j] = pw2[j] + xx * w;
+            }
+        }
         int end_group = ((r + 1) % RW == 0) || r + 1 == R;
         if (end_group) {
-            for (int64_t j = 0; j < C; ++j) { ps[j] = ps[j] + pw[j]; pw[j] = 0.0f; }
+            for (int64_t j = 0; j < C; ++j) {
+                ps[j] = ps[j] + pw[j]; pw[j] = 0.0f;
+                ps2[j] = ps2[j] + pw2[j]; pw2[j] = 0.0f;
+            }
             int64_t g = r / RW;
             if ((g + 1) % KAON_WAVES == 0 || r + 1 == R) {
-                for (int64_t j = 0; j < C; ++j) { pr[j] = pr[j] + ps[j]; ps[j] = 0.0f; }
+                for (int64_t j = 0; j < C; ++j) {
+                    pr[j] = pr[j] + ps[j]; ps[j] = 0.0f;
+                    pr2[j] = pr2[j] + ps2[j]; ps2[j] = 0.0f;
+                }
                 int64_t s = g / KAON_WAVES;
                 if ((s + 1) % KAON_RUN == 0 || r + 1 == R)
-                    for (int64_t j = 0; j < C; ++j) { colsum[j] = colsum[j] + pr[j]; pr[j] = 0.0f; }
+                    for (int64_t j = 0; j < C; ++j) {
+                        colsum[j] = colsum[j] + pr[j]; pr[j] = 0.0f;
+                        colsum2[j] = colsum2[j] + pr2[j]; pr2[j] = 0.0f;
+                    }
             }
         }
     }
@@ -675,16 +727,53 @@ static void factored_state(const KoTensor* t, const float* x, float w2, float ep
         free(sq);
     }
     for (int64_t j = 0; j < C; ++j) t->col[j] = ko_lerp(t->col[j], colsum[j] / (float)R, w2);
+    float rm = 0.0f;
+    if (rf && cf) rm = factored_factors(t, rf, cf);
+    if (alg) {
+        if (!(rf && cf)) rm = ko_csum(t->row, R) / (float)R;
+        float th[KAON_WG_THREADS];
+        float S = 0.0f;
+        for (int64_t j0 = 0; j0 < C; j0 += KAON_COLITEM_ORACLE) {
+            const int64_t j1 = j0 + KAON_COLITEM_ORACLE < C ? j0 + KAON_COLITEM_ORACLE : C;
+            for (int k = 0; k < KAON_WG_THREADS; ++k) {
+                float a = 0.0f;
+                for (int64_t j = j0 + k; j < j1; j += KAON_WG_THREADS) a = a + colsum2[j] / t->col[j];
+                th[k] = a;
+            }
+            S = S + wg_sum(th);
+        }
+        *clip_ss = rm * S;
+    }
     free(q); free(pw); free(ps); free(pr); free(colsum); free(rowold);
-    if (rf && cf) factored_factors(t, rf, cf);
+    free(pw2); free(ps2); free(pr2); free(colsum2);
 }
 
-/* The factored step's U = (x * r) * c. */
-static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u) {
+/* The 1-D clip sum in its algebraic form (header): t_j = (g_j * g_j) / v_j
+ * with the new v, thread k of 256 adding the elements of chunks k, k+256, ...
+ * in order, then the waves. */
+static float clip_ss_1d(const float* g, const float* v, int64_t n) {
+    float th[KAON_WG_THREADS];
+    const int64_t nch = (n + KAON_CHUNK - 1) / KAON_CHUNK;
+    for (int k = 0; k < KAON_WG_THREADS; ++k) {
+        float a = 0.0f;
+        for (int64_t c = k; c < nch; c += KAON_WG_THREADS)
+            for (int e = 0; e < KAON_CHUNK; ++e) {
+                const int64_t i = c * KAON_CHUNK + e;
+                if (i >= n) break;
+                a = a + (g[i] * g[i]) / v[i];
+            }
+        th[k] = a;
+    }
+    return wg_sum(th);
+}
+
+/* The factored step's U = (x * r) * c, and the clip's algebraic sum of squares. */
+static void factored_update(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps, float* u,
+                            float* clip_ss) {
     int64_t R = t->R, C = t->C;
     float* rf = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
     float* cf = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
-    factored_state(t, x, w2, eps1f, add_eps, rf, cf);
+    factored_state(t, x, w2, eps1f, add_eps, rf, cf, clip_ss);
     for (int64_t r = 0; r < R; ++r)
         for (int64_t j = 0; j < C; ++j) u[r * C + j] = (x[r * C + j] * rf[r]) * cf[j];
     free(rf); free(cf);
@@ -709,21 +798,31 @@ float ko_torch_sumsq(const float* u, int64_t n) {
 
 /* RMS clip then scale (adakaon.py:1000-1002; adamuon.py:586-588):
  * u /= max((||u|| / sqrt(n)) / clip, 1); u *= scale.  The sum of squares is
- * canonical (CSUM of the rows' CSUMs), or torch's order with torch_order. */
-static void clip_scale(const KoTensor* t, float* u, double clip, float scale) {
+ * torch's with torch_order; otherwise the canonical algebraic form in ss_alg
+ * (Adakaon, AdaMuon), or, with ss_alg NULL (AdaPNM), CSUM of the rows' CSUMs
+ * of u^2. */
+static void clip_scale(const KoTensor* t, float* u, double clip, float scale, const float* ss_alg) {
     int64_t R = t->R, C = t->C, n = R * C;
-    float* rs = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
-    float* sq = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
-    for (int64_t r = 0; r < R; ++r) {
-        for (int64_t j = 0; j < C; ++j) sq[j] = u[r * C + j] * u[r * C + j];
-        rs[r] = ko_csum(sq, C);
+    float ss;
+    if (t->torch_order) {
+        ss = ko_torch_sumsq(u, n);
+    } else if (ss_alg) {
+        ss = *ss_alg;
+    } else {
+        float* rs = (float*)malloc(sizeof(float) * (size_t)(R > 0 ? R : 1));
+        float* sq = (float*)malloc(sizeof(float) * (size_t)(C > 0 ? C : 1));
+        for (int64_t r = 0; r < R; ++r) {
+            for (int64_t j = 0; j < C; ++j) sq[j] = u[r * C + j] * u[r * C + j];
+            rs[r] = ko_csum(sq, C);
+        }
+        ss = ko_csum(rs, R);
+        free(rs); free(sq);
     }
-    float ss = t->torch_order ? ko_torch_sumsq(u, n) : ko_csum(rs, R);
+    if (t->ss_out) *t->ss_out = ss;
     float rmsv = sqrtf(ss) / (float)sqrt((double)(n > 1 ? n : 1));
     float fac = fmaxf(rmsv / (float)clip, 1.0f);
     if (t->fac_override) fac = *t->fac_override;
     for (int64_t i = 0; i < n; ++i) u[i] = (u[i] / fac) * scale;
-    free(rs); free(sq);
 }
 
 /* ------------------------------------------------------------- Adakaon */
@@ -741,8 +840,9 @@ int ko_adakaon_tensor(const KoTensor* t, const KoHyper* h) {
      * removal factor is (-1) * (-k) = k). */
     if (h->nk_remove) msam_apply(t, h, (float)(h->nk_k), (float)h->nk_bound_old, 0);
 
+    float ss_alg = 0.0f;
     if (t->factored) {
-        factored_update(t, g, w2, eps1f, h->eps1 > 0, u);
+        factored_update(t, g, w2, eps1f, h->eps1 > 0, u, &ss_alg);
     } else {
         for (int64_t i = 0; i < n; ++i) {
             float q = g[i] * g[i];
@@ -750,8 +850,9 @@ int ko_adakaon_tensor(const KoTensor* t, const KoHyper* h) {
             t->v[i] = ko_lerp(t->v[i], q, w2);
             u[i] = g[i] * ko_rsqrt(t->v[i]);
         }
+        ss_alg = clip_ss_1d(g, t->v, n);
     }
-    clip_scale(t, u, h->clip, (float)h->lr);
+    clip_scale(t, u, h->clip, (float)h->lr, &ss_alg);
     if (h->beta1 > 0 && t->codec != KO_MOM_NONE) codec_ema(t, u, w1, d);
     else memcpy(d, u, sizeof(float) * (size_t)n);
     if (h->wd != 0) {
@@ -840,7 +941,7 @@ int ko_adapnm_tensor(const KoTensor* t, const KoHyper* h) {
     if (t->factored) {
         rf = (float*)malloc(sizeof(float) * (size_t)t->R);
         cf = (float*)malloc(sizeof(float) * (size_t)t->C);
-        factored_state(t, g, fa2, feps, h->eps1 > 0, rf, cf);
+        factored_state(t, g, fa2, feps, h->eps1 > 0, rf, cf, NULL);
     }
     /* both momenta as fp32; EMA of the positive one with the raw gradient
      * (mul_(beta1^2).add_(g, alpha=1-beta1^2)), stored back through its codec */
@@ -870,7 +971,7 @@ int ko_adapnm_tensor(const KoTensor* t, const KoHyper* h) {
             u[i] = pn / de;
         }
     }
-    if (h->clip > 0) clip_scale(t, u, h->clip, fstep);
+    if (h->clip > 0) clip_scale(t, u, h->clip, fstep, NULL);
     else for (int64_t i = 0; i < n; ++i) u[i] = u[i] * fstep;
     if (h->cautious) cautious(u, g, n);
     write_sub(t, u, h, 1);
@@ -949,7 +1050,7 @@ int ko_kprodigy_pass1_tensor(const KoTensor* t, const KoHyper* h, float* num_out
         const float val = (float)(h->pd_d * h->pd_d * (1.0 - h->beta2)), b2 = (float)h->beta2;
         for (int64_t i = 0; i < n; ++i) t->v[i] = fmaf(val * g[i], g[i], t->v[i] * b2);
     } else {
-        factored_state(t, g, (float)(1.0 - h->beta2), (float)h->eps1, h->eps1 > 0, NULL, NULL);
+        factored_state(t, g, (float)(1.0 - h->beta2), (float)h->eps1, h->eps1 > 0, NULL, NULL, NULL);
     }
     free(g);
     return 0;
@@ -1069,8 +1170,9 @@ int ko_adamuon_tensor(const KoTensor* t, const KoHyper* h) {
         float* o = (float*)malloc(sizeof(float) * (size_t)n);
         ko_newton_schulz(mm, t->R, t->C, h->ns_steps, o);
         if (t->out_m) memcpy(t->out_m, o, sizeof(float) * (size_t)n);
-        factored_update(t, o, w2, eps1f, h->eps1 > 0, u);
-        clip_scale(t, u, h->clip, scale);
+        float ss_alg = 0.0f;
+        factored_update(t, o, w2, eps1f, h->eps1 > 0, u, &ss_alg);
+        clip_scale(t, u, h->clip, scale, &ss_alg);
         memcpy(d, u, sizeof(float) * (size_t)n);
         free(mm); free(o);
     } else {
@@ -1080,7 +1182,8 @@ int ko_adamuon_tensor(const KoTensor* t, const KoHyper* h) {
             t->v[i] = ko_lerp(t->v[i], q, w2);
             u[i] = g[i] * ko_rsqrt(t->v[i]);
         }
-        clip_scale(t, u, h->clip, scale);
+        const float ss_alg = clip_ss_1d(g, t->v, n);
+        clip_scale(t, u, h->clip, scale, &ss_alg);
         if (h->beta1 > 0 && t->codec != KO_MOM_NONE) codec_ema(t, u, w1, d);
         else memcpy(d, u, sizeof(float) * (size_t)n);
     }

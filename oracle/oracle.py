@@ -73,6 +73,7 @@ class KoTensor(ctypes.Structure):
         ("pd_s", ctypes.c_void_p), ("pd_p0", ctypes.c_void_p), ("pd_np0", ctypes.c_int64),
         ("pd_slice", ctypes.c_int32), ("full_v", ctypes.c_int32),
         ("torch_order", ctypes.c_int32),
+        ("ss_out", ctypes.c_void_p),
     ]
 
 
@@ -431,7 +432,7 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
 TORCH_ORDER = [False]
 
 
-def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) -> KoTensor:
+def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None, ss_out=None) -> KoTensor:
     st = prm.state
     R, C = prm.eff
     t = KoTensor()
@@ -456,6 +457,7 @@ def _tensor(prm: OParam, codec: str, noise=None, out_m=None, fac_override=None) 
     t.out_m = _ptr(out_m)
     t.fac_override = _ptr(fac_override)
     t.torch_order = int(TORCH_ORDER[0])
+    t.ss_out = _ptr(ss_out)
     return t
 
 
@@ -659,7 +661,11 @@ class OracleOptimizer:
                 self.msam_apply(+1.0, noise)
                 self.has_e = True
 
-    def step(self, noise: dict[int, list] | None = None, fac_override: dict[int, np.ndarray] | None = None) -> None:
+    def step(self, noise: dict[int, list] | None = None, fac_override: dict[int, np.ndarray] | None = None,
+             ss_out: dict[int, np.ndarray] | None = None) -> None:
+        """One step.  ``fac_override`` injects clip divisors per tensor id;
+        ``ss_out`` (tensor id -> float32 [1]) receives the clip's sum of squares
+        of the Adakaon / Nekaon / MSAM / AdaMuon / AdaPNM steps."""
         self.t += 1
         if self.opt == "kprodigy":
             self._kprodigy_step(noise)
@@ -692,10 +698,12 @@ class OracleOptimizer:
                 continue
             if self.opt == "adapnm":
                 t = _pnm_tensor(prm, md, self.t, None if noise is None else noise.get(prm.tensor_id))
+                t.ss_out = _ptr(None if ss_out is None else ss_out.get(prm.tensor_id))
                 _check(lib().ko_adapnm_tensor(ctypes.byref(t), ctypes.byref(h)))
                 continue
             t = _tensor(prm, md, None if noise is None else noise.get(prm.tensor_id),
-                        fac_override=None if fac_override is None else fac_override.get(prm.tensor_id))
+                        fac_override=None if fac_override is None else fac_override.get(prm.tensor_id),
+                        ss_out=None if ss_out is None else ss_out.get(prm.tensor_id))
             if self.opt in ("adakaon", "nekaon", "msam"):
                 _check(lib().ko_adakaon_tensor(ctypes.byref(t), ctypes.byref(h)))
             elif self.opt == "lion":

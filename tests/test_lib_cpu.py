@@ -180,9 +180,9 @@ def test_plan_covers_every_row_and_element_once(g_dtype):
         spans.append((d.ws_row, d.ws_row + 5 * d.R))
         if d.factored:
             spans.append((d.ws_col, d.ws_col + d.C))
-            spans.append((d.ws_part, d.ws_part + d.ngroups * d.C))
+            spans.append((d.ws_part, d.ws_part + 2 * d.ngroups * d.C))  # G^2 and the clip's G^2 / row
         spans.append((d.ws_blk, d.ws_blk + 2 * nb))
-        spans.append((d.ws_scal, d.ws_scal + 4))
+        spans.append((d.ws_scal, d.ws_scal + 5 + (-(-d.C // 2048) if d.factored else 1)))
         assert d.ngroups == -(-d.R // (16 * O.rows_per_wave(d.C)))
         assert d.sqrt_n == np.float32(np.sqrt(float(max(d.n, 1))))
     spans.sort()
@@ -305,7 +305,8 @@ def test_adamuon_plan_pads_and_tiles_newton_schulz():
         words = ((d.R * d.C + 1) // 2 + 3) // 4 * 4 + 2 * ((d.m_pad * d.k_pad // 2 + 3) // 4 * 4) \
             + 2 * ((d.m_pad * d.m_pad // 2 + 3) // 4 * 4)
         spans += [(d.ws_row, d.ws_row + 5 * d.R), (d.ws_col, d.ws_col + d.C),
-                  (d.ws_part, d.ws_part + d.ngroups * d.C), (d.ws_scal, d.ws_scal + 4), (d.ws_aux, d.ws_aux + words)]
+                  (d.ws_part, d.ws_part + 2 * d.ngroups * d.C), (d.ws_scal, d.ws_scal + 5 + -(-d.C // 2048)),
+                  (d.ws_aux, d.ws_aux + words)]
     spans.sort()
     for (a0, a1), (b0, _b1) in zip(spans, spans[1:]):
         assert a1 <= b0

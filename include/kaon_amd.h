@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 8
+#define KAON_ABI_VERSION 9
 
 /* element types of params / grads (p.dtype, p.grad.dtype); fp16 params and
  * grads (both fp16) step in Adakaon, Lion, AdaMuon and AdaPNM plans only,
@@ -71,8 +71,9 @@ enum {
                                (decouple=False, kprodigy.py:342-349) */
   KAON_F_PD_STATS = 2048,   /* KProdigy pass 1: update s and the D statistics this step */
   KAON_F_GC_WRITE = 4096,   /* Adakaon / Lion apply and KProdigy pass 2: also store the
-                               centralized gradient over p.grad, as the reference's native
-                               path leaves it (centralize_grads_, _backend.py:147-177) */
+                               centralized gradient over p.grad of the tensors whose
+                               gc_write is set, as the reference's native path leaves it
+                               (centralize_grads_, _backend.py:147-177) */
   KAON_F_TORCH_ORDER = 8192 /* Adakaon / Lion steps and kaon_momentum_sumsq: the step's fp32
                                sums in torch CPU's order instead of the canonical 64-lane one
                                (below): the GC row means (_backend.py:147-177), the factored
@@ -116,9 +117,12 @@ typedef struct KaonTensor {
   /* workspace offsets, in 4-byte words from the workspace base (kaon_plan) */
   int64_t ws_row;         /* 5 arrays of R words: mu, rf, rs, amax, oldscale */
   int64_t ws_col;         /* cf [C] */
-  int64_t ws_part;        /* column partials [ngroups][C], one row per run */
+  int64_t ws_part;        /* column partials [2][ngroups][C], one row per run: of q = g^2 (+eps1)
+                             and, for the RMS clip, of g^2 / row */
   int64_t ws_blk;         /* 4-bit: 2 arrays of nblocks words: amax, oldscale */
-  int64_t ws_scal;        /* 4 words: fac, keep-count, KProdigy num, KProdigy den */
+  int64_t ws_scal;        /* 5 + ceil(C / KAON_COLITEM) words (6 for 1-D): clip divisor, keep
+                             count, KProdigy num / den (MSAM / AdaMuon norms), mean(row), then
+                             the clip's partial sums, one per finalize item */
   int64_t ws_aux;         /* AdaMuon: Newton-Schulz buffers, bf16: M then O [R*C], the iterate
                              X and its successor [m_pad*k_pad] each, A and B [m_pad^2] each;
                              KProdigy: the D statistics' block sums, [2][ceil(pd_ns / KAON_FLAT_ITEM)] */
@@ -133,6 +137,10 @@ typedef struct KaonTensor {
   int32_t m_pad, k_pad;   /* AdaMuon: min(R,C) and max(R,C) rounded up to the tile (KAON_NS_TILE,
                              or twice that for big matrices) */
   int32_t fast_lanes;     /* set by kaon_plan: lanes per row of the phase-5/6 fast kernel (8..64) */
+  int32_t gc_write;       /* under KAON_F_GC_WRITE: 1 = store this tensor's centralized gradient
+                             over g, 0 = leave g as given (the reference's fused Adakaon
+                             centralizes p.grad in place only for the params it routes to its
+                             native path, adakaon.py:396-401, 448-468) */
 } KaonTensor;
 
 /* A work item.  Runs and slices: rows [row0, row0 + nrows) of tensor

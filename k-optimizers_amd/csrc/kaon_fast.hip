@@ -45,6 +45,7 @@ __device__ __forceinline__ uint32_t pack_int8x4(float a, float b, float c, float
 struct FastCtx {
   const KAON_G uint8_t* g;       // bf16 grads
   KAON_G uint8_t* gw;            // the same, written by the apply under FF_GCW
+  bool gcw;                      // ... for tensors whose gc_write is set
   KAON_G uint8_t* p;             // bf16 params
   KAON_G uint8_t* m;             // momentum codes or bf16 momentum
   KAON_G uint8_t* msc;           // momentum scales (per row or per block)
@@ -472,7 +473,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     ov = sr_chunk(y, nz2);
   }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
-  if (PHASE == 6 && (FLAGS & FF_GCW) && GC) {
+  if (PHASE == 6 && (FLAGS & FF_GCW) && GC && X.gcw) {
     // the centralized gradient, already rounded to bf16 (its low halves are zero)
     ku4 gv;
     gv.x = pack_hi16(__float_as_uint(g[0]), __float_as_uint(g[1]));
@@ -522,6 +523,7 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   FastCtx X;
   X.g = (const KAON_G uint8_t*)G(T.g);
   X.gw = (KAON_G uint8_t*)G(const_cast<void*>(T.g));
+  X.gcw = T.gc_write != 0;
   X.p = (KAON_G uint8_t*)G(T.p);
   // AdaPNM: m is this step's positive buffer (m on odd steps, m2 on even ones)
   const bool swap = PNM && (hp.step & 1u) == 0u;

@@ -527,12 +527,37 @@ __device__ __forceinline__ void seg_fold(float (*seg)[512], int nw, int64_t col0
   }
   *dst = ku2{__float_as_uint(a0), __float_as_uint(a1)};
 }
+// seg_fold with the run partial of the thread's two columns of segment k in
+// registers (r0, r1) instead of LDS; the order is the same.
+__device__ __forceinline__ void seg_fold_reg(float (*seg)[512], int nw, int64_t col0, int64_t C,
+                                             KAON_G float* part, bool acc, bool last, int tid, float& r0,
+                                             float& r1) {
+  const int c = 2 * tid;
+  if (col0 + c >= C) return;
+  float a0 = seg[0][c], a1 = seg[0][c + 1];
+  for (int w = 1; w < nw; ++w) {
+    a0 = a0 + seg[w][c];
+    a1 = a1 + seg[w][c + 1];
+  }
+  if (acc) {
+    a0 = r0 + a0;
+    a1 = r1 + a1;
+  }
+  if (!last) {
+    r0 = a0;
+    r1 = a1;
+    return;
+  }
+  *(KAON_G ku2*)(part + col0 + c) = ku2{__float_as_uint(a0), __float_as_uint(a1)};
+}
 
-template <int CPL, int RW, int EPS>
+// The second (clip) partial's run accumulator: racc2 in LDS (REG2 false), or
+// the thread's two columns per segment in registers rr2 (REG2 true).
+template <int CPL, int RW, int EPS, bool REG2>
 __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonItem& it, const Ws& ws,
                                               const KaonHyper& hp, int mode, float (*seg)[4][512],
                                               KAON_G float* part, bool acc, bool last, float* racc,
-                                              KAON_G float* part2, float* racc2) {
+                                              KAON_G float* part2, float* racc2, float (&rr2)[48]) {
   const int64_t C = T.C;
   const int nch = (int)(C >> 3);
   WaveRows wr = wave_rows(it);
@@ -636,7 +661,10 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
       seg_put(seg[(CPL + k) & 1], wr.w, wr.lane, v);
     }
     __syncthreads();
-    seg_fold(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, racc2);
+    if (REG2)
+      seg_fold_reg(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, rr2[2 * k], rr2[2 * k + 1]);
+    else
+      seg_fold(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, racc2);
   }
 }
 
@@ -672,7 +700,7 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
     case 24: if (CLS == 2) BODY<24, 1 X>(__VA_ARGS__); break;                                  \
   }
 
-template <int CLS, int EPS>
+template <int CLS, int EPS, bool REG2>
 __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, const KaonItem* __restrict__ items,
                                              const Ws& ws, const KaonHyper& hp, int mode, float (*seg)[4][512],
                                              float* racc, float* racc2) {
@@ -684,21 +712,24 @@ __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, c
   KAON_G float* part = run_part(ws, T, it);
   KAON_G float* part2 = part + (int64_t)T.ngroups * T.C;
   const int nsl = run_slices(it);
+  float rr2[48];
+#pragma unroll
+  for (int i = 0; i < 48; ++i) rr2[i] = 0.0f;
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nsl; ++sl) {
     if (sl > 0) __syncthreads();  // the LDS fold buffers are reused
     const KaonItem si = slice_item(it, sl);
-    KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS, T, si, ws, hp, mode, seg, part, sl > 0, sl + 1 == nsl,
-                   racc, part2, racc2)
+    KAON_PF_SWITCH(CLS, pf_stats_body, KAON_COMMA EPS KAON_COMMA REG2, T, si, ws, hp, mode, seg, part, sl > 0,
+                   sl + 1 == nsl, racc, part2, racc2, rr2)
   }
 }
 
-// Classes 0 and 1 are held to 4 waves per SIMD (128 VGPRs), which their
-// bodies fit without spilling; class 2 rows take more registers.  Every
-// class keeps its run partial in LDS (rows of at most 2048, 5120 and 12288
-// elements) and stores it once per run; the clip's second partial is kept in
-// LDS too in class 0 and accumulated in the workspace in classes 1 and 2 (two
-// run partials in LDS would halve their workgroups per CU).
+// Classes 0 and 1 are held to 4 waves per SIMD (128 VGPRs).  Every class
+// keeps its run partial in LDS (rows of at most 2048, 5120 and 12288
+// elements) and stores it once per run.  The clip's second run partial is
+// kept in LDS too in class 0, accumulated in the workspace in class 1 (in
+// registers it would cost class 1 a wave per SIMD, measured slower) and kept
+// in registers in class 2, whose LDS already limits it to 2 waves per SIMD.
 template <int CLS, int EPS>
 __global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __restrict__ D,
                                                          const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
@@ -706,7 +737,7 @@ __global__ __launch_bounds__(KAON_WG, 4) void k_pf_stats(const KaonTensor* __res
   __shared__ __attribute__((aligned(16))) float seg[2][4][512];
   __shared__ __attribute__((aligned(16))) float racc[CLS == 0 ? 4 * 512 : 10 * 512];
   __shared__ __attribute__((aligned(16))) float racc2[CLS == 0 ? 4 * 512 : 1];
-  pf_stats_run<CLS, EPS>(D, items, ws, hp, mode, seg, racc, CLS == 0 ? racc2 : nullptr);
+  pf_stats_run<CLS, EPS, false>(D, items, ws, hp, mode, seg, racc, CLS == 0 ? racc2 : nullptr);
 }
 template <int EPS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __restrict__ D,
@@ -714,7 +745,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __r
                                                            int mode) {
   __shared__ __attribute__((aligned(16))) float seg[2][4][512];
   __shared__ __attribute__((aligned(16))) float racc[24 * 512];
-  pf_stats_run<2, EPS>(D, items, ws, hp, mode, seg, racc, nullptr);
+  pf_stats_run<2, EPS, true>(D, items, ws, hp, mode, seg, racc, nullptr);
 }
 
 #undef KAON_PF_SWITCH
@@ -1288,7 +1319,7 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
       }
       if (cnt <= 0) continue;
       // ---------------- phase 6 writes
-      if (gc && (hp.flags & KAON_F_GC_WRITE) && (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)) {
+      if (gc && (hp.flags & KAON_F_GC_WRITE) && T.gc_write && (OPT == KAON_OPT_ADAKAON || OPT == KAON_OPT_LION)) {
         // the centralized gradient over p.grad (already rounded to the grad dtype)
         if (GT == KAON_F32) {
           st8_f32(const_cast<void*>(T.g), e0, cnt, vec, g);
@@ -2371,7 +2402,7 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
         dout[i] = cautious ? div_r64(d * (kp ? 1.0f : 0.0f), rden) : d;
       }
       if (PHASE != 6) continue;
-      if (gc && (hp.flags & KAON_F_GC_WRITE)) {
+      if (gc && (hp.flags & KAON_F_GC_WRITE) && T.gc_write) {
         // the centralized gradient over p.grad (already rounded to the grad dtype)
         if (GT == KAON_F32) {
           st8_f32(const_cast<void*>(T.g), e0, cnt, vec, g);
@@ -2429,7 +2460,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
 // The centralized gradient written back over p.grad, as the reference's native
 // path leaves it (centralize_grads_, _backend.py:147-177: g -= mean over the
 // fan-in, in the grad dtype, for params of 2 dims or more): g = round(g - mu)
-// with the row means phase 1 stored.  One slice per workgroup, as phase 3.
+// with the row means phase 1 stored, for the tensors whose gc_write is set.
+// One slice per workgroup.
 template <int GT>
 __global__ __launch_bounds__(KAON_WG) void k_gc_write(const KaonTensor* __restrict__ D,
                                                       const KaonItem* __restrict__ items, Ws ws) {
@@ -2438,7 +2470,7 @@ __global__ __launch_bounds__(KAON_WG) void k_gc_write(const KaonTensor* __restri
   if (sl >= run_slices(run)) return;
   const KaonItem it = slice_item(run, sl);
   const KaonTensor& T = D[it.tensor];
-  if (!T.factored || T.n == 0) return;
+  if (!T.factored || T.n == 0 || !T.gc_write) return;
   const int64_t C = T.C, nch = (C + 7) >> 3;
   const bool vec = T.vec_rows != 0;
   const WaveRows wr = wave_rows(it);

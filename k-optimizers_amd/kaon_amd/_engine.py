@@ -119,6 +119,9 @@ class Plan:
             d.factored = 1 if e["factored"] else 0
             d.block4 = int(e.get("block4", 0))
             d.tensor_id = int(e["tensor_id"])
+            d.gc_write = 1 if e.get("gc_write", True) else 0
+        # whether a launch with KAON_F_GC_WRITE would store any tensor's gradient
+        self.any_gc_write = any(e.get("gc_write", True) and e["factored"] for e in entries)
         info = L.KaonPlanInfo()
         args = L.KaonPlanArgs(opt, codec, p_dtype, g_dtype, bf16_method)
         lib = L.lib()

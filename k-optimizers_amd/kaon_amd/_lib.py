@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, BF16, F16 = 0, 1, 2
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -51,6 +51,7 @@ class KaonTensor(ctypes.Structure):
         ("ngroups", ctypes.c_int32), ("sqrt_n", ctypes.c_float),
         ("vec_rows", ctypes.c_int32), ("vec_flat", ctypes.c_int32), ("ns_tr", ctypes.c_int32),
         ("m_pad", ctypes.c_int32), ("k_pad", ctypes.c_int32), ("fast_lanes", ctypes.c_int32),
+        ("gc_write", ctypes.c_int32),
     ]
 
 

@@ -13,8 +13,9 @@ and state come out of one path whatever they say (``fused`` decides only what
 default (``fused=False``, the reference's native path, which centralizes
 ``p.grad`` in place, src/kaon/_backend.py:147-177) stores the centralized
 gradient over ``p.grad`` from the apply kernel (``KAON_F_GC_WRITE``);
-``fused=True`` (the reference's fused path centralizes inside its kernels,
-adakaon.py:387-409) leaves ``p.grad`` as given.
+``fused=True`` does so only for the params the reference's fused step routes
+to its native path (``fused_routes_native``) and leaves the others' ``p.grad``
+as given, as its fused kernels do (adakaon.py:387-409).
 
 Difference from the reference, by design:
 * stochastic rounding draws Philox4x32-10 noise keyed by (``sr_seed``, step,
@@ -31,6 +32,38 @@ from . import _engine as E
 from . import _lib as L
 from ._base import (FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_momentum_state, validate_common,
                     validate_reduction_order)
+
+
+# The reference's one-block tile cap (src/kaon/_fused_triton.py:70): 2^17 padded elements.
+_TILE_CAP = 1 << 17
+
+
+def _next_pow2(n: int) -> int:
+    return 1 << max(int(n) - 1, 0).bit_length()
+
+
+def fused_routes_native(p: torch.Tensor, group: dict[str, Any], tile_cap: int = _TILE_CAP) -> bool:
+    """Whether the reference's ``fused=True`` Adakaon sends a param of 2 or more dims
+    to its native path, which centralizes ``p.grad`` in place (``_fused_partition``,
+    src/kaon/adakaon.py:437-468, with ``fused_eligible`` / ``eff_2d``,
+    src/kaon/_fused_triton.py:100-139): momentum off, a bf16 param without
+    stochastic rounding, a conv (ndim > 2) with int8 / 4-bit momentum, a dtype
+    other than fp32 / bf16, or a one-block tile with 4-bit momentum and an odd
+    row length.  The one-block and big-tensor kernels centralize in their own
+    registers and leave ``p.grad`` as given.  1-D params are never centralized."""
+    if p.ndim < 2 or p.numel() == 0:
+        return False
+    md = group["momentum_dtype"]
+    momentum = group["betas"][0] > 0
+    bf_ok = p.dtype != torch.bfloat16 or group["bf16_method"] == "stochastic_rounding"
+    conv_ok = p.ndim <= 2 or (p.grad is not None and p.grad.is_contiguous() and md in ("bfloat16", "float32"))
+    two_d = momentum and bf_ok and conv_ok and p.is_contiguous() and p.dtype in (torch.float32, torch.bfloat16)
+    R = p.shape[0]
+    C = p.numel() // R
+    tile = _next_pow2(R) * _next_pow2(C)
+    one_block = two_d and tile <= tile_cap and not (md == "4bit" and C % 2 != 0)
+    big = two_d and tile > tile_cap
+    return not (one_block or big)
 
 
 class Adakaon(KaonOptimizer):
@@ -84,9 +117,7 @@ class Adakaon(KaonOptimizer):
         self._foreach_batch_cutoff = foreach_batch_cutoff
         self._foreach_stack_budget = foreach_stack_budget
         self._fused = bool(fused)
-        # the fused path centralizes inside its kernels and leaves p.grad as it was
-        # (adakaon.py:387-409); the native path centralizes p.grad in place
-        self.centralize_grads_in_place = not self._fused
+        self._fused_tile_cap = _TILE_CAP if fused_tile_cap is None else int(fused_tile_cap)
 
     @torch.no_grad()
     def _init_state(self, p: torch.Tensor, state: dict[str, Any], group: dict[str, Any]) -> None:
@@ -103,6 +134,13 @@ class Adakaon(KaonOptimizer):
             init_momentum_state(state, grad, group)
         if p.dtype in (torch.bfloat16, torch.float16) and group["bf16_method"] == "kahan":
             state["shift"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+
+    def _entries(self, group: dict[str, Any], params: list[torch.Tensor], tids: dict[int, int]) -> list[dict]:
+        out = super()._entries(group, params, tids)
+        if self._fused:
+            for e, p in zip(out, params):
+                e["gc_write"] = fused_routes_native(p, group, self._fused_tile_cap)
+        return out
 
     def _hyper(self, group: dict[str, Any], pdt: int, gdt: int, nk: dict | None, gid: int) -> L.KaonHyper:
         beta1, beta2 = group["betas"]
@@ -163,6 +201,8 @@ class Adakaon(KaonOptimizer):
                 continue
             for plan, pdt, gdt, dev in self._launches(gid, group, params, pkey):
                 hp = self._hyper(group, pdt, gdt, nk, gid)
+                if not plan.any_gc_write:
+                    hp.flags &= ~L.F_GC_WRITE
                 L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_adakaon_step")
                 if nk is not None:  # under MSAM / Nekaon the apply carries the perturbation instead

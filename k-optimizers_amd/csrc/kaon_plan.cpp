@@ -69,7 +69,7 @@ int32_t fast_lanes(int64_t C, int64_t gl) {
   return best;
 }
 
-// row class of a slice (phase-1 and phase-3 kernels): 0-2 bf16 grads in
+// row class of a slice (phase 1, AdaPNM's phase 3): 0-2 bf16 grads in
 // 16-byte rows of <= 4, 10, 24 chunks per lane, loaded whole into registers
 // by the prefetching kernels; 3-5 other rows held in registers up to 4, 10
 // and 24 chunks per lane (24 only for bf16 grads); 6 streamed rows
@@ -180,9 +180,10 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     return plan_fail("kaon_plan: unknown param dtype");
   if (g_dtype == KAON_F16 || args->p_dtype == KAON_F16) {
     // fp16 params (RN or kahan writes, _backend.py:82-98) with fp16 grads, on the
-    // generic kernels of Adakaon, Lion, AdaMuon and AdaPNM
-    if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM)
-      return plan_fail("kaon_plan: fp16 params step in Adakaon, Lion, AdaMuon and AdaPNM plans only");
+    // generic kernels of Adakaon, Lion, AdaMuon, AdaPNM and KProdigy
+    if (opt != KAON_OPT_ADAKAON && opt != KAON_OPT_LION && opt != KAON_OPT_ADAMUON && opt != KAON_OPT_ADAPNM &&
+        opt != KAON_OPT_KPRODIGY)
+      return plan_fail("kaon_plan: fp16 params step in Adakaon, Lion, AdaMuon, AdaPNM and KProdigy plans only");
     if (g_dtype != KAON_F16 || args->p_dtype != KAON_F16) return plan_fail("kaon_plan: fp16 params take fp16 grads");
   }
   std::memset(info, 0, sizeof(*info));

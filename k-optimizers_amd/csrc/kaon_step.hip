@@ -64,12 +64,27 @@ int check_launch(const char* what) {
 // Columns per LDS segment of the streamed rows' column fold (phase 1).
 constexpr int kSeg = 4096;
 
+// KProdigy's coupled decay folded into the gradient its second moment sees,
+// g' = fma(wd, p, GC(g)) (_collect_grad, kprodigy.py:406-414; torch's add with
+// alpha is one fused multiply-add), for the generic phase-1 kernel.
+__device__ __forceinline__ void add_coupled_wd(const KaonTensor& T, const KaonHyper& hp, int64_t e0, int cnt, bool vv,
+                                               float x[8]) {
+  float p[8];
+  if (hp.p_dtype == KAON_BF16) ld8<KAON_BF16>(T.p, e0, cnt, vv, p);
+  else if (hp.p_dtype == KAON_F16) ld8<KAON_F16>(T.p, e0, cnt, vv, p);
+  else ld8<KAON_F32>(T.p, e0, cnt, vv, p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = __fmaf_rn(hp.wdl, p[i], x[i]);
+}
+
 // =============================================================== phase 1
 // mode 0 (Adakaon): GC row mean (stored), row EMA of mean_C(G^2), column
 // partial of the slice (wave groups folded in order in LDS); 1-D tensors: v
 // EMA.  mode 1 (Lion): GC row means only.  CPL > 0 keeps a row of up to CPL
 // chunks per lane in registers; CPL == 0 streams the row from memory (used for
 // rows longer than 24 chunks per lane, fp32 grads with long rows, and 1-D).
+// With KAON_F_PD_COUPLED (KProdigy, factored, coupled decay) G is the decayed
+// gradient fma(wd, p, GC(g)); the GC mean is still the raw gradient's.
 template <int GT, int CPL>
 __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict__ D,
                                                    const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
@@ -88,6 +103,7 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const bool vec = T.vec_rows != 0;
   const bool eps = (hp.flags & KAON_F_EPS) != 0;
   const bool alg = clip_alg(hp, mode);
+  const bool cwd = mode == 0 && (hp.flags & KAON_F_PD_COUPLED) != 0;
 
   if (!T.factored) {
     if (mode == 0) stats_1d<GT>(T, gsrc, hp, alg ? ws.scal(T) : nullptr, red4);
@@ -149,6 +165,14 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
         }
       }
       if (mode == 1) continue;
+      if (cwd) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+          const int64_t c = wr.lane + 64 * k;
+          const int cnt = k < cpl ? chunk_cnt(c, C) : 0;
+          if (cnt > 0) add_coupled_wd(T, hp, rowoff + c * 8, cnt, vec && cnt == 8, xb[k]);
+        }
+      }
       float a2 = 0.0f;
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
@@ -193,11 +217,15 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
         if (cnt <= 0) continue;
         float x[8];
         ld8<GT>(gsrc, rowoff + c * 8, cnt, vec && cnt == 8, x);
+        if (gc) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = round_to<GT>(x[i] - mu);
+        }
+        if (cwd) add_coupled_wd(T, hp, rowoff + c * 8, cnt, vec && cnt == 8, x);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           if (i < cnt) {
-            const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
-            float q = gv * gv;
+            float q = x[i] * x[i];
             if (eps) q = q + hp.eps1;
             a2 = a2 + q;
           }
@@ -228,11 +256,15 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
             const int cnt = chunk_cnt(c, C);
             float x[8];
             ld8<GT>(gsrc, r * C + c * 8, cnt, vec && cnt == 8, x);
+            if (gc) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) x[i] = round_to<GT>(x[i] - mu);
+            }
+            if (cwd) add_coupled_wd(T, hp, r * C + c * 8, cnt, vec && cnt == 8, x);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
               if (i < cnt) {
-                const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
-                float v = gv * gv;
+                float v = x[i] * x[i];
                 if (eps) v = v + hp.eps1;
                 const int64_t j = c * 8 + i - c0;
                 lds_col[j] = wf == 0 ? v : lds_col[j] + v;
@@ -2180,8 +2212,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pd_stats(const KaonTensor* __restri
         float gv = 0.0f, pv = 0.0f;
         if (jj < len) {
           const int64_t e = (j0 + jj) * sp;
-          gv = GT == KAON_BF16 ? bf2f(G((const uint16_t*)T.g)[e]) : G((const float*)T.g)[e];
-          pv = PT == KAON_BF16 ? bf2f(G((const uint16_t*)T.p)[e]) : G((const float*)T.p)[e];
+          gv = GT == KAON_F32 ? G((const float*)T.g)[e] : lp2f<GT>(G((const uint16_t*)T.g)[e]);
+          pv = PT == KAON_F32 ? G((const float*)T.p)[e] : lp2f<PT>(G((const uint16_t*)T.p)[e]);
         }
         sg[lane + 64 * u] = gv;
         spv[lane + 64 * u] = pv;
@@ -2312,10 +2344,10 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
       ld8<GT>(T.g, e0, cnt, vec, g);
       const bool need_p = PHASE == 6 || decoupled_wd || (coupled && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT));
       if (need_p) {
-        if (PT == KAON_BF16) {
+        if (PT != KAON_F32) {
           ld8_bits(T.p, e0, cnt, vec, pb);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) p[i] = bf2f(pb[i]);
+          for (int i = 0; i < 8; ++i) p[i] = lp2f<PT>(pb[i]);
         } else {
           ld8<KAON_F32>(T.p, e0, cnt, vec, p);
         }
@@ -2426,16 +2458,20 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
           ld8_bits(T.shift, e0, cnt, vec, sh);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float s = rbf(bf2f(sh[i]) - rbf(dout[i]));
+            // shift -= lp(delta); p0 = p; p += shift; shift += p0 - p, in the
+            // param dtype (_backend.py:90-94)
+            const float s = round_to<PT>(lp2f<PT>(sh[i]) - round_to<PT>(dout[i]));
             const float p0 = p[i];
-            const float p1 = rbf(p0 + s);
-            o[i] = f2bf(p1);
-            sh[i] = f2bf(s + rbf(p0 - p1));
+            const float p1 = round_to<PT>(p0 + s);
+            o[i] = f2lp<PT>(p1);
+            sh[i] = f2lp<PT>(s + round_to<PT>(p0 - p1));
           }
           st8_bits(T.shift, e0, cnt, vec, sh);
-        } else if (hp.bf16_method == KAON_RN) {
+        } else if (hp.bf16_method == KAON_RN || PT == KAON_F16) {
+          // fp16 params are written by RN under "stochastic_rounding" too: the
+          // reference's SR write is bf16-only (_backend.py:95-98)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(p[i] - rbf(dout[i]));
+          for (int i = 0; i < 8; ++i) o[i] = f2lp<PT>(p[i] - round_to<PT>(dout[i]));
         } else {
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = sr_bf16(p[i] - dout[i], nz[i]);
@@ -2771,16 +2807,20 @@ MsamFn msam_fn(int pt, int codec) {
 }
 
 // Phase-1 launches, one per register class run (slices are sorted by class).
+// KProdigy's coupled decay reads p beside g: the prefetching classes 0-2 then
+// run on the register classes 3-5 of the same chunks per lane (the same order).
 int launch_stats(const KaonLaunch& L, Ws ws, const KaonHyper& hp, int mode, hipStream_t st) {
   int32_t off = 0;
+  const bool generic = mode == 0 && (hp.flags & KAON_F_PD_COUPLED) != 0;
   for (int cls = 0; cls < KAON_ROW_CLASSES; ++cls) {
     const int32_t cnt = L.row_runs[cls];
     if (cnt <= 0) continue;
     if (cls < 3 && hp.g_dtype != KAON_BF16) return fail("kaon: prefetching row class planned for non-bf16 grads");
+    const int kcls = generic && cls < 3 ? cls + 3 : cls;
     const int eps = !(hp.flags & KAON_F_EPS) ? 0 : (hp.eps1 == 0.0f || hp.eps1 >= 0x1p-100f) ? 1 : 2;
-    StatsFn fn = stats_fn(hp.g_dtype, cls, eps);
+    StatsFn fn = stats_fn(hp.g_dtype, kcls, eps);
     if (!fn) return fail("kaon: no row-statistics kernel for this grad dtype and row class");
-    const size_t lds = (mode == 0 && cls >= 3) ? sizeof(float) * (size_t)kClassMaxC[cls] : 0;
+    const size_t lds = (mode == 0 && kcls >= 3) ? sizeof(float) * (size_t)kClassMaxC[kcls] : 0;
     hipLaunchKernelGGL(fn, dim3(cnt), dim3(KAON_WG), lds, st, L.descs, L.row_items + off, ws, hp, mode);
     off += cnt;
   }
@@ -2836,6 +2876,7 @@ PdFn pd1_by_codec(int codec) {
   return nullptr;
 }
 PdFn pd1_fn(int pt, int gt, int codec) {
+  if (gt == KAON_F16 && pt == KAON_F16) return pd1_by_codec<KAON_F16, KAON_F16>(codec);
   if (gt == KAON_BF16 && pt == KAON_BF16) return pd1_by_codec<KAON_BF16, KAON_BF16>(codec);
   if (gt == KAON_BF16 && pt == KAON_F32) return pd1_by_codec<KAON_BF16, KAON_F32>(codec);
   if (gt == KAON_F32 && pt == KAON_BF16) return pd1_by_codec<KAON_F32, KAON_BF16>(codec);
@@ -2843,6 +2884,7 @@ PdFn pd1_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 PdStatsFn pd_stats_fn(int pt, int gt) {
+  if (gt == KAON_F16 && pt == KAON_F16) return k_pd_stats<KAON_F16, KAON_F16>;
   if (gt == KAON_BF16 && pt == KAON_BF16) return k_pd_stats<KAON_BF16, KAON_BF16>;
   if (gt == KAON_BF16 && pt == KAON_F32) return k_pd_stats<KAON_BF16, KAON_F32>;
   if (gt == KAON_F32 && pt == KAON_BF16) return k_pd_stats<KAON_F32, KAON_BF16>;
@@ -2862,6 +2904,7 @@ PdFn pd2_by_codec(int codec) {
 }
 template <int PHASE>
 PdFn pd2_fn(int pt, int gt, int codec) {
+  if (pt == KAON_F16 && gt == KAON_F16) return pd2_by_codec<PHASE, KAON_F16, KAON_F16>(codec);
   if (pt == KAON_BF16 && gt == KAON_BF16) return pd2_by_codec<PHASE, KAON_BF16, KAON_BF16>(codec);
   if (pt == KAON_BF16 && gt == KAON_F32) return pd2_by_codec<PHASE, KAON_BF16, KAON_F32>(codec);
   if (pt == KAON_F32 && gt == KAON_BF16) return pd2_by_codec<PHASE, KAON_F32, KAON_BF16>(codec);
@@ -2869,7 +2912,7 @@ PdFn pd2_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon, AdaPNM
+// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon, AdaPNM, KProdigy
 // and the gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
 // rides along (the reference's add_stochastic_ has no fp16 path,
 // _stochastic_rounding.py:55-68).
@@ -2881,7 +2924,7 @@ int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool hal
     return fail("kaon: bad g_dtype");
   if (hp->p_dtype == KAON_F16 || hp->g_dtype == KAON_F16) {
     if (!half_ok)
-      return fail((std::string(who) + ": fp16 params step in Adakaon, Lion, AdaMuon and AdaPNM plans only").c_str());
+      return fail((std::string(who) + ": fp16 params step in Adakaon, Lion, AdaMuon, AdaPNM and KProdigy plans only").c_str());
     if (hp->p_dtype != KAON_F16 || hp->g_dtype != KAON_F16) return fail("kaon: fp16 params take fp16 grads");
     if (hp->flags & (KAON_F_NK_REMOVE | KAON_F_NK_CLIMB))
       return fail("kaon: the Nekaon / MSAM perturbation has no fp16 write (add_stochastic_ is bf16 / fp32 only)");
@@ -3112,7 +3155,7 @@ int kaon_momentum_sumsq(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
 }
 
 int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
-  int rc = validate(L, hp, "kaon_kprodigy_pass1: null argument");
+  int rc = validate(L, hp, "kaon_kprodigy_pass1: null argument", true);
   if (rc) return rc;
   if (hp->flags & KAON_F_TORCH_ORDER)
     return fail("kaon_kprodigy_pass1: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");
@@ -3147,7 +3190,7 @@ int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
 }
 
 int kaon_kprodigy_pass2(const KaonLaunch* L, const KaonHyper* hp, void* stream) {
-  int rc = validate(L, hp, "kaon_kprodigy_pass2: null argument");
+  int rc = validate(L, hp, "kaon_kprodigy_pass2: null argument", true);
   if (rc) return rc;
   if (hp->flags & KAON_F_TORCH_ORDER)
     return fail("kaon_kprodigy_pass2: torch-order sums are built for the Adakaon (Nekaon, MSAM) and Lion steps");

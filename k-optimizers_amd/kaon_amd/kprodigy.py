@@ -15,11 +15,15 @@ passes (``_step_scope``, :306-386):
 * pass 2 on the GPU (``kaon_kprodigy_pass2``): the update with the new ``d`` and
   the ``dlr`` of the old one.
 
-The ``foreach`` knobs are accepted and have no effect.  Not supported here
-(raise): a coupled weight decay (``decouple=False`` with ``weight_decay != 0``)
-together with the factored second moment, and ``factor_conv_as_matrix=False`` on
-conv weights under the factored second moment.  Gradients are read, never
-written; SR noise is keyed by (``sr_seed``, step, param index, element).
+The ``foreach`` knobs are accepted and have no effect.  A coupled weight decay
+(``decouple=False``) folds ``wd * p`` into the gradient of pass 1 (the momentum,
+the full or factored second moment and the D statistics, ``_collect_grad``,
+:406-414).  fp16 params take fp16 grads and are written by RN or kahan, as the
+reference's ``subtract_one_`` writes them.  With gradient centralization on,
+pass 2 leaves ``p.grad`` centralized, as the reference's native path does.  Not
+supported here (raises): ``factor_conv_as_matrix=False`` on conv weights under
+the factored second moment.  SR noise is keyed by (``sr_seed``, step, param
+index, element).
 """
 from __future__ import annotations
 
@@ -38,6 +42,7 @@ from ._base import FOREACH_BATCH_CUTOFF, _FOURBIT_BLOCK, KaonOptimizer, init_mom
 class KProdigy(KaonOptimizer):
     _OPT = L.OPT_KPRODIGY
     _NAME = "KProdigy"
+    _HALF = True  # fp16 params with fp16 grads: RN / kahan writes (subtract_one_, _backend.py:82-98)
 
     def __init__(
         self,
@@ -120,9 +125,6 @@ class KProdigy(KaonOptimizer):
         if factored and p.ndim > 2 and not group["factor_conv_as_matrix"]:
             raise NotImplementedError("kaon_amd: KProdigy factors conv weights as [out, in*kh*kw] matrices "
                                       "(factor_conv_as_matrix=True)")
-        if factored and group["weight_decay"] != 0 and not group["decouple"]:
-            raise NotImplementedError("kaon_amd: KProdigy's factored second moment with a coupled weight decay "
-                                      "(decouple=False) is not supported")
         sliced = p.detach().flatten()[:: group["slice_p"]]
         state["step"] = 0
         state["s"] = torch.zeros_like(sliced, dtype=torch.float32, memory_format=torch.contiguous_format)

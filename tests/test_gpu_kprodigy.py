@@ -43,7 +43,12 @@ def _run_both(case):
         for i, (p, op) in enumerate(zip(gparams, oparams)):
             g = grad_values(case, i, step)
             p.grad = torch.from_numpy(g).to(DEV, gdt)
-            op.g = O.f32_to_bf16(g).reshape(op.shape) if op.g_dtype == O.BF16 else g.copy()
+            if op.g_dtype == O.BF16:
+                op.g = O.f32_to_bf16(g).reshape(op.shape)
+            elif op.g_dtype == O.F16:
+                op.g = O.f32_to_f16(g).reshape(op.shape)
+            else:
+                op.g = g.copy()
         gopt.step()
         oopt.step()
         assert gopt.param_groups[0]["d"] == oopt.group["d"], (step, gopt.param_groups[0]["d"], oopt.group["d"])
@@ -79,6 +84,24 @@ EXTRA = {
                                                   use_bias_correction=True), p="bf16", g="f32"),
     "nomom_growth": _case([[64, 32], [33]], dict(lr=1.0, betas=(0.0, 0.99), growth_rate=1.02, d_coef=2.0,
                                                  safeguard_warmup=True), steps=6),
+    # the factored second moment of the decayed gradient fma(wd, p, GC(g)) (_collect_grad,
+    # kprodigy.py:406-414): every row class (prefetching-class rows on the register kernel,
+    # ragged rows, a row of the widest class, a streamed row of 2500 chunks), int8 momentum
+    "factored_coupled": _case([[96, 48], [32, 16, 3, 3], [33, 45], [40, 1280], [6, 11520], [4, 20000], [77]],
+                              dict(lr=1.0, second_moment="factored", momentum_dtype="int8", decouple=False,
+                                   weight_decay=0.1, cautious=True), steps=3),
+    # fp16 params and grads (RN under "stochastic_rounding", kahan in fp16): full and factored v
+    "f16_full_sr": _case([[48, 40], [16, 8, 3, 3], [70]], dict(lr=1.0, momentum_dtype="int8", weight_decay=0.01,
+                                                              cautious=True), p="f16", g="f16"),
+    "f16_factored_kahan": _case([[64, 48], [33, 45], [20]], dict(lr=1.0, second_moment="factored",
+                                                                 momentum_dtype="bfloat16", bf16_method="kahan",
+                                                                 decouple=False, weight_decay=0.05),
+                                p="f16", g="f16"),
+    # fp32 params under the coupled decay, bf16 grads, 4-bit momentum, no GC
+    "factored_coupled_f32p": _case([[64, 40], [16, 8, 3, 3], [50]],
+                                   dict(lr=1.0, second_moment="factored", momentum_dtype="4bit",
+                                        momentum_4bit_block=32, decouple=False, weight_decay=0.05,
+                                        gradient_centralization=False), p="f32", g="bf16", steps=3),
 }
 
 

@@ -74,12 +74,14 @@ enum {
                                centralized gradient over p.grad of the tensors whose
                                gc_write is set, as the reference's native path leaves it
                                (centralize_grads_, _backend.py:147-177) */
-  KAON_F_TORCH_ORDER = 8192 /* Adakaon / Lion steps and kaon_momentum_sumsq: the step's fp32
+  KAON_F_TORCH_ORDER = 8192, /* Adakaon / Lion steps and kaon_momentum_sumsq: the step's fp32
                                sums in torch CPU's order instead of the canonical 64-lane one
                                (below): the GC row means (_backend.py:147-177), the factored
                                row / column means and the row factors' mean (_factored.py:48-52,
                                76-82), the RMS clip norm (_backend.py:45-47), MSAM's per-tensor
                                momentum norm (msam.py:219-221) */
+  KAON_F_PD_BLOCKFAC = 16384 /* KProdigy pass 1: some tensor of the plan has fb_r > 0 (its
+                                second moment factored over its last two dims) */
 };
 
 /*
@@ -141,6 +143,10 @@ typedef struct KaonTensor {
                              over g, 0 = leave g as given (the reference's fused Adakaon
                              centralizes p.grad in place only for the params it routes to its
                              native path, adakaon.py:396-401, 448-468) */
+  int32_t fb_r, fb_c;     /* KProdigy factor_conv_as_matrix=False on a tensor of 3+ dims: the
+                             second moment is factored over its last two dims, blocks of
+                             [fb_r, fb_c] elements ("row" [n / fb_c], "col" [n / fb_r],
+                             kprodigy.py:286-288); 0 = the [R, C] factoring */
 } KaonTensor;
 
 /* A work item.  Runs and slices: rows [row0, row0 + nrows) of tensor

@@ -238,8 +238,15 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
         return plan_fail("kaon_plan: KProdigy tensor " + std::to_string(i) + " has pd_ns != ceil(n / slice_p)");
       if (t.R * t.C > 0 && (!t.pd_s || !t.pd_p0))
         return plan_fail("kaon_plan: KProdigy tensor " + std::to_string(i) + " needs s and p0");
+      if (t.fb_r != 0 || t.fb_c != 0) {
+        // factored over the last two dims: whole blocks inside each matrixized row
+        if (t.fb_r < 1 || t.fb_c < 1 || t.full_v || !t.factored || t.C % ((int64_t)t.fb_r * t.fb_c) != 0)
+          return plan_fail("kaon_plan: KProdigy tensor " + std::to_string(i) +
+                           " has a bad block factoring (fb_r x fb_c must divide its rows)");
+      }
     } else {
       t.full_v = 0;
+      t.fb_r = t.fb_c = 0;
     }
     if (opt == KAON_OPT_ADAPNM && (!t.m || !t.m2))
       return plan_fail("kaon_plan: AdaPNM tensor " + std::to_string(i) + " needs both momentum buffers (m, m2)");
@@ -253,7 +260,12 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     off = round4(off + 5 * t.R);
     t.ws_col = off;
     t.ws_part = off;
-    if (t.factored && !t.full_v) {
+    if (t.fb_r > 0) {
+      // block factoring: the blocks' column factors [n / fb_r], then their row factors [n / fb_c]
+      off = round4(off + t.n / t.fb_r);
+      t.ws_part = off;
+      off = round4(off + t.n / t.fb_c);
+    } else if (t.factored && !t.full_v) {
       off = round4(off + t.C);
       t.ws_part = off;
       // the column partials of G^2 and, after them, of the clip's G^2 / row
@@ -333,7 +345,7 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
       }
     }
     // finalize items (the factored second moment of every optimizer but Lion)
-    if (t.factored && !t.full_v && opt != KAON_OPT_LION) {
+    if (t.factored && !t.full_v && t.fb_r == 0 && opt != KAON_OPT_LION) {
       for (int64_t c0 = 0; c0 < t.C; c0 += KAON_COLITEM)
         fins.push_back(KaonItem{i, (int32_t)c0, (int32_t)std::min<int64_t>(KAON_COLITEM, t.C - c0), 0});
       fins.push_back(KaonItem{i, 0, (int32_t)t.R, 1});

@@ -94,7 +94,8 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   __shared__ float red4[4];
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
-  if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
+  // KProdigy's per-element v and its block-factored tensors: their own pass 1 kernels
+  if (T.full_v || T.fb_r) return;
   zero_accumulators(T, it, ws, hp.codec);
   const void* gsrc = ws.src(T, hp.flags);
   const int64_t C = T.C;
@@ -738,7 +739,8 @@ __device__ __forceinline__ void pf_stats_run(const KaonTensor* __restrict__ D, c
                                              float* racc, float* racc2) {
   const KaonItem it = items[blockIdx.x];
   const KaonTensor& T = D[it.tensor];
-  if (T.full_v) return;  // KProdigy's per-element v: its own pass 1 kernel
+  // KProdigy's per-element v and its block-factored tensors: their own pass 1 kernels
+  if (T.full_v || T.fb_r) return;
   zero_accumulators(T, it, ws, hp.codec);
   const int cpl = (int)(((T.C >> 3) + 63) >> 6);
   KAON_G float* part = run_part(ws, T, it);
@@ -2135,6 +2137,65 @@ __global__ __launch_bounds__(KAON_WG) void k_pd1(const KaonTensor* __restrict__ 
   if (CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
 }
 
+// One element of a 16-bit or fp32 tensor, as fp32.
+template <int DT>
+__device__ __forceinline__ float ld1(const void* base, int64_t e) {
+  return DT == KAON_F32 ? G((const float*)base)[e] : lp2f<DT>(G((const uint16_t*)base)[e]);
+}
+
+// Pass 1 for the tensors whose second moment is factored over their last two
+// dims (factor_conv_as_matrix=False, kprodigy.py:286-288; update_factored_state
+// and factored_inv_sqrt_factors, _factored.py:48-83, on the unreshaped weight):
+// one thread per [fb_r, fb_c] block.  q = g'^2 (+eps1), g' = GC(g) with the row
+// means k_pd1 stored (plus wd * p under the coupled decay); row[b, a] =
+// lerp(row, mean_c q, 1-beta2), col[b, c] = lerp(col, mean_a q, 1-beta2), every
+// sum sequential from +0.0f; then the block's factors for pass 2, c = 1 /
+// sqrt(col) into the workspace's column words and r = 1 / sqrt(row / mean_a row)
+// into its partial words.  Workgroup (t, y) takes tensor t's blocks y*256 + tid,
+// stepping by gridDim.y * 256.
+template <int GT, int PT>
+__global__ __launch_bounds__(KAON_WG) void k_pd_bfac(const KaonTensor* __restrict__ D, Ws ws, KaonHyper hp) {
+  const KaonTensor& T = D[blockIdx.x];
+  if (T.fb_r <= 0 || T.n == 0) return;
+  const int64_t Rb = T.fb_r, Cb = T.fb_c, bsz = Rb * Cb, nb = T.n / bsz;
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  const bool coupled = (hp.flags & KAON_F_PD_COUPLED) != 0;
+  const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  KAON_G float* cfb = ws.cf(T);
+  KAON_G float* rfb = ws.part(T);
+  KAON_G float* row = G(T.row);
+  KAON_G float* col = G(T.col);
+  for (int64_t b = (int64_t)blockIdx.y * KAON_WG + threadIdx.x; b < nb; b += (int64_t)gridDim.y * KAON_WG) {
+    const int64_t e0 = b * bsz;
+    const float mu = gc ? ws.mu(T)[e0 / T.C] : 0.0f;
+    auto q = [&](int64_t e) {
+      float x = ld1<GT>(T.g, e);
+      if (gc) x = round_to<GT>(x - mu);
+      if (coupled) x = __fmaf_rn(hp.wdl, ld1<PT>(T.p, e), x);
+      float v = x * x;
+      if (eps) v = v + hp.eps1;
+      return v;
+    };
+    float rsum = 0.0f;
+    for (int64_t a = 0; a < Rb; ++a) {
+      float s = 0.0f;
+      for (int64_t c = 0; c < Cb; ++c) s = s + q(e0 + a * Cb + c);
+      const float nr = klerp(row[b * Rb + a], s / (float)Cb, hp.w2);
+      row[b * Rb + a] = nr;
+      rsum = rsum + nr;
+    }
+    for (int64_t c = 0; c < Cb; ++c) {
+      float s = 0.0f;
+      for (int64_t a = 0; a < Rb; ++a) s = s + q(e0 + a * Cb + c);
+      const float nc = klerp(col[b * Cb + c], s / (float)Rb, hp.w2);
+      col[b * Cb + c] = nc;
+      cfb[b * Cb + c] = 1.0f / sqrtf(nc);
+    }
+    const float rm = rsum / (float)Rb;
+    for (int64_t a = 0; a < Rb; ++a) rfb[b * Rb + a] = 1.0f / sqrtf(row[b * Rb + a] / rm);
+  }
+}
+
 // Pass 1, D statistics: one wave per flat item of KAON_FLAT_ITEM sliced
 // elements j (element j * slice_p): s_j = fma(alpha_s, g', s_j * beta3), and the
 // item's sums of g' (p0 - p) and |s| in the 64-lane order (lane l adds chunks
@@ -2323,7 +2384,8 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
   double c_r = 1.0;
   for (int64_t r = wr.rb; r < wr.re; ++r) {
     const float mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    const float rf = factored ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    // block-factored tensors: r and c come per element (f below), the row factor is 1
+    const float rf = factored ? (T.fb_r ? 1.0f : uniform_f(ws.rf(T)[r])) : 0.0f;
     float oldsc = 1.0f, newsc = 1.0f;
     double rnew = 1.0;
     if (CODEC == KAON_MOM_INT8) {
@@ -2356,8 +2418,22 @@ __global__ __launch_bounds__(KAON_WG) void k_pd2(const KaonTensor* __restrict__ 
         for (int i = 0; i < 8; ++i) p[i] = 0.0f;
       }
       if (CODEC != KAON_MOM_NONE) ld_mom_at<CODEC>(T.m, e0, cnt, vec, mq);
-      if (factored) ld8<KAON_F32>((const float*)ws.cf(T), j0, cnt, vec, f);
-      else ld8<KAON_F32>(T.v, e0, cnt, vec, f);
+      if (factored && T.fb_r) {
+        // r c of each element's [fb_r, fb_c] block (n < 2^31: 32-bit indices)
+        const uint32_t Rb = (uint32_t)T.fb_r, Cb = (uint32_t)T.fb_c, bsz = Rb * Cb;
+        const KAON_G float* cfb = ws.cf(T);
+        const KAON_G float* rfb = ws.part(T);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t e = (uint32_t)(e0 + min(i, cnt - 1));
+          const uint32_t b = e / bsz, w = e - b * bsz, a = w / Cb, c = w - a * Cb;
+          f[i] = rfb[b * Rb + a] * cfb[b * Cb + c];
+        }
+      } else if (factored) {
+        ld8<KAON_F32>((const float*)ws.cf(T), j0, cnt, vec, f);
+      } else {
+        ld8<KAON_F32>(T.v, e0, cnt, vec, f);
+      }
       uint32_t nz[8];
       if (PHASE == 6 && lowp && hp.bf16_method == KAON_SR) {
         if ((e0 & 7) == 0) noise8(hp.seed, hp.step, (uint32_t)T.tensor_id, 1u, e0, T.noise[1], cnt, nz);
@@ -2883,6 +2959,15 @@ PdFn pd1_fn(int pt, int gt, int codec) {
   if (gt == KAON_F32 && pt == KAON_F32) return pd1_by_codec<KAON_F32, KAON_F32>(codec);
   return nullptr;
 }
+using PdBfacFn = void (*)(const KaonTensor*, Ws, KaonHyper);
+PdBfacFn pd_bfac_fn(int pt, int gt) {
+  if (gt == KAON_F16 && pt == KAON_F16) return k_pd_bfac<KAON_F16, KAON_F16>;
+  if (gt == KAON_BF16 && pt == KAON_BF16) return k_pd_bfac<KAON_BF16, KAON_BF16>;
+  if (gt == KAON_BF16 && pt == KAON_F32) return k_pd_bfac<KAON_BF16, KAON_F32>;
+  if (gt == KAON_F32 && pt == KAON_BF16) return k_pd_bfac<KAON_F32, KAON_BF16>;
+  if (gt == KAON_F32 && pt == KAON_F32) return k_pd_bfac<KAON_F32, KAON_F32>;
+  return nullptr;
+}
 PdStatsFn pd_stats_fn(int pt, int gt) {
   if (gt == KAON_F16 && pt == KAON_F16) return k_pd_stats<KAON_F16, KAON_F16>;
   if (gt == KAON_BF16 && pt == KAON_BF16) return k_pd_stats<KAON_BF16, KAON_BF16>;
@@ -3180,6 +3265,13 @@ int kaon_kprodigy_pass1(const KaonLaunch* L, const KaonHyper* hp, void* stream) 
   }
   hipLaunchKernelGGL(f1, dim3(L->n_row_items), dim3(KAON_WG), 0, st, L->descs, L->row_items, ws, h);
   if ((rc = check_launch("kaon: KProdigy pass-1 launch"))) return rc;
+  if (h.flags & KAON_F_PD_BLOCKFAC) {
+    // after k_pd1: the block-factored second moment reads its GC means
+    PdBfacFn fb = pd_bfac_fn(h.p_dtype, h.g_dtype);
+    if (!fb) return fail("kaon_kprodigy_pass1: unsupported dtype combination");
+    hipLaunchKernelGGL(fb, dim3(L->n_tensors, 64), dim3(KAON_WG), 0, st, L->descs, ws, h);
+    if ((rc = check_launch("kaon: KProdigy block-factored launch"))) return rc;
+  }
   if ((h.flags & KAON_F_PD_STATS) && L->n_flat_items > 0) {
     hipLaunchKernelGGL(fs, dim3((L->n_flat_items + 3) / 4), dim3(KAON_WG), 0, st, L->descs, L->flat_items,
                        L->n_flat_items, ws, h);

@@ -85,7 +85,9 @@ def _check_state(e: dict[str, Any], codec: int, i: int) -> None:
             need(key, m, _MOM_DTYPE[codec], n)
             if codec == L.MOM_INT8:
                 need(skey, e.get(skey), torch.float32, R if e["factored"] else 1)
-    for key, numel in (("row", R), ("col", C), ("v", n), ("max_v", n)):
+    fb_r, fb_c = e.get("fb", (0, 0))
+    rows, cols = (n // fb_c, n // fb_r) if fb_r else (R, C)
+    for key, numel in (("row", rows), ("col", cols), ("v", n), ("max_v", n)):
         t = e.get(key)
         if t is not None:
             need(key, t, torch.float32, numel)
@@ -120,8 +122,11 @@ class Plan:
             d.block4 = int(e.get("block4", 0))
             d.tensor_id = int(e["tensor_id"])
             d.gc_write = 1 if e.get("gc_write", True) else 0
+            d.fb_r, d.fb_c = e.get("fb", (0, 0))
         # whether a launch with KAON_F_GC_WRITE would store any tensor's gradient
         self.any_gc_write = any(e.get("gc_write", True) and e["factored"] for e in entries)
+        # whether a tensor's second moment is factored over its last two dims (KProdigy)
+        self.any_fb = any(e.get("fb") for e in entries)
         info = L.KaonPlanInfo()
         args = L.KaonPlanArgs(opt, codec, p_dtype, g_dtype, bf16_method)
         lib = L.lib()

@@ -24,6 +24,7 @@ OPT_ADAKAON, OPT_LION, OPT_ADAMUON, OPT_ADAPNM, OPT_KPRODIGY = 0, 1, 2, 3, 4
 F_GC, F_CAUTIOUS, F_WD, F_EPS, F_MOMENTUM, F_NK_REMOVE, F_NK_CLIMB, F_SRC_O = 1, 2, 4, 8, 16, 32, 64, 128
 F_GC_WRITE = 4096
 F_TORCH_ORDER = 8192
+F_PD_BLOCKFAC = 16384
 F_PNM, F_AMS, F_PD_COUPLED, F_PD_STATS = 256, 512, 1024, 2048
 
 ROW_BUDGET = 20
@@ -51,7 +52,7 @@ class KaonTensor(ctypes.Structure):
         ("ngroups", ctypes.c_int32), ("sqrt_n", ctypes.c_float),
         ("vec_rows", ctypes.c_int32), ("vec_flat", ctypes.c_int32), ("ns_tr", ctypes.c_int32),
         ("m_pad", ctypes.c_int32), ("k_pad", ctypes.c_int32), ("fast_lanes", ctypes.c_int32),
-        ("gc_write", ctypes.c_int32),
+        ("gc_write", ctypes.c_int32), ("fb_r", ctypes.c_int32), ("fb_c", ctypes.c_int32),
     ]
 
 
@@ -103,7 +104,7 @@ class KaonHyper(ctypes.Structure):
     ]
 
 
-assert ctypes.sizeof(KaonTensor) == 272, ctypes.sizeof(KaonTensor)
+assert ctypes.sizeof(KaonTensor) == 280, ctypes.sizeof(KaonTensor)
 assert ctypes.sizeof(KaonItem) == 16
 assert ctypes.sizeof(KaonHyper) == 144, ctypes.sizeof(KaonHyper)
 

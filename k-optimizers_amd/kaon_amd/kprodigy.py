@@ -20,10 +20,12 @@ The ``foreach`` knobs are accepted and have no effect.  A coupled weight decay
 the full or factored second moment and the D statistics, ``_collect_grad``,
 :406-414).  fp16 params take fp16 grads and are written by RN or kahan, as the
 reference's ``subtract_one_`` writes them.  With gradient centralization on,
-pass 2 leaves ``p.grad`` centralized, as the reference's native path does.  Not
-supported here (raises): ``factor_conv_as_matrix=False`` on conv weights under
-the factored second moment.  SR noise is keyed by (``sr_seed``, step, param
-index, element).
+pass 2 leaves ``p.grad`` centralized, as the reference's native path does.
+``factor_conv_as_matrix=False`` factors the second moment of a weight of 3+
+dims over its last two dims (``row`` of shape[:-1], ``col`` of shape[:-2] +
+shape[-1:]), each [kh, kw] block on its own, as the reference's per-param path
+does (its foreach path cannot unpack those shapes).  SR noise is keyed by
+(``sr_seed``, step, param index, element).
 """
 from __future__ import annotations
 
@@ -122,9 +124,6 @@ class KProdigy(KaonOptimizer):
     def _init_state(self, p: torch.Tensor, state: dict[str, Any], group: dict[str, Any]) -> None:
         """kprodigy.py:262-291."""
         factored = group["second_moment"] == "factored" and p.ndim >= 2
-        if factored and p.ndim > 2 and not group["factor_conv_as_matrix"]:
-            raise NotImplementedError("kaon_amd: KProdigy factors conv weights as [out, in*kh*kw] matrices "
-                                      "(factor_conv_as_matrix=True)")
         sliced = p.detach().flatten()[:: group["slice_p"]]
         state["step"] = 0
         state["s"] = torch.zeros_like(sliced, dtype=torch.float32, memory_format=torch.contiguous_format)
@@ -134,7 +133,11 @@ class KProdigy(KaonOptimizer):
             state["p0"] = torch.zeros((), device=p.device, dtype=torch.float32)
         if group["betas"][0] > 0:
             init_momentum_state(state, p, group)
-        if factored:
+        if factored and p.ndim > 2 and not group["factor_conv_as_matrix"]:
+            # factored over the last two dims, blocks of [shape[-2], shape[-1]] (kprodigy.py:286-288)
+            state["row"] = torch.zeros(p.shape[:-1], dtype=torch.float32, device=p.device)
+            state["col"] = torch.zeros(p.shape[:-2] + p.shape[-1:], dtype=torch.float32, device=p.device)
+        elif factored:
             R = p.shape[0]
             state["row"] = torch.zeros((R,), dtype=torch.float32, device=p.device)
             state["col"] = torch.zeros((p.numel() // R if R else 0,), dtype=torch.float32, device=p.device)
@@ -148,6 +151,8 @@ class KProdigy(KaonOptimizer):
         for e, p in zip(out, params):
             st = self.state[p]
             e.update(pd_s=st["s"], pd_p0=st["p0"], pd_slice=group["slice_p"], full_v="v" in st)
+            if "row" in st and st["row"].dim() > 1:  # factored over the last two dims
+                e["fb"] = (int(p.shape[-2]), int(p.shape[-1]))
         return out
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],
@@ -247,6 +252,8 @@ class KProdigy(KaonOptimizer):
             per_group.append((group, params, launches))
             for plan, pdt, gdt, dev, positions, stat_idx in launches:
                 hp = self._hyper(group, pdt, gdt, c)
+                if plan.any_fb:
+                    hp.flags |= L.F_PD_BLOCKFAC
                 L.check(lib.kaon_kprodigy_pass1(ctypes.byref(plan.launch), ctypes.byref(hp),
                                                 E.stream_handle(dev)), "kaon_kprodigy_pass1")
                 if group["lr"] > 0.0 and should_update_d:

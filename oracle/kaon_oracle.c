@@ -294,6 +294,10 @@ typedef struct {
      * the canonical one (the GPU's reduction_order="torch" mode). */
     int32_t torch_order;
     float* ss_out;       /* optional: the clip's sum of squares as used (diagnostics) */
+    /* KProdigy factor_conv_as_matrix=False on a tensor of 3+ dims: the second
+     * moment is factored over its last two dims, blocks of [fb_r, fb_c] (row
+     * [n / fb_c], col [n / fb_r]); 0 = the matrixized [R, C] factoring */
+    int64_t fb_r, fb_c;
 } KoTensor;
 
 typedef struct {
@@ -991,6 +995,53 @@ static float* pd_grad(const KoTensor* t, const KoHyper* h) {
     return g;
 }
 
+/* The second moment factored over a tensor's last two dims (KProdigy with
+ * factor_conv_as_matrix=False, kprodigy.py:286-288; update_factored_state,
+ * _factored.py:48-52, on the unreshaped gradient): each block b of fb_r x fb_c
+ * elements has row[b, a] = lerp(row, mean_c q, w2) and col[b, c] = lerp(col,
+ * mean_a q, w2), q = g^2 (+eps1).  Sums sequential from +0.0f (the canonical
+ * order of these blocks; for blocks of at most 8 x 8 it is also the 64-lane
+ * order of the matrix factoring, whose single lane and single wave group add
+ * the same terms in the same order). */
+static void block_factored_state(const KoTensor* t, const float* x, float w2, float eps1f, int add_eps) {
+    const int64_t Rb = t->fb_r, Cb = t->fb_c, nb = (t->R * t->C) / (Rb * Cb);
+    for (int64_t b = 0; b < nb; ++b) {
+        const float* xb = x + b * Rb * Cb;
+        for (int64_t a = 0; a < Rb; ++a) {
+            float s = 0.0f;
+            for (int64_t c = 0; c < Cb; ++c) {
+                float q = xb[a * Cb + c] * xb[a * Cb + c];
+                if (add_eps) q = q + eps1f;
+                s = s + q;
+            }
+            t->row[b * Rb + a] = ko_lerp(t->row[b * Rb + a], s / (float)Cb, w2);
+        }
+        for (int64_t c = 0; c < Cb; ++c) {
+            float s = 0.0f;
+            for (int64_t a = 0; a < Rb; ++a) {
+                float q = xb[a * Cb + c] * xb[a * Cb + c];
+                if (add_eps) q = q + eps1f;
+                s = s + q;
+            }
+            t->col[b * Cb + c] = ko_lerp(t->col[b * Cb + c], s / (float)Rb, w2);
+        }
+    }
+}
+
+/* factored_inv_sqrt_factors (_factored.py:62-83) per block: r = rsqrt(row /
+ * mean over the block's rows), c = rsqrt(col), into rf [n / fb_c] and cf
+ * [n / fb_r]; the mean a sequential sum / fb_r. */
+static void block_factored_factors(const KoTensor* t, float* rf, float* cf) {
+    const int64_t Rb = t->fb_r, Cb = t->fb_c, nb = (t->R * t->C) / (Rb * Cb);
+    for (int64_t b = 0; b < nb; ++b) {
+        float s = 0.0f;
+        for (int64_t a = 0; a < Rb; ++a) s = s + t->row[b * Rb + a];
+        const float rm = s / (float)Rb;
+        for (int64_t a = 0; a < Rb; ++a) rf[b * Rb + a] = ko_rsqrt(t->row[b * Rb + a] / rm);
+        for (int64_t c = 0; c < Cb; ++c) cf[b * Cb + c] = ko_rsqrt(t->col[b * Cb + c]);
+    }
+}
+
 /* Pass 1 of one tensor (_pass1_per_param body, kprodigy.py:392-441): the D
  * statistics over every pd_slice-th element (num = FSUM(g * (p0 - p)), the s
  * EMA s*beta3 + alpha_s*g, den = FSUM(|s|)), the first moment of d*g in its
@@ -1049,6 +1100,8 @@ int ko_kprodigy_pass1_tensor(const KoTensor* t, const KoHyper* h, float* num_out
     if (t->full_v || !t->factored) {
         const float val = (float)(h->pd_d * h->pd_d * (1.0 - h->beta2)), b2 = (float)h->beta2;
         for (int64_t i = 0; i < n; ++i) t->v[i] = fmaf(val * g[i], g[i], t->v[i] * b2);
+    } else if (t->fb_r > 0) {
+        block_factored_state(t, g, (float)(1.0 - h->beta2), (float)h->eps1, h->eps1 > 0);
     } else {
         factored_state(t, g, (float)(1.0 - h->beta2), (float)h->eps1, h->eps1 > 0, NULL, NULL, NULL);
     }
@@ -1072,6 +1125,18 @@ int ko_kprodigy_pass2_tensor(const KoTensor* t, const KoHyper* h) {
     if (t->full_v || !t->factored) {
         const float floor = (float)(h->pd_d * h->pd_eps);
         for (int64_t i = 0; i < n; ++i) d[i] = d[i] / fmaxf(sqrtf(t->v[i]), floor);
+    } else if (t->fb_r > 0) {
+        const int64_t Rb = t->fb_r, Cb = t->fb_c;
+        float* rf = (float*)malloc(sizeof(float) * (size_t)(n / Cb));
+        float* cf = (float*)malloc(sizeof(float) * (size_t)(n / Rb));
+        block_factored_factors(t, rf, cf);
+        const float cap = (float)(1.0 / (h->pd_d * h->pd_eps));
+        for (int64_t i = 0; i < n; ++i) {
+            const int64_t b = i / (Rb * Cb), a = (i / Cb) % Rb, c = i % Cb;
+            const float inv = fminf((rf[b * Rb + a] * cf[b * Cb + c]) / df, cap);
+            d[i] = d[i] * inv;
+        }
+        free(rf); free(cf);
     } else {
         float* rf = (float*)malloc(sizeof(float) * (size_t)t->R);
         float* cf = (float*)malloc(sizeof(float) * (size_t)t->C);

@@ -74,6 +74,7 @@ class KoTensor(ctypes.Structure):
         ("pd_slice", ctypes.c_int32), ("full_v", ctypes.c_int32),
         ("torch_order", ctypes.c_int32),
         ("ss_out", ctypes.c_void_p),
+        ("fb_r", ctypes.c_int64), ("fb_c", ctypes.c_int64),
     ]
 
 
@@ -382,8 +383,13 @@ def init_state(prm: OParam, opt: str, group: dict[str, Any]) -> None:
         if group["betas"][0] > 0:
             _alloc_momentum(st, "m", prm, group)
         if group["second_moment"] == "factored" and prm.factored:
-            st["row"] = np.zeros(R, dtype=np.float32)
-            st["col"] = np.zeros(C, dtype=np.float32)
+            if len(prm.shape) > 2 and not group.get("factor_conv_as_matrix", True):
+                # factored over the last two dims (kprodigy.py:286-288)
+                st["row"] = np.zeros(prm.shape[:-1], dtype=np.float32)
+                st["col"] = np.zeros(prm.shape[:-2] + prm.shape[-1:], dtype=np.float32)
+            else:
+                st["row"] = np.zeros(R, dtype=np.float32)
+                st["col"] = np.zeros(C, dtype=np.float32)
         else:
             st["v"] = np.zeros(prm.shape, dtype=np.float32)
         if prm.p_dtype in (BF16, F16) and group.get("bf16_method") == "kahan":
@@ -473,6 +479,8 @@ def _pd_tensor(prm: OParam, group: dict[str, Any], noise=None) -> KoTensor:
         t.pd_p0, t.pd_np0 = _ptr(p0), p0.size
     t.pd_slice = int(group["slice_p"])
     t.full_v = int("v" in st)
+    if "row" in st and st["row"].ndim > 1:  # factored over the last two dims
+        t.fb_r, t.fb_c = prm.shape[-2], prm.shape[-1]
     return t
 
 

@@ -131,6 +131,13 @@ CASES = {
                                                     foreach=False), steps=6),
     "pd_kahan": _case("kprodigy", _SMALL, dict(lr=1.0, momentum_dtype="bfloat16", bf16_method="kahan",
                                                second_moment="factored", foreach=False), steps=6),
+    # factor_conv_as_matrix=False: the second moment of the 3-D / 4-D weights factored over
+    # their last two dims (kprodigy.py:286-288); the reference's foreach path cannot unpack
+    # those shapes (kprodigy.py:689, 866), so its per-param path
+    "pd_conv_blockfac": _case("kprodigy", [[8, 6, 3, 3], [4, 5, 3, 2], [6, 5, 4], [24, 20], [30]],
+                              dict(lr=1.0, momentum_dtype="bfloat16", second_moment="factored",
+                                   factor_conv_as_matrix=False, cautious=True, weight_decay=0.01,
+                                   foreach=False), steps=6),
 }
 
 # Adakaon on a conv [320,320,3,3] and a linear [1280,1280],

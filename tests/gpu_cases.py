@@ -57,7 +57,7 @@ def make_opt(case, params, group=None, extra=None):
         kw = {k: g[k] for k in ("lr", "betas", "beta3", "eps", "weight_decay", "decouple", "use_bias_correction",
                                 "safeguard_warmup", "d0", "d_coef", "growth_rate", "d_update_freq", "slice_p",
                                 "momentum_dtype", "momentum_4bit_block", "second_moment", "eps_factored", "cautious",
-                                "gradient_centralization", "bf16_method")}
+                                "gradient_centralization", "bf16_method", "factor_conv_as_matrix")}
         opt = KProdigy(params, **kw)
         opt.sr_seed = case["seed"]
     elif name == "adapnm":

@@ -97,6 +97,18 @@ EXTRA = {
                                                                  momentum_dtype="bfloat16", bf16_method="kahan",
                                                                  decouple=False, weight_decay=0.05),
                                 p="f16", g="f16"),
+    # factor_conv_as_matrix=False: the second moment of the 3-D / 4-D weights factored over
+    # their last two dims, each [kh, kw] block on its own (k_pd_bfac)
+    "blockfac_int8": _case([[16, 8, 3, 3], [6, 5, 4], [32, 24], [20]],
+                           dict(lr=1.0, second_moment="factored", factor_conv_as_matrix=False,
+                                momentum_dtype="int8", cautious=True, weight_decay=0.01), steps=3),
+    "blockfac_coupled_f32p": _case([[8, 4, 5, 3], [12, 10]],
+                                   dict(lr=1.0, second_moment="factored", factor_conv_as_matrix=False,
+                                        momentum_dtype="4bit", momentum_4bit_block=16, decouple=False,
+                                        weight_decay=0.05), p="f32", g="bf16", steps=3),
+    "blockfac_sdxl_conv": _case([[320, 320, 3, 3]], dict(lr=1.0, second_moment="factored",
+                                                         factor_conv_as_matrix=False, momentum_dtype="bfloat16"),
+                                steps=2),
     # fp32 params under the coupled decay, bf16 grads, 4-bit momentum, no GC
     "factored_coupled_f32p": _case([[64, 40], [16, 8, 3, 3], [50]],
                                    dict(lr=1.0, second_moment="factored", momentum_dtype="4bit",

@@ -113,10 +113,16 @@ typedef __bf16 kbf16x2 __attribute__((ext_vector_type(2)));
 // gives inf (a NaN whose payload sits in the low half plus a carry-free noise)
 // or 0x7FC0, the instruction some NaN, so a chunk with a NaN anywhere in the
 // wave takes the trick itself.  nzh: noise in the high halves.
-__device__ __forceinline__ ku4 sr_chunk(const float x[8], const uint32_t nzh[8]) {
+// CLEAN: the caller has shown that no x is NaN (no ballots); nan_out receives
+// the wave's NaN ballot otherwise.
+template <bool CLEAN = false>
+__device__ __forceinline__ ku4 sr_chunk(const float x[8], const uint32_t nzh[8], uint64_t* nan_out = nullptr) {
   uint64_t nan = 0;
+  if (!CLEAN) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) nan |= __builtin_amdgcn_ballot_w64(x[i] != x[i]);
+    for (int i = 0; i < 8; ++i) nan |= __builtin_amdgcn_ballot_w64(x[i] != x[i]);
+  }
+  if (nan_out) *nan_out = nan;
   uint32_t w[4];
   if (nan == 0) {
 #pragma unroll
@@ -234,9 +240,10 @@ __device__ __forceinline__ void fast_settle(const FastIn& in) {
   }
 }
 
-// FAC1: clip divisor 1 (skip the exact division).  DQX: int8 dequant as
-// q*scale for rows whose old scale (AdaPNM: either buffer's) is too large for
-// the fma form.  WLO: the momentum lerp weight is below 0.5 (its branch of
+// FAC1: clip divisor 1 (skip the exact division).  DQX: a wave some of whose
+// momentum scales are too large for the fma dequant form (int8 q*scale; AdaPNM:
+// either buffer's) or, with int8 / 4-bit momentum outside AdaPNM and AdaMuon,
+// whose new scales or Nekaon factor are not below 2^120 (the NaN-safe clamps).  WLO: the momentum lerp weight is below 0.5 (its branch of
 // torch's lerp).
 template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX, bool WLO>
 __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, const KaonHyper& hp, uint32_t e0,
@@ -299,17 +306,29 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   if (PHASE == 6) noise8_hi(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
   if (PHASE == 6 && NKC) noise8_hi(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
 
+  // !DQX (int8, 4-bit): every lane's momentum scales are below 2^120 (the
+  // caller's wave-wide test, with the new scales and a finite Nekaon factor in
+  // the apply).  Then each dequantized momentum and each perturbation before
+  // its clamp is a finite number: the clamps need no NaN case, the climb's
+  // input is NaN only where the update's was, and a code dequantizes as
+  // fma(code, s, -128 s) / fma(code, s, -8 s), exact since -128 s / -8 s and
+  // the sum are then one rounding of (code - 128) s / (code - 8) s.
+  constexpr bool SANE = !DQX && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON;
   float mold[8];
+  // 4-bit: the codes as floats, from the bytes of the even and the odd nibbles
+  const uint32_t nlo = m4 & 0x0F0F0F0Fu, nhi = (m4 >> 4) & 0x0F0F0F0Fu;
+  const float b8 = -8.0f * b_old;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    if (CODEC == KAON_MOM_INT8) {
+    if (CODEC == KAON_MOM_4BIT) {
+      const float cv = (float)((((i & 1) ? nhi : nlo) >> (8 * (i >> 1))) & 0xFFu);
+      mold[i] = SANE ? __fmaf_rn(cv, b_old, b8) : (cv - 8.0f) * b_old;
+    } else if (CODEC == KAON_MOM_INT8) {
       const uint32_t w = i < 4 ? mi8.x : mi8.y;
       if (DQX)
         mold[i] = (float)(int8_t)(uint8_t)((w >> (8 * (i & 3))) & 0xFFu) * oldsc;
       else
         mold[i] = __fmaf_rn((float)(((w ^ 0x80808080u) >> (8 * (i & 3))) & 0xFFu), oldsc, m128);
-    } else if (CODEC == KAON_MOM_4BIT) {
-      mold[i] = ((float)((m4 >> (4 * i)) & 0xFu) - 8.0f) * b_old;
     } else if (CODEC == KAON_MOM_BF16) {
       const uint32_t mw[4] = {mb16.x, mb16.y, mb16.z, mb16.w};
       const uint32_t w = mw[i >> 1];
@@ -344,7 +363,10 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   if (NKR && NEEDP) {
     const float nf_old = msam_nanfill(hp.nk_bound_old);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xr[i] = p[i] + msam_e(mold[i] * hp.nk_k, hp.nk_bound_old, nf_old);
+    for (int i = 0; i < 8; ++i) {
+      const float x = mold[i] * hp.nk_k;
+      xr[i] = p[i] + (SANE ? fminf(fmaxf(x, -hp.nk_bound_old), hp.nk_bound_old) : msam_e(x, hp.nk_bound_old, nf_old));
+    }
     if (PHASE == 6) {
       unpack8(sr_chunk(xr, nz0), p);
     } else if (!LAZY) {
@@ -435,7 +457,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   }
   // ---- phase 6: requant, cautious, SR write (+ Nekaon climb)
   float mdq[8];
-  uint32_t codes[8];
+  float codes[8];  // 4-bit: code + 8 in [1, 15], as a float
   float xq[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -445,7 +467,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     } else if (CODEC == KAON_MOM_4BIT) {
       float x = rintf(div_r64(mf[i], b_r));
       x = fminf(fmaxf(x, -7.0f), 7.0f);
-      codes[i] = (uint32_t)((int)x + 8);
+      codes[i] = x + 8.0f;
       mdq[i] = x * b_new;
     } else if (CODEC == KAON_MOM_BF16) {
       mdq[i] = mf[i];
@@ -463,14 +485,19 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     const float pd = PNM && WD ? rbf(p[i] * hp.wdl) : p[i];
     xs[i] = pd - dd;
   }
-  ku4 ov = sr_chunk(xs, nz1);
+  uint64_t nan_u = 0;
+  ku4 ov = sr_chunk(xs, nz1, &nan_u);
   if (NKC) {
     float y[8];
     unpack8(ov, y);
     const float nf_new = msam_nanfill(hp.nk_bound_new);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = y[i] + msam_e(mdq[i] * (-hp.nk_k), hp.nk_bound_new, nf_new);
-    ov = sr_chunk(y, nz2);
+    for (int i = 0; i < 8; ++i) {
+      const float x = mdq[i] * (-hp.nk_k);
+      y[i] = y[i] + (SANE ? fminf(fmaxf(x, -hp.nk_bound_new), hp.nk_bound_new) : msam_e(x, hp.nk_bound_new, nf_new));
+    }
+    // the update's values were not NaN: neither are these (a finite step added)
+    ov = (SANE && nan_u == 0) ? sr_chunk<true>(y, nz2) : sr_chunk(y, nz2);
   }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
   if (PHASE == 6 && (FLAGS & FF_GCW) && GC && X.gcw) {
@@ -488,9 +515,11 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     mv.y = pack_int8x4(xq[4], xq[5], xq[6], xq[7]);
     st_stream((KAON_G ku2*)(X.m + e0), mv);
   } else if (CODEC == KAON_MOM_4BIT) {
-    uint32_t v = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v |= (codes[i] & 0xFu) << (4 * i);
+    // byte k = code 2k + 16 code 2k+1 (exact small integers), packed by v_cvt_pk_u8_f32
+    uint32_t v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[1], 16.0f, codes[0]), 0, 0u);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[3], 16.0f, codes[2]), 1, v);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[5], 16.0f, codes[4]), 2, v);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[7], 16.0f, codes[6]), 3, v);
     *(KAON_G uint32_t*)(X.m + (e0 >> 1)) = v;
     if ((e0 & ((1u << X.bsh) - 1u)) == 0u) *(KAON_G float*)(X.msc + blk4) = b_new;  // the block's first chunk
   } else if (CODEC == KAON_MOM_BF16) {
@@ -639,6 +668,13 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     const uint32_t c = cl + L * (uint32_t)k;
     const bool full = valid && c < nfull;
     float camax = 0.0f;
+    if (QUANT && !PNM && !MUON) {
+      // the wave's scales against 2^120 (see fast_chunk), one ballot per chunk
+      const float s0 = CODEC == KAON_MOM_4BIT ? cur.bo : oldsc;
+      const float s1 = PHASE != 6 ? 0.0f : CODEC == KAON_MOM_4BIT ? fmaxf(cur.ba, 1e-12f) / 7.0f : newsc;
+      const bool ok = fabsf(s0) < 0x1p120f && fabsf(s1) < 0x1p120f;
+      dqf = __builtin_amdgcn_ballot_w64(!ok) == 0 && fabsf(hp.nk_k) < 0x1p120f;
+    }
     if (full) {
       const uint32_t e0 = rowe + 8u * c;
       if (wlo) {

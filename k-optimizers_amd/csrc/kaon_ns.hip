@@ -293,9 +293,11 @@ constexpr int BK = 64;           // K per stage
 constexpr int BLD = BK + 8;      // LDS row stride (bf16): 144 B, 16-B aligned rows, no bank aliasing
 constexpr int WLD = 128 + 8;     // epilogue staging row stride (bf16): a wave's 128 x 128 tile
 // MODE 2 keeps x as it lies in memory, BK rows of K by BT columns, and reads its
-// MFMA fragments with the LDS transpose read (ds_read_b64_tr_b16): row stride
-// 544 B puts consecutive rows 8 banks apart
-constexpr int XLD = BT + 16;
+// MFMA fragments with the LDS transpose read (ds_read_b64_tr_b16).  A 16-lane
+// group reads 32 bytes from each of 4 consecutive rows, and the group 16
+// columns on is served in the same LDS cycle: a row stride of 576 B (64 B past
+// a multiple of 256) puts the two groups' 8 pieces in distinct banks.
+constexpr int XLD = BT + 32;
 static_assert(BK * XLD <= BT * BLD, "the x tile fits the B stage");
 constexpr int NS_LDS = (2 * 2 * BT * BLD > 4 * 128 * WLD) ? 2 * 2 * BT * BLD : 4 * 128 * WLD;
 

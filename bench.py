@@ -214,6 +214,32 @@ def make_opt(name, params):
     return Nekaon(params, **w["kw"])
 
 
+def gc_written_elems(opt, name) -> int:
+    """Elements whose p.grad the step stores back centralized (2-D+ params only).
+
+    Lion writes every 2-D+ gradient back; Adakaon does so on its native path and,
+    under ``fused=True``, only for the params the reference's fused step routes to
+    its native path (``fused_routes_native``). Other optimizers' headline kernels
+    do not store the gradient."""
+    from kaon_amd.adakaon import fused_routes_native
+
+    w = WORKLOADS[name]
+    if w["opt"] not in ("lion", "adakaon") or not getattr(opt, "centralize_grads_in_place", False):
+        return 0
+    n = 0
+    for g in opt.param_groups:
+        if not g.get("gradient_centralization", True):
+            continue
+        for p in g["params"]:
+            if p.ndim < 2:
+                continue
+            if w["opt"] == "adakaon" and getattr(opt, "_fused", False) and \
+                    not fused_routes_native(p, g, opt._fused_tile_cap):
+                continue
+            n += p.numel()
+    return n
+
+
 def ns_flops(shapes, steps: int) -> float:
     """Newton-Schulz FLOPs per optimizer step: sum over 2-D / conv matrices of
     steps * (4 m^2 n + 2 m^3), m = min(R, C), n = max(R, C) (x x^T, A A, B x)."""
@@ -622,11 +648,10 @@ def main() -> int:
     gps = nparam / (ms * 1e-3) / 1e9
     bm = w["bm"]
     eb = 4.0 if pdt == torch.float32 else 2.0   # param and grad element bytes
-    # a step that leaves p.grad centralized (Lion; Adakaon / AdaPNM off their fused path)
-    # also writes the gradient once: eb more bytes per param
-    gc_write = bool(getattr(opt, "centralize_grads_in_place", False)) and \
-        w["kw"].get("gradient_centralization", True) and w["opt"] in ("lion", "adakaon")
-    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0) + w.get("b_extra", 0.0) + (eb if gc_write else 0.0)
+    # a step that leaves p.grad centralized writes those gradients once more: eb bytes
+    # per written element, averaged over the set
+    gcw = gc_written_elems(opt, args.workload) / nparam
+    b_alg = eb + 2.0 * eb + 2.0 * bm + w.get("b_neg", 0.0) + w.get("b_extra", 0.0) + eb * gcw
     step_gbs = b_alg * nparam / (ms * 1e-3) / 1e9
     print(f"[bench] {ms:.3f} ms/step, {gps:.1f} Gparam/s (wall {wall / args.steps * 1e3:.3f} ms/step)",
           file=sys.stderr, flush=True)
@@ -673,7 +698,7 @@ def main() -> int:
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
                                "avg_ms": round(br[dom], 4), "source": kernel_source_hash()}
         else:
-            bpp = phase_bytes(dom, bm, wd, w["opt"], w) + (2.0 if gc_write and dom == 6 else 0.0)
+            bpp = phase_bytes(dom, bm, wd, w["opt"], w) + (eb * gcw if dom == 6 else 0.0)
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0
             out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload, dom),

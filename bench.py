@@ -215,17 +215,20 @@ def make_opt(name, params):
 
 
 def gc_written_elems(opt, name) -> int:
-    """Elements whose p.grad the step stores back centralized (2-D+ params only).
+    """Elements whose p.grad the step's apply stores back centralized (2-D+ params only).
 
-    Lion writes every 2-D+ gradient back; Adakaon does so on its native path and,
-    under ``fused=True``, only for the params the reference's fused step routes to
-    its native path (``fused_routes_native``). Other optimizers' headline kernels
-    do not store the gradient."""
+    Lion writes every 2-D+ gradient back; Adakaon (and the Nekaon / MSAM steps over
+    it) does so on its native path and, under ``fused=True``, only for the params
+    the reference's fused step routes to its native path (``fused_routes_native``).
+    Other optimizers' headline kernels do not store the gradient."""
     from kaon_amd.adakaon import fused_routes_native
 
     w = WORKLOADS[name]
-    if w["opt"] not in ("lion", "adakaon") or not getattr(opt, "centralize_grads_in_place", False):
+    inner = getattr(opt, "inner", opt)  # Nekaon / MSAM step an inner Adakaon
+    if w["opt"] not in ("lion", "adakaon", "nekaon", "msam") or \
+            not getattr(inner, "centralize_grads_in_place", False):
         return 0
+    fused = w["opt"] != "lion" and getattr(inner, "_fused", False)
     n = 0
     for g in opt.param_groups:
         if not g.get("gradient_centralization", True):
@@ -233,8 +236,7 @@ def gc_written_elems(opt, name) -> int:
         for p in g["params"]:
             if p.ndim < 2:
                 continue
-            if w["opt"] == "adakaon" and getattr(opt, "_fused", False) and \
-                    not fused_routes_native(p, g, opt._fused_tile_cap):
+            if fused and not fused_routes_native(p, g, inner._fused_tile_cap):
                 continue
             n += p.numel()
     return n

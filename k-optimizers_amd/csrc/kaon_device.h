@@ -76,6 +76,19 @@ __device__ __forceinline__ float klerp_b(float a, float b, float w) {
 // inputs (exact quotients included); inf and NaN propagate as in IEEE division.
 __device__ __forceinline__ float div_r64(float a, double r) { return (float)((double)a * r); }
 __device__ __forceinline__ double rcp64(float b) { return 1.0 / (double)b; }
+// A reciprocal for div_r64 without the IEEE division sequence, for finite
+// normal b with 2^-126 <= |b| < 2^126: v_rcp_f64 and two Newton steps
+// r' = r + r (1 - b r) leave r within a few 2^-53 of 1/b (relative), so the
+// product's error stays far inside div_r64's 2^-49 margin and the quotient is
+// RN32(a/b) as with RN64(1/b).
+__device__ __forceinline__ double rcp64_nr(float b) {
+  const double d = (double)b;
+  double r = __builtin_amdgcn_rcp(d);
+  double e = __builtin_fma(-d, r, 1.0);
+  r = __builtin_fma(r, e, r);
+  e = __builtin_fma(-d, r, 1.0);
+  return __builtin_fma(r, e, r);
+}
 
 __device__ __forceinline__ float ksign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
 

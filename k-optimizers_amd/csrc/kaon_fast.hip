@@ -83,7 +83,11 @@ __device__ __forceinline__ void noise8_u32(uint64_t seed, uint32_t step, uint32_
 }
 
 // noise8_u32 with each 16-bit value in the high half of its word (the random
-// operand of v_cvt_sr_bf16_f32).
+// operand of v_cvt_sr_bf16_f32).  The instruction reads only bits 31:16 of
+// that operand (a device check over every bf16 high half with random, all-ones
+// and carry-boundary low halves found no difference from the masked word), so
+// the odd element's word is the Philox word itself, its low half unmasked;
+// sr_chunk's NaN path shifts the noise down and never sees the low half.
 __device__ __forceinline__ void noise8_hi(uint64_t seed, uint32_t step, uint32_t tid, uint32_t stream, uint32_t e0,
                                           const KAON_G uint16_t* inj, uint32_t w[8]) {
   if (inj) {
@@ -99,7 +103,7 @@ __device__ __forceinline__ void noise8_hi(uint64_t seed, uint32_t step, uint32_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     w[2 * i] = c[i] << 16;
-    w[2 * i + 1] = c[i] & 0xFFFF0000u;
+    w[2 * i + 1] = c[i];
   }
 }
 
@@ -119,8 +123,9 @@ template <bool CLEAN = false>
 __device__ __forceinline__ ku4 sr_chunk(const float x[8], const uint32_t nzh[8], uint64_t* nan_out = nullptr) {
   uint64_t nan = 0;
   if (!CLEAN) {
+    // one unordered compare per pair: true where either value is NaN
 #pragma unroll
-    for (int i = 0; i < 8; ++i) nan |= __builtin_amdgcn_ballot_w64(x[i] != x[i]);
+    for (int i = 0; i < 8; i += 2) nan |= __builtin_amdgcn_ballot_w64(__builtin_isunordered(x[i], x[i + 1]));
   }
   if (nan_out) *nan_out = nan;
   uint32_t w[4];
@@ -249,7 +254,7 @@ template <int OPT, int PHASE, int CODEC, int FLAGS, bool FAC1, bool DQX, bool WL
 __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, const KaonHyper& hp, uint32_t e0,
                                            float mu, float rf, float oldsc, float m128, float negsc, float m128n,
                                            float newsc, double rnew, double rfac, double rden, int lane,
-                                           uint32_t& keep, float& amax) {
+                                           uint32_t& keep, float& amax, float bnew4) {
   constexpr bool GC = FLAGS & FF_GC, CAUT = FLAGS & FF_CAUT, WD = FLAGS & FF_WD;
   constexpr bool NKR = FLAGS & FF_NKR, NKC = FLAGS & FF_NKC;
   constexpr bool MOM = CODEC != KAON_MOM_NONE;
@@ -263,7 +268,18 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     f[0] = in.c0.x; f[1] = in.c0.y; f[2] = in.c0.z; f[3] = in.c0.w;
     f[4] = in.c1.x; f[5] = in.c1.y; f[6] = in.c1.z; f[7] = in.c1.w;
   }
-  // 4-bit: one block per chunk
+  // !DQX (int8, 4-bit): every lane's momentum scales are below 2^120 (the
+  // caller's wave-wide test, with the new scales and a finite Nekaon factor in
+  // the apply, and positive Nekaon / MSAM bounds).  Then each dequantized
+  // momentum and each perturbation before its clamp is a number that is not
+  // NaN: the clamps need no NaN case and take one v_med3_f32 (the median of
+  // x, -b, b is the clamp for b > 0, +inf included), the climb's input is NaN
+  // only where the update's was, and a code dequantizes as
+  // fma(code, s, -128 s) / fma(code, s, -8 s), exact since -128 s / -8 s and
+  // the sum are then one rounding of (code - 128) s / (code - 8) s.
+  constexpr bool SANE = !DQX && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON;
+  // 4-bit: one block per chunk; the apply's new scale max(|m| max, 1e-12) / 7
+  // comes from the caller (bnew4)
   float b_old = 1.0f, b_new = 1.0f;
   double b_r = 1.0;
   uint32_t blk4 = 0;  // byte offset of the chunk's block in the per-block arrays
@@ -271,8 +287,9 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     blk4 = (e0 >> X.bsh) * 4u;
     b_old = in.bo;
     if (PHASE == 6) {
-      b_new = fmaxf(in.ba, 1e-12f) / 7.0f;
-      b_r = rcp64(b_new);
+      b_new = bnew4;
+      // SANE: 1.4e-13 < b_new < 2^120
+      b_r = SANE ? rcp64_nr(b_new) : rcp64(b_new);
     }
   }
   float g[8], p[8];
@@ -306,17 +323,16 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   if (PHASE == 6) noise8_hi(hp.seed, hp.step, X.tid, 1u, e0, X.nz[1], nz1);
   if (PHASE == 6 && NKC) noise8_hi(hp.seed, hp.step, X.tid, 2u, e0, X.nz[2], nz2);
 
-  // !DQX (int8, 4-bit): every lane's momentum scales are below 2^120 (the
-  // caller's wave-wide test, with the new scales and a finite Nekaon factor in
-  // the apply).  Then each dequantized momentum and each perturbation before
-  // its clamp is a finite number: the clamps need no NaN case, the climb's
-  // input is NaN only where the update's was, and a code dequantizes as
-  // fma(code, s, -128 s) / fma(code, s, -8 s), exact since -128 s / -8 s and
-  // the sum are then one rounding of (code - 128) s / (code - 8) s.
-  constexpr bool SANE = !DQX && (CODEC == KAON_MOM_INT8 || CODEC == KAON_MOM_4BIT) && !PNM && !MUON;
   float mold[8];
   // 4-bit: the codes as floats, from the bytes of the even and the odd nibbles
-  const uint32_t nlo = m4 & 0x0F0F0F0Fu, nhi = (m4 >> 4) & 0x0F0F0F0Fu;
+  uint32_t nlo = m4 & 0x0F0F0F0Fu, nhi = (m4 >> 4) & 0x0F0F0F0Fu;
+  if (CODEC == KAON_MOM_4BIT) {
+    // opaque to the optimizer: otherwise it folds each byte's extraction back
+    // into a bit-field extract of m4 and a conversion (two instructions per
+    // code instead of one v_cvt_f32_ubyteN)
+    asm volatile("" : "+v"(nlo));
+    asm volatile("" : "+v"(nhi));
+  }
   const float b8 = -8.0f * b_old;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -365,7 +381,8 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = mold[i] * hp.nk_k;
-      xr[i] = p[i] + (SANE ? fminf(fmaxf(x, -hp.nk_bound_old), hp.nk_bound_old) : msam_e(x, hp.nk_bound_old, nf_old));
+      xr[i] = p[i] + (SANE ? __builtin_amdgcn_fmed3f(x, -hp.nk_bound_old, hp.nk_bound_old)
+                           : msam_e(x, hp.nk_bound_old, nf_old));
     }
     if (PHASE == 6) {
       unpack8(sr_chunk(xr, nz0), p);
@@ -457,7 +474,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
   }
   // ---- phase 6: requant, cautious, SR write (+ Nekaon climb)
   float mdq[8];
-  float codes[8];  // 4-bit: code + 8 in [1, 15], as a float
+  float codes[8];  // 4-bit: the centred code in [-7, 7], as a float
   float xq[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -467,7 +484,7 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     } else if (CODEC == KAON_MOM_4BIT) {
       float x = rintf(div_r64(mf[i], b_r));
       x = fminf(fmaxf(x, -7.0f), 7.0f);
-      codes[i] = x + 8.0f;
+      codes[i] = x;
       mdq[i] = x * b_new;
     } else if (CODEC == KAON_MOM_BF16) {
       mdq[i] = mf[i];
@@ -494,13 +511,16 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = mdq[i] * (-hp.nk_k);
-      y[i] = y[i] + (SANE ? fminf(fmaxf(x, -hp.nk_bound_new), hp.nk_bound_new) : msam_e(x, hp.nk_bound_new, nf_new));
+      y[i] = y[i] + (SANE ? __builtin_amdgcn_fmed3f(x, -hp.nk_bound_new, hp.nk_bound_new)
+                         : msam_e(x, hp.nk_bound_new, nf_new));
     }
     // the update's values were not NaN: neither are these (a finite step added)
     ov = (SANE && nan_u == 0) ? sr_chunk<true>(y, nz2) : sr_chunk(y, nz2);
   }
   st_stream((KAON_G ku4*)(X.p + 2u * e0), ov);
-  if (PHASE == 6 && (FLAGS & FF_GCW) && GC && X.gcw) {
+  // Nekaon / MSAM applies test the launch flag at run time (X.gcw) rather than
+  // taking a template variant of their own
+  if (PHASE == 6 && ((FLAGS & FF_GCW) || NKR || NKC) && GC && X.gcw) {
     // the centralized gradient, already rounded to bf16 (its low halves are zero)
     ku4 gv;
     gv.x = pack_hi16(__float_as_uint(g[0]), __float_as_uint(g[1]));
@@ -515,11 +535,12 @@ __device__ __forceinline__ void fast_chunk(const FastCtx& X, const FastIn& in, c
     mv.y = pack_int8x4(xq[4], xq[5], xq[6], xq[7]);
     st_stream((KAON_G ku2*)(X.m + e0), mv);
   } else if (CODEC == KAON_MOM_4BIT) {
-    // byte k = code 2k + 16 code 2k+1 (exact small integers), packed by v_cvt_pk_u8_f32
-    uint32_t v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[1], 16.0f, codes[0]), 0, 0u);
-    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[3], 16.0f, codes[2]), 1, v);
-    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[5], 16.0f, codes[4]), 2, v);
-    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[7], 16.0f, codes[6]), 3, v);
+    // byte k = (c_2k + 8) + 16 (c_2k+1 + 8) = 16 c_2k+1 + (c_2k + 136), exact small
+    // integers, packed by v_cvt_pk_u8_f32
+    uint32_t v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[1], 16.0f, codes[0] + 136.0f), 0, 0u);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[3], 16.0f, codes[2] + 136.0f), 1, v);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[5], 16.0f, codes[4] + 136.0f), 2, v);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__fmaf_rn(codes[7], 16.0f, codes[6] + 136.0f), 3, v);
     *(KAON_G uint32_t*)(X.m + (e0 >> 1)) = v;
     if ((e0 & ((1u << X.bsh) - 1u)) == 0u) *(KAON_G float*)(X.msc + blk4) = b_new;  // the block's first chunk
   } else if (CODEC == KAON_MOM_BF16) {
@@ -552,7 +573,8 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   FastCtx X;
   X.g = (const KAON_G uint8_t*)G(T.g);
   X.gw = (KAON_G uint8_t*)G(const_cast<void*>(T.g));
-  X.gcw = T.gc_write != 0;
+  // the launch stores centralized gradients and this tensor is one of them
+  X.gcw = T.gc_write != 0 && (hp.flags & KAON_F_GC_WRITE) != 0;
   X.p = (KAON_G uint8_t*)G(T.p);
   // AdaPNM: m is this step's positive buffer (m on odd steps, m2 on even ones)
   const bool swap = PNM && (hp.step & 1u) == 0u;
@@ -627,6 +649,10 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
   float mu = 0.0f, rf = 1.0f, oldsc = 1.0f, newsc = 1.0f, m128 = 0.0f, amax = 0.0f, negsc = 1.0f, m128n = 0.0f;
   double rnew = 1.0;
   bool dqf = true;
+  // Nekaon / MSAM factors the fast clamp form allows (see fast_chunk): a factor
+  // below 2^120 and positive bounds
+  const bool nk_ok = fabsf(hp.nk_k) < 0x1p120f && (!(FLAGS & FF_NKR) || hp.nk_bound_old > 0.0f) &&
+                     (!(FLAGS & FF_NKC) || hp.nk_bound_new > 0.0f);
   // One position: arithmetic on `cur`, loads of the next position into `nxt`.
   // Called with the two buffers alternating, so no register copies wait on
   // the loads in flight.
@@ -668,35 +694,38 @@ __global__ __launch_bounds__(KAON_WG) void k_fast(const KaonTensor* __restrict__
     const uint32_t c = cl + L * (uint32_t)k;
     const bool full = valid && c < nfull;
     float camax = 0.0f;
+    // 4-bit apply: the block's new scale max(|m| max, 1e-12) / 7, rounded once
+    // (div_r64 by RN64(1/7) is the IEEE quotient)
+    const float bnew4 = CODEC == KAON_MOM_4BIT && PHASE == 6 ? div_r64(fmaxf(cur.ba, 1e-12f), 1.0 / 7.0) : 1.0f;
     if (QUANT && !PNM && !MUON) {
       // the wave's scales against 2^120 (see fast_chunk), one ballot per chunk
       const float s0 = CODEC == KAON_MOM_4BIT ? cur.bo : oldsc;
-      const float s1 = PHASE != 6 ? 0.0f : CODEC == KAON_MOM_4BIT ? fmaxf(cur.ba, 1e-12f) / 7.0f : newsc;
+      const float s1 = PHASE != 6 ? 0.0f : CODEC == KAON_MOM_4BIT ? bnew4 : newsc;
       const bool ok = fabsf(s0) < 0x1p120f && fabsf(s1) < 0x1p120f;
-      dqf = __builtin_amdgcn_ballot_w64(!ok) == 0 && fabsf(hp.nk_k) < 0x1p120f;
+      dqf = __builtin_amdgcn_ballot_w64(!ok) == 0 && nk_ok;
     }
     if (full) {
       const uint32_t e0 = rowe + 8u * c;
       if (wlo) {
         if (fac == 1.0f && dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
         else if (dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
         else
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, true>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
       } else {
         if (fac == 1.0f && dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, true, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
         else if (dqf)
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, false, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
         else
           fast_chunk<OPT, PHASE, CODEC, FLAGS, false, true, false>(
-              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax);
+              X, cur, hp, e0, mu, rf, oldsc, m128, negsc, m128n, newsc, rnew, rfac, rden, wr.lane, keep, camax, bnew4);
       }
     }
     if (PHASE == 5 && QUANT && !PNM && !MUON) {
@@ -780,6 +809,9 @@ ElemFn fast_by_flags(int ff) {
     }
   }
   if constexpr (OPT == KAON_OPT_ADAKAON && CODEC != KAON_MOM_NONE) {
+    // the Nekaon / MSAM kernels store the centralized gradient under a run-time
+    // test of the launch flag: one kernel with or without the write
+    if (ff & (FF_NKR | FF_NKC)) ff &= ~FF_GCW;
     // phase 5 reads the weights (and so the removal) only under weight decay
     switch (ff) {
       case FF_GC | FF_CAUT | FF_WD | FF_NKR:

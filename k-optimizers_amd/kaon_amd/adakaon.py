@@ -156,7 +156,7 @@ class Adakaon(KaonOptimizer):
         flags = 0
         if group["gradient_centralization"]:
             flags |= L.F_GC
-            if self.centralize_grads_in_place and nk is None:
+            if self.centralize_grads_in_place:
                 flags |= L.F_GC_WRITE  # the apply stores the centralized gradient
         if group["cautious"]:
             flags |= L.F_CAUTIOUS
@@ -205,8 +205,6 @@ class Adakaon(KaonOptimizer):
                     hp.flags &= ~L.F_GC_WRITE
                 L.check(lib.kaon_adakaon_step(ctypes.byref(plan.launch), ctypes.byref(hp), E.stream_handle(dev)),
                         "kaon_adakaon_step")
-                if nk is not None:  # under MSAM / Nekaon the apply carries the perturbation instead
-                    self._gc_writeback(group, plan, hp, dev)
         return loss
 
     def _build_launches(self, gid: int, group: dict[str, Any], params: list[torch.Tensor],

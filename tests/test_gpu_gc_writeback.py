@@ -9,9 +9,11 @@ centralize in-kernel and leave p.grad as it was (src/kaon/adakaon.py:387-409);
 the fused Adakaon still sends some params to its native path (fp16, convs with
 quantized momentum, beta1 = 0, bf16 without SR, one-block 4-bit matrices of odd
 width: _fused_partition, adakaon.py:437-468), whose p.grad it centralizes.
-The Adakaon / Lion apply and KProdigy's pass 2 store the centralized gradient
-as they read it (KAON_F_GC_WRITE); AdaPNM and AdaMuon write it back after the
-step with kaon_gc_writeback.  Checked against the oracle's bf16 GC.
+The Adakaon / Lion apply (Nekaon's and MSAM's removal / climb applies
+included) and KProdigy's pass 2 store the centralized gradient as they read it
+(KAON_F_GC_WRITE); AdaPNM and AdaMuon write it back after the step with
+kaon_gc_writeback.  Checked against the oracle's bf16 GC, after the last of
+the case's steps (Nekaon and MSAM: the second, whose apply carries the removal).
 """
 import numpy as np
 import pytest
@@ -32,8 +34,8 @@ def _need_gpu():
         pytest.skip("needs a ROCm GPU")
 
 
-def _case(opt, **kw):
-    return dict(steps=1, seed=5, p_dtype="bf16", g_dtype="bf16", opt=opt, shapes=SHAPES, kwargs=kw)
+def _case(opt, steps=1, **kw):
+    return dict(steps=steps, seed=5, p_dtype="bf16", g_dtype="bf16", opt=opt, shapes=SHAPES, kwargs=kw)
 
 
 ALL = True
@@ -56,6 +58,10 @@ CASES = {
     "adapnm": (_case("adapnm", lr=1e-3, momentum_dtype="bfloat16"), ALL, None),
     "kprodigy": (_case("kprodigy", lr=1.0, momentum_dtype="bfloat16"), ALL, None),
     "adamuon_gc": (_case("adamuon", lr=2e-2, momentum_dtype="int8", gradient_centralization=True), ALL, None),
+    # the removal and the climb ride in the Adakaon apply
+    "nekaon_4bit": (_case("nekaon", steps=2, lr=1e-3, momentum_dtype="4bit", momentum_4bit_block=8), ALL, None),
+    "nekaon_fused": (_case("nekaon", steps=2, lr=1e-3, momentum_dtype="int8"), {1}, FUSED),
+    "msam_global": (_case("msam", steps=2, lr=1e-3, momentum_dtype="int8"), ALL, None),
 }
 
 
@@ -66,11 +72,12 @@ def test_grad_after_step(name):
     params = [torch.nn.Parameter(torch.from_numpy(param_values(case, i)).to(DEV, torch.bfloat16))
               for i in range(len(SHAPES))]
     opt = make_opt(case, params, extra=extra)
-    raw = []
-    for i, p in enumerate(params):
-        p.grad = torch.from_numpy(grad_values(case, i, 1)).to(DEV, torch.bfloat16)
-        raw.append(to_bits(p.grad))
-    opt.step()
+    for step in range(1, case["steps"] + 1):
+        raw = []
+        for i, p in enumerate(params):
+            p.grad = torch.from_numpy(grad_values(case, i, step)).to(DEV, torch.bfloat16)
+            raw.append(to_bits(p.grad))
+        opt.step()
     torch.cuda.synchronize()
     for i, p in enumerate(params):
         got = to_bits(p.grad)

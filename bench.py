@@ -258,6 +258,50 @@ def ns_flops(shapes, steps: int) -> float:
     return tot
 
 
+def ns_library_ms(dev, shapes, steps: int, reps: int = 5) -> dict:
+    """The same Newton-Schulz products through the vendor GEMM (torch.bmm: hipBLASLt /
+    rocBLAS), batched per distinct (m, n): X X^T ([b,m,n] x [b,n,m]), A A ([b,m,m] x
+    [b,m,m]) and B X ([b,m,m] x [b,m,n]), operands contiguous, no epilogues.  Their
+    summed time per step is a library composition of the phase to set beside the
+    HIP kernels (which also exploit the symmetry of X X^T and A A, and fuse the
+    b A + c A A and a X + B X epilogues).  Random bf16 operands: GEMM time does not
+    depend on the values."""
+    import torch
+
+    groups: dict[tuple[int, int], int] = {}
+    for s in shapes:
+        if len(s) < 2:
+            continue
+        c = 1
+        for d in s[1:]:
+            c *= d
+        m, n = min(s[0], c), max(s[0], c)
+        groups[(m, n)] = groups.get((m, n), 0) + 1
+    per = {"xxt": 0.0, "aa": 0.0, "bx": 0.0}
+    flops = 0.0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for (m, n), b in sorted(groups.items()):
+        for name, (k, cols, rows) in (("xxt", (n, m, m)), ("aa", (m, m, m)), ("bx", (m, n, m))):
+            a = torch.randn(b, rows, k, device=dev, dtype=torch.bfloat16)
+            x = torch.randn(b, k, cols, device=dev, dtype=torch.bfloat16)
+            o = torch.empty(b, rows, cols, device=dev, dtype=torch.bfloat16)
+            torch.bmm(a, x, out=o)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                torch.bmm(a, x, out=o)
+            e1.record()
+            torch.cuda.synchronize()
+            per[name] += e0.elapsed_time(e1) / reps
+            flops += 2.0 * b * rows * k * cols
+            del a, x, o
+    torch.cuda.empty_cache()
+    tot = steps * sum(per.values())
+    return {"ms_per_step": round(tot, 3), "tflops": round(steps * flops / (tot * 1e-3) / 1e12, 1),
+            "ms_per_iteration": {k: round(v, 3) for k, v in per.items()},
+            "note": "torch.bmm per distinct (m, n) of the set, products only (no symmetry, no epilogues)"}
+
+
 def copy_ceiling_gbs(dev, nbytes=4 << 30, reps=10) -> float:
     import torch
     from kaon_amd import _lib
@@ -408,14 +452,25 @@ def phase_breakdown(opt, name, reps=5) -> dict[int, float]:
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: the model string, with its family /
+    model / stepping numbers, the microcode revision and the logical CPU count (a
+    virtualized host may report only a short model name)."""
+    info: dict[str, str] = {}
+    n = 0
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    continue
+                k, v = (s.strip() for s in line.split(":", 1))
+                if k == "processor":
+                    n += 1
+                info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    detail = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping", "microcode") if k in info)
+    return f"{name} ({detail}; {n} logical CPUs)" if detail else f"{name} ({n} logical CPUs)"
 
 
 def cpu_baseline(params, name, budget_s: float) -> dict:
@@ -699,6 +754,7 @@ def main() -> int:
                                "traffic": measured_traffic(args.workload, dom),
                                "kernel": "phase 9 (newton_schulz: bf16 MFMA GEMMs)", "flops_per_launch": fl,
                                "avg_ms": round(br[dom], 4), "source": kernel_source_hash()}
+            out["ns_library"] = ns_library_ms(dev, shapes, w["kw"]["ns_steps"])
         else:
             bpp = phase_bytes(dom, bm, wd, w["opt"], w) + (eb * gcw if dom == 6 else 0.0)
             ach = bpp * nparam / (br[dom] * 1e-3) / 1e9 if bpp else 0.0

@@ -368,6 +368,12 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     if (a.cls != b.cls) return a.cls < b.cls;
     return a.size > b.size;
   });
+  // finalize items tallest tensors first: an item's work grows with R (its
+  // column sums run down the rows), so the longest start early.  Each item
+  // writes only its own columns (or its tensor's row factors) and its clip
+  // partial goes to its column block's slot, so the order moves no result.
+  std::stable_sort(fins.begin(), fins.end(),
+                   [&](const KaonItem& a, const KaonItem& b) { return descs[a.tensor].R > descs[b.tensor].R; });
   info->n_row_items = (int32_t)rows.size();
   info->n_fast = 0;
   for (const RowIt& r : elems) info->n_fast += r.fast ? 1 : 0;

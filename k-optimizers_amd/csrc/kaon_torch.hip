@@ -158,34 +158,202 @@ __global__ __launch_bounds__(KAON_WG) void k_trow(const KaonTensor* __restrict__
 }
 
 // =============================================================== phase 2
-// Finalize items, eight workgroups each.  kind 0: columns [row0, row0 + nrows),
-// 256 per workgroup, one per thread: the column sum of G^2 (+eps1) over the rows
-// (ko_torch_outer_sum: a cascade down the rows for the blocks of 32 columns --
-// blocks of 4 when C < 8 -- and four row slots for the columns after them), then
-// col = lerp(col, sum / R, 1-beta2) and cf = 1/sqrt(col).  kind 1: the row EMA's
-// mean in torch's row order, rf = 1/sqrt(row / mean).
-constexpr int kTfinSub = 8;
+// Finalize items, four one-wave workgroups each.  kind 0: columns [row0,
+// row0 + nrows): the column sum of G^2 (+eps1) over the rows (ko_torch_outer_sum:
+// a cascade down the rows for the blocks of 32 columns -- blocks of 4 when C < 8
+// -- and four row slots for the columns after them), then col = lerp(col, sum /
+// R, 1-beta2) and cf = 1/sqrt(col).  A lane takes eight adjacent columns.  With
+// aligned rows of C % 8 == 0 it runs their cascades side by side from one
+// 16-byte load per row (fp32: two); otherwise, and for the columns after the
+// 32-column blocks, one column after another.  (Two or four columns per lane
+// for the tallest tensors, to even out the lanes' work, measured slower: the
+// pass is bound by its load instructions, and narrower loads issue more.)
+// kind 1 (workgroup 0): the row EMA's mean in torch's row order, rf =
+// 1/sqrt(row / mean).
+constexpr int kTfinSub = 4;
+constexpr int kTfinWG = 64;
+constexpr int kTfinCols = 8;  // columns per lane
+static_assert(kTfinSub * kTfinWG * kTfinCols == KAON_COLITEM, "a finalize item's columns");
 
-template <int GT, bool GC>
-__global__ __launch_bounds__(KAON_WG) void k_tfin(const KaonTensor* __restrict__ D,
-                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ float rm_s;
-  const KaonItem it = items[blockIdx.x / kTfinSub];
-  const int sb = (int)(blockIdx.x % kTfinSub);
-  const KaonTensor& T = D[it.tensor];
+// tcascade of K accumulator positions side by side: position c sums term(i)[c]
+// over i with exactly tcascade's additions.  `load(i, raw)` issues row i's
+// loads, `term(i, raw, q)` forms its K terms.  A leaf's sum starts from 0 and
+// depends on no other leaf, so with 16-term leaves the loads run two leaves
+// ahead of the additions (three register sets, every load issued
+// unconditionally from a row inside the range): a lane waits for memory about
+// once per three leaves rather than once per leaf.
+template <int K, class Raw, class L, class F>
+__device__ void tcascade_k(int64_t size, L load, F term, float out[K]) {
+  const int lp0 = ceil_log2_u64((uint64_t)size) / 4;
+  const int lp = lp0 > 4 ? lp0 : 4;
+  const int64_t step = (int64_t)1 << lp, mask = step - 1;
+  float a0[K], a1[K], a2[K], a3[K];
+#pragma unroll
+  for (int c = 0; c < K; ++c) a0[c] = a1[c] = a2[c] = a3[c] = 0.0f;
+  auto add_row = [&](int64_t i, const Raw& r) {
+    float q[K];
+    term(i, r, q);
+#pragma unroll
+    for (int c = 0; c < K; ++c) a0[c] = a0[c] + q[c];
+  };
+  // the leaf ending at row i is done: into level 1, and on up the levels
+  auto close_leaf = [&](int64_t i) {
+#pragma unroll
+    for (int c = 0; c < K; ++c) {
+      a1[c] = a1[c] + a0[c];
+      a0[c] = 0.0f;
+    }
+    if ((i & (mask << lp)) == 0) {
+#pragma unroll
+      for (int c = 0; c < K; ++c) {
+        a2[c] = a2[c] + a1[c];
+        a1[c] = 0.0f;
+      }
+      if ((i & (mask << (2 * lp))) == 0) {
+#pragma unroll
+        for (int c = 0; c < K; ++c) {
+          a3[c] = a3[c] + a2[c];
+          a2[c] = 0.0f;
+        }
+      }
+    }
+  };
+  int64_t i = 0;
+  if (lp == 4) {
+    const int64_t nleaf = size >> 4;
+    if (nleaf > 0) {
+      Raw r0[16], r1[16], r2[16];
+      auto ld_leaf = [&](int64_t l, Raw(&r)[16]) {
+        const int64_t b = (l < nleaf ? l : nleaf - 1) * 16;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) load(b + j, r[j]);
+      };
+      auto do_leaf = [&](int64_t l, const Raw(&r)[16]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) add_row(l * 16 + j, r[j]);
+        close_leaf((l + 1) * 16);
+      };
+      ld_leaf(0, r0);
+      ld_leaf(1, r1);
+      for (int64_t l = 0; l < nleaf; l += 3) {
+        ld_leaf(l + 2, r2);
+        do_leaf(l, r0);
+        if (l + 1 >= nleaf) break;
+        ld_leaf(l + 3, r0);
+        do_leaf(l + 1, r1);
+        if (l + 2 >= nleaf) break;
+        ld_leaf(l + 4, r1);
+        do_leaf(l + 2, r2);
+      }
+      i = nleaf * 16;
+    }
+  } else {
+    while (i + step <= size) {
+      for (int64_t j = 0; j < step; ++j) {
+        Raw r;
+        load(i + j, r);
+        add_row(i + j, r);
+      }
+      i += step;
+      close_leaf(i);
+    }
+  }
+  for (; i < size; ++i) {
+    Raw r;
+    load(i, r);
+    add_row(i, r);
+  }
+#pragma unroll
+  for (int c = 0; c < K; ++c) out[c] = ((a0[c] + a1[c]) + a2[c]) + a3[c];
+}
+
+// One row's K grad values at the lane's columns, as loaded (16-bit grads
+// packed two to a word).
+template <int GT, int K>
+struct TfRaw {
+  uint32_t w[GT == KAON_F32 ? K : K / 2];
+};
+
+// The column sums of columns j0 .. j0 + K - 1 (vector path: aligned rows of C %
+// 8 == 0, all K inside the 32-column blocks), col / cf written.  FUSE: the term
+// x*x + eps1 as one fused multiply-add, the same bits for 16-bit x when eps1 is
+// 0 or at least 2^-100 (x*x is then exact, or below half an ulp of eps1).
+template <int GT, bool GC, int K, bool FUSE>
+__device__ __forceinline__ void tfin_cols(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, int64_t j0) {
   const int64_t R = T.R, C = T.C;
-  if (it.kind == 0) {
-    const int64_t j = (int64_t)it.row0 + (int64_t)sb * KAON_WG + threadIdx.x;
-    if (j >= (int64_t)it.row0 + it.nrows) return;
-    const void* gsrc = T.g;
-    const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
-    const KAON_G float* mu = ws.mu(T);
+  const void* gsrc = T.g;
+  const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
+  const KAON_G float* mu = ws.mu(T);
+  constexpr int NW = GT == KAON_F32 ? K : K / 2;  // 32-bit words per row
+  float cs[K];
+  tcascade_k<K, TfRaw<GT, K>>(
+      R,
+      [&](int64_t i, TfRaw<GT, K>& r) {
+        const KAON_G uint8_t* p =
+            (const KAON_G uint8_t*)G(gsrc) + (i * C + j0) * (GT == KAON_F32 ? 4 : 2);
+        if (NW == 8) {
+          const ku4 v0 = *(const KAON_G ku4*)p, v1 = *(const KAON_G ku4*)(p + 16);
+          r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+          r.w[4 % NW] = v1.x; r.w[5 % NW] = v1.y; r.w[6 % NW] = v1.z; r.w[7 % NW] = v1.w;
+        } else if (NW == 4) {
+          const ku4 v = *(const KAON_G ku4*)p;
+          r.w[0] = v.x; r.w[1 % NW] = v.y; r.w[2 % NW] = v.z; r.w[3 % NW] = v.w;
+        } else if (NW == 2) {
+          const ku2 v = *(const KAON_G ku2*)p;
+          r.w[0] = v.x; r.w[1 % NW] = v.y;
+        } else {
+          r.w[0] = *(const KAON_G uint32_t*)p;
+        }
+      },
+      [&](int64_t i, const TfRaw<GT, K>& r, float q[K]) {
+        const float m = GC ? mu[i] : 0.0f;
+#pragma unroll
+        for (int c = 0; c < K; c += 2) {
+          float x[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            x[h] = GT == KAON_F32 ? __uint_as_float(r.w[(c + h) % NW])
+                                  : lp2f<GT>(h ? (r.w[(c >> 1) % NW] >> 16) : (r.w[(c >> 1) % NW] & 0xFFFFu));
+          if (GC) {
+            x[0] = x[0] - m;
+            x[1] = x[1] - m;
+            // bf16: the packed conversion, RNE as round_to for every value but
+            // NaN (whose term makes the column sum NaN either way)
+            if (GT == KAON_BF16) {
+              rbf2(x[0], x[1]);
+            } else {
+              x[0] = round_to<GT>(x[0]);
+              x[1] = round_to<GT>(x[1]);
+            }
+          }
+          q[c] = FUSE ? __fmaf_rn(x[0], x[0], eadd) : x[0] * x[0] + eadd;
+          q[c + 1] = FUSE ? __fmaf_rn(x[1], x[1], eadd) : x[1] * x[1] + eadd;
+        }
+      },
+      cs);
+#pragma unroll
+  for (int c = 0; c < K; ++c) {
+    const int64_t j = j0 + c;
+    const float nc = klerp(G(T.col)[j], cs[c] / (float)R, hp.w2);
+    G(T.col)[j] = nc;
+    ws.cf(T)[j] = 1.0f / sqrtf(nc);
+  }
+}
+
+// Columns j0 .. min(j0 + K, end) - 1 one at a time (any row layout).
+template <int GT, bool GC>
+__device__ void tfin_scalar(const KaonTensor& T, const Ws& ws, const KaonHyper& hp, int64_t j0, int k, int64_t end) {
+  const int64_t R = T.R, C = T.C;
+  const void* gsrc = T.g;
+  const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
+  const KAON_G float* mu = ws.mu(T);
+  const int64_t jd = C >= 8 ? (C / 32) * 32 : (C / 4) * 4;
+  for (int64_t j = j0; j < j0 + k && j < end; ++j) {
     auto q = [&](int64_t i) {
       float x = ldx<GT>(gsrc, i * C + j);
       if (GC) x = round_to<GT>(x - mu[i]);
       return x * x + eadd;
     };
-    const int64_t jd = C >= 8 ? (C / 32) * 32 : (C / 4) * 4;
     float cs;
     if (j < jd) {
       cs = tcascade(R, q);
@@ -193,24 +361,46 @@ __global__ __launch_bounds__(KAON_WG) void k_tfin(const KaonTensor* __restrict__
       const int64_t size = R / 4;
       float ps[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) ps[k] = tcascade(size, [&](int64_t i) { return q(4 * i + k); });
+      for (int s = 0; s < 4; ++s) ps[s] = tcascade(size, [&](int64_t i) { return q(4 * i + s); });
       for (int64_t i = 4 * size; i < R; ++i) ps[0] = ps[0] + q(i);
       cs = ((ps[0] + ps[1]) + ps[2]) + ps[3];
     }
     const float nc = klerp(G(T.col)[j], cs / (float)R, hp.w2);
     G(T.col)[j] = nc;
     ws.cf(T)[j] = 1.0f / sqrtf(nc);
+  }
+}
+
+template <int GT, bool GC>
+__global__ __launch_bounds__(kTfinWG) void k_tfin(const KaonTensor* __restrict__ D,
+                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  const KaonItem it = items[blockIdx.x / kTfinSub];
+  const int sb = (int)(blockIdx.x % kTfinSub);
+  const KaonTensor& T = D[it.tensor];
+  const int64_t R = T.R, C = T.C;
+  const int lane = (int)threadIdx.x;
+  if (it.kind == 0) {
+    const int64_t end = (int64_t)it.row0 + it.nrows;
+    const int64_t j0 = (int64_t)it.row0 + ((int64_t)sb * kTfinWG + lane) * kTfinCols;
+    if (j0 >= end) return;
+    const int64_t jd = C >= 8 ? (C / 32) * 32 : (C / 4) * 4;
+    // aligned rows of C % 8 == 0: the lane's eight columns lie in one aligned
+    // vector of every row, and all inside the 32-column blocks or all after them
+    const float eadd = (hp.flags & KAON_F_EPS) ? hp.eps1 : 0.0f;
+    if (T.vec_rows && C % 8 == 0 && j0 + kTfinCols <= jd) {
+      if (GT != KAON_F32 && (eadd == 0.0f || eadd >= 0x1p-100f))
+        tfin_cols<GT, GC, kTfinCols, GT != KAON_F32>(T, ws, hp, j0);
+      else
+        tfin_cols<GT, GC, kTfinCols, false>(T, ws, hp, j0);
+    } else
+      tfin_scalar<GT, GC>(T, ws, hp, j0, kTfinCols, end);
   } else {
     if (sb != 0) return;
     const KAON_G float* row = G((const float*)T.row);
-    if (threadIdx.x < 64) {
-      const float s = tinner32(R, (int)(threadIdx.x & 31), [&](int64_t i) { return row[i]; });
-      if (threadIdx.x == 0) rm_s = s / (float)R;
-    }
-    __syncthreads();
-    const float rm = rm_s;
+    // every lane of the wave returns the whole sum
+    const float rm = tinner32(R, lane & 31, [&](int64_t i) { return row[i]; }) / (float)R;
     KAON_G float* rf = ws.rf(T);
-    for (int64_t i = threadIdx.x; i < R; i += KAON_WG) rf[i] = 1.0f / sqrtf(row[i] / rm);
+    for (int64_t i = lane; i < R; i += kTfinWG) rf[i] = 1.0f / sqrtf(row[i] / rm);
   }
 }
 
@@ -537,7 +727,7 @@ int torch_phases_gt(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mas
   }
   if (mode == 0 && (mask & (1u << 2)) && L.n_fin_items > 0) {
     TfinFn f = gc ? k_tfin<GT, true> : k_tfin<GT, false>;
-    hipLaunchKernelGGL(f, dim3(L.n_fin_items * kTfinSub), dim3(KAON_WG), 0, st, L.descs, L.fin_items, ws, h);
+    hipLaunchKernelGGL(f, dim3(L.n_fin_items * kTfinSub), dim3(kTfinWG), 0, st, L.descs, L.fin_items, ws, h);
   }
   if (mode == 0 && (mask & (1u << 3))) {
     TclipFn f = gc ? k_tclip<GT, true> : k_tclip<GT, false>;

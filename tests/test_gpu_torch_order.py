@@ -166,6 +166,10 @@ EXTRA = {
                             dict(lr=1e-3, betas=(0.8, 0.99), momentum_dtype="int8", bf16_method="none",
                                  gradient_centralization=False, cautious=False), steps=3),
     # many rows (the cascade's second level) and long 1-D tensors (rows of > 2^16 terms)
+    # column sums at four columns per lane (1536 < R <= 3072), 2048 rows with int8
+    # codes and 1600 rows of 96 columns
+    "mid_rows_bf16": _case("adakaon", [[2048, 640], [1600, 96], [640]],
+                           dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8", weight_decay=0.01)),
     "tall_f32": _case("adakaon", [[4100, 40], [70000]],
                       dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="float32", weight_decay=0.01),
                       p="f32", g="f32"),

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KAON_ABI_VERSION 9
+#define KAON_ABI_VERSION 10
 
 /* element types of params / grads (p.dtype, p.grad.dtype); fp16 params and
  * grads (both fp16) step in Adakaon, Lion, AdaMuon and AdaPNM plans only,
@@ -218,6 +218,13 @@ typedef struct KaonPlanInfo {
   int32_t n_ns_sq_big;    /* of which the leading big-tile items (kind 1) */
   int32_t n_ns_rect_big;
   int64_t ws_words;       /* workspace size in 4-byte words */
+  /* The tensors whose torch-order clip norm is long (descs[k].by_size for k <
+   * n_long; see kaon_adakaon_step): their chains run on a second stream beside
+   * the other tensors' clip, keep count and apply.  Their phase-5/6 items are the
+   * leading n_long_fast of the specialized items and the leading n_long_rest of
+   * the others (elem_items[n_fast ..)).  n_long = 0: one stream. */
+  int32_t n_long, n_long_fast, n_long_rest;
+  int32_t reserved;
 } KaonPlanInfo;
 
 /* What a plan is built for (one param group and dtype pair). */
@@ -251,6 +258,9 @@ typedef struct KaonLaunch {
   void* workspace;            /* device, ws_words * 4 bytes, 16-byte aligned */
   int64_t ws_words;           /* KaonPlanInfo.ws_words of the plan that filled descs: the
                                  workspace the descriptors' offsets address, in 4-byte words */
+  int32_t n_long, n_long_fast, n_long_rest; /* KaonPlanInfo's (0, or n_fast lowered below
+                                 n_long_fast: the torch-order step on one stream) */
+  int32_t reserved;
 } KaonLaunch;
 
 /* Per-launch hyper-parameters of one param group, rounded to fp32 on the

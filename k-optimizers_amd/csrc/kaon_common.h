@@ -246,6 +246,9 @@ enum { FF_GC = 1, FF_CAUT = 2, FF_WD = 4, FF_NKR = 8, FF_NKC = 16, FF_GCW = 32 }
 // order.  Both return a HIP status.
 int torch_phases(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mask, int mode, hipStream_t st);
 int torch_momentum_sumsq(const KaonLaunch& L, Ws ws, int codec, hipStream_t st);
+// Phase 3 in torch's order (the clip norm's chains) for the tensors of size ranks
+// [t0, t1) (descs[k].by_size); a HIP status.
+int torch_clip(const KaonLaunch& L, Ws ws, const KaonHyper& h, int32_t t0, int32_t t1, hipStream_t st);
 
 // A phase-5/6 kernel over work items: (descriptors, items, workspace, hyper-parameters).
 using ElemFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);

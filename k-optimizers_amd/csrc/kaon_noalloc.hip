@@ -85,5 +85,6 @@ extern "C" int kaon_adakaon_step_noalloc(const KaonLaunch* L, const KaonHyper* h
   if (rc) return rc;
   KaonLaunch l = *L;
   l.workspace = ws;
+  l.n_long = 0;  // a torch-order step on the caller's stream alone: the side stream would be created here
   return kaon_adakaon_step(&l, hp, stream);
 }

@@ -390,6 +390,26 @@ extern "C" int kaon_plan(const KaonPlanArgs* args, KaonTensor* descs, int32_t n,
     for (int32_t i = 0; i < n; ++i) ord[i] = i;
     std::stable_sort(ord.begin(), ord.end(), [&](int32_t a, int32_t b) { return descs[a].n > descs[b].n; });
     for (int32_t k = 0; k < n; ++k) descs[k].by_size = ord[k];
+    // The torch-order clip norm of a tensor is n / 8 dependent fmas.  The tensors
+    // whose chain is at least half the longest (when that is at least 2^18 steps
+    // and shorter tensors remain) run their chains on a second stream while the
+    // rest step (Adakaon plans: kaon_adakaon_step).  They are a prefix of by_size,
+    // and their phase-5/6 items a prefix of the specialized items and of the
+    // others (both sorted largest tensors first).
+    const int64_t nmax = n > 0 ? descs[ord[0]].n : 0;
+    if (opt == KAON_OPT_ADAKAON && nmax >= (int64_t)1 << 21) {
+      const int64_t thr = (nmax + 1) / 2;
+      int32_t nl = 0;
+      while (nl < n && descs[ord[nl]].n >= thr) ++nl;
+      if (nl < n) {
+        info->n_long = nl;
+        for (const RowIt& r : elems) {
+          if (descs[r.it.tensor].n < thr) continue;
+          if (r.fast) ++info->n_long_fast;
+          else ++info->n_long_rest;
+        }
+      }
+    }
   }
   if (row_items)
     for (size_t k = 0; k < rows.size(); ++k) row_items[k] = rows[k].it;

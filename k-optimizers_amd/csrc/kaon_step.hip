@@ -31,6 +31,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "kaon_common.h"
@@ -3001,6 +3002,40 @@ PdFn pd2_fn(int pt, int gt, int codec) {
 // and the gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
 // rides along (the reference's add_stochastic_ has no fp16 path,
 // _stochastic_rounding.py:55-68).
+// The second stream of a torch-order Adakaon step (the long tensors' clip
+// chains), one per device, created on first use with default priority and
+// non-blocking (no implicit order with the legacy default stream), with the
+// fork and join events.  The mutex is held while a step enqueues its fork and
+// join, so steps issued from several host threads do not interleave their
+// records of the shared events.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex mu;
+};
+constexpr int kSideDevices = 64;
+SideStream g_side[kSideDevices];
+std::mutex g_side_mu;
+
+int side_stream(SideStream** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("kaon: hipGetDevice", e);
+  if (dev < 0 || dev >= kSideDevices) return fail("kaon: device index out of range for the side stream");
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream& ss = g_side[dev];
+  if (!ss.s) {
+    if ((e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess)
+      return fail("kaon: side-stream event", e);
+    if ((e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess)
+      return fail("kaon: side-stream event", e);
+    if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess)
+      return fail("kaon: side stream", e);
+  }
+  *out = &ss;
+  return 0;
+}
+
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool half_ok = false) {
   if (!L || !hp) return fail(who);
   if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16 && hp->p_dtype != KAON_F16)
@@ -3040,6 +3075,54 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
   const int codec = mom ? h.codec : KAON_MOM_NONE;
   if (!mom) h.flags &= ~(KAON_F_MOMENTUM | KAON_F_NK_REMOVE | KAON_F_NK_CLIMB);
   h.codec = codec;
+  const bool quant = codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT;
+  // phases 5 and 6 over a launch's elem items (or a sub-range of them)
+  auto elem_phases = [&](const KaonLaunch& l) {
+    int r = 0;
+    if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant) &&
+        (r = launch_elem<KAON_OPT_ADAKAON, 5>(l, ws, h, codec, st)))
+      return r;
+    if ((mask & (1u << 6)) && (r = launch_elem<KAON_OPT_ADAKAON, 6>(l, ws, h, codec, st))) return r;
+    return 0;
+  };
+  // the long-chain split as the planner left it (a caller that lowers n_fast
+  // below n_long_fast, to send items to the generic kernel, gets one stream)
+  const bool split_ok = L->n_long > 0 && L->n_long < L->n_tensors && L->n_long_fast >= 0 &&
+                        L->n_long_fast <= L->n_fast && L->n_long_rest >= 0 &&
+                        L->n_long_rest <= L->n_elem_items - L->n_fast;
+  if ((h.flags & KAON_F_TORCH_ORDER) && split_ok && (mask & 0x68u) == 0x68u) {
+    // The torch-order clip norm is n / 8 dependent fmas per tensor; the long
+    // tensors' chains run on the side stream while the launch stream does the
+    // other tensors' clip, keep count and apply, then theirs.  Each tensor's
+    // kernels and their order are those of the one-stream step.
+    int e = torch_phases(*L, ws, h, mask & 0x06u, 0, st);
+    if (e) return fail("kaon: torch-order sum launch", (hipError_t)e);
+    SideStream* ss = nullptr;
+    if ((rc = side_stream(&ss))) return rc;
+    // the elem items of the long tensors (leading in both parts) and of the others
+    KaonLaunch lf = *L, lr = *L, sf = *L, sr = *L;
+    lf.n_fast = lf.n_elem_items = L->n_long_fast;
+    lr.elem_items = L->elem_items + L->n_fast;
+    lr.n_fast = 0;
+    lr.n_elem_items = L->n_long_rest;
+    sf.elem_items = L->elem_items + L->n_long_fast;
+    sf.n_fast = sf.n_elem_items = L->n_fast - L->n_long_fast;
+    sr.elem_items = L->elem_items + L->n_fast + L->n_long_rest;
+    sr.n_fast = 0;
+    sr.n_elem_items = L->n_elem_items - L->n_fast - L->n_long_rest;
+    std::lock_guard<std::mutex> lock(ss->mu);
+    hipError_t he;
+    if ((he = hipEventRecord(ss->fork, st)) != hipSuccess) return fail("kaon: side-stream fork", he);
+    if ((he = hipStreamWaitEvent(ss->s, ss->fork, 0)) != hipSuccess) return fail("kaon: side-stream fork", he);
+    if ((e = torch_clip(*L, ws, h, 0, L->n_long, ss->s))) return fail("kaon: torch-order clip launch", (hipError_t)e);
+    if ((he = hipEventRecord(ss->join, ss->s)) != hipSuccess) return fail("kaon: side-stream join", he);
+    if ((e = torch_clip(*L, ws, h, L->n_long, L->n_tensors, st)))
+      return fail("kaon: torch-order clip launch", (hipError_t)e);
+    if ((rc = elem_phases(sf)) || (rc = elem_phases(sr))) return rc;
+    if ((he = hipStreamWaitEvent(st, ss->join, 0)) != hipSuccess) return fail("kaon: side-stream join", he);
+    if ((rc = elem_phases(lf)) || (rc = elem_phases(lr))) return rc;
+    return 0;
+  }
   if (h.flags & KAON_F_TORCH_ORDER) {
     // the GC / row / column / row-factor means and the clip norm in torch CPU's order
     const int e = torch_phases(*L, ws, h, mask & 0x1Eu, 0, st);
@@ -3059,14 +3142,7 @@ int kaon_adakaon_phases(const KaonLaunch* L, const KaonHyper* hp, uint32_t mask,
       if ((rc = check_launch("kaon: k_clipdiv launch"))) return rc;
     }
   }
-  const bool quant = codec == KAON_MOM_INT8 || codec == KAON_MOM_4BIT;
-  if ((mask & (1u << 5)) && ((h.flags & KAON_F_CAUTIOUS) || quant)) {
-    if ((rc = launch_elem<KAON_OPT_ADAKAON, 5>(*L, ws, h, codec, st))) return rc;
-  }
-  if (mask & (1u << 6)) {
-    if ((rc = launch_elem<KAON_OPT_ADAKAON, 6>(*L, ws, h, codec, st))) return rc;
-  }
-  return 0;
+  return elem_phases(*L);
 }
 
 int kaon_adakaon_step(const KaonLaunch* L, const KaonHyper* hp, void* stream) {

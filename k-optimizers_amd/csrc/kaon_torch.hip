@@ -664,13 +664,15 @@ __device__ __forceinline__ void tclip_body(const KaonTensor& T, const Ws& ws, co
 }
 
 template <int GT, bool GC>
-__global__ __launch_bounds__(kTcWG) void k_tclip(const KaonTensor* __restrict__ D, int32_t n_tensors, Ws ws,
+__global__ __launch_bounds__(kTcWG) void k_tclip(const KaonTensor* __restrict__ D, int32_t t0, int32_t t1, Ws ws,
                                                  KaonHyper hp) {
   __shared__ __align__(16) float lds[2 * 8 * kTcLd];
   __shared__ int simd[kTcWG / 64];
-  if ((int)blockIdx.x >= n_tensors) return;
-  // the longest tensors first: their chains are the phase's critical path
-  const KaonTensor& T = D[D[blockIdx.x].by_size];
+  // ranks [t0, t1) of the tensors by decreasing size: the longest first, their
+  // chains are the phase's critical path
+  const int rank = t0 + (int)blockIdx.x;
+  if (rank >= t1) return;
+  const KaonTensor& T = D[D[rank].by_size];
   if (T.n == 0) return;
   // each wave's SIMD (HW_ID bits 5:4); the chain wave's SIMD mates stay idle
   // unless more than two of the eight waves share that SIMD
@@ -715,7 +717,7 @@ __global__ __launch_bounds__(64) void k_tmsq(const KaonTensor* __restrict__ D, i
 
 using TrowFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper, int);
 using TfinFn = void (*)(const KaonTensor*, const KaonItem*, Ws, KaonHyper);
-using TclipFn = void (*)(const KaonTensor*, int32_t, Ws, KaonHyper);
+using TclipFn = void (*)(const KaonTensor*, int32_t, int32_t, Ws, KaonHyper);
 
 
 template <int GT>
@@ -729,10 +731,18 @@ int torch_phases_gt(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mas
     TfinFn f = gc ? k_tfin<GT, true> : k_tfin<GT, false>;
     hipLaunchKernelGGL(f, dim3(L.n_fin_items * kTfinSub), dim3(kTfinWG), 0, st, L.descs, L.fin_items, ws, h);
   }
-  if (mode == 0 && (mask & (1u << 3))) {
+  if (mode == 0 && (mask & (1u << 3)) && L.n_tensors > 0) {
     TclipFn f = gc ? k_tclip<GT, true> : k_tclip<GT, false>;
-    hipLaunchKernelGGL(f, dim3(L.n_tensors), dim3(kTcWG), 0, st, L.descs, L.n_tensors, ws, h);
+    hipLaunchKernelGGL(f, dim3(L.n_tensors), dim3(kTcWG), 0, st, L.descs, 0, L.n_tensors, ws, h);
   }
+  return (int)hipGetLastError();
+}
+
+template <int GT>
+int torch_clip_gt(const KaonLaunch& L, Ws ws, const KaonHyper& h, int32_t t0, int32_t t1, hipStream_t st) {
+  if (t1 <= t0) return 0;
+  TclipFn f = (h.flags & KAON_F_GC) ? k_tclip<GT, true> : k_tclip<GT, false>;
+  hipLaunchKernelGGL(f, dim3(t1 - t0), dim3(kTcWG), 0, st, L.descs, t0, t1, ws, h);
   return (int)hipGetLastError();
 }
 
@@ -746,6 +756,15 @@ int torch_phases(const KaonLaunch& L, Ws ws, const KaonHyper& h, uint32_t mask, 
   return gt == KAON_BF16  ? torch_phases_gt<KAON_BF16>(L, ws, h, mask, mode, st)
          : gt == KAON_F16 ? torch_phases_gt<KAON_F16>(L, ws, h, mask, mode, st)
                           : torch_phases_gt<KAON_F32>(L, ws, h, mask, mode, st);
+}
+
+// Phase 3 of an Adakaon step in torch's order for the tensors of size ranks
+// [t0, t1) (descs[k].by_size).  Returns a HIP status.
+int torch_clip(const KaonLaunch& L, Ws ws, const KaonHyper& h, int32_t t0, int32_t t1, hipStream_t st) {
+  const int gt = h.g_dtype;
+  return gt == KAON_BF16  ? torch_clip_gt<KAON_BF16>(L, ws, h, t0, t1, st)
+         : gt == KAON_F16 ? torch_clip_gt<KAON_F16>(L, ws, h, t0, t1, st)
+                          : torch_clip_gt<KAON_F32>(L, ws, h, t0, t1, st);
 }
 
 // kaon_momentum_sumsq in torch's order (MSAM norm="tensor").

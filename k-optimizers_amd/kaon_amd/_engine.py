@@ -171,6 +171,7 @@ class Plan:
         la.n_ns_sq_big, la.n_ns_rect_big = info.n_ns_sq_big, info.n_ns_rect_big
         la.workspace = self.workspace.data_ptr()
         la.ws_words = int(info.ws_words)
+        la.n_long, la.n_long_fast, la.n_long_rest = info.n_long, info.n_long_fast, info.n_long_rest
         self.launch = la
 
 

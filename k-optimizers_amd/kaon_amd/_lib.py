@@ -12,7 +12,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkaon_amd.so")
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 F32, BF16, F16 = 0, 1, 2
 MOM_NONE, MOM_F32, MOM_BF16, MOM_INT8, MOM_4BIT = 0, 1, 2, 3, 4
@@ -66,7 +66,9 @@ class KaonPlanInfo(ctypes.Structure):
                 ("n_fin_items", ctypes.c_int32), ("n_flat_items", ctypes.c_int32),
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
-                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("ws_words", ctypes.c_int64)]
+                ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("ws_words", ctypes.c_int64),
+                ("n_long", ctypes.c_int32), ("n_long_fast", ctypes.c_int32), ("n_long_rest", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
 
 
 class KaonPlanArgs(ctypes.Structure):
@@ -83,7 +85,8 @@ class KaonLaunch(ctypes.Structure):
                 ("row_runs", ctypes.c_int32 * ROW_CLASSES), ("n_fast", ctypes.c_int32),
                 ("n_elem_items", ctypes.c_int32), ("n_ns_sq", ctypes.c_int32), ("n_ns_rect", ctypes.c_int32),
                 ("n_ns_sq_big", ctypes.c_int32), ("n_ns_rect_big", ctypes.c_int32), ("workspace", ctypes.c_void_p),
-                ("ws_words", ctypes.c_int64)]
+                ("ws_words", ctypes.c_int64), ("n_long", ctypes.c_int32), ("n_long_fast", ctypes.c_int32),
+                ("n_long_rest", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class KaonHyper(ctypes.Structure):

@@ -512,3 +512,46 @@ def test_plan_orders_tensors_longest_first():
     sizes = [descs[i].n for i in order]
     assert sizes == sorted(sizes, reverse=True)
     assert order.index(0) < order.index(3)  # equal sizes keep param order
+
+
+def _plan_elems(shapes, opt=0):
+    L = _lib()
+    n = len(shapes)
+    descs = (L.KaonTensor * n)()
+    for i, s in enumerate(shapes):
+        d = descs[i]
+        numel = int(np.prod(s))
+        d.R, d.C, d.factored = (s[0], numel // s[0], 1) if len(s) >= 2 else (1, numel, 0)
+        d.block4 = 128
+        d.tensor_id = i
+        d.g = d.p = d.m = d.m_scale = 0x1000 * (i + 1)
+    info = L.KaonPlanInfo()
+    args = L.KaonPlanArgs(opt, 3, 1, 1, 0)
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, None, None, None, None, None, ctypes.byref(info)) == 0
+    elems = (L.KaonItem * max(info.n_elem_items, 1))()
+    assert L.lib().kaon_plan(ctypes.byref(args), descs, n, None, elems, None, None, None, None,
+                             ctypes.byref(info)) == 0
+    return descs, info, elems
+
+
+def test_plan_marks_the_long_clip_chains():
+    """The torch-order step's long-chain split (KaonPlanInfo.n_long*): the tensors of at
+    least half the largest numel, a prefix of by_size, and their phase-5/6 items the
+    leading ones of the specialized and of the generic items."""
+    shapes = [[5120, 1280], [1280, 1280, 3, 3], [1280], [640, 11520], [1280, 11520], [8000000], [320, 2880]]
+    descs, info, elems = _plan_elems(shapes)
+    ns = [int(np.prod(s)) for s in shapes]
+    thr = (max(ns) + 1) // 2
+    long_t = {i for i, v in enumerate(ns) if v >= thr}
+    assert info.n_long == len(long_t) == 4  # both 14.7M, the 7.37M conv, the 8M vector
+    ranks = [descs[k].by_size for k in range(len(shapes))]
+    assert set(ranks[:info.n_long]) == long_t
+    fast = [elems[k].tensor for k in range(info.n_fast)]
+    rest = [elems[k].tensor for k in range(info.n_fast, info.n_elem_items)]
+    assert all(t in long_t for t in fast[:info.n_long_fast]) and not any(t in long_t for t in fast[info.n_long_fast:])
+    assert all(t in long_t for t in rest[:info.n_long_rest]) and not any(t in long_t for t in rest[info.n_long_rest:])
+    assert info.n_long_fast > 0 and info.n_long_rest > 0  # the 8M vector takes generic items
+    # no split: every tensor long, the largest under 2^21 elements, a Lion plan
+    for shp, opt in (([[1280, 11520], [1280, 11520]], 0), ([[1024, 2040], [8, 8]], 0), (shapes, 1)):
+        _, info, _ = _plan_elems(shp, opt)
+        assert (info.n_long, info.n_long_fast, info.n_long_rest) == (0, 0, 0), (shp, opt)

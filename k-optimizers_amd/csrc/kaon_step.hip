@@ -2998,10 +2998,6 @@ PdFn pd2_fn(int pt, int gt, int codec) {
   return nullptr;
 }
 
-// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon, AdaPNM, KProdigy
-// and the gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
-// rides along (the reference's add_stochastic_ has no fp16 path,
-// _stochastic_rounding.py:55-68).
 // The second stream of a torch-order Adakaon step (the long tensors' clip
 // chains), one per device, created on first use with default priority and
 // non-blocking (no implicit order with the legacy default stream), with the
@@ -3036,6 +3032,10 @@ int side_stream(SideStream** out) {
   return 0;
 }
 
+// half_ok: the entry point steps fp16 params (Adakaon, Lion, AdaMuon, AdaPNM, KProdigy
+// and the gradient write-back); their grads are fp16 too and no Nekaon / MSAM perturbation
+// rides along (the reference's add_stochastic_ has no fp16 path,
+// _stochastic_rounding.py:55-68).
 int validate(const KaonLaunch* L, const KaonHyper* hp, const char* who, bool half_ok = false) {
   if (!L || !hp) return fail(who);
   if (hp->p_dtype != KAON_F32 && hp->p_dtype != KAON_BF16 && hp->p_dtype != KAON_F16)

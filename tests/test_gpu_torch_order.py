@@ -194,3 +194,39 @@ def test_extra_case_bit_exact_against_oracle_in_torch_order(name):
     with O.torch_order():
         oparams, _oopt, oeval = oracle_case_run(case)
     assert_same_as_oracle(case, oparams, params, opt, evalp=evalp, oeval=oeval, label=name)
+
+
+def test_long_chain_split_matches_one_stream(monkeypatch):
+    """The torch-order step with the long tensors' clip chains on the side stream
+    (KaonLaunch.n_long > 0) against the same steps with every kernel on the launch
+    stream (n_long forced to 0): equal weights, codes, scales and state, bit for bit.
+    Two long convs (14.7 M and 7.4 M elements: both at least half the largest), short
+    matrices and 1-D vectors, so the split covers specialized and generic items
+    on both sides; Nekaon adds the removal and the climb."""
+    print("[gpu] torch order: long-chain split against one stream", flush=True)
+    from kaon_amd import _engine as E
+
+    shapes = [[1280, 1280, 3, 3], [640, 1280, 3, 3], [1280, 1280], [320, 2880], [5120], [1000]]
+    for name, kw in (("adakaon", dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8")),
+                     ("nekaon", dict(lr=1e-4, k=1.5, betas=(0.2, 0.999), momentum_dtype="4bit",
+                                     momentum_4bit_block=64))):
+        case = _case(name, shapes, kw, steps=2, seed=31)
+        split_params, split_opt, _ = run_gpu(case, extra=TORCH)
+        inner = getattr(split_opt, "inner", split_opt)
+        plans = [pl for _key, (_ptrs, pl) in inner._plans.items()]
+        assert plans and max(pl.launch.n_long for pl in plans) == 2, [pl.launch.n_long for pl in plans]
+
+        class OneStreamPlan(E.Plan):
+            def __init__(self, *a, **k):
+                super().__init__(*a, **k)
+                self.launch.n_long = 0
+
+        monkeypatch.setattr(E, "Plan", OneStreamPlan)
+        one_params, one_opt, _ = run_gpu(case, extra=TORCH)
+        monkeypatch.undo()
+        for i, (a, b) in enumerate(zip(split_params, one_params)):
+            assert np.array_equal(to_bits(a), to_bits(b)), (name, i)
+            sa, sb = state_of(split_opt, a), state_of(one_opt, b)
+            for k in sa:
+                if torch.is_tensor(sa[k]):
+                    assert np.array_equal(to_bits(sa[k]), to_bits(sb[k])), (name, i, k)

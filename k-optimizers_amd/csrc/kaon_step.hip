@@ -635,6 +635,13 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
   // q = (G - mu)^2 (+eps1) once per element: into the row sums (lane order:
   // chunk by chunk) and the wave group's column partial (row order)
   const int nw = (int)min<int64_t>(4, ((int64_t)it.nrows + RW - 1) / RW);
+  // Segments per barrier: the wide class (REG2: the clip's run partial in
+  // registers) has the LDS for two, so it waits half as often.  The buffer
+  // sets alternate from one barrier group to the next, across both passes;
+  // each column's partials are added in the same order either way.
+  constexpr int SEGG = REG2 ? 2 : 1;
+  constexpr int NG = (CPL + SEGG - 1) / SEGG;  // barrier groups per pass
+  auto sbuf = [&](int pass, int k) { return seg[((pass * NG + k / SEGG) & 1) * SEGG + k % SEGG]; };
   float a2[RW];
 #pragma unroll
   for (int j = 0; j < RW; ++j) a2[j] = 0.0f;
@@ -655,10 +662,14 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
           }
         }
       }
-      seg_put(seg[k & 1], wr.w, wr.lane, v);
+      seg_put(sbuf(0, k), wr.w, wr.lane, v);
     }
-    __syncthreads();
-    seg_fold(seg[k & 1], nw, (int64_t)k * 512, C, part, acc, last, tid, racc);
+    if (k % SEGG == SEGG - 1 || k == CPL - 1) {
+      __syncthreads();
+#pragma unroll
+      for (int kk = k - k % SEGG; kk <= k; ++kk)
+        seg_fold(sbuf(0, kk), nw, (int64_t)kk * 512, C, part, acc, last, tid, racc);
+    }
   }
   float wr_inv[RW];  // 1 / row_j (the new row) for the clip partial
 #pragma unroll
@@ -692,13 +703,18 @@ __device__ __forceinline__ void pf_stats_body(const KaonTensor& T, const KaonIte
           }
         }
       }
-      seg_put(seg[(CPL + k) & 1], wr.w, wr.lane, v);
+      seg_put(sbuf(1, k), wr.w, wr.lane, v);
     }
-    __syncthreads();
-    if (REG2)
-      seg_fold_reg(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, rr2[2 * k], rr2[2 * k + 1]);
-    else
-      seg_fold(seg[(CPL + k) & 1], nw, (int64_t)k * 512, C, part2, acc, last, tid, racc2);
+    if (k % SEGG == SEGG - 1 || k == CPL - 1) {
+      __syncthreads();
+#pragma unroll
+      for (int kk = k - k % SEGG; kk <= k; ++kk) {
+        if (REG2)
+          seg_fold_reg(sbuf(1, kk), nw, (int64_t)kk * 512, C, part2, acc, last, tid, rr2[2 * kk], rr2[2 * kk + 1]);
+        else
+          seg_fold(sbuf(1, kk), nw, (int64_t)kk * 512, C, part2, acc, last, tid, racc2);
+      }
+    }
   }
 }
 
@@ -778,7 +794,7 @@ template <int EPS>
 __global__ __launch_bounds__(KAON_WG) void k_pf_stats_wide(const KaonTensor* __restrict__ D,
                                                            const KaonItem* __restrict__ items, Ws ws, KaonHyper hp,
                                                            int mode) {
-  __shared__ __attribute__((aligned(16))) float seg[2][4][512];
+  __shared__ __attribute__((aligned(16))) float seg[4][4][512];  // two buffer sets of two segments
   __shared__ __attribute__((aligned(16))) float racc[24 * 512];
   pf_stats_run<2, EPS, true>(D, items, ws, hp, mode, seg, racc, nullptr);
 }

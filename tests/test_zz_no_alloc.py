@@ -6,7 +6,9 @@ allocation-free entry point, which takes the workspace from the library's
 static device array.  Weights and every state tensor must agree bit for bit,
 on two calls in a row (the second plan smaller than the first, so the array
 still holds the first call's contents), over two steps each.  A plan larger
-than the static workspace is refused with an error, before any launch.
+than the static workspace is refused with an error, before any launch.  In torch
+order the allocation-free step keeps the long clip chains on the caller's stream
+(no side stream) and agrees with the two-stream step.
 """
 import ctypes
 
@@ -54,7 +56,7 @@ def _step_noalloc(opt):
             L.check(rc, "kaon_adakaon_step_noalloc")
 
 
-def _run(shapes, momentum_dtype, seed, steps=2):
+def _run(shapes, momentum_dtype, seed, steps=2, **kw):
     from kaon_amd import Adakaon
 
     rng = np.random.default_rng(seed)
@@ -65,7 +67,7 @@ def _run(shapes, momentum_dtype, seed, steps=2):
     for use_noalloc in (False, True):
         params = [torch.nn.Parameter(torch.from_numpy(v).to(DEV, torch.bfloat16)) for v in init]
         opt = Adakaon(params, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01, momentum_dtype=momentum_dtype,
-                      momentum_4bit_block=64)
+                      momentum_4bit_block=64, **kw)
         opt.sr_seed = seed
         for k in range(steps):
             for p, g in zip(params, grads[k]):
@@ -101,6 +103,15 @@ def test_noalloc_matches_step_two_calls_second_smaller():
     ws_small = max(pl.info.ws_words for _k, (_ptrs, pl) in opt._plans.items())
     assert ws_small < ws_big
     assert L.lib().kaon_abi_version() == L.ABI_VERSION
+
+
+def test_noalloc_torch_order_matches_the_split_step():
+    """reduction_order="torch" on a plan with a long clip chain (KaonLaunch.n_long > 0):
+    kaon_adakaon_step runs that chain on its side stream, the allocation-free entry point
+    keeps the whole step on the caller's stream; the results agree bit for bit."""
+    print("[gpu] noalloc: torch order, a 14.7M-element conv beside short tensors", flush=True)
+    opt = _run([[1280, 1280, 3, 3], [1280, 1280], [1280]], "int8", seed=3, reduction_order="torch")
+    assert max(pl.launch.n_long for _k, (_ptrs, pl) in opt._plans.items()) == 1
 
 
 def test_noalloc_rejects_a_plan_beyond_the_static_workspace():

@@ -118,6 +118,13 @@ EXTRA = {
     # BASELINE configs[1] as given: Lion int8, betas=(0.95, 0.98), lr 2e-4, wd 0 (the
     # specialized kernel without weight decay), cautious, GC, SR
     "cfg1_lion_int8": _case("lion", _SDXL, dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="int8"), steps=4),
+    # rows of three chunks per lane whose third chunk fills 32, 16 or 2 lanes (C = 1280,
+    # 1152, 1040), in wave groups of odd row counts (37 rows: waves of 6, 6, 1 and none;
+    # 5 rows; 1 row), clipped
+    "ada_int8_rows_1040_1280": _case("adakaon", [[37, 1280], [5, 1152], [1, 1280], [30, 1040], [1280]],
+                                     dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="int8", clip_threshold=0.05)),
+    "lion_int8_rows_1040_1280": _case("lion", [[37, 1280], [5, 1152], [30, 1040]],
+                                      dict(lr=2e-4, betas=(0.95, 0.98), momentum_dtype="int8")),
 }
 
 

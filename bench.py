@@ -35,7 +35,7 @@ Besides the JSON line's ``value`` (Gparam/s) the line carries
   give the reference's bits; ms per step and its phases;
 * ``cpu_baseline``: the reference's CPU path, its native foreach step restated
   in torch (oracle/torch_foreach.py, pinned bit for bit against the reference's
-  fixtures), on the job's host cores over a fixed sample of the set (every 8th
+  fixtures), on the job's host cores over a fixed sample of the set (every 2nd
   tensor by default, ``--cpu-stride 1`` for the whole set), the median of three
   steps after a warmup; ``cpu_oracle_baseline`` beside it is the C oracle
   (oracle/kaon_oracle.c) on the same host (at most 16 threads).  4-bit
@@ -642,7 +642,8 @@ def cpu_torch_foreach(params, name, stride: int) -> dict:
         opt.step()
         walls.append(time.perf_counter() - t0)
     med = statistics.median(walls)
-    what = "the whole set" if stride == 1 else f"every {stride}th tensor of a fixed random order of the set"
+    nth = {2: "2nd", 3: "3rd"}.get(stride, f"{stride}th")
+    what = "the whole set" if stride == 1 else f"every {nth} tensor of a fixed random order of the set"
     return {"value": round(nparam / med / 1e9, 4), "unit": "Gparam/s", "cores": threads, "kind": "port",
             "cpu_model": _cpu_model(), "ms_per_step": round(med * 1e3, 1),
             "full_set_s_per_step_est": round(med * sum(p.numel() for p in params) / nparam, 2),
@@ -662,9 +663,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of one CPU-baseline step (the whole set is timed when it fits)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-stride", type=int, default=8,
+    ap.add_argument("--cpu-stride", type=int, default=2,
                     help="the torch-CPU baseline (Adakaon / Lion workloads) times every N-th tensor of a fixed "
-                         "order of the set; 1 = the whole set")
+                         "order of the set (the default 2: half the set, ≈20 s of CPU work); 1 = the whole set")
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-torch-order", action="store_true",
                     help="skip the reduction_order='torch' timing of Adakaon / Lion workloads")

@@ -3037,12 +3037,20 @@ int side_stream(SideStream** out) {
   std::lock_guard<std::mutex> lock(g_side_mu);
   SideStream& ss = g_side[dev];
   if (!ss.s) {
-    if ((e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess)
-      return fail("kaon: side-stream event", e);
-    if ((e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess)
-      return fail("kaon: side-stream event", e);
-    if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess)
+    // all three or none: a failed call leaves nothing behind for the next to trip on
+    hipEvent_t fork = nullptr, join = nullptr;
+    hipStream_t st = nullptr;
+    if ((e = hipEventCreateWithFlags(&fork, hipEventDisableTiming)) == hipSuccess &&
+        (e = hipEventCreateWithFlags(&join, hipEventDisableTiming)) == hipSuccess &&
+        (e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) == hipSuccess) {
+      ss.fork = fork;
+      ss.join = join;
+      ss.s = st;
+    } else {
+      if (join) (void)hipEventDestroy(join);
+      if (fork) (void)hipEventDestroy(fork);
       return fail("kaon: side stream", e);
+    }
   }
   *out = &ss;
   return 0;

@@ -3,7 +3,7 @@
 The shape vocabulary is BASELINE's configs[1]: conv [C_out, C_in, 3, 3] with
 C in {320, 640, 1280}, linears [1280|2048|5120 x 640|1280|2048|5120] and 1-D
 norm/bias vectors; the counts follow SDXL's block structure: 1,678 tensors,
-2,663,994,880 params (74.5 % of them in tensors above 2M elements, the ones the
+2,664,150,400 params (74.5 % of them in tensors above 2M elements, the ones the
 reference's foreach path steps one by one, src/kaon/adakaon.py:765-791).
 
 Inputs are generated on the device, one torch generator per tensor keyed by

@@ -722,7 +722,7 @@ def main() -> int:
                "config": {"workload": w["desc"], "n_tensors": len(shapes), "n_params": nparam, "params": "f32",
                           "grads": "f32", "momentum": w["kw"]["momentum_dtype"], "parallelism": "none (1 GPU)",
                           "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
-                          "launches_per_step": "6 kernels"}}
+                          "launches_per_step": "5 kernels"}}
         if not args.no_breakdown:
             out["phases_ms"] = {PHASE_NAMES[k]: round(v, 4) for k, v in sorted(phase_breakdown(opt, args.workload)
                                                                                  .items())}

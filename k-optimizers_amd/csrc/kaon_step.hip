@@ -79,6 +79,154 @@ __device__ __forceinline__ void add_coupled_wd(const KaonTensor& T, const KaonHy
 }
 
 // =============================================================== phase 1
+// The canonical row sum of a row held by an aligned group of 2^lsh <= 32
+// lanes (lane cl of the group holding the sum of its chunk cl, 0 past the
+// row's chunks).  The 64-lane butterfly of the one-row-per-wave layout adds,
+// at offsets 32 ... 2^lsh, only the +0 of lanes past the row, which leaves each
+// lane sum x as x + 0 (-0 becomes +0); its offsets 2^(lsh-1) ... 1 pair lanes
+// of the same group.  So the sum is that group's butterfly of x + 0.
+__device__ __forceinline__ float group_csum(float a, int lsh) {
+  float v = a + 0.0f;
+  for (int o = (1 << lsh) >> 1; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Phase 1 of one slice of a factored tensor whose rows have at most 32 chunks
+// (the register layouts, RW > 1 rows per wave group, no coupled decay).  A
+// wave works on 64 / L of its rows side by side, L = 2^ceil(log2(chunks))
+// lanes per row, lane cl of a row's group taking chunk cl: one memory round
+// trip per 64 / L rows instead of one per row.  Every value and every sum
+// order is that of k_stats's one-row-at-a-time body: the row sums through
+// group_csum, and each column partial (the wave group's rows added in row
+// order, then the wave groups folded in order in LDS) built by lane group 0,
+// which takes each row's values from that row's lane group in turn.
+template <int GT>
+__device__ __forceinline__ void stats_packed(const KaonTensor& T, const KaonItem& sit, const Ws& ws,
+                                             const KaonHyper& hp, int mode, const void* gsrc, KAON_G float* part,
+                                             KAON_G float* part2, bool first, bool alg, float* lds_col) {
+  const int64_t C = T.C;
+  const int nch = (int)((C + 7) >> 3);
+  const bool vec = T.vec_rows != 0;
+  const bool eps = (hp.flags & KAON_F_EPS) != 0;
+  const bool gc = (hp.flags & KAON_F_GC) != 0;
+  const WaveRows wr = wave_rows(sit);
+  const int lsh = nch <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nch - 1));
+  const int P = 64 >> lsh;
+  const int grp = wr.lane >> lsh;
+  const int cl = wr.lane & ((1 << lsh) - 1);
+  const int cnt0 = chunk_cnt(cl, C);  // elements of the lane's chunk in any row
+  KAON_G float* mu_arr = ws.mu(T);
+  float colacc[8], acc2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    colacc[i] = 0.0f;
+    acc2[i] = 0.0f;
+  }
+  for (int64_t r0 = wr.rb; r0 < wr.re; r0 += P) {
+    const int nv = (int)min<int64_t>(P, wr.re - r0);  // rows of this pass (wave-uniform)
+    const bool rvalid = grp < nv;
+    const int64_t r = rvalid ? r0 + grp : wr.rb;
+    const int cnt = rvalid ? cnt0 : 0;
+    float x[8];
+    if (cnt > 0) {
+      ld8<GT>(gsrc, r * C + (int64_t)cl * 8, cnt, vec && cnt == 8, x);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = 0.0f;
+    }
+    const float row_old = mode == 0 ? T.row[r] : 0.0f;
+    float xb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xb[i] = x[i];
+    float mu = 0.0f;
+    if (gc) {
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < cnt) a = a + x[i];
+      mu = round_to<GT>(group_csum(a, lsh) / (float)C);
+      if (rvalid && cl == 0) mu_arr[r] = mu;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float a0 = xb[i] - mu, a1 = xb[i + 1] - mu;
+        round_pair<GT>(a0, a1);
+        xb[i] = a0;
+        xb[i + 1] = a1;
+      }
+    }
+    if (mode == 1) continue;
+    float q[8];
+    float a2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      q[i] = xb[i] * xb[i];
+      if (eps) q[i] = q[i] + hp.eps1;
+      if (i < cnt) a2 = a2 + q[i];
+    }
+    const float s2 = group_csum(a2, lsh);
+    const float nr = klerp(row_old, s2 / (float)C, hp.w2);
+    if (rvalid && cl == 0) T.row[r] = nr;
+    // the column partial: rows r0, r0 + 1, ... in order
+    for (int g = 0; g < nv; ++g) {
+      const int src = (g << lsh) + cl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) colacc[i] = colacc[i] + __shfl(q[i], src, 64);
+    }
+    if (alg) {
+      // the clip's second column partial, t = (G * G) / row (the new row; no
+      // eps1), G formed again from the raw gradient as the row-by-row body does
+      const float w = 1.0f / nr;
+      float t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float gv = gc ? round_to<GT>(x[i] - mu) : x[i];
+        t[i] = (gv * gv) * w;
+      }
+      for (int g = 0; g < nv; ++g) {
+        const int src = (g << lsh) + cl;
+        const bool start = r0 == wr.rb && g == 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float tv = __shfl(t[i], src, 64);
+          acc2[i] = start ? tv : acc2[i] + tv;
+        }
+      }
+    }
+  }
+  if (mode == 1) return;
+  // fold the wave-group partials in group order into the slice partial (lane
+  // group 0 holds them, lane cl for chunk cl), then into the run partial
+  const bool has_rows = wr.re > wr.rb;
+  const bool holder = grp == 0 && has_rows;
+  for (int wf = 0; wf < 4; ++wf) {
+    if (wr.w == wf && holder) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < cnt0) {
+          const int j = cl * 8 + i;
+          lds_col[j] = wf == 0 ? colacc[i] : lds_col[j] + colacc[i];
+        }
+    }
+    __syncthreads();
+  }
+  for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part[j] = first ? lds_col[j] : part[j] + lds_col[j];
+  __syncthreads();  // lds_col is reused
+  if (!alg) return;
+  for (int wf = 0; wf < 4; ++wf) {
+    if (wr.w == wf && holder) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < cnt0) {
+          const int j = cl * 8 + i;
+          lds_col[j] = wf == 0 ? acc2[i] : lds_col[j] + acc2[i];
+        }
+    }
+    __syncthreads();
+  }
+  for (int64_t j = threadIdx.x; j < C; j += KAON_WG) part2[j] = first ? lds_col[j] : part2[j] + lds_col[j];
+  __syncthreads();  // lds_col is reused by the next slice
+}
+
 // mode 0 (Adakaon): GC row mean (stored), row EMA of mean_C(G^2), column
 // partial of the slice (wave groups folded in order in LDS); 1-D tensors: v
 // EMA.  mode 1 (Lion): GC row means only.  CPL > 0 keeps a row of up to CPL
@@ -118,8 +266,17 @@ __global__ __launch_bounds__(KAON_WG) void k_stats(const KaonTensor* __restrict_
   const int RW = it.kind;
   KAON_G float* part = run_part(ws, T, it);
   const int nsl = run_slices(it);
+  // rows of at most 32 chunks (the class of 1-4 chunks per lane): side by side
+  const bool packed = CPL == 4 && nch <= 32 && RW > 1 && !cwd;
 #pragma clang loop unroll(disable)
   for (int sl = 0; sl < nsl; ++sl) {
+  if constexpr (CPL == 4) {
+    if (packed) {
+      stats_packed<GT>(T, slice_item(it, sl), ws, hp, mode, gsrc, part, part + (int64_t)T.ngroups * C, sl == 0, alg,
+                       lds_col);
+      continue;
+    }
+  }
   const WaveRows wr = wave_rows(slice_item(it, sl));
 
   // registers: row buffer (CPL chunks) and the wave-group column partial
@@ -1072,12 +1229,23 @@ struct RowCtx {
   bool fast;
 };
 
-template <int OPT, int PHASE, int PT, int GT, int CODEC>
-__global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__ D,
-                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
-  __shared__ uint32_t keep_s[4];
-  const KaonItem it = items[blockIdx.x];
-  const KaonTensor& T = D[it.tensor];
+// A row value read once per row: wave-uniform (a scalar) when the wave works
+// on one row at a time, per lane when it packs several rows.
+template <bool PK>
+__device__ __forceinline__ float row_val(float x) {
+  return PK ? x : uniform_f(x);
+}
+
+// The rows of a wave's share of a slice, phases 5 and 6.  PK == false: one row
+// at a time, lane l taking chunks l, l+64, ....  PK == true (rows of at most 32
+// chunks): L = 2^ceil(log2(chunks)) lanes per row, 64 / L rows side by side,
+// lane cl of a row's lane group taking chunk cl.  Every element's arithmetic
+// is the same either way; the only reductions across lanes are the keep count
+// (an integer sum) and the int8 row absmax (a maximum), neither of which
+// depends on the order.  Returns the lane's keep count.
+template <int OPT, int PHASE, int PT, int GT, int CODEC, bool PK>
+__device__ __forceinline__ uint32_t elem_rows(const KaonTensor& T, const KaonItem& it, const Ws& ws,
+                                              const KaonHyper& hp) {
   const int64_t C = T.C, n = T.n;
   const int64_t nch = (C + 7) >> 3;
   const int cpl = (int)((nch + 63) >> 6);
@@ -1119,19 +1287,30 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   uint32_t c_blk = 0xFFFFFFFFu;
   float c_old = 1.0f, c_new = 1.0f;
   double c_r = 1.0;
+  // lanes per row (2^lsh) and rows side by side (P); the lane's row in a pass
+  // and its chunk
+  const int lsh = PK ? (nch <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nch - 1))) : 6;
+  const int P = 64 >> lsh;
+  const int grp = wr.lane >> lsh;
+  const int cl = wr.lane & ((1 << lsh) - 1);
+  const bool lead = cl == 0;  // the lane that stores the row's values
 
-  for (int64_t r = wr.rb; r < wr.re; ++r) {
-    // ---- per-row context (wave-uniform)
+  for (int64_t r0 = wr.rb; r0 < wr.re; r0 += P) {
+    // the lane's row; lanes past the wave's rows read the first row's context
+    // and take no chunk
+    const bool rvalid = r0 + grp < wr.re;
+    const int64_t r = rvalid ? r0 + grp : wr.rb;
+    // ---- per-row context (wave-uniform unless PK)
     RowCtx rc;
-    rc.mu = gc ? uniform_f(ws.mu(T)[r]) : 0.0f;
-    rc.rf = (OPT != KAON_OPT_LION && factored) ? uniform_f(ws.rf(T)[r]) : 0.0f;
+    rc.mu = gc ? row_val<PK>(ws.mu(T)[r]) : 0.0f;
+    rc.rf = (OPT != KAON_OPT_LION && factored) ? row_val<PK>(ws.rf(T)[r]) : 0.0f;
     rc.oldsc = 1.0f;
     rc.newsc = 1.0f;
     rc.rnew = 1.0;
     if (CODEC == KAON_MOM_INT8 && mom) {
-      rc.oldsc = uniform_f(PHASE == 5 ? T.m_scale[r] : ws.roldsc(T)[r]);
+      rc.oldsc = row_val<PK>(PHASE == 5 ? T.m_scale[r] : ws.roldsc(T)[r]);
       if (PHASE == 6) {
-        rc.newsc = uniform_f(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
+        rc.newsc = row_val<PK>(fmaxf(__uint_as_float(ws.ramax(T)[r]), 1e-12f) / 127.0f);
         rc.rnew = rcp64(rc.newsc);
       }
     }
@@ -1140,8 +1319,8 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
     float row_amax = 0.0f;
 
     for (int k = 0; k < cpl; ++k) {
-      const int64_t c = wr.lane + 64 * k;
-      const int cnt = chunk_cnt(c, C);
+      const int64_t c = cl + 64 * k;
+      const int cnt = rvalid ? chunk_cnt(c, C) : 0;
       const int64_t j0 = c * 8;
       const int64_t e0 = r * C + j0;
       const bool vec = vec_t && cnt == 8;
@@ -1428,20 +1607,47 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
     // ---- end of row
     if (CODEC == KAON_MOM_INT8 && quant) {
       if (PHASE == 5) {
-        const float am = wave_max(row_amax);
-        if (wr.lane == 0) {
+        float am;
+        if (PK) {
+          // the maximum over the row's lane group (the other lanes of a
+          // 64-lane row hold 0, which a maximum of |m| ignores)
+          am = row_amax;
+          for (int o = (1 << lsh) >> 1; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        } else {
+          am = wave_max(row_amax);
+        }
+        if (rvalid && lead) {
           ws.ramax(T)[r] = __float_as_uint(am);
           ws.roldsc(T)[r] = rc.oldsc;
         }
-      } else if (wr.lane == 0) {
+      } else if (rvalid && lead) {
         T.m_scale[r] = rc.newsc;
       }
     }
   }
 
   if (PHASE == 5 && CODEC == KAON_MOM_4BIT) bm4.flush(ws.bamax(T));
+  return keep;
+}
+
+template <int OPT, int PHASE, int PT, int GT, int CODEC>
+__global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__ D,
+                                                  const KaonItem* __restrict__ items, Ws ws, KaonHyper hp) {
+  __shared__ uint32_t keep_s[4];
+  const KaonItem it = items[blockIdx.x];
+  const KaonTensor& T = D[it.tensor];
+  const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
+  uint32_t keep;
+  // rows of at most 32 chunks side by side (4-bit blocks are walked row by row)
+  if constexpr (CODEC != KAON_MOM_4BIT) {
+    if (((T.C + 7) >> 3) <= 32) keep = elem_rows<OPT, PHASE, PT, GT, CODEC, true>(T, it, ws, hp);
+    else keep = elem_rows<OPT, PHASE, PT, GT, CODEC, false>(T, it, ws, hp);
+  } else {
+    keep = elem_rows<OPT, PHASE, PT, GT, CODEC, false>(T, it, ws, hp);
+  }
   if (PHASE == 5 && cautious) {
     const uint32_t wsum = wave_sum_u32(keep);
+    const WaveRows wr = wave_rows(it);
     if (wr.lane == 0) keep_s[wr.w] = wsum;
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -63,3 +63,53 @@ def test_non_tensors_are_refused():
     except TypeError:
         return
     raise AssertionError("expected a TypeError")
+
+
+def test_any_sequence_or_iterable_and_gradless_runs():
+    """Tuples and generators give the same result as lists; params without a grad at the
+    start, middle and end are left out, and the key's records stay aligned."""
+    ps = _params(20)
+    ps[0].grad = None
+    ps[19].grad = None
+    want = [p for p in ps if p.grad is not None]
+    for arg in (ps, tuple(ps), (p for p in ps)):
+        kept, key = K.group_key(arg)
+        assert type(kept) is list and all(a is b for a, b in zip(kept, want)) and len(kept) == len(want)
+        assert key == K.group_key(want)[1]
+    # every record: param pointer, grad pointer, then dtype / contiguity / sparsity tags
+    kept, key = K.group_key(ps)
+    for j, p in enumerate(kept):
+        rec = key[19 * j:19 * (j + 1)]
+        assert int.from_bytes(rec[0:8], "little") == p.data_ptr()
+        assert int.from_bytes(rec[8:16], "little") == p.grad.data_ptr()
+        assert rec[17] == 1 and rec[18] == 0
+    none = [torch.nn.Parameter(torch.zeros(2)) for _ in range(3)]
+    assert K.group_key(none) == ([], b"")
+
+
+def test_a_refused_element_after_kept_params_leaves_them_intact():
+    ps = _params(4)
+    refs = [p for p in ps]
+    for bad in ([ps[0], ps[1], 3], (ps[2], "x")):
+        try:
+            K.group_key(bad)
+        except TypeError:
+            pass
+        else:
+            raise AssertionError("expected a TypeError")
+    assert all(a is b for a, b in zip(ps, refs))
+    assert K.group_key(ps)[0] == [p for p in ps if p.grad is not None]
+
+
+def test_no_reference_leak():
+    import sys
+
+    ps = _params(8)
+    before = [sys.getrefcount(p) for p in ps]
+    for _ in range(200):
+        K.group_key(ps)
+        try:
+            K.group_key(ps + [None])
+        except TypeError:
+            pass
+    assert [sys.getrefcount(p) for p in ps] == before

@@ -1236,14 +1236,17 @@ __device__ __forceinline__ float row_val(float x) {
   return PK ? x : uniform_f(x);
 }
 
-// The rows of a wave's share of a slice, phases 5 and 6.  PK == false: one row
-// at a time, lane l taking chunks l, l+64, ....  PK == true (rows of at most 32
-// chunks): L = 2^ceil(log2(chunks)) lanes per row, 64 / L rows side by side,
-// lane cl of a row's lane group taking chunk cl.  Every element's arithmetic
-// is the same either way; the only reductions across lanes are the keep count
-// (an integer sum) and the int8 row absmax (a maximum), neither of which
-// depends on the order.  Returns the lane's keep count.
-template <int OPT, int PHASE, int PT, int GT, int CODEC, bool PK>
+// The rows of a wave's share of a slice, phases 5 and 6, in one of three
+// layouts.  LAY 0: one row at a time, lane l taking chunks l, l+64, ....
+// LAY 1 (rows of at most 32 chunks): L = 2^ceil(log2(chunks)) lanes per row,
+// 64 / L rows side by side, lane cl of a row's lane group taking chunk cl.
+// LAY 2 (an item of one row, e.g. a 1-D tensor): the four waves share the row,
+// wave w taking the chunk rounds w, w+4, ... of LAY 0.  Every element's
+// arithmetic is the same in all three; the only reductions across lanes are
+// the keep count (an integer sum), the int8 row absmax and the 4-bit block
+// absmax (maxima; blocks that cross chunks go through atomicMax), none of
+// which depends on the order.  Returns the lane's keep count.
+template <int OPT, int PHASE, int PT, int GT, int CODEC, int LAY>
 __device__ __forceinline__ uint32_t elem_rows(const KaonTensor& T, const KaonItem& it, const Ws& ws,
                                               const KaonHyper& hp) {
   const int64_t C = T.C, n = T.n;
@@ -1289,17 +1292,24 @@ __device__ __forceinline__ uint32_t elem_rows(const KaonTensor& T, const KaonIte
   double c_r = 1.0;
   // lanes per row (2^lsh) and rows side by side (P); the lane's row in a pass
   // and its chunk
+  constexpr bool PK = LAY == 1;
   const int lsh = PK ? (nch <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nch - 1))) : 6;
   const int P = 64 >> lsh;
   const int grp = wr.lane >> lsh;
   const int cl = wr.lane & ((1 << lsh) - 1);
-  const bool lead = cl == 0;  // the lane that stores the row's values
+  // the lane that stores the row's values (LAY 2: of wave 0)
+  const bool lead = cl == 0 && (LAY != 2 || wr.w == 0);
+  // the rows and the chunk rounds of this wave
+  const int64_t rbeg = LAY == 2 ? (int64_t)it.row0 : wr.rb;
+  const int64_t rend = LAY == 2 ? (int64_t)it.row0 + 1 : wr.re;
+  const int k0 = LAY == 2 ? wr.w : 0;
+  constexpr int kstep = LAY == 2 ? 4 : 1;
 
-  for (int64_t r0 = wr.rb; r0 < wr.re; r0 += P) {
+  for (int64_t r0 = rbeg; r0 < rend; r0 += P) {
     // the lane's row; lanes past the wave's rows read the first row's context
     // and take no chunk
-    const bool rvalid = r0 + grp < wr.re;
-    const int64_t r = rvalid ? r0 + grp : wr.rb;
+    const bool rvalid = r0 + grp < rend;
+    const int64_t r = rvalid ? r0 + grp : rbeg;
     // ---- per-row context (wave-uniform unless PK)
     RowCtx rc;
     rc.mu = gc ? row_val<PK>(ws.mu(T)[r]) : 0.0f;
@@ -1318,7 +1328,7 @@ __device__ __forceinline__ uint32_t elem_rows(const KaonTensor& T, const KaonIte
     rc.m128 = -128.0f * rc.oldsc;
     float row_amax = 0.0f;
 
-    for (int k = 0; k < cpl; ++k) {
+    for (int k = k0; k < cpl; k += kstep) {
       const int64_t c = cl + 64 * k;
       const int cnt = rvalid ? chunk_cnt(c, C) : 0;
       const int64_t j0 = c * 8;
@@ -1615,6 +1625,13 @@ __device__ __forceinline__ uint32_t elem_rows(const KaonTensor& T, const KaonIte
           for (int o = (1 << lsh) >> 1; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
         } else {
           am = wave_max(row_amax);
+          if (LAY == 2) {
+            // the four waves' maxima (every wave is here: the row is the item's)
+            __shared__ float wmax[4];
+            if (wr.lane == 0) wmax[wr.w] = am;
+            __syncthreads();
+            am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+          }
         }
         if (rvalid && lead) {
           ws.ramax(T)[r] = __float_as_uint(am);
@@ -1638,12 +1655,18 @@ __global__ __launch_bounds__(KAON_WG) void k_elem(const KaonTensor* __restrict__
   const KaonTensor& T = D[it.tensor];
   const bool cautious = (hp.flags & KAON_F_CAUTIOUS) != 0;
   uint32_t keep;
-  // rows of at most 32 chunks side by side (4-bit blocks are walked row by row)
+  // rows of at most 32 chunks side by side (4-bit blocks are walked row by
+  // row); an item of one row over the four waves; otherwise a row per wave
+  bool done = false;
   if constexpr (CODEC != KAON_MOM_4BIT) {
-    if (((T.C + 7) >> 3) <= 32) keep = elem_rows<OPT, PHASE, PT, GT, CODEC, true>(T, it, ws, hp);
-    else keep = elem_rows<OPT, PHASE, PT, GT, CODEC, false>(T, it, ws, hp);
-  } else {
-    keep = elem_rows<OPT, PHASE, PT, GT, CODEC, false>(T, it, ws, hp);
+    if (((T.C + 7) >> 3) <= 32) {
+      keep = elem_rows<OPT, PHASE, PT, GT, CODEC, 1>(T, it, ws, hp);
+      done = true;
+    }
+  }
+  if (!done) {
+    if (it.nrows == 1) keep = elem_rows<OPT, PHASE, PT, GT, CODEC, 2>(T, it, ws, hp);
+    else keep = elem_rows<OPT, PHASE, PT, GT, CODEC, 0>(T, it, ws, hp);
   }
   if (PHASE == 5 && cautious) {
     const uint32_t wsum = wave_sum_u32(keep);

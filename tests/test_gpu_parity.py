@@ -59,6 +59,7 @@ _MIX = [[640, 640, 3, 3], [1280, 2048], [5120, 640], [1280], [77, 33], [3, 5, 7]
 _SDXL = [[640, 640, 3, 3], [1280, 1280], [256, 2048], [96, 5120], [320, 320, 3, 3], [64, 640, 3, 3], [5120, 640],
          [1280], [640], [77, 33]]
 _PACKED = [[3, 1], [85, 7], [21, 9], [41, 20], [19, 33], [66, 100], [7, 129], [23, 256], [5, 257], [2, 3, 5], [40]]
+_VECS = [[5120], [1280], [20001], [1, 11520], [640], [320], [777], [2, 5120]]
 EXTRA = {
     "ada_int8_mix": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8")),
     "ada_4bit_mix_b64": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="4bit",
@@ -139,6 +140,15 @@ EXTRA = {
                                        p="f32", g="f32"),
     "nekaon_int8_packed_rows_f32": _case("nekaon", _PACKED, dict(lr=1e-4, k=1.5, momentum_dtype="int8"),
                                          p="f32", g="f32", steps=4),
+    # items of one row (1-D tensors, a one-row matrix) shared by the four waves of the
+    # phase-5/6 workgroup: int8 scales over the whole row, 4-bit blocks that cross
+    # chunks (96) and blocks of whole chunks (64)
+    "ada_int8_vectors": _case("adakaon", _VECS, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="int8",
+                                                     weight_decay=0.05)),
+    "ada_int8_vectors_f32": _case("adakaon", _VECS, dict(lr=1e-3, momentum_dtype="int8"), p="f32", g="f32"),
+    "ada_4bit_b96_vectors": _case("adakaon", _VECS, dict(lr=1e-3, momentum_dtype="4bit", momentum_4bit_block=96)),
+    "lion_4bit_b64_vectors": _case("lion", _VECS, dict(lr=2e-4, momentum_dtype="4bit", momentum_4bit_block=64)),
+    "nekaon_int8_vectors": _case("nekaon", _VECS, dict(lr=1e-4, k=1.5, momentum_dtype="int8"), steps=4),
 }
 
 

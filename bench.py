@@ -348,9 +348,11 @@ def apply_mix_ceiling_gbs(dev, n=512 << 20, reps=10) -> float:
     return 8.0 * n / (ms * 1e-3) / 1e9
 
 
-def lora_bag_ms(dev, steps=50, warmup=5) -> float:
+def lora_bag_ms(dev, steps=200, warmup=5) -> float:
     """ms per step of the launch-bound regime: the reference's LoRA proxy bag
-    (512 fp32 [8, 16] tensors, Adakaon with bf16 momentum), HIP events."""
+    (512 fp32 [8, 16] tensors, Adakaon with bf16 momentum), HIP events over 200
+    steps (about 8 ms: fewer would let one pause of the host thread weigh on the
+    mean of a host-bound step)."""
     import torch
     from kaon_amd import workloads
 

@@ -58,7 +58,8 @@ _MIX = [[640, 640, 3, 3], [1280, 2048], [5120, 640], [1280], [77, 33], [3, 5, 7]
 # 5120, 5760) plus 1-D, at sizes the oracle steps in about a second
 _SDXL = [[640, 640, 3, 3], [1280, 1280], [256, 2048], [96, 5120], [320, 320, 3, 3], [64, 640, 3, 3], [5120, 640],
          [1280], [640], [77, 33]]
-_PACKED = [[3, 1], [85, 7], [21, 9], [41, 20], [19, 33], [66, 100], [7, 129], [23, 256], [5, 257], [2, 3, 5], [40]]
+_PACKED = [[3, 1], [85, 7], [21, 9], [41, 20], [19, 33], [66, 100], [7, 129], [23, 256], [5, 257], [2, 3, 5], [40],
+           [700, 9], [1000, 20]]
 _VECS = [[5120], [1280], [20001], [1, 11520], [640], [320], [777], [2, 5120]]
 EXTRA = {
     "ada_int8_mix": _case("adakaon", _MIX, dict(lr=1e-4, betas=(0.9, 0.999), momentum_dtype="int8")),
@@ -130,7 +131,8 @@ EXTRA = {
     # short rows side by side in a wave (rows of at most 32 chunks): 1 to 32 chunks per row
     # (lane groups of 1 to 32 lanes, some with lanes past the row), 1 to 64 rows per pass,
     # wave groups of 20 rows split over several passes, two slices ([85, 7]), ragged chunks;
-    # [5, 257] (33 chunks) is the first length kept one row at a time
+    # [5, 257] (33 chunks) is the first length kept one row at a time; [700, 9] and [1000, 20]
+    # span 3 and 4 runs of 320 rows (one column partial per run)
     "ada_int8_packed_rows_f32": _case("adakaon", _PACKED, dict(lr=1e-3, betas=(0.9, 0.999), momentum_dtype="int8",
                                                                weight_decay=0.05, clip_threshold=0.05),
                                       p="f32", g="f32"),

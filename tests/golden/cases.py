@@ -173,4 +173,14 @@ def grad_values(case, i, step) -> np.ndarray:
         z = rng.standard_normal(shape)
         chi = sum(rng.standard_normal(shape) ** 2 for _ in range(3)) / 3.0
         g = np.where(mask, z / np.sqrt(chi) * sig, g)
-    return g.astype(np.float32)
+    g = g.astype(np.float32)
+    # ``poison``: {step: [(param, kind, index), ...]} writes a NaN / +inf / -inf at a flat
+    # index, or zeros a whole row ("zero_row", index = row), into that step's gradient
+    for pi, kind, idx in case.get("poison", {}).get(step, ()):
+        if pi != i:
+            continue
+        if kind == "zero_row":
+            g.reshape(shape[0], -1)[idx] = 0.0
+        else:
+            g.reshape(-1)[idx % g.size] = {"nan": np.nan, "inf": np.inf, "-inf": -np.inf}[kind]
+    return g

@@ -79,3 +79,19 @@ def test_nonfinite_grads_match_oracle(name):
     oparams, _, _ = oracle_case_run(case)
     params, opt, _ = run_gpu(case)
     _check(case, oparams, params, opt, name)
+
+
+TORCH_CASES = ("ada_int8", "ada_bf16_f32", "lion_int8", "nekaon_int8")
+
+
+@pytest.mark.parametrize("name", TORCH_CASES)
+def test_nonfinite_grads_match_oracle_in_torch_order(name):
+    """The same poisoned gradients through the torch-order kernels (reduction_order="torch":
+    torch CPU's cascades for the means, its 8 fma chains for the clip norm), against the
+    oracle in that order."""
+    case = CASES[name]
+    print(f"[gpu] non-finite grads, torch order {name}", flush=True)
+    with O.torch_order():
+        oparams, _, _ = oracle_case_run(case)
+    params, opt, _ = run_gpu(case, extra={"reduction_order": "torch"})
+    _check(case, oparams, params, opt, f"{name} torch order")

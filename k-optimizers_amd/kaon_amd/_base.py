@@ -9,9 +9,11 @@ State keys, dtypes and shapes are the reference's (K-Optimizers "kaon"
 from __future__ import annotations
 
 import ctypes
+from itertools import chain
 from typing import Any, Iterable
 
 import torch
+import torch.optim.optimizer as _topt
 
 from . import _engine as E
 from . import _keys as K
@@ -254,8 +256,42 @@ class KaonOptimizer(torch.optim.Optimizer):
             self.sr_seed = int(extra.get("sr_seed", self.sr_seed))
         self._invalidate()
 
-    def step(self, closure: Any = None) -> Any:
-        return self._step_impl(closure)
+    def step(self, *args: Any, **kwargs: Any) -> Any:
+        """One optimizer step; ``closure`` optional, as torch.optim's.
+
+        torch.optim.Optimizer wraps a subclass's ``step`` in a profiler range
+        and the step hooks unless the method is marked ``hooked``.  This one is:
+        it runs the same hooks in the same order (the global then the instance
+        pre-hooks, which may replace the arguments; the step; the instance then
+        the global post-hooks) and opens the same profiler range, but only while
+        a profiler is active.  The wrapper's range costs as much host time as the
+        rest of a step over a bag of small tensors."""
+        if torch.autograd._profiler_enabled():
+            with torch.autograd.profiler.record_function(f"Optimizer.step#{type(self).__name__}.step"):
+                return self._hooked_step(args, kwargs)
+        return self._hooked_step(args, kwargs)
+
+    step.hooked = True  # type: ignore[attr-defined]
+
+    def _hooked_step(self, args: tuple, kwargs: dict) -> Any:
+        a = (self,) + tuple(args)
+        pre, post = self._optimizer_step_pre_hooks, self._optimizer_step_post_hooks
+        gpre, gpost = _topt._global_optimizer_pre_hooks, _topt._global_optimizer_post_hooks
+        if pre or gpre:
+            for hook in chain(gpre.values(), pre.values()):
+                result = hook(self, a, kwargs)
+                if result is not None:
+                    if isinstance(result, tuple) and len(result) == 2:
+                        a, kwargs = result
+                    else:
+                        raise RuntimeError(f"{self.step} must return None or a tuple of (new_args, new_kwargs), "
+                                           f"but got {result}.")
+        out = self._step_impl(*a[1:], **kwargs)
+        self._optimizer_step_code()
+        if post or gpost:
+            for hook in chain(post.values(), gpost.values()):
+                hook(self, a, kwargs)
+        return out
 
     def _step_impl(self, closure: Any = None, nk: Any = None) -> Any:  # pragma: no cover - abstract
         raise NotImplementedError
